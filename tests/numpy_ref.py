@@ -1,0 +1,90 @@
+"""Vectorised numpy restatement of the block formulas and of the CpuScalar
+accumulation order, written independently of oracle/oracle.c so the two can
+check each other (a dropped term, a wrong shift or a transposed index in
+either shows up as a mismatch).
+
+Block formulas: backends/cpu/src/matmul.rs:162-280 and
+quant/src/schemes/{q8,q4,q4_k,q5_k,q6_k}.rs (dequantize_*).
+"""
+import numpy as np
+
+f32 = np.float32
+
+
+def _kquant_sc_m(scales):
+    """scales: [B,12] u8 -> (sc [B,8], m [B,8]) as u8 (matmul.rs:192-201)."""
+    s = scales.astype(np.uint8)
+    sc = np.empty((s.shape[0], 8), np.uint8)
+    mn = np.empty((s.shape[0], 8), np.uint8)
+    sc[:, :4] = s[:, 0:4] & 63
+    mn[:, :4] = s[:, 4:8] & 63
+    sc[:, 4:] = (s[:, 8:12] & 15) | ((s[:, 0:4] >> 6) << 4)
+    mn[:, 4:] = (s[:, 8:12] >> 4) | ((s[:, 4:8] >> 6) << 4)
+    return sc, mn
+
+
+def dequant_q8_0(b):
+    return (b["scale"][:, None] * b["values"].astype(f32)).astype(f32).ravel()
+
+
+def dequant_q4_0(b):
+    return (b["scale"][:, None] * (b["values"].astype(f32) - f32(8))).astype(f32).ravel()
+
+
+def _k4_codes(values):
+    """values [B,128] -> q [B,256]: element l uses byte 32*(l//64) + l%32,
+    low nibble when l%64 < 32 (matmul.rs:202-209)."""
+    v = values.reshape(-1, 4, 32)
+    lo = v & 15
+    hi = v >> 4
+    return np.stack([lo, hi], axis=2).reshape(-1, 256)
+
+
+def dequant_q4_k(b):
+    sc, mn = _kquant_sc_m(b["scales"])
+    q = _k4_codes(b["values"]).astype(f32)
+    sub = np.arange(256) // 32
+    d = b["scale"][:, None]
+    dm = b["min_scale"][:, None]
+    return ((d * sc[:, sub].astype(f32)) * q - dm * mn[:, sub].astype(f32)).astype(f32).ravel()
+
+
+def dequant_q5_k(b):
+    sc, mn = _kquant_sc_m(b["scales"])
+    q = _k4_codes(b["values"]).astype(np.int32)
+    l = np.arange(256)
+    g, w = l // 64, l % 64
+    bit = 2 * g + (w >= 32)
+    hb = b["high_bits"][:, w % 32]
+    q = q + 16 * ((hb >> bit) & 1)
+    sub = l // 32
+    d = b["scale"][:, None]
+    dm = b["min_scale"][:, None]
+    return ((d * sc[:, sub].astype(f32)) * q.astype(f32) - dm * mn[:, sub].astype(f32)).astype(f32).ravel()
+
+
+def dequant_q6_k(b):
+    l = np.arange(256)
+    ip, r = l // 128, l % 128
+    c, il = r // 32, r % 32
+    byte = b["low_bits"][:, 64 * ip + np.where(c % 2 == 0, il, 32 + il)]
+    low = np.where(c < 2, byte & 15, byte >> 4).astype(np.int32)
+    high = ((b["high_bits"][:, 32 * ip + il] >> (2 * c)) & 3).astype(np.int32)
+    q = low | (high << 4)
+    sc = b["scales"][:, l // 16].astype(f32)
+    return ((b["scale"][:, None] * sc) * (q - 32).astype(f32)).astype(f32).ravel()
+
+
+DEQUANT = {1: dequant_q8_0, 2: dequant_q4_0, 3: dequant_q4_k, 4: dequant_q5_k, 5: dequant_q6_k}
+
+
+def sequential_f32(x, w_rows):
+    """CpuScalar order: for every output, acc = acc + x[k]*w[k] in f32, k
+    ascending, no FMA. x [M,K], w_rows [N,K] -> y [M,N]."""
+    x = x.astype(f32)
+    w = w_rows.astype(f32)
+    m, k = x.shape
+    acc = np.zeros((m, w.shape[0]), f32)
+    for i in range(k):
+        acc = (acc + (x[:, i:i + 1] * w[None, :, i]).astype(f32)).astype(f32)
+    return acc
