@@ -1,0 +1,176 @@
+"""Benchmark of the hot path: quantized decode GEMV on one MI355X.
+
+Workload (the shape the metric is quoted on):
+Q4_K output-rows weight, K=4096, N=14336, M=1 f32 activation row, F32 mode.
+A step is one GEMV over the whole weight. Inputs are resident in HBM before
+the timed region; 16 distinct weight copies (530 MB, above the 256 MB
+Infinity Cache) are rotated so every step streams its weight from HBM.
+
+Prints ONE JSON line (the driver's contract) with a `roofline` object for the
+GEMV kernel (algorithmic bytes / measured average kernel duration vs 8 TB/s)
+and a `cpu_baseline` object (the oracle's CpuScalar port on one host core).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import re
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBPS = 8000.0
+K, N, M = 4096, 14336, 1
+WIRE = {1: 34, 2: 18, 3: 144, 4: 176, 5: 210}
+BLOCK = {1: 32, 2: 32, 3: 256, 4: 256, 5: 256}
+
+
+def algorithmic_bytes(qtype: int, k: int, n: int, m: int) -> int:
+    """GGUF wire weight bytes + activations + outputs (f32)."""
+    return n * (k // BLOCK[qtype]) * WIRE[qtype] + m * k * 4 + m * n * 4
+
+
+def traffic_from_profile(name: str):
+    """HBM bytes per launch from the committed rocprofv3 PMC summary, if any."""
+    path = os.path.join(ROOT, "profiles", name)
+    if not os.path.exists(path):
+        return None
+    m = re.search(r"traffic_bytes_per_launch:\s*([0-9.]+)", open(path).read())
+    return float(m.group(1)) if m else None
+
+
+def gpu_measure(qtype: int, steps: int, warmup: int, copies_mb: float = 512.0):
+    import numpy as np
+    import torch
+
+    import quantinfer_amd as qa
+    from oracle import pyoracle as po  # input generation only (the quantizer restatement)
+
+    ctx = qa.Context(0)
+    blocks = po.make_weights(qtype, K, N, seed=0x5EED0000 + qtype, outliers=qtype >= 3)
+    wbytes = N * (K // BLOCK[qtype]) * WIRE[qtype]
+    copies = max(1, int(-(-copies_mb * 1e6 // wbytes)))
+    weights = [ctx.weights(qtype, qa.OUTPUT_ROWS, K, N, blocks) for _ in range(copies)]
+    x = torch.from_numpy(po.fill_normal(0x5EED1000, M * K).reshape(M, K)).to("cuda:0")
+    y = torch.empty((M, N), dtype=torch.float32, device="cuda:0")
+    stream = torch.cuda.current_stream()
+    sptr = stream.cuda_stream
+
+    def step(i):
+        weights[i % copies].linear_device(x.data_ptr(), M, y.data_ptr(), qa.MODE_F32, sptr)
+
+    for i in range(warmup):
+        step(i)
+    torch.cuda.synchronize()
+
+    # timed region: `steps` back-to-back GEMVs, bracketed by events on the launch stream
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record(stream)
+    for i in range(steps):
+        step(i)
+    end.record(stream)
+    torch.cuda.synchronize()
+    region_ms = start.elapsed_time(end)
+
+    # per-launch kernel duration (events around each launch on the same stream)
+    pairs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+             for _ in range(steps)]
+    for i, (a, b) in enumerate(pairs):
+        a.record(stream)
+        step(i)
+        b.record(stream)
+    torch.cuda.synchronize()
+    kernel_ms = statistics.median(a.elapsed_time(b) for a, b in pairs)
+
+    name = ctx.device_name()
+    for w in weights:
+        w.free()
+    ctx.close()
+    return {"region_ms": region_ms, "kernel_ms": kernel_ms, "copies": copies, "device": name}
+
+
+def cpu_baseline(qtype: int, repeats: int = 3):
+    """The oracle's port of CpuScalar::matmul_q4_k_output_rows (single-threaded,
+    as the reference's output-row kernels are), pinned to one host core."""
+    from oracle import pyoracle as po
+
+    blocks = po.make_weights(qtype, K, N, seed=0x5EED0000 + qtype, outliers=qtype >= 3)
+    x = po.fill_normal(0x5EED1000, M * K).reshape(M, K)
+    try:
+        old = os.sched_getaffinity(0)
+        os.sched_setaffinity(0, {min(old)})
+    except (AttributeError, OSError):
+        old = None
+    times = []
+    try:
+        for _ in range(repeats):
+            t = time.perf_counter()
+            po.matmul_output_rows(qtype, x, blocks, N)
+            times.append(time.perf_counter() - t)
+    finally:
+        if old is not None:
+            os.sched_setaffinity(0, old)
+    sec = statistics.median(times)
+    return {
+        "value": round(algorithmic_bytes(qtype, K, N, M) / sec / 1e9, 3),
+        "unit": "GB/s", "cores": 1, "kind": "port",
+        "sample": f"full workload (M=1, K={K}, N={N}) x{repeats}, median {sec * 1e3:.1f} ms; "
+                  f"oracle C port of CpuScalar output-row kernel, 1 pinned core",
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (asked for {args.gpus}); "
+              "the multi-GPU sharding is a design note, not a measured path", file=sys.stderr)
+        sys.exit(2)
+
+    qtype = 3  # Q4_K
+    g = gpu_measure(qtype, args.steps, args.warmup)
+    abytes = algorithmic_bytes(qtype, K, N, M)
+    ms_per_step = g["region_ms"] / args.steps
+    value = abytes / (ms_per_step * 1e-3) / 1e9
+    achieved = abytes / (g["kernel_ms"] * 1e-3) / 1e9
+    line = {
+        "metric": "quant GEMV GB/s (% of HBM peak) at 4096x14336; Qwen3-8B-shape decode tok/s",
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic: N(0,0.02^2) weights with 0.5% N(0,0.2^2) outliers, Q4_K-quantized "
+                "by the restated reference quantizer; x ~ N(0,1)",
+        "config": {"workload": "q4_k_gemv_output_rows_m1_k4096_n14336", "qtype": "q4_k",
+                   "m": M, "k": K, "n": N, "mode": "f32", "weight_copies": g["copies"],
+                   "device": g["device"]},
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 2),
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBPS, 4),
+            "traffic": traffic_from_profile("q4_k_gemv_4096x14336_traffic.md"),
+        },
+        "cpu_baseline": None if args.no_cpu else cpu_baseline(qtype),
+    }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

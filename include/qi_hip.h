@@ -1,0 +1,166 @@
+/*
+ * qi_hip: MI355X (gfx950) quantized-linear backend for QuantInfer, C ABI.
+ *
+ * This is the drop-in boundary a `backends/hip` crate binds. It replaces the
+ * quantized-matmul methods of the reference's operator contract
+ *   trait KernelBackend            crates/quantinfer-kernel/src/lib.rs:83-154
+ * for the GGML block formats Q8_0, Q4_0, Q4_K, Q5_K, Q6_K (and F32), in both
+ * the row-major (QuantInfer) and output-rows (GGML) layouts.
+ *
+ * Conventions follow the reference's own C ABI (bindings/c/include/quantinfer.h:
+ * 12-19 status codes, :36-37 thread-local last error):
+ *  - every call returns a qi_hip_status; on failure qi_hip_last_error() holds a
+ *    message for the calling thread;
+ *  - plain pointers and sizes only; the caller owns host buffers; a weights
+ *    handle owns its device memory; a context owns its stream, its scratch
+ *    workspace and a mutex (calls on one context are serialized, handles may
+ *    cross threads);
+ *  - status -> reference error: QI_HIP_INVALID_INPUT -> KernelError::InvalidInput,
+ *    QI_HIP_UNSUPPORTED and QI_HIP_RUNTIME_ERROR -> KernelError::Unsupported
+ *    (crates/quantinfer-kernel/src/lib.rs:14-19; the device-failure mapping is
+ *    the one backends/cuda/src/native.rs:238-244 uses).
+ */
+#ifndef QI_HIP_H
+#define QI_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define QI_HIP_ABI_VERSION 1
+
+typedef int32_t qi_hip_status;
+#define QI_HIP_OK 0
+#define QI_HIP_INVALID_INPUT 1
+#define QI_HIP_UNSUPPORTED 2
+#define QI_HIP_RUNTIME_ERROR 3
+
+/* Weight element types (core DType / runtime LinearWeight variants,
+ * crates/quantinfer-runtime/src/linear.rs:14-30). */
+#define QI_HIP_F32 0
+#define QI_HIP_Q8_0 1
+#define QI_HIP_Q4_0 2
+#define QI_HIP_Q4_K 3
+#define QI_HIP_Q5_K 4
+#define QI_HIP_Q6_K 5
+
+/* Layouts of the logical RHS [K, N] (core quantized/mod.rs:10 names the second):
+ * ROW_MAJOR   element (k, n) at flat index k*N + n; blocks run along N
+ *             (backends/cpu/src/matmul.rs:162-168).
+ * OUTPUT_ROWS blocks ordered output-major: output n owns K/bs consecutive
+ *             blocks (crates/quantinfer-kernel/src/lib.rs:101, matmul.rs:141-158). */
+#define QI_HIP_LAYOUT_ROW_MAJOR 0
+#define QI_HIP_LAYOUT_OUTPUT_ROWS 1
+
+/* Arithmetic modes of a linear call.
+ * AUTO  F32 below 128 activation rows, MFMA at 128 and above (the decode /
+ *       prefill split of the kernels).
+ * F32   f32 accumulation of f32 products for any M (GEMV kernels), judged by
+ *       tolerance against the CPU reference.
+ * EXACT bit-identical to CpuScalar: per output, acc = acc + x[k]*w[k] in f32,
+ *       k ascending, no FMA (backends/cpu/src/matmul.rs:146-157, 319-330).
+ * MFMA  f16 operands into f32 matrix-core accumulation (prefill GEMM). */
+#define QI_HIP_MODE_AUTO 0
+#define QI_HIP_MODE_F32 1
+#define QI_HIP_MODE_EXACT 2
+#define QI_HIP_MODE_MFMA 3
+
+/* Logical blocks: field-for-field the reference core structs, which are not
+ * repr(C); the Rust glue copies fields into these. No padding. */
+typedef struct { float scale; int8_t values[32]; } qi_hip_q8_0_block;     /* core quantized/q8.rs:7-11  */
+typedef struct { float scale; uint8_t values[32]; } qi_hip_q4_0_block;    /* core quantized/q4.rs:7-13  */
+typedef struct {
+  float scale, min_scale;
+  uint8_t scales[12];
+  uint8_t values[128];
+} qi_hip_q4_k_block;                                                      /* core quantized/q4.rs:72-78 */
+typedef struct {
+  float scale, min_scale;
+  uint8_t scales[12];
+  uint8_t high_bits[32];
+  uint8_t values[128];
+} qi_hip_q5_k_block;                                                      /* core quantized/k.rs:7-14   */
+typedef struct {
+  float scale;
+  int8_t scales[16];
+  uint8_t low_bits[128];
+  uint8_t high_bits[64];
+} qi_hip_q6_k_block;                                                      /* core quantized/k.rs:55-61  */
+
+typedef struct qi_hip_ctx qi_hip_ctx;
+typedef struct qi_hip_weights qi_hip_weights;
+
+typedef struct {
+  int32_t qtype, layout;
+  uint64_t k, n;
+  uint64_t device_bytes;   /* bytes of the resident device image */
+  int32_t f16_scales;      /* 1: every scale is f16-exact, so the image has GGUF wire size */
+} qi_hip_weights_info;
+
+/* ABI version; the glue refuses a library whose version differs. */
+int32_t qi_hip_abi_version(void);
+
+/* Message of the calling thread's last failure ("" if none). */
+const char *qi_hip_last_error(void);
+
+/* Open device `device` (HIP ordinal). QI_HIP_UNSUPPORTED when no gfx950 device
+ * is visible or the HIP runtime is unavailable.
+ * Replaces: CudaBackend::open (backends/cuda/src/native.rs:29-57). */
+qi_hip_status qi_hip_open(int32_t device, qi_hip_ctx **out);
+void qi_hip_close(qi_hip_ctx *ctx);
+
+/* Device marketing name, NUL-terminated into buf.
+ * Replaces: CudaBackend::device_name (backends/cuda/src/native.rs:59-61). */
+qi_hip_status qi_hip_device_name(qi_hip_ctx *ctx, char *buf, size_t len);
+
+/* Upload logical blocks as a resident weight of logical shape [K, N].
+ * `blocks` holds `count` qi_hip_*_block structs of `qtype` in the reference's
+ * block order for `layout`, or K*N f32 values (row-major [K, N]) for QI_HIP_F32.
+ * Validation is the reference's: QuantizedTensor*::from_blocks
+ * (core quantized/q8.rs:20-40, q4.rs:22-51, q4.rs:87-120, k.rs:23-41, k.rs:70-85)
+ * plus the matmul shape checks (backends/cpu/src/matmul.rs:131-140, 293-314).
+ * Replaces: the per-call weight upload of CudaBackend::multiply
+ * (backends/cuda/src/native.rs:99-104) with a resident handle. */
+qi_hip_status qi_hip_weights_create(qi_hip_ctx *ctx, int32_t qtype, int32_t layout, uint64_t k,
+                                    uint64_t n, const void *blocks, uint64_t count,
+                                    qi_hip_weights **out);
+void qi_hip_weights_free(qi_hip_weights *w);
+qi_hip_status qi_hip_weights_info_get(const qi_hip_weights *w, qi_hip_weights_info *out);
+
+/* y[M, N] = x[M, K] * W, host buffers, synchronous.
+ * Replaces: KernelBackend::matmul (lib.rs:95), matmul_q8_0 / matmul_q4_0
+ * (lib.rs:97-99), matmul_q8_0_output_rows / matmul_q4_0_output_rows
+ * (lib.rs:102-113), matmul_q4_k / q5_k / q6_k (lib.rs:115-119) and
+ * matmul_q{4,5,6}_k_output_rows (lib.rs:122-140): the variant is selected by the
+ * handle's qtype and layout. */
+qi_hip_status qi_hip_linear(qi_hip_ctx *ctx, const qi_hip_weights *w, const float *x_host,
+                            uint64_t m, float *y_host, int32_t mode);
+
+/* Same on device buffers, enqueued on `stream` (a hipStream_t; NULL = the
+ * context's stream). Returns after the launch; no host synchronisation. */
+qi_hip_status qi_hip_linear_device(qi_hip_ctx *ctx, const qi_hip_weights *w, const float *x_dev,
+                                   uint64_t m, float *y_dev, int32_t mode, void *stream);
+
+/* Bit-exact f32 dequantization in block order (K*N floats).
+ * Replaces: dequantize_q8_0 / q4_0 / q4_k / q5_k / q6_k
+ * (crates/quantinfer-quant/src/schemes/q8.rs:33-45, q4.rs:35-47, q4_k.rs:90-121,
+ * q5_k.rs:96-135, q6_k.rs:74-103). */
+qi_hip_status qi_hip_dequantize(qi_hip_ctx *ctx, const qi_hip_weights *w, float *out_host);
+qi_hip_status qi_hip_dequantize_device(qi_hip_ctx *ctx, const qi_hip_weights *w, float *out_dev,
+                                       void *stream);
+
+/* Host-only: build the device image of a weight without a device (validation
+ * and packing exactly as qi_hip_weights_create). With out == NULL only the
+ * size is returned in *bytes. Replaces the GGUF block writers' role
+ * (crates/quantinfer-format/src/gguf/writer.rs:183-261) for the device layout. */
+qi_hip_status qi_hip_pack_weights(int32_t qtype, int32_t layout, uint64_t k, uint64_t n,
+                                  const void *blocks, uint64_t count, void *out, uint64_t *bytes,
+                                  int32_t *f16_scales);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

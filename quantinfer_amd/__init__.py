@@ -1,0 +1,187 @@
+"""quantinfer_amd: MI355X (gfx950) quantized-linear backend for QuantInfer.
+
+The product is the C-ABI library libqi_hip.so (include/qi_hip.h) built from
+quantinfer_amd/csrc by quantinfer_amd/build.py. This module is ctypes
+plumbing over that ABI for Python callers (tests, bench.py); it contains no
+compute of its own and raises if the native library is missing.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libqi_hip.so")
+
+OK, INVALID_INPUT, UNSUPPORTED, RUNTIME_ERROR = 0, 1, 2, 3
+F32, Q8_0, Q4_0, Q4_K, Q5_K, Q6_K = 0, 1, 2, 3, 4, 5
+QTYPES = {"f32": F32, "q8_0": Q8_0, "q4_0": Q4_0, "q4_k": Q4_K, "q5_k": Q5_K, "q6_k": Q6_K}
+ROW_MAJOR, OUTPUT_ROWS = 0, 1
+MODE_AUTO, MODE_F32, MODE_EXACT, MODE_MFMA = 0, 1, 2, 3
+
+# qi_hip_*_block (include/qi_hip.h), field-for-field the reference core structs.
+BLOCK_DTYPES = {
+    Q8_0: np.dtype([("scale", "<f4"), ("values", "i1", (32,))]),
+    Q4_0: np.dtype([("scale", "<f4"), ("values", "u1", (32,))]),
+    Q4_K: np.dtype([("scale", "<f4"), ("min_scale", "<f4"), ("scales", "u1", (12,)),
+                    ("values", "u1", (128,))]),
+    Q5_K: np.dtype([("scale", "<f4"), ("min_scale", "<f4"), ("scales", "u1", (12,)),
+                    ("high_bits", "u1", (32,)), ("values", "u1", (128,))]),
+    Q6_K: np.dtype([("scale", "<f4"), ("scales", "i1", (16,)), ("low_bits", "u1", (128,)),
+                    ("high_bits", "u1", (64,))]),
+}
+BLOCK_ELEMS = {F32: 1, Q8_0: 32, Q4_0: 32, Q4_K: 256, Q5_K: 256, Q6_K: 256}
+WIRE_BYTES = {Q8_0: 34, Q4_0: 18, Q4_K: 144, Q5_K: 176, Q6_K: 210}
+
+
+class QiError(RuntimeError):
+    def __init__(self, status: int, message: str):
+        super().__init__(f"[status {status}] {message}")
+        self.status = status
+
+
+class WeightsInfo(ctypes.Structure):
+    _fields_ = [("qtype", ctypes.c_int32), ("layout", ctypes.c_int32), ("k", ctypes.c_uint64),
+                ("n", ctypes.c_uint64), ("device_bytes", ctypes.c_uint64),
+                ("f16_scales", ctypes.c_int32)]
+
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    """Load libqi_hip.so. Raises if it has not been built: there is no fallback."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is missing: build it with quantinfer_amd/build.py "
+                               "(or __graft_entry__.build()); there is no CPU fallback")
+        l = ctypes.CDLL(LIB_PATH)
+        vp, u64, i32 = ctypes.c_void_p, ctypes.c_uint64, ctypes.c_int32
+        l.qi_hip_abi_version.restype = i32
+        l.qi_hip_last_error.restype = ctypes.c_char_p
+        l.qi_hip_open.argtypes = [i32, ctypes.POINTER(vp)]
+        l.qi_hip_close.argtypes = [vp]
+        l.qi_hip_close.restype = None
+        l.qi_hip_device_name.argtypes = [vp, ctypes.c_char_p, ctypes.c_size_t]
+        l.qi_hip_weights_create.argtypes = [vp, i32, i32, u64, u64, vp, u64, ctypes.POINTER(vp)]
+        l.qi_hip_weights_free.argtypes = [vp]
+        l.qi_hip_weights_free.restype = None
+        l.qi_hip_weights_info_get.argtypes = [vp, ctypes.POINTER(WeightsInfo)]
+        l.qi_hip_linear.argtypes = [vp, vp, vp, u64, vp, i32]
+        l.qi_hip_linear_device.argtypes = [vp, vp, vp, u64, vp, i32, vp]
+        l.qi_hip_dequantize.argtypes = [vp, vp, vp]
+        l.qi_hip_dequantize_device.argtypes = [vp, vp, vp, vp]
+        l.qi_hip_pack_weights.argtypes = [i32, i32, u64, u64, vp, u64, vp,
+                                          ctypes.POINTER(u64), ctypes.POINTER(i32)]
+        for name in ("qi_hip_open", "qi_hip_device_name", "qi_hip_weights_create",
+                     "qi_hip_weights_info_get", "qi_hip_linear", "qi_hip_linear_device",
+                     "qi_hip_dequantize", "qi_hip_dequantize_device", "qi_hip_pack_weights"):
+            getattr(l, name).restype = i32
+        if l.qi_hip_abi_version() != 1:
+            raise RuntimeError("libqi_hip.so ABI version mismatch")
+        _lib = l
+    return _lib
+
+
+def _check(status: int) -> None:
+    if status != OK:
+        raise QiError(status, lib().qi_hip_last_error().decode())
+
+
+def _ptr(a: np.ndarray) -> int:
+    if not a.flags["C_CONTIGUOUS"]:
+        raise ValueError("array must be C-contiguous")
+    return a.ctypes.data
+
+
+def pack_weights(qtype: int, layout: int, k: int, n: int, blocks: np.ndarray):
+    """Host-only device image (bytes, f16_scales) exactly as weights_create builds it."""
+    b = np.ascontiguousarray(blocks)
+    size = ctypes.c_uint64(0)
+    f16 = ctypes.c_int32(0)
+    _check(lib().qi_hip_pack_weights(qtype, layout, k, n, _ptr(b), b.size, None,
+                                     ctypes.byref(size), ctypes.byref(f16)))
+    out = np.zeros(size.value, dtype=np.uint8)
+    _check(lib().qi_hip_pack_weights(qtype, layout, k, n, _ptr(b), b.size, _ptr(out),
+                                     ctypes.byref(size), ctypes.byref(f16)))
+    return out, bool(f16.value)
+
+
+class Context:
+    """An open gfx950 device (qi_hip_open)."""
+
+    def __init__(self, device: int = 0):
+        h = ctypes.c_void_p()
+        _check(lib().qi_hip_open(device, ctypes.byref(h)))
+        self.handle = h
+
+    def close(self) -> None:
+        if self.handle:
+            lib().qi_hip_close(self.handle)
+            self.handle = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def device_name(self) -> str:
+        buf = ctypes.create_string_buffer(256)
+        _check(lib().qi_hip_device_name(self.handle, buf, 256))
+        return buf.value.decode()
+
+    def weights(self, qtype: int, layout: int, k: int, n: int, blocks: np.ndarray) -> "Weights":
+        return Weights(self, qtype, layout, k, n, blocks)
+
+
+class Weights:
+    """A resident weight of logical shape [K, N] (qi_hip_weights_create)."""
+
+    def __init__(self, ctx: Context, qtype: int, layout: int, k: int, n: int, blocks: np.ndarray):
+        b = np.ascontiguousarray(blocks)
+        h = ctypes.c_void_p()
+        _check(lib().qi_hip_weights_create(ctx.handle, qtype, layout, k, n, _ptr(b), b.size,
+                                           ctypes.byref(h)))
+        self.ctx, self.handle, self.qtype, self.layout, self.k, self.n = ctx, h, qtype, layout, k, n
+
+    def free(self) -> None:
+        if self.handle:
+            lib().qi_hip_weights_free(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+    def info(self) -> WeightsInfo:
+        out = WeightsInfo()
+        _check(lib().qi_hip_weights_info_get(self.handle, ctypes.byref(out)))
+        return out
+
+    def linear(self, x: np.ndarray, mode: int = MODE_AUTO) -> np.ndarray:
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        if x.ndim != 2 or x.shape[1] != self.k:
+            raise ValueError(f"x must be [M, {self.k}]")
+        y = np.empty((x.shape[0], self.n), dtype=np.float32)
+        _check(lib().qi_hip_linear(self.ctx.handle, self.handle, _ptr(x), x.shape[0], _ptr(y), mode))
+        return y
+
+    def linear_device(self, x_ptr: int, m: int, y_ptr: int, mode: int = MODE_AUTO,
+                      stream: int = 0) -> None:
+        _check(lib().qi_hip_linear_device(self.ctx.handle, self.handle, x_ptr, m, y_ptr, mode,
+                                          stream or None))
+
+    def dequantize(self) -> np.ndarray:
+        out = np.empty(self.k * self.n, dtype=np.float32)
+        _check(lib().qi_hip_dequantize(self.ctx.handle, self.handle, _ptr(out)))
+        return out
+
+    def dequantize_device(self, out_ptr: int, stream: int = 0) -> None:
+        _check(lib().qi_hip_dequantize_device(self.ctx.handle, self.handle, out_ptr,
+                                              stream or None))

@@ -1,0 +1,332 @@
+// C ABI of the MI355X quantized-linear backend (include/qi_hip.h).
+//
+// The context owns one HIP stream (default priority), a split-K workspace
+// (partial sums + per-row-tile tickets, zeroed once at open) and grow-only
+// staging buffers for the synchronous host entry points. A mutex serializes
+// calls on one context; device-side work of two calls on one context must not
+// overlap (they share the workspace), which holds for every entry point here
+// because each enqueues on a single stream.
+#include <hip/hip_runtime.h>
+#include <string.h>
+
+#include <mutex>
+#include <string>
+
+#include "../../include/qi_hip.h"
+#include "qi_image.h"
+#include "qi_internal.h"
+
+using qi::Image;
+
+struct qi_hip_ctx {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  std::mutex mu;
+  std::string name;
+  float* partials = nullptr;
+  uint64_t partials_cap = 0;  // floats
+  uint32_t* tickets = nullptr;
+  uint64_t tickets_cap = 0;
+  float* xbuf = nullptr;
+  uint64_t xcap = 0;  // floats
+  float* ybuf = nullptr;
+  uint64_t ycap = 0;
+};
+
+struct qi_hip_weights {
+  qi_hip_ctx* ctx = nullptr;
+  Image im;
+  void* dev = nullptr;
+};
+
+namespace {
+
+thread_local std::string g_last_error;
+
+qi_hip_status fail(qi_hip_status st, const std::string& msg) {
+  g_last_error = msg;
+  return st;
+}
+
+qi_hip_status hip_fail(hipError_t e, const char* what) {
+  return fail(QI_HIP_RUNTIME_ERROR, std::string("HIP ") + what + ": " + hipGetErrorString(e));
+}
+
+#define QI_HIP_TRY(expr, what)                  \
+  do {                                          \
+    hipError_t e_ = (expr);                     \
+    if (e_ != hipSuccess) return hip_fail(e_, what); \
+  } while (0)
+
+constexpr uint64_t kPartialsFloats = 8ull << 20;  // 32 MiB of split-K partials
+constexpr uint64_t kTickets = 1ull << 20;
+
+qi_hip_status grow(float** buf, uint64_t* cap, uint64_t need, const char* what) {
+  if (need <= *cap) return QI_HIP_OK;
+  if (*buf) (void)hipFree(*buf);
+  *buf = nullptr;
+  *cap = 0;
+  QI_HIP_TRY(hipMalloc(reinterpret_cast<void**>(buf), need * sizeof(float)), what);
+  *cap = need;
+  return QI_HIP_OK;
+}
+
+qi_hip_status ensure_tickets(qi_hip_ctx* c, uint64_t need) {
+  if (need <= c->tickets_cap) return QI_HIP_OK;
+  QI_HIP_TRY(hipStreamSynchronize(c->stream), "synchronize before growing tickets");
+  if (c->tickets) (void)hipFree(c->tickets);
+  c->tickets = nullptr;
+  c->tickets_cap = 0;
+  QI_HIP_TRY(hipMalloc(reinterpret_cast<void**>(&c->tickets), need * sizeof(uint32_t)), "alloc tickets");
+  QI_HIP_TRY(hipMemset(c->tickets, 0, need * sizeof(uint32_t)), "zero tickets");
+  QI_HIP_TRY(hipDeviceSynchronize(), "zero tickets");
+  c->tickets_cap = need;
+  return QI_HIP_OK;
+}
+
+qi_hip_status check_call(qi_hip_ctx* ctx, const qi_hip_weights* w, uint64_t m) {
+  if (ctx == nullptr || w == nullptr) return fail(QI_HIP_INVALID_INPUT, "null context or weights");
+  if (w->ctx != ctx) return fail(QI_HIP_INVALID_INPUT, "weights belong to another context");
+  // lhs rows must be nonzero (core tensor.rs:85-93); grid.y limits exact-mode rows
+  if (m == 0) return fail(QI_HIP_INVALID_INPUT, "matmul lhs must have at least one row");
+  if (m > 65535) return fail(QI_HIP_INVALID_INPUT, "matmul lhs has more than 65535 rows");
+  return QI_HIP_OK;
+}
+
+qi_hip_status run_linear(qi_hip_ctx* c, const qi_hip_weights* w, const float* x, uint64_t m,
+                         float* y, int32_t mode, hipStream_t st) {
+  const Image& im = w->im;
+  const qi::View v = qi::make_view(im, w->dev);
+  if (mode < QI_HIP_MODE_AUTO || mode > QI_HIP_MODE_MFMA)
+    return fail(QI_HIP_INVALID_INPUT, "unknown arithmetic mode");
+  bool use_gemm = false;
+  if (mode == QI_HIP_MODE_MFMA) {
+    if (!qi::gemm_supported(im.qtype, im.layout, im.k, im.n))
+      return fail(QI_HIP_UNSUPPORTED, "MFMA GEMM does not support this weight type/layout/shape");
+    use_gemm = true;
+  } else if (mode == QI_HIP_MODE_AUTO) {
+    use_gemm = m >= 128 && qi::gemm_supported(im.qtype, im.layout, im.k, im.n);
+  }
+  if (use_gemm) {
+    qi::GemmArgs ga{v, x, y, m};
+    QI_HIP_TRY(qi::launch_gemm(im, ga, st), "launch gemm");
+    return QI_HIP_OK;
+  }
+  const bool fast = mode != QI_HIP_MODE_EXACT && im.qtype != qi::kF32 &&
+                    im.layout == qi::kOutputRows;
+  if (!fast) {
+    QI_HIP_TRY(qi::launch_exact(im, v, x, m, y, st), "launch exact matmul");
+    return QI_HIP_OK;
+  }
+  for (uint64_t m0 = 0; m0 < m; m0 += 16) {
+    const int rows = static_cast<int>(m - m0 < 16 ? m - m0 : 16);
+    const int mt = rows == 1 ? 1 : rows == 2 ? 2 : rows <= 4 ? 4 : rows <= 8 ? 8 : 16;
+    qi::GemvPlan plan = qi::plan_gemv(im.qtype, im.k, im.n, mt, c->partials_cap);
+    if (plan.splits > 1) {
+      qi_hip_status s = ensure_tickets(c, plan.row_tiles);
+      if (s != QI_HIP_OK) return s;
+    }
+    qi::GemvArgs ga;
+    ga.w = v;
+    ga.x = x + m0 * im.k;
+    ga.y = y + m0 * im.n;
+    ga.m = rows;
+    ga.slots_per_split = plan.slots_per_split;
+    ga.partials = c->partials;
+    ga.tickets = c->tickets;
+    QI_HIP_TRY(qi::launch_gemv(im.qtype, im.wide != 0, mt, ga, plan, st), "launch gemv");
+  }
+  return QI_HIP_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int32_t qi_hip_abi_version(void) { return QI_HIP_ABI_VERSION; }
+
+const char* qi_hip_last_error(void) { return g_last_error.c_str(); }
+
+qi_hip_status qi_hip_open(int32_t device, qi_hip_ctx** out) {
+  if (out == nullptr) return fail(QI_HIP_INVALID_INPUT, "null output pointer");
+  *out = nullptr;
+  int count = 0;
+  hipError_t e = hipGetDeviceCount(&count);
+  if (e != hipSuccess || count == 0)
+    return fail(QI_HIP_UNSUPPORTED, "no HIP device is available");
+  if (device < 0 || device >= count) return fail(QI_HIP_UNSUPPORTED, "HIP device ordinal out of range");
+  hipDeviceProp_t prop;
+  e = hipGetDeviceProperties(&prop, device);
+  if (e != hipSuccess) return hip_fail(e, "device properties");
+  if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+    return fail(QI_HIP_UNSUPPORTED, std::string("device is ") + prop.gcnArchName + ", gfx950 is required");
+  e = hipSetDevice(device);
+  if (e != hipSuccess) return hip_fail(e, "set device");
+  qi_hip_ctx* c = new qi_hip_ctx();
+  c->device = device;
+  c->name = prop.name;
+  e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
+  if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&c->partials), kPartialsFloats * 4);
+  if (e == hipSuccess) {
+    c->partials_cap = kPartialsFloats;
+    e = hipMalloc(reinterpret_cast<void**>(&c->tickets), kTickets * 4);
+  }
+  if (e == hipSuccess) {
+    c->tickets_cap = kTickets;
+    e = hipMemset(c->tickets, 0, kTickets * 4);
+  }
+  if (e == hipSuccess) e = hipDeviceSynchronize();
+  if (e != hipSuccess) {
+    qi_hip_close(c);
+    return hip_fail(e, "context setup");
+  }
+  *out = c;
+  return QI_HIP_OK;
+}
+
+void qi_hip_close(qi_hip_ctx* c) {
+  if (c == nullptr) return;
+  (void)hipSetDevice(c->device);
+  if (c->stream) (void)hipStreamSynchronize(c->stream);
+  if (c->partials) (void)hipFree(c->partials);
+  if (c->tickets) (void)hipFree(c->tickets);
+  if (c->xbuf) (void)hipFree(c->xbuf);
+  if (c->ybuf) (void)hipFree(c->ybuf);
+  if (c->stream) (void)hipStreamDestroy(c->stream);
+  delete c;
+}
+
+qi_hip_status qi_hip_device_name(qi_hip_ctx* c, char* buf, size_t len) {
+  if (c == nullptr || buf == nullptr || len == 0) return fail(QI_HIP_INVALID_INPUT, "null argument");
+  strncpy(buf, c->name.c_str(), len - 1);
+  buf[len - 1] = '\0';
+  return QI_HIP_OK;
+}
+
+qi_hip_status qi_hip_pack_weights(int32_t qtype, int32_t layout, uint64_t k, uint64_t n,
+                                  const void* blocks, uint64_t count, void* out, uint64_t* bytes,
+                                  int32_t* f16_scales) {
+  if (bytes == nullptr) return fail(QI_HIP_INVALID_INPUT, "null size pointer");
+  Image im;
+  const char* why = "";
+  qi_hip_status s = qi::plan_image(qtype, layout, k, n, blocks, count, &im, &why);
+  if (s != QI_HIP_OK) return fail(s, why);
+  if (out != nullptr) {
+    if (*bytes < im.bytes) return fail(QI_HIP_INVALID_INPUT, "output buffer too small");
+    qi::fill_image(im, blocks, out);
+  }
+  *bytes = im.bytes;
+  if (f16_scales) *f16_scales = im.wide ? 0 : 1;
+  return QI_HIP_OK;
+}
+
+qi_hip_status qi_hip_weights_create(qi_hip_ctx* c, int32_t qtype, int32_t layout, uint64_t k,
+                                    uint64_t n, const void* blocks, uint64_t count,
+                                    qi_hip_weights** out) {
+  if (c == nullptr || out == nullptr) return fail(QI_HIP_INVALID_INPUT, "null context or output");
+  *out = nullptr;
+  Image im;
+  const char* why = "";
+  qi_hip_status s = qi::plan_image(qtype, layout, k, n, blocks, count, &im, &why);
+  if (s != QI_HIP_OK) return fail(s, why);
+  std::lock_guard<std::mutex> lock(c->mu);
+  QI_HIP_TRY(hipSetDevice(c->device), "set device");
+  void* host = nullptr;
+  QI_HIP_TRY(hipHostMalloc(&host, im.bytes, hipHostMallocDefault), "pinned staging");
+  qi::fill_image(im, blocks, host);
+  void* dev = nullptr;
+  hipError_t e = hipMalloc(&dev, im.bytes);
+  if (e == hipSuccess) e = hipMemcpyAsync(dev, host, im.bytes, hipMemcpyHostToDevice, c->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+  (void)hipHostFree(host);
+  if (e != hipSuccess) {
+    if (dev) (void)hipFree(dev);
+    return hip_fail(e, "upload weights");
+  }
+  qi_hip_weights* w = new qi_hip_weights();
+  w->ctx = c;
+  w->im = im;
+  w->dev = dev;
+  *out = w;
+  return QI_HIP_OK;
+}
+
+void qi_hip_weights_free(qi_hip_weights* w) {
+  if (w == nullptr) return;
+  if (w->ctx) {
+    std::lock_guard<std::mutex> lock(w->ctx->mu);
+    (void)hipSetDevice(w->ctx->device);
+    (void)hipStreamSynchronize(w->ctx->stream);
+    if (w->dev) (void)hipFree(w->dev);
+  }
+  delete w;
+}
+
+qi_hip_status qi_hip_weights_info_get(const qi_hip_weights* w, qi_hip_weights_info* out) {
+  if (w == nullptr || out == nullptr) return fail(QI_HIP_INVALID_INPUT, "null argument");
+  out->qtype = w->im.qtype;
+  out->layout = w->im.layout;
+  out->k = w->im.k;
+  out->n = w->im.n;
+  out->device_bytes = w->im.bytes;
+  out->f16_scales = w->im.wide ? 0 : 1;
+  return QI_HIP_OK;
+}
+
+qi_hip_status qi_hip_linear(qi_hip_ctx* c, const qi_hip_weights* w, const float* x_host, uint64_t m,
+                            float* y_host, int32_t mode) {
+  qi_hip_status s = check_call(c, w, m);
+  if (s != QI_HIP_OK) return s;
+  if (x_host == nullptr || y_host == nullptr) return fail(QI_HIP_INVALID_INPUT, "null activation buffer");
+  std::lock_guard<std::mutex> lock(c->mu);
+  QI_HIP_TRY(hipSetDevice(c->device), "set device");
+  const uint64_t xn = m * w->im.k, yn = m * w->im.n;
+  if ((s = grow(&c->xbuf, &c->xcap, xn + 64, "alloc activations")) != QI_HIP_OK) return s;
+  if ((s = grow(&c->ybuf, &c->ycap, yn, "alloc outputs")) != QI_HIP_OK) return s;
+  QI_HIP_TRY(hipMemcpyAsync(c->xbuf, x_host, xn * 4, hipMemcpyHostToDevice, c->stream), "copy x");
+  s = run_linear(c, w, c->xbuf, m, c->ybuf, mode, c->stream);
+  if (s != QI_HIP_OK) return s;
+  QI_HIP_TRY(hipMemcpyAsync(y_host, c->ybuf, yn * 4, hipMemcpyDeviceToHost, c->stream), "copy y");
+  QI_HIP_TRY(hipStreamSynchronize(c->stream), "synchronize");
+  return QI_HIP_OK;
+}
+
+qi_hip_status qi_hip_linear_device(qi_hip_ctx* c, const qi_hip_weights* w, const float* x_dev,
+                                   uint64_t m, float* y_dev, int32_t mode, void* stream) {
+  qi_hip_status s = check_call(c, w, m);
+  if (s != QI_HIP_OK) return s;
+  if (x_dev == nullptr || y_dev == nullptr) return fail(QI_HIP_INVALID_INPUT, "null activation buffer");
+  std::lock_guard<std::mutex> lock(c->mu);
+  QI_HIP_TRY(hipSetDevice(c->device), "set device");
+  hipStream_t st = stream ? static_cast<hipStream_t>(stream) : c->stream;
+  return run_linear(c, w, x_dev, m, y_dev, mode, st);
+}
+
+qi_hip_status qi_hip_dequantize_device(qi_hip_ctx* c, const qi_hip_weights* w, float* out_dev,
+                                       void* stream) {
+  if (c == nullptr || w == nullptr || out_dev == nullptr) return fail(QI_HIP_INVALID_INPUT, "null argument");
+  if (w->ctx != c) return fail(QI_HIP_INVALID_INPUT, "weights belong to another context");
+  std::lock_guard<std::mutex> lock(c->mu);
+  QI_HIP_TRY(hipSetDevice(c->device), "set device");
+  hipStream_t st = stream ? static_cast<hipStream_t>(stream) : c->stream;
+  QI_HIP_TRY(qi::launch_dequant(w->im, qi::make_view(w->im, w->dev), out_dev, st), "launch dequant");
+  return QI_HIP_OK;
+}
+
+qi_hip_status qi_hip_dequantize(qi_hip_ctx* c, const qi_hip_weights* w, float* out_host) {
+  if (c == nullptr || w == nullptr || out_host == nullptr) return fail(QI_HIP_INVALID_INPUT, "null argument");
+  if (w->ctx != c) return fail(QI_HIP_INVALID_INPUT, "weights belong to another context");
+  std::lock_guard<std::mutex> lock(c->mu);
+  QI_HIP_TRY(hipSetDevice(c->device), "set device");
+  const uint64_t n = w->im.k * w->im.n;
+  float* tmp = nullptr;
+  QI_HIP_TRY(hipMalloc(reinterpret_cast<void**>(&tmp), n * 4), "alloc dequant output");
+  hipError_t e = qi::launch_dequant(w->im, qi::make_view(w->im, w->dev), tmp, c->stream);
+  if (e == hipSuccess) e = hipMemcpyAsync(out_host, tmp, n * 4, hipMemcpyDeviceToHost, c->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+  (void)hipFree(tmp);
+  if (e != hipSuccess) return hip_fail(e, "dequantize");
+  return QI_HIP_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,45 @@
+// Kernel launchers shared between the ABI layer and the kernel translation units.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "qi_image.h"
+
+namespace qi {
+
+struct GemvArgs {
+  View w;
+  const float* x;       // [m, k] device
+  float* y;             // [m, n] device
+  int m;                // activation rows in this launch (<= compile-time tile)
+  uint32_t slots_per_split;
+  float* partials;      // [splits, m, n] workspace (split-K only)
+  uint32_t* tickets;    // one per row tile, zero between launches
+};
+
+struct GemvPlan {
+  uint32_t row_tiles = 0, splits = 1, slots_per_split = 0;
+};
+
+int gemv_tile_rows(int mt);
+int gemv_slot_elems(int32_t qtype);
+GemvPlan plan_gemv(int32_t qtype, uint64_t k, uint64_t n, int mt, uint64_t max_partials);
+hipError_t launch_gemv(int32_t qtype, bool wide, int mt, const GemvArgs& a, const GemvPlan& plan,
+                       hipStream_t st);
+
+// Exact-order matmul: bit-identical to CpuScalar (any M, either layout).
+hipError_t launch_exact(const Image& im, const View& w, const float* x, uint64_t m, float* y,
+                        hipStream_t st);
+// Bit-exact dequantization in block order.
+hipError_t launch_dequant(const Image& im, const View& w, float* out, hipStream_t st);
+
+struct GemmArgs {
+  View w;
+  const float* x;  // [m, k] f32 device
+  float* y;        // [m, n]
+  uint64_t m;
+};
+bool gemm_supported(int32_t qtype, int32_t layout, uint64_t k, uint64_t n);
+hipError_t launch_gemm(const Image& im, const GemmArgs& a, hipStream_t st);
+
+}  // namespace qi

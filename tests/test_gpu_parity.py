@@ -1,0 +1,273 @@
+"""GPU parity of the HIP path against the oracle, through the C ABI.
+
+Bars:
+- dequantize: bit-exact against the reference dequantize_* (oracle) for
+  every block type, f16 and f32 scale planes, subnormal f16 scales included;
+- EXACT mode: bit-identical to CpuScalar (oracle) in both layouts;
+- F32 mode (the decode GEMV): max_i |y_i - e_i| / max(|e_i|, 2^-10 sum_k |x_k w_ik|)
+  <= 1e-5 against the f64 product of the dequantized weights (e), and the
+  reference bound |y - e| < 1e-4 + 1e-5|e| (runtime/src/linear/tests.rs:152).
+"""
+import numpy as np
+import pytest
+
+import quantinfer_amd as qa
+from oracle import pyoracle as po
+from tests.helpers import (blocks_from_dicts, guarded_rel_err, lhs_from_case, load_golden,
+                           reference_bound_ok)
+
+pytestmark = pytest.mark.gpu
+
+ALL_Q = [qa.Q8_0, qa.Q4_0, qa.Q4_K, qa.Q5_K, qa.Q6_K]
+NAMES = {qa.Q8_0: "q8_0", qa.Q4_0: "q4_0", qa.Q4_K: "q4_k", qa.Q5_K: "q5_k", qa.Q6_K: "q6_k"}
+F32_TOL = 1e-5
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    c = qa.Context(0)
+    yield c
+    c.close()
+
+
+def _wide_blocks(qtype, count, seed):
+    """Random codes with f32 scales that are not f16-representable (as the
+    reference's hand-built test blocks, e.g. scale 0.1)."""
+    rng = np.random.default_rng(seed)
+    raw = rng.integers(0, 256, size=(count, po.BLOCK_DTYPES[qtype].itemsize), dtype=np.uint8)
+    b = raw.view(po.BLOCK_DTYPES[qtype]).ravel().copy()
+    b["scale"] = (rng.standard_normal(count) * 0.01 + 0.001).astype(np.float32)
+    b["scale"] += np.float32(1e-9)
+    if "min_scale" in b.dtype.names:
+        b["min_scale"] = (rng.standard_normal(count) * 0.01).astype(np.float32)
+    if qtype == po.Q4_0:
+        b["values"] &= 15
+    return b
+
+
+def _f64_check(y, x, blocks, qtype, n):
+    k = x.shape[1]
+    w = po.dequantize(qtype, blocks).reshape(n, k)
+    exact = x.astype(np.float64) @ w.astype(np.float64).T
+    err = guarded_rel_err(y, exact, x, w)
+    return err, reference_bound_ok(y, exact)
+
+
+# ------------------------------------------------------------------ dequant
+
+@pytest.mark.parametrize("qtype", ALL_Q, ids=lambda q: NAMES[q])
+def test_dequant_bit_exact_f16_scales(ctx, qtype):
+    k, n = 1024, 48
+    blocks = po.make_weights(qtype, k, n, seed=1000 + qtype, outliers=True)
+    w = ctx.weights(qtype, qa.OUTPUT_ROWS, k, n, blocks)
+    assert w.info().f16_scales == 1
+    assert w.dequantize().tobytes() == po.dequantize(qtype, blocks).tobytes()
+
+
+@pytest.mark.parametrize("qtype", ALL_Q, ids=lambda q: NAMES[q])
+def test_dequant_bit_exact_f32_scales(ctx, qtype):
+    bs = po.BLOCK_ELEMS[qtype]
+    blocks = _wide_blocks(qtype, 64, 7 + qtype)
+    w = ctx.weights(qtype, qa.OUTPUT_ROWS, bs * 8, 8, blocks)
+    assert w.info().f16_scales == 0
+    assert w.dequantize().tobytes() == po.dequantize(qtype, blocks).tobytes()
+
+
+@pytest.mark.parametrize("qtype", [qa.Q4_K, qa.Q5_K, qa.Q6_K], ids=lambda q: NAMES[q])
+def test_dequant_bit_exact_subnormal_f16_scales(ctx, qtype):
+    # N(0, 0.02^2) weights give Q5_K/Q6_K super-block scales below f16's
+    # smallest normal (6.1e-5); Q4_K gets there with a smaller weight scale.
+    vals = po.fill_normal(77, 256 * 64, 0.02 if qtype != qa.Q4_K else 0.002)
+    blocks = po.quantize(qtype, vals)
+    assert np.any(blocks["scale"] < 6.103515625e-05), "fixture must contain subnormal d"
+    w = ctx.weights(qtype, qa.OUTPUT_ROWS, 256 * 8, 8, blocks)
+    assert w.dequantize().tobytes() == po.dequantize(qtype, blocks).tobytes()
+
+
+# --------------------------------------------------------------- exact mode
+
+@pytest.mark.parametrize("qtype", ALL_Q, ids=lambda q: NAMES[q])
+@pytest.mark.parametrize("m", [1, 3])
+def test_exact_mode_output_rows_bit_identical(ctx, qtype, m):
+    k, n = 512, 40
+    blocks = po.make_weights(qtype, k, n, seed=2000 + qtype, outliers=True)
+    x = po.fill_normal(3000 + m, m * k).reshape(m, k)
+    w = ctx.weights(qtype, qa.OUTPUT_ROWS, k, n, blocks)
+    y = w.linear(x, qa.MODE_EXACT)
+    assert y.tobytes() == po.matmul_output_rows(qtype, x, blocks, n).tobytes()
+
+
+@pytest.mark.parametrize("qtype", ALL_Q, ids=lambda q: NAMES[q])
+def test_exact_mode_row_major_bit_identical(ctx, qtype):
+    k, n, m = 48 if qtype in (qa.Q8_0, qa.Q4_0) else 64, 256, 2
+    blocks = po.make_weights(qtype, k, n, seed=2100 + qtype)
+    x = po.fill_normal(3100, m * k).reshape(m, k)
+    w = ctx.weights(qtype, qa.ROW_MAJOR, k, n, blocks)
+    for mode in (qa.MODE_EXACT, qa.MODE_AUTO, qa.MODE_F32):
+        y = w.linear(x, mode)
+        assert y.tobytes() == po.matmul_row_major(qtype, x, blocks, n).tobytes()
+
+
+def test_exact_mode_f32_weights_bit_identical(ctx):
+    k, n = 300, 1000
+    wt = po.fill_normal(5, k * n, 0.02).reshape(k, n)
+    for m in (1, 3, 17):
+        x = po.fill_normal(6 + m, m * k).reshape(m, k)
+        w = ctx.weights(qa.F32, qa.ROW_MAJOR, k, n, wt)
+        assert w.linear(x, qa.MODE_AUTO).tobytes() == po.matmul_f32(x, wt).tobytes()
+
+
+def test_exact_mode_wide_scales_bit_identical(ctx):
+    for qtype in ALL_Q:
+        bs = po.BLOCK_ELEMS[qtype]
+        blocks = _wide_blocks(qtype, 32, 40 + qtype)
+        k, n = bs * 4, 8
+        x = po.fill_normal(41, 2 * k).reshape(2, k)
+        w = ctx.weights(qtype, qa.OUTPUT_ROWS, k, n, blocks)
+        assert w.linear(x, qa.MODE_EXACT).tobytes() == \
+            po.matmul_output_rows(qtype, x, blocks, n).tobytes()
+
+
+def test_reference_known_answers_on_gpu(ctx):
+    cases = {c["name"]: c for c in load_golden()["known_answers"]}
+    for name in ("q8_0_ones_scale_two", "q4_0_code_eight_is_zero", "q4_k_0x99", "q5_k_0x99"):
+        c = cases[name]
+        q = po.QTYPES[c["qtype"]]
+        blocks = blocks_from_dicts(q, c["blocks"])
+        x = lhs_from_case(c)
+        k, n = c["rhs_shape"]
+        for layout in (qa.ROW_MAJOR, qa.OUTPUT_ROWS):
+            w = ctx.weights(q, layout, k, n, blocks)
+            for mode in (qa.MODE_EXACT, qa.MODE_F32):
+                y = w.linear(x, mode)
+                if c["expect"] == "equal":
+                    assert y.ravel().tolist() == c["expected"], (name, layout, mode)
+                else:
+                    assert y.ravel()[0] > c["bound"]
+                    assert y.ravel()[0] == po.matmul_row_major(q, x, blocks, n).ravel()[0] or \
+                        mode == qa.MODE_F32
+    c = cases["threaded_q8_equals_scalar"]
+    blocks = blocks_from_dicts(qa.Q8_0, c["blocks"])
+    w = ctx.weights(qa.Q8_0, qa.OUTPUT_ROWS, 32, 1, blocks)
+    assert w.linear(lhs_from_case(c), qa.MODE_F32).ravel().tolist() == c["expected"]
+
+
+# ---------------------------------------------------------- F32 GEMV path
+
+@pytest.mark.parametrize("qtype", ALL_Q, ids=lambda q: NAMES[q])
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 8, 11, 16, 17, 40])
+def test_f32_gemv_tolerance_small(ctx, qtype, m):
+    k, n = 1024, 70  # n not a multiple of the row tile: exercises the ragged tile
+    blocks = po.make_weights(qtype, k, n, seed=4000 + qtype, outliers=True)
+    x = po.fill_normal(5000 + m, m * k).reshape(m, k)
+    w = ctx.weights(qtype, qa.OUTPUT_ROWS, k, n, blocks)
+    y = w.linear(x, qa.MODE_F32)
+    err, ok = _f64_check(y, x, blocks, qtype, n)
+    assert err <= F32_TOL and ok, err
+
+
+@pytest.mark.parametrize("qtype", ALL_Q, ids=lambda q: NAMES[q])
+def test_f32_gemv_split_k_deterministic(ctx, qtype):
+    # few output rows and a long K force split-K with the last-block reduction
+    k, n = 14336, 12
+    blocks = po.make_weights(qtype, k, n, seed=4100 + qtype, outliers=True)
+    w = ctx.weights(qtype, qa.OUTPUT_ROWS, k, n, blocks)
+    for m in (1, 8, 16):
+        x = po.fill_normal(4200 + m, m * k).reshape(m, k)
+        y = w.linear(x, qa.MODE_F32)
+        err, ok = _f64_check(y, x, blocks, qtype, n)
+        assert err <= F32_TOL and ok, (m, err)
+        for _ in range(3):
+            assert w.linear(x, qa.MODE_F32).tobytes() == y.tobytes()
+
+
+def test_f32_gemv_unrounded_scales(ctx):
+    # quantize_q8_0 output without storage rounding keeps f32 scales
+    for qtype in (qa.Q8_0, qa.Q4_0):
+        blocks = po.quantize(qtype, po.fill_normal(4300, 2048 * 33, 0.02))
+        w = ctx.weights(qtype, qa.OUTPUT_ROWS, 2048, 33, blocks)
+        assert w.info().f16_scales == 0
+        x = po.fill_normal(4301, 3 * 2048).reshape(3, 2048)
+        err, ok = _f64_check(w.linear(x, qa.MODE_F32), x, blocks, qtype, 33)
+        assert err <= F32_TOL and ok
+
+
+# ------------------------------------------------ BASELINE.json config shapes
+
+CONFIGS = [
+    # (qtype, K, N, M list, outliers) -- configs[0..2] of BASELINE.json
+    (qa.Q8_0, 4096, 4096, [1], False),
+    (qa.Q4_0, 4096, 4096, [1, 4, 16], False),
+    (qa.Q4_0, 4096, 1024, [1, 4, 16], False),
+    (qa.Q4_0, 4096, 12288, [1, 4, 16], False),
+    (qa.Q4_0, 12288, 4096, [1, 4, 16], False),
+    (qa.Q4_K, 4096, 14336, [1, 8], True),
+    (qa.Q4_K, 14336, 4096, [1, 8], True),
+    (qa.Q5_K, 4096, 14336, [1, 8], True),
+    (qa.Q5_K, 14336, 4096, [1, 8], True),
+    (qa.Q6_K, 4096, 14336, [1, 8], True),
+    (qa.Q6_K, 14336, 4096, [1, 8], True),
+    (qa.Q8_0, 4096, 14336, [1], False),
+]
+
+
+@pytest.mark.parametrize("cfg", CONFIGS, ids=lambda c: f"{NAMES[c[0]]}-K{c[1]}-N{c[2]}")
+def test_config_shapes_f32_tolerance(ctx, cfg):
+    qtype, k, n, ms, outliers = cfg
+    blocks = po.make_weights(qtype, k, n, seed=0x5EED0000 + qtype, outliers=outliers)
+    w = ctx.weights(qtype, qa.OUTPUT_ROWS, k, n, blocks)
+    wd = po.dequantize(qtype, blocks).reshape(n, k).astype(np.float64)
+    absw = np.abs(wd)
+    for m in ms:
+        x = po.fill_normal(0x5EED1000 + m, m * k).reshape(m, k)
+        y = w.linear(x, qa.MODE_F32)
+        exact = x.astype(np.float64) @ wd.T
+        denom = np.maximum(np.abs(exact), (np.abs(x.astype(np.float64)) @ absw.T) * 2.0 ** -10)
+        err = float(np.max(np.abs(y - exact) / denom))
+        assert err <= F32_TOL, (m, err)
+        assert reference_bound_ok(y, exact)
+
+
+def test_config_q4_k_exact_mode_full_size(ctx):
+    k, n = 4096, 14336
+    blocks = po.make_weights(qa.Q4_K, k, n, seed=0x5EED0003, outliers=True)
+    x = po.fill_normal(0x5EED2001, k).reshape(1, k)
+    w = ctx.weights(qa.Q4_K, qa.OUTPUT_ROWS, k, n, blocks)
+    assert w.linear(x, qa.MODE_EXACT).tobytes() == \
+        po.matmul_output_rows(qa.Q4_K, x, blocks, n, threads=8).tobytes()
+
+
+# ------------------------------------------------------------ ABI behaviour
+
+def test_linear_device_matches_host_path(ctx):
+    torch = pytest.importorskip("torch")
+    k, n, m = 4096, 512, 3
+    blocks = po.make_weights(qa.Q4_K, k, n, seed=9, outliers=True)
+    w = ctx.weights(qa.Q4_K, qa.OUTPUT_ROWS, k, n, blocks)
+    x = po.fill_normal(10, m * k).reshape(m, k)
+    xd = torch.from_numpy(x).to("cuda:0")
+    yd = torch.empty((m, n), dtype=torch.float32, device="cuda:0")
+    stream = torch.cuda.current_stream().cuda_stream
+    w.linear_device(xd.data_ptr(), m, yd.data_ptr(), qa.MODE_F32, stream)
+    torch.cuda.synchronize()
+    assert yd.cpu().numpy().tobytes() == w.linear(x, qa.MODE_F32).tobytes()
+    out = torch.empty(k * n, dtype=torch.float32, device="cuda:0")
+    w.dequantize_device(out.data_ptr(), stream)
+    torch.cuda.synchronize()
+    assert out.cpu().numpy().tobytes() == po.dequantize(qa.Q4_K, blocks).tobytes()
+
+
+def test_gpu_error_paths(ctx):
+    blocks = po.make_weights(qa.Q8_0, 64, 4, seed=1)
+    w = ctx.weights(qa.Q8_0, qa.OUTPUT_ROWS, 64, 4, blocks)
+    lib = qa.lib()
+    x = np.ones((1, 64), dtype=np.float32)
+    y = np.empty((1, 4), dtype=np.float32)
+    assert lib.qi_hip_linear(ctx.handle, w.handle, x.ctypes.data, 0, y.ctypes.data, 0) == qa.INVALID_INPUT
+    assert lib.qi_hip_linear(ctx.handle, w.handle, x.ctypes.data, 1, y.ctypes.data, 9) == qa.INVALID_INPUT
+    with pytest.raises(ValueError):
+        w.linear(np.ones((1, 32), dtype=np.float32))
+    with qa.Context(0) as other:
+        assert lib.qi_hip_linear(other.handle, w.handle, x.ctypes.data, 1, y.ctypes.data, 0) == \
+            qa.INVALID_INPUT
+    assert ctx.device_name()
