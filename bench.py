@@ -44,52 +44,57 @@ def traffic_from_profile(name: str):
 
 
 def gpu_measure(qtype: int, steps: int, warmup: int, copies_mb: float = 512.0):
-    import numpy as np
-    import torch
-
     import quantinfer_amd as qa
     from oracle import pyoracle as po  # input generation only (the quantizer restatement)
+    from quantinfer_amd import hiprt
 
     ctx = qa.Context(0)
     blocks = po.make_weights(qtype, K, N, seed=0x5EED0000 + qtype, outliers=qtype >= 3)
     wbytes = N * (K // BLOCK[qtype]) * WIRE[qtype]
     copies = max(1, int(-(-copies_mb * 1e6 // wbytes)))
     weights = [ctx.weights(qtype, qa.OUTPUT_ROWS, K, N, blocks) for _ in range(copies)]
-    x = torch.from_numpy(po.fill_normal(0x5EED1000, M * K).reshape(M, K)).to("cuda:0")
-    y = torch.empty((M, N), dtype=torch.float32, device="cuda:0")
-    stream = torch.cuda.current_stream()
-    sptr = stream.cuda_stream
+    x = hiprt.DeviceBuffer.from_array(po.fill_normal(0x5EED1000, M * K).reshape(M, K))
+    y = hiprt.DeviceBuffer(M * N * 4)
+    stream = hiprt.Stream()
 
     def step(i):
-        weights[i % copies].linear_device(x.data_ptr(), M, y.data_ptr(), qa.MODE_F32, sptr)
+        weights[i % copies].linear_device(x.ptr, M, y.ptr, qa.MODE_F32, stream.handle)
 
     for i in range(warmup):
         step(i)
-    torch.cuda.synchronize()
+    stream.synchronize()
 
-    # timed region: `steps` back-to-back GEMVs, bracketed by events on the launch stream
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
+    # timed region: `steps` back-to-back GEMVs, bracketed by HIP events on the
+    # stream the kernels are launched on
+    start, end = hiprt.Event(), hiprt.Event()
+    hiprt.synchronize()
     start.record(stream)
     for i in range(steps):
         step(i)
     end.record(stream)
-    torch.cuda.synchronize()
-    region_ms = start.elapsed_time(end)
+    stream.synchronize()
+    region_ms = start.elapsed_ms(end)
 
-    # per-launch kernel duration (events around each launch on the same stream)
-    pairs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-             for _ in range(steps)]
+    # per-launch kernel duration: an event pair around each launch
+    pairs = [(hiprt.Event(), hiprt.Event()) for _ in range(steps)]
     for i, (a, b) in enumerate(pairs):
         a.record(stream)
         step(i)
         b.record(stream)
-    torch.cuda.synchronize()
-    kernel_ms = statistics.median(a.elapsed_time(b) for a, b in pairs)
+    stream.synchronize()
+    kernel_ms = statistics.median(a.elapsed_ms(b) for a, b in pairs)
 
     name = ctx.device_name()
+    for a, b in pairs:
+        a.destroy()
+        b.destroy()
+    start.destroy()
+    end.destroy()
     for w in weights:
         w.free()
+    x.free()
+    y.free()
+    stream.destroy()
     ctx.close()
     return {"region_ms": region_ms, "kernel_ms": kernel_ms, "copies": copies, "device": name}
 

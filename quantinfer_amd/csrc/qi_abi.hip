@@ -9,6 +9,7 @@
 #include <hip/hip_runtime.h>
 #include <string.h>
 
+#include <atomic>
 #include <mutex>
 #include <string>
 
@@ -18,7 +19,12 @@
 
 using qi::Image;
 
+// A context is reference counted: the caller's handle and every live weights
+// handle hold one reference, so qi_hip_close and qi_hip_weights_free may come
+// in any order; the stream and workspace go away with the last reference.
 struct qi_hip_ctx {
+  std::atomic<int> refs{1};
+  bool closed = false;
   int device = 0;
   hipStream_t stream = nullptr;
   std::mutex mu;
@@ -84,8 +90,24 @@ qi_hip_status ensure_tickets(qi_hip_ctx* c, uint64_t need) {
   return QI_HIP_OK;
 }
 
+void ctx_destroy(qi_hip_ctx* c) {
+  (void)hipSetDevice(c->device);
+  if (c->stream) (void)hipStreamSynchronize(c->stream);
+  if (c->partials) (void)hipFree(c->partials);
+  if (c->tickets) (void)hipFree(c->tickets);
+  if (c->xbuf) (void)hipFree(c->xbuf);
+  if (c->ybuf) (void)hipFree(c->ybuf);
+  if (c->stream) (void)hipStreamDestroy(c->stream);
+  delete c;
+}
+
+void ctx_release(qi_hip_ctx* c) {
+  if (c->refs.fetch_sub(1, std::memory_order_acq_rel) == 1) ctx_destroy(c);
+}
+
 qi_hip_status check_call(qi_hip_ctx* ctx, const qi_hip_weights* w, uint64_t m) {
   if (ctx == nullptr || w == nullptr) return fail(QI_HIP_INVALID_INPUT, "null context or weights");
+  if (ctx->closed) return fail(QI_HIP_INVALID_INPUT, "context is closed");
   if (w->ctx != ctx) return fail(QI_HIP_INVALID_INPUT, "weights belong to another context");
   // lhs rows must be nonzero (core tensor.rs:85-93); grid.y limits exact-mode rows
   if (m == 0) return fail(QI_HIP_INVALID_INPUT, "matmul lhs must have at least one row");
@@ -164,7 +186,7 @@ qi_hip_status qi_hip_open(int32_t device, qi_hip_ctx** out) {
   if (e != hipSuccess) return hip_fail(e, "set device");
   qi_hip_ctx* c = new qi_hip_ctx();
   c->device = device;
-  c->name = prop.name;
+  c->name = prop.name[0] ? std::string(prop.name) : std::string("AMD ") + prop.gcnArchName;
   e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
   if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&c->partials), kPartialsFloats * 4);
   if (e == hipSuccess) {
@@ -177,7 +199,7 @@ qi_hip_status qi_hip_open(int32_t device, qi_hip_ctx** out) {
   }
   if (e == hipSuccess) e = hipDeviceSynchronize();
   if (e != hipSuccess) {
-    qi_hip_close(c);
+    ctx_destroy(c);
     return hip_fail(e, "context setup");
   }
   *out = c;
@@ -186,14 +208,12 @@ qi_hip_status qi_hip_open(int32_t device, qi_hip_ctx** out) {
 
 void qi_hip_close(qi_hip_ctx* c) {
   if (c == nullptr) return;
-  (void)hipSetDevice(c->device);
-  if (c->stream) (void)hipStreamSynchronize(c->stream);
-  if (c->partials) (void)hipFree(c->partials);
-  if (c->tickets) (void)hipFree(c->tickets);
-  if (c->xbuf) (void)hipFree(c->xbuf);
-  if (c->ybuf) (void)hipFree(c->ybuf);
-  if (c->stream) (void)hipStreamDestroy(c->stream);
-  delete c;
+  {
+    std::lock_guard<std::mutex> lock(c->mu);
+    if (c->closed) return;  // a second close of the same handle is a no-op
+    c->closed = true;
+  }
+  ctx_release(c);
 }
 
 qi_hip_status qi_hip_device_name(qi_hip_ctx* c, char* buf, size_t len) {
@@ -225,6 +245,7 @@ qi_hip_status qi_hip_weights_create(qi_hip_ctx* c, int32_t qtype, int32_t layout
                                     qi_hip_weights** out) {
   if (c == nullptr || out == nullptr) return fail(QI_HIP_INVALID_INPUT, "null context or output");
   *out = nullptr;
+  if (c->closed) return fail(QI_HIP_INVALID_INPUT, "context is closed");
   Image im;
   const char* why = "";
   qi_hip_status s = qi::plan_image(qtype, layout, k, n, blocks, count, &im, &why);
@@ -244,6 +265,7 @@ qi_hip_status qi_hip_weights_create(qi_hip_ctx* c, int32_t qtype, int32_t layout
     return hip_fail(e, "upload weights");
   }
   qi_hip_weights* w = new qi_hip_weights();
+  c->refs.fetch_add(1, std::memory_order_relaxed);
   w->ctx = c;
   w->im = im;
   w->dev = dev;
@@ -253,11 +275,15 @@ qi_hip_status qi_hip_weights_create(qi_hip_ctx* c, int32_t qtype, int32_t layout
 
 void qi_hip_weights_free(qi_hip_weights* w) {
   if (w == nullptr) return;
-  if (w->ctx) {
-    std::lock_guard<std::mutex> lock(w->ctx->mu);
-    (void)hipSetDevice(w->ctx->device);
-    (void)hipStreamSynchronize(w->ctx->stream);
-    if (w->dev) (void)hipFree(w->dev);
+  qi_hip_ctx* c = w->ctx;
+  if (c) {
+    {
+      std::lock_guard<std::mutex> lock(c->mu);
+      (void)hipSetDevice(c->device);
+      (void)hipStreamSynchronize(c->stream);
+      if (w->dev) (void)hipFree(w->dev);
+    }
+    ctx_release(c);
   }
   delete w;
 }
@@ -305,6 +331,7 @@ qi_hip_status qi_hip_linear_device(qi_hip_ctx* c, const qi_hip_weights* w, const
 qi_hip_status qi_hip_dequantize_device(qi_hip_ctx* c, const qi_hip_weights* w, float* out_dev,
                                        void* stream) {
   if (c == nullptr || w == nullptr || out_dev == nullptr) return fail(QI_HIP_INVALID_INPUT, "null argument");
+  if (c->closed) return fail(QI_HIP_INVALID_INPUT, "context is closed");
   if (w->ctx != c) return fail(QI_HIP_INVALID_INPUT, "weights belong to another context");
   std::lock_guard<std::mutex> lock(c->mu);
   QI_HIP_TRY(hipSetDevice(c->device), "set device");
@@ -315,6 +342,7 @@ qi_hip_status qi_hip_dequantize_device(qi_hip_ctx* c, const qi_hip_weights* w, f
 
 qi_hip_status qi_hip_dequantize(qi_hip_ctx* c, const qi_hip_weights* w, float* out_host) {
   if (c == nullptr || w == nullptr || out_host == nullptr) return fail(QI_HIP_INVALID_INPUT, "null argument");
+  if (c->closed) return fail(QI_HIP_INVALID_INPUT, "context is closed");
   if (w->ctx != c) return fail(QI_HIP_INVALID_INPUT, "weights belong to another context");
   std::lock_guard<std::mutex> lock(c->mu);
   QI_HIP_TRY(hipSetDevice(c->device), "set device");

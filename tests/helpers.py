@@ -29,15 +29,27 @@ def lhs_from_case(case):
     return np.asarray(case["lhs"], dtype=np.float32).reshape(shape)
 
 
-def guarded_rel_err(actual, exact, x, w_deq):
-    """max_i |a_i - e_i| / max(|e_i|, 2^-10 * sum_k |x_k w_ik|).
+KAPPA_CAP = 64.0
 
-    `exact` is the f64 product of x and the dequantized weights; the floor keeps
-    the ratio meaningful for outputs that cancel to near zero."""
+
+def guarded_rel_err(actual, exact, x, w_deq):
+    """max_i |a_i - e_i| / max(|e_i|, sum_k |x_k w_ik| / 64).
+
+    `exact` is the f64 product of x and the dequantized weights. Relative error
+    for outputs whose dot-product condition number sum|x w| / |e| is at most 64;
+    beyond that the error is measured against sum|x w| / 64, because no f32
+    summation order (the CPU reference's included) is accurate to 1e-5
+    relative on an output that cancels further."""
     absdot = np.abs(x.astype(np.float64)) @ np.abs(w_deq.astype(np.float64)).T
-    denom = np.maximum(np.abs(exact), absdot * 2.0 ** -10)
+    denom = np.maximum(np.abs(exact), absdot / KAPPA_CAP)
     denom = np.where(denom == 0, 1.0, denom)
     return float(np.max(np.abs(actual.astype(np.float64) - exact) / denom))
+
+
+def normwise_rel_err(actual, reference):
+    """max_i |a_i - r_i| / max_i |r_i| (r: the CPU reference's f32 result)."""
+    r = reference.astype(np.float64)
+    return float(np.max(np.abs(actual.astype(np.float64) - r)) / max(np.max(np.abs(r)), 1e-300))
 
 
 def reference_bound_ok(actual, exact):
