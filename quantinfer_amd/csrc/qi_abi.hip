@@ -7,6 +7,7 @@
 // overlap (they share the workspace), which holds for every entry point here
 // because each enqueues on a single stream.
 #include <hip/hip_runtime.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include <atomic>
@@ -37,6 +38,7 @@ struct qi_hip_ctx {
   uint64_t xcap = 0;  // floats
   float* ybuf = nullptr;
   uint64_t ycap = 0;
+  int gemv_split = 0;  // QI_HIP_GEMV_SPLIT tuning override (K parts per GEMV workgroup)
 };
 
 struct qi_hip_weights {
@@ -140,9 +142,16 @@ qi_hip_status run_linear(qi_hip_ctx* c, const qi_hip_weights* w, const float* x,
     QI_HIP_TRY(qi::launch_exact(im, v, x, m, y, st), "launch exact matmul");
     return QI_HIP_OK;
   }
+  const bool mfma = qi::gemv_mfma_supported(im.qtype, im.layout, im.k);
   for (uint64_t m0 = 0; m0 < m; m0 += 16) {
     const int rows = static_cast<int>(m - m0 < 16 ? m - m0 : 16);
     const int mt = rows == 1 ? 1 : rows == 2 ? 2 : rows <= 4 ? 4 : rows <= 8 ? 8 : 16;
+    if (mfma) {
+      qi::GemvMfmaArgs ga{v, x + m0 * im.k, y + m0 * im.n, rows};
+      const int split = c->gemv_split > 0 ? c->gemv_split : qi::gemv_mfma_split(im.n);
+      QI_HIP_TRY(qi::launch_gemv_mfma(im.qtype, im.wide != 0, mt, split, ga, st), "launch gemv");
+      continue;
+    }
     qi::GemvPlan plan = qi::plan_gemv(im.qtype, im.k, im.n, mt, c->partials_cap);
     if (plan.splits > 1) {
       qi_hip_status s = ensure_tickets(c, plan.row_tiles);
@@ -186,6 +195,7 @@ qi_hip_status qi_hip_open(int32_t device, qi_hip_ctx** out) {
   if (e != hipSuccess) return hip_fail(e, "set device");
   qi_hip_ctx* c = new qi_hip_ctx();
   c->device = device;
+  if (const char* env = getenv("QI_HIP_GEMV_SPLIT")) c->gemv_split = atoi(env);
   c->name = prop.name[0] ? std::string(prop.name) : std::string("AMD ") + prop.gcnArchName;
   e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
   if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&c->partials), kPartialsFloats * 4);

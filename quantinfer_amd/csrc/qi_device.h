@@ -36,74 +36,148 @@ __device__ __forceinline__ void kquant_sc_m(uint32_t w0, uint32_t w1, uint32_t w
 }
 
 // ---------------------------------------------------------------------------
+// Block byte access for either image arrangement (planar or tiled records).
+
+template <int QT>
+struct Geo {
+  static constexpr uint32_t kCode = QT == kQ8_0 ? 32 : QT == kQ4_0 ? 16 : 128;  // code bytes/block
+  static constexpr uint32_t kQh = QT == kQ5_K ? 32 : QT == kQ6_K ? 64 : 0;
+  static constexpr uint32_t kSc = (QT == kQ4_K || QT == kQ5_K) ? 12 : QT == kQ6_K ? 16 : 0;
+  static constexpr uint32_t kBpu = (QT == kQ8_0 || QT == kQ4_0) ? 8 : 1;  // blocks per unit
+  static constexpr uint32_t kSlice = kCode * kBpu;                          // code bytes/unit/row
+};
+
+struct BlockLoc {
+  const uint8_t* rec;  // tiled: the record; planar: nullptr
+  uint64_t blk;        // planar block index
+  uint32_t col, bi;    // tiled: row within the tile, block within the unit
+};
+
+// Block b of output row n (output-rows layout), or flat block b (n = 0).
+template <int QT>
+__device__ __forceinline__ BlockLoc locate(const View& v, uint64_t n, uint64_t b) {
+  BlockLoc L;
+  if (v.tiled) {
+    const uint64_t u = b / Geo<QT>::kBpu;
+    L.rec = v.qs + ((n / 16) * v.units + u) * v.rec.bytes;
+    L.col = static_cast<uint32_t>(n % 16);
+    L.bi = static_cast<uint32_t>(b % Geo<QT>::kBpu);
+    L.blk = 0;
+  } else {
+    L.rec = nullptr;
+    L.blk = n * v.nb + b;
+    L.col = L.bi = 0;
+  }
+  return L;
+}
+
+template <int QT>
+__device__ __forceinline__ uint8_t code_byte(const View& v, const BlockLoc& L, uint32_t o) {
+  if (L.rec == nullptr) return v.qs[L.blk * Geo<QT>::kCode + o];
+  const uint32_t s = L.bi * Geo<QT>::kCode + o, quarter = Geo<QT>::kSlice / 4;
+  const uint32_t g = s / quarter, q = (s % quarter) / 16, r = s % 16;
+  return L.rec[v.rec.qs + q * 1024 + (16 * g + L.col) * 16 + r];
+}
+
+template <int QT>
+__device__ __forceinline__ uint8_t qh_byte(const View& v, const BlockLoc& L, uint32_t o) {
+  if (L.rec == nullptr) return v.qh[L.blk * Geo<QT>::kQh + o];
+  return L.rec[v.rec.qh + (o / 16) * 256 + L.col * 16 + o % 16];
+}
+
+template <int QT>
+__device__ __forceinline__ uint8_t sc_byte(const View& v, const BlockLoc& L, uint32_t o) {
+  if (L.rec == nullptr) return v.sc[L.blk * Geo<QT>::kSc + o];
+  return L.rec[v.rec.sc + L.col * Geo<QT>::kSc + o];
+}
+
+template <int QT, bool WIDE>
+__device__ __forceinline__ float scale_d(const View& v, const BlockLoc& L) {
+  if (L.rec == nullptr) return load_scale<WIDE>(v.d, L.blk);
+  return load_scale<WIDE>(L.rec + v.rec.d, L.col * Geo<QT>::kBpu + L.bi);
+}
+
+template <int QT, bool WIDE>
+__device__ __forceinline__ float scale_dmin(const View& v, const BlockLoc& L) {
+  if (L.rec == nullptr) return load_scale<WIDE>(v.dmin, L.blk);
+  return load_scale<WIDE>(L.rec + v.rec.dmin, L.col);
+}
+
+// ---------------------------------------------------------------------------
 // Exact per-element values: the reference's f32 operation sequence
 // (backends/cpu/src/matmul.rs:162-280, identical to dequantize_* in
-// quant/src/schemes). `blk` is the block index, `l` the element within it.
+// quant/src/schemes). `L` locates the block, `l` is the element within it.
 
 template <int QT, bool WIDE>
 struct Exact;
 
 template <bool WIDE>
 struct Exact<kQ8_0, WIDE> {
-  __device__ static float value(const View& v, uint64_t blk, uint32_t l) {
-    const float d = load_scale<WIDE>(v.d, blk);
-    const float q = static_cast<float>(reinterpret_cast<const int8_t*>(v.qs)[blk * 32 + l]);
+  __device__ static float value(const View& v, const BlockLoc& L, uint32_t l) {
+    const float d = scale_d<kQ8_0, WIDE>(v, L);
+    const float q = static_cast<float>(static_cast<int8_t>(code_byte<kQ8_0>(v, L, l)));
     return d * q;  // matmul.rs:167
   }
 };
 
 template <bool WIDE>
 struct Exact<kQ4_0, WIDE> {
-  __device__ static float value(const View& v, uint64_t blk, uint32_t l) {
-    const float d = load_scale<WIDE>(v.d, blk);
-    const uint8_t byte = v.qs[blk * 16 + (l & 15)];
+  __device__ static float value(const View& v, const BlockLoc& L, uint32_t l) {
+    const float d = scale_d<kQ4_0, WIDE>(v, L);
+    const uint8_t byte = code_byte<kQ4_0>(v, L, l & 15);
     const uint32_t code = l < 16 ? (byte & 15u) : (byte >> 4);
     return d * (static_cast<float>(code) - 8.0f);  // matmul.rs:179
   }
 };
 
-template <bool WIDE, bool FIVE>
-__device__ __forceinline__ float exact_q45k(const View& v, uint64_t blk, uint32_t l) {
-  const uint32_t* scw = reinterpret_cast<const uint32_t*>(v.sc + blk * 12);
+template <int QT, bool WIDE>
+__device__ __forceinline__ float exact_q45k(const View& v, const BlockLoc& L, uint32_t l) {
+  uint32_t w[3];
+#pragma unroll
+  for (int i = 0; i < 3; ++i)
+    w[i] = static_cast<uint32_t>(sc_byte<QT>(v, L, 4 * i)) |
+           (static_cast<uint32_t>(sc_byte<QT>(v, L, 4 * i + 1)) << 8) |
+           (static_cast<uint32_t>(sc_byte<QT>(v, L, 4 * i + 2)) << 16) |
+           (static_cast<uint32_t>(sc_byte<QT>(v, L, 4 * i + 3)) << 24);
   uint32_t sc, mn;
-  kquant_sc_m(scw[0], scw[1], scw[2], static_cast<int>(l / 32), sc, mn);
+  kquant_sc_m(w[0], w[1], w[2], static_cast<int>(l / 32), sc, mn);
   const uint32_t group = l / 64, within = l % 64;
-  const uint8_t packed = v.qs[blk * 128 + group * 32 + within % 32];
+  const uint8_t packed = code_byte<QT>(v, L, group * 32 + within % 32);
   uint32_t q = within < 32 ? (packed & 15u) : (packed >> 4);
-  if constexpr (FIVE) {
+  if constexpr (QT == kQ5_K) {
     const uint32_t bit = within < 32 ? 2 * group : 2 * group + 1;
-    if ((v.qh[blk * 32 + within % 32] >> bit) & 1u) q += 16;
+    if ((qh_byte<QT>(v, L, within % 32) >> bit) & 1u) q += 16;
   }
-  const float d = load_scale<WIDE>(v.d, blk);
-  const float dmin = load_scale<WIDE>(v.dmin, blk);
+  const float d = scale_d<QT, WIDE>(v, L);
+  const float dmin = scale_dmin<QT, WIDE>(v, L);
   // block.scale * f32(sc) * f32(q) - block.min_scale * f32(m)  (matmul.rs:211-214)
   return d * static_cast<float>(sc) * static_cast<float>(q) - dmin * static_cast<float>(mn);
 }
 
 template <bool WIDE>
 struct Exact<kQ4_K, WIDE> {
-  __device__ static float value(const View& v, uint64_t blk, uint32_t l) {
-    return exact_q45k<WIDE, false>(v, blk, l);
+  __device__ static float value(const View& v, const BlockLoc& L, uint32_t l) {
+    return exact_q45k<kQ4_K, WIDE>(v, L, l);
   }
 };
 
 template <bool WIDE>
 struct Exact<kQ5_K, WIDE> {
-  __device__ static float value(const View& v, uint64_t blk, uint32_t l) {
-    return exact_q45k<WIDE, true>(v, blk, l);
+  __device__ static float value(const View& v, const BlockLoc& L, uint32_t l) {
+    return exact_q45k<kQ5_K, WIDE>(v, L, l);
   }
 };
 
 template <bool WIDE>
 struct Exact<kQ6_K, WIDE> {
-  __device__ static float value(const View& v, uint64_t blk, uint32_t l) {
+  __device__ static float value(const View& v, const BlockLoc& L, uint32_t l) {
     const uint32_t ip = l / 128, within = l % 128, chunk = within / 32, il = within % 32;
-    const uint8_t packed = v.qs[blk * 128 + ip * 64 + ((chunk & 1) == 0 ? il : 32 + il)];
+    const uint8_t packed = code_byte<kQ6_K>(v, L, ip * 64 + ((chunk & 1) == 0 ? il : 32 + il));
     const uint32_t low = chunk < 2 ? (packed & 15u) : (packed >> 4);
-    const uint32_t high = v.qh[blk * 64 + ip * 32 + il];
+    const uint32_t high = qh_byte<kQ6_K>(v, L, ip * 32 + il);
     const int32_t q = static_cast<int32_t>(low | (((high >> (chunk * 2)) & 3u) << 4));
-    const float sc = static_cast<float>(reinterpret_cast<const int8_t*>(v.sc)[blk * 16 + l / 16]);
-    const float d = load_scale<WIDE>(v.d, blk);
+    const float sc = static_cast<float>(static_cast<int8_t>(sc_byte<kQ6_K>(v, L, l / 16)));
+    const float d = scale_d<kQ6_K, WIDE>(v, L);
     return d * sc * static_cast<float>(q - 32);  // matmul.rs:279
   }
 };

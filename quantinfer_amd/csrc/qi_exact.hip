@@ -18,15 +18,18 @@ namespace qi {
 // ------------------------------------------------------------------ dequant
 
 template <int QT, bool WIDE>
-__global__ __launch_bounds__(256) void dequant_kernel(View w, uint64_t elements, float* out) {
+__global__ __launch_bounds__(256) void dequant_kernel(View w, uint64_t elements, uint64_t nb,
+                                                      float* out) {
   const uint64_t e0 = (static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x) * 8;
   if (e0 >= elements) return;
   constexpr uint32_t bs = (QT == kQ8_0 || QT == kQ4_0) ? 32 : 256;
   const uint64_t blk = e0 / bs;
   const uint32_t l0 = static_cast<uint32_t>(e0 % bs);  // 8 | bs, so all 8 share the block
+  // block order: output n owns blocks [n*nb, n*nb+nb) (row major: nb = all blocks)
+  const BlockLoc L = locate<QT>(w, blk / nb, blk % nb);
   float v[8];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) v[j] = Exact<QT, WIDE>::value(w, blk, l0 + j);
+  for (int j = 0; j < 8; ++j) v[j] = Exact<QT, WIDE>::value(w, L, l0 + j);
   float4* o = reinterpret_cast<float4*>(out + e0);
   o[0] = make_float4(v[0], v[1], v[2], v[3]);
   o[1] = make_float4(v[4], v[5], v[6], v[7]);
@@ -49,9 +52,9 @@ __global__ __launch_bounds__(256) void exact_output_rows_kernel(View w, const fl
   const float* left = x + r * w.k;
   float sum = 0.0f;
   for (uint32_t b = 0; b < w.nb; ++b) {
-    const uint64_t blk = n * w.nb + b;
+    const BlockLoc L = locate<QT>(w, n, b);
     const float* lb = left + static_cast<uint64_t>(b) * bs;
-    for (uint32_t l = 0; l < bs; ++l) sum += lb[l] * Exact<QT, WIDE>::value(w, blk, l);
+    for (uint32_t l = 0; l < bs; ++l) sum += lb[l] * Exact<QT, WIDE>::value(w, L, l);
   }
   y[r * w.n + n] = sum;
 }
@@ -69,7 +72,7 @@ __global__ __launch_bounds__(256) void exact_row_major_kernel(View w, const floa
   float sum = 0.0f;
   for (uint64_t k = 0; k < w.k; ++k) {
     const uint64_t f = k * w.n + n;  // flat index of element (k, n)
-    sum += left[k] * Exact<QT, WIDE>::value(w, f / bs, static_cast<uint32_t>(f % bs));
+    sum += left[k] * Exact<QT, WIDE>::value(w, locate<QT>(w, 0, f / bs), static_cast<uint32_t>(f % bs));
   }
   y[r * w.n + n] = sum;
 }
@@ -103,11 +106,11 @@ __global__ __launch_bounds__(256) void f32_rows_kernel(const float* W, uint64_t 
 namespace {
 
 template <int QT, bool WIDE>
-hipError_t dequant_one(const View& w, uint64_t elements, float* out, hipStream_t st) {
+hipError_t dequant_one(const View& w, uint64_t elements, uint64_t nb, float* out, hipStream_t st) {
   const uint64_t threads = (elements + 7) / 8;
   const uint64_t grid = (threads + 255) / 256;
   hipLaunchKernelGGL((dequant_kernel<QT, WIDE>), dim3(static_cast<uint32_t>(grid)), dim3(256), 0, st,
-                     w, elements, out);
+                     w, elements, nb, out);
   return hipGetLastError();
 }
 
@@ -132,8 +135,9 @@ hipError_t exact_wide(const Image& im, const View& w, const float* x, uint64_t m
 template <int QT>
 hipError_t dequant_wide(const Image& im, const View& w, float* out, hipStream_t st) {
   const uint64_t elements = im.k * im.n;
-  return im.wide ? dequant_one<QT, true>(w, elements, out, st)
-                 : dequant_one<QT, false>(w, elements, out, st);
+  const uint64_t nb = im.layout == kOutputRows ? im.k / block_elems(im.qtype) : im.nblocks;
+  return im.wide ? dequant_one<QT, true>(w, elements, nb, out, st)
+                 : dequant_one<QT, false>(w, elements, nb, out, st);
 }
 
 }  // namespace

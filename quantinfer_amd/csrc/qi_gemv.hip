@@ -157,13 +157,13 @@ GemvPlan plan_gemv(int32_t qtype, uint64_t k, uint64_t n, int mt, uint64_t max_p
   const uint64_t rw = static_cast<uint64_t>(gemv_tile_rows(mt));
   p.row_tiles = static_cast<uint32_t>((n + rw - 1) / rw);
   const uint32_t slots = static_cast<uint32_t>(k / static_cast<uint64_t>(gemv_slot_elems(qtype)));
-  // aim for >= 2048 single-wave workgroups (8 per CU) and >= 32 slots per split
+  // This kernel only serves shapes the matrix-core GEMV does not (K not a
+  // multiple of 256): short rows, no split of K across workgroups (a
+  // cross-workgroup reduction needs device-scope fences, which write back the
+  // per-XCD L2 on MI355X).
   uint32_t splits = 1;
-  const uint32_t target = 2048;
-  if (p.row_tiles < target) splits = (target + p.row_tiles - 1) / p.row_tiles;
-  splits = min(splits, max(1u, slots / 32u));
-  splits = min(splits, 64u);
-  while (splits > 1 && static_cast<uint64_t>(splits) * mt * n > max_partials) --splits;
+  (void)max_partials;
+  (void)mt;
   p.slots_per_split = (slots + splits - 1) / splits;
   p.splits = (slots + p.slots_per_split - 1) / p.slots_per_split;
   return p;

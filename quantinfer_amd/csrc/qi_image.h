@@ -1,14 +1,13 @@
-// Device image of a resident weight: the logical blocks split into planes
-// ("structure of arrays"), each plane contiguous in block order.
+// Device image of a resident weight.
 //
-// Block order is the reference's: for the output-rows layout output n owns
-// blocks [n*NB, n*NB+NB) with NB = K / block_elems, so every plane is
-// row-contiguous and a wavefront's 16-byte loads of one plane are coalesced.
-// The planes hold exactly the bytes of the GGUF wire block (codes, high bits,
-// packed 6-bit scales, f16 d/dmin), so the image of an f16-scale tensor has
-// wire size: Q8_0 34, Q4_0 18, Q4_K 144, Q5_K 176, Q6_K 210 bytes per block.
-// Scales that are not f16-exact (hand-built blocks, unrounded Q8_0/Q4_0
-// quantizer output) switch the whole tensor to f32 scale planes ("wide").
+// Every image holds exactly the bytes of the GGUF wire blocks (codes, high
+// bits, packed 6-bit scales, f16 d/dmin): Q8_0 34, Q4_0 18, Q4_K 144, Q5_K 176,
+// Q6_K 210 bytes per block. Scales that are not all f16-exact (hand-built
+// blocks, unrounded Q8_0/Q4_0 quantizer output) switch the tensor to f32 scale
+// entries ("wide"). Two arrangements:
+//
+// planar (row-major weights, or K not a multiple of 256): one plane per field
+//   in the reference block order, each plane contiguous.
 //
 //   plane   Q8_0        Q4_0              Q4_K        Q5_K        Q6_K
 //   qs      32 B i8     16 B split-half   128 B       128 B       128 B ql
@@ -16,7 +15,20 @@
 //   sc      -           -                 12 B 6-bit  12 B 6-bit  16 B i8
 //   d       f16|f32     f16|f32           f16|f32     f16|f32     f16|f32
 //   dmin    -           -                 f16|f32     f16|f32     -
-// F32 weights keep the row-major [K, N] f32 matrix in qs.
+//
+// tiled (output rows, K a multiple of 256; what the decode GEMV streams): the
+//   outputs are grouped in tiles of 16 (the last tile zero-padded) and K in
+//   units of 256 elements; one record per (tile, unit) holds the 16 rows'
+//   bytes of that unit, records ordered [tile][unit]. Inside a record:
+//     codes  the row slice of S code bytes (Q8_0 S=256, others 128) is split
+//            in four lane groups of S/4 bytes and 16-byte chunks; chunk q of
+//            lane group g of row c sits at q*1024 + (16g + c)*16, so a
+//            wavefront load (lane 16g + c) of chunk q reads 1 KB contiguous;
+//     qh     16-byte chunk h of row c at h*256 + c*16 (Q5_K 2, Q6_K 4 chunks);
+//     sc     row c's packed scales at c*12 (Q4_K/Q5_K) or c*16 (Q6_K);
+//     d      row c's scales: c*8 + block (Q8_0/Q4_0) or c (K-quants) entries;
+//     dmin   row c at c (Q4_K/Q5_K).
+//   F32 weights keep the row-major [K, N] f32 matrix in qs.
 #pragma once
 #include <stdint.h>
 
@@ -30,7 +42,7 @@ struct PlaneSizes {
   bool has_dmin;
 };
 
-inline PlaneSizes plane_sizes(int32_t qtype) {
+constexpr PlaneSizes plane_sizes(int32_t qtype) {
   switch (qtype) {
     case kQ8_0: return {32, 0, 0, false};
     case kQ4_0: return {16, 0, 0, false};
@@ -41,7 +53,7 @@ inline PlaneSizes plane_sizes(int32_t qtype) {
   }
 }
 
-inline uint32_t block_elems(int32_t qtype) {
+constexpr uint32_t block_elems(int32_t qtype) {
   switch (qtype) {
     case kQ8_0:
     case kQ4_0: return 32;
@@ -53,23 +65,60 @@ inline uint32_t block_elems(int32_t qtype) {
   }
 }
 
+// Record geometry of the tiled arrangement (per 16-row tile, 256-element unit).
+struct Record {
+  uint32_t bytes = 0;                              // record size
+  uint32_t qs = 0, qh = 0, sc = 0, d = 0, dmin = 0;  // section offsets
+  uint32_t bpu = 0;                                // blocks per unit per row (8 or 1)
+  uint32_t slice = 0;                              // code bytes per row per unit
+};
+
+constexpr Record record_geometry(int32_t qtype, bool wide) {
+  Record r;
+  const PlaneSizes ps = plane_sizes(qtype);
+  const uint32_t be = block_elems(qtype);
+  if (be == 0 || qtype == kF32) return r;
+  r.bpu = 256 / be;
+  r.slice = ps.qs * r.bpu;
+  const uint32_t ss = wide ? 4 : 2;
+  uint32_t off = 16 * r.slice;
+  r.qs = 0;
+  r.qh = off;
+  off += 16 * ps.qh;
+  r.sc = off;
+  off += 16 * ps.sc;
+  r.d = off;
+  off += 16 * r.bpu * ss;
+  r.dmin = off;
+  off += ps.has_dmin ? 16 * ss : 0;
+  r.bytes = (off + 15) & ~15u;
+  return r;
+}
+
 struct Image {
   int32_t qtype = 0, layout = 0;
   uint64_t k = 0, n = 0, nblocks = 0;
-  int32_t wide = 0;  // 1: f32 scale planes
-  uint64_t off_qs = 0, off_qh = 0, off_sc = 0, off_d = 0, off_dmin = 0;
+  int32_t wide = 0;   // 1: f32 scale entries
+  int32_t tiled = 0;  // 1: tiled arrangement
+  uint64_t off_qs = 0, off_qh = 0, off_sc = 0, off_d = 0, off_dmin = 0;  // planar
+  uint64_t tiles = 0, units = 0;  // tiled: 16-row tiles, 256-element units per row
+  Record rec;
   uint64_t bytes = 0;
 };
 
 // Device-side view of an image (plain pointers, passed by value to kernels).
 struct View {
-  const uint8_t* qs;
+  const uint8_t* qs;  // planar qs plane, or the first record
   const uint8_t* qh;
   const uint8_t* sc;
   const void* d;
   const void* dmin;
   uint64_t k, n;
-  uint32_t nb;  // blocks per output row (output-rows layout)
+  uint32_t nb;     // blocks per output row (output-rows layout)
+  uint32_t tiled;  // 1: records
+  uint32_t units;  // tiled: units per row
+  uint32_t tiles;  // tiled: tiles
+  Record rec;
 };
 
 inline View make_view(const Image& im, const void* base) {
@@ -82,8 +131,12 @@ inline View make_view(const Image& im, const void* base) {
   v.dmin = b + im.off_dmin;
   v.k = im.k;
   v.n = im.n;
-  uint32_t be = block_elems(im.qtype);
+  const uint32_t be = block_elems(im.qtype);
   v.nb = be ? static_cast<uint32_t>(im.k / be) : 0;
+  v.tiled = static_cast<uint32_t>(im.tiled);
+  v.units = static_cast<uint32_t>(im.units);
+  v.tiles = static_cast<uint32_t>(im.tiles);
+  v.rec = im.rec;
   return v;
 }
 
@@ -91,7 +144,7 @@ inline View make_view(const Image& im, const void* base) {
 // with a message in *why.
 int32_t plan_image(int32_t qtype, int32_t layout, uint64_t k, uint64_t n, const void* blocks,
                    uint64_t count, Image* out, const char** why);
-// Write the planes of a planned image into host memory of im.bytes bytes.
+// Write the image into host memory of im.bytes bytes.
 void fill_image(const Image& im, const void* blocks, void* out);
 
 }  // namespace qi

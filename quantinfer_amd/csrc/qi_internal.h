@@ -27,6 +27,18 @@ GemvPlan plan_gemv(int32_t qtype, uint64_t k, uint64_t n, int mt, uint64_t max_p
 hipError_t launch_gemv(int32_t qtype, bool wide, int mt, const GemvArgs& a, const GemvPlan& plan,
                        hipStream_t st);
 
+// Matrix-core decode GEMV (int8 digits of the activations x raw weight codes).
+struct GemvMfmaArgs {
+  View w;
+  const float* x;  // [m, k] device, 16-byte aligned rows
+  float* y;        // [m, n]
+  int m;           // rows in this launch (<= compile-time tile)
+};
+bool gemv_mfma_supported(int32_t qtype, int32_t layout, uint64_t k);
+int gemv_mfma_split(uint64_t n);
+hipError_t launch_gemv_mfma(int32_t qtype, bool wide, int mt, int split, const GemvMfmaArgs& a,
+                            hipStream_t st);
+
 // Exact-order matmul: bit-identical to CpuScalar (any M, either layout).
 hipError_t launch_exact(const Image& im, const View& w, const float* x, uint64_t m, float* y,
                         hipStream_t st);

@@ -97,6 +97,17 @@ int32_t plan_image(int32_t qtype, int32_t layout, uint64_t k, uint64_t n, const 
   const uint64_t scale_bytes = all_f16 ? 2 : 4;
   im.nblocks = count;
   im.wide = all_f16 ? 0 : 1;
+  if (layout == kOutputRows && k % 256 == 0) {
+    // tiled records: 16-output tiles x 256-element units
+    im.tiled = 1;
+    im.tiles = (n + 15) / 16;
+    im.units = k / 256;
+    im.rec = record_geometry(qtype, im.wide != 0);
+    im.off_qs = im.off_qh = im.off_sc = im.off_d = im.off_dmin = 0;
+    im.bytes = im.tiles * im.units * im.rec.bytes + 256;
+    *out = im;
+    return QI_HIP_OK;
+  }
   uint64_t off = 0;
   im.off_qs = off;
   off = align256(off + count * ps.qs);
@@ -113,16 +124,62 @@ int32_t plan_image(int32_t qtype, int32_t layout, uint64_t k, uint64_t n, const 
   return QI_HIP_OK;
 }
 
+
 namespace {
 
-void put_scale(uint8_t* plane, uint64_t i, float v, bool wide) {
-  if (wide) {
-    memcpy(plane + 4 * i, &v, 4);
-  } else {
-    _Float16 h = static_cast<_Float16>(v);
-    memcpy(plane + 2 * i, &h, 2);
+// Byte destinations of one block (n, b) in the image, for either arrangement.
+struct Dest {
+  const Image* im;
+  uint8_t* base;
+  uint64_t blk = 0;      // planar block index
+  uint8_t* rec = nullptr;  // tiled record
+  uint32_t col = 0, bi = 0;
+
+  void at(uint64_t n, uint64_t b) {
+    if (!im->tiled) {
+      blk = n * (im->k / block_elems(im->qtype)) + b;
+      return;
+    }
+    const uint64_t tile = n / 16, u = b / im->rec.bpu;
+    col = static_cast<uint32_t>(n % 16);
+    bi = static_cast<uint32_t>(b % im->rec.bpu);
+    rec = base + (tile * im->units + u) * im->rec.bytes;
   }
-}
+  uint8_t* code(uint32_t o) const {
+    const PlaneSizes ps = plane_sizes(im->qtype);
+    if (!im->tiled) return base + im->off_qs + blk * ps.qs + o;
+    const uint32_t s = bi * ps.qs + o, quarter = im->rec.slice / 4;
+    const uint32_t g = s / quarter, q = (s % quarter) / 16, r = s % 16;
+    return rec + im->rec.qs + q * 1024 + (16 * g + col) * 16 + r;
+  }
+  uint8_t* qh(uint32_t o) const {
+    if (!im->tiled) return base + im->off_qh + blk * plane_sizes(im->qtype).qh + o;
+    return rec + im->rec.qh + (o / 16) * 256 + col * 16 + o % 16;
+  }
+  uint8_t* sc(uint32_t o) const {
+    const uint32_t scb = plane_sizes(im->qtype).sc;
+    if (!im->tiled) return base + im->off_sc + blk * scb + o;
+    return rec + im->rec.sc + col * scb + o;
+  }
+  void scale(float v, bool min_plane) const {
+    const bool wide = im->wide != 0;
+    uint8_t* p;
+    const uint32_t ss = wide ? 4 : 2;
+    if (!im->tiled) {
+      p = base + (min_plane ? im->off_dmin : im->off_d) + blk * ss;
+    } else if (min_plane) {
+      p = rec + im->rec.dmin + col * ss;
+    } else {
+      p = rec + im->rec.d + (col * im->rec.bpu + bi) * ss;
+    }
+    if (wide) {
+      memcpy(p, &v, 4);
+    } else {
+      _Float16 h = static_cast<_Float16>(v);
+      memcpy(p, &h, 2);
+    }
+  }
+};
 
 }  // namespace
 
@@ -133,51 +190,50 @@ void fill_image(const Image& im, const void* blocks, void* out) {
     memcpy(base, blocks, im.nblocks * 4);
     return;
   }
-  uint8_t* qs = base + im.off_qs;
-  uint8_t* qh = base + im.off_qh;
-  uint8_t* sc = base + im.off_sc;
-  uint8_t* d = base + im.off_d;
-  uint8_t* dmin = base + im.off_dmin;
-  const bool wide = im.wide != 0;
+  const uint64_t be = block_elems(im.qtype);
+  // block order of the reference: output rows (n, b) -> n*NB + b; row major is flat
+  const uint64_t nb = im.layout == kOutputRows ? im.k / be : im.nblocks;
+  Dest dst{&im, base};
   for (uint64_t i = 0; i < im.nblocks; ++i) {
+    dst.at(i / nb, i % nb);
     switch (im.qtype) {
       case kQ8_0: {
         const auto& b = as_blocks<qi_hip_q8_0_block>(blocks)[i];
-        memcpy(qs + 32 * i, b.values, 32);
-        put_scale(d, i, b.scale, wide);
+        for (uint32_t o = 0; o < 32; ++o) *dst.code(o) = static_cast<uint8_t>(b.values[o]);
+        dst.scale(b.scale, false);
         break;
       }
       case kQ4_0: {
         // GGML split-half nibble order (format gguf/writer.rs:201-203)
         const auto& b = as_blocks<qi_hip_q4_0_block>(blocks)[i];
-        for (int j = 0; j < 16; ++j)
-          qs[16 * i + j] = static_cast<uint8_t>(b.values[j] | (b.values[j + 16] << 4));
-        put_scale(d, i, b.scale, wide);
+        for (uint32_t j = 0; j < 16; ++j)
+          *dst.code(j) = static_cast<uint8_t>(b.values[j] | (b.values[j + 16] << 4));
+        dst.scale(b.scale, false);
         break;
       }
       case kQ4_K: {
         const auto& b = as_blocks<qi_hip_q4_k_block>(blocks)[i];
-        memcpy(qs + 128 * i, b.values, 128);
-        memcpy(sc + 12 * i, b.scales, 12);
-        put_scale(d, i, b.scale, wide);
-        put_scale(dmin, i, b.min_scale, wide);
+        for (uint32_t o = 0; o < 128; ++o) *dst.code(o) = b.values[o];
+        for (uint32_t o = 0; o < 12; ++o) *dst.sc(o) = b.scales[o];
+        dst.scale(b.scale, false);
+        dst.scale(b.min_scale, true);
         break;
       }
       case kQ5_K: {
         const auto& b = as_blocks<qi_hip_q5_k_block>(blocks)[i];
-        memcpy(qs + 128 * i, b.values, 128);
-        memcpy(qh + 32 * i, b.high_bits, 32);
-        memcpy(sc + 12 * i, b.scales, 12);
-        put_scale(d, i, b.scale, wide);
-        put_scale(dmin, i, b.min_scale, wide);
+        for (uint32_t o = 0; o < 128; ++o) *dst.code(o) = b.values[o];
+        for (uint32_t o = 0; o < 32; ++o) *dst.qh(o) = b.high_bits[o];
+        for (uint32_t o = 0; o < 12; ++o) *dst.sc(o) = b.scales[o];
+        dst.scale(b.scale, false);
+        dst.scale(b.min_scale, true);
         break;
       }
       case kQ6_K: {
         const auto& b = as_blocks<qi_hip_q6_k_block>(blocks)[i];
-        memcpy(qs + 128 * i, b.low_bits, 128);
-        memcpy(qh + 64 * i, b.high_bits, 64);
-        memcpy(sc + 16 * i, b.scales, 16);
-        put_scale(d, i, b.scale, wide);
+        for (uint32_t o = 0; o < 128; ++o) *dst.code(o) = b.low_bits[o];
+        for (uint32_t o = 0; o < 64; ++o) *dst.qh(o) = b.high_bits[o];
+        for (uint32_t o = 0; o < 16; ++o) *dst.sc(o) = static_cast<uint8_t>(b.scales[o]);
+        dst.scale(b.scale, false);
         break;
       }
     }

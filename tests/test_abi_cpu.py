@@ -48,11 +48,14 @@ def test_open_without_device_is_unsupported():
         pytest.skip("a gfx950 device is visible")
 
 
+SIZES = {qa.Q8_0: (32, 0, 0, False), qa.Q4_0: (16, 0, 0, False), qa.Q4_K: (128, 0, 12, True),
+         qa.Q5_K: (128, 32, 12, True), qa.Q6_K: (128, 64, 16, False)}
+
+
 def _planes(qtype, image, count, f16):
-    """Split an image into its planes (offsets: 256-byte aligned, in the order
-    qs, qh, sc, d, dmin)."""
-    sizes = {qa.Q8_0: (32, 0, 0, False), qa.Q4_0: (16, 0, 0, False), qa.Q4_K: (128, 0, 12, True),
-             qa.Q5_K: (128, 32, 12, True), qa.Q6_K: (128, 64, 16, False)}[qtype]
+    """Split a planar image into its planes (offsets: 256-byte aligned, in the
+    order qs, qh, sc, d, dmin)."""
+    sizes = SIZES[qtype]
     sb = 2 if f16 else 4
     al = lambda x: (x + 255) // 256 * 256
     off = 0
@@ -64,37 +67,106 @@ def _planes(qtype, image, count, f16):
     return out
 
 
+def _check_wire_fields(qtype, fields, wire):
+    """fields: per block (qs, qh, sc, d, dmin) byte arrays; wire: GGUF blocks."""
+    count = wire.shape[0]
+    qs, qh, sc, d, dmin = (np.asarray(f, dtype=np.uint8).reshape(count, -1) for f in fields)
+    if qtype == qa.Q8_0:
+        assert np.array_equal(d, wire[:, 0:2]) and np.array_equal(qs, wire[:, 2:34])
+    elif qtype == qa.Q4_0:
+        assert np.array_equal(d, wire[:, 0:2]) and np.array_equal(qs, wire[:, 2:18])
+    elif qtype in (qa.Q4_K, qa.Q5_K):
+        assert np.array_equal(d, wire[:, 0:2]) and np.array_equal(dmin, wire[:, 2:4])
+        assert np.array_equal(sc, wire[:, 4:16])
+        if qtype == qa.Q4_K:
+            assert np.array_equal(qs, wire[:, 16:144])
+        else:
+            assert np.array_equal(qh, wire[:, 16:48]) and np.array_equal(qs, wire[:, 48:176])
+    else:
+        assert np.array_equal(qs, wire[:, 0:128]) and np.array_equal(qh, wire[:, 128:192])
+        assert np.array_equal(sc, wire[:, 192:208]) and np.array_equal(d, wire[:, 208:210])
+
+
 @pytest.mark.parametrize("qtype", ALL_Q)
-def test_packed_planes_hold_exactly_the_wire_bytes(qtype):
+def test_planar_image_holds_exactly_the_wire_bytes(qtype):
+    # row-major weights keep one plane per field in the reference block order
     k, n = 512, 6
     blocks = po.make_weights(qtype, k, n, seed=21 + qtype, outliers=True)
-    image, f16 = qa.pack_weights(qtype, qa.OUTPUT_ROWS, k, n, blocks)
+    image, f16 = qa.pack_weights(qtype, qa.ROW_MAJOR, k, n, blocks)
     assert f16
     count = blocks.size
     p = _planes(qtype, image, count, True)
     wire = po.wire_pack(qtype, blocks).reshape(count, po.WIRE_BYTES[qtype])
-    if qtype == qa.Q8_0:
-        assert np.array_equal(p["d"].view("<u2"), wire[:, 0:2].copy().view("<u2").ravel())
-        assert np.array_equal(p["qs"].reshape(count, 32), wire[:, 2:34])
-    elif qtype == qa.Q4_0:
-        assert np.array_equal(p["d"].view("<u2"), wire[:, 0:2].copy().view("<u2").ravel())
-        assert np.array_equal(p["qs"].reshape(count, 16), wire[:, 2:18])
-    elif qtype in (qa.Q4_K, qa.Q5_K):
-        assert np.array_equal(p["d"].view("<u2"), wire[:, 0:2].copy().view("<u2").ravel())
-        assert np.array_equal(p["dmin"].view("<u2"), wire[:, 2:4].copy().view("<u2").ravel())
-        assert np.array_equal(p["sc"].reshape(count, 12), wire[:, 4:16])
-        if qtype == qa.Q4_K:
-            assert np.array_equal(p["qs"].reshape(count, 128), wire[:, 16:144])
-        else:
-            assert np.array_equal(p["qh"].reshape(count, 32), wire[:, 16:48])
-            assert np.array_equal(p["qs"].reshape(count, 128), wire[:, 48:176])
-    else:
-        assert np.array_equal(p["qs"].reshape(count, 128), wire[:, 0:128])
-        assert np.array_equal(p["qh"].reshape(count, 64), wire[:, 128:192])
-        assert np.array_equal(p["sc"].reshape(count, 16), wire[:, 192:208])
-        assert np.array_equal(p["d"].view("<u2"), wire[:, 208:210].copy().view("<u2").ravel())
+    empty = np.zeros((count, 0), np.uint8)
+    _check_wire_fields(qtype, [p["qs"], p["qh"] if p["qh"].size else empty, p["sc"] if p["sc"].size else empty,
+                               p["d"], p["dmin"] if p["dmin"].size else empty], wire)
     payload = sum(v.size for v in p.values())
     assert payload == po.WIRE_BYTES[qtype] * count  # the image of an f16 tensor has wire size
+
+
+def _untile(qtype, image, k, n, f16):
+    """Per-block fields of a tiled output-rows image, read back from the record
+    arrangement: records of (16-output tile, 256-element unit) ordered
+    [tile][unit]; inside a record the code slice of row c (its unit's code bytes
+    in block order) is cut in four lane groups and 16-byte chunks, chunk q of
+    group g at q*1024 + (16g + c)*16; qh chunk h at h*256 + c*16; packed scales
+    at c*|sc|; d entries at c*bpu + block; dmin at c. Also returns the bytes of
+    the padding rows."""
+    qsb, qhb, scb, has_dmin = SIZES[qtype]
+    bpu = 8 if qtype in (qa.Q8_0, qa.Q4_0) else 1
+    ss = 2 if f16 else 4
+    slice_ = qsb * bpu
+    off_qh = 16 * slice_
+    off_sc = off_qh + 16 * qhb
+    off_d = off_sc + 16 * scb
+    off_dm = off_d + 16 * bpu * ss
+    rec_bytes = -(-(off_dm + (16 * ss if has_dmin else 0)) // 16) * 16
+    tiles, units = -(-n // 16), k // 256
+    assert image.size == tiles * units * rec_bytes + 256
+    nb = k // (32 if bpu == 8 else 256)
+    fields = [[] for _ in range(5)]
+    pad = []
+    for row in range(tiles * 16):
+        t, c = divmod(row, 16)
+        for u in range(units):
+            rec = image[(t * units + u) * rec_bytes:(t * units + u + 1) * rec_bytes]
+            quarter = slice_ // 4
+            code = np.concatenate([rec[q * 1024 + (16 * g + c) * 16:][:16]
+                                   for g in range(4) for q in range(quarter // 16)])
+            qh = np.concatenate([rec[off_qh + h * 256 + c * 16:][:16] for h in range(qhb // 16)] or [[]])
+            sc = rec[off_sc + c * scb:][:scb]
+            per = [(code[bi * qsb:(bi + 1) * qsb], qh, sc, rec[off_d + (c * bpu + bi) * ss:][:ss],
+                    rec[off_dm + c * ss:][:ss] if has_dmin else np.zeros(0, np.uint8)) for bi in range(bpu)]
+            if row < n:
+                for blk in per:
+                    for i in range(5):
+                        fields[i].append(blk[i])
+            else:
+                pad.extend(np.concatenate(blk) for blk in per)
+    assert len(fields[0]) == n * nb
+    return [np.concatenate(f) if f and f[0].size else np.zeros((n * nb, 0), np.uint8) for f in fields], pad
+
+
+@pytest.mark.parametrize("qtype", ALL_Q)
+def test_tiled_image_holds_exactly_the_wire_bytes(qtype):
+    # output rows with K a multiple of 256: tile records; 21 outputs leave
+    # 11 padding rows in the second tile, which must read as zero
+    k, n = 512, 21
+    blocks = po.make_weights(qtype, k, n, seed=41 + qtype, outliers=True)
+    image, f16 = qa.pack_weights(qtype, qa.OUTPUT_ROWS, k, n, blocks)
+    assert f16
+    fields, pad = _untile(qtype, image, k, n, True)
+    wire = po.wire_pack(qtype, blocks).reshape(blocks.size, po.WIRE_BYTES[qtype])
+    _check_wire_fields(qtype, fields, wire)
+    assert pad and not any(p.any() for p in pad)
+
+
+def test_tiled_image_with_unrounded_scales_keeps_f32_entries():
+    blocks = po.quantize(po.Q8_0, po.fill_normal(5, 256 * 3, 0.02))
+    image, f16 = qa.pack_weights(qa.Q8_0, qa.OUTPUT_ROWS, 256, 3, blocks)
+    assert not f16
+    fields, _ = _untile(qa.Q8_0, image, 256, 3, False)
+    assert np.array_equal(fields[3].view("<f4"), blocks["scale"])
 
 
 def test_unrounded_scales_switch_to_f32_planes():
