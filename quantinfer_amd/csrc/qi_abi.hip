@@ -38,7 +38,7 @@ struct qi_hip_ctx {
   uint64_t xcap = 0;  // floats
   float* ybuf = nullptr;
   uint64_t ycap = 0;
-  int gemv_split = 0;  // QI_HIP_GEMV_SPLIT tuning override (K parts per GEMV workgroup)
+  int gemv_split = 0;  // QI_HIP_GEMV_SPLIT tuning override (wavefronts per GEMV workgroup: 4 or 8)
 };
 
 struct qi_hip_weights {
@@ -148,7 +148,7 @@ qi_hip_status run_linear(qi_hip_ctx* c, const qi_hip_weights* w, const float* x,
     const int mt = rows == 1 ? 1 : rows == 2 ? 2 : rows <= 4 ? 4 : rows <= 8 ? 8 : 16;
     if (mfma) {
       qi::GemvMfmaArgs ga{v, x + m0 * im.k, y + m0 * im.n, rows};
-      const int split = c->gemv_split > 0 ? c->gemv_split : qi::gemv_mfma_split(im.n);
+      const int split = c->gemv_split > 0 ? c->gemv_split : qi::gemv_mfma_split(im.k, im.n);
       QI_HIP_TRY(qi::launch_gemv_mfma(im.qtype, im.wide != 0, mt, split, ga, st), "launch gemv");
       continue;
     }

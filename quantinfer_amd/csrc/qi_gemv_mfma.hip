@@ -1,32 +1,39 @@
 // Decode GEMV on the int8 matrix cores (v_mfma_i32_16x16x32_i8), output-rows
 // layout, M <= 16 activation rows, K a multiple of 256.
 //
-// Arithmetic. Each activation x is turned into a 30-bit fixed-point integer
-// F = rint(x * 2^s) (one power-of-two s per activation row and K chunk, chosen
-// from the chunk's max |x|) written as four signed 8-bit digits
-// F = d0 + d1*2^8 + d2*2^16 + d3*2^24. The weight codes enter the matrix cores
-// unchanged (Q8_0 int8 codes, Q4_0/Q4_K/Q5_K/Q6_K unsigned codes), so every
-// product digit*code is exact in int32, and
+// Arithmetic. The activations are cut into windows of 32 consecutive
+// elements. Each activation x of a window becomes a 30-bit fixed-point
+// integer F = rint(x * 2^s), with one power of two 2^s per (activation row,
+// window) chosen from the window's max |x|, written as four signed 8-bit
+// digits F = d0 + d1*2^8 + d2*2^16 + d3*2^24. The weight codes enter the
+// matrix cores unchanged (Q8_0 int8 codes, Q4_0/Q4_K/Q5_K/Q6_K unsigned
+// codes), so every product digit*code is exact in int32, and over a window
 //   sum_k x_k q_k = 2^-s * (C0 + C1*2^8 + C2*2^16 + C3*2^24),  Ci = sum_k di_k q_k
-// up to the 2^-30-of-chunk-max rounding of x. Per sub-block scale a and
-// offset b of the format (w = a*q - b) are applied in f32 once per window:
+// up to the 2^-30-of-window-max rounding of x. The sub-block scale a and
+// offset b of the format (w = a*q - b) are applied in f32 once per window
+// (Q6_K: per 16-element half window, one int8 sub-scale each):
 //   y += a * 2^-s * combine(C) - b * sum_k x_k.
 // This reorders the reference arithmetic and is judged by tolerance.
 //
-// Operand layout (16x16x32, verified on gfx950: A[i][k] lane i+16*(k/8),
-// B[k][j] lane j+16*(k/8), C[i][j] lane j+16*(i/4) element i%4). For a tile of
-// 16 outputs (B columns) the 4 lane groups g = lane/16 each stream their own
-// 8 codes per step; A row i = 4*sigma + digit carries digit `digit` of lane
-// group sigma's 8 activations and is zero elsewhere, so C row 4*sigma + digit
-// holds lane group sigma's own digit sums: after a window of steps, lane
-// (n, g) holds the four digit sums of its own codes in its four C registers,
-// next to its own scale. A 256-element unit is 8 steps x 4 groups x 8 codes.
+// Operand layout (16x16x32: A[i][k] lane i+16*(k/8), B[k][j] lane j+16*(k/8),
+// C[i][j] lane j+16*(i/4) element i%4). For a tile of 16 outputs (B columns)
+// the 4 lane groups g = lane/16 each stream their own 8 codes per step; A row
+// i = 4*sigma + digit carries digit `digit` of lane group sigma's 8
+// activations and is zero elsewhere, so C row 4*sigma + digit holds lane
+// group sigma's own digit sums: after a window of steps, lane (n, g) holds
+// the four digit sums of its own codes in its four C registers, next to its
+// own scale. A 256-element unit is 8 steps x 4 groups x 8 codes.
 //
-// Work split: a workgroup of 4 wavefronts owns TILES_C x 16 outputs; its
-// wavefronts split those tiles (WC per row of tiles) and the K range (SW
-// parts, reduced through LDS at the end). The activation digits for a K chunk
-// are built once per workgroup into LDS. No state is shared between
-// workgroups, so there are no device-scope fences.
+// Work split: one workgroup per tile of 16 outputs, SW wavefronts splitting
+// the tile's K range (contiguous runs of units, reduced through LDS at the
+// end). The activation digits of a K chunk are built once per workgroup into
+// LDS (half a window per thread, the window max from the neighbouring lane:
+// a single barrier).
+// Each wavefront issues its activation loads, then the loads of up to D
+// units, before it waits for anything (vector loads complete in order, so
+// waiting for the activations never waits for the weights); a workgroup's
+// whole weight slice is in flight at once.
+// No state is shared between workgroups, so there are no device-scope fences.
 #include "qi_device.h"
 #include "qi_internal.h"
 
@@ -34,7 +41,10 @@ namespace qi {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 
-constexpr int kLdsA = 32768;  // activation digit bytes per chunk (all rows)
+constexpr uint32_t kZeroBytes = 1024;  // zero A operand for the lanes of other lane groups
+constexpr uint32_t kUnitDigitBytes = 1024;  // 256 activations x 4 digits, per row
+constexpr uint32_t kUnitAuxBytes = 128;     // 8 windows x float4 {2^-s, sum lo16, sum hi16, 0}
+constexpr uint32_t kMaxLds = 160 * 1024;
 
 template <int QT>
 struct Unit;  // per-format code/scale access for one (output n, lane group g, unit u)
@@ -143,7 +153,7 @@ struct UnitQ45K {
     uint4 q[2];
     uint4 h[2];
     uint32_t sc[3];
-    uint32_t s0, s1;  // d | dmin << 16 in s0 (f16), or d and dmin (f32)
+    uint32_t s0, s1;  // d and dmin: f16 bits (zero-extended) or f32 bits
   };
   template <bool W>
   __device__ static void load(const uint8_t* rec, uint32_t lane, Raw& r) {
@@ -161,10 +171,9 @@ struct UnitQ45K {
       r.s0 = reinterpret_cast<const uint32_t*>(rec + R.d)[col];
       r.s1 = reinterpret_cast<const uint32_t*>(rec + R.dmin)[col];
     } else {
-      const uint32_t d = reinterpret_cast<const uint16_t*>(rec + R.d)[col];
-      const uint32_t dm = reinterpret_cast<const uint16_t*>(rec + R.dmin)[col];
-      r.s0 = d | (dm << 16);
-      r.s1 = 0;
+      // kept apart until scales(): combining them here would wait for the loads
+      r.s0 = reinterpret_cast<const uint16_t*>(rec + R.d)[col];
+      r.s1 = reinterpret_cast<const uint16_t*>(rec + R.dmin)[col];
     }
   }
   template <bool W>
@@ -174,8 +183,8 @@ struct UnitQ45K {
       d = __builtin_bit_cast(float, r.s0);
       dmin = __builtin_bit_cast(float, r.s1);
     } else {
-      d = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(r.s0 & 0xFFFFu)));
-      dmin = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(r.s0 >> 16)));
+      d = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(r.s0)));
+      dmin = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(r.s1)));
     }
     uint32_t s0, m0, s1, m1;
     kquant_sc_m(r.sc[0], r.sc[1], r.sc[2], static_cast<int>(2 * g), s0, m0);
@@ -263,43 +272,6 @@ struct Unit<kQ6_K> {
   }
 };
 
-// Unit-relative element of 8-element group p (0..31): the first element.
-template <int QT>
-__device__ __forceinline__ uint32_t group_first_element(uint32_t p) {
-  if constexpr (QT == kQ6_K) {
-    // p = 16ip + r; r < 8: c = r/4, t = r%4 (low nibbles); r >= 8: c = (r-8)/4, t = 4 + r%4
-    const uint32_t ip = p >> 4, r = p & 15;
-    const uint32_t c = (r & 7) >> 2, t = (r & 3) + (r >= 8 ? 4 : 0);
-    return 128 * ip + 32 * c + 8 * (t & 3) + (t >= 4 ? 64 : 0);
-  } else {
-    return 8 * p;  // e = 64g + 8t + j with p = 8g + t
-  }
-}
-// (lane group, step) of 8-element group p
-template <int QT>
-__device__ __forceinline__ void group_slot(uint32_t p, uint32_t& g, uint32_t& t) {
-  if constexpr (QT == kQ6_K) {
-    const uint32_t ip = p >> 4, r = p & 15;
-    g = 2 * ip + ((r & 7) >> 2);
-    t = (r & 3) + (r >= 8 ? 4 : 0);
-  } else {
-    g = p >> 3;
-    t = p & 7;
-  }
-}
-
-__device__ __forceinline__ float wave_max(float v) {
-  v = fmaxf(v, __builtin_amdgcn_update_dpp(0.0f, v, 0xB1, 0xF, 0xF, false));
-  v = fmaxf(v, __builtin_amdgcn_update_dpp(0.0f, v, 0x4E, 0xF, 0xF, false));
-  v = fmaxf(v, __builtin_amdgcn_update_dpp(0.0f, v, 0x141, 0xF, 0xF, false));
-  v = fmaxf(v, __builtin_amdgcn_update_dpp(0.0f, v, 0x140, 0xF, 0xF, false));
-  const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
-  const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16));
-  const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
-  const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 48));
-  return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
-}
-
 // Byte transpose of four digit words (one per activation) into four words
 // (one per digit): out[i] byte e = in[e] byte i.
 __device__ __forceinline__ void transpose4(const uint32_t in[4], uint32_t out[4]) {
@@ -313,31 +285,111 @@ __device__ __forceinline__ void transpose4(const uint32_t in[4], uint32_t out[4]
   out[3] = __builtin_amdgcn_perm(t3, t1, 0x07060302u);
 }
 
-template <int QT, bool WIDE, int MT, int WC, int SW>
-__global__ __launch_bounds__(64 * WC * SW) void gemv_mfma_kernel(GemvMfmaArgs a) {
-  using U = Unit<QT>;
-  constexpr int kThreads = 64 * WC * SW;
-  constexpr int kWaves = WC * SW;
-  constexpr int kChunk = kLdsA / (4 * MT);  // activations per row per chunk
-  constexpr int kUnitsChunk = kChunk / 256;
-  // digits [m][unit][t][g][digit] x 8 B, then 1 KB of zeros read by the lanes
-  // whose A row belongs to another lane group
-  __shared__ __attribute__((aligned(16))) uint8_t lds_a[kLdsA + 1024];
-  __shared__ __attribute__((aligned(16))) float lds_gs[MT * kUnitsChunk * 32];  // [m][u][g][t] sums of 8
-  __shared__ float lds_inv[MT];
-  __shared__ int lds_shift[MT];
-  __shared__ float lds_max[kWaves][MT];
-  __shared__ float lds_red[SW > 1 ? SW : 1][MT][16 * WC];
+// First unit element of window (g, h): Q6_K lane group g = 2*ip + c holds
+// elements 128ip + 32c + [0, 32) (h = 0) and + 64 (h = 1); the other formats'
+// lane group g holds elements 64g + [0, 64).
+template <int QT>
+__device__ __forceinline__ uint32_t window_first(uint32_t g, uint32_t h) {
+  if constexpr (QT == kQ6_K) return 128 * (g >> 1) + 32 * (g & 1) + 64 * h;
+  return 64 * g + 32 * h;
+}
 
-  const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const uint32_t wc = wave % WC, sw = wave / WC;
-  const uint32_t col = lane & 15, g = lane >> 4;
-  const uint64_t n_raw = (static_cast<uint64_t>(blockIdx.x) * WC + wc) * 16 + col;
-  // this wavefront's tile of 16 outputs (the grid's last tiles may be past
-  // the end: they re-read the last tile, whose rows past n are zero padding)
+// Half window item hi of a chunk of `units` units: window (row m, unit u,
+// lane group g, half h) = hi / 2, elements 16 * (hi % 2) + [0, 16) of it.
+// The two halves of a window sit in adjacent lanes.
+struct Item {
+  uint32_t m, u, g, h, half;
+};
+__device__ __forceinline__ Item item_of(uint32_t hi, uint32_t units) {
+  Item it;
+  const uint32_t w = hi >> 1;
+  it.half = hi & 1;
+  it.m = w / (units * 8);
+  const uint32_t r = w % (units * 8);
+  it.u = r >> 3;
+  it.g = (r >> 1) & 3;
+  it.h = r & 1;
+  return it;
+}
+
+struct HalfX {
+  float4 v[4];
+};
+
+template <int QT>
+__device__ __forceinline__ void load_half(const float* x, uint32_t K, uint32_t k0, const Item& it,
+                                          HalfX& o) {
+  const float4* p = reinterpret_cast<const float4*>(
+      x + static_cast<uint64_t>(it.m) * K + k0 + 256 * it.u + window_first<QT>(it.g, it.h) + 16 * it.half);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) o.v[i] = p[i];
+}
+
+// Digits and sums of one half window into LDS. Every lane of the wavefront
+// takes part (the window max and the other half's sum come from the
+// neighbouring lane); only `valid` items store.
+//   digits: [m][u][t][g] 32-byte records, digit d of the 8 activations of
+//           step t at byte 8*d;
+//   aux:    [m][u][g][h] float4 {2^-s, sum of elements 0-15, of 16-31, 0}.
+__device__ __forceinline__ void store_half(const HalfX& o, const Item& it, bool valid,
+                                           uint8_t* digits, float4* aux, uint32_t cu) {
+  const float xs[16] = {o.v[0].x, o.v[0].y, o.v[0].z, o.v[0].w, o.v[1].x, o.v[1].y, o.v[1].z, o.v[1].w,
+                        o.v[2].x, o.v[2].y, o.v[2].z, o.v[2].w, o.v[3].x, o.v[3].y, o.v[3].z, o.v[3].w};
+  float mx = 0.0f, sum = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    mx = fmaxf(mx, fabsf(xs[j]));
+    sum += xs[j];
+  }
+  mx = fmaxf(mx, __shfl_xor(mx, 1));
+  const float other = __shfl_xor(sum, 1);
+  // 2^s with max|x| * 2^s < 2^29: F = rint(x * 2^s) keeps 30 bits with headroom
+  const int e = mx > 0.0f ? __builtin_amdgcn_frexp_expf(mx) : 0;
+  const int sh = 29 - e;
+  const float inv = mx > 0.0f ? ldexpf(1.0f, e - 29) : 0.0f;
+  if (!valid) return;
+  const uint32_t t0 = 4 * it.h + 2 * it.half;
+  uint8_t* dst0 = digits + ((it.m * cu + it.u) * 8 + t0) * 128 + it.g * 32;
+#pragma unroll
+  for (int tt = 0; tt < 2; ++tt) {
+    uint32_t dig[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int F = static_cast<int>(rintf(ldexpf(xs[8 * tt + j], sh)));
+      // signed base-256 digits: byte i of (F + 0x808080) ^ 0x808080
+      dig[j] = (static_cast<uint32_t>(F) + 0x00808080u) ^ 0x00808080u;
+    }
+    uint32_t lo[4], hi[4];
+    transpose4(dig, lo);
+    transpose4(dig + 4, hi);
+    uint8_t* dst = dst0 + tt * 128;
+    *reinterpret_cast<uint4*>(dst) = make_uint4(lo[0], hi[0], lo[1], hi[1]);
+    *reinterpret_cast<uint4*>(dst + 16) = make_uint4(lo[2], hi[2], lo[3], hi[3]);
+  }
+  if (it.half == 0)
+    aux[(it.m * cu + it.u) * 8 + it.g * 2 + it.h] = make_float4(inv, sum, other, 0.0f);
+}
+
+// SW wavefronts per workgroup (one 16-output tile), D units in flight per
+// wavefront, XP half windows of activations preloaded per thread.
+template <int QT, bool WIDE, int MT, int SW, int D>
+__global__ __launch_bounds__(64 * SW) void gemv_mfma_kernel(GemvMfmaArgs a) {
+  using U = Unit<QT>;
+  constexpr int kThreads = 64 * SW;
+  constexpr int XP = SW == 4 ? 1 : 2;
   constexpr Record R = record_geometry(QT, WIDE);
-  const uint32_t tile = min(blockIdx.x * WC + wc, a.w.tiles - 1);
-  const uint8_t* trec = a.w.qs + static_cast<uint64_t>(tile) * a.w.units * R.bytes;
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  // [0, kZeroBytes) zeros | digits [m][chunk unit][t][g] | aux [m][chunk unit][g][h]
+  const uint32_t cu = a.chunk_units;
+  uint8_t* const digits = lds + kZeroBytes;
+  float4* const aux = reinterpret_cast<float4*>(digits + MT * cu * kUnitDigitBytes);
+
+  const uint32_t tid = threadIdx.x, lane = tid & 63, sw = tid >> 6;
+  const uint32_t col = lane & 15, g = lane >> 4;
+  const uint32_t tile = blockIdx.x;
+  const uint64_t n_out = static_cast<uint64_t>(tile) * 16 + col;
+  const uint32_t units_total = a.w.units;
+  const uint8_t* trec = a.w.qs + static_cast<uint64_t>(tile) * units_total * R.bytes;
   const uint32_t K = static_cast<uint32_t>(a.w.k);
   const int M = a.m;
 
@@ -345,120 +397,65 @@ __global__ __launch_bounds__(64 * WC * SW) void gemv_mfma_kernel(GemvMfmaArgs a)
   const uint32_t arow = lane & 15, sigma = arow >> 2, digit = arow & 3;
   const bool a_live = sigma == g;
 
-  for (uint32_t i = tid; i < 256; i += kThreads) reinterpret_cast<uint32_t*>(lds_a + kLdsA)[i] = 0;
+  for (uint32_t i = tid; i < kZeroBytes / 4; i += kThreads) reinterpret_cast<uint32_t*>(lds)[i] = 0;
 
   float acc[MT];
 #pragma unroll
   for (int m = 0; m < MT; ++m) acc[m] = 0.0f;
 
-  // Units in flight per wavefront: their weight loads are issued before the
-  // activation prep of the chunk and refilled as units are consumed.
-  constexpr int D = (kWaves >= 16 || MT > 2) ? 2 : 4;
   typename U::Raw ring[D];
 
-  for (uint32_t k0 = 0; k0 < K; k0 += kChunk) {
-    const uint32_t kc = min(static_cast<uint32_t>(kChunk), K - k0);
-    const uint32_t units = kc / 256;
-    const uint32_t ku0 = k0 / 256;
-    const uint32_t u_begin = (units * sw) / SW, u_end = (units * (sw + 1)) / SW;
+  for (uint32_t ku0 = 0; ku0 < units_total; ku0 += cu) {
+    const uint32_t units = min(cu, units_total - ku0);
+    const uint32_t k0 = ku0 * 256;
+    const uint32_t halves = static_cast<uint32_t>(M) * units * 16;
+    // this wavefront's contiguous run of the chunk's units (balanced split)
+    const uint32_t u_begin = (units * sw) / SW;
+    const uint32_t u_count = (units * (sw + 1)) / SW - u_begin;
+    const uint32_t u_last = ku0 + (u_count ? u_begin + u_count - 1 : 0);
+
+    // activations first (so that waiting for them never waits for the
+    // weights), then this wavefront's first D units, unconditionally (slots
+    // past the run re-read its last unit)
+    HalfX xp[XP];
+    Item ip[XP];
+#pragma unroll
+    for (int i = 0; i < XP; ++i) {
+      const uint32_t hi = tid + kThreads * i;
+      ip[i] = item_of(hi < halves ? hi : 0, units);
+      load_half<QT>(a.x, K, k0, ip[i], xp[i]);
+    }
 #pragma unroll
     for (int i = 0; i < D; ++i)
-      if (u_begin + i < u_end) U::template load<WIDE>(trec + (ku0 + u_begin + i) * R.bytes, lane, ring[i]);
+      U::template load<WIDE>(trec + min(ku0 + u_begin + i, u_last) * R.bytes, lane, ring[i]);
 
-    // ---- prep: 8-element groups (m, unit, t, g), g fastest across threads ----
-    constexpr int kGroups = MT * kChunk / 8;
-    constexpr int kPer = (kGroups + kThreads - 1) / kThreads;
-    float xv[kPer][8];
-    float mx[MT];
 #pragma unroll
-    for (int m = 0; m < MT; ++m) mx[m] = 0.0f;
-#pragma unroll
-    for (int i = 0; i < kPer; ++i) {
-      const uint32_t gi = tid + kThreads * i;
-      const uint32_t m = gi / (units * 32), r = gi % (units * 32);
-      const uint32_t u = r >> 5, t = (r & 31) >> 2, gg = r & 3;
-      const bool ok = gi < static_cast<uint32_t>(MT) * units * 32 && static_cast<int>(m) < M;
-      if (ok) {
-        uint32_t e;
-        if constexpr (QT == kQ6_K) {
-          e = 128 * (gg >> 1) + 32 * (gg & 1) + 8 * (t & 3) + (t >= 4 ? 64 : 0);
-        } else {
-          e = 64 * gg + 8 * t;
-        }
-        const float4* xp = reinterpret_cast<const float4*>(a.x + static_cast<uint64_t>(m) * K + k0 + 256 * u + e);
-        const float4 x0 = xp[0], x1 = xp[1];
-        xv[i][0] = x0.x; xv[i][1] = x0.y; xv[i][2] = x0.z; xv[i][3] = x0.w;
-        xv[i][4] = x1.x; xv[i][5] = x1.y; xv[i][6] = x1.z; xv[i][7] = x1.w;
-      } else {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) xv[i][j] = 0.0f;
-      }
-      float lm = 0.0f;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) lm = fmaxf(lm, fabsf(xv[i][j]));
-#pragma unroll
-      for (int mm = 0; mm < MT; ++mm)
-        if (static_cast<uint32_t>(mm) == m) mx[mm] = fmaxf(mx[mm], lm);
-    }
-#pragma unroll
-    for (int m = 0; m < MT; ++m) {
-      const float w = wave_max(mx[m]);
-      if (lane == 0) lds_max[wave][m] = w;
-    }
-    __syncthreads();
-    if (tid < static_cast<uint32_t>(MT)) {
-      float mm = 0.0f;
-#pragma unroll
-      for (int w = 0; w < kWaves; ++w) mm = fmaxf(mm, lds_max[w][tid]);
-      // 2^s with max|x| * 2^s < 2^29: F = rint(x * 2^s) keeps 30 bits with headroom
-      const int e = mm > 0.0f ? __builtin_amdgcn_frexp_expf(mm) : 0;
-      lds_shift[tid] = 29 - e;
-      lds_inv[tid] = mm > 0.0f ? ldexpf(1.0f, e - 29) : 0.0f;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int i = 0; i < kPer; ++i) {
-      const uint32_t gi = tid + kThreads * i;
-      const uint32_t m = gi / (units * 32), r = gi % (units * 32);
-      const uint32_t u = r >> 5, t = (r & 31) >> 2, gg = r & 3;
-      if (gi < static_cast<uint32_t>(MT) * units * 32 && static_cast<int>(m) < M) {
-        const int sh = lds_shift[m];
-        uint32_t dig[8];
-        float s = 0.0f;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const int F = static_cast<int>(rintf(ldexpf(xv[i][j], sh)));
-          dig[j] = (static_cast<uint32_t>(F) + 0x00808080u) ^ 0x00808080u;
-          s += xv[i][j];
-        }
-        uint32_t lo[4], hi[4];
-        transpose4(dig, lo);
-        transpose4(dig + 4, hi);
-        uint8_t* dst = lds_a + ((((m * kUnitsChunk + u) * 8 + t) * 4 + gg) * 32);
-        *reinterpret_cast<uint4*>(dst) = make_uint4(lo[0], hi[0], lo[1], hi[1]);
-        *reinterpret_cast<uint4*>(dst + 16) = make_uint4(lo[2], hi[2], lo[3], hi[3]);
-        lds_gs[((m * kUnitsChunk + u) * 4 + gg) * 8 + t] = s;
-      }
+    for (int i = 0; i < XP; ++i) store_half(xp[i], ip[i], tid + kThreads * i < halves, digits, aux, cu);
+    for (uint32_t h0 = XP * kThreads; h0 < halves; h0 += kThreads) {
+      const uint32_t hi = h0 + tid;
+      Item it = item_of(hi < halves ? hi : 0, units);
+      HalfX xh;
+      load_half<QT>(a.x, K, k0, it, xh);
+      store_half(xh, it, hi < halves, digits, aux, cu);
     }
     __syncthreads();
 
-    // ---- main: this wavefront's units of the chunk, D in flight ----
-    for (uint32_t ub = u_begin; ub < u_end; ub += D) {
+    // ---- main: this wavefront's units, D in flight ----
+    // The first batch is straight-line code on the registers loaded above (a
+    // loop over it would copy the ring into loop-carried registers, waiting
+    // for every load); later batches reload the ring and consume it.
+    auto consume = [&](uint32_t j) {
 #pragma unroll
       for (int i = 0; i < D; ++i) {
-        const uint32_t u = ub + i;
-        if (u >= u_end) break;
+        if (j + i >= u_count) break;
+        const uint32_t u = u_begin + j + i;  // chunk-relative unit
         float sa[U::kWindows], sb[U::kWindows];
         U::template scales<WIDE>(g, ring[i], sa, sb);
-        const typename U::Raw cur = ring[i];
-        if (u + D < u_end) U::template load<WIDE>(trec + (ku0 + u + D) * R.bytes, lane, ring[i]);
 #pragma unroll
         for (int m = 0; m < MT; ++m) {
           if (m >= M) break;
-          const uint8_t* abase = a_live ? lds_a + (((m * kUnitsChunk + u) * 8) * 4 + g) * 32 + digit * 8
-                                        : lds_a + kLdsA;
-          const float inv = lds_inv[m];
-          const float* gs = lds_gs + ((m * kUnitsChunk + u) * 4 + g) * 8;
+          const uint8_t* abase = a_live ? digits + ((m * cu + u) * 8 * 4 + g) * 32 + digit * 8 : lds;
+          const float4* ax = aux + (m * cu + u) * 8 + g * 2;
 #pragma unroll
           for (int w = 0; w < U::kWindows; ++w) {
             v4i c = {0, 0, 0, 0};
@@ -466,29 +463,31 @@ __global__ __launch_bounds__(64 * WC * SW) void gemv_mfma_kernel(GemvMfmaArgs a)
             for (int s = 0; s < U::kSteps; ++s) {
               const int t = w * U::kSteps + s;
               const long av = *reinterpret_cast<const long*>(abase + t * 128);
-              c = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, U::codes(cur, g, t), c, 0, 0, 0);
+              c = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, U::codes(ring[i], g, t), c, 0, 0, 0);
             }
             // combine digit sums (exact int32) in f32
             const float comb = fmaf(fmaf(fmaf(static_cast<float>(c[3]), 256.0f, static_cast<float>(c[2])),
                                          256.0f, static_cast<float>(c[1])),
                                     256.0f, static_cast<float>(c[0]));
-            acc[m] = fmaf(sa[w] * inv, comb, acc[m]);
+            const int h = U::kSteps == 4 ? w : (w >> 1);
+            const float4 wx = ax[h];
+            acc[m] = fmaf(sa[w] * wx.x, comb, acc[m]);
             if constexpr (U::kMin) {
-              float xs;
-              if constexpr (U::kSteps == 4) {
-                const float4 v = *reinterpret_cast<const float4*>(gs + 4 * w);
-                xs = (v.x + v.y) + (v.z + v.w);
-              } else {
-                const float2 v = *reinterpret_cast<const float2*>(gs + 2 * w);
-                xs = v.x + v.y;
-              }
+              const float xs = U::kSteps == 4 ? wx.y + wx.z : ((w & 1) ? wx.z : wx.y);
               acc[m] = fmaf(-sb[w], xs, acc[m]);
             }
           }
         }
       }
+    };
+    consume(0);
+    for (uint32_t j = D; j < u_count; j += D) {
+#pragma unroll
+      for (int i = 0; i < D; ++i)
+        U::template load<WIDE>(trec + min(ku0 + u_begin + j + i, u_last) * R.bytes, lane, ring[i]);
+      consume(j);
     }
-    __syncthreads();  // LDS reused by the next chunk
+    __syncthreads();  // LDS reused by the next chunk / the reduction
   }
 
   // ---- reduce: 4 lane groups of a column, then the SW K-parts ----
@@ -499,71 +498,84 @@ __global__ __launch_bounds__(64 * WC * SW) void gemv_mfma_kernel(GemvMfmaArgs a)
     v += __shfl_xor(v, 32);
     acc[m] = v;
   }
-  if constexpr (SW > 1) {
-    if (g == 0) {
+  float* red = reinterpret_cast<float*>(digits);  // [SW][MT][16]
+  if (g == 0) {
 #pragma unroll
-      for (int m = 0; m < MT; ++m) lds_red[sw][m][wc * 16 + col] = acc[m];
-    }
-    __syncthreads();
-    if (sw == 0 && g == 0 && n_raw < a.w.n) {
+    for (int m = 0; m < MT; ++m) red[(sw * MT + m) * 16 + col] = acc[m];
+  }
+  __syncthreads();
+  if (sw == 0 && g == 0 && n_out < a.w.n) {
 #pragma unroll
-      for (int m = 0; m < MT; ++m) {
-        if (m >= M) break;
-        float v = lds_red[0][m][wc * 16 + col];
+    for (int m = 0; m < MT; ++m) {
+      if (m >= M) break;
+      float v = red[m * 16 + col];
 #pragma unroll
-        for (int p = 1; p < SW; ++p) v += lds_red[p][m][wc * 16 + col];
-        a.y[static_cast<uint64_t>(m) * a.w.n + n_raw] = v;
-      }
-    }
-  } else {
-    if (g == 0 && n_raw < a.w.n) {
-#pragma unroll
-      for (int m = 0; m < MT; ++m) {
-        if (m >= M) break;
-        a.y[static_cast<uint64_t>(m) * a.w.n + n_raw] = acc[m];
-      }
+      for (int p = 1; p < SW; ++p) v += red[(p * MT + m) * 16 + col];
+      a.y[static_cast<uint64_t>(m) * a.w.n + n_out] = v;
     }
   }
 }
 
 namespace {
 
-template <int QT, bool WIDE, int MT, int WC, int SW>
-hipError_t launch4(const GemvMfmaArgs& a, hipStream_t st) {
-  const uint64_t tiles = (a.w.n + 15) / 16;
-  const uint32_t grid = static_cast<uint32_t>((tiles + WC - 1) / WC);
-  hipLaunchKernelGGL((gemv_mfma_kernel<QT, WIDE, MT, WC, SW>), dim3(grid), dim3(64 * WC * SW), 0, st, a);
+uint32_t lds_bytes(int mt, uint32_t chunk_units, int sw) {
+  const uint32_t main = kZeroBytes + static_cast<uint32_t>(mt) * chunk_units * (kUnitDigitBytes + kUnitAuxBytes);
+  const uint32_t red = kZeroBytes + static_cast<uint32_t>(sw * mt * 16 * 4);
+  return main > red ? main : red;
+}
+
+template <int QT, bool WIDE, int MT, int SW, int D>
+hipError_t launch4(GemvMfmaArgs a, hipStream_t st) {
+  const uint32_t cap = (kMaxLds - kZeroBytes) / (MT * (kUnitDigitBytes + kUnitAuxBytes));
+  a.chunk_units = a.w.units < cap ? a.w.units : cap;
+  const uint32_t bytes = lds_bytes(MT, a.chunk_units, SW);
+  auto kern = gemv_mfma_kernel<QT, WIDE, MT, SW, D>;
+  if (bytes > 65536) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(bytes));
+    if (e != hipSuccess) return e;
+  }
+  hipLaunchKernelGGL(kern, dim3(a.w.tiles), dim3(64 * SW), bytes, st, a);
   return hipGetLastError();
 }
 
-// shape id -> (output tiles per workgroup WC, K parts SW)
+// (wavefronts per workgroup, units in flight per wavefront) for `sw` and the
+// units each wavefront holds
 template <int QT, bool WIDE, int MT>
-hipError_t launch_split(const GemvMfmaArgs& a, int shape, hipStream_t st) {
-  switch (shape) {
-    case 0: return launch4<QT, WIDE, MT, 4, 1>(a, st);
-    case 1: return launch4<QT, WIDE, MT, 4, 2>(a, st);
-    case 2: return launch4<QT, WIDE, MT, 4, 4>(a, st);
-    case 3: return launch4<QT, WIDE, MT, 2, 8>(a, st);
-    case 4: return launch4<QT, WIDE, MT, 1, 16>(a, st);
-    case 5: return launch4<QT, WIDE, MT, 2, 4>(a, st);
-    default: return launch4<QT, WIDE, MT, 1, 8>(a, st);
+hipError_t launch_split(const GemvMfmaArgs& a, int sw, hipStream_t st) {
+  const uint32_t cap = (kMaxLds - kZeroBytes) / (MT * (kUnitDigitBytes + kUnitAuxBytes));
+  const uint32_t chunk = a.w.units < cap ? a.w.units : cap;
+  if constexpr (MT >= 8) {
+    // eight or more activation rows: only 4-wavefront workgroups keep the
+    // accumulators and the ring in registers without spilling
+    (void)sw;
+    (void)chunk;
+    return launch4<QT, WIDE, MT, 4, 4>(a, st);
+  } else {
+    if (sw == 4) return launch4<QT, WIDE, MT, 4, 4>(a, st);
+    const uint32_t upw = (chunk + 7) / 8;
+    if (upw <= 2) return launch4<QT, WIDE, MT, 8, 2>(a, st);
+    if constexpr (MT == 1) {
+      if (upw > 4) return launch4<QT, WIDE, MT, 8, 8>(a, st);
+    }
+    return launch4<QT, WIDE, MT, 8, 4>(a, st);
   }
 }
 
 template <int QT, bool WIDE>
-hipError_t launch_m(const GemvMfmaArgs& a, int mt, int split, hipStream_t st) {
+hipError_t launch_m(const GemvMfmaArgs& a, int mt, int sw, hipStream_t st) {
   switch (mt) {
-    case 1: return launch_split<QT, WIDE, 1>(a, split, st);
-    case 2: return launch_split<QT, WIDE, 2>(a, split, st);
-    case 4: return launch_split<QT, WIDE, 4>(a, split, st);
-    case 8: return launch_split<QT, WIDE, 8>(a, split, st);
-    default: return launch_split<QT, WIDE, 16>(a, split, st);
+    case 1: return launch_split<QT, WIDE, 1>(a, sw, st);
+    case 2: return launch_split<QT, WIDE, 2>(a, sw, st);
+    case 4: return launch_split<QT, WIDE, 4>(a, sw, st);
+    case 8: return launch_split<QT, WIDE, 8>(a, sw, st);
+    default: return launch_split<QT, WIDE, 16>(a, sw, st);
   }
 }
 
 template <int QT>
-hipError_t launch_w(const GemvMfmaArgs& a, bool wide, int mt, int split, hipStream_t st) {
-  return wide ? launch_m<QT, true>(a, mt, split, st) : launch_m<QT, false>(a, mt, split, st);
+hipError_t launch_w(const GemvMfmaArgs& a, bool wide, int mt, int sw, hipStream_t st) {
+  return wide ? launch_m<QT, true>(a, mt, sw, st) : launch_m<QT, false>(a, mt, sw, st);
 }
 
 }  // namespace
@@ -572,24 +584,24 @@ bool gemv_mfma_supported(int32_t qtype, int32_t layout, uint64_t k) {
   return layout == kOutputRows && qtype >= kQ8_0 && qtype <= kQ6_K && k % 256 == 0 && k > 0;
 }
 
-int gemv_mfma_split(uint64_t n) {
-  // Workgroup shape: 64 outputs and 4 K parts per workgroup when there are
-  // enough outputs to give every CU one; fewer outputs and more K parts per
-  // workgroup otherwise (the activation prep is shared by the workgroup).
+int gemv_mfma_split(uint64_t k, uint64_t n) {
+  // Wavefronts per workgroup (K parts of one 16-output tile): 4 when there
+  // are enough tiles for ~2 workgroups per CU, 8 otherwise, so that the grid
+  // keeps >= ~2048 wavefronts streaming.
+  (void)k;
   const uint64_t tiles = (n + 15) / 16;
-  if (tiles / 4 >= 192) return 2;
-  if (tiles / 2 >= 192) return 3;
-  return 4;
+  return tiles >= 512 ? 4 : 8;
 }
 
-hipError_t launch_gemv_mfma(int32_t qtype, bool wide, int mt, int split, const GemvMfmaArgs& a,
+hipError_t launch_gemv_mfma(int32_t qtype, bool wide, int mt, int sw, const GemvMfmaArgs& a,
                             hipStream_t st) {
+  if (sw != 4 && sw != 8) return hipErrorInvalidValue;
   switch (qtype) {
-    case kQ8_0: return launch_w<kQ8_0>(a, wide, mt, split, st);
-    case kQ4_0: return launch_w<kQ4_0>(a, wide, mt, split, st);
-    case kQ4_K: return launch_w<kQ4_K>(a, wide, mt, split, st);
-    case kQ5_K: return launch_w<kQ5_K>(a, wide, mt, split, st);
-    case kQ6_K: return launch_w<kQ6_K>(a, wide, mt, split, st);
+    case kQ8_0: return launch_w<kQ8_0>(a, wide, mt, sw, st);
+    case kQ4_0: return launch_w<kQ4_0>(a, wide, mt, sw, st);
+    case kQ4_K: return launch_w<kQ4_K>(a, wide, mt, sw, st);
+    case kQ5_K: return launch_w<kQ5_K>(a, wide, mt, sw, st);
+    case kQ6_K: return launch_w<kQ6_K>(a, wide, mt, sw, st);
     default: return hipErrorInvalidValue;
   }
 }

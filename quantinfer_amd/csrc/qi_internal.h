@@ -33,9 +33,10 @@ struct GemvMfmaArgs {
   const float* x;  // [m, k] device, 16-byte aligned rows
   float* y;        // [m, n]
   int m;           // rows in this launch (<= compile-time tile)
+  uint32_t chunk_units = 0;  // set by the launcher: K units whose activation digits fit LDS
 };
 bool gemv_mfma_supported(int32_t qtype, int32_t layout, uint64_t k);
-int gemv_mfma_split(uint64_t n);
+int gemv_mfma_split(uint64_t k, uint64_t n);
 hipError_t launch_gemv_mfma(int32_t qtype, bool wide, int mt, int split, const GemvMfmaArgs& a,
                             hipStream_t st);
 
