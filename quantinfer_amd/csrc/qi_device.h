@@ -130,17 +130,35 @@ struct Exact<kQ4_0, WIDE> {
   }
 };
 
+// (sc, m) of sub-block `sub` of a Q4_K/Q5_K block: the reference's packed
+// bytes in planar images, the lane-group field in tiled records (qi_image.h).
+template <int QT>
+__device__ __forceinline__ void kq_scale_min(const View& v, const BlockLoc& L, uint32_t sub,
+                                             uint32_t& sc, uint32_t& mn) {
+  if (L.rec == nullptr) {
+    uint32_t w[3];
+#pragma unroll
+    for (int i = 0; i < 3; ++i)
+      w[i] = static_cast<uint32_t>(sc_byte<QT>(v, L, 4 * i)) |
+             (static_cast<uint32_t>(sc_byte<QT>(v, L, 4 * i + 1)) << 8) |
+             (static_cast<uint32_t>(sc_byte<QT>(v, L, 4 * i + 2)) << 16) |
+             (static_cast<uint32_t>(sc_byte<QT>(v, L, 4 * i + 3)) << 24);
+    kquant_sc_m(w[0], w[1], w[2], static_cast<int>(sub), sc, mn);
+    return;
+  }
+  const uint32_t g = sub / 2;
+  const uint32_t f = static_cast<uint32_t>(sc_byte<QT>(v, L, 3 * g)) |
+                     (static_cast<uint32_t>(sc_byte<QT>(v, L, 3 * g + 1)) << 8) |
+                     (static_cast<uint32_t>(sc_byte<QT>(v, L, 3 * g + 2)) << 16);
+  const uint32_t sh = (sub & 1) ? 12 : 0;
+  sc = (f >> sh) & 63u;
+  mn = (f >> (sh + 6)) & 63u;
+}
+
 template <int QT, bool WIDE>
 __device__ __forceinline__ float exact_q45k(const View& v, const BlockLoc& L, uint32_t l) {
-  uint32_t w[3];
-#pragma unroll
-  for (int i = 0; i < 3; ++i)
-    w[i] = static_cast<uint32_t>(sc_byte<QT>(v, L, 4 * i)) |
-           (static_cast<uint32_t>(sc_byte<QT>(v, L, 4 * i + 1)) << 8) |
-           (static_cast<uint32_t>(sc_byte<QT>(v, L, 4 * i + 2)) << 16) |
-           (static_cast<uint32_t>(sc_byte<QT>(v, L, 4 * i + 3)) << 24);
   uint32_t sc, mn;
-  kquant_sc_m(w[0], w[1], w[2], static_cast<int>(l / 32), sc, mn);
+  kq_scale_min<QT>(v, L, l / 32, sc, mn);
   const uint32_t group = l / 64, within = l % 64;
   const uint8_t packed = code_byte<QT>(v, L, group * 32 + within % 32);
   uint32_t q = within < 32 ? (packed & 15u) : (packed >> 4);
@@ -176,7 +194,8 @@ struct Exact<kQ6_K, WIDE> {
     const uint32_t low = chunk < 2 ? (packed & 15u) : (packed >> 4);
     const uint32_t high = qh_byte<kQ6_K>(v, L, ip * 32 + il);
     const int32_t q = static_cast<int32_t>(low | (((high >> (chunk * 2)) & 3u) << 4));
-    const float sc = static_cast<float>(static_cast<int8_t>(sc_byte<kQ6_K>(v, L, l / 16)));
+    const uint32_t si = L.rec == nullptr ? l / 16 : q6_scale_pos(l / 16);
+    const float sc = static_cast<float>(static_cast<int8_t>(sc_byte<kQ6_K>(v, L, si)));
     const float d = scale_d<kQ6_K, WIDE>(v, L);
     return d * sc * static_cast<float>(q - 32);  // matmul.rs:279
   }

@@ -24,11 +24,11 @@
 // the four digit sums of its own codes in its four C registers, next to its
 // own scale. A 256-element unit is 8 steps x 4 groups x 8 codes.
 //
-// Work split: one workgroup per tile of 16 outputs, SW wavefronts splitting
-// the tile's K range (contiguous runs of units, reduced through LDS at the
+// Work split: WC tiles of 16 outputs per workgroup, SW wavefronts per tile
+// splitting its K range (contiguous runs of units, reduced through LDS at the
 // end). The activation digits of a K chunk are built once per workgroup into
-// LDS (half a window per thread, the window max from the neighbouring lane:
-// a single barrier).
+// LDS and shared by its WC tiles (half a window per thread, the window max
+// from the neighbouring lane: a single barrier).
 // Each wavefront issues its activation loads, then the loads of up to D
 // units, before it waits for anything (vector loads complete in order, so
 // waiting for the activations never waits for the weights); a workgroup's
@@ -186,13 +186,16 @@ struct UnitQ45K {
       d = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(r.s0)));
       dmin = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(r.s1)));
     }
-    uint32_t s0, m0, s1, m1;
-    kquant_sc_m(r.sc[0], r.sc[1], r.sc[2], static_cast<int>(2 * g), s0, m0);
-    kquant_sc_m(r.sc[0], r.sc[1], r.sc[2], static_cast<int>(2 * g + 1), s1, m1);
-    a[0] = d * static_cast<float>(s0);
-    b[0] = dmin * static_cast<float>(m0);
-    a[1] = d * static_cast<float>(s1);
-    b[1] = dmin * static_cast<float>(m1);
+    // lane group g's 24-bit field sits at bytes 3g..3g+2 of the 12 scale
+    // bytes: one byte permute from the word pair that holds it
+    const uint32_t lo = g < 2 ? r.sc[0] : r.sc[1];
+    const uint32_t hi = g < 2 ? r.sc[1] : r.sc[2];
+    const uint32_t first = g == 0 ? 0 : g == 1 ? 3 : g == 2 ? 2 : 5;
+    const uint32_t f = __builtin_amdgcn_perm(hi, lo, first * 0x00010101u + 0x0C020100u);
+    a[0] = d * static_cast<float>(f & 63u);
+    b[0] = dmin * static_cast<float>((f >> 6) & 63u);
+    a[1] = d * static_cast<float>((f >> 12) & 63u);
+    b[1] = dmin * static_cast<float>(f >> 18);
   }
   __device__ static long codes(const Raw& r, uint32_t g, int t) {
     const int tt = t & 3;
@@ -228,8 +231,8 @@ struct Unit<kQ6_K> {
   struct Raw {
     uint4 q[2];
     uint4 h[2];
-    uint2 sc;
-    uint32_t d;  // f16 in the low half, or f32
+    uint32_t sc;  // this lane group's four int8 sub-scales
+    uint32_t d;   // f16 in the low half, or f32
   };
   template <bool W>
   __device__ static void load(const uint8_t* rec, uint32_t lane, Raw& r) {
@@ -239,22 +242,19 @@ struct Unit<kQ6_K> {
     r.q[0] = p[0]; r.q[1] = p[64];
     const uint4* h = reinterpret_cast<const uint4*>(rec + R.qh) + 32 * ip + col;
     r.h[0] = h[0]; r.h[1] = h[16];
-    r.sc = *reinterpret_cast<const uint2*>(rec + R.sc + col * 16 + 8 * ip);
+    r.sc = *reinterpret_cast<const uint32_t*>(rec + R.sc + col * 16 + 4 * (lane >> 4));
     if constexpr (W) r.d = reinterpret_cast<const uint32_t*>(rec + R.d)[col];
     else r.d = reinterpret_cast<const uint16_t*>(rec + R.d)[col];
   }
   template <bool W>
-  __device__ static void scales(uint32_t g, const Raw& r, float a[4], float b[4]) {
+  __device__ static void scales(uint32_t, const Raw& r, float a[4], float b[4]) {
     float d;
     if constexpr (W) d = __builtin_bit_cast(float, r.d);
     else d = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(r.d)));
-    const uint32_t c = g & 1;
-    const uint32_t lo = c ? (r.sc.x >> 16) : r.sc.x;  // sub-scales 2c, 2c+1 of this half
-    const uint32_t hi = c ? (r.sc.y >> 16) : r.sc.y;  // sub-scales 2c+4, 2c+5
-    a[0] = d * static_cast<float>(static_cast<int8_t>(lo & 0xFFu));
-    a[1] = d * static_cast<float>(static_cast<int8_t>((lo >> 8) & 0xFFu));
-    a[2] = d * static_cast<float>(static_cast<int8_t>(hi & 0xFFu));
-    a[3] = d * static_cast<float>(static_cast<int8_t>((hi >> 8) & 0xFFu));
+    // sub-scales 8ip + 2c + {0, 1, 4, 5} of lane group g = 2ip + c
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      a[i] = d * static_cast<float>(static_cast<int32_t>(r.sc << (24 - 8 * i)) >> 24);
 #pragma unroll
     for (int i = 0; i < 4; ++i) b[i] = 32.0f * a[i];
   }
@@ -370,13 +370,14 @@ __device__ __forceinline__ void store_half(const HalfX& o, const Item& it, bool 
     aux[(it.m * cu + it.u) * 8 + it.g * 2 + it.h] = make_float4(inv, sum, other, 0.0f);
 }
 
-// SW wavefronts per workgroup (one 16-output tile), D units in flight per
-// wavefront, XP half windows of activations preloaded per thread.
-template <int QT, bool WIDE, int MT, int SW, int D>
-__global__ __launch_bounds__(64 * SW) void gemv_mfma_kernel(GemvMfmaArgs a) {
+// WC tiles of 16 outputs per workgroup, SW wavefronts per tile splitting its
+// K range, D units in flight per wavefront, XP half windows of activations
+// preloaded per thread (the WC tiles share one activation prep).
+template <int QT, bool WIDE, int MT, int SW, int D, int WC>
+__global__ __launch_bounds__(64 * SW * WC) void gemv_mfma_kernel(GemvMfmaArgs a) {
   using U = Unit<QT>;
-  constexpr int kThreads = 64 * SW;
-  constexpr int XP = SW == 4 ? 1 : 2;
+  constexpr int kThreads = 64 * SW * WC;
+  constexpr int XP = SW == 8 ? 2 : 1;
   constexpr Record R = record_geometry(QT, WIDE);
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   // [0, kZeroBytes) zeros | digits [m][chunk unit][t][g] | aux [m][chunk unit][g][h]
@@ -384,10 +385,14 @@ __global__ __launch_bounds__(64 * SW) void gemv_mfma_kernel(GemvMfmaArgs a) {
   uint8_t* const digits = lds + kZeroBytes;
   float4* const aux = reinterpret_cast<float4*>(digits + MT * cu * kUnitDigitBytes);
 
-  const uint32_t tid = threadIdx.x, lane = tid & 63, sw = tid >> 6;
+  const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const uint32_t sw = wave % SW, wc = wave / SW;
   const uint32_t col = lane & 15, g = lane >> 4;
-  const uint32_t tile = blockIdx.x;
-  const uint64_t n_out = static_cast<uint64_t>(tile) * 16 + col;
+  // the grid's last workgroup may hold a tile past the end: it streams the
+  // last tile again and stores nothing
+  const uint32_t tile_raw = blockIdx.x * WC + wc;
+  const uint32_t tile = min(tile_raw, a.w.tiles - 1);
+  const uint64_t n_out = static_cast<uint64_t>(tile_raw) * 16 + col;
   const uint32_t units_total = a.w.units;
   const uint8_t* trec = a.w.qs + static_cast<uint64_t>(tile) * units_total * R.bytes;
   const uint32_t K = static_cast<uint32_t>(a.w.k);
@@ -465,10 +470,10 @@ __global__ __launch_bounds__(64 * SW) void gemv_mfma_kernel(GemvMfmaArgs a) {
               const long av = *reinterpret_cast<const long*>(abase + t * 128);
               c = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, U::codes(ring[i], g, t), c, 0, 0, 0);
             }
-            // combine digit sums (exact int32) in f32
-            const float comb = fmaf(fmaf(fmaf(static_cast<float>(c[3]), 256.0f, static_cast<float>(c[2])),
-                                         256.0f, static_cast<float>(c[1])),
-                                    256.0f, static_cast<float>(c[0]));
+            // combine the digit sums: pairs exactly in int32 (|C0| < 2^20,
+            // |C1 * 256| < 2^28), the two halves in f32
+            const float comb = fmaf(static_cast<float>(c[2] + c[3] * 256), 65536.0f,
+                                    static_cast<float>(c[0] + c[1] * 256));
             const int h = U::kSteps == 4 ? w : (w >> 1);
             const float4 wx = ax[h];
             acc[m] = fmaf(sa[w] * wx.x, comb, acc[m]);
@@ -498,19 +503,19 @@ __global__ __launch_bounds__(64 * SW) void gemv_mfma_kernel(GemvMfmaArgs a) {
     v += __shfl_xor(v, 32);
     acc[m] = v;
   }
-  float* red = reinterpret_cast<float*>(digits);  // [SW][MT][16]
+  float* red = reinterpret_cast<float*>(digits);  // [WC][SW][MT][16]
   if (g == 0) {
 #pragma unroll
-    for (int m = 0; m < MT; ++m) red[(sw * MT + m) * 16 + col] = acc[m];
+    for (int m = 0; m < MT; ++m) red[((wc * SW + sw) * MT + m) * 16 + col] = acc[m];
   }
   __syncthreads();
   if (sw == 0 && g == 0 && n_out < a.w.n) {
 #pragma unroll
     for (int m = 0; m < MT; ++m) {
       if (m >= M) break;
-      float v = red[m * 16 + col];
+      float v = red[(wc * SW * MT + m) * 16 + col];
 #pragma unroll
-      for (int p = 1; p < SW; ++p) v += red[(p * MT + m) * 16 + col];
+      for (int p = 1; p < SW; ++p) v += red[((wc * SW + p) * MT + m) * 16 + col];
       a.y[static_cast<uint64_t>(m) * a.w.n + n_out] = v;
     }
   }
@@ -518,24 +523,24 @@ __global__ __launch_bounds__(64 * SW) void gemv_mfma_kernel(GemvMfmaArgs a) {
 
 namespace {
 
-uint32_t lds_bytes(int mt, uint32_t chunk_units, int sw) {
+uint32_t lds_bytes(int mt, uint32_t chunk_units, int waves) {
   const uint32_t main = kZeroBytes + static_cast<uint32_t>(mt) * chunk_units * (kUnitDigitBytes + kUnitAuxBytes);
-  const uint32_t red = kZeroBytes + static_cast<uint32_t>(sw * mt * 16 * 4);
+  const uint32_t red = kZeroBytes + static_cast<uint32_t>(waves * mt * 16 * 4);
   return main > red ? main : red;
 }
 
-template <int QT, bool WIDE, int MT, int SW, int D>
+template <int QT, bool WIDE, int MT, int SW, int D, int WC>
 hipError_t launch4(GemvMfmaArgs a, hipStream_t st) {
   const uint32_t cap = (kMaxLds - kZeroBytes) / (MT * (kUnitDigitBytes + kUnitAuxBytes));
   a.chunk_units = a.w.units < cap ? a.w.units : cap;
-  const uint32_t bytes = lds_bytes(MT, a.chunk_units, SW);
-  auto kern = gemv_mfma_kernel<QT, WIDE, MT, SW, D>;
+  const uint32_t bytes = lds_bytes(MT, a.chunk_units, SW * WC);
+  auto kern = gemv_mfma_kernel<QT, WIDE, MT, SW, D, WC>;
   if (bytes > 65536) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(bytes));
     if (e != hipSuccess) return e;
   }
-  hipLaunchKernelGGL(kern, dim3(a.w.tiles), dim3(64 * SW), bytes, st, a);
+  hipLaunchKernelGGL(kern, dim3((a.w.tiles + WC - 1) / WC), dim3(64 * SW * WC), bytes, st, a);
   return hipGetLastError();
 }
 
@@ -546,19 +551,25 @@ hipError_t launch_split(const GemvMfmaArgs& a, int sw, hipStream_t st) {
   const uint32_t cap = (kMaxLds - kZeroBytes) / (MT * (kUnitDigitBytes + kUnitAuxBytes));
   const uint32_t chunk = a.w.units < cap ? a.w.units : cap;
   if constexpr (MT >= 8) {
-    // eight or more activation rows: only 4-wavefront workgroups keep the
-    // accumulators and the ring in registers without spilling
+    // eight or more activation rows: only 4-wavefront workgroups (one tile)
+    // keep the accumulators and the ring in registers without spilling
     (void)sw;
     (void)chunk;
-    return launch4<QT, WIDE, MT, 4, 4>(a, st);
+    return launch4<QT, WIDE, MT, 4, 4, 1>(a, st);
   } else {
-    if (sw == 4) return launch4<QT, WIDE, MT, 4, 4>(a, st);
-    const uint32_t upw = (chunk + 7) / 8;
-    if (upw <= 2) return launch4<QT, WIDE, MT, 8, 2>(a, st);
-    if constexpr (MT == 1) {
-      if (upw > 4) return launch4<QT, WIDE, MT, 8, 8>(a, st);
+    if (sw == 4) {
+      // two tiles share the activation prep where the register budget of an
+      // 8-wavefront workgroup keeps occupancy (measured: Q4_K and Q8_0 gain,
+      // Q4_0/Q5_K/Q6_K lose)
+      if constexpr (QT == kQ4_K || QT == kQ8_0) return launch4<QT, WIDE, MT, 4, 4, 2>(a, st);
+      else return launch4<QT, WIDE, MT, 4, 4, 1>(a, st);
     }
-    return launch4<QT, WIDE, MT, 8, 4>(a, st);
+    const uint32_t upw = (chunk + 7) / 8;
+    if (upw <= 2) return launch4<QT, WIDE, MT, 8, 2, 1>(a, st);
+    if constexpr (MT == 1) {
+      if (upw > 4) return launch4<QT, WIDE, MT, 8, 8, 1>(a, st);
+    }
+    return launch4<QT, WIDE, MT, 8, 4, 1>(a, st);
   }
 }
 

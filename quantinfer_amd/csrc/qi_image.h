@@ -25,7 +25,13 @@
 //            lane group g of row c sits at q*1024 + (16g + c)*16, so a
 //            wavefront load (lane 16g + c) of chunk q reads 1 KB contiguous;
 //     qh     16-byte chunk h of row c at h*256 + c*16 (Q5_K 2, Q6_K 4 chunks);
-//     sc     row c's packed scales at c*12 (Q4_K/Q5_K) or c*16 (Q6_K);
+//     sc     Q4_K/Q5_K: row c's 12 bytes at c*12 hold the same 96 bits as the
+//            GGUF packed 6-bit scales, regrouped per lane group: field g at
+//            bytes 3g..3g+2 (little endian) = sc[2g] | m[2g] << 6 |
+//            sc[2g+1] << 12 | m[2g+1] << 18, sub-block j's (sc, m) being what
+//            the reference unpacks (backends/cpu/src/matmul.rs:192-201);
+//            Q6_K: row c's 16 int8 sub-scales at c*16, lane group g = 2ip + h
+//            holding sub-scales 8ip + 2h + {0, 1, 4, 5} at bytes 4g..4g+3;
 //     d      row c's scales: c*8 + block (Q8_0/Q4_0) or c (K-quants) entries;
 //     dmin   row c at c (Q4_K/Q5_K).
 //   F32 weights keep the row-major [K, N] f32 matrix in qs.
@@ -146,5 +152,10 @@ int32_t plan_image(int32_t qtype, int32_t layout, uint64_t k, uint64_t n, const 
                    uint64_t count, Image* out, const char** why);
 // Write the image into host memory of im.bytes bytes.
 void fill_image(const Image& im, const void* blocks, void* out);
+
+// Tiled Q6_K record: byte position (0..15) of sub-scale i within a row's 16.
+constexpr uint32_t q6_scale_pos(uint32_t i) {
+  return 4 * (2 * (i / 8) + ((i % 8) % 4) / 2) + (i % 2) + 2 * ((i % 8) / 4);
+}
 
 }  // namespace qi

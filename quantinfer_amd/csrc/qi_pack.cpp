@@ -181,6 +181,39 @@ struct Dest {
   }
 };
 
+// 6-bit scale and min of sub-block j from a Q4_K/Q5_K block's 12 packed
+// bytes (backends/cpu/src/matmul.rs:192-201).
+void kq_unpack(const uint8_t s[12], int j, uint32_t* sc, uint32_t* m) {
+  if (j < 4) {
+    *sc = s[j] & 63u;
+    *m = s[j + 4] & 63u;
+  } else {
+    *sc = (s[j + 4] & 15u) | ((static_cast<uint32_t>(s[j - 4]) >> 6) << 4);
+    *m = (static_cast<uint32_t>(s[j + 4]) >> 4) | ((static_cast<uint32_t>(s[j]) >> 6) << 4);
+  }
+}
+
+// Scale bytes of a K-quant block: reference order in planar images, the
+// per-lane-group arrangement of the tiled records (qi_image.h).
+void put_kq_scales(const Dest& dst, const uint8_t s[12]) {
+  if (!dst.im->tiled) {
+    for (uint32_t o = 0; o < 12; ++o) *dst.sc(o) = s[o];
+    return;
+  }
+  for (int g = 0; g < 4; ++g) {
+    uint32_t sc0, m0, sc1, m1;
+    kq_unpack(s, 2 * g, &sc0, &m0);
+    kq_unpack(s, 2 * g + 1, &sc1, &m1);
+    const uint32_t f = sc0 | (m0 << 6) | (sc1 << 12) | (m1 << 18);
+    for (int b = 0; b < 3; ++b) *dst.sc(3 * g + b) = static_cast<uint8_t>(f >> (8 * b));
+  }
+}
+
+void put_q6_scales(const Dest& dst, const int8_t s[16]) {
+  for (uint32_t i = 0; i < 16; ++i)
+    *dst.sc(dst.im->tiled ? q6_scale_pos(i) : i) = static_cast<uint8_t>(s[i]);
+}
+
 }  // namespace
 
 void fill_image(const Image& im, const void* blocks, void* out) {
@@ -214,7 +247,7 @@ void fill_image(const Image& im, const void* blocks, void* out) {
       case kQ4_K: {
         const auto& b = as_blocks<qi_hip_q4_k_block>(blocks)[i];
         for (uint32_t o = 0; o < 128; ++o) *dst.code(o) = b.values[o];
-        for (uint32_t o = 0; o < 12; ++o) *dst.sc(o) = b.scales[o];
+        put_kq_scales(dst, b.scales);
         dst.scale(b.scale, false);
         dst.scale(b.min_scale, true);
         break;
@@ -223,7 +256,7 @@ void fill_image(const Image& im, const void* blocks, void* out) {
         const auto& b = as_blocks<qi_hip_q5_k_block>(blocks)[i];
         for (uint32_t o = 0; o < 128; ++o) *dst.code(o) = b.values[o];
         for (uint32_t o = 0; o < 32; ++o) *dst.qh(o) = b.high_bits[o];
-        for (uint32_t o = 0; o < 12; ++o) *dst.sc(o) = b.scales[o];
+        put_kq_scales(dst, b.scales);
         dst.scale(b.scale, false);
         dst.scale(b.min_scale, true);
         break;
@@ -232,7 +265,7 @@ void fill_image(const Image& im, const void* blocks, void* out) {
         const auto& b = as_blocks<qi_hip_q6_k_block>(blocks)[i];
         for (uint32_t o = 0; o < 128; ++o) *dst.code(o) = b.low_bits[o];
         for (uint32_t o = 0; o < 64; ++o) *dst.qh(o) = b.high_bits[o];
-        for (uint32_t o = 0; o < 16; ++o) *dst.sc(o) = static_cast<uint8_t>(b.scales[o]);
+        put_q6_scales(dst, b.scales);
         dst.scale(b.scale, false);
         break;
       }

@@ -27,6 +27,7 @@ def hip() -> ctypes.CDLL:
         h.hipMalloc.argtypes = [ctypes.POINTER(vp), sz]
         h.hipFree.argtypes = [vp]
         h.hipMemcpy.argtypes = [vp, vp, sz, i32]
+        h.hipMemcpyAsync.argtypes = [vp, vp, sz, i32, vp]
         h.hipMemset.argtypes = [vp, i32, sz]
         h.hipDeviceSynchronize.argtypes = []
         h.hipStreamCreate.argtypes = [ctypes.POINTER(vp)]
@@ -69,6 +70,10 @@ class DeviceBuffer:
         out = np.empty(shape, dtype=dtype)
         _ok(hip().hipMemcpy(out.ctypes.data, self.ptr, out.nbytes, D2H), "hipMemcpy D2H")
         return out
+
+    def copy_from(self, src: "DeviceBuffer", nbytes: int, stream: "Stream") -> None:
+        """Device-to-device copy on `stream` (the HIP runtime's copy kernel)."""
+        _ok(hip().hipMemcpyAsync(self.ptr, src.ptr, nbytes, D2D, stream.handle), "hipMemcpyAsync D2D")
 
     def free(self) -> None:
         if self.ptr:

@@ -104,14 +104,48 @@ def test_planar_image_holds_exactly_the_wire_bytes(qtype):
     assert payload == po.WIRE_BYTES[qtype] * count  # the image of an f16 tensor has wire size
 
 
+def _kq_packed_from_fields(sc):
+    """Tiled Q4_K/Q5_K scale bytes -> the GGUF 12-byte packing. The tiled
+    record holds field g = sc[2g] | m[2g] << 6 | sc[2g+1] << 12 | m[2g+1] << 18
+    at bytes 3g..3g+2; the GGUF packing (format gguf/writer.rs:216-219, read
+    back by backends/cpu/src/matmul.rs:192-201) keeps sc[i], m[i] (i < 4) in the
+    low 6 bits of bytes i, 4+i, their top bits holding bits 4-5 of sc[4+i],
+    m[4+i], whose low 4 bits fill bytes 8+i."""
+    sc = np.asarray(sc, dtype=np.uint32)
+    f = [int(sc[3 * g]) | int(sc[3 * g + 1]) << 8 | int(sc[3 * g + 2]) << 16 for g in range(4)]
+    s = [0] * 8
+    m = [0] * 8
+    for g in range(4):
+        s[2 * g], m[2 * g] = f[g] & 63, (f[g] >> 6) & 63
+        s[2 * g + 1], m[2 * g + 1] = (f[g] >> 12) & 63, (f[g] >> 18) & 63
+    out = [0] * 12
+    for i in range(4):
+        out[i] = s[i] | ((s[4 + i] >> 4) << 6)
+        out[4 + i] = m[i] | ((m[4 + i] >> 4) << 6)
+        out[8 + i] = (s[4 + i] & 15) | ((m[4 + i] & 15) << 4)
+    return np.asarray(out, dtype=np.uint8)
+
+
+def _q6_scales_from_tiled(sc):
+    """Tiled Q6_K sub-scales -> reference order: lane group g = 2ip + h holds
+    sub-scales 8ip + 2h + {0, 1, 4, 5} at bytes 4g..4g+3."""
+    out = np.zeros(16, dtype=np.uint8)
+    for g in range(4):
+        ip, h = divmod(g, 2)
+        for j, off in enumerate((0, 1, 4, 5)):
+            out[8 * ip + 2 * h + off] = sc[4 * g + j]
+    return out
+
+
 def _untile(qtype, image, k, n, f16):
     """Per-block fields of a tiled output-rows image, read back from the record
     arrangement: records of (16-output tile, 256-element unit) ordered
     [tile][unit]; inside a record the code slice of row c (its unit's code bytes
     in block order) is cut in four lane groups and 16-byte chunks, chunk q of
-    group g at q*1024 + (16g + c)*16; qh chunk h at h*256 + c*16; packed scales
-    at c*|sc|; d entries at c*bpu + block; dmin at c. Also returns the bytes of
-    the padding rows."""
+    group g at q*1024 + (16g + c)*16; qh chunk h at h*256 + c*16; scales at
+    c*|sc| (K-quants regrouped per lane group, returned here in GGUF order); d
+    entries at c*bpu + block; dmin at c. Also returns the bytes of the padding
+    rows."""
     qsb, qhb, scb, has_dmin = SIZES[qtype]
     bpu = 8 if qtype in (qa.Q8_0, qa.Q4_0) else 1
     ss = 2 if f16 else 4
@@ -135,6 +169,10 @@ def _untile(qtype, image, k, n, f16):
                                    for g in range(4) for q in range(quarter // 16)])
             qh = np.concatenate([rec[off_qh + h * 256 + c * 16:][:16] for h in range(qhb // 16)] or [[]])
             sc = rec[off_sc + c * scb:][:scb]
+            if qtype in (qa.Q4_K, qa.Q5_K):
+                sc = _kq_packed_from_fields(sc)
+            elif qtype == qa.Q6_K:
+                sc = _q6_scales_from_tiled(sc)
             per = [(code[bi * qsb:(bi + 1) * qsb], qh, sc, rec[off_d + (c * bpu + bi) * ss:][:ss],
                     rec[off_dm + c * ss:][:ss] if has_dmin else np.zeros(0, np.uint8)) for bi in range(bpu)]
             if row < n:
