@@ -112,6 +112,56 @@ def copy_calibration(steps: int, mib: int = 256) -> None:
     stream.destroy()
 
 
+MFMA_F16_PEAK_TFLOPS = 2500.0
+
+
+def gemm_bench(qtype: int, m: int, k: int, n: int, steps: int, warmup: int) -> dict:
+    """Prefill GEMM (MFMA mode, f16 operands, f32 accumulation): `steps`
+    back-to-back linear calls on resident inputs, event-timed on the launch
+    stream (each call is the f16 activation conversion plus the GEMM)."""
+    import quantinfer_amd as qa
+    from oracle import pyoracle as po  # input generation only
+    from quantinfer_amd import hiprt
+
+    ctx = qa.Context(0)
+    blocks = po.make_weights(qtype, k, n, seed=0x5EED0010 + qtype, outliers=qtype >= 3)
+    weights = [ctx.weights(qtype, qa.OUTPUT_ROWS, k, n, blocks) for _ in range(2)]
+    x = hiprt.DeviceBuffer.from_array(po.fill_normal(0x5EED3000, m * k).reshape(m, k))
+    y = hiprt.DeviceBuffer(m * n * 4)
+    stream = hiprt.Stream()
+    for i in range(warmup):
+        weights[i % 2].linear_device(x.ptr, m, y.ptr, qa.MODE_MFMA, stream.handle)
+    stream.synchronize()
+    start, end = hiprt.Event(), hiprt.Event()
+    start.record(stream)
+    for i in range(steps):
+        weights[i % 2].linear_device(x.ptr, m, y.ptr, qa.MODE_MFMA, stream.handle)
+    end.record(stream)
+    stream.synchronize()
+    ms = start.elapsed_ms(end) / steps
+    name = ctx.device_name()
+    for w in weights:
+        w.free()
+    for b in (x, y):
+        b.free()
+    stream.destroy()
+    ctx.close()
+    tflops = 2.0 * m * n * k / (ms * 1e-3) / 1e12
+    qname = {1: "q8_0", 2: "q4_0", 3: "q4_k", 4: "q5_k", 5: "q6_k"}[qtype]
+    return {
+        "metric": "prefill GEMM TFLOP/s (% of dense f16 MFMA peak)",
+        "value": round(tflops, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": steps,
+        "warmup": warmup, "ms_per_step": round(ms, 5), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f16 operands, f32 accumulation",
+        "data": "synthetic: N(0,0.02^2) weights quantized by the restated reference quantizer; x ~ N(0,1)",
+        "config": {"workload": f"{qname}_gemm_output_rows_m{m}_k{k}_n{n}", "qtype": qname,
+                   "m": m, "k": k, "n": n, "mode": "mfma", "device": name},
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": MFMA_F16_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4),
+                     "traffic": None},
+    }
+
+
 def cpu_baseline(qtype: int, repeats: int = 3):
     """The oracle's port of CpuScalar::matmul_q4_k_output_rows (single-threaded,
     as the reference's output-row kernels are), pinned to one host core."""
@@ -150,6 +200,10 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="time device-to-device copies of 256 MiB instead (counter calibration)")
+    ap.add_argument("--workload", choices=["gemv", "gemm"], default="gemv",
+                    help="gemv: the headline decode GEMV (default); gemm: the MFMA prefill GEMM")
+    ap.add_argument("--qtype", default="q4_k", help="gemm only: q8_0, q4_0, q4_k, q5_k or q6_k")
+    ap.add_argument("--mkn", default="2048,4096,12288", help="gemm only: M,K,N")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for {args.gpus}); "
@@ -158,6 +212,11 @@ def main():
 
     if args.copy_calibration:
         copy_calibration(args.steps)
+        return
+    if args.workload == "gemm":
+        qt = {"q8_0": 1, "q4_0": 2, "q4_k": 3, "q5_k": 4, "q6_k": 5}[args.qtype]
+        m, k, n = (int(v) for v in args.mkn.split(","))
+        print(json.dumps(gemm_bench(qt, m, k, n, min(args.steps, 50), min(args.warmup, 5))))
         return
 
     qtype = 3  # Q4_K

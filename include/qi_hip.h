@@ -140,7 +140,8 @@ qi_hip_status qi_hip_linear(qi_hip_ctx *ctx, const qi_hip_weights *w, const floa
                             uint64_t m, float *y_host, int32_t mode);
 
 /* Same on device buffers, enqueued on `stream` (a hipStream_t; NULL = the
- * context's stream). Returns after the launch; no host synchronisation. */
+ * context's stream). Returns after the launch; no host synchronisation.
+ * x_dev and y_dev must be 16-byte aligned (QI_HIP_INVALID_INPUT otherwise). */
 qi_hip_status qi_hip_linear_device(qi_hip_ctx *ctx, const qi_hip_weights *w, const float *x_dev,
                                    uint64_t m, float *y_dev, int32_t mode, void *stream);
 

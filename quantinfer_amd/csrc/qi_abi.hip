@@ -38,6 +38,8 @@ struct qi_hip_ctx {
   uint64_t xcap = 0;  // floats
   float* ybuf = nullptr;
   uint64_t ycap = 0;
+  float* hbuf = nullptr;  // f16 activations of the prefill GEMM (capacity in floats)
+  uint64_t hcap = 0;
   int gemv_split = 0;  // QI_HIP_GEMV_SPLIT tuning override (wavefronts per GEMV workgroup: 4 or 8)
 };
 
@@ -99,6 +101,7 @@ void ctx_destroy(qi_hip_ctx* c) {
   if (c->tickets) (void)hipFree(c->tickets);
   if (c->xbuf) (void)hipFree(c->xbuf);
   if (c->ybuf) (void)hipFree(c->ybuf);
+  if (c->hbuf) (void)hipFree(c->hbuf);
   if (c->stream) (void)hipStreamDestroy(c->stream);
   delete c;
 }
@@ -132,7 +135,15 @@ qi_hip_status run_linear(qi_hip_ctx* c, const qi_hip_weights* w, const float* x,
     use_gemm = m >= 128 && qi::gemm_supported(im.qtype, im.layout, im.k, im.n);
   }
   if (use_gemm) {
-    qi::GemmArgs ga{v, x, y, m};
+    const uint64_t m_pad = qi::gemm_padded_rows(m);
+    const uint64_t halves = m_pad * im.k;
+    if (halves > c->hcap * 2) {
+      // the workspace may still be read by queued work of this context
+      QI_HIP_TRY(hipStreamSynchronize(st), "synchronize before growing the GEMM workspace");
+      qi_hip_status s = grow(&c->hbuf, &c->hcap, (halves + 1) / 2, "alloc GEMM workspace");
+      if (s != QI_HIP_OK) return s;
+    }
+    qi::GemmArgs ga{v, x, y, m, reinterpret_cast<_Float16*>(c->hbuf), m_pad};
     QI_HIP_TRY(qi::launch_gemm(im, ga, st), "launch gemm");
     return QI_HIP_OK;
   }
@@ -332,6 +343,9 @@ qi_hip_status qi_hip_linear_device(qi_hip_ctx* c, const qi_hip_weights* w, const
   qi_hip_status s = check_call(c, w, m);
   if (s != QI_HIP_OK) return s;
   if (x_dev == nullptr || y_dev == nullptr) return fail(QI_HIP_INVALID_INPUT, "null activation buffer");
+  // the kernels read activation rows with 16-byte loads
+  if ((reinterpret_cast<uintptr_t>(x_dev) | reinterpret_cast<uintptr_t>(y_dev)) & 15u)
+    return fail(QI_HIP_INVALID_INPUT, "device activation and output buffers must be 16-byte aligned");
   std::lock_guard<std::mutex> lock(c->mu);
   QI_HIP_TRY(hipSetDevice(c->device), "set device");
   hipStream_t st = stream ? static_cast<hipStream_t>(stream) : c->stream;

@@ -1,11 +1,279 @@
-// Prefill GEMM (M >= 128) on MFMA. Not yet enabled: every call falls back to
-// the f32 GEMV path until the kernel lands.
+// Prefill GEMM on the f16 matrix cores (v_mfma_f32_16x16x32_f16), output-rows
+// layout, K a multiple of 256, any M (meant for M >= 128).
+//
+// Arithmetic. The activations are rounded once to f16 (x_to_f16_kernel, rows
+// padded to the 128-row tile with zeros). Each weight is rounded once to f16:
+// Q8_0 / Q4_0 as (code - bias) * d, an exact f16 integer times the stored f16
+// scale; the K-quants from the reference's own f32 value (d * sc) * q -
+// dmin * m (Q6_K (d * sc) * (q - 32)), so no rounding is shared by the 32
+// weights of a sub-block (rounding d * sc or dmin * m to f16 would be, and
+// cancels badly in blocks whose range an outlier stretched). Products
+// accumulate in f32 on the matrix cores. This is the tolerance-judged MFMA
+// mode (f16 operands, f32 accumulation).
+//
+// Tiling. A workgroup of WN wavefronts owns 128 activation rows x 64 WN
+// outputs; each wavefront owns all 128 rows and its own 64 outputs, i.e. 8 x 4
+// MFMA tiles of 16 x 16 (128 f32 accumulators per lane), so a weight fragment
+// feeds 8 MFMAs. K runs in units of 256, each as four stages of 2 MFMA steps.
+// Step t of a unit covers, for lane group g, elements window_first(g, t / 4) +
+// 8 (t % 4) + [0, 8) on both operands, the element order the weight records
+// store, so neither operand is reshuffled:
+//   A (activations) is staged per stage through LDS, double buffered, laid out
+//     [step][row tile][lane] x 16 bytes so that a fragment read is 1 KB
+//     contiguous, shared by the workgroup's wavefronts;
+//   B (weights) never touches LDS: each wavefront streams its 4 output tiles'
+//     records of the next unit into registers (the GEMV's coalesced loads)
+//     while it computes the current one, and dequantizes the 8 codes of a
+//     step into an f16 fragment right before the 8 MFMAs that use it.
+#include "qi_device.h"
 #include "qi_internal.h"
+#include "qi_unit.h"
 
 namespace qi {
 
-bool gemm_supported(int32_t, int32_t, uint64_t, uint64_t) { return false; }
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef float f4 __attribute__((ext_vector_type(4)));
 
-hipError_t launch_gemm(const Image&, const GemmArgs&, hipStream_t) { return hipErrorNotSupported; }
+constexpr int kTileM = 128;
+
+__global__ __launch_bounds__(256) void x_to_f16_kernel(const float* __restrict__ x, uint64_t m,
+                                                       uint64_t k, uint64_t m_pad,
+                                                       _Float16* __restrict__ xh) {
+  const uint64_t i = (static_cast<uint64_t>(blockIdx.x) * 256 + threadIdx.x) * 8;
+  if (i >= m_pad * k) return;
+  h8 o;
+  if (i / k < m) {
+    const float4* p = reinterpret_cast<const float4*>(x + i);
+    const float4 a = p[0], b = p[1];
+    o = h8{static_cast<_Float16>(a.x), static_cast<_Float16>(a.y), static_cast<_Float16>(a.z),
+           static_cast<_Float16>(a.w), static_cast<_Float16>(b.x), static_cast<_Float16>(b.y),
+           static_cast<_Float16>(b.z), static_cast<_Float16>(b.w)};
+  } else {
+    o = h8{0, 0, 0, 0, 0, 0, 0, 0};
+  }
+  *reinterpret_cast<h8*>(xh + i) = o;
+}
+
+// 8 codes (bytes of a long) -> 8 exact f16 integers q - bias (Q8_0, Q4_0).
+template <int QT>
+__device__ __forceinline__ void codes_to_f16(long codes, h2 out[4]) {
+  uint32_t w[2] = {static_cast<uint32_t>(codes), static_cast<uint32_t>(static_cast<uint64_t>(codes) >> 32)};
+  // Q8_0 codes are signed: flip the sign bit so the byte is code + 128
+  if constexpr (QT == kQ8_0) {
+    w[0] ^= 0x80808080u;
+    w[1] ^= 0x80808080u;
+  }
+  constexpr float bias = QT == kQ8_0 ? 1152.0f : 1032.0f;
+  const h2 sub = {static_cast<_Float16>(bias), static_cast<_Float16>(bias)};
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    out[2 * i] = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, w[i], 0x04010400u)) - sub;
+    out[2 * i + 1] = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, w[i], 0x04030402u)) - sub;
+  }
+}
+
+// f16 weight fragment of 8 codes. Q8_0 / Q4_0: w = (q - bias) * d with d the
+// stored f16 scale, one rounding. K-quants: the reference's f32 value
+// (d * sc) * q - dmin * m (Q6_K: (d * sc) * (q - 32)), then one rounding to
+// f16, so no rounding error is shared by the weights of a sub-block.
+template <int QT>
+__device__ __forceinline__ h8 weight_fragment(long codes, float a, float b) {
+  if constexpr (QT == kQ8_0 || QT == kQ4_0) {
+    h2 q[4];
+    codes_to_f16<QT>(codes, q);
+    const _Float16 ha = static_cast<_Float16>(a);
+    const h2 a2 = {ha, ha};
+    h2 w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) w[i] = q[i] * a2;
+    return h8{w[0][0], w[0][1], w[1][0], w[1][1], w[2][0], w[2][1], w[3][0], w[3][1]};
+  } else {
+    const uint64_t c = static_cast<uint64_t>(codes);
+    h8 out;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float q = static_cast<float>(static_cast<uint32_t>(c >> (8 * j)) & 0xFFu);
+      float w;
+      if constexpr (QT == kQ6_K) w = a * (q - 32.0f);
+      else w = a * q - b;
+      out[j] = static_cast<_Float16>(w);
+    }
+    return out;
+  }
+}
+
+// Workgroup: WN wavefronts side by side, each owning 128 activation rows x 64
+// outputs (8 x 4 MFMA tiles); the workgroup covers 128 rows x 64 WN outputs.
+// Activations are staged two MFMA steps at a time.
+template <int QT, bool WIDE, int WN>
+__global__ __launch_bounds__(64 * WN) void gemm_kernel(GemmArgs a) {
+  using U = Unit<QT>;
+  constexpr int kThreads = 64 * WN;
+  constexpr Record R = record_geometry(QT, WIDE);
+  constexpr uint32_t kStage = 2 * 8 * 64 * 16;  // [step][row tile][lane] x 16 B
+  constexpr int kChunks = 1024 / kThreads;      // 16-byte chunks per thread per stage
+  __shared__ __attribute__((aligned(16))) uint8_t lds[2 * kStage];
+
+  const uint32_t tid = threadIdx.x, lane = tid & 63, wn = tid >> 6;
+  const uint32_t g = lane >> 4, c16 = lane & 15;
+  const uint32_t units = a.w.units;
+  const uint32_t K = static_cast<uint32_t>(a.w.k);
+  const uint64_t m0 = static_cast<uint64_t>(blockIdx.y) * kTileM;
+
+  // this wavefront's 4 output tiles (clamped: past-the-end tiles re-read the
+  // last tile and store nothing)
+  const uint8_t* trec[4];
+  uint32_t tile_raw[4];
+#pragma unroll
+  for (int ct = 0; ct < 4; ++ct) {
+    tile_raw[ct] = (blockIdx.x * WN + wn) * 4 + ct;
+    const uint32_t t = min(tile_raw[ct], a.w.tiles - 1);
+    trec[ct] = a.w.qs + static_cast<uint64_t>(t) * units * R.bytes;
+  }
+
+  // stage q (0..3) of unit u holds steps 2q, 2q+1: for each (row, lane group)
+  // the 16 elements window_first(g, q / 2) + 16 (q % 2) + [0, 16), two chunks
+  auto stage_load = [&](uint32_t u, uint32_t q, uint4 regs[kChunks]) {
+#pragma unroll
+    for (int i = 0; i < kChunks; ++i) {
+      const uint32_t cid = tid + kThreads * i;
+      const uint32_t row = cid >> 3, gg = (cid >> 1) & 3, tt = cid & 1;
+      const uint32_t e = 256 * u + window_first<QT>(gg, q >> 1) + 16 * (q & 1) + 8 * tt;
+      regs[i] = *reinterpret_cast<const uint4*>(a.xh + (m0 + row) * K + e);
+    }
+  };
+  auto stage_store = [&](uint32_t buf, const uint4 regs[kChunks]) {
+#pragma unroll
+    for (int i = 0; i < kChunks; ++i) {
+      const uint32_t cid = tid + kThreads * i;
+      const uint32_t row = cid >> 3, gg = (cid >> 1) & 3, tt = cid & 1;
+      const uint32_t off = ((tt * 8 + (row >> 4)) * 64 + gg * 16 + (row & 15)) * 16;
+      *reinterpret_cast<uint4*>(lds + buf * kStage + off) = regs[i];
+    }
+  };
+
+  f4 acc[8][4];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f4{0, 0, 0, 0};
+
+  typename U::Raw cur[4], nxt[4];
+#pragma unroll
+  for (int ct = 0; ct < 4; ++ct) U::template load<WIDE>(trec[ct], lane, cur[ct]);
+  uint4 areg[kChunks];
+  stage_load(0, 0, areg);
+  stage_store(0, areg);
+  __syncthreads();
+
+  uint32_t buf = 0;
+  for (uint32_t u = 0; u < units; ++u) {
+    float sa[4][U::kWindows], sb[4][U::kWindows];
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct) U::template scales<WIDE>(g, cur[ct], sa[ct], sb[ct]);
+    if (u + 1 < units) {
+#pragma unroll
+      for (int ct = 0; ct < 4; ++ct)
+        U::template load<WIDE>(trec[ct] + static_cast<uint64_t>(u + 1) * R.bytes, lane, nxt[ct]);
+    }
+#pragma unroll
+    for (uint32_t q = 0; q < 4; ++q) {
+      // next stage's activations into registers while this one computes
+      const bool more = q < 3 || u + 1 < units;
+      if (more) stage_load(q < 3 ? u : u + 1, (q + 1) & 3, areg);
+      const uint8_t* sbase = lds + buf * kStage;
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt) {
+        const int t = 2 * q + tt;
+        h8 af[8];
+#pragma unroll
+        for (int rt = 0; rt < 8; ++rt)
+          af[rt] = *reinterpret_cast<const h8*>(sbase + ((tt * 8 + rt) * 64 + lane) * 16);
+#pragma unroll
+        for (int ct = 0; ct < 4; ++ct) {
+          const int w = t / U::kSteps;
+          const h8 bf = weight_fragment<QT>(U::codes(cur[ct], g, t), sa[ct][w], sb[ct][w]);
+#pragma unroll
+          for (int rt = 0; rt < 8; ++rt)
+            acc[rt][ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[rt], bf, acc[rt][ct], 0, 0, 0);
+        }
+      }
+      if (more) stage_store(buf ^ 1, areg);
+      __syncthreads();
+      buf ^= 1;
+    }
+    if (u + 1 < units) {
+#pragma unroll
+      for (int ct = 0; ct < 4; ++ct) cur[ct] = nxt[ct];
+    }
+  }
+
+  // C[i][j]: lane j + 16 (i / 4), element i % 4
+#pragma unroll
+  for (int rt = 0; rt < 8; ++rt) {
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct) {
+      const uint64_t n = static_cast<uint64_t>(tile_raw[ct]) * 16 + c16;
+      if (n >= a.w.n) continue;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const uint64_t m = m0 + rt * 16 + 4 * g + r;
+        if (m < a.m) a.y[m * a.w.n + n] = acc[rt][ct][r];
+      }
+    }
+  }
+}
+
+namespace {
+
+template <int QT, bool WIDE, int WN>
+hipError_t launch_wn(const Image& im, const GemmArgs& a, hipStream_t st) {
+  const uint32_t nblk = static_cast<uint32_t>((im.tiles + 4 * WN - 1) / (4 * WN));
+  const uint32_t mblk = static_cast<uint32_t>(a.m_pad / kTileM);
+  hipLaunchKernelGGL((gemm_kernel<QT, WIDE, WN>), dim3(nblk, mblk), dim3(64 * WN), 0, st, a);
+  return hipGetLastError();
+}
+
+template <int QT>
+hipError_t launch_q(const Image& im, const GemmArgs& a, hipStream_t st) {
+  // 4 wavefronts (256 outputs) per workgroup when that still gives every CU a
+  // workgroup, 2 otherwise
+  const uint64_t wgs4 = ((im.tiles + 15) / 16) * (a.m_pad / kTileM);
+  const bool wide4 = wgs4 >= 256 || QT == kQ5_K;  // Q5_K spills at 2 wavefronts
+  if constexpr (QT == kQ5_K) {
+    (void)wide4;
+    return im.wide ? launch_wn<QT, true, 4>(im, a, st) : launch_wn<QT, false, 4>(im, a, st);
+  } else {
+    if (im.wide) return wide4 ? launch_wn<QT, true, 4>(im, a, st) : launch_wn<QT, true, 2>(im, a, st);
+    return wide4 ? launch_wn<QT, false, 4>(im, a, st) : launch_wn<QT, false, 2>(im, a, st);
+  }
+}
+
+}  // namespace
+
+bool gemm_supported(int32_t qtype, int32_t layout, uint64_t k, uint64_t n) {
+  (void)n;
+  return layout == kOutputRows && qtype >= kQ8_0 && qtype <= kQ6_K && k % 256 == 0 && k > 0;
+}
+
+uint64_t gemm_padded_rows(uint64_t m) { return (m + kTileM - 1) / kTileM * kTileM; }
+
+hipError_t launch_gemm(const Image& im, const GemmArgs& a, hipStream_t st) {
+  if (!im.tiled || a.xh == nullptr || a.m_pad != gemm_padded_rows(a.m)) return hipErrorInvalidValue;
+  const uint64_t elems = a.m_pad * im.k;
+  const uint32_t blocks = static_cast<uint32_t>((elems / 8 + 255) / 256);
+  hipLaunchKernelGGL(x_to_f16_kernel, dim3(blocks), dim3(256), 0, st, a.x, a.m, im.k, a.m_pad, a.xh);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  switch (im.qtype) {
+    case kQ8_0: return launch_q<kQ8_0>(im, a, st);
+    case kQ4_0: return launch_q<kQ4_0>(im, a, st);
+    case kQ4_K: return launch_q<kQ4_K>(im, a, st);
+    case kQ5_K: return launch_q<kQ5_K>(im, a, st);
+    case kQ6_K: return launch_q<kQ6_K>(im, a, st);
+    default: return hipErrorInvalidValue;
+  }
+}
 
 }  // namespace qi

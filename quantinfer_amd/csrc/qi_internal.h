@@ -51,8 +51,11 @@ struct GemmArgs {
   const float* x;  // [m, k] f32 device
   float* y;        // [m, n]
   uint64_t m;
+  _Float16* xh;    // [m_pad, k] f16 workspace (the activations rounded once)
+  uint64_t m_pad;  // gemm_padded_rows(m)
 };
 bool gemm_supported(int32_t qtype, int32_t layout, uint64_t k, uint64_t n);
+uint64_t gemm_padded_rows(uint64_t m);
 hipError_t launch_gemm(const Image& im, const GemmArgs& a, hipStream_t st);
 
 }  // namespace qi

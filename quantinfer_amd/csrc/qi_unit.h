@@ -1,0 +1,247 @@
+// Per-format access to one unit (256 elements) of one output row of a tiled
+// weight record, shared by the matrix-core GEMV and GEMM: a wavefront's lane
+// 16g + c loads row c's lane-group-g bytes of the record (layout in
+// qi_image.h), decodes the affine scales of its windows and hands out, per
+// step t (0..7), the 8 codes of elements window_first(g, t / 4) + 8 (t % 4) +
+// [0, 8) as bytes (Q8_0 signed, the other formats unsigned).
+#pragma once
+#include "qi_device.h"
+
+namespace qi {
+
+template <int QT>
+struct Unit;  // per-format code/scale access for one (output n, lane group g, unit u)
+
+// Loads read one (tile, unit) record (layout in qi_image.h): lane 16g + c
+// takes row c's lane-group-g code chunks at q*1024 + lane*16 (each wavefront
+// load is 1 KB contiguous), its scales from the record's scale sections.
+
+template <>
+struct Unit<kQ8_0> {
+  static constexpr int kWindows = 2, kSteps = 4;  // two 32-element blocks per lane
+  static constexpr bool kMin = false;
+  struct Raw {
+    uint4 q[4];
+    uint32_t s0, s1;  // f16 pair in s0, or two f32 scales
+  };
+  template <bool W>
+  __device__ static void load(const uint8_t* rec, uint32_t lane, Raw& r) {
+    constexpr Record R = record_geometry(kQ8_0, W);
+    const uint4* p = reinterpret_cast<const uint4*>(rec + R.qs) + lane;
+    r.q[0] = p[0]; r.q[1] = p[64]; r.q[2] = p[128]; r.q[3] = p[192];
+    const uint32_t e = (lane & 15) * 8 + 2 * (lane >> 4);  // blocks 2g, 2g+1 of row c
+    if constexpr (W) {
+      const uint2 d = *reinterpret_cast<const uint2*>(rec + R.d + e * 4);
+      r.s0 = d.x; r.s1 = d.y;
+    } else {
+      r.s0 = *reinterpret_cast<const uint32_t*>(rec + R.d + e * 2);
+      r.s1 = 0;
+    }
+  }
+  template <bool W>
+  __device__ static void scales(uint32_t, const Raw& r, float a[2], float b[2]) {
+    if constexpr (W) {
+      a[0] = __builtin_bit_cast(float, r.s0);
+      a[1] = __builtin_bit_cast(float, r.s1);
+    } else {
+      a[0] = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(r.s0 & 0xFFFFu)));
+      a[1] = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(r.s0 >> 16)));
+    }
+    b[0] = b[1] = 0.0f;
+  }
+  // step t (0..7): block h = t/4, bytes 8*(t%4) .. +8 of that block
+  __device__ static long codes(const Raw& r, uint32_t, int t) {
+    const uint4 q = r.q[(t >> 2) * 2 + ((t & 3) >> 1)];
+    const uint32_t lo = (t & 1) ? q.z : q.x, hi = (t & 1) ? q.w : q.y;
+    return static_cast<long>((static_cast<uint64_t>(hi) << 32) | lo);
+  }
+};
+
+template <>
+struct Unit<kQ4_0> {
+  static constexpr int kWindows = 2, kSteps = 4;
+  static constexpr bool kMin = true;  // w = d*q - 8d
+  struct Raw {
+    uint4 q[2];
+    uint32_t s0, s1;
+  };
+  template <bool W>
+  __device__ static void load(const uint8_t* rec, uint32_t lane, Raw& r) {
+    constexpr Record R = record_geometry(kQ4_0, W);
+    const uint4* p = reinterpret_cast<const uint4*>(rec + R.qs) + lane;
+    r.q[0] = p[0]; r.q[1] = p[64];
+    const uint32_t e = (lane & 15) * 8 + 2 * (lane >> 4);
+    if constexpr (W) {
+      const uint2 d = *reinterpret_cast<const uint2*>(rec + R.d + e * 4);
+      r.s0 = d.x; r.s1 = d.y;
+    } else {
+      r.s0 = *reinterpret_cast<const uint32_t*>(rec + R.d + e * 2);
+      r.s1 = 0;
+    }
+  }
+  template <bool W>
+  __device__ static void scales(uint32_t, const Raw& r, float a[2], float b[2]) {
+    if constexpr (W) {
+      a[0] = __builtin_bit_cast(float, r.s0);
+      a[1] = __builtin_bit_cast(float, r.s1);
+    } else {
+      a[0] = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(r.s0 & 0xFFFFu)));
+      a[1] = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(r.s0 >> 16)));
+    }
+    b[0] = 8.0f * a[0];
+    b[1] = 8.0f * a[1];
+  }
+  // block h = t/4 (16 bytes: byte i = element i | element i+16 << 4);
+  // quarter t%4: 0 = low nibbles of bytes 0-7, 1 = low of 8-15, 2 = high of 0-7, 3 = high of 8-15
+  __device__ static long codes(const Raw& r, uint32_t, int t) {
+    const uint4 q = r.q[t >> 2];
+    const int qq = t & 3;
+    const uint32_t lo = (qq & 1) ? q.z : q.x, hi = (qq & 1) ? q.w : q.y;
+    const int sh = qq >= 2 ? 4 : 0;
+    const uint32_t l2 = (lo >> sh) & 0x0F0F0F0Fu, h2 = (hi >> sh) & 0x0F0F0F0Fu;
+    return static_cast<long>((static_cast<uint64_t>(h2) << 32) | l2);
+  }
+};
+
+// Q4_K / Q5_K: lane group g holds code bytes [32g, 32g+32) of the super-block:
+// step t < 4 takes the low nibbles of bytes 8t..8t+7 (sub-block 2g), t >= 4 the
+// high nibbles of bytes 8(t-4).. (sub-block 2g+1); Q5_K adds bit 2g (low) or
+// 2g+1 (high) of qh[byte] as bit 4.
+template <bool FIVE>
+struct UnitQ45K {
+  static constexpr int kQT = FIVE ? kQ5_K : kQ4_K;
+  static constexpr int kWindows = 2, kSteps = 4;
+  static constexpr bool kMin = true;
+  struct Raw {
+    uint4 q[2];
+    uint4 h[2];
+    uint32_t sc[3];
+    uint32_t s0, s1;  // d and dmin: f16 bits (zero-extended) or f32 bits
+  };
+  template <bool W>
+  __device__ static void load(const uint8_t* rec, uint32_t lane, Raw& r) {
+    constexpr Record R = record_geometry(kQT, W);
+    const uint32_t col = lane & 15;
+    const uint4* p = reinterpret_cast<const uint4*>(rec + R.qs) + lane;
+    r.q[0] = p[0]; r.q[1] = p[64];
+    if constexpr (FIVE) {
+      const uint4* h = reinterpret_cast<const uint4*>(rec + R.qh) + col;
+      r.h[0] = h[0]; r.h[1] = h[16];
+    }
+    const uint32_t* s = reinterpret_cast<const uint32_t*>(rec + R.sc + col * 12);
+    r.sc[0] = s[0]; r.sc[1] = s[1]; r.sc[2] = s[2];
+    if constexpr (W) {
+      r.s0 = reinterpret_cast<const uint32_t*>(rec + R.d)[col];
+      r.s1 = reinterpret_cast<const uint32_t*>(rec + R.dmin)[col];
+    } else {
+      // kept apart until scales(): combining them here would wait for the loads
+      r.s0 = reinterpret_cast<const uint16_t*>(rec + R.d)[col];
+      r.s1 = reinterpret_cast<const uint16_t*>(rec + R.dmin)[col];
+    }
+  }
+  template <bool W>
+  __device__ static void scales(uint32_t g, const Raw& r, float a[2], float b[2]) {
+    float d, dmin;
+    if constexpr (W) {
+      d = __builtin_bit_cast(float, r.s0);
+      dmin = __builtin_bit_cast(float, r.s1);
+    } else {
+      d = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(r.s0)));
+      dmin = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(r.s1)));
+    }
+    // lane group g's 24-bit field sits at bytes 3g..3g+2 of the 12 scale
+    // bytes: one byte permute from the word pair that holds it
+    const uint32_t lo = g < 2 ? r.sc[0] : r.sc[1];
+    const uint32_t hi = g < 2 ? r.sc[1] : r.sc[2];
+    const uint32_t first = g == 0 ? 0 : g == 1 ? 3 : g == 2 ? 2 : 5;
+    const uint32_t f = __builtin_amdgcn_perm(hi, lo, first * 0x00010101u + 0x0C020100u);
+    a[0] = d * static_cast<float>(f & 63u);
+    b[0] = dmin * static_cast<float>((f >> 6) & 63u);
+    a[1] = d * static_cast<float>((f >> 12) & 63u);
+    b[1] = dmin * static_cast<float>(f >> 18);
+  }
+  __device__ static long codes(const Raw& r, uint32_t g, int t) {
+    const int tt = t & 3;
+    const uint4 q = r.q[tt >> 1];
+    const uint32_t lo = (tt & 1) ? q.z : q.x, hi = (tt & 1) ? q.w : q.y;
+    const int sh = t >= 4 ? 4 : 0;
+    uint32_t l2 = (lo >> sh) & 0x0F0F0F0Fu, h2 = (hi >> sh) & 0x0F0F0F0Fu;
+    if constexpr (FIVE) {
+      const uint4 h = r.h[tt >> 1];
+      const uint32_t hl = (tt & 1) ? h.z : h.x, hh = (tt & 1) ? h.w : h.y;
+      const int bit = static_cast<int>(2 * g) + (t >= 4 ? 1 : 0);
+      l2 |= ((hl >> bit) & 0x01010101u) << 4;
+      h2 |= ((hh >> bit) & 0x01010101u) << 4;
+    }
+    return static_cast<long>((static_cast<uint64_t>(h2) << 32) | l2);
+  }
+};
+
+template <>
+struct Unit<kQ4_K> : UnitQ45K<false> {};
+template <>
+struct Unit<kQ5_K> : UnitQ45K<true> {};
+
+// Q6_K: lane group g = 2*ip + c holds ql bytes [64ip + 32c, +32) and qh bytes
+// [32ip, +32). Step t < 4: low nibbles of ql bytes 8t.. with qh bits 2c (elements
+// 128ip + 32c + 8t + j); t >= 4: high nibbles of ql bytes 8(t-4).. with qh bits
+// 2c+4 (elements 128ip + 32c + 64 + 8(t-4) + j). Windows are pairs of steps
+// (16-element sub-blocks 8ip + 2c + {0, 1, 4, 5}); w = a*q - 32a.
+template <>
+struct Unit<kQ6_K> {
+  static constexpr int kWindows = 4, kSteps = 2;
+  static constexpr bool kMin = true;
+  struct Raw {
+    uint4 q[2];
+    uint4 h[2];
+    uint32_t sc;  // this lane group's four int8 sub-scales
+    uint32_t d;   // f16 in the low half, or f32
+  };
+  template <bool W>
+  __device__ static void load(const uint8_t* rec, uint32_t lane, Raw& r) {
+    constexpr Record R = record_geometry(kQ6_K, W);
+    const uint32_t col = lane & 15, ip = lane >> 5;
+    const uint4* p = reinterpret_cast<const uint4*>(rec + R.qs) + lane;
+    r.q[0] = p[0]; r.q[1] = p[64];
+    const uint4* h = reinterpret_cast<const uint4*>(rec + R.qh) + 32 * ip + col;
+    r.h[0] = h[0]; r.h[1] = h[16];
+    r.sc = *reinterpret_cast<const uint32_t*>(rec + R.sc + col * 16 + 4 * (lane >> 4));
+    if constexpr (W) r.d = reinterpret_cast<const uint32_t*>(rec + R.d)[col];
+    else r.d = reinterpret_cast<const uint16_t*>(rec + R.d)[col];
+  }
+  template <bool W>
+  __device__ static void scales(uint32_t, const Raw& r, float a[4], float b[4]) {
+    float d;
+    if constexpr (W) d = __builtin_bit_cast(float, r.d);
+    else d = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(r.d)));
+    // sub-scales 8ip + 2c + {0, 1, 4, 5} of lane group g = 2ip + c
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      a[i] = d * static_cast<float>(static_cast<int32_t>(r.sc << (24 - 8 * i)) >> 24);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) b[i] = 32.0f * a[i];
+  }
+  __device__ static long codes(const Raw& r, uint32_t g, int t) {
+    const int tt = t & 3;
+    const uint4 q = r.q[tt >> 1];
+    const uint4 h = r.h[tt >> 1];
+    const uint32_t lo = (tt & 1) ? q.z : q.x, hi = (tt & 1) ? q.w : q.y;
+    const uint32_t hl = (tt & 1) ? h.z : h.x, hh = (tt & 1) ? h.w : h.y;
+    const int sh = t >= 4 ? 4 : 0;
+    const int hs = 2 * static_cast<int>(g & 1) + (t >= 4 ? 4 : 0);
+    const uint32_t l2 = ((lo >> sh) & 0x0F0F0F0Fu) | (((hl >> hs) & 0x03030303u) << 4);
+    const uint32_t h2 = ((hi >> sh) & 0x0F0F0F0Fu) | (((hh >> hs) & 0x03030303u) << 4);
+    return static_cast<long>((static_cast<uint64_t>(h2) << 32) | l2);
+  }
+};
+
+// First unit element of window (g, h): Q6_K lane group g = 2*ip + c holds
+// elements 128ip + 32c + [0, 32) (h = 0) and + 64 (h = 1); the other formats'
+// lane group g holds elements 64g + [0, 64).
+template <int QT>
+__device__ __forceinline__ uint32_t window_first(uint32_t g, uint32_t h) {
+  if constexpr (QT == kQ6_K) return 128 * (g >> 1) + 32 * (g & 1) + 64 * h;
+  return 64 * g + 32 * h;
+}
+
+}  // namespace qi

@@ -32,7 +32,7 @@ def lhs_from_case(case):
 KAPPA_CAP = 64.0
 
 
-def guarded_rel_err(actual, exact, x, w_deq):
+def guarded_rel_err(actual, exact, x, w_deq, kappa=KAPPA_CAP):
     """max_i |a_i - e_i| / max(|e_i|, sum_k |x_k w_ik| / 64).
 
     `exact` is the f64 product of x and the dequantized weights. Relative error
@@ -41,7 +41,7 @@ def guarded_rel_err(actual, exact, x, w_deq):
     summation order (the CPU reference's included) is accurate to 1e-5
     relative on an output that cancels further."""
     absdot = np.abs(x.astype(np.float64)) @ np.abs(w_deq.astype(np.float64)).T
-    denom = np.maximum(np.abs(exact), absdot / KAPPA_CAP)
+    denom = np.maximum(np.abs(exact), absdot / kappa)
     denom = np.where(denom == 0, 1.0, denom)
     return float(np.max(np.abs(actual.astype(np.float64) - exact) / denom))
 

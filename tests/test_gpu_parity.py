@@ -282,3 +282,85 @@ def test_gpu_error_paths(ctx):
         assert lib.qi_hip_linear(other.handle, w.handle, x.ctypes.data, 1, y.ctypes.data, 0) == \
             qa.INVALID_INPUT
     assert ctx.device_name()
+
+
+# ------------------------------------------------ MFMA prefill GEMM (f16 operands)
+
+# Bars of the MFMA mode (f16 activations and weights, f32 accumulation):
+#   normwise  max_i |y_i - e_i| / max_i |e_i| <= 2e-3, against the f64 product
+#             e and against the CPU reference (CpuScalar, on sampled rows);
+#   componentwise max_i |y_i - e_i| / max(|e_i|, sum_k |x_k w_ik| / 16) <= 2e-3:
+#             relative error wherever the dot product's condition number is
+#             <= 16. f16 operands carry a unit roundoff of 4.9e-4, so an output
+#             that cancels 64-fold (the F32 mode's cap) is beyond 2e-3 for any
+#             f16 arithmetic.
+MFMA_TOL = 2e-3
+MFMA_KAPPA = 16.0
+
+
+def _mfma_checks(y, x, blocks, qtype, n, cpu_rows=None):
+    """(componentwise vs f64, normwise vs f64, normwise vs CpuScalar on rows)"""
+    k = x.shape[1]
+    w = po.dequantize(qtype, blocks).reshape(n, k).astype(np.float64)
+    exact = x.astype(np.float64) @ w.T
+    comp = guarded_rel_err(y, exact, x, w, kappa=MFMA_KAPPA)
+    norm = normwise_rel_err(y, exact)
+    rows = np.arange(x.shape[0]) if cpu_rows is None else cpu_rows
+    cpu = po.matmul_output_rows(qtype, np.ascontiguousarray(x[rows]), blocks, n, threads=8)
+    return comp, norm, normwise_rel_err(y[rows], cpu)
+
+
+@pytest.mark.parametrize("qtype", ALL_Q, ids=lambda q: NAMES[q])
+@pytest.mark.parametrize("m", [1, 5, 128, 200])
+def test_mfma_gemm_tolerance_small(ctx, qtype, m):
+    # N = 300 leaves a partial 128-output block and a partial 16-output tile
+    k, n = 1024, 300
+    blocks = po.make_weights(qtype, k, n, seed=6000 + qtype, outliers=True)
+    x = po.fill_normal(6100 + m, m * k).reshape(m, k)
+    w = ctx.weights(qtype, qa.OUTPUT_ROWS, k, n, blocks)
+    y = w.linear(x, qa.MODE_MFMA)
+    comp, norm, cpu = _mfma_checks(y, x, blocks, qtype, n)
+    assert comp <= MFMA_TOL and norm <= MFMA_TOL and cpu <= MFMA_TOL, (comp, norm, cpu)
+    if m >= 128:  # AUTO picks the GEMM from 128 rows on
+        assert w.linear(x, qa.MODE_AUTO).tobytes() == y.tobytes()
+
+
+def test_mfma_gemm_wide_scales(ctx):
+    for qtype in ALL_Q:
+        blocks = _wide_blocks(qtype, 2 * 1024 // po.BLOCK_ELEMS[qtype] * 16, 70 + qtype)
+        if qtype in (qa.Q4_K, qa.Q5_K):
+            blocks["min_scale"] = np.abs(blocks["min_scale"])
+        k, n = 2048 // 2, 32
+        blocks = blocks[: n * k // po.BLOCK_ELEMS[qtype]]
+        x = po.fill_normal(71, 130 * k).reshape(130, k)
+        w = ctx.weights(qtype, qa.OUTPUT_ROWS, k, n, blocks)
+        assert w.info().f16_scales == 0
+        y = w.linear(x, qa.MODE_MFMA)
+        wd = po.dequantize(qtype, blocks).reshape(n, k).astype(np.float64)
+        exact = x.astype(np.float64) @ wd.T
+        assert normwise_rel_err(y, exact) <= MFMA_TOL, NAMES[qtype]
+
+
+GEMM_CONFIGS = [
+    # BASELINE.json configs[3]: Q8_0 and Q4_K, K=4096 N in {4096, 12288}, K=12288 N=4096
+    (qa.Q8_0, 4096, 4096, [128, 512]),
+    (qa.Q4_K, 4096, 4096, [128, 512]),
+    (qa.Q8_0, 4096, 12288, [2048]),
+    (qa.Q4_K, 4096, 12288, [2048]),
+    (qa.Q4_K, 12288, 4096, [2048]),
+]
+
+
+@pytest.mark.parametrize("cfg", GEMM_CONFIGS, ids=lambda c: f"{NAMES[c[0]]}-K{c[1]}-N{c[2]}")
+def test_config_shapes_mfma_tolerance(ctx, cfg):
+    qtype, k, n, ms = cfg
+    blocks = po.make_weights(qtype, k, n, seed=0x5EED0010 + qtype, outliers=qtype != qa.Q8_0)
+    w = ctx.weights(qtype, qa.OUTPUT_ROWS, k, n, blocks)
+    rng = np.random.default_rng(3)
+    for m in ms:
+        x = po.fill_normal(0x5EED3000 + m, m * k).reshape(m, k)
+        y = w.linear(x, qa.MODE_MFMA)
+        rows = np.sort(rng.choice(m, size=min(m, 32), replace=False))
+        comp, norm, cpu = _mfma_checks(y, x, blocks, qtype, n, cpu_rows=rows)
+        print(f"mfma {NAMES[qtype]} M={m} K={k} N={n}: comp {comp:.2e} norm {norm:.2e} cpu {cpu:.2e}")
+        assert comp <= MFMA_TOL and norm <= MFMA_TOL and cpu <= MFMA_TOL, (m, comp, norm, cpu)
