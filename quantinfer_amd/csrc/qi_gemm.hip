@@ -14,7 +14,7 @@
 // Tiling. A workgroup of WN wavefronts owns 128 activation rows x 64 WN
 // outputs; each wavefront owns all 128 rows and its own 64 outputs, i.e. 8 x 4
 // MFMA tiles of 16 x 16 (128 f32 accumulators per lane), so a weight fragment
-// feeds 8 MFMAs. K runs in units of 256, each as four stages of 2 MFMA steps.
+// feeds 8 MFMAs. K runs in units of 256, each as two stages of 4 MFMA steps.
 // Step t of a unit covers, for lane group g, elements window_first(g, t / 4) +
 // 8 (t % 4) + [0, 8) on both operands, the element order the weight records
 // store, so neither operand is reshuffled:
@@ -29,11 +29,14 @@
 #include "qi_internal.h"
 #include "qi_unit.h"
 
+#include <type_traits>
+
 namespace qi {
 
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef float f4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kTileM = 128;
 
@@ -89,15 +92,14 @@ __device__ __forceinline__ h8 weight_fragment(long codes, float a, float b) {
     for (int i = 0; i < 4; ++i) w[i] = q[i] * a2;
     return h8{w[0][0], w[0][1], w[1][0], w[1][1], w[2][0], w[2][1], w[3][0], w[3][1]};
   } else {
-    const uint64_t c = static_cast<uint64_t>(codes);
+    const uint32_t w[2] = {static_cast<uint32_t>(codes),
+                           static_cast<uint32_t>(static_cast<uint64_t>(codes) >> 32)};
+    const float nb = QT == kQ6_K ? -32.0f * a : -b;  // Q6_K: (d * sc) * (q - 32) = a * q - 32 a
     h8 out;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const float q = static_cast<float>(static_cast<uint32_t>(c >> (8 * j)) & 0xFFu);
-      float w;
-      if constexpr (QT == kQ6_K) w = a * (q - 32.0f);
-      else w = a * q - b;
-      out[j] = static_cast<_Float16>(w);
+      const float q = static_cast<float>((w[j >> 2] >> (8 * (j & 3))) & 0xFFu);
+      out[j] = static_cast<_Float16>(fmaf(a, q, nb));
     }
     return out;
   }
@@ -105,15 +107,23 @@ __device__ __forceinline__ h8 weight_fragment(long codes, float a, float b) {
 
 // Workgroup: WN wavefronts side by side, each owning 128 activation rows x 64
 // outputs (8 x 4 MFMA tiles); the workgroup covers 128 rows x 64 WN outputs.
-// Activations are staged two MFMA steps at a time.
+// Activations are staged four MFMA steps (half a unit) at a time.
+//
+// Load order per unit (vector loads complete in order, so a wait for one load
+// is a wait for every older one): the activations of the next stage first,
+// then the next unit's weights. The wait at the end of stage 0 (for the stage
+// 1 activations) then leaves the weights in flight; they are waited for only
+// at the end of stage 1, two stages after they were issued.
 template <int QT, bool WIDE, int WN>
 __global__ __launch_bounds__(64 * WN) void gemm_kernel(GemmArgs a) {
   using U = Unit<QT>;
   constexpr int kThreads = 64 * WN;
   constexpr Record R = record_geometry(QT, WIDE);
-  constexpr uint32_t kStage = 2 * 8 * 64 * 16;  // [step][row tile][lane] x 16 B
-  constexpr int kChunks = 1024 / kThreads;      // 16-byte chunks per thread per stage
-  __shared__ __attribute__((aligned(16))) uint8_t lds[2 * kStage];
+  constexpr uint32_t kStage = 4 * 8 * 64 * 16;  // [step][row tile][lane] x 16 B = 32 KB
+  constexpr int kChunks = 2048 / kThreads;      // 16-byte chunks per thread per stage
+  // element offset of stage h (0/1) within a unit: window_first(g, h) - window_first(g, 0)
+  constexpr uint32_t kHalf = QT == kQ6_K ? 64 : 32;
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
 
   const uint32_t tid = threadIdx.x, lane = tid & 63, wn = tid >> 6;
   const uint32_t g = lane >> 4, c16 = lane & 15;
@@ -132,26 +142,36 @@ __global__ __launch_bounds__(64 * WN) void gemm_kernel(GemmArgs a) {
     trec[ct] = a.w.qs + static_cast<uint64_t>(t) * units * R.bytes;
   }
 
-  // stage q (0..3) of unit u holds steps 2q, 2q+1: for each (row, lane group)
-  // the 16 elements window_first(g, q / 2) + 16 (q % 2) + [0, 16), two chunks
-  auto stage_load = [&](uint32_t u, uint32_t q, uint4 regs[kChunks]) {
-#pragma unroll
-    for (int i = 0; i < kChunks; ++i) {
-      const uint32_t cid = tid + kThreads * i;
-      const uint32_t row = cid >> 3, gg = (cid >> 1) & 3, tt = cid & 1;
-      const uint32_t e = 256 * u + window_first<QT>(gg, q >> 1) + 16 * (q & 1) + 8 * tt;
-      regs[i] = *reinterpret_cast<const uint4*>(a.xh + (m0 + row) * K + e);
-    }
+  // Staging: chunk i of this thread is (row = tid / 16 + (256 / 16) i ...):
+  // for each (row, lane group) a stage holds the 32 elements
+  // window_first(g, h) + [0, 32) as four 16-byte chunks (tt).
+  constexpr uint32_t kRowsPerPass = kThreads / 16;
+  const uint32_t srow = tid >> 4, sg = (tid >> 2) & 3, stt = tid & 3;
+  const _Float16* abase = a.xh + (m0 + srow) * K + window_first<QT>(sg, 0) + 8 * stt;
+  const uint64_t arow_step = static_cast<uint64_t>(kRowsPerPass) * K;  // elements per pass
+  const uint32_t sbase = ((stt * 8 + (srow >> 4)) * 64 + sg * 16 + (srow & 15)) * 16;
+  // LDS byte offset of pass i relative to pass 0: row srow + i * kRowsPerPass
+  // (kRowsPerPass divides 16, srow < kRowsPerPass)
+  auto lds_pass = [](int i) -> uint32_t {
+    const uint32_t r = static_cast<uint32_t>(i) * kRowsPerPass;
+    return (r >> 4) * 64 * 16 + (r & 15) * 16;
   };
-  auto stage_store = [&](uint32_t buf, const uint4 regs[kChunks]) {
-#pragma unroll
-    for (int i = 0; i < kChunks; ++i) {
-      const uint32_t cid = tid + kThreads * i;
-      const uint32_t row = cid >> 3, gg = (cid >> 1) & 3, tt = cid & 1;
-      const uint32_t off = ((tt * 8 + (row >> 4)) * 64 + gg * 16 + (row & 15)) * 16;
-      *reinterpret_cast<uint4*>(lds + buf * kStage + off) = regs[i];
-    }
-  };
+
+  // staging registers: a native vector array (HIP's uint4 wraps a union,
+  // which keeps a returned copy out of registers)
+  u32x4 areg[kChunks];
+#define QI_STAGE_LOAD(U_, H_)                                                           \
+  do {                                                                                  \
+    const _Float16* p_ = abase + 256 * (U_) + kHalf * (H_);                             \
+    _Pragma("unroll") for (int i_ = 0; i_ < kChunks; ++i_) areg[i_] =                   \
+        *reinterpret_cast<const u32x4*>(p_ + i_ * arow_step);                           \
+  } while (0)
+#define QI_STAGE_STORE(BUF_)                                                            \
+  do {                                                                                  \
+    uint8_t* p_ = lds + (BUF_) * kStage + sbase;                                        \
+    _Pragma("unroll") for (int i_ = 0; i_ < kChunks; ++i_)                              \
+        *reinterpret_cast<u32x4*>(p_ + lds_pass(i_)) = areg[i_];                        \
+  } while (0)
 
   f4 acc[8][4];
 #pragma unroll
@@ -160,11 +180,10 @@ __global__ __launch_bounds__(64 * WN) void gemm_kernel(GemmArgs a) {
     for (int j = 0; j < 4; ++j) acc[i][j] = f4{0, 0, 0, 0};
 
   typename U::Raw cur[4], nxt[4];
+  QI_STAGE_LOAD(0u, 0u);
 #pragma unroll
   for (int ct = 0; ct < 4; ++ct) U::template load<WIDE>(trec[ct], lane, cur[ct]);
-  uint4 areg[kChunks];
-  stage_load(0, 0, areg);
-  stage_store(0, areg);
+  QI_STAGE_STORE(0u);
   __syncthreads();
 
   uint32_t buf = 0;
@@ -172,24 +191,26 @@ __global__ __launch_bounds__(64 * WN) void gemm_kernel(GemmArgs a) {
     float sa[4][U::kWindows], sb[4][U::kWindows];
 #pragma unroll
     for (int ct = 0; ct < 4; ++ct) U::template scales<WIDE>(g, cur[ct], sa[ct], sb[ct]);
-    if (u + 1 < units) {
+    const bool next_unit = u + 1 < units;
+    // the two stages of the unit, with the stage index a compile-time constant
+    // (a runtime step index would put the per-window arrays in scratch memory)
+    auto stage = [&](auto hc) {
+      constexpr uint32_t h = decltype(hc)::value;
+      const bool more = h == 0 || next_unit;
+      if (more) QI_STAGE_LOAD(h == 0 ? u : u + 1, h ^ 1);
+      if (h == 0 && next_unit) {
 #pragma unroll
-      for (int ct = 0; ct < 4; ++ct)
-        U::template load<WIDE>(trec[ct] + static_cast<uint64_t>(u + 1) * R.bytes, lane, nxt[ct]);
-    }
+        for (int ct = 0; ct < 4; ++ct)
+          U::template load<WIDE>(trec[ct] + static_cast<uint64_t>(u + 1) * R.bytes, lane, nxt[ct]);
+      }
+      const uint8_t* sb_ = lds + buf * kStage;
 #pragma unroll
-    for (uint32_t q = 0; q < 4; ++q) {
-      // next stage's activations into registers while this one computes
-      const bool more = q < 3 || u + 1 < units;
-      if (more) stage_load(q < 3 ? u : u + 1, (q + 1) & 3, areg);
-      const uint8_t* sbase = lds + buf * kStage;
-#pragma unroll
-      for (int tt = 0; tt < 2; ++tt) {
-        const int t = 2 * q + tt;
+      for (int tt = 0; tt < 4; ++tt) {
+        const int t = 4 * h + tt;
         h8 af[8];
 #pragma unroll
         for (int rt = 0; rt < 8; ++rt)
-          af[rt] = *reinterpret_cast<const h8*>(sbase + ((tt * 8 + rt) * 64 + lane) * 16);
+          af[rt] = *reinterpret_cast<const h8*>(sb_ + ((tt * 8 + rt) * 64 + lane) * 16);
 #pragma unroll
         for (int ct = 0; ct < 4; ++ct) {
           const int w = t / U::kSteps;
@@ -199,31 +220,38 @@ __global__ __launch_bounds__(64 * WN) void gemm_kernel(GemmArgs a) {
             acc[rt][ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[rt], bf, acc[rt][ct], 0, 0, 0);
         }
       }
-      if (more) stage_store(buf ^ 1, areg);
+      if (more) QI_STAGE_STORE(buf ^ 1);
       __syncthreads();
       buf ^= 1;
-    }
-    if (u + 1 < units) {
+    };
+    stage(std::integral_constant<uint32_t, 0>{});
+    stage(std::integral_constant<uint32_t, 1>{});
+    if (next_unit) {
 #pragma unroll
       for (int ct = 0; ct < 4; ++ct) cur[ct] = nxt[ct];
     }
   }
 
   // C[i][j]: lane j + 16 (i / 4), element i % 4
+  const uint64_t ld = a.w.n;
+  float* yrow = a.y + (m0 + 4 * g) * ld;
 #pragma unroll
-  for (int rt = 0; rt < 8; ++rt) {
+  for (int ct = 0; ct < 4; ++ct) {
+    const uint64_t n = static_cast<uint64_t>(tile_raw[ct]) * 16 + c16;
+    if (n >= a.w.n) continue;
 #pragma unroll
-    for (int ct = 0; ct < 4; ++ct) {
-      const uint64_t n = static_cast<uint64_t>(tile_raw[ct]) * 16 + c16;
-      if (n >= a.w.n) continue;
+    for (int rt = 0; rt < 8; ++rt) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const uint64_t m = m0 + rt * 16 + 4 * g + r;
-        if (m < a.m) a.y[m * a.w.n + n] = acc[rt][ct][r];
+        if (m < a.m) yrow[(rt * 16 + r) * ld + n] = acc[rt][ct][r];
       }
     }
   }
 }
+
+#undef QI_STAGE_LOAD
+#undef QI_STAGE_STORE
 
 namespace {
 
@@ -231,7 +259,8 @@ template <int QT, bool WIDE, int WN>
 hipError_t launch_wn(const Image& im, const GemmArgs& a, hipStream_t st) {
   const uint32_t nblk = static_cast<uint32_t>((im.tiles + 4 * WN - 1) / (4 * WN));
   const uint32_t mblk = static_cast<uint32_t>(a.m_pad / kTileM);
-  hipLaunchKernelGGL((gemm_kernel<QT, WIDE, WN>), dim3(nblk, mblk), dim3(64 * WN), 0, st, a);
+  hipLaunchKernelGGL((gemm_kernel<QT, WIDE, WN>), dim3(nblk, mblk), dim3(64 * WN), 2 * 4 * 8 * 64 * 16,
+                     st, a);
   return hipGetLastError();
 }
 
