@@ -105,6 +105,33 @@ __device__ __forceinline__ h8 weight_fragment(long codes, float a, float b) {
   }
 }
 
+// Two elements (2p, 2p + 1) of a step's f16 weight fragment, as one packed
+// register, from the step's 8 code bytes w[2]: the same arithmetic as
+// weight_fragment, split so that it can be spread between MFMA issues.
+template <int QT>
+__device__ __forceinline__ uint32_t weight_pair(const uint32_t w[2], float a, float b, int p) {
+  uint32_t word = w[p >> 1];
+  if constexpr (QT == kQ8_0 || QT == kQ4_0) {
+    if constexpr (QT == kQ8_0) word ^= 0x80808080u;
+    constexpr float bias = QT == kQ8_0 ? 1152.0f : 1032.0f;
+    const h2 sub = {static_cast<_Float16>(bias), static_cast<_Float16>(bias)};
+    const h2 q = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, word, (p & 1) ? 0x04030402u
+                                                                                   : 0x04010400u)) - sub;
+    const _Float16 ha = static_cast<_Float16>(a);
+    return __builtin_bit_cast(uint32_t, q * h2{ha, ha});
+  } else {
+    // the codes as exact f16 integers, then fma in f32 with one rounding to
+    // f16 (v_fma_mix: f16 code, f32 scale and offset)
+    const float nb = QT == kQ6_K ? -32.0f * a : -b;
+    const h2 sub = {static_cast<_Float16>(1024.0f), static_cast<_Float16>(1024.0f)};
+    const h2 q = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, word, (p & 1) ? 0x04030402u
+                                                                                   : 0x04010400u)) - sub;
+    const h2 r = {static_cast<_Float16>(fmaf(a, static_cast<float>(q[0]), nb)),
+                  static_cast<_Float16>(fmaf(a, static_cast<float>(q[1]), nb))};
+    return __builtin_bit_cast(uint32_t, r);
+  }
+}
+
 // Workgroup: WN wavefronts side by side, each owning 128 activation rows x 64
 // outputs (8 x 4 MFMA tiles); the workgroup covers 128 rows x 64 WN outputs.
 // Activations are staged four MFMA steps (half a unit) at a time.
@@ -117,10 +144,8 @@ __device__ __forceinline__ h8 weight_fragment(long codes, float a, float b) {
 template <int QT, bool WIDE, int WN>
 __global__ __launch_bounds__(64 * WN) void gemm_kernel(GemmArgs a) {
   using U = Unit<QT>;
-  constexpr int kThreads = 64 * WN;
   constexpr Record R = record_geometry(QT, WIDE);
   constexpr uint32_t kStage = 4 * 8 * 64 * 16;  // [step][row tile][lane] x 16 B = 32 KB
-  constexpr int kChunks = 2048 / kThreads;      // 16-byte chunks per thread per stage
   // element offset of stage h (0/1) within a unit: window_first(g, h) - window_first(g, 0)
   constexpr uint32_t kHalf = QT == kQ6_K ? 64 : 32;
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
@@ -142,35 +167,34 @@ __global__ __launch_bounds__(64 * WN) void gemm_kernel(GemmArgs a) {
     trec[ct] = a.w.qs + static_cast<uint64_t>(t) * units * R.bytes;
   }
 
-  // Staging: chunk i of this thread is (row = tid / 16 + (256 / 16) i ...):
-  // for each (row, lane group) a stage holds the 32 elements
-  // window_first(g, h) + [0, 32) as four 16-byte chunks (tt).
-  constexpr uint32_t kRowsPerPass = kThreads / 16;
-  const uint32_t srow = tid >> 4, sg = (tid >> 2) & 3, stt = tid & 3;
-  const _Float16* abase = a.xh + (m0 + srow) * K + window_first<QT>(sg, 0) + 8 * stt;
-  const uint64_t arow_step = static_cast<uint64_t>(kRowsPerPass) * K;  // elements per pass
-  const uint32_t sbase = ((stt * 8 + (srow >> 4)) * 64 + sg * 16 + (srow & 15)) * 16;
-  // LDS byte offset of pass i relative to pass 0: row srow + i * kRowsPerPass
-  // (kRowsPerPass divides 16, srow < kRowsPerPass)
-  auto lds_pass = [](int i) -> uint32_t {
-    const uint32_t r = static_cast<uint32_t>(i) * kRowsPerPass;
-    return (r >> 4) * 64 * 16 + (r & 15) * 16;
-  };
+  // Staging of one stage (128 rows x 4 lane groups x 32 elements, 32 KB):
+  // thread t owns row 16 rt + i with i = t % 16, lane group sg = (t / 16) % 4
+  // and row tiles rt = t / 64 + 4 p (p = 0, 1); it loads that row's 32
+  // elements window_first(sg, h) + [0, 32) as four 16-byte chunks (steps tt)
+  // and writes chunk tt to slot 16 sg + i of block (tt, rt). One store
+  // instruction of a wavefront thus fills one contiguous 1 KB block (no LDS
+  // bank conflicts), the same pattern the fragment reads use.
+  static_assert(WN == 4, "staging assumes 4 wavefronts");
+  constexpr int kChunks = 8;
+  const uint32_t si = tid & 15, sg = (tid >> 4) & 3, srt = tid >> 6;
+  const _Float16* abase = a.xh + (m0 + 16 * srt + si) * K + window_first<QT>(sg, 0);
+  const uint64_t apass = static_cast<uint64_t>(64) * K;  // 4 row tiles further down
+  const uint32_t sbase = (srt * 64 + sg * 16 + si) * 16;
 
   // staging registers: a native vector array (HIP's uint4 wraps a union,
-  // which keeps a returned copy out of registers)
+  // which keeps a returned copy out of registers); index 4 p + tt
   u32x4 areg[kChunks];
 #define QI_STAGE_LOAD(U_, H_)                                                           \
   do {                                                                                  \
     const _Float16* p_ = abase + 256 * (U_) + kHalf * (H_);                             \
     _Pragma("unroll") for (int i_ = 0; i_ < kChunks; ++i_) areg[i_] =                   \
-        *reinterpret_cast<const u32x4*>(p_ + i_ * arow_step);                           \
+        *reinterpret_cast<const u32x4*>(p_ + (i_ >> 2) * apass + 8 * (i_ & 3));         \
   } while (0)
 #define QI_STAGE_STORE(BUF_)                                                            \
   do {                                                                                  \
     uint8_t* p_ = lds + (BUF_) * kStage + sbase;                                        \
     _Pragma("unroll") for (int i_ = 0; i_ < kChunks; ++i_)                              \
-        *reinterpret_cast<u32x4*>(p_ + lds_pass(i_)) = areg[i_];                        \
+        *reinterpret_cast<u32x4*>(p_ + ((i_ & 3) * 8 + 4 * (i_ >> 2)) * 64 * 16) = areg[i_]; \
   } while (0)
 
   f4 acc[8][4];
@@ -186,49 +210,99 @@ __global__ __launch_bounds__(64 * WN) void gemm_kernel(GemmArgs a) {
   QI_STAGE_STORE(0u);
   __syncthreads();
 
+  // Software pipeline: while the 32 MFMAs of a step issue, the operands of
+  // the next step are prepared in between them (one MFMA, then a slice of the
+  // LDS reads and of the weight dequantization, fenced by sched_barrier so
+  // that the matrix core and the VALU overlap), including across stages and
+  // into the next unit (whose weights were prefetched two stages earlier).
+  float sa[4][U::kWindows], sb[4][U::kWindows];
+#pragma unroll
+  for (int ct = 0; ct < 4; ++ct) U::template scales<WIDE>(g, cur[ct], sa[ct], sb[ct]);
+  uint32_t bk[4][4];  // the current step's weight fragments, packed f16 pairs
+#pragma unroll
+  for (int ct = 0; ct < 4; ++ct) {
+    const uint64_t c = static_cast<uint64_t>(U::codes(cur[ct], g, 0));
+    const uint32_t w[2] = {static_cast<uint32_t>(c), static_cast<uint32_t>(c >> 32)};
+#pragma unroll
+    for (int p = 0; p < 4; ++p) bk[ct][p] = weight_pair<QT>(w, sa[ct][0], sb[ct][0], p);
+  }
+
   uint32_t buf = 0;
   for (uint32_t u = 0; u < units; ++u) {
-    float sa[4][U::kWindows], sb[4][U::kWindows];
-#pragma unroll
-    for (int ct = 0; ct < 4; ++ct) U::template scales<WIDE>(g, cur[ct], sa[ct], sb[ct]);
     const bool next_unit = u + 1 < units;
+    // after the last unit the prefetches re-read it (unused, always in bounds)
+    const uint32_t un = next_unit ? u + 1 : u;
+    float nsa[4][U::kWindows], nsb[4][U::kWindows];
     // the two stages of the unit, with the stage index a compile-time constant
     // (a runtime step index would put the per-window arrays in scratch memory)
     auto stage = [&](auto hc) {
       constexpr uint32_t h = decltype(hc)::value;
-      const bool more = h == 0 || next_unit;
-      if (more) QI_STAGE_LOAD(h == 0 ? u : u + 1, h ^ 1);
-      if (h == 0 && next_unit) {
+      QI_STAGE_LOAD(h == 0 ? u : un, h ^ 1);
+      if constexpr (h == 0) {
 #pragma unroll
         for (int ct = 0; ct < 4; ++ct)
-          U::template load<WIDE>(trec[ct] + static_cast<uint64_t>(u + 1) * R.bytes, lane, nxt[ct]);
+          U::template load<WIDE>(trec[ct] + static_cast<uint64_t>(un) * R.bytes, lane, nxt[ct]);
+      } else {
+#pragma unroll
+        for (int ct = 0; ct < 4; ++ct) U::template scales<WIDE>(g, nxt[ct], nsa[ct], nsb[ct]);
       }
       const uint8_t* sb_ = lds + buf * kStage;
+      h8 af[8];
+#pragma unroll
+      for (int rt = 0; rt < 8; ++rt)
+        af[rt] = *reinterpret_cast<const h8*>(sb_ + (rt * 64 + lane) * 16);
 #pragma unroll
       for (int tt = 0; tt < 4; ++tt) {
-        const int t = 4 * h + tt;
-        h8 af[8];
+        const int t = 4 * static_cast<int>(h) + tt;
+        const bool to_next_unit = t == 7;  // the next step is the next unit's step 0
+        h8 afn[8];
+        uint32_t bn[4][4];
+        uint32_t cw[2] = {0, 0};
+        float ca = 0.0f, cb = 0.0f;
 #pragma unroll
-        for (int rt = 0; rt < 8; ++rt)
-          af[rt] = *reinterpret_cast<const h8*>(sb_ + ((tt * 8 + rt) * 64 + lane) * 16);
-#pragma unroll
-        for (int ct = 0; ct < 4; ++ct) {
-          const int w = t / U::kSteps;
-          const h8 bf = weight_fragment<QT>(U::codes(cur[ct], g, t), sa[ct][w], sb[ct][w]);
-#pragma unroll
-          for (int rt = 0; rt < 8; ++rt)
-            acc[rt][ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[rt], bf, acc[rt][ct], 0, 0, 0);
+        for (int i = 0; i < 32; ++i) {
+          const int ct = i >> 3, rt = i & 7;
+          acc[rt][ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[rt], __builtin_bit_cast(h8, bk[ct]),
+                                                              acc[rt][ct], 0, 0, 0);
+          if (tt < 3 && i < 8)
+            afn[i] = *reinterpret_cast<const h8*>(sb_ + (((tt + 1) * 8 + i) * 64 + lane) * 16);
+          const int j = i & 7;
+          if (j == 0) {
+            const int tn = to_next_unit ? 0 : t + 1;
+            const uint64_t c = static_cast<uint64_t>(to_next_unit ? U::codes(nxt[ct], g, 0)
+                                                                  : U::codes(cur[ct], g, tn));
+            cw[0] = static_cast<uint32_t>(c);
+            cw[1] = static_cast<uint32_t>(c >> 32);
+            const int w = tn / U::kSteps;
+            ca = to_next_unit ? nsa[ct][0] : sa[ct][w];
+            cb = to_next_unit ? nsb[ct][0] : sb[ct][w];
+          }
+          if (j & 1) bn[ct][j >> 1] = weight_pair<QT>(cw, ca, cb, j >> 1);
+          __builtin_amdgcn_sched_barrier(0);
         }
+        if (tt < 3) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) af[i] = afn[i];
+        }
+#pragma unroll
+        for (int ct = 0; ct < 4; ++ct)
+#pragma unroll
+          for (int p = 0; p < 4; ++p) bk[ct][p] = bn[ct][p];
       }
-      if (more) QI_STAGE_STORE(buf ^ 1);
+      QI_STAGE_STORE(buf ^ 1);
       __syncthreads();
       buf ^= 1;
     };
     stage(std::integral_constant<uint32_t, 0>{});
     stage(std::integral_constant<uint32_t, 1>{});
-    if (next_unit) {
 #pragma unroll
-      for (int ct = 0; ct < 4; ++ct) cur[ct] = nxt[ct];
+    for (int ct = 0; ct < 4; ++ct) {
+      cur[ct] = nxt[ct];
+#pragma unroll
+      for (int w = 0; w < U::kWindows; ++w) {
+        sa[ct][w] = nsa[ct][w];
+        sb[ct][w] = nsb[ct][w];
+      }
     }
   }
 
@@ -266,17 +340,7 @@ hipError_t launch_wn(const Image& im, const GemmArgs& a, hipStream_t st) {
 
 template <int QT>
 hipError_t launch_q(const Image& im, const GemmArgs& a, hipStream_t st) {
-  // 4 wavefronts (256 outputs) per workgroup when that still gives every CU a
-  // workgroup, 2 otherwise
-  const uint64_t wgs4 = ((im.tiles + 15) / 16) * (a.m_pad / kTileM);
-  const bool wide4 = wgs4 >= 256 || QT == kQ5_K;  // Q5_K spills at 2 wavefronts
-  if constexpr (QT == kQ5_K) {
-    (void)wide4;
-    return im.wide ? launch_wn<QT, true, 4>(im, a, st) : launch_wn<QT, false, 4>(im, a, st);
-  } else {
-    if (im.wide) return wide4 ? launch_wn<QT, true, 4>(im, a, st) : launch_wn<QT, true, 2>(im, a, st);
-    return wide4 ? launch_wn<QT, false, 4>(im, a, st) : launch_wn<QT, false, 2>(im, a, st);
-  }
+  return im.wide ? launch_wn<QT, true, 4>(im, a, st) : launch_wn<QT, false, 4>(im, a, st);
 }
 
 }  // namespace
