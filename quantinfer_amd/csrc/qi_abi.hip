@@ -40,6 +40,8 @@ struct qi_hip_ctx {
   uint64_t ycap = 0;
   float* hbuf = nullptr;  // f16 activations of the prefill GEMM (capacity in floats)
   uint64_t hcap = 0;
+  float* dbuf = nullptr;  // activation records of the decode GEMV, 2+ rows (capacity in floats)
+  uint64_t dcap = 0;
   int gemv_split = 0;  // QI_HIP_GEMV_SPLIT tuning override (wavefronts per GEMV workgroup: 4 or 8)
 };
 
@@ -102,6 +104,7 @@ void ctx_destroy(qi_hip_ctx* c) {
   if (c->xbuf) (void)hipFree(c->xbuf);
   if (c->ybuf) (void)hipFree(c->ybuf);
   if (c->hbuf) (void)hipFree(c->hbuf);
+  if (c->dbuf) (void)hipFree(c->dbuf);
   if (c->stream) (void)hipStreamDestroy(c->stream);
   delete c;
 }
@@ -159,6 +162,19 @@ qi_hip_status run_linear(qi_hip_ctx* c, const qi_hip_weights* w, const float* x,
     const int mt = rows == 1 ? 1 : rows == 2 ? 2 : rows <= 4 ? 4 : rows <= 8 ? 8 : 16;
     if (mfma) {
       qi::GemvMfmaArgs ga{v, x + m0 * im.k, y + m0 * im.n, rows};
+      if (rows >= 2) {
+        // activation records built once for the whole call
+        const uint64_t need = (qi::gemv_digits_bytes(im.k, static_cast<uint32_t>(rows)) + 3) / 4;
+        if (need > c->dcap) {
+          QI_HIP_TRY(hipStreamSynchronize(st), "synchronize before growing the GEMV workspace");
+          qi_hip_status s = grow(&c->dbuf, &c->dcap, need, "alloc GEMV workspace");
+          if (s != QI_HIP_OK) return s;
+        }
+        QI_HIP_TRY(qi::launch_gemv_digits(im.qtype, ga.x, im.k, static_cast<uint32_t>(rows),
+                                          reinterpret_cast<uint8_t*>(c->dbuf), st),
+                   "launch gemv activation records");
+        ga.digits = reinterpret_cast<const uint8_t*>(c->dbuf);
+      }
       const int split = c->gemv_split > 0 ? c->gemv_split : qi::gemv_mfma_split(im.k, im.n);
       QI_HIP_TRY(qi::launch_gemv_mfma(im.qtype, im.wide != 0, mt, split, ga, st), "launch gemv");
       continue;

@@ -43,8 +43,14 @@ namespace qi {
 typedef int v4i __attribute__((ext_vector_type(4)));
 
 constexpr uint32_t kZeroBytes = 1024;  // zero A operand for the lanes of other lane groups
-constexpr uint32_t kUnitDigitBytes = 1024;  // 256 activations x 4 digits, per row
-constexpr uint32_t kUnitAuxBytes = 128;     // 8 windows x float4 {2^-s, sum lo16, sum hi16, 0}
+// Activation record of one (row, unit): 256 activations x 4 digits (1024 B,
+// [step t][lane group g] x 32 B, digit d of the 8 activations at byte 8 d),
+// then 8 windows x float4 {2^-s, sum of elements 0-15, of 16-31, 0} (128 B,
+// [g][h]). Built in LDS by the workgroup, or once per call in global memory
+// by gemv_digits_kernel and copied into LDS.
+constexpr uint32_t kUnitDigitBytes = 1024;
+constexpr uint32_t kUnitAuxBytes = 128;
+constexpr uint32_t kUnitRecBytes = kUnitDigitBytes + kUnitAuxBytes;
 constexpr uint32_t kMaxLds = 160 * 1024;
 
 // Byte transpose of four digit words (one per activation) into four words
@@ -91,14 +97,12 @@ __device__ __forceinline__ void load_half(const float* x, uint32_t K, uint32_t k
   for (int i = 0; i < 4; ++i) o.v[i] = p[i];
 }
 
-// Digits and sums of one half window into LDS. Every lane of the wavefront
-// takes part (the window max and the other half's sum come from the
-// neighbouring lane); only `valid` items store.
-//   digits: [m][u][t][g] 32-byte records, digit d of the 8 activations of
-//           step t at byte 8*d;
-//   aux:    [m][u][g][h] float4 {2^-s, sum of elements 0-15, of 16-31, 0}.
-__device__ __forceinline__ void store_half(const HalfX& o, const Item& it, bool valid,
-                                           uint8_t* digits, float4* aux, uint32_t cu) {
+// Digits and sums of one half window into the activation records
+// recs[m][u] (cu units per row). Every lane of the wavefront takes part (the
+// window max and the other half's sum come from the neighbouring lane); only
+// `valid` items store.
+__device__ __forceinline__ void store_half(const HalfX& o, const Item& it, bool valid, uint8_t* recs,
+                                           uint32_t cu) {
   const float xs[16] = {o.v[0].x, o.v[0].y, o.v[0].z, o.v[0].w, o.v[1].x, o.v[1].y, o.v[1].z, o.v[1].w,
                         o.v[2].x, o.v[2].y, o.v[2].z, o.v[2].w, o.v[3].x, o.v[3].y, o.v[3].z, o.v[3].w};
   float mx = 0.0f, sum = 0.0f;
@@ -115,7 +119,8 @@ __device__ __forceinline__ void store_half(const HalfX& o, const Item& it, bool 
   const float inv = mx > 0.0f ? ldexpf(1.0f, e - 29) : 0.0f;
   if (!valid) return;
   const uint32_t t0 = 4 * it.h + 2 * it.half;
-  uint8_t* dst0 = digits + ((it.m * cu + it.u) * 8 + t0) * 128 + it.g * 32;
+  uint8_t* const rec = recs + (static_cast<uint64_t>(it.m) * cu + it.u) * kUnitRecBytes;
+  uint8_t* dst0 = rec + (t0 * 4 + it.g) * 32;
 #pragma unroll
   for (int tt = 0; tt < 2; ++tt) {
     uint32_t dig[8];
@@ -133,23 +138,25 @@ __device__ __forceinline__ void store_half(const HalfX& o, const Item& it, bool 
     *reinterpret_cast<uint4*>(dst + 16) = make_uint4(lo[2], hi[2], lo[3], hi[3]);
   }
   if (it.half == 0)
-    aux[(it.m * cu + it.u) * 8 + it.g * 2 + it.h] = make_float4(inv, sum, other, 0.0f);
+    reinterpret_cast<float4*>(rec + kUnitDigitBytes)[it.g * 2 + it.h] = make_float4(inv, sum, other, 0.0f);
 }
 
 // WC tiles of 16 outputs per workgroup, SW wavefronts per tile splitting its
 // K range, D units in flight per wavefront, XP half windows of activations
 // preloaded per thread (the WC tiles share one activation prep).
-template <int QT, bool WIDE, int MT, int SW, int D, int WC>
+// PRE: the activation records were built by gemv_digits_kernel (a.digits);
+// the workgroup copies its chunk into LDS with global-to-LDS loads instead of
+// building it.
+template <int QT, bool WIDE, int MT, int SW, int D, int WC, bool PRE>
 __global__ __launch_bounds__(64 * SW * WC) void gemv_mfma_kernel(GemvMfmaArgs a) {
   using U = Unit<QT>;
   constexpr int kThreads = 64 * SW * WC;
   constexpr int XP = SW == 8 ? 2 : 1;
   constexpr Record R = record_geometry(QT, WIDE);
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-  // [0, kZeroBytes) zeros | digits [m][chunk unit][t][g] | aux [m][chunk unit][g][h]
+  // [0, kZeroBytes) zeros | activation records [m][chunk unit]
   const uint32_t cu = a.chunk_units;
-  uint8_t* const digits = lds + kZeroBytes;
-  float4* const aux = reinterpret_cast<float4*>(digits + MT * cu * kUnitDigitBytes);
+  uint8_t* const recs = lds + kZeroBytes;
 
   const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const uint32_t sw = wave % SW, wc = wave / SW;
@@ -185,29 +192,50 @@ __global__ __launch_bounds__(64 * SW * WC) void gemv_mfma_kernel(GemvMfmaArgs a)
     const uint32_t u_count = (units * (sw + 1)) / SW - u_begin;
     const uint32_t u_last = ku0 + (u_count ? u_begin + u_count - 1 : 0);
 
-    // activations first (so that waiting for them never waits for the
-    // weights), then this wavefront's first D units, unconditionally (slots
-    // past the run re-read its last unit)
-    HalfX xp[XP];
-    Item ip[XP];
+    if constexpr (PRE) {
+      // copy the chunk's records: row m's units [ku0, ku0 + units) are
+      // contiguous in both places; one global-to-LDS load per wavefront
+      // moves 1 KB (lanes past the end of a row's run stay idle)
+      const uint32_t bytes = units * kUnitRecBytes, pieces = (bytes + 1023) / 1024;
+      for (uint32_t pi = wave; pi < static_cast<uint32_t>(M) * pieces; pi += kThreads / 64) {
+        const uint32_t m = pi / pieces, p = pi % pieces, off = p * 1024 + lane * 16;
+        if (off < bytes)
+          __builtin_amdgcn_global_load_lds(
+              a.digits + (static_cast<uint64_t>(m) * units_total + ku0) * kUnitRecBytes + off,
+              (__attribute__((address_space(3))) void*)(recs + (m * cu) * kUnitRecBytes + p * 1024), 16, 0,
+              0);
+      }
 #pragma unroll
-    for (int i = 0; i < XP; ++i) {
-      const uint32_t hi = tid + kThreads * i;
-      ip[i] = item_of(hi < halves ? hi : 0, units);
-      load_half<QT>(a.x, K, k0, ip[i], xp[i]);
-    }
+      for (int i = 0; i < D; ++i)
+        U::template load<WIDE>(trec + min(ku0 + u_begin + i, u_last) * R.bytes, lane, ring[i]);
+      (void)halves;
+      (void)K;
+      (void)k0;
+    } else {
+      // activations first (so that waiting for them never waits for the
+      // weights), then this wavefront's first D units, unconditionally (slots
+      // past the run re-read its last unit)
+      HalfX xp[XP];
+      Item ip[XP];
 #pragma unroll
-    for (int i = 0; i < D; ++i)
-      U::template load<WIDE>(trec + min(ku0 + u_begin + i, u_last) * R.bytes, lane, ring[i]);
+      for (int i = 0; i < XP; ++i) {
+        const uint32_t hi = tid + kThreads * i;
+        ip[i] = item_of(hi < halves ? hi : 0, units);
+        load_half<QT>(a.x, K, k0, ip[i], xp[i]);
+      }
+#pragma unroll
+      for (int i = 0; i < D; ++i)
+        U::template load<WIDE>(trec + min(ku0 + u_begin + i, u_last) * R.bytes, lane, ring[i]);
 
 #pragma unroll
-    for (int i = 0; i < XP; ++i) store_half(xp[i], ip[i], tid + kThreads * i < halves, digits, aux, cu);
-    for (uint32_t h0 = XP * kThreads; h0 < halves; h0 += kThreads) {
-      const uint32_t hi = h0 + tid;
-      Item it = item_of(hi < halves ? hi : 0, units);
-      HalfX xh;
-      load_half<QT>(a.x, K, k0, it, xh);
-      store_half(xh, it, hi < halves, digits, aux, cu);
+      for (int i = 0; i < XP; ++i) store_half(xp[i], ip[i], tid + kThreads * i < halves, recs, cu);
+      for (uint32_t h0 = XP * kThreads; h0 < halves; h0 += kThreads) {
+        const uint32_t hi = h0 + tid;
+        Item it = item_of(hi < halves ? hi : 0, units);
+        HalfX xh;
+        load_half<QT>(a.x, K, k0, it, xh);
+        store_half(xh, it, hi < halves, recs, cu);
+      }
     }
     __syncthreads();
 
@@ -222,26 +250,41 @@ __global__ __launch_bounds__(64 * SW * WC) void gemv_mfma_kernel(GemvMfmaArgs a)
         const uint32_t u = u_begin + j + i;  // chunk-relative unit
         float sa[U::kWindows], sb[U::kWindows];
         U::template scales<WIDE>(g, ring[i], sa, sb);
+        // Rows are independent: per step, all rows' activation words are read
+        // together and their MFMAs issued together (one LDS latency per step,
+        // not one per row). Rows past M compute on stale records and are never
+        // stored.
+        const uint8_t* abase[MT];
+        const float4* ax[MT];
 #pragma unroll
         for (int m = 0; m < MT; ++m) {
-          if (m >= M) break;
-          const uint8_t* abase = a_live ? digits + ((m * cu + u) * 8 * 4 + g) * 32 + digit * 8 : lds;
-          const float4* ax = aux + (m * cu + u) * 8 + g * 2;
+          const uint8_t* rec = recs + (m * cu + u) * kUnitRecBytes;
+          abase[m] = a_live ? rec + g * 32 + digit * 8 : lds;
+          ax[m] = reinterpret_cast<const float4*>(rec + kUnitDigitBytes) + g * 2;
+        }
 #pragma unroll
-          for (int w = 0; w < U::kWindows; ++w) {
-            v4i c = {0, 0, 0, 0};
+        for (int w = 0; w < U::kWindows; ++w) {
+          v4i c[MT];
 #pragma unroll
-            for (int s = 0; s < U::kSteps; ++s) {
-              const int t = w * U::kSteps + s;
-              const long av = *reinterpret_cast<const long*>(abase + t * 128);
-              c = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, U::codes(ring[i], g, t), c, 0, 0, 0);
-            }
+          for (int m = 0; m < MT; ++m) c[m] = v4i{0, 0, 0, 0};
+#pragma unroll
+          for (int s = 0; s < U::kSteps; ++s) {
+            const int t = w * U::kSteps + s;
+            long av[MT];
+#pragma unroll
+            for (int m = 0; m < MT; ++m) av[m] = *reinterpret_cast<const long*>(abase[m] + t * 128);
+            const long cb = U::codes(ring[i], g, t);
+#pragma unroll
+            for (int m = 0; m < MT; ++m) c[m] = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[m], cb, c[m], 0, 0, 0);
+          }
+          const int h = U::kSteps == 4 ? w : (w >> 1);
+#pragma unroll
+          for (int m = 0; m < MT; ++m) {
             // combine the digit sums: pairs exactly in int32 (|C0| < 2^20,
             // |C1 * 256| < 2^28), the two halves in f32
-            const float comb = fmaf(static_cast<float>(c[2] + c[3] * 256), 65536.0f,
-                                    static_cast<float>(c[0] + c[1] * 256));
-            const int h = U::kSteps == 4 ? w : (w >> 1);
-            const float4 wx = ax[h];
+            const float comb = fmaf(static_cast<float>(c[m][2] + c[m][3] * 256), 65536.0f,
+                                    static_cast<float>(c[m][0] + c[m][1] * 256));
+            const float4 wx = ax[m][h];
             acc[m] = fmaf(sa[w] * wx.x, comb, acc[m]);
             if constexpr (U::kMin) {
               const float xs = U::kSteps == 4 ? wx.y + wx.z : ((w & 1) ? wx.z : wx.y);
@@ -269,7 +312,7 @@ __global__ __launch_bounds__(64 * SW * WC) void gemv_mfma_kernel(GemvMfmaArgs a)
     v += __shfl_xor(v, 32);
     acc[m] = v;
   }
-  float* red = reinterpret_cast<float*>(digits);  // [WC][SW][MT][16]
+  float* red = reinterpret_cast<float*>(recs);  // [WC][SW][MT][16]
   if (g == 0) {
 #pragma unroll
     for (int m = 0; m < MT; ++m) red[((wc * SW + sw) * MT + m) * 16 + col] = acc[m];
@@ -287,20 +330,51 @@ __global__ __launch_bounds__(64 * SW * WC) void gemv_mfma_kernel(GemvMfmaArgs a)
   }
 }
 
+// Activation records of all M rows and K units, once per call (gemv_mfma
+// kernels with PRE copy them instead of building them per workgroup).
+template <int QT>
+__global__ __launch_bounds__(256) void gemv_digits_kernel(const float* x, uint32_t K, uint32_t units,
+                                                          uint32_t m, uint8_t* out) {
+  const uint32_t hi = blockIdx.x * 256 + threadIdx.x;  // half windows, [m][unit][16]
+  const bool valid = hi < m * units * 16;
+  const Item it = item_of(valid ? hi : 0, units);
+  HalfX xh;
+  load_half<QT>(x, K, 0, it, xh);
+  store_half(xh, it, valid, out, units);
+}
+
+hipError_t launch_gemv_digits(int32_t qtype, const float* x, uint64_t k, uint32_t m, uint8_t* out,
+                              hipStream_t st) {
+  const uint32_t units = static_cast<uint32_t>(k / 256);
+  const uint32_t blocks = (m * units * 16 + 255) / 256;
+  if (qtype == kQ6_K)
+    hipLaunchKernelGGL(gemv_digits_kernel<kQ6_K>, dim3(blocks), dim3(256), 0, st, x, static_cast<uint32_t>(k),
+                       units, m, out);
+  else
+    hipLaunchKernelGGL(gemv_digits_kernel<kQ4_K>, dim3(blocks), dim3(256), 0, st, x, static_cast<uint32_t>(k),
+                       units, m, out);
+  return hipGetLastError();
+}
+
+uint64_t gemv_digits_bytes(uint64_t k, uint32_t m) { return (k / 256) * m * kUnitRecBytes; }
+
 namespace {
 
 uint32_t lds_bytes(int mt, uint32_t chunk_units, int waves) {
-  const uint32_t main = kZeroBytes + static_cast<uint32_t>(mt) * chunk_units * (kUnitDigitBytes + kUnitAuxBytes);
+  const uint32_t main = kZeroBytes + static_cast<uint32_t>(mt) * chunk_units * kUnitRecBytes;
   const uint32_t red = kZeroBytes + static_cast<uint32_t>(waves * mt * 16 * 4);
   return main > red ? main : red;
 }
 
 template <int QT, bool WIDE, int MT, int SW, int D, int WC>
-hipError_t launch4(GemvMfmaArgs a, hipStream_t st) {
-  const uint32_t cap = (kMaxLds - kZeroBytes) / (MT * (kUnitDigitBytes + kUnitAuxBytes));
+hipError_t launch4(GemvMfmaArgs a, hipStream_t st, uint32_t chunk_target = 0) {
+  const uint32_t cap = chunk_target ? chunk_target : (kMaxLds - kZeroBytes) / (MT * kUnitRecBytes);
   a.chunk_units = a.w.units < cap ? a.w.units : cap;
   const uint32_t bytes = lds_bytes(MT, a.chunk_units, SW * WC);
-  auto kern = gemv_mfma_kernel<QT, WIDE, MT, SW, D, WC>;
+  // two or more activation rows read records built once per call
+  constexpr bool kPre = MT >= 2;
+  if (kPre && a.digits == nullptr) return hipErrorInvalidValue;
+  auto kern = gemv_mfma_kernel<QT, WIDE, MT, SW, D, WC, kPre>;
   if (bytes > 65536) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(bytes));
@@ -314,14 +388,18 @@ hipError_t launch4(GemvMfmaArgs a, hipStream_t st) {
 // units each wavefront holds
 template <int QT, bool WIDE, int MT>
 hipError_t launch_split(const GemvMfmaArgs& a, int sw, hipStream_t st) {
-  const uint32_t cap = (kMaxLds - kZeroBytes) / (MT * (kUnitDigitBytes + kUnitAuxBytes));
+  const uint32_t cap = (kMaxLds - kZeroBytes) / (MT * kUnitRecBytes);
   const uint32_t chunk = a.w.units < cap ? a.w.units : cap;
-  if constexpr (MT >= 8) {
-    // eight or more activation rows: only 4-wavefront workgroups (one tile)
-    // keep the accumulators and the ring in registers without spilling
+  if constexpr (MT >= 2) {
+    // Two or more rows copy prebuilt activation records, so small K chunks
+    // cost little: chunks of 8 units (4 at 16 rows), 4 wavefronts of one tile
+    // each holding 2 (1 at 8+ rows) units per chunk, so that several
+    // workgroups fit a CU's LDS.
     (void)sw;
     (void)chunk;
-    return launch4<QT, WIDE, MT, 4, 4, 1>(a, st);
+    if constexpr (MT >= 16) return launch4<QT, WIDE, MT, 4, 1, 1>(a, st, 4);
+    else if constexpr (MT >= 8) return launch4<QT, WIDE, MT, 4, 1, 1>(a, st, 4);
+    else return launch4<QT, WIDE, MT, 4, 2, 1>(a, st, 8);
   } else {
     if (sw == 4) {
       // two tiles share the activation prep where the register budget of an

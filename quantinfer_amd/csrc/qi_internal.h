@@ -34,8 +34,14 @@ struct GemvMfmaArgs {
   float* y;        // [m, n]
   int m;           // rows in this launch (<= compile-time tile)
   uint32_t chunk_units = 0;  // set by the launcher: K units whose activation digits fit LDS
+  const uint8_t* digits = nullptr;  // activation records from launch_gemv_digits (2+ rows), or null
 };
 bool gemv_mfma_supported(int32_t qtype, int32_t layout, uint64_t k);
+// Activation records of m rows (digits + window scales, the GEMV's LDS layout)
+// into `out` of gemv_digits_bytes(k, m) bytes.
+hipError_t launch_gemv_digits(int32_t qtype, const float* x, uint64_t k, uint32_t m, uint8_t* out,
+                              hipStream_t st);
+uint64_t gemv_digits_bytes(uint64_t k, uint32_t m);
 int gemv_mfma_split(uint64_t k, uint64_t n);
 hipError_t launch_gemv_mfma(int32_t qtype, bool wide, int mt, int split, const GemvMfmaArgs& a,
                             hipStream_t st);
