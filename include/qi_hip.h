@@ -161,6 +161,126 @@ qi_hip_status qi_hip_pack_weights(int32_t qtype, int32_t layout, uint64_t k, uin
                                   const void *blocks, uint64_t count, void *out, uint64_t *bytes,
                                   int32_t *f16_scales);
 
+/* ------------------------------------------------------------------------
+ * GPU-resident Qwen3 dense decoder.
+ *
+ * Replaces, for a model whose tensors live on the device: Qwen3Model::new /
+ * forward / forward_batch (crates/quantinfer-runtime/src/qwen3/mod.rs:211-378),
+ * KvCache (runtime/src/cache.rs:14-125) and generate_qwen3_stream with greedy
+ * selection (runtime/src/generation.rs:58-76, 160-201). The layer arithmetic is
+ * qwen3/mod.rs:117-208, attention.rs:7-141 and batch.rs:21-67; the element-wise
+ * operators are the KernelBackend methods rms_norm, rms_norm_heads, silu_mul,
+ * apply_rope and embedding (kernel lib.rs:142-153, cpu backend.rs:172-298).
+ * Weights, activations and the KV cache stay in device memory; a call moves
+ * only token ids (and, on request, the last row's logits) across PCIe.
+ * ------------------------------------------------------------------------ */
+
+/* The Qwen3Config fields the forward pass reads (crates/quantinfer-model/src/
+ * qwen3.rs:11-37; head_dim is effective_head_dim()). */
+typedef struct {
+  uint32_t vocab_size;
+  uint32_t hidden_size;
+  uint32_t intermediate_size;
+  uint32_t num_hidden_layers;
+  uint32_t num_attention_heads;
+  uint32_t num_key_value_heads;
+  uint32_t head_dim;
+  uint32_t max_position_embeddings;
+  float rms_norm_eps;
+  float rope_theta;
+} qi_hip_qwen3_config;
+
+/* One linear weight as the runtime holds it (LinearWeight, runtime/src/
+ * linear.rs:14-30): qtype/layout as for qi_hip_weights_create, `data` the
+ * logical blocks (or row-major f32 values for QI_HIP_F32), `count` the number
+ * of blocks (of floats for QI_HIP_F32). Logical shape [K, N] = [in, out]. */
+typedef struct {
+  int32_t qtype;
+  int32_t layout;
+  const void *data;
+  uint64_t count;
+} qi_hip_linear_weight;
+
+/* Qwen3LayerWeights (qwen3/mod.rs:10-22); norms are f32 host vectors. */
+typedef struct {
+  const float *input_layernorm;          /* [hidden] */
+  const float *q_norm;                   /* [head_dim] */
+  const float *k_norm;                   /* [head_dim] */
+  const float *post_attention_layernorm; /* [hidden] */
+  qi_hip_linear_weight q_proj;           /* [hidden, heads*head_dim] */
+  qi_hip_linear_weight k_proj;           /* [hidden, kv_heads*head_dim] */
+  qi_hip_linear_weight v_proj;           /* [hidden, kv_heads*head_dim] */
+  qi_hip_linear_weight o_proj;           /* [heads*head_dim, hidden] */
+  qi_hip_linear_weight gate_proj;        /* [hidden, intermediate] */
+  qi_hip_linear_weight up_proj;          /* [hidden, intermediate] */
+  qi_hip_linear_weight down_proj;        /* [intermediate, hidden] */
+} qi_hip_qwen3_layer;
+
+typedef struct qi_hip_qwen3 qi_hip_qwen3;
+typedef struct qi_hip_kv_cache qi_hip_kv_cache;
+
+/* Create an empty model on the context's device (Qwen3Model::new validation,
+ * qwen3/mod.rs:220-258 and Qwen3Config::validate). head_dim must be 64 or 128,
+ * hidden_size a multiple of 256. Every set_* call below must be made once
+ * before the first forward. */
+qi_hip_status qi_hip_qwen3_create(qi_hip_ctx *ctx, const qi_hip_qwen3_config *config,
+                                  qi_hip_qwen3 **out);
+/* embedding: f32 [vocab_size, hidden_size] row-major (the runtime's embedding
+ * Tensor). */
+qi_hip_status qi_hip_qwen3_set_embedding(qi_hip_qwen3 *model, const float *embedding);
+/* Layer `index`: q/k/v and gate/up are fused into one device image each, so
+ * each pair/triple must share qtype and layout. */
+qi_hip_status qi_hip_qwen3_set_layer(qi_hip_qwen3 *model, uint32_t index,
+                                     const qi_hip_qwen3_layer *layer);
+/* final_norm: f32 [hidden]; lm_head: [hidden, vocab] (a Q6_K output-rows head
+ * stays quantized on the device instead of being dequantized at load as
+ * runtime/src/qwen3/loader.rs:47-61 does). */
+qi_hip_status qi_hip_qwen3_set_output(qi_hip_qwen3 *model, const float *final_norm,
+                                      const qi_hip_linear_weight *lm_head);
+/* Arithmetic mode of every linear layer (QI_HIP_MODE_*; default AUTO: GEMV for
+ * decode, MFMA GEMM for prompt chunks of 128+ tokens). */
+qi_hip_status qi_hip_qwen3_set_mode(qi_hip_qwen3 *model, int32_t mode);
+void qi_hip_qwen3_free(qi_hip_qwen3 *model);
+
+/* KvCache::new(num_layers, max_sequence_length, num_key_value_heads, head_dim)
+ * (cache.rs:25-60), in device memory. */
+qi_hip_status qi_hip_kv_cache_create(qi_hip_ctx *ctx, uint32_t num_layers,
+                                     uint32_t max_sequence_length, uint32_t num_key_value_heads,
+                                     uint32_t head_dim, qi_hip_kv_cache **out);
+qi_hip_status qi_hip_kv_cache_length(const qi_hip_kv_cache *cache, uint64_t *out);
+/* Forget every cached position (a fresh KvCache of the same shape). */
+qi_hip_status qi_hip_kv_cache_reset(qi_hip_kv_cache *cache);
+void qi_hip_kv_cache_free(qi_hip_kv_cache *cache);
+
+/* Qwen3Model::forward(token_ids, cache) (qwen3/mod.rs:260-263, 297-335): runs
+ * the tokens at the next cache positions and appends their keys/values.
+ * Writes the LAST token's logits to `last_logits` ([vocab], host, may be NULL)
+ * and their argmax (generation.rs:58-76) to `next_token` (may be NULL); the
+ * rows before the last are not projected to logits. */
+qi_hip_status qi_hip_qwen3_forward(qi_hip_qwen3 *model, qi_hip_kv_cache *cache,
+                                   const int32_t *tokens, uint64_t count, float *last_logits,
+                                   int32_t *next_token);
+
+/* generate_qwen3_stream with temperature 0 (generation.rs:160-201): forward the
+ * prompt, then repeatedly select the argmax and forward it, up to
+ * max_new_tokens or until eos_token_id (< 0: none) is selected. Writes the
+ * selected ids to out_tokens and their number to *out_count. Decode steps run
+ * as one replayed HIP graph per token. */
+qi_hip_status qi_hip_qwen3_generate(qi_hip_qwen3 *model, qi_hip_kv_cache *cache,
+                                    const int32_t *prompt, uint64_t prompt_count,
+                                    uint64_t max_new_tokens, int32_t eos_token_id,
+                                    int32_t *out_tokens, uint64_t *out_count);
+
+/* Device time of the last qi_hip_qwen3_generate on this model, from HIP events
+ * on the context stream: the prompt forward and the decode steps. */
+typedef struct {
+  double prefill_ms;
+  double decode_ms;
+  uint64_t prompt_tokens;
+  uint64_t decode_steps;
+} qi_hip_qwen3_timing;
+qi_hip_status qi_hip_qwen3_last_timing(const qi_hip_qwen3 *model, qi_hip_qwen3_timing *out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -113,6 +113,52 @@ int qo_wire_unpack(int qtype, const uint8_t *bytes, size_t count, int legacy, vo
 void qo_fill_normal(uint64_t seed, size_t n, double std, double outlier_rate,
                     double outlier_std, float *out);
 
+/* ---- Qwen3 dense decoder (oracle/qwen3.c; runtime/src/qwen3/mod.rs,
+ * attention.rs, batch.rs, cache.rs, generation.rs, cpu backend.rs:172-298) ---- */
+int qo_rms_norm(const float *x, size_t rows, size_t dim, const float *w, float eps, float *out);
+int qo_softmax(const float *x, size_t rows, size_t dim, float *out);
+int qo_silu_mul(const float *gate, const float *up, size_t n, float *out);
+int qo_rope_tables(float theta, size_t head_dim, size_t start, size_t length, float *cos_out,
+                   float *sin_out);
+int qo_apply_rope(const float *x, size_t tokens, size_t heads, size_t head_dim,
+                  const float *cos_t, const float *sin_t, size_t table_rows, float *out);
+int qo_embedding(const float *table, size_t vocab, size_t hidden, const int32_t *tokens, size_t n,
+                 float *out);
+int qo_gqa_attention(const float *q, size_t q_tokens, size_t q_heads, size_t kv_heads,
+                     size_t head_dim, const float *keys, const float *values, size_t key_tokens,
+                     size_t start, float *out);
+int qo_argmax(const float *logits, size_t n, int32_t *out);
+/* y[m][n] = sum_k x[m][k] w[n][k], the CpuScalar per-output sequence, outputs
+ * split over `threads` OpenMP threads (bit-identical to one thread). */
+int qo_linear_rows(const float *x, size_t m, size_t k, const float *w, size_t n, float *y,
+                   int threads);
+
+typedef struct {
+  uint32_t vocab, hidden, intermediate, layers, heads, kv_heads, head_dim, max_positions;
+  float eps, theta;
+} qo_qwen3_config;
+
+/* Projections are dequantized f32 output rows w[n][k]: q [heads*hd][hidden],
+ * k and v [kv_heads*hd][hidden], o [hidden][heads*hd], gate and up
+ * [intermediate][hidden], down [hidden][intermediate]. Norms are f32 vectors.
+ * The model borrows every pointer. */
+typedef struct {
+  const float *input_norm, *q, *k, *v, *q_norm, *k_norm, *o, *post_norm, *gate, *up, *down;
+} qo_qwen3_layer;
+
+typedef struct qo_qwen3 qo_qwen3;
+/* embedding [vocab][hidden]; head [vocab][hidden] (output rows); capacity =
+ * KV cache positions. */
+qo_qwen3 *qo_qwen3_new(const qo_qwen3_config *cfg, const float *embedding,
+                       const qo_qwen3_layer *layers, const float *final_norm, const float *head,
+                       size_t capacity, int threads);
+void qo_qwen3_free(qo_qwen3 *m);
+size_t qo_qwen3_length(const qo_qwen3 *m);
+void qo_qwen3_reset(qo_qwen3 *m);
+int qo_qwen3_forward(qo_qwen3 *m, const int32_t *tokens, size_t n, int last_only, float *logits);
+int qo_qwen3_generate(qo_qwen3 *m, const int32_t *prompt, size_t n, size_t max_new, int32_t eos,
+                      int32_t *out, size_t *count);
+
 #ifdef __cplusplus
 }
 #endif

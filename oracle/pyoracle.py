@@ -87,6 +87,25 @@ def _declare(l: ctypes.CDLL) -> None:
     l.qo_fill_normal.argtypes = [ctypes.c_uint64, sz, ctypes.c_double, ctypes.c_double,
                                  ctypes.c_double, fp]
     l.qo_fill_normal.restype = None
+    l.qo_rms_norm.argtypes = [fp, sz, sz, fp, ctypes.c_float, fp]
+    l.qo_softmax.argtypes = [fp, sz, sz, fp]
+    l.qo_silu_mul.argtypes = [fp, fp, sz, fp]
+    l.qo_rope_tables.argtypes = [ctypes.c_float, sz, sz, sz, fp, fp]
+    l.qo_apply_rope.argtypes = [fp, sz, sz, sz, fp, fp, sz, fp]
+    l.qo_embedding.argtypes = [fp, sz, sz, vp, sz, fp]
+    l.qo_gqa_attention.argtypes = [fp, sz, sz, sz, sz, fp, fp, sz, sz, fp]
+    l.qo_argmax.argtypes = [fp, sz, vp]
+    l.qo_linear_rows.argtypes = [fp, sz, sz, fp, sz, fp, i32]
+    l.qo_qwen3_new.argtypes = [vp, fp, vp, fp, fp, sz, i32]
+    l.qo_qwen3_new.restype = vp
+    l.qo_qwen3_free.argtypes = [vp]
+    l.qo_qwen3_free.restype = None
+    l.qo_qwen3_length.argtypes = [vp]
+    l.qo_qwen3_length.restype = sz
+    l.qo_qwen3_reset.argtypes = [vp]
+    l.qo_qwen3_reset.restype = None
+    l.qo_qwen3_forward.argtypes = [vp, vp, sz, i32, fp]
+    l.qo_qwen3_generate.argtypes = [vp, vp, sz, sz, ctypes.c_int32, vp, ctypes.POINTER(sz)]
 
 
 def _ptr(a: np.ndarray) -> int:
@@ -246,3 +265,157 @@ def make_weights(qtype: int, k: int, n: int, seed: int, storage_f16: bool = True
     if storage_f16:
         blocks = storage_precision(qtype, blocks)
     return blocks
+
+
+# ------------------------------------------------------- Qwen3 decoder
+
+def _f32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def rms_norm(x, w, eps: float) -> np.ndarray:
+    x = _f32(x)
+    w = _f32(w)
+    out = np.empty_like(x)
+    dim = w.size
+    _check(lib().qo_rms_norm(_ptr(x), x.size // dim, dim, _ptr(w), eps, _ptr(out)), "rms_norm")
+    return out
+
+
+def softmax(x) -> np.ndarray:
+    x = _f32(x)
+    out = np.empty_like(x)
+    _check(lib().qo_softmax(_ptr(x), x.size // x.shape[-1], x.shape[-1], _ptr(out)), "softmax")
+    return out
+
+
+def silu_mul(g, u) -> np.ndarray:
+    g, u = _f32(g), _f32(u)
+    out = np.empty_like(g)
+    _check(lib().qo_silu_mul(_ptr(g), _ptr(u), g.size, _ptr(out)), "silu_mul")
+    return out
+
+
+def rope_tables(theta: float, head_dim: int, start: int, length: int):
+    c = np.empty((length, head_dim // 2), dtype=np.float32)
+    s = np.empty_like(c)
+    _check(lib().qo_rope_tables(theta, head_dim, start, length, _ptr(c), _ptr(s)), "rope_tables")
+    return c, s
+
+
+def apply_rope(x, cos, sin) -> np.ndarray:
+    """x [tokens, heads, head_dim]; tables [1 or tokens, head_dim/2]."""
+    x, cos, sin = _f32(x), _f32(cos), _f32(sin)
+    t, h, d = x.shape
+    rows = cos.size // (d // 2)
+    out = np.empty_like(x)
+    _check(lib().qo_apply_rope(_ptr(x), t, h, d, _ptr(cos), _ptr(sin), rows, _ptr(out)),
+           "apply_rope")
+    return out
+
+
+def embedding(table, tokens) -> np.ndarray:
+    table = _f32(table)
+    tok = np.ascontiguousarray(tokens, dtype=np.int32)
+    out = np.empty((tok.size, table.shape[1]), dtype=np.float32)
+    _check(lib().qo_embedding(_ptr(table), table.shape[0], table.shape[1], _ptr(tok), tok.size,
+                              _ptr(out)), "embedding")
+    return out
+
+
+def gqa_attention(q, keys, values, start: int) -> np.ndarray:
+    """q [tq, heads, hd]; keys/values [tk, kv_heads, hd]."""
+    q, keys, values = _f32(q), _f32(keys), _f32(values)
+    tq, hq, hd = q.shape
+    tk, hk, _ = keys.shape
+    out = np.empty_like(q)
+    _check(lib().qo_gqa_attention(_ptr(q), tq, hq, hk, hd, _ptr(keys), _ptr(values), tk, start,
+                                  _ptr(out)), "gqa_attention")
+    return out
+
+
+def argmax(logits) -> int:
+    x = _f32(logits)
+    out = np.zeros(1, dtype=np.int32)
+    _check(lib().qo_argmax(_ptr(x), x.size, _ptr(out)), "argmax")
+    return int(out[0])
+
+
+def linear_rows(x, w, threads: int = 1) -> np.ndarray:
+    """y[m, n] = sum_k x[m, k] w[n, k] in the CpuScalar per-output order."""
+    x, w = _f32(x), _f32(w)
+    m, k = x.shape
+    n = w.shape[0]
+    y = np.empty((m, n), dtype=np.float32)
+    _check(lib().qo_linear_rows(_ptr(x), m, k, _ptr(w), n, _ptr(y), threads), "linear_rows")
+    return y
+
+
+class Qwen3Config(ctypes.Structure):
+    """The Qwen3Config fields the forward pass reads (quantinfer-model qwen3.rs:11-37)."""
+    _fields_ = [("vocab", ctypes.c_uint32), ("hidden", ctypes.c_uint32),
+                ("intermediate", ctypes.c_uint32), ("layers", ctypes.c_uint32),
+                ("heads", ctypes.c_uint32), ("kv_heads", ctypes.c_uint32),
+                ("head_dim", ctypes.c_uint32), ("max_positions", ctypes.c_uint32),
+                ("eps", ctypes.c_float), ("theta", ctypes.c_float)]
+
+
+LAYER_FIELDS = ("input_norm", "q", "k", "v", "q_norm", "k_norm", "o", "post_norm", "gate",
+                "up", "down")
+
+
+class _Layer(ctypes.Structure):
+    _fields_ = [(f, ctypes.c_void_p) for f in LAYER_FIELDS]
+
+
+class Qwen3:
+    """The oracle decoder. `layers` is a list of dicts of f32 arrays keyed by
+    LAYER_FIELDS (projections as dequantized output rows [n, k]); `head` is
+    [vocab, hidden] output rows. Arrays are kept alive by this object."""
+
+    def __init__(self, cfg: dict, embedding, layers, final_norm, head, capacity: int,
+                 threads: int = 1):
+        self.cfg = Qwen3Config(**cfg)
+        self._keep = [_f32(embedding), _f32(final_norm), _f32(head)]
+        lay = (_Layer * len(layers))()
+        for i, d in enumerate(layers):
+            for f in LAYER_FIELDS:
+                a = _f32(d[f])
+                self._keep.append(a)
+                setattr(lay[i], f, a.ctypes.data)
+        self._layers = lay
+        self.vocab = cfg["vocab"]
+        h = lib().qo_qwen3_new(ctypes.byref(self.cfg), _ptr(self._keep[0]), lay,
+                               _ptr(self._keep[1]), _ptr(self._keep[2]), capacity, threads)
+        if not h:
+            raise OracleError("qo_qwen3_new rejected its configuration")
+        self._h = h
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h:
+            lib().qo_qwen3_free(h)
+            self._h = None
+
+    @property
+    def length(self) -> int:
+        return int(lib().qo_qwen3_length(self._h))
+
+    def reset(self) -> None:
+        lib().qo_qwen3_reset(self._h)
+
+    def forward(self, tokens, last_only: bool = False) -> np.ndarray:
+        tok = np.ascontiguousarray(tokens, dtype=np.int32)
+        rows = 1 if last_only else tok.size
+        out = np.empty((rows, self.vocab), dtype=np.float32)
+        _check(lib().qo_qwen3_forward(self._h, _ptr(tok), tok.size, int(last_only), _ptr(out)),
+               "qwen3_forward")
+        return out
+
+    def generate(self, prompt, max_new: int, eos: int = -1) -> list:
+        tok = np.ascontiguousarray(prompt, dtype=np.int32)
+        out = np.zeros(max(max_new, 1), dtype=np.int32)
+        count = ctypes.c_size_t(0)
+        _check(lib().qo_qwen3_generate(self._h, _ptr(tok), tok.size, max_new, eos, _ptr(out),
+                                       ctypes.byref(count)), "qwen3_generate")
+        return [int(t) for t in out[:count.value]]

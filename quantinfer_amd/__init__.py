@@ -48,6 +48,36 @@ class WeightsInfo(ctypes.Structure):
                 ("f16_scales", ctypes.c_int32)]
 
 
+class Qwen3Config(ctypes.Structure):
+    """qi_hip_qwen3_config (the Qwen3Config fields the forward pass reads)."""
+    _fields_ = [("vocab_size", ctypes.c_uint32), ("hidden_size", ctypes.c_uint32),
+                ("intermediate_size", ctypes.c_uint32), ("num_hidden_layers", ctypes.c_uint32),
+                ("num_attention_heads", ctypes.c_uint32), ("num_key_value_heads", ctypes.c_uint32),
+                ("head_dim", ctypes.c_uint32), ("max_position_embeddings", ctypes.c_uint32),
+                ("rms_norm_eps", ctypes.c_float), ("rope_theta", ctypes.c_float)]
+
+
+class LinearWeight(ctypes.Structure):
+    """qi_hip_linear_weight: logical blocks of one projection."""
+    _fields_ = [("qtype", ctypes.c_int32), ("layout", ctypes.c_int32), ("data", ctypes.c_void_p),
+                ("count", ctypes.c_uint64)]
+
+
+PROJECTIONS = ("q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj", "down_proj")
+LAYER_NORMS = ("input_layernorm", "q_norm", "k_norm", "post_attention_layernorm")
+
+
+class Qwen3Layer(ctypes.Structure):
+    """qi_hip_qwen3_layer (Qwen3LayerWeights)."""
+    _fields_ = ([(n, ctypes.c_void_p) for n in LAYER_NORMS] +
+                [(p, LinearWeight) for p in PROJECTIONS])
+
+
+class Qwen3Timing(ctypes.Structure):
+    _fields_ = [("prefill_ms", ctypes.c_double), ("decode_ms", ctypes.c_double),
+                ("prompt_tokens", ctypes.c_uint64), ("decode_steps", ctypes.c_uint64)]
+
+
 _lib = None
 
 
@@ -76,9 +106,29 @@ def lib() -> ctypes.CDLL:
         l.qi_hip_dequantize_device.argtypes = [vp, vp, vp, vp]
         l.qi_hip_pack_weights.argtypes = [i32, i32, u64, u64, vp, u64, vp,
                                           ctypes.POINTER(u64), ctypes.POINTER(i32)]
+        u32 = ctypes.c_uint32
+        l.qi_hip_qwen3_create.argtypes = [vp, ctypes.POINTER(Qwen3Config), ctypes.POINTER(vp)]
+        l.qi_hip_qwen3_set_embedding.argtypes = [vp, vp]
+        l.qi_hip_qwen3_set_layer.argtypes = [vp, u32, ctypes.POINTER(Qwen3Layer)]
+        l.qi_hip_qwen3_set_output.argtypes = [vp, vp, ctypes.POINTER(LinearWeight)]
+        l.qi_hip_qwen3_set_mode.argtypes = [vp, i32]
+        l.qi_hip_qwen3_free.argtypes = [vp]
+        l.qi_hip_qwen3_free.restype = None
+        l.qi_hip_kv_cache_create.argtypes = [vp, u32, u32, u32, u32, ctypes.POINTER(vp)]
+        l.qi_hip_kv_cache_length.argtypes = [vp, ctypes.POINTER(u64)]
+        l.qi_hip_kv_cache_reset.argtypes = [vp]
+        l.qi_hip_kv_cache_free.argtypes = [vp]
+        l.qi_hip_kv_cache_free.restype = None
+        l.qi_hip_qwen3_forward.argtypes = [vp, vp, vp, u64, vp, vp]
+        l.qi_hip_qwen3_generate.argtypes = [vp, vp, vp, u64, u64, i32, vp, ctypes.POINTER(u64)]
+        l.qi_hip_qwen3_last_timing.argtypes = [vp, ctypes.POINTER(Qwen3Timing)]
         for name in ("qi_hip_open", "qi_hip_device_name", "qi_hip_weights_create",
                      "qi_hip_weights_info_get", "qi_hip_linear", "qi_hip_linear_device",
-                     "qi_hip_dequantize", "qi_hip_dequantize_device", "qi_hip_pack_weights"):
+                     "qi_hip_dequantize", "qi_hip_dequantize_device", "qi_hip_pack_weights",
+                     "qi_hip_qwen3_create", "qi_hip_qwen3_set_embedding", "qi_hip_qwen3_set_layer",
+                     "qi_hip_qwen3_set_output", "qi_hip_qwen3_set_mode", "qi_hip_kv_cache_create",
+                     "qi_hip_kv_cache_length", "qi_hip_kv_cache_reset", "qi_hip_qwen3_forward",
+                     "qi_hip_qwen3_generate", "qi_hip_qwen3_last_timing"):
             getattr(l, name).restype = i32
         if l.qi_hip_abi_version() != 1:
             raise RuntimeError("libqi_hip.so ABI version mismatch")
@@ -185,3 +235,116 @@ class Weights:
     def dequantize_device(self, out_ptr: int, stream: int = 0) -> None:
         _check(lib().qi_hip_dequantize_device(self.ctx.handle, self.handle, out_ptr,
                                               stream or None))
+
+
+def _linear_weight(qtype: int, layout: int, data: np.ndarray, keep: list) -> LinearWeight:
+    d = np.ascontiguousarray(data)
+    keep.append(d)
+    return LinearWeight(qtype, layout, d.ctypes.data, d.size)
+
+
+class KvCache:
+    """A device KV cache (qi_hip_kv_cache_create; KvCache::new)."""
+
+    def __init__(self, ctx: Context, layers: int, max_sequence_length: int, kv_heads: int,
+                 head_dim: int):
+        h = ctypes.c_void_p()
+        _check(lib().qi_hip_kv_cache_create(ctx.handle, layers, max_sequence_length, kv_heads,
+                                            head_dim, ctypes.byref(h)))
+        self.ctx, self.handle = ctx, h
+
+    @property
+    def length(self) -> int:
+        out = ctypes.c_uint64(0)
+        _check(lib().qi_hip_kv_cache_length(self.handle, ctypes.byref(out)))
+        return out.value
+
+    def reset(self) -> None:
+        _check(lib().qi_hip_kv_cache_reset(self.handle))
+
+    def free(self) -> None:
+        if self.handle:
+            lib().qi_hip_kv_cache_free(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class Qwen3:
+    """A GPU-resident Qwen3 decoder (qi_hip_qwen3_*). `cfg` holds the
+    qi_hip_qwen3_config fields; weights are given per layer as dicts with the
+    four norms (f32 arrays) and the seven projections as (qtype, layout,
+    blocks) triples of logical blocks."""
+
+    def __init__(self, ctx: Context, cfg: dict):
+        self.cfg = dict(cfg)
+        c = Qwen3Config(**cfg)
+        h = ctypes.c_void_p()
+        _check(lib().qi_hip_qwen3_create(ctx.handle, ctypes.byref(c), ctypes.byref(h)))
+        self.ctx, self.handle = ctx, h
+
+    def set_embedding(self, table: np.ndarray) -> None:
+        t = np.ascontiguousarray(table, dtype=np.float32)
+        _check(lib().qi_hip_qwen3_set_embedding(self.handle, _ptr(t)))
+
+    def set_layer(self, index: int, layer: dict) -> None:
+        keep = []
+        s = Qwen3Layer()
+        for n in LAYER_NORMS:
+            a = np.ascontiguousarray(layer[n], dtype=np.float32)
+            keep.append(a)
+            setattr(s, n, a.ctypes.data)
+        for p in PROJECTIONS:
+            qtype, layout, blocks = layer[p]
+            setattr(s, p, _linear_weight(qtype, layout, blocks, keep))
+        _check(lib().qi_hip_qwen3_set_layer(self.handle, index, ctypes.byref(s)))
+
+    def set_output(self, final_norm: np.ndarray, head) -> None:
+        keep = []
+        fn = np.ascontiguousarray(final_norm, dtype=np.float32)
+        hw = _linear_weight(*head, keep)
+        _check(lib().qi_hip_qwen3_set_output(self.handle, _ptr(fn), ctypes.byref(hw)))
+
+    def set_mode(self, mode: int) -> None:
+        _check(lib().qi_hip_qwen3_set_mode(self.handle, mode))
+
+    def kv_cache(self, max_sequence_length: int) -> KvCache:
+        return KvCache(self.ctx, self.cfg["num_hidden_layers"], max_sequence_length,
+                       self.cfg["num_key_value_heads"], self.cfg["head_dim"])
+
+    def forward(self, cache: KvCache, tokens, logits: bool = True):
+        """Returns (last-row logits or None, argmax token)."""
+        tok = np.ascontiguousarray(tokens, dtype=np.int32)
+        out = np.empty(self.cfg["vocab_size"], dtype=np.float32) if logits else None
+        nxt = ctypes.c_int32(0)
+        _check(lib().qi_hip_qwen3_forward(self.handle, cache.handle, _ptr(tok), tok.size,
+                                          _ptr(out) if logits else None, ctypes.byref(nxt)))
+        return out, nxt.value
+
+    def generate(self, cache: KvCache, prompt, max_new_tokens: int, eos: int = -1) -> list:
+        tok = np.ascontiguousarray(prompt, dtype=np.int32)
+        out = np.zeros(max(max_new_tokens, 1), dtype=np.int32)
+        count = ctypes.c_uint64(0)
+        _check(lib().qi_hip_qwen3_generate(self.handle, cache.handle, _ptr(tok), tok.size,
+                                           max_new_tokens, eos, _ptr(out), ctypes.byref(count)))
+        return [int(t) for t in out[:count.value]]
+
+    def last_timing(self) -> Qwen3Timing:
+        t = Qwen3Timing()
+        _check(lib().qi_hip_qwen3_last_timing(self.handle, ctypes.byref(t)))
+        return t
+
+    def free(self) -> None:
+        if self.handle:
+            lib().qi_hip_qwen3_free(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass

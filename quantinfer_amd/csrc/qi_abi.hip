@@ -17,43 +17,14 @@
 #include "../../include/qi_hip.h"
 #include "qi_image.h"
 #include "qi_internal.h"
+#include "qi_ctx.h"
 
 using qi::Image;
 
-// A context is reference counted: the caller's handle and every live weights
-// handle hold one reference, so qi_hip_close and qi_hip_weights_free may come
-// in any order; the stream and workspace go away with the last reference.
-struct qi_hip_ctx {
-  std::atomic<int> refs{1};
-  bool closed = false;
-  int device = 0;
-  hipStream_t stream = nullptr;
-  std::mutex mu;
-  std::string name;
-  float* partials = nullptr;
-  uint64_t partials_cap = 0;  // floats
-  uint32_t* tickets = nullptr;
-  uint64_t tickets_cap = 0;
-  float* xbuf = nullptr;
-  uint64_t xcap = 0;  // floats
-  float* ybuf = nullptr;
-  uint64_t ycap = 0;
-  float* hbuf = nullptr;  // f16 activations of the prefill GEMM (capacity in floats)
-  uint64_t hcap = 0;
-  float* dbuf = nullptr;  // activation records of the decode GEMV, 2+ rows (capacity in floats)
-  uint64_t dcap = 0;
-  int gemv_split = 0;  // QI_HIP_GEMV_SPLIT tuning override (wavefronts per GEMV workgroup: 4 or 8)
-};
-
-struct qi_hip_weights {
-  qi_hip_ctx* ctx = nullptr;
-  Image im;
-  void* dev = nullptr;
-};
-
-namespace {
+namespace qi_abi {
 
 thread_local std::string g_last_error;
+std::atomic<uint64_t> g_ws_version{0};
 
 qi_hip_status fail(qi_hip_status st, const std::string& msg) {
   g_last_error = msg;
@@ -64,17 +35,15 @@ qi_hip_status hip_fail(hipError_t e, const char* what) {
   return fail(QI_HIP_RUNTIME_ERROR, std::string("HIP ") + what + ": " + hipGetErrorString(e));
 }
 
-#define QI_HIP_TRY(expr, what)                  \
-  do {                                          \
-    hipError_t e_ = (expr);                     \
-    if (e_ != hipSuccess) return hip_fail(e_, what); \
-  } while (0)
 
 constexpr uint64_t kPartialsFloats = 8ull << 20;  // 32 MiB of split-K partials
 constexpr uint64_t kTickets = 1ull << 20;
 
+uint64_t workspace_version() { return g_ws_version.load(std::memory_order_relaxed); }
+
 qi_hip_status grow(float** buf, uint64_t* cap, uint64_t need, const char* what) {
   if (need <= *cap) return QI_HIP_OK;
+  ++g_ws_version;
   if (*buf) (void)hipFree(*buf);
   *buf = nullptr;
   *cap = 0;
@@ -197,7 +166,42 @@ qi_hip_status run_linear(qi_hip_ctx* c, const qi_hip_weights* w, const float* x,
   return QI_HIP_OK;
 }
 
-}  // namespace
+qi_hip_status create_weights_locked(qi_hip_ctx* c, const Image& im, const void* blocks,
+                                    qi_hip_weights** out) {
+  QI_HIP_TRY(hipSetDevice(c->device), "set device");
+  void* host = nullptr;
+  QI_HIP_TRY(hipHostMalloc(&host, im.bytes, hipHostMallocDefault), "pinned staging");
+  qi::fill_image(im, blocks, host);
+  void* dev = nullptr;
+  hipError_t e = hipMalloc(&dev, im.bytes);
+  if (e == hipSuccess) e = hipMemcpyAsync(dev, host, im.bytes, hipMemcpyHostToDevice, c->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+  (void)hipHostFree(host);
+  if (e != hipSuccess) {
+    if (dev) (void)hipFree(dev);
+    return hip_fail(e, "upload weights");
+  }
+  qi_hip_weights* w = new qi_hip_weights();
+  c->refs.fetch_add(1, std::memory_order_relaxed);
+  w->ctx = c;
+  w->im = im;
+  w->dev = dev;
+  *out = w;
+  return QI_HIP_OK;
+}
+
+void free_weights_locked(qi_hip_weights* w) {
+  if (w == nullptr) return;
+  (void)hipSetDevice(w->ctx->device);
+  (void)hipStreamSynchronize(w->ctx->stream);
+  if (w->dev) (void)hipFree(w->dev);
+  w->ctx->refs.fetch_sub(1, std::memory_order_acq_rel);  // the caller still holds its own reference
+  delete w;
+}
+
+}  // namespace qi_abi
+
+using namespace qi_abi;
 
 extern "C" {
 
@@ -288,26 +292,7 @@ qi_hip_status qi_hip_weights_create(qi_hip_ctx* c, int32_t qtype, int32_t layout
   qi_hip_status s = qi::plan_image(qtype, layout, k, n, blocks, count, &im, &why);
   if (s != QI_HIP_OK) return fail(s, why);
   std::lock_guard<std::mutex> lock(c->mu);
-  QI_HIP_TRY(hipSetDevice(c->device), "set device");
-  void* host = nullptr;
-  QI_HIP_TRY(hipHostMalloc(&host, im.bytes, hipHostMallocDefault), "pinned staging");
-  qi::fill_image(im, blocks, host);
-  void* dev = nullptr;
-  hipError_t e = hipMalloc(&dev, im.bytes);
-  if (e == hipSuccess) e = hipMemcpyAsync(dev, host, im.bytes, hipMemcpyHostToDevice, c->stream);
-  if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
-  (void)hipHostFree(host);
-  if (e != hipSuccess) {
-    if (dev) (void)hipFree(dev);
-    return hip_fail(e, "upload weights");
-  }
-  qi_hip_weights* w = new qi_hip_weights();
-  c->refs.fetch_add(1, std::memory_order_relaxed);
-  w->ctx = c;
-  w->im = im;
-  w->dev = dev;
-  *out = w;
-  return QI_HIP_OK;
+  return create_weights_locked(c, im, blocks, out);
 }
 
 void qi_hip_weights_free(qi_hip_weights* w) {

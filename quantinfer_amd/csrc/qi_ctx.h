@@ -1,0 +1,74 @@
+// Internal: the context and weights handles behind include/qi_hip.h, shared by
+// the C ABI (qi_abi.hip) and the Qwen3 decoder (qi_qwen3.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <atomic>
+#include <mutex>
+#include <string>
+
+#include "../../include/qi_hip.h"
+#include "qi_image.h"
+
+// A context is reference counted: the caller's handle and every live weights
+// handle hold one reference, so qi_hip_close and qi_hip_weights_free may come
+// in any order; the stream and workspace go away with the last reference.
+struct qi_hip_ctx {
+  std::atomic<int> refs{1};
+  bool closed = false;
+  int device = 0;
+  hipStream_t stream = nullptr;
+  std::mutex mu;
+  std::string name;
+  float* partials = nullptr;
+  uint64_t partials_cap = 0;  // floats
+  uint32_t* tickets = nullptr;
+  uint64_t tickets_cap = 0;
+  float* xbuf = nullptr;
+  uint64_t xcap = 0;  // floats
+  float* ybuf = nullptr;
+  uint64_t ycap = 0;
+  float* hbuf = nullptr;  // f16 activations of the prefill GEMM (capacity in floats)
+  uint64_t hcap = 0;
+  float* dbuf = nullptr;  // activation records of the decode GEMV, 2+ rows (capacity in floats)
+  uint64_t dcap = 0;
+  int gemv_split = 0;  // QI_HIP_GEMV_SPLIT tuning override (wavefronts per GEMV workgroup: 4 or 8)
+};
+
+struct qi_hip_weights {
+  qi_hip_ctx* ctx = nullptr;
+  qi::Image im;
+  void* dev = nullptr;
+};
+
+namespace qi_abi {
+
+// Set the calling thread's last error and return `st`.
+qi_hip_status fail(qi_hip_status st, const std::string& msg);
+qi_hip_status hip_fail(hipError_t e, const char* what);
+// Grow-only device buffer (capacity in floats); the caller synchronizes first
+// when queued work may still read the old buffer.
+qi_hip_status grow(float** buf, uint64_t* cap, uint64_t need, const char* what);
+// One linear layer on device buffers, no locking (the caller holds c->mu).
+qi_hip_status run_linear(qi_hip_ctx* c, const qi_hip_weights* w, const float* x, uint64_t m,
+                         float* y, int32_t mode, hipStream_t st);
+// Upload a planned image; the caller holds c->mu. The handle holds a context
+// reference, as one made by qi_hip_weights_create.
+qi_hip_status create_weights_locked(qi_hip_ctx* c, const qi::Image& im, const void* blocks,
+                                    qi_hip_weights** out);
+// Free a handle made by create_weights_locked while holding c->mu (the caller
+// keeps its own context reference, so the context cannot go away here).
+void free_weights_locked(qi_hip_weights* w);
+void ctx_release(qi_hip_ctx* c);
+// Number of workspace reallocations so far (any context): a captured graph
+// that reads a workspace is stale once this changes.
+uint64_t workspace_version();
+
+}  // namespace qi_abi
+
+#define QI_HIP_TRY(expr, what)                                   \
+  do {                                                           \
+    hipError_t e_ = (expr);                                      \
+    if (e_ != hipSuccess) return qi_abi::hip_fail(e_, what);     \
+  } while (0)

@@ -1,0 +1,1192 @@
+// GPU-resident Qwen3 dense decoder (include/qi_hip.h, "GPU-resident Qwen3").
+//
+// The forward pass of crates/quantinfer-runtime/src/qwen3/mod.rs:117-378 with
+// weights, activations and the KV cache in device memory:
+//
+//   embedding + RMSNorm           residual_norm_kernel<EMBED>
+//   q|k|v projection              one fused GEMV/GEMM image (qi_gemv_mfma / qi_gemm)
+//   q_norm/k_norm, RoPE, KV append qk_norm_rope_kernel
+//   GQA attention                 attn_partial_kernel (64 positions per wavefront)
+//                                 + attn_combine_kernel
+//   o projection                  GEMV/GEMM
+//   residual + RMSNorm            residual_norm_kernel<ADD>
+//   gate|up projection            one fused image
+//   SiLU(gate) * up               silu_mul_kernel
+//   down projection               GEMV/GEMM
+//   residual + next RMSNorm       residual_norm_kernel<ADD> (the final norm after the last layer)
+//   LM head on the last row       GEMV (a Q6_K head stays quantized)
+//   greedy argmax                 argmax_partial_kernel + argmax_final_kernel
+//
+// Position bookkeeping lives on the device: the cache holds the token history
+// (tok[p] = token at position p) and the current length. Every kernel reads
+// the length from device memory, and the last kernel of a step writes the
+// selected token at tok[len + rows] and advances the length. A decode step
+// therefore has fixed launch arguments and is captured once as a HIP graph and
+// replayed for every generated token.
+//
+// KV cache layout per layer (positions rounded up to 64):
+//   keys   [kv_head][dim][position]  - lanes of a wavefront read 64 consecutive
+//                                      positions of one dimension (256 B)
+//   values [kv_head][position][dim]  - lanes read one position's dimensions
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <atomic>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "qi_ctx.h"
+#include "qi_internal.h"
+
+using qi_abi::fail;
+using qi_abi::hip_fail;
+
+namespace {
+
+constexpr uint32_t kChunk = 64;       // attention positions per wavefront
+constexpr uint32_t kMaxRows = 512;    // prompt tokens per forward chunk
+constexpr uint32_t kArgBlocks = 256;  // argmax partial blocks
+constexpr uint64_t kPartialBudget = 64ull << 20;  // bytes of attention partials per row batch
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  return __shfl(v, 0);  // one value for every lane
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+  return __shfl(v, 0);
+}
+
+// ---------------------------------------------------------------- RMSNorm
+// backends/cpu/src/backend.rs:172-190: out = v * (1/sqrt(mean(v^2) + eps)) * w.
+// EMBED: h = embedding[tok[len + row]] (backend.rs:281-298). ADD: h = h + y
+// (runtime/src/linear.rs:129-142). Then x = RMSNorm(h) * w.
+template <bool EMBED>
+__global__ __launch_bounds__(256) void residual_norm_kernel(
+    float* __restrict__ h, const float* __restrict__ y, const float* __restrict__ table,
+    const int32_t* __restrict__ tok, const uint32_t* __restrict__ len, float* __restrict__ x,
+    const float* __restrict__ w, uint32_t hidden, float eps) {
+  __shared__ float red[4];
+  const uint32_t r = blockIdx.x;
+  const uint32_t n4 = hidden / 4;
+  float4* hr = reinterpret_cast<float4*>(h + static_cast<uint64_t>(r) * hidden);
+  const float4* src;
+  if constexpr (EMBED) {
+    const int32_t t = tok[*len + r];
+    src = reinterpret_cast<const float4*>(table + static_cast<uint64_t>(t) * hidden);
+  } else {
+    src = reinterpret_cast<const float4*>(y + static_cast<uint64_t>(r) * hidden);
+  }
+  float ss = 0.0f;
+  for (uint32_t i = threadIdx.x; i < n4; i += 256) {
+    float4 v = src[i];
+    if constexpr (!EMBED) {
+      const float4 o = hr[i];
+      v.x = o.x + v.x;
+      v.y = o.y + v.y;
+      v.z = o.z + v.z;
+      v.w = o.w + v.w;
+    }
+    hr[i] = v;
+    ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+  }
+  ss = wave_sum(ss);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  const float total = (red[0] + red[1]) + (red[2] + red[3]);
+  const float inv = 1.0f / sqrtf(total / static_cast<float>(hidden) + eps);
+  float4* xr = reinterpret_cast<float4*>(x + static_cast<uint64_t>(r) * hidden);
+  const float4* wr = reinterpret_cast<const float4*>(w);
+  for (uint32_t i = threadIdx.x; i < n4; i += 256) {
+    const float4 v = hr[i], g = wr[i];
+    xr[i] = make_float4(v.x * inv * g.x, v.y * inv * g.y, v.z * inv * g.z, v.w * inv * g.w);
+  }
+}
+
+// ------------------------------------------- head RMSNorm, RoPE, KV append
+// One wavefront per (head, row). Heads [0, heads) are query heads, the next
+// kv_heads are key heads (which also copy their value head into the cache).
+// rms_norm_heads (backend.rs:192-198), then apply_rope with the pair (p,
+// p + head_dim/2) (backend.rs:239-279) at position len + row, then
+// KvCache::append (cache.rs:96-125) of the rotated key and the value.
+struct HeadArgs {
+  const float* qkv;  // [rows][row_stride]: q | k | v
+  uint32_t row_stride, heads, kv_heads, head_dim;
+  const float* q_norm;
+  const float* k_norm;
+  float eps;
+  const float* rope_cos;  // [position][head_dim/2]
+  const float* rope_sin;
+  const uint32_t* len;
+  float* q_out;  // [rows][heads*head_dim]
+  float* keys;   // this layer: [kv_head][dim][cap]
+  float* values; // this layer: [kv_head][cap][dim]
+  uint32_t cap;
+};
+
+__global__ __launch_bounds__(64) void qk_norm_rope_kernel(HeadArgs a) {
+  const uint32_t r = blockIdx.y, hidx = blockIdx.x, lane = threadIdx.x;
+  const uint32_t pos = *a.len + r;
+  const uint32_t hd = a.head_dim, pairs = hd / 2;
+  const bool is_q = hidx < a.heads;
+  const uint32_t g = is_q ? 0 : hidx - a.heads;
+  const float* row = a.qkv + static_cast<uint64_t>(r) * a.row_stride;
+  const float* src = is_q ? row + hidx * hd : row + a.heads * hd + g * hd;
+  const float* wn = is_q ? a.q_norm : a.k_norm;
+  // head_dim <= 128: at most one pair per lane
+  const bool act = lane < pairs;
+  const float x0 = act ? src[lane] : 0.0f;
+  const float x1 = act ? src[lane + pairs] : 0.0f;
+  const float ss = wave_sum(x0 * x0 + x1 * x1);
+  const float inv = 1.0f / sqrtf(ss / static_cast<float>(hd) + a.eps);
+  if (act) {
+    const float f = x0 * inv * wn[lane];
+    const float s = x1 * inv * wn[lane + pairs];
+    const float c = a.rope_cos[static_cast<uint64_t>(pos) * pairs + lane];
+    const float sn = a.rope_sin[static_cast<uint64_t>(pos) * pairs + lane];
+    const float o0 = f * c - s * sn;
+    const float o1 = f * sn + s * c;
+    if (is_q) {
+      float* q = a.q_out + static_cast<uint64_t>(r) * a.heads * hd + hidx * hd;
+      q[lane] = o0;
+      q[lane + pairs] = o1;
+    } else {
+      float* kt = a.keys + static_cast<uint64_t>(g) * hd * a.cap;
+      kt[static_cast<uint64_t>(lane) * a.cap + pos] = o0;
+      kt[static_cast<uint64_t>(lane + pairs) * a.cap + pos] = o1;
+    }
+  }
+  if (!is_q) {
+    const float* v = row + (a.heads + a.kv_heads) * hd + g * hd;
+    float* vc = a.values + (static_cast<uint64_t>(g) * a.cap + pos) * hd;
+    for (uint32_t d = lane; d < hd; d += 64) vc[d] = v[d];
+  }
+}
+
+// ------------------------------------------------------------- attention
+// runtime/src/attention.rs:37-141: for query token r at position p = len + r,
+// head h of kv group g: scores s_j = (q . k_j) / sqrt(head_dim) for j <= p,
+// weights softmax(s), output sum_j weight_j v_j. Split over chunks of 64
+// positions: each wavefront keeps its chunk's max m, sum l = sum exp(s - m) and
+// unnormalized output o = sum exp(s - m) v; the combine rescales the chunks by
+// exp(m - max m) (the same softmax, evaluated in pieces).
+struct AttnArgs {
+  const float* q;  // [rows][heads*hd]
+  const float* keys;
+  const float* values;
+  const uint32_t* len;
+  float* pm;  // [batch row][heads][chunks]
+  float* pl;
+  float* po;  // [batch row][heads][chunks][hd]
+  uint32_t heads, kv_heads, cap, chunks;
+  uint32_t row0;  // first row of this batch (blockIdx row 0)
+  float scale;
+  float* out;  // [rows][heads*hd]
+};
+
+template <int HD, int G>
+__global__ __launch_bounds__(64) void attn_partial_kernel(AttnArgs a) {
+  constexpr int DPL = HD / 64;  // dimensions per lane in the value product
+  __shared__ float4 qs[G][HD / 4];
+  const uint32_t c = blockIdx.x, g = blockIdx.y, rb = blockIdx.z, lane = threadIdx.x;
+  const uint32_t r = rb + a.row0;
+  const uint32_t pos = *a.len + r;
+  const uint32_t t0 = c * kChunk;
+  if (t0 > pos) return;  // the combine skips chunks past the query position
+  const float* qg = a.q + (static_cast<uint64_t>(r) * a.heads + g * G) * HD;
+  for (uint32_t i = lane; i < G * HD / 4; i += 64)
+    qs[i / (HD / 4)][i % (HD / 4)] = reinterpret_cast<const float4*>(qg)[i];
+  __syncthreads();
+
+  const uint32_t p = t0 + lane;  // < cap (a multiple of 64)
+  const bool valid = p <= pos;
+  const float* kt = a.keys + static_cast<uint64_t>(g) * HD * a.cap + p;
+  float s[G];
+#pragma unroll
+  for (int h = 0; h < G; ++h) s[h] = 0.0f;
+#pragma unroll 4
+  for (int d4 = 0; d4 < HD / 4; ++d4) {
+    const float k0 = kt[static_cast<uint64_t>(4 * d4 + 0) * a.cap];
+    const float k1 = kt[static_cast<uint64_t>(4 * d4 + 1) * a.cap];
+    const float k2 = kt[static_cast<uint64_t>(4 * d4 + 2) * a.cap];
+    const float k3 = kt[static_cast<uint64_t>(4 * d4 + 3) * a.cap];
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      const float4 qv = qs[h][d4];
+      s[h] = fmaf(qv.x, k0, s[h]);
+      s[h] = fmaf(qv.y, k1, s[h]);
+      s[h] = fmaf(qv.z, k2, s[h]);
+      s[h] = fmaf(qv.w, k3, s[h]);
+    }
+  }
+  float e[G], m[G], l[G];
+#pragma unroll
+  for (int h = 0; h < G; ++h) {
+    const float sc = valid ? s[h] * a.scale : -INFINITY;
+    m[h] = wave_max(sc);
+    e[h] = valid ? expf(sc - m[h]) : 0.0f;
+    l[h] = wave_sum(e[h]);
+  }
+  // values: lane owns dimensions lane*DPL .. lane*DPL + DPL - 1
+  const uint32_t nvalid = (pos - t0 + 1) < kChunk ? (pos - t0 + 1) : kChunk;
+  const float* vb = a.values + (static_cast<uint64_t>(g) * a.cap + t0) * HD + lane * DPL;
+  float acc[G][DPL];
+#pragma unroll
+  for (int h = 0; h < G; ++h)
+#pragma unroll
+    for (int j = 0; j < DPL; ++j) acc[h][j] = 0.0f;
+  for (uint32_t t = 0; t < nvalid; ++t) {
+    float v[DPL];
+    if constexpr (DPL == 2) {
+      const float2 v2 = *reinterpret_cast<const float2*>(vb + static_cast<uint64_t>(t) * HD);
+      v[0] = v2.x;
+      v[1] = v2.y;
+    } else {
+      v[0] = vb[static_cast<uint64_t>(t) * HD];
+    }
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      const float wt = __shfl(e[h], static_cast<int>(t));
+#pragma unroll
+      for (int j = 0; j < DPL; ++j) acc[h][j] = fmaf(wt, v[j], acc[h][j]);
+    }
+  }
+#pragma unroll
+  for (int h = 0; h < G; ++h) {
+    const uint64_t idx = (static_cast<uint64_t>(rb) * a.heads + g * G + h) * a.chunks + c;
+    if (lane == 0) {
+      a.pm[idx] = m[h];
+      a.pl[idx] = l[h];
+    }
+    float* o = a.po + idx * HD + lane * DPL;
+#pragma unroll
+    for (int j = 0; j < DPL; ++j) o[j] = acc[h][j];
+  }
+}
+
+template <int HD>
+__global__ __launch_bounds__(64) void attn_combine_kernel(AttnArgs a) {
+  constexpr int DPL = HD / 64;
+  const uint32_t h = blockIdx.x, rb = blockIdx.y, lane = threadIdx.x;
+  const uint32_t r = rb + a.row0;
+  const uint32_t pos = *a.len + r;
+  const uint32_t nc = pos / kChunk + 1;
+  const uint64_t base = (static_cast<uint64_t>(rb) * a.heads + h) * a.chunks;
+  float mx = -INFINITY;
+  for (uint32_t c = 0; c < nc; ++c) mx = fmaxf(mx, a.pm[base + c]);
+  float denom = 0.0f, acc[DPL];
+#pragma unroll
+  for (int j = 0; j < DPL; ++j) acc[j] = 0.0f;
+  for (uint32_t c = 0; c < nc; ++c) {
+    const float f = expf(a.pm[base + c] - mx);
+    denom = fmaf(f, a.pl[base + c], denom);
+    const float* o = a.po + (base + c) * HD + lane * DPL;
+#pragma unroll
+    for (int j = 0; j < DPL; ++j) acc[j] = fmaf(f, o[j], acc[j]);
+  }
+  float* out = a.out + (static_cast<uint64_t>(r) * a.heads + h) * HD + lane * DPL;
+#pragma unroll
+  for (int j = 0; j < DPL; ++j) out[j] = acc[j] / denom;
+}
+
+// --------------------------------------------------------------- SiLU*up
+// backends/cpu/src/backend.rs:224-237: gate / (1 + exp(-gate)) * up, with gate
+// and up the two halves of the fused gate|up output row.
+__global__ __launch_bounds__(256) void silu_mul_kernel(const float* __restrict__ gu,
+                                                       float* __restrict__ out, uint32_t inter,
+                                                       uint64_t total) {
+  const uint64_t i = static_cast<uint64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= total) return;
+  const uint64_t r = i / inter, j = i % inter;
+  const float g = gu[r * 2 * inter + j];
+  const float u = gu[r * 2 * inter + inter + j];
+  out[i] = g / (1.0f + expf(-g)) * u;
+}
+
+// ----------------------------------------------------------------- argmax
+// generation.rs:58-76: the first index of the largest logit; a non-finite
+// logit is an error (flagged, reported by the host).
+__device__ __forceinline__ void better(float& bv, uint32_t& bi, float v, uint32_t i) {
+  if (v > bv || (v == bv && i < bi)) {
+    bv = v;
+    bi = i;
+  }
+}
+
+__global__ __launch_bounds__(256) void argmax_partial_kernel(const float* __restrict__ logits,
+                                                             uint32_t n, float* __restrict__ pv,
+                                                             uint32_t* __restrict__ pi,
+                                                             int32_t* __restrict__ bad) {
+  __shared__ float sv[256];
+  __shared__ uint32_t si[256];
+  const uint32_t per = (n + kArgBlocks - 1) / kArgBlocks;
+  const uint32_t b0 = blockIdx.x * per;
+  const uint32_t b1 = b0 + per < n ? b0 + per : n;
+  float bv = -INFINITY;
+  uint32_t bi = 0xffffffffu;
+  bool nonfinite = false;
+  for (uint32_t i = b0 + threadIdx.x; i < b1; i += 256) {
+    const float v = logits[i];
+    nonfinite |= !isfinite(v);
+    better(bv, bi, v, i);
+  }
+  if (nonfinite) *bad = 1;
+  sv[threadIdx.x] = bv;
+  si[threadIdx.x] = bi;
+  __syncthreads();
+  for (uint32_t s = 128; s > 0; s >>= 1) {
+    if (threadIdx.x < s) {
+      float v = sv[threadIdx.x];
+      uint32_t i = si[threadIdx.x];
+      better(v, i, sv[threadIdx.x + s], si[threadIdx.x + s]);
+      sv[threadIdx.x] = v;
+      si[threadIdx.x] = i;
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    pv[blockIdx.x] = sv[0];
+    pi[blockIdx.x] = si[0];
+  }
+}
+
+// Reduce the partials, store the token at tok[len + rows] and advance len.
+__global__ __launch_bounds__(256) void argmax_final_kernel(const float* __restrict__ pv,
+                                                           const uint32_t* __restrict__ pi,
+                                                           int32_t* __restrict__ tok,
+                                                           uint32_t* __restrict__ len,
+                                                           uint32_t rows) {
+  __shared__ float sv[kArgBlocks];
+  __shared__ uint32_t si[kArgBlocks];
+  sv[threadIdx.x] = pv[threadIdx.x];
+  si[threadIdx.x] = pi[threadIdx.x];
+  __syncthreads();
+  for (uint32_t s = kArgBlocks / 2; s > 0; s >>= 1) {
+    if (threadIdx.x < s) {
+      float v = sv[threadIdx.x];
+      uint32_t i = si[threadIdx.x];
+      better(v, i, sv[threadIdx.x + s], si[threadIdx.x + s]);
+      sv[threadIdx.x] = v;
+      si[threadIdx.x] = i;
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    const uint32_t next = *len + rows;
+    tok[next] = static_cast<int32_t>(si[0] == 0xffffffffu ? 0u : si[0]);
+    *len = next;
+  }
+}
+
+__global__ void advance_kernel(uint32_t* len, uint32_t rows) {
+  if (threadIdx.x == 0) *len = *len + rows;
+}
+
+// ------------------------------------------------------------------ host
+
+std::atomic<uint64_t> g_next_model_id{1};
+
+struct Linear {
+  qi_hip_weights* w = nullptr;
+  uint64_t k = 0, n = 0;
+};
+
+struct Layer {
+  float* norms = nullptr;  // input | q | k | post (device)
+  Linear qkv, o, gate_up, down;
+  bool set = false;
+};
+
+size_t logical_bytes(int32_t qtype) {
+  switch (qtype) {
+    case QI_HIP_F32: return 4;
+    case QI_HIP_Q8_0: return sizeof(qi_hip_q8_0_block);
+    case QI_HIP_Q4_0: return sizeof(qi_hip_q4_0_block);
+    case QI_HIP_Q4_K: return sizeof(qi_hip_q4_k_block);
+    case QI_HIP_Q5_K: return sizeof(qi_hip_q5_k_block);
+    case QI_HIP_Q6_K: return sizeof(qi_hip_q6_k_block);
+    default: return 0;
+  }
+}
+
+uint32_t elems_per_block(int32_t qtype) {
+  return qtype == QI_HIP_F32 ? 1u : qi::block_elems(qtype);
+}
+
+}  // namespace
+
+struct qi_hip_qwen3 {
+  qi_hip_ctx* ctx = nullptr;
+  qi_hip_qwen3_config cfg{};
+  int32_t mode = QI_HIP_MODE_AUTO;
+  uint64_t id = 0;
+  std::vector<Layer> layers;
+  float* embedding = nullptr;
+  float* final_norm = nullptr;
+  Linear head;
+  float* rope_cos = nullptr;
+  float* rope_sin = nullptr;
+  // activations for up to kMaxRows rows
+  float *h = nullptr, *x = nullptr, *qkv = nullptr, *q = nullptr, *att = nullptr, *y = nullptr;
+  float *gu = nullptr, *act = nullptr, *logits = nullptr, *apv = nullptr;
+  uint32_t* api = nullptr;
+  int32_t* bad = nullptr;
+  hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
+  qi_hip_qwen3_timing timing{};
+  bool eager = false;  // QI_HIP_QWEN3_EAGER=1: launch decode steps one by one (no graph)
+};
+
+struct qi_hip_kv_cache {
+  qi_hip_ctx* ctx = nullptr;
+  uint32_t layers = 0, max_seq = 0, kv_heads = 0, head_dim = 0, cap = 0;
+  float* keys = nullptr;    // [layer][kv_head][dim][cap]
+  float* values = nullptr;  // [layer][kv_head][cap][dim]
+  int32_t* tok = nullptr;   // [cap + 1]
+  uint32_t* len_dev = nullptr;
+  uint64_t len = 0;         // host mirror of *len_dev
+  // attention partials for row batches of `rb` rows
+  float *pm = nullptr, *pl = nullptr, *po = nullptr;
+  uint32_t rb = 0, heads = 0;
+  hipGraphExec_t exec = nullptr;
+  uint64_t graph_model = 0, graph_ws = 0;
+};
+
+namespace {
+
+void dev_free(void* p) {
+  if (p) (void)hipFree(p);
+}
+
+qi_hip_status dev_alloc(void** p, uint64_t bytes, const char* what) {
+  *p = nullptr;
+  hipError_t e = hipMalloc(p, bytes ? bytes : 16);
+  if (e != hipSuccess) return hip_fail(e, what);
+  return QI_HIP_OK;
+}
+
+template <class T>
+qi_hip_status dev_alloc_t(T** p, uint64_t count, const char* what) {
+  return dev_alloc(reinterpret_cast<void**>(p), count * sizeof(T), what);
+}
+
+qi_hip_status upload(void* dst, const void* src, uint64_t bytes, hipStream_t st) {
+  QI_HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, st), "upload");
+  QI_HIP_TRY(hipStreamSynchronize(st), "upload");
+  return QI_HIP_OK;
+}
+
+// Concatenate linear weights along N (the output dimension) into one logical
+// buffer and upload it as one image. Output rows: each part is [N_i][K/bs]
+// blocks, so the parts follow one another. Row-major: each part is
+// [K][N_i/bs] blocks, so row k of the result is row k of every part in turn.
+qi_hip_status make_linear(qi_hip_ctx* c, const qi_hip_linear_weight* const* parts, int count,
+                          uint64_t k, const uint64_t* ns, const char* name, Linear* out) {
+  const int32_t qtype = parts[0]->qtype, layout = parts[0]->layout;
+  const size_t lb = logical_bytes(qtype);
+  if (lb == 0) return fail(QI_HIP_INVALID_INPUT, std::string(name) + ": unknown weight type");
+  const uint32_t bs = elems_per_block(qtype);
+  uint64_t n = 0;
+  for (int i = 0; i < count; ++i) {
+    if (parts[i]->qtype != qtype || parts[i]->layout != layout)
+      return fail(QI_HIP_UNSUPPORTED,
+                  std::string(name) + ": fused projections must share weight type and layout");
+    if (parts[i]->data == nullptr) return fail(QI_HIP_INVALID_INPUT, std::string(name) + ": null weight");
+    n += ns[i];
+  }
+  const bool rows = layout == QI_HIP_LAYOUT_OUTPUT_ROWS;
+  for (int i = 0; i < count; ++i) {
+    const uint64_t per = rows ? ns[i] * (k / bs) : k * (ns[i] / bs);
+    if ((rows ? k % bs : ns[i] % bs) != 0 || parts[i]->count != per)
+      return fail(QI_HIP_INVALID_INPUT, std::string(name) + ": block count does not match its shape");
+  }
+  std::vector<uint8_t> joined;
+  const void* blocks = parts[0]->data;
+  uint64_t total = parts[0]->count;
+  if (count > 1) {
+    total = 0;
+    for (int i = 0; i < count; ++i) total += parts[i]->count;
+    joined.resize(total * lb);
+    uint8_t* dst = joined.data();
+    if (rows) {
+      for (int i = 0; i < count; ++i) {
+        memcpy(dst, parts[i]->data, parts[i]->count * lb);
+        dst += parts[i]->count * lb;
+      }
+    } else {
+      for (uint64_t kk = 0; kk < k; ++kk) {
+        for (int i = 0; i < count; ++i) {
+          const uint64_t row = ns[i] / bs * lb;
+          memcpy(dst, static_cast<const uint8_t*>(parts[i]->data) + kk * row, row);
+          dst += row;
+        }
+      }
+    }
+    blocks = joined.data();
+  }
+  qi::Image im;
+  const char* why = "";
+  qi_hip_status s = qi::plan_image(qtype, layout, k, n, blocks, total, &im, &why);
+  if (s != QI_HIP_OK) return fail(s, std::string(name) + ": " + why);
+  s = qi_abi::create_weights_locked(c, im, blocks, &out->w);
+  if (s != QI_HIP_OK) return s;
+  out->k = k;
+  out->n = n;
+  return QI_HIP_OK;
+}
+
+void free_linear(Linear* l) {
+  if (l->w) qi_abi::free_weights_locked(l->w);
+  l->w = nullptr;
+}
+
+bool model_ready(const qi_hip_qwen3* m) {
+  if (!m->embedding || !m->final_norm || !m->head.w) return false;
+  for (const Layer& l : m->layers)
+    if (!l.set) return false;
+  return true;
+}
+
+qi_hip_status linear(qi_hip_qwen3* m, const Linear& l, const float* x, uint32_t rows, float* y) {
+  return qi_abi::run_linear(m->ctx, l.w, x, rows, y, m->mode, m->ctx->stream);
+}
+
+// Launch the attention of `rows` query rows (positions len .. len+rows-1).
+qi_hip_status attention(qi_hip_qwen3* m, qi_hip_kv_cache* c, uint32_t layer, uint32_t rows) {
+  const qi_hip_qwen3_config& k = m->cfg;
+  const uint32_t hd = k.head_dim, group = k.num_attention_heads / k.num_key_value_heads;
+  const uint64_t lay = static_cast<uint64_t>(k.num_key_value_heads) * hd * c->cap;
+  AttnArgs a;
+  a.q = m->q;
+  a.keys = c->keys + layer * lay;
+  a.values = c->values + layer * lay;
+  a.len = c->len_dev;
+  a.pm = c->pm;
+  a.pl = c->pl;
+  a.po = c->po;
+  a.heads = k.num_attention_heads;
+  a.kv_heads = k.num_key_value_heads;
+  a.cap = c->cap;
+  a.chunks = c->cap / kChunk;
+  a.scale = 1.0f / sqrtf(static_cast<float>(hd));
+  a.out = m->att;
+  hipStream_t st = m->ctx->stream;
+  for (uint32_t r0 = 0; r0 < rows; r0 += c->rb) {
+    const uint32_t nr = rows - r0 < c->rb ? rows - r0 : c->rb;
+    AttnArgs b = a;
+    b.row0 = r0;
+    const dim3 pg(a.chunks, a.kv_heads, nr), cg(a.heads, nr);
+#define QI_ATTN(HD_, G_)                                                          \
+  if (hd == HD_ && group == G_) {                                                 \
+    hipLaunchKernelGGL((attn_partial_kernel<HD_, G_>), pg, dim3(64), 0, st, b);   \
+    hipLaunchKernelGGL((attn_combine_kernel<HD_>), cg, dim3(64), 0, st, b);       \
+  } else
+    QI_ATTN(128, 1) QI_ATTN(128, 2) QI_ATTN(128, 4) QI_ATTN(128, 8)
+    QI_ATTN(64, 1) QI_ATTN(64, 2) QI_ATTN(64, 4) QI_ATTN(64, 8)
+    return fail(QI_HIP_UNSUPPORTED, "attention supports head_dim 64/128 and 1/2/4/8 query heads per KV head");
+#undef QI_ATTN
+    QI_HIP_TRY(hipGetLastError(), "launch attention");
+  }
+  return QI_HIP_OK;
+}
+
+// Enqueue the forward of `rows` tokens tok[len .. len+rows) on the context
+// stream. With `project`, the last row goes through the final norm, the LM
+// head and the argmax (token stored at tok[len+rows]); len advances by rows.
+qi_hip_status enqueue_forward(qi_hip_qwen3* m, qi_hip_kv_cache* c, uint32_t rows, bool project) {
+  const qi_hip_qwen3_config& k = m->cfg;
+  hipStream_t st = m->ctx->stream;
+  const uint32_t H = k.hidden_size, I = k.intermediate_size, hd = k.head_dim;
+  const uint32_t QS = k.num_attention_heads * hd, KS = k.num_key_value_heads * hd;
+  const uint64_t lay = static_cast<uint64_t>(k.num_key_value_heads) * hd * c->cap;
+  qi_hip_status s;
+  hipLaunchKernelGGL(residual_norm_kernel<true>, dim3(rows), dim3(256), 0, st, m->h, nullptr,
+                     m->embedding, c->tok, c->len_dev, m->x, m->layers[0].norms, H, k.rms_norm_eps);
+  for (uint32_t l = 0; l < k.num_hidden_layers; ++l) {
+    Layer& L = m->layers[l];
+    if ((s = linear(m, L.qkv, m->x, rows, m->qkv)) != QI_HIP_OK) return s;
+    HeadArgs ha;
+    ha.qkv = m->qkv;
+    ha.row_stride = QS + 2 * KS;
+    ha.heads = k.num_attention_heads;
+    ha.kv_heads = k.num_key_value_heads;
+    ha.head_dim = hd;
+    ha.q_norm = L.norms + H;
+    ha.k_norm = L.norms + H + hd;
+    ha.eps = k.rms_norm_eps;
+    ha.rope_cos = m->rope_cos;
+    ha.rope_sin = m->rope_sin;
+    ha.len = c->len_dev;
+    ha.q_out = m->q;
+    ha.keys = c->keys + l * lay;
+    ha.values = c->values + l * lay;
+    ha.cap = c->cap;
+    hipLaunchKernelGGL(qk_norm_rope_kernel, dim3(ha.heads + ha.kv_heads, rows), dim3(64), 0, st, ha);
+    if ((s = attention(m, c, l, rows)) != QI_HIP_OK) return s;
+    if ((s = linear(m, L.o, m->att, rows, m->y)) != QI_HIP_OK) return s;
+    hipLaunchKernelGGL(residual_norm_kernel<false>, dim3(rows), dim3(256), 0, st, m->h, m->y,
+                       nullptr, nullptr, nullptr, m->x, L.norms + H + 2 * hd, H, k.rms_norm_eps);
+    if ((s = linear(m, L.gate_up, m->x, rows, m->gu)) != QI_HIP_OK) return s;
+    const uint64_t total = static_cast<uint64_t>(rows) * I;
+    hipLaunchKernelGGL(silu_mul_kernel, dim3(static_cast<uint32_t>((total + 255) / 256)), dim3(256),
+                       0, st, m->gu, m->act, I, total);
+    if ((s = linear(m, L.down, m->act, rows, m->y)) != QI_HIP_OK) return s;
+    const float* next = l + 1 < k.num_hidden_layers ? m->layers[l + 1].norms : m->final_norm;
+    hipLaunchKernelGGL(residual_norm_kernel<false>, dim3(rows), dim3(256), 0, st, m->h, m->y,
+                       nullptr, nullptr, nullptr, m->x, next, H, k.rms_norm_eps);
+  }
+  if (project) {
+    const float* last = m->x + static_cast<uint64_t>(rows - 1) * H;
+    if ((s = linear(m, m->head, last, 1, m->logits)) != QI_HIP_OK) return s;
+    hipLaunchKernelGGL(argmax_partial_kernel, dim3(kArgBlocks), dim3(256), 0, st, m->logits,
+                       k.vocab_size, m->apv, m->api, m->bad);
+    hipLaunchKernelGGL(argmax_final_kernel, dim3(1), dim3(kArgBlocks), 0, st, m->apv, m->api,
+                       c->tok, c->len_dev, rows);
+  } else {
+    hipLaunchKernelGGL(advance_kernel, dim3(1), dim3(64), 0, st, c->len_dev, rows);
+  }
+  QI_HIP_TRY(hipGetLastError(), "launch decoder kernels");
+  return QI_HIP_OK;
+}
+
+qi_hip_status check_pair(qi_hip_qwen3* m, qi_hip_kv_cache* c) {
+  if (m == nullptr || c == nullptr) return fail(QI_HIP_INVALID_INPUT, "null model or cache");
+  if (m->ctx != c->ctx) return fail(QI_HIP_INVALID_INPUT, "model and cache belong to different contexts");
+  if (m->ctx->closed) return fail(QI_HIP_INVALID_INPUT, "context is closed");
+  if (!model_ready(m)) return fail(QI_HIP_INVALID_INPUT, "Qwen3 model weights are not all set");
+  // KvCache::validate_layout (cache.rs:67-94)
+  if (c->layers != m->cfg.num_hidden_layers || c->kv_heads != m->cfg.num_key_value_heads ||
+      c->head_dim != m->cfg.head_dim)
+    return fail(QI_HIP_INVALID_INPUT, "KV cache layout differs from model");
+  return QI_HIP_OK;
+}
+
+// Size the cache's attention partials for this model's head count.
+qi_hip_status ensure_partials(qi_hip_qwen3* m, qi_hip_kv_cache* c) {
+  const uint32_t heads = m->cfg.num_attention_heads;
+  if (c->pm && c->heads == heads) return QI_HIP_OK;
+  QI_HIP_TRY(hipStreamSynchronize(m->ctx->stream), "synchronize before sizing partials");
+  dev_free(c->pm);
+  dev_free(c->pl);
+  dev_free(c->po);
+  c->pm = c->pl = c->po = nullptr;
+  if (c->exec) (void)hipGraphExecDestroy(c->exec);
+  c->exec = nullptr;
+  const uint64_t chunks = c->cap / kChunk;
+  const uint64_t per_row = static_cast<uint64_t>(heads) * chunks * (c->head_dim + 2) * 4;
+  uint64_t rb = kPartialBudget / per_row;
+  rb = rb < 1 ? 1 : (rb > kMaxRows ? kMaxRows : rb);
+  const uint64_t hc = static_cast<uint64_t>(heads) * chunks * rb;
+  qi_hip_status s;
+  if ((s = dev_alloc_t(&c->pm, hc, "alloc attention partials")) != QI_HIP_OK) return s;
+  if ((s = dev_alloc_t(&c->pl, hc, "alloc attention partials")) != QI_HIP_OK) return s;
+  if ((s = dev_alloc_t(&c->po, hc * c->head_dim, "alloc attention partials")) != QI_HIP_OK) return s;
+  c->rb = static_cast<uint32_t>(rb);
+  c->heads = heads;
+  return QI_HIP_OK;
+}
+
+// Prompt forward: upload tokens, run chunks of kMaxRows, project the last row.
+qi_hip_status forward_locked(qi_hip_qwen3* m, qi_hip_kv_cache* c, const int32_t* tokens,
+                             uint64_t count) {
+  hipStream_t st = m->ctx->stream;
+  if (count == 0) return fail(QI_HIP_INVALID_INPUT, "Qwen3 forward requires at least one token");
+  for (uint64_t i = 0; i < count; ++i)
+    if (tokens[i] < 0 || static_cast<uint64_t>(tokens[i]) >= m->cfg.vocab_size)
+      return fail(QI_HIP_INVALID_INPUT, "token id " + std::to_string(tokens[i]) +
+                                            " is outside vocabulary size " +
+                                            std::to_string(m->cfg.vocab_size));
+  if (c->len + count > m->cfg.max_position_embeddings)
+    return fail(QI_HIP_INVALID_INPUT, "input exceeds Qwen3 max_position_embeddings");
+  if (c->len + count > c->max_seq)
+    return fail(QI_HIP_INVALID_INPUT, "KV cache capacity is smaller than the requested sequence");
+  qi_hip_status s = ensure_partials(m, c);
+  if (s != QI_HIP_OK) return s;
+  QI_HIP_TRY(hipMemcpyAsync(c->tok + c->len, tokens, count * 4, hipMemcpyHostToDevice, st),
+             "upload tokens");
+  QI_HIP_TRY(hipMemsetAsync(m->bad, 0, 4, st), "clear logits flag");
+  for (uint64_t r0 = 0; r0 < count; r0 += kMaxRows) {
+    const uint32_t rows = static_cast<uint32_t>(count - r0 < kMaxRows ? count - r0 : kMaxRows);
+    const bool last = r0 + rows == count;
+    if ((s = enqueue_forward(m, c, rows, last)) != QI_HIP_OK) return s;
+  }
+  c->len += count;
+  return QI_HIP_OK;
+}
+
+qi_hip_status read_bad(qi_hip_qwen3* m) {
+  int32_t bad = 0;
+  QI_HIP_TRY(hipMemcpyAsync(&bad, m->bad, 4, hipMemcpyDeviceToHost, m->ctx->stream), "read flag");
+  QI_HIP_TRY(hipStreamSynchronize(m->ctx->stream), "synchronize");
+  if (bad) return fail(QI_HIP_INVALID_INPUT, "logits must contain only finite values");
+  return QI_HIP_OK;
+}
+
+// One decode step (the token at tok[len]) as a replay of the cache's graph,
+// captured on first use for this model and context workspace generation.
+qi_hip_status decode_step(qi_hip_qwen3* m, qi_hip_kv_cache* c) {
+  hipStream_t st = m->ctx->stream;
+  if (m->eager) return enqueue_forward(m, c, 1, true);
+  if (c->exec == nullptr || c->graph_model != m->id || c->graph_ws != qi_abi::workspace_version()) {
+    if (c->exec) {
+      QI_HIP_TRY(hipStreamSynchronize(st), "synchronize before recapture");
+      (void)hipGraphExecDestroy(c->exec);
+      c->exec = nullptr;
+    }
+    // An eager step first: it grows any context workspace the step needs, so
+    // the capture below allocates nothing.
+    qi_hip_status s = enqueue_forward(m, c, 1, true);
+    if (s != QI_HIP_OK) return s;
+    const uint64_t ws = qi_abi::workspace_version();
+    hipGraph_t graph = nullptr;
+    QI_HIP_TRY(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal), "begin capture");
+    s = enqueue_forward(m, c, 1, true);
+    hipError_t e = hipStreamEndCapture(st, &graph);
+    if (s != QI_HIP_OK) {
+      if (graph) (void)hipGraphDestroy(graph);
+      return s;
+    }
+    if (e != hipSuccess) return hip_fail(e, "capture decode step");
+    e = hipGraphInstantiate(&c->exec, graph, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(graph);
+    if (e != hipSuccess) {
+      c->exec = nullptr;
+      return hip_fail(e, "instantiate decode graph");
+    }
+    c->graph_model = m->id;
+    c->graph_ws = ws;
+    return QI_HIP_OK;  // the eager step was this step
+  }
+  QI_HIP_TRY(hipGraphLaunch(c->exec, st), "launch decode graph");
+  return QI_HIP_OK;
+}
+
+void model_destroy(qi_hip_qwen3* m) {
+  qi_hip_ctx* c = m->ctx;
+  {
+    std::lock_guard<std::mutex> lock(c->mu);
+    (void)hipSetDevice(c->device);
+    (void)hipStreamSynchronize(c->stream);
+    for (Layer& l : m->layers) {
+      dev_free(l.norms);
+      free_linear(&l.qkv);
+      free_linear(&l.o);
+      free_linear(&l.gate_up);
+      free_linear(&l.down);
+    }
+    free_linear(&m->head);
+    for (void* p : {static_cast<void*>(m->embedding), static_cast<void*>(m->final_norm),
+                    static_cast<void*>(m->rope_cos), static_cast<void*>(m->rope_sin),
+                    static_cast<void*>(m->h), static_cast<void*>(m->x), static_cast<void*>(m->qkv),
+                    static_cast<void*>(m->q), static_cast<void*>(m->att), static_cast<void*>(m->y),
+                    static_cast<void*>(m->gu), static_cast<void*>(m->act),
+                    static_cast<void*>(m->logits), static_cast<void*>(m->apv),
+                    static_cast<void*>(m->api), static_cast<void*>(m->bad)})
+      dev_free(p);
+    for (hipEvent_t e : m->ev)
+      if (e) (void)hipEventDestroy(e);
+  }
+  qi_abi::ctx_release(c);
+  delete m;
+}
+
+}  // namespace
+
+extern "C" {
+
+qi_hip_status qi_hip_qwen3_create(qi_hip_ctx* ctx, const qi_hip_qwen3_config* cfg,
+                                  qi_hip_qwen3** out) {
+  if (ctx == nullptr || cfg == nullptr || out == nullptr) return fail(QI_HIP_INVALID_INPUT, "null argument");
+  *out = nullptr;
+  if (ctx->closed) return fail(QI_HIP_INVALID_INPUT, "context is closed");
+  const qi_hip_qwen3_config& k = *cfg;
+  // Qwen3Config::validate / LlamaConfig::validate (quantinfer-model llama.rs:64-100)
+  if (k.vocab_size == 0 || k.hidden_size == 0 || k.intermediate_size == 0 ||
+      k.num_hidden_layers == 0 || k.num_attention_heads == 0 || k.num_key_value_heads == 0 ||
+      k.max_position_embeddings == 0)
+    return fail(QI_HIP_INVALID_INPUT, "Qwen3 dimensions must be greater than zero");
+  if (k.num_attention_heads % k.num_key_value_heads != 0)
+    return fail(QI_HIP_INVALID_INPUT, "attention heads must be divisible by key/value heads");
+  if (k.head_dim == 0 || k.head_dim % 2 != 0)
+    return fail(QI_HIP_INVALID_INPUT, "head_dim must be positive and even for RoPE");
+  if (!(k.rms_norm_eps > 0.0f) || !isfinite(k.rms_norm_eps) || !(k.rope_theta > 0.0f) ||
+      !isfinite(k.rope_theta))
+    return fail(QI_HIP_INVALID_INPUT, "rms_norm_eps and rope_theta must be positive and finite");
+  // shapes this device implementation covers
+  if (k.head_dim != 64 && k.head_dim != 128)
+    return fail(QI_HIP_UNSUPPORTED, "the device decoder supports head_dim 64 and 128");
+  const uint32_t group = k.num_attention_heads / k.num_key_value_heads;
+  if (group != 1 && group != 2 && group != 4 && group != 8)
+    return fail(QI_HIP_UNSUPPORTED, "the device decoder supports 1, 2, 4 or 8 query heads per KV head");
+  if (k.hidden_size % 4 != 0) return fail(QI_HIP_UNSUPPORTED, "hidden_size must be a multiple of 4");
+
+  qi_hip_qwen3* m = new qi_hip_qwen3();
+  m->cfg = k;
+  m->layers.resize(k.num_hidden_layers);
+  if (const char* env = getenv("QI_HIP_QWEN3_EAGER")) m->eager = atoi(env) != 0;
+  std::lock_guard<std::mutex> lock(ctx->mu);
+  ctx->refs.fetch_add(1, std::memory_order_relaxed);
+  m->ctx = ctx;
+  m->id = g_next_model_id++;
+  auto bail = [&](qi_hip_status s) {
+    ctx->mu.unlock();
+    model_destroy(m);
+    ctx->mu.lock();
+    return s;
+  };
+  hipError_t e = hipSetDevice(ctx->device);
+  if (e != hipSuccess) return bail(hip_fail(e, "set device"));
+  // RoPE tables for every position (attention.rs:7-35, evaluated once with
+  // the same f32 library functions)
+  const uint32_t pairs = k.head_dim / 2;
+  std::vector<float> cs(static_cast<uint64_t>(k.max_position_embeddings) * pairs);
+  std::vector<float> sn(cs.size());
+  for (uint64_t p = 0; p < k.max_position_embeddings; ++p) {
+    const float position = static_cast<float>(p);
+    for (uint32_t i = 0; i < pairs; ++i) {
+      const float exponent = (2.0f * static_cast<float>(i)) / static_cast<float>(k.head_dim);
+      const float angle = position * powf(k.rope_theta, -exponent);
+      cs[p * pairs + i] = cosf(angle);
+      sn[p * pairs + i] = sinf(angle);
+    }
+  }
+  const uint64_t H = k.hidden_size, I = k.intermediate_size;
+  const uint64_t QS = static_cast<uint64_t>(k.num_attention_heads) * k.head_dim;
+  const uint64_t KS = static_cast<uint64_t>(k.num_key_value_heads) * k.head_dim;
+  qi_hip_status s;
+  if ((s = dev_alloc_t(&m->rope_cos, cs.size(), "alloc rope tables")) != QI_HIP_OK) return bail(s);
+  if ((s = dev_alloc_t(&m->rope_sin, sn.size(), "alloc rope tables")) != QI_HIP_OK) return bail(s);
+  if ((s = upload(m->rope_cos, cs.data(), cs.size() * 4, ctx->stream)) != QI_HIP_OK) return bail(s);
+  if ((s = upload(m->rope_sin, sn.data(), sn.size() * 4, ctx->stream)) != QI_HIP_OK) return bail(s);
+  const uint64_t R = kMaxRows;
+  if ((s = dev_alloc_t(&m->h, R * H, "alloc activations")) != QI_HIP_OK ||
+      (s = dev_alloc_t(&m->x, R * H, "alloc activations")) != QI_HIP_OK ||
+      (s = dev_alloc_t(&m->qkv, R * (QS + 2 * KS), "alloc activations")) != QI_HIP_OK ||
+      (s = dev_alloc_t(&m->q, R * QS, "alloc activations")) != QI_HIP_OK ||
+      (s = dev_alloc_t(&m->att, R * QS, "alloc activations")) != QI_HIP_OK ||
+      (s = dev_alloc_t(&m->y, R * H, "alloc activations")) != QI_HIP_OK ||
+      (s = dev_alloc_t(&m->gu, R * 2 * I, "alloc activations")) != QI_HIP_OK ||
+      (s = dev_alloc_t(&m->act, R * I, "alloc activations")) != QI_HIP_OK ||
+      (s = dev_alloc_t(&m->logits, k.vocab_size, "alloc logits")) != QI_HIP_OK ||
+      (s = dev_alloc_t(&m->apv, kArgBlocks, "alloc argmax")) != QI_HIP_OK ||
+      (s = dev_alloc_t(&m->api, kArgBlocks, "alloc argmax")) != QI_HIP_OK ||
+      (s = dev_alloc_t(&m->bad, 1, "alloc flag")) != QI_HIP_OK)
+    return bail(s);
+  for (hipEvent_t& ev : m->ev) {
+    e = hipEventCreate(&ev);
+    if (e != hipSuccess) return bail(hip_fail(e, "create events"));
+  }
+  *out = m;
+  return QI_HIP_OK;
+}
+
+qi_hip_status qi_hip_qwen3_set_embedding(qi_hip_qwen3* m, const float* table) {
+  if (m == nullptr || table == nullptr) return fail(QI_HIP_INVALID_INPUT, "null argument");
+  std::lock_guard<std::mutex> lock(m->ctx->mu);
+  QI_HIP_TRY(hipSetDevice(m->ctx->device), "set device");
+  const uint64_t n = static_cast<uint64_t>(m->cfg.vocab_size) * m->cfg.hidden_size;
+  if (m->embedding == nullptr) {
+    qi_hip_status s = dev_alloc_t(&m->embedding, n, "alloc embedding");
+    if (s != QI_HIP_OK) return s;
+  }
+  return upload(m->embedding, table, n * 4, m->ctx->stream);
+}
+
+qi_hip_status qi_hip_qwen3_set_layer(qi_hip_qwen3* m, uint32_t index, const qi_hip_qwen3_layer* L) {
+  if (m == nullptr || L == nullptr) return fail(QI_HIP_INVALID_INPUT, "null argument");
+  const qi_hip_qwen3_config& k = m->cfg;
+  if (index >= k.num_hidden_layers) return fail(QI_HIP_INVALID_INPUT, "layer index is out of bounds");
+  if (!L->input_layernorm || !L->q_norm || !L->k_norm || !L->post_attention_layernorm)
+    return fail(QI_HIP_INVALID_INPUT, "null norm weight");
+  const uint64_t H = k.hidden_size, I = k.intermediate_size, hd = k.head_dim;
+  const uint64_t QS = k.num_attention_heads * hd, KS = k.num_key_value_heads * hd;
+  std::lock_guard<std::mutex> lock(m->ctx->mu);
+  QI_HIP_TRY(hipSetDevice(m->ctx->device), "set device");
+  QI_HIP_TRY(hipStreamSynchronize(m->ctx->stream), "synchronize");
+  Layer fresh;
+  qi_hip_status s = dev_alloc_t(&fresh.norms, 2 * H + 2 * hd, "alloc norms");
+  auto cleanup = [&](qi_hip_status st) {
+    dev_free(fresh.norms);
+    free_linear(&fresh.qkv);
+    free_linear(&fresh.o);
+    free_linear(&fresh.gate_up);
+    free_linear(&fresh.down);
+    return st;
+  };
+  if (s != QI_HIP_OK) return cleanup(s);
+  std::vector<float> norms(2 * H + 2 * hd);
+  memcpy(norms.data(), L->input_layernorm, H * 4);
+  memcpy(norms.data() + H, L->q_norm, hd * 4);
+  memcpy(norms.data() + H + hd, L->k_norm, hd * 4);
+  memcpy(norms.data() + H + 2 * hd, L->post_attention_layernorm, H * 4);
+  if ((s = upload(fresh.norms, norms.data(), norms.size() * 4, m->ctx->stream)) != QI_HIP_OK)
+    return cleanup(s);
+  const qi_hip_linear_weight* qkv[3] = {&L->q_proj, &L->k_proj, &L->v_proj};
+  const uint64_t nqkv[3] = {QS, KS, KS};
+  const qi_hip_linear_weight* gu[2] = {&L->gate_proj, &L->up_proj};
+  const uint64_t ngu[2] = {I, I};
+  const qi_hip_linear_weight* o[1] = {&L->o_proj};
+  const qi_hip_linear_weight* dn[1] = {&L->down_proj};
+  const uint64_t nh[1] = {H};
+  if ((s = make_linear(m->ctx, qkv, 3, H, nqkv, "q/k/v projection", &fresh.qkv)) != QI_HIP_OK ||
+      (s = make_linear(m->ctx, o, 1, QS, nh, "o projection", &fresh.o)) != QI_HIP_OK ||
+      (s = make_linear(m->ctx, gu, 2, H, ngu, "gate/up projection", &fresh.gate_up)) != QI_HIP_OK ||
+      (s = make_linear(m->ctx, dn, 1, I, nh, "down projection", &fresh.down)) != QI_HIP_OK)
+    return cleanup(s);
+  Layer& dst = m->layers[index];
+  dev_free(dst.norms);
+  free_linear(&dst.qkv);
+  free_linear(&dst.o);
+  free_linear(&dst.gate_up);
+  free_linear(&dst.down);
+  dst = fresh;
+  dst.set = true;
+  m->id = g_next_model_id++;  // captured decode graphs of this model are stale
+  return QI_HIP_OK;
+}
+
+qi_hip_status qi_hip_qwen3_set_output(qi_hip_qwen3* m, const float* final_norm,
+                                      const qi_hip_linear_weight* head) {
+  if (m == nullptr || final_norm == nullptr || head == nullptr)
+    return fail(QI_HIP_INVALID_INPUT, "null argument");
+  const uint64_t H = m->cfg.hidden_size, V = m->cfg.vocab_size;
+  std::lock_guard<std::mutex> lock(m->ctx->mu);
+  QI_HIP_TRY(hipSetDevice(m->ctx->device), "set device");
+  QI_HIP_TRY(hipStreamSynchronize(m->ctx->stream), "synchronize");
+  Linear fresh;
+  const qi_hip_linear_weight* parts[1] = {head};
+  const uint64_t nv[1] = {V};
+  qi_hip_status s = make_linear(m->ctx, parts, 1, H, nv, "lm_head", &fresh);
+  if (s != QI_HIP_OK) return s;
+  if (m->final_norm == nullptr && (s = dev_alloc_t(&m->final_norm, H, "alloc final norm")) != QI_HIP_OK) {
+    free_linear(&fresh);
+    return s;
+  }
+  if ((s = upload(m->final_norm, final_norm, H * 4, m->ctx->stream)) != QI_HIP_OK) {
+    free_linear(&fresh);
+    return s;
+  }
+  free_linear(&m->head);
+  m->head = fresh;
+  m->id = g_next_model_id++;
+  return QI_HIP_OK;
+}
+
+qi_hip_status qi_hip_qwen3_set_mode(qi_hip_qwen3* m, int32_t mode) {
+  if (m == nullptr) return fail(QI_HIP_INVALID_INPUT, "null model");
+  if (mode < QI_HIP_MODE_AUTO || mode > QI_HIP_MODE_MFMA) return fail(QI_HIP_INVALID_INPUT, "unknown arithmetic mode");
+  std::lock_guard<std::mutex> lock(m->ctx->mu);
+  m->mode = mode;
+  m->id = g_next_model_id++;
+  return QI_HIP_OK;
+}
+
+void qi_hip_qwen3_free(qi_hip_qwen3* m) {
+  if (m) model_destroy(m);
+}
+
+qi_hip_status qi_hip_kv_cache_create(qi_hip_ctx* ctx, uint32_t layers, uint32_t max_seq,
+                                     uint32_t kv_heads, uint32_t head_dim, qi_hip_kv_cache** out) {
+  if (ctx == nullptr || out == nullptr) return fail(QI_HIP_INVALID_INPUT, "null argument");
+  *out = nullptr;
+  if (ctx->closed) return fail(QI_HIP_INVALID_INPUT, "context is closed");
+  // KvCache::new (cache.rs:25-60)
+  if (layers == 0 || max_seq == 0 || kv_heads == 0 || head_dim == 0)
+    return fail(QI_HIP_INVALID_INPUT, "KV cache dimensions must be greater than zero");
+  qi_hip_kv_cache* c = new qi_hip_kv_cache();
+  c->layers = layers;
+  c->max_seq = max_seq;
+  c->kv_heads = kv_heads;
+  c->head_dim = head_dim;
+  c->cap = (max_seq + kChunk - 1) / kChunk * kChunk;
+  const uint64_t per = static_cast<uint64_t>(layers) * kv_heads * head_dim * c->cap;
+  std::lock_guard<std::mutex> lock(ctx->mu);
+  qi_hip_status s = QI_HIP_OK;
+  hipError_t e = hipSetDevice(ctx->device);
+  if (e != hipSuccess) s = hip_fail(e, "set device");
+  if (s == QI_HIP_OK) s = dev_alloc_t(&c->keys, per, "alloc KV cache");
+  if (s == QI_HIP_OK) s = dev_alloc_t(&c->values, per, "alloc KV cache");
+  if (s == QI_HIP_OK) s = dev_alloc_t(&c->tok, c->cap + 1, "alloc token history");
+  if (s == QI_HIP_OK) s = dev_alloc_t(&c->len_dev, 1, "alloc cache length");
+  if (s == QI_HIP_OK) {
+    // positions past the length are never read, but keep them finite
+    e = hipMemsetAsync(c->keys, 0, per * 4, ctx->stream);
+    if (e == hipSuccess) e = hipMemsetAsync(c->values, 0, per * 4, ctx->stream);
+    if (e == hipSuccess) e = hipMemsetAsync(c->len_dev, 0, 4, ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) s = hip_fail(e, "clear KV cache");
+  }
+  if (s != QI_HIP_OK) {
+    dev_free(c->keys);
+    dev_free(c->values);
+    dev_free(c->tok);
+    dev_free(c->len_dev);
+    delete c;
+    return s;
+  }
+  ctx->refs.fetch_add(1, std::memory_order_relaxed);
+  c->ctx = ctx;
+  *out = c;
+  return QI_HIP_OK;
+}
+
+qi_hip_status qi_hip_kv_cache_length(const qi_hip_kv_cache* c, uint64_t* out) {
+  if (c == nullptr || out == nullptr) return fail(QI_HIP_INVALID_INPUT, "null argument");
+  *out = c->len;
+  return QI_HIP_OK;
+}
+
+qi_hip_status qi_hip_kv_cache_reset(qi_hip_kv_cache* c) {
+  if (c == nullptr) return fail(QI_HIP_INVALID_INPUT, "null cache");
+  std::lock_guard<std::mutex> lock(c->ctx->mu);
+  QI_HIP_TRY(hipSetDevice(c->ctx->device), "set device");
+  QI_HIP_TRY(hipMemsetAsync(c->len_dev, 0, 4, c->ctx->stream), "reset cache");
+  QI_HIP_TRY(hipStreamSynchronize(c->ctx->stream), "reset cache");
+  c->len = 0;
+  return QI_HIP_OK;
+}
+
+void qi_hip_kv_cache_free(qi_hip_kv_cache* c) {
+  if (c == nullptr) return;
+  qi_hip_ctx* ctx = c->ctx;
+  {
+    std::lock_guard<std::mutex> lock(ctx->mu);
+    (void)hipSetDevice(ctx->device);
+    (void)hipStreamSynchronize(ctx->stream);
+    if (c->exec) (void)hipGraphExecDestroy(c->exec);
+    for (void* p : {static_cast<void*>(c->keys), static_cast<void*>(c->values),
+                    static_cast<void*>(c->tok), static_cast<void*>(c->len_dev),
+                    static_cast<void*>(c->pm), static_cast<void*>(c->pl), static_cast<void*>(c->po)})
+      dev_free(p);
+  }
+  qi_abi::ctx_release(ctx);
+  delete c;
+}
+
+qi_hip_status qi_hip_qwen3_forward(qi_hip_qwen3* m, qi_hip_kv_cache* c, const int32_t* tokens,
+                                   uint64_t count, float* last_logits, int32_t* next_token) {
+  qi_hip_status s = check_pair(m, c);
+  if (s != QI_HIP_OK) return s;
+  if (tokens == nullptr && count > 0) return fail(QI_HIP_INVALID_INPUT, "null token array");
+  std::lock_guard<std::mutex> lock(m->ctx->mu);
+  QI_HIP_TRY(hipSetDevice(m->ctx->device), "set device");
+  hipStream_t st = m->ctx->stream;
+  const uint64_t start = c->len;
+  if ((s = forward_locked(m, c, tokens, count)) != QI_HIP_OK) {
+    (void)hipStreamSynchronize(st);
+    return s;
+  }
+  if (last_logits)
+    QI_HIP_TRY(hipMemcpyAsync(last_logits, m->logits, static_cast<uint64_t>(m->cfg.vocab_size) * 4,
+                              hipMemcpyDeviceToHost, st), "read logits");
+  int32_t tok = 0;
+  QI_HIP_TRY(hipMemcpyAsync(&tok, c->tok + start + count, 4, hipMemcpyDeviceToHost, st), "read token");
+  QI_HIP_TRY(hipStreamSynchronize(st), "synchronize");
+  if (next_token) {
+    if ((s = read_bad(m)) != QI_HIP_OK) return s;
+    *next_token = tok;
+  }
+  return QI_HIP_OK;
+}
+
+qi_hip_status qi_hip_qwen3_generate(qi_hip_qwen3* m, qi_hip_kv_cache* c, const int32_t* prompt,
+                                    uint64_t n, uint64_t max_new, int32_t eos, int32_t* out,
+                                    uint64_t* out_count) {
+  qi_hip_status s = check_pair(m, c);
+  if (s != QI_HIP_OK) return s;
+  if (out_count == nullptr || (out == nullptr && max_new > 0) || (prompt == nullptr && n > 0))
+    return fail(QI_HIP_INVALID_INPUT, "null argument");
+  *out_count = 0;
+  if (n == 0) return fail(QI_HIP_INVALID_INPUT, "streaming generation requires a non-empty prompt");
+  std::lock_guard<std::mutex> lock(m->ctx->mu);
+  QI_HIP_TRY(hipSetDevice(m->ctx->device), "set device");
+  hipStream_t st = m->ctx->stream;
+  m->timing = qi_hip_qwen3_timing{};
+  QI_HIP_TRY(hipEventRecord(m->ev[0], st), "record event");
+  if ((s = forward_locked(m, c, prompt, n)) != QI_HIP_OK) {
+    (void)hipStreamSynchronize(st);
+    return s;
+  }
+  QI_HIP_TRY(hipEventRecord(m->ev[1], st), "record event");
+  // Token i (i = 0..max_new-1) is tok[base + i]: token 0 comes from the prompt
+  // forward and forwarding token i produces token i + 1. Every selected token
+  // but an EOS is forwarded (generation.rs:189-199). Without an EOS all steps
+  // are enqueued back to back; with one, steps run in batches of 16 and the
+  // host looks at the tokens between batches, undoing the steps past an EOS
+  // (their cache positions are dropped by resetting the length).
+  const uint64_t base = c->len;
+  const uint64_t limit = c->max_seq < m->cfg.max_position_embeddings ? c->max_seq
+                                                                     : m->cfg.max_position_embeddings;
+  std::vector<int32_t> toks(max_new + 1);
+  uint64_t forwarded = 0, checked = 0, count = max_new;
+  const uint64_t batch = eos < 0 ? (max_new ? max_new : 1) : 16;
+  while (true) {
+    if (eos >= 0 && checked < max_new) {
+      const uint64_t upto = forwarded < max_new - 1 ? forwarded : max_new - 1;  // tokens 0..upto exist
+      QI_HIP_TRY(hipMemcpyAsync(toks.data() + checked, c->tok + base + checked,
+                                (upto + 1 - checked) * 4, hipMemcpyDeviceToHost, st), "read tokens");
+      QI_HIP_TRY(hipStreamSynchronize(st), "synchronize");
+      bool hit = false;
+      for (uint64_t i = checked; i <= upto; ++i)
+        if (toks[i] == eos) {
+          count = i + 1;
+          hit = true;
+          break;
+        }
+      checked = upto + 1;
+      if (hit) {
+        if (forwarded > count - 1) {
+          // only tokens 0..count-2 were to be forwarded
+          c->len = base + (count - 1);
+          const uint32_t len32 = static_cast<uint32_t>(c->len);
+          QI_HIP_TRY(hipMemcpyAsync(c->len_dev, &len32, 4, hipMemcpyHostToDevice, st), "reset length");
+          QI_HIP_TRY(hipStreamSynchronize(st), "synchronize");
+          forwarded = count - 1;
+        }
+        break;
+      }
+    }
+    if (forwarded >= max_new) break;
+    uint64_t todo = max_new - forwarded < batch ? max_new - forwarded : batch;
+    if (c->len + 1 > limit) {
+      (void)hipStreamSynchronize(st);
+      return fail(QI_HIP_INVALID_INPUT, "KV cache capacity is smaller than the requested sequence");
+    }
+    if (c->len + todo > limit) todo = limit - c->len;
+    for (uint64_t i = 0; i < todo; ++i) {
+      if ((s = decode_step(m, c)) != QI_HIP_OK) {
+        (void)hipStreamSynchronize(st);
+        return s;
+      }
+      c->len += 1;
+      ++forwarded;
+    }
+  }
+  QI_HIP_TRY(hipEventRecord(m->ev[2], st), "record event");
+  if (count > checked)
+    QI_HIP_TRY(hipMemcpyAsync(toks.data() + checked, c->tok + base + checked, (count - checked) * 4,
+                              hipMemcpyDeviceToHost, st), "read tokens");
+  QI_HIP_TRY(hipStreamSynchronize(st), "synchronize");
+  if ((s = read_bad(m)) != QI_HIP_OK) return s;
+  memcpy(out, toks.data(), count * 4);
+  *out_count = count;
+  float ms = 0.0f;
+  if (hipEventElapsedTime(&ms, m->ev[0], m->ev[1]) == hipSuccess) m->timing.prefill_ms = ms;
+  if (hipEventElapsedTime(&ms, m->ev[1], m->ev[2]) == hipSuccess) m->timing.decode_ms = ms;
+  m->timing.prompt_tokens = n;
+  m->timing.decode_steps = forwarded;
+  return QI_HIP_OK;
+}
+
+qi_hip_status qi_hip_qwen3_last_timing(const qi_hip_qwen3* m, qi_hip_qwen3_timing* out) {
+  if (m == nullptr || out == nullptr) return fail(QI_HIP_INVALID_INPUT, "null argument");
+  *out = m->timing;
+  return QI_HIP_OK;
+}
+
+}  // extern "C"

@@ -167,6 +167,25 @@ def linear_layout_case():
     }
 
 
+def decoder_cases():
+    return [
+        # backends/cpu/src/tests.rs:136-143: half-split RoPE rotation
+        {"name": "half_split_rope_rotation", "source": "backends/cpu/src/tests.rs:136-143",
+         "op": "apply_rope", "input_shape": [1, 1, 4], "input": [1.0, 2.0, 3.0, 4.0],
+         "cos": [0.0, 1.0], "sin": [1.0, 0.0], "expected": [-3.0, 2.0, 1.0, 4.0]},
+        # crates/quantinfer-runtime/src/qwen3/tests.rs:22-99: the constant-filled
+        # one-layer model; prefill [1, 2] then decode [3]
+        {"name": "qwen3_filled_prefill_decode", "source": "runtime/src/qwen3/tests.rs:22-99",
+         "config": {"vocab": 16, "hidden": 8, "intermediate": 16, "layers": 1, "heads": 2,
+                    "kv_heads": 1, "head_dim": 4, "max_positions": 32, "eps": 1e-6,
+                    "theta": 1000000.0},
+         "fill": {"embedding": 0.01, "norms": 1.0, "projections": 0.01, "lm_head": 0.01},
+         "prefill_tokens": [1, 2], "decode_tokens": [3],
+         "expected_prefill_logits_shape": [2, 16], "expected_length_after_prefill": 2,
+         "expected_decode_logits_shape": [1, 16], "expected_length_after_decode": 3},
+    ]
+
+
 def main():
     data = {
         "about": "Known answers transcribed from aiqubits/quantinfer tests (data only).",
@@ -175,6 +194,7 @@ def main():
         "quantizer_bounds": quantizer_bounds(),
         "numerical_gate": numerical_gate(),
         "linear_layout": linear_layout_case(),
+        "decoder": decoder_cases(),
     }
     path = os.path.join(HERE, "reference_known_answers.json")
     with open(path, "w") as f:

@@ -88,3 +88,72 @@ def sequential_f32(x, w_rows):
     for i in range(k):
         acc = (acc + (x[:, i:i + 1] * w[None, :, i]).astype(f32)).astype(f32)
     return acc
+
+
+# ------------------------------------------------------------------ Qwen3
+# Float64 restatement of the Qwen3 forward pass (runtime/src/qwen3/mod.rs:
+# 117-378, attention.rs:7-141, cpu backend.rs:172-298), vectorised and written
+# without looking at oracle/qwen3.c: softmax attention over all cached keys,
+# rotate-half RoPE, RMSNorm. It checks the C oracle within rounding, not bit
+# for bit.
+
+def _rms64(x, w, eps):
+    ms = np.mean(x * x, axis=-1, keepdims=True)
+    return x / np.sqrt(ms + eps) * w
+
+
+def _rope64(x, pos, theta):
+    # x [T, heads, d]; pair (i, i + d/2) rotated by pos * theta^(-2i/d)
+    d = x.shape[-1]
+    half = d // 2
+    inv = theta ** (-(2.0 * np.arange(half)) / d)
+    ang = pos[:, None] * inv[None, :]
+    c, s = np.cos(ang)[:, None, :], np.sin(ang)[:, None, :]
+    a, b = x[..., :half], x[..., half:]
+    return np.concatenate([a * c - b * s, a * s + b * c], axis=-1)
+
+
+class Qwen3F64:
+    """Same interface as the oracle model (cfg in oracle field names, layers
+    as dicts of dequantized output-row weights), all arithmetic in float64."""
+
+    def __init__(self, cfg, embedding, layers, final_norm, head):
+        self.c = cfg
+        self.emb = np.asarray(embedding, np.float64)
+        self.layers = [{k: np.asarray(v, np.float64) for k, v in L.items()} for L in layers]
+        self.fn = np.asarray(final_norm, np.float64)
+        self.head = np.asarray(head, np.float64)
+        self.keys = [np.zeros((0, cfg["kv_heads"], cfg["head_dim"])) for _ in layers]
+        self.values = [np.zeros((0, cfg["kv_heads"], cfg["head_dim"])) for _ in layers]
+
+    def forward(self, tokens):
+        c = self.c
+        hq, hk, d = c["heads"], c["kv_heads"], c["head_dim"]
+        t = len(tokens)
+        start = self.keys[0].shape[0]
+        pos = np.arange(start, start + t, dtype=np.float64)
+        h = self.emb[np.asarray(tokens)]
+        for li, L in enumerate(self.layers):
+            x = _rms64(h, L["input_norm"], c["eps"])
+            q = (x @ L["q"].T).reshape(t, hq, d)
+            k = (x @ L["k"].T).reshape(t, hk, d)
+            v = (x @ L["v"].T).reshape(t, hk, d)
+            q = _rope64(_rms64(q, L["q_norm"], c["eps"]), pos, c["theta"])
+            k = _rope64(_rms64(k, L["k_norm"], c["eps"]), pos, c["theta"])
+            self.keys[li] = np.concatenate([self.keys[li], k])
+            self.values[li] = np.concatenate([self.values[li], v])
+            K, V = self.keys[li], self.values[li]
+            g = hq // hk
+            att = np.empty((t, hq, d))
+            for head in range(hq):
+                kh, vh = K[:, head // g, :], V[:, head // g, :]
+                sc = (q[:, head, :] @ kh.T) / np.sqrt(d)
+                mask = np.arange(K.shape[0])[None, :] > (start + np.arange(t))[:, None]
+                sc = np.where(mask, -np.inf, sc)
+                sc = np.exp(sc - sc.max(axis=1, keepdims=True))
+                att[:, head, :] = (sc / sc.sum(axis=1, keepdims=True)) @ vh
+            h = h + att.reshape(t, hq * d) @ L["o"].T
+            x = _rms64(h, L["post_norm"], c["eps"])
+            gt, up = x @ L["gate"].T, x @ L["up"].T
+            h = h + (gt / (1.0 + np.exp(-gt)) * up) @ L["down"].T
+        return _rms64(h, self.fn, c["eps"]) @ self.head.T
