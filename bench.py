@@ -9,6 +9,15 @@ Infinity Cache) are rotated so every step streams its weight from HBM.
 Prints ONE JSON line (the driver's contract) with a `roofline` object for the
 GEMV kernel (algorithmic bytes / measured average kernel duration vs 8 TB/s)
 and a `cpu_baseline` object (the oracle's CpuScalar port on one host core).
+The line also carries `e2e`, the second half of the metric: Qwen3-8B-shape
+decode tokens/s of the GPU-resident decoder (36
+Q4_K layers, Q6_K head, 512-token prompt, 128 greedy decode steps), with its
+own roofline (bytes one decode step moves vs 8 TB/s) and CPU baseline.
+
+Inputs are synthetic. Weight blocks are drawn directly (synth_blocks): uniform
+random codes and sub-scales with f16-exact scales of the size the reference
+quantizer gives N(0, 0.02^2) weights. Kernel time does not depend on the
+values, and nothing in the measured legs touches the test oracle.
 """
 from __future__ import annotations
 
@@ -43,17 +52,46 @@ def traffic_from_profile(name: str):
     return float(m.group(1)) if m else None
 
 
+# f16-exact scale magnitudes of quantized N(0, 0.02^2) blocks: (d, dmin)
+SCALE_SIZE = {1: (0.05 / 127, 0.0), 2: (0.05 / 7, 0.0), 3: (1.7e-4, 1.3e-3), 4: (8.5e-5, 1.3e-3),
+              5: (2.4e-5, 0.0)}
+
+
+def synth_blocks(qtype: int, count: int, seed: int):
+    """`count` random valid logical blocks (bench input only): random bytes in
+    every code and sub-scale field, f16-exact d (and dmin) of the quantizer's
+    magnitude, Q4_0 codes masked to four bits."""
+    import numpy as np
+    import quantinfer_amd as qa
+
+    dt = qa.BLOCK_DTYPES[qtype]
+    rng = np.random.default_rng(seed)
+    b = np.frombuffer(rng.bytes(count * dt.itemsize), dtype=np.uint8).copy().view(dt)
+    d, dmin = SCALE_SIZE[qtype]
+    f16 = lambda v: v.astype(np.float16).astype(np.float32)  # noqa: E731
+    b["scale"] = f16(rng.uniform(0.7, 1.3, count) * d)
+    if dmin:
+        b["min_scale"] = f16(rng.uniform(0.7, 1.3, count) * dmin)
+    if qtype == 2:
+        b["values"] &= 15
+    return b
+
+
+def normal(seed: int, n: int, std: float = 1.0):
+    import numpy as np
+    return (np.random.default_rng(seed).standard_normal(n, dtype=np.float32) * np.float32(std))
+
+
 def gpu_measure(qtype: int, steps: int, warmup: int, copies_mb: float = 512.0):
     import quantinfer_amd as qa
-    from oracle import pyoracle as po  # input generation only (the quantizer restatement)
     from quantinfer_amd import hiprt
 
     ctx = qa.Context(0)
-    blocks = po.make_weights(qtype, K, N, seed=0x5EED0000 + qtype, outliers=qtype >= 3)
+    blocks = synth_blocks(qtype, N * (K // BLOCK[qtype]), seed=0x5EED0000 + qtype)
     wbytes = N * (K // BLOCK[qtype]) * WIRE[qtype]
     copies = max(1, int(-(-copies_mb * 1e6 // wbytes)))
     weights = [ctx.weights(qtype, qa.OUTPUT_ROWS, K, N, blocks) for _ in range(copies)]
-    x = hiprt.DeviceBuffer.from_array(po.fill_normal(0x5EED1000, M * K).reshape(M, K))
+    x = hiprt.DeviceBuffer.from_array(normal(0x5EED1000, M * K).reshape(M, K))
     y = hiprt.DeviceBuffer(M * N * 4)
     stream = hiprt.Stream()
 
@@ -120,13 +158,12 @@ def gemm_bench(qtype: int, m: int, k: int, n: int, steps: int, warmup: int) -> d
     back-to-back linear calls on resident inputs, event-timed on the launch
     stream (each call is the f16 activation conversion plus the GEMM)."""
     import quantinfer_amd as qa
-    from oracle import pyoracle as po  # input generation only
     from quantinfer_amd import hiprt
 
     ctx = qa.Context(0)
-    blocks = po.make_weights(qtype, k, n, seed=0x5EED0010 + qtype, outliers=qtype >= 3)
+    blocks = synth_blocks(qtype, n * (k // BLOCK[qtype]), seed=0x5EED0010 + qtype)
     weights = [ctx.weights(qtype, qa.OUTPUT_ROWS, k, n, blocks) for _ in range(2)]
-    x = hiprt.DeviceBuffer.from_array(po.fill_normal(0x5EED3000, m * k).reshape(m, k))
+    x = hiprt.DeviceBuffer.from_array(normal(0x5EED3000, m * k).reshape(m, k))
     y = hiprt.DeviceBuffer(m * n * 4)
     stream = hiprt.Stream()
     for i in range(warmup):
@@ -153,7 +190,7 @@ def gemm_bench(qtype: int, m: int, k: int, n: int, steps: int, warmup: int) -> d
         "value": round(tflops, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": steps,
         "warmup": warmup, "ms_per_step": round(ms, 5), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "f16 operands, f32 accumulation",
-        "data": "synthetic: N(0,0.02^2) weights quantized by the restated reference quantizer; x ~ N(0,1)",
+        "data": "synthetic: random Q-format blocks with f16-exact scales (synth_blocks); x ~ N(0,1)",
         "config": {"workload": f"{qname}_gemm_output_rows_m{m}_k{k}_n{n}", "qtype": qname,
                    "m": m, "k": k, "n": n, "mode": "mfma", "device": name},
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": MFMA_F16_PEAK_TFLOPS,
@@ -167,8 +204,8 @@ def cpu_baseline(qtype: int, repeats: int = 3):
     as the reference's output-row kernels are), pinned to one host core."""
     from oracle import pyoracle as po
 
-    blocks = po.make_weights(qtype, K, N, seed=0x5EED0000 + qtype, outliers=qtype >= 3)
-    x = po.fill_normal(0x5EED1000, M * K).reshape(M, K)
+    blocks = synth_blocks(qtype, N * (K // BLOCK[qtype]), seed=0x5EED0000 + qtype)
+    x = normal(0x5EED1000, M * K).reshape(M, K)
     try:
         old = os.sched_getaffinity(0)
         os.sched_setaffinity(0, {min(old)})
@@ -192,6 +229,153 @@ def cpu_baseline(qtype: int, repeats: int = 3):
     }
 
 
+# --------------------------------------------------------------- e2e decode
+
+QWEN3_8B = dict(vocab_size=151936, hidden_size=4096, intermediate_size=12288, num_hidden_layers=36,
+                num_attention_heads=32, num_key_value_heads=8, head_dim=128,
+                max_position_embeddings=40960, rms_norm_eps=1e-6, rope_theta=1e6)
+E2E_PROMPT, E2E_NEW = 512, 128
+
+
+def e2e_shapes(cfg):
+    """(name, K, N) of the seven projections of one layer."""
+    H, I = cfg["hidden_size"], cfg["intermediate_size"]
+    QS = cfg["num_attention_heads"] * cfg["head_dim"]
+    KS = cfg["num_key_value_heads"] * cfg["head_dim"]
+    return [("q_proj", H, QS), ("k_proj", H, KS), ("v_proj", H, KS), ("o_proj", QS, H),
+            ("gate_proj", H, I), ("up_proj", H, I), ("down_proj", I, H)]
+
+
+def e2e_layer(cfg, index: int):
+    import numpy as np
+    rng = np.random.default_rng(0x5EED4000 + index)
+    H, hd = cfg["hidden_size"], cfg["head_dim"]
+    layer = {n: (1.0 + 0.05 * rng.standard_normal(d)).astype(np.float32)
+             for n, d in (("input_layernorm", H), ("q_norm", hd), ("k_norm", hd),
+                          ("post_attention_layernorm", H))}
+    for j, (name, k, n) in enumerate(e2e_shapes(cfg)):
+        layer[name] = (3, 1, synth_blocks(3, n * (k // 256), seed=(index << 4) + j + 0x5EED5000))
+    return layer
+
+
+def e2e_step_bytes(cfg, position: int) -> int:
+    """HBM bytes one decode step at `position` must move: every layer's Q4_K
+    weights and the Q6_K head (wire bytes), the keys and values of positions
+    0..position read and one position written (f32), the embedding row and the
+    f32 activation rows of each GEMV."""
+    H, V = cfg["hidden_size"], cfg["vocab_size"]
+    L, hd, kvh = cfg["num_hidden_layers"], cfg["head_dim"], cfg["num_key_value_heads"]
+    weights = sum(n * (k // 256) * 144 + (k + n) * 4 for _, k, n in e2e_shapes(cfg))
+    kv = (position + 2) * kvh * hd * 4 * 2
+    head = V * (H // 256) * 210 + (H + V) * 4
+    return L * (weights + kv) + head + H * 4
+
+
+def e2e_bench(repeats: int = 3, with_cpu: bool = True) -> dict:
+    """Qwen3-8B-shape decode tokens/s: build the random-init model on the
+    device, then `repeats` x (reset cache, 512-token prompt, 128 greedy decode
+    steps); the decode time is the HIP-event time of the decode steps."""
+    import numpy as np
+    import quantinfer_amd as qa
+
+    cfg = dict(QWEN3_8B)
+    t0 = time.perf_counter()
+    ctx = qa.Context(0)
+    model = qa.Qwen3(ctx, cfg)
+    model.set_embedding(normal(0x5EED6000, cfg["vocab_size"] * cfg["hidden_size"], 0.02))
+    for i in range(cfg["num_hidden_layers"]):
+        model.set_layer(i, e2e_layer(cfg, i))
+    head = synth_blocks(5, cfg["vocab_size"] * (cfg["hidden_size"] // 256), seed=0x5EED7000)
+    final_norm = (1.0 + 0.05 * np.random.default_rng(0x5EED7001)
+                  .standard_normal(cfg["hidden_size"])).astype(np.float32)
+    model.set_output(final_norm, (5, 1, head))
+    build_s = time.perf_counter() - t0
+    cache = model.kv_cache(E2E_PROMPT + E2E_NEW)
+    prompt = np.random.default_rng(0x5EED7002).integers(0, cfg["vocab_size"], E2E_PROMPT)
+    model.generate(cache, prompt, E2E_NEW)  # warm-up: workspaces and the decode graph
+    runs, tokens = [], None
+    for _ in range(repeats):
+        cache.reset()
+        out = model.generate(cache, prompt, E2E_NEW)
+        t = model.last_timing()
+        if tokens is not None and out != tokens:
+            raise RuntimeError("decode is not deterministic across runs")
+        tokens = out
+        runs.append((t.decode_ms, t.prefill_ms, t.decode_steps))
+    device = ctx.device_name()
+    cache.free()
+    model.free()
+    ctx.close()
+    decode_ms = statistics.median(r[0] for r in runs)
+    prefill_ms = statistics.median(r[1] for r in runs)
+    steps = runs[0][2]
+    ms_tok = decode_ms / steps
+    tok_s = 1e3 / ms_tok
+    avg_bytes = sum(e2e_step_bytes(cfg, E2E_PROMPT + i) for i in range(steps)) / steps
+    achieved = avg_bytes / (ms_tok * 1e-3) / 1e9
+    return {
+        "metric": "Qwen3-8B-shape decode tok/s",
+        "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": steps,
+        "warmup": 1, "ms_per_step": round(ms_tok, 5), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32 activations, Q4_K linears (Q6_K head), f32 KV cache",
+        "data": "synthetic random-init model: random Q4_K/Q6_K blocks with f16-exact scales, "
+                "N(0,0.02^2) f32 embedding, N(1,0.05^2) norms; uniform random prompt ids",
+        "config": {"workload": "qwen3_8b_shape_decode_prompt512_new128", "layers": 36,
+                   "hidden": 4096, "heads": 32, "kv_heads": 8, "head_dim": 128,
+                   "intermediate": 12288, "vocab": 151936, "prompt_tokens": E2E_PROMPT,
+                   "decode_steps": steps, "mode": "auto (GEMV decode, MFMA GEMM prefill)",
+                   "repeats": repeats, "device": device},
+        "prefill_tok_s": round(E2E_PROMPT / (prefill_ms * 1e-3), 1),
+        "prefill_ms": round(prefill_ms, 3),
+        "model_build_s": round(build_s, 1),
+        "roofline": {"bound": "hbm", "scope": "one whole decode step (all kernels of a token)",
+                     "achieved": round(achieved, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBPS, 4),
+                     "bytes_per_step": int(avg_bytes), "traffic": None},
+        "cpu_baseline": e2e_cpu_baseline(cfg) if with_cpu else None,
+    }
+
+
+def e2e_cpu_baseline(cfg) -> dict:
+    """The oracle's CpuScalar port on one pinned core, on a bounded sample:
+    the seven Q4_K output-row matmuls of one layer at M=1 and the f32 LM head
+    (the reference dequantizes a Q6_K head to f32 at load,
+    runtime/src/qwen3/loader.rs:47-61), scaled to 36 layers per token.
+    Attention and the norms (under 1% of the work) are left out."""
+    import numpy as np
+    from oracle import pyoracle as po
+
+    layer = e2e_layer(cfg, 0)
+    H, V = cfg["hidden_size"], cfg["vocab_size"]
+    head = po.dequantize(5, synth_blocks(5, V * (H // 256), seed=0x5EED7000)).reshape(V, H)
+    try:
+        old = os.sched_getaffinity(0)
+        os.sched_setaffinity(0, {min(old)})
+    except (AttributeError, OSError):
+        old = None
+    try:
+        t_layer = 0.0
+        for name, k, n in e2e_shapes(cfg):
+            x = normal(0x5EED8000, k).reshape(1, k)
+            t = time.perf_counter()
+            po.matmul_output_rows(3, x, layer[name][2], n)
+            t_layer += time.perf_counter() - t
+        x = normal(0x5EED8001, H).reshape(1, H)
+        t = time.perf_counter()
+        po.linear_rows(x, head, 1)
+        t_head = time.perf_counter() - t
+    finally:
+        if old is not None:
+            os.sched_setaffinity(0, old)
+    sec = cfg["num_hidden_layers"] * t_layer + t_head
+    del head
+    return {"value": round(1.0 / sec, 4), "unit": "tok/s", "cores": 1, "kind": "port",
+            "sample": f"one layer's 7 Q4_K projections ({t_layer:.2f} s) x36 + f32 LM head "
+                      f"({t_head:.2f} s) at M=1: {sec:.1f} s per decode token; oracle C port of "
+                      f"CpuScalar (matmul.rs:282-332, :92-117), 1 pinned core"}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -200,8 +384,10 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="time device-to-device copies of 256 MiB instead (counter calibration)")
-    ap.add_argument("--workload", choices=["gemv", "gemm"], default="gemv",
-                    help="gemv: the headline decode GEMV (default); gemm: the MFMA prefill GEMM")
+    ap.add_argument("--workload", choices=["gemv", "gemm", "e2e"], default="gemv",
+                    help="gemv: the headline decode GEMV, with the e2e decode line embedded "
+                         "(default); gemm: the MFMA prefill GEMM; e2e: Qwen3-8B-shape decode only")
+    ap.add_argument("--no-e2e", action="store_true", help="gemv: leave out the e2e decode run")
     ap.add_argument("--qtype", default="q4_k", help="gemm only: q8_0, q4_0, q4_k, q5_k or q6_k")
     ap.add_argument("--mkn", default="2048,4096,12288", help="gemm only: M,K,N")
     args = ap.parse_args()
@@ -217,6 +403,10 @@ def main():
         qt = {"q8_0": 1, "q4_0": 2, "q4_k": 3, "q5_k": 4, "q6_k": 5}[args.qtype]
         m, k, n = (int(v) for v in args.mkn.split(","))
         print(json.dumps(gemm_bench(qt, m, k, n, min(args.steps, 50), min(args.warmup, 5))))
+        return
+
+    if args.workload == "e2e":
+        print(json.dumps(e2e_bench(with_cpu=not args.no_cpu)))
         return
 
     qtype = 3  # Q4_K
@@ -239,8 +429,7 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
-        "data": "synthetic: N(0,0.02^2) weights with 0.5% N(0,0.2^2) outliers, Q4_K-quantized "
-                "by the restated reference quantizer; x ~ N(0,1)",
+        "data": "synthetic: random Q4_K blocks with f16-exact d/dmin (synth_blocks); x ~ N(0,1)",
         "config": {"workload": "q4_k_gemv_output_rows_m1_k4096_n14336", "qtype": "q4_k",
                    "m": M, "k": K, "n": N, "mode": "f32", "weight_copies": g["copies"],
                    "device": g["device"]},
@@ -254,6 +443,8 @@ def main():
         },
         "cpu_baseline": None if args.no_cpu else cpu_baseline(qtype),
     }
+    if not args.no_e2e:
+        line["e2e"] = e2e_bench(with_cpu=not args.no_cpu)
     print(json.dumps(line))
 
 

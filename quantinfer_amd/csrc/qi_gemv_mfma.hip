@@ -147,7 +147,8 @@ __device__ __forceinline__ void store_half(const HalfX& o, const Item& it, bool 
 // PRE: the activation records were built by gemv_digits_kernel (a.digits);
 // the workgroup copies its chunk into LDS with global-to-LDS loads instead of
 // building it.
-template <int QT, bool WIDE, int MT, int SW, int D, int WC, bool PRE>
+// XS (one row only): the activation source, see XSource.
+template <int QT, bool WIDE, int MT, int SW, int D, int WC, bool PRE, int XS = kXPlain>
 __global__ __launch_bounds__(64 * SW * WC) void gemv_mfma_kernel(GemvMfmaArgs a) {
   using U = Unit<QT>;
   constexpr int kThreads = 64 * SW * WC;
@@ -217,23 +218,49 @@ __global__ __launch_bounds__(64 * SW * WC) void gemv_mfma_kernel(GemvMfmaArgs a)
       // past the run re-read its last unit)
       HalfX xp[XP];
       Item ip[XP];
+      [[maybe_unused]] HalfX up[XP];  // kXSilu: the up halves
 #pragma unroll
       for (int i = 0; i < XP; ++i) {
         const uint32_t hi = tid + kThreads * i;
         ip[i] = item_of(hi < halves ? hi : 0, units);
-        load_half<QT>(a.x, K, k0, ip[i], xp[i]);
+        if constexpr (XS == kXSilu) {
+          load_half<QT>(a.gu, K, k0, ip[i], xp[i]);
+          load_half<QT>(a.gu + K, K, k0, ip[i], up[i]);
+        } else {
+          load_half<QT>(a.x, K, k0, ip[i], xp[i]);
+        }
       }
 #pragma unroll
       for (int i = 0; i < D; ++i)
         U::template load<WIDE>(trec + min(ku0 + u_begin + i, u_last) * R.bytes, lane, ring[i]);
 
+      // kXSilu: x = gate / (1 + exp(-gate)) * up (backend.rs:224-237)
+      [[maybe_unused]] auto silu = [](HalfX& gx, const HalfX& ux) {
 #pragma unroll
-      for (int i = 0; i < XP; ++i) store_half(xp[i], ip[i], tid + kThreads * i < halves, recs, cu);
+        for (int q = 0; q < 4; ++q) {
+          float4& g4 = gx.v[q];
+          const float4 u4 = ux.v[q];
+          g4 = make_float4(g4.x / (1.0f + expf(-g4.x)) * u4.x, g4.y / (1.0f + expf(-g4.y)) * u4.y,
+                           g4.z / (1.0f + expf(-g4.z)) * u4.z, g4.w / (1.0f + expf(-g4.w)) * u4.w);
+        }
+      };
+#pragma unroll
+      for (int i = 0; i < XP; ++i) {
+        if constexpr (XS == kXSilu) silu(xp[i], up[i]);
+        store_half(xp[i], ip[i], tid + kThreads * i < halves, recs, cu);
+      }
       for (uint32_t h0 = XP * kThreads; h0 < halves; h0 += kThreads) {
         const uint32_t hi = h0 + tid;
         Item it = item_of(hi < halves ? hi : 0, units);
         HalfX xh;
-        load_half<QT>(a.x, K, k0, it, xh);
+        if constexpr (XS == kXSilu) {
+          HalfX uh;
+          load_half<QT>(a.gu, K, k0, it, xh);
+          load_half<QT>(a.gu + K, K, k0, it, uh);
+          silu(xh, uh);
+        } else {
+          load_half<QT>(a.x, K, k0, it, xh);
+        }
         store_half(xh, it, hi < halves, recs, cu);
       }
     }
@@ -366,7 +393,7 @@ uint32_t lds_bytes(int mt, uint32_t chunk_units, int waves) {
   return main > red ? main : red;
 }
 
-template <int QT, bool WIDE, int MT, int SW, int D, int WC>
+template <int QT, bool WIDE, int MT, int SW, int D, int WC, int XS = kXPlain>
 hipError_t launch4(GemvMfmaArgs a, hipStream_t st, uint32_t chunk_target = 0) {
   const uint32_t cap = chunk_target ? chunk_target : (kMaxLds - kZeroBytes) / (MT * kUnitRecBytes);
   a.chunk_units = a.w.units < cap ? a.w.units : cap;
@@ -374,7 +401,7 @@ hipError_t launch4(GemvMfmaArgs a, hipStream_t st, uint32_t chunk_target = 0) {
   // two or more activation rows read records built once per call
   constexpr bool kPre = MT >= 2;
   if (kPre && a.digits == nullptr) return hipErrorInvalidValue;
-  auto kern = gemv_mfma_kernel<QT, WIDE, MT, SW, D, WC, kPre>;
+  auto kern = gemv_mfma_kernel<QT, WIDE, MT, SW, D, WC, kPre, XS>;
   if (bytes > 65536) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(bytes));
@@ -386,7 +413,7 @@ hipError_t launch4(GemvMfmaArgs a, hipStream_t st, uint32_t chunk_target = 0) {
 
 // (wavefronts per workgroup, units in flight per wavefront) for `sw` and the
 // units each wavefront holds
-template <int QT, bool WIDE, int MT>
+template <int QT, bool WIDE, int MT, int XS = kXPlain>
 hipError_t launch_split(const GemvMfmaArgs& a, int sw, hipStream_t st) {
   const uint32_t cap = (kMaxLds - kZeroBytes) / (MT * kUnitRecBytes);
   const uint32_t chunk = a.w.units < cap ? a.w.units : cap;
@@ -405,20 +432,29 @@ hipError_t launch_split(const GemvMfmaArgs& a, int sw, hipStream_t st) {
       // two tiles share the activation prep where the register budget of an
       // 8-wavefront workgroup keeps occupancy (measured: Q4_K and Q8_0 gain,
       // Q4_0/Q5_K/Q6_K lose)
-      if constexpr (QT == kQ4_K || QT == kQ8_0) return launch4<QT, WIDE, MT, 4, 4, 2>(a, st);
-      else return launch4<QT, WIDE, MT, 4, 4, 1>(a, st);
+      if constexpr (QT == kQ4_K || QT == kQ8_0) return launch4<QT, WIDE, MT, 4, 4, 2, XS>(a, st);
+      else return launch4<QT, WIDE, MT, 4, 4, 1, XS>(a, st);
     }
     const uint32_t upw = (chunk + 7) / 8;
-    if (upw <= 2) return launch4<QT, WIDE, MT, 8, 2, 1>(a, st);
+    if (upw <= 2) return launch4<QT, WIDE, MT, 8, 2, 1, XS>(a, st);
     if constexpr (MT == 1) {
-      if (upw > 4) return launch4<QT, WIDE, MT, 8, 8, 1>(a, st);
+      if (upw > 4) return launch4<QT, WIDE, MT, 8, 8, 1, XS>(a, st);
     }
-    return launch4<QT, WIDE, MT, 8, 4, 1>(a, st);
+    return launch4<QT, WIDE, MT, 8, 4, 1, XS>(a, st);
   }
 }
 
 template <int QT, bool WIDE>
 hipError_t launch_m(const GemvMfmaArgs& a, int mt, int sw, hipStream_t st) {
+  if (a.xs != kXPlain) {
+    // the decoder's fused down projection: one row, f16-scale images
+    if constexpr (WIDE) {
+      return hipErrorInvalidValue;
+    } else {
+      if (a.xs != kXSilu || a.gu == nullptr || mt != 1 || a.m != 1) return hipErrorInvalidValue;
+      return launch_split<QT, WIDE, 1, kXSilu>(a, sw, st);
+    }
+  }
   switch (mt) {
     case 1: return launch_split<QT, WIDE, 1>(a, sw, st);
     case 2: return launch_split<QT, WIDE, 2>(a, sw, st);

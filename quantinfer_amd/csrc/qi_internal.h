@@ -28,6 +28,13 @@ hipError_t launch_gemv(int32_t qtype, bool wide, int mt, const GemvArgs& a, cons
                        hipStream_t st);
 
 // Matrix-core decode GEMV (int8 digits of the activations x raw weight codes).
+// Activation source of a one-row GEMV. The decoder fuses the element-wise
+// step before the down projection into the GEMV's activation prep:
+//   kXPlain  x
+//   kXSilu   x = g / (1 + exp(-g)) * u with g = gu[k], u = gu[K + k]
+//            (backends/cpu/src/backend.rs:224-237)
+enum XSource : int { kXPlain = 0, kXSilu = 2 };
+
 struct GemvMfmaArgs {
   View w;
   const float* x;  // [m, k] device, 16-byte aligned rows
@@ -35,6 +42,8 @@ struct GemvMfmaArgs {
   int m;           // rows in this launch (<= compile-time tile)
   uint32_t chunk_units = 0;  // set by the launcher: K units whose activation digits fit LDS
   const uint8_t* digits = nullptr;  // activation records from launch_gemv_digits (2+ rows), or null
+  int xs = kXPlain;  // one row, f16-scale images only
+  const float* gu = nullptr;  // kXSilu: [gate | up] row
 };
 bool gemv_mfma_supported(int32_t qtype, int32_t layout, uint64_t k);
 // Activation records of m rows (digits + window scales, the GEMV's LDS layout)

@@ -6,8 +6,8 @@
 //   embedding + RMSNorm           residual_norm_kernel<EMBED>
 //   q|k|v projection              one fused GEMV/GEMM image (qi_gemv_mfma / qi_gemm)
 //   q_norm/k_norm, RoPE, KV append qk_norm_rope_kernel
-//   GQA attention                 attn_partial_kernel (64 positions per wavefront)
-//                                 + attn_combine_kernel
+//   GQA attention                 attn_kernel (a 4-wavefront workgroup per 64 positions;
+//                                 the last workgroup of a KV head combines the chunks)
 //   o projection                  GEMV/GEMM
 //   residual + RMSNorm            residual_norm_kernel<ADD>
 //   gate|up projection            one fused image
@@ -65,9 +65,11 @@ __device__ __forceinline__ float wave_max(float v) {
 
 // ---------------------------------------------------------------- RMSNorm
 // backends/cpu/src/backend.rs:172-190: out = v * (1/sqrt(mean(v^2) + eps)) * w.
-// EMBED: h = embedding[tok[len + row]] (backend.rs:281-298). ADD: h = h + y
-// (runtime/src/linear.rs:129-142). Then x = RMSNorm(h) * w.
-template <bool EMBED>
+// EMBED: h = embedding[tok[len + row]] (backend.rs:281-298). Otherwise h = h + y
+// (runtime/src/linear.rs:129-142). Then x = RMSNorm(h) * w. A row is held in
+// registers (NV float4 per thread), so every load is issued before the
+// reduction and nothing is read twice.
+template <bool EMBED, int NV>
 __global__ __launch_bounds__(256) void residual_norm_kernel(
     float* __restrict__ h, const float* __restrict__ y, const float* __restrict__ table,
     const int32_t* __restrict__ tok, const uint32_t* __restrict__ len, float* __restrict__ x,
@@ -83,18 +85,28 @@ __global__ __launch_bounds__(256) void residual_norm_kernel(
   } else {
     src = reinterpret_cast<const float4*>(y + static_cast<uint64_t>(r) * hidden);
   }
-  float ss = 0.0f;
-  for (uint32_t i = threadIdx.x; i < n4; i += 256) {
-    float4 v = src[i];
-    if constexpr (!EMBED) {
-      const float4 o = hr[i];
-      v.x = o.x + v.x;
-      v.y = o.y + v.y;
-      v.z = o.z + v.z;
-      v.w = o.w + v.w;
+  const float4* wr = reinterpret_cast<const float4*>(w);
+  float4 v[NV], g[NV];
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const uint32_t i = threadIdx.x + 256u * j;
+    v[j] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    g[j] = v[j];
+    if (i < n4) {
+      v[j] = src[i];
+      g[j] = wr[i];
+      if constexpr (!EMBED) {
+        const float4 o = hr[i];
+        v[j] = make_float4(o.x + v[j].x, o.y + v[j].y, o.z + v[j].z, o.w + v[j].w);
+      }
     }
-    hr[i] = v;
-    ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+  }
+  float ss = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const uint32_t i = threadIdx.x + 256u * j;
+    if (i < n4) hr[i] = v[j];
+    ss += v[j].x * v[j].x + v[j].y * v[j].y + v[j].z * v[j].z + v[j].w * v[j].w;
   }
   ss = wave_sum(ss);
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
@@ -102,10 +114,12 @@ __global__ __launch_bounds__(256) void residual_norm_kernel(
   const float total = (red[0] + red[1]) + (red[2] + red[3]);
   const float inv = 1.0f / sqrtf(total / static_cast<float>(hidden) + eps);
   float4* xr = reinterpret_cast<float4*>(x + static_cast<uint64_t>(r) * hidden);
-  const float4* wr = reinterpret_cast<const float4*>(w);
-  for (uint32_t i = threadIdx.x; i < n4; i += 256) {
-    const float4 v = hr[i], g = wr[i];
-    xr[i] = make_float4(v.x * inv * g.x, v.y * inv * g.y, v.z * inv * g.z, v.w * inv * g.w);
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const uint32_t i = threadIdx.x + 256u * j;
+    if (i < n4)
+      xr[i] = make_float4(v[j].x * inv * g[j].x, v[j].y * inv * g[j].y, v[j].z * inv * g[j].z,
+                          v[j].w * inv * g[j].w);
   }
 }
 
@@ -177,7 +191,7 @@ __global__ __launch_bounds__(64) void qk_norm_rope_kernel(HeadArgs a) {
 // unnormalized output o = sum exp(s - m) v; the combine rescales the chunks by
 // exp(m - max m) (the same softmax, evaluated in pieces).
 struct AttnArgs {
-  const float* q;  // [rows][heads*hd]
+  const float* q;  // [rows][heads*hd] (rotated queries; unfused path)
   const float* keys;
   const float* values;
   const uint32_t* len;
@@ -188,111 +202,270 @@ struct AttnArgs {
   uint32_t row0;  // first row of this batch (blockIdx row 0)
   float scale;
   float* out;  // [rows][heads*hd]
+  // fused path (one decode row): q/k/v straight from the projection
+  const float* qkv;
+  uint32_t row_stride;
+  const float* q_norm;
+  const float* k_norm;
+  float eps;
+  const float* rope_cos;
+  const float* rope_sin;
+  float* keys_w;    // writable views of the same cache (the new position)
+  float* values_w;
+  uint32_t* tickets;  // [batch row][kv head] chunk counters, zero between launches
 };
 
+// RMSNorm of one head from preloaded values (lane owns the pair (lane,
+// lane + hd/2); head_dim <= 128) and RoPE: returns the rotated pair. Lanes past
+// head_dim/2 (`act` false) hold clamped copies and add nothing to the sum.
+__device__ __forceinline__ float2 norm_rope(float x0, float x1, float w0, float w1, float c, float sn,
+                                            float hd, float eps, bool act) {
+  const float ss = wave_sum(act ? x0 * x0 + x1 * x1 : 0.0f);
+  const float inv = 1.0f / sqrtf(ss / hd + eps);
+  const float f = x0 * inv * w0;
+  const float s = x1 * inv * w1;
+  return make_float2(f * c - s * sn, f * sn + s * c);
+}
+
+// Partials are exchanged between the workgroups of one (row, KV head) through
+// device-coherent stores and loads (bypassing the non-coherent per-XCD L2
+// copies), ordered by waiting for the stores before the ticket increment, so
+// no cache-wide writeback or invalidate is needed.
+__device__ __forceinline__ void store_coherent(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_coherent(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+constexpr int kAttnWaves = 4;
+
+// LDS of one attention workgroup: keys [dim][64 positions], values [64][dim],
+// the rotated queries of the group, the new position's key and value.
 template <int HD, int G>
-__global__ __launch_bounds__(64) void attn_partial_kernel(AttnArgs a) {
-  constexpr int DPL = HD / 64;  // dimensions per lane in the value product
-  __shared__ float4 qs[G][HD / 4];
-  const uint32_t c = blockIdx.x, g = blockIdx.y, rb = blockIdx.z, lane = threadIdx.x;
+constexpr uint32_t attn_lds_bytes() {
+  return static_cast<uint32_t>((2 * HD * kChunk + G * HD + 2 * HD) * sizeof(float) + 16);
+}
+
+// One 4-wavefront workgroup per (chunk of 64 positions, KV head, row). The
+// workgroup copies the chunk's keys and values into LDS with global-to-LDS
+// loads, issued before any arithmetic; wavefront w then handles query heads
+// w, w + 4, ... of the KV group: lane t scores position t0 + t, the chunk's
+// softmax pieces (max m, sum l of exp(s - m), unnormalized output o) are
+// published, and the last workgroup of the (row, KV head) combines all chunks
+// of its query heads and resets the ticket.
+// FUSED (one decode row): the query heads are normalized and rotated here from
+// the raw projection, and the workgroup whose chunk holds the new position
+// also normalizes/rotates its key, appends key and value to the cache
+// (KvCache::append, cache.rs:96-125) and uses them for that position.
+template <int HD, int G, bool FUSED>
+__global__ __launch_bounds__(64 * kAttnWaves) void attn_kernel(AttnArgs a) {
+  constexpr int DPL = HD / 64;  // value dimensions per lane
+  constexpr uint32_t P = HD / 2;
+  constexpr int HPW = (G + kAttnWaves - 1) / kAttnWaves;  // query heads per wavefront
+  extern __shared__ __attribute__((aligned(16))) float attn_lds[];
+  float* ks = attn_lds;                  // [HD][64]
+  float* vs = ks + HD * kChunk;          // [64][HD]
+  float* qs = vs + kChunk * HD;          // [G][HD]
+  float* kn = qs + G * HD;               // [HD]
+  float* vn = kn + HD;                   // [HD]
+  uint32_t* flag = reinterpret_cast<uint32_t*>(vn + HD);
+  const uint32_t c = blockIdx.x, g = blockIdx.y, rb = blockIdx.z;
+  const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const uint32_t r = rb + a.row0;
   const uint32_t pos = *a.len + r;
   const uint32_t t0 = c * kChunk;
-  if (t0 > pos) return;  // the combine skips chunks past the query position
-  const float* qg = a.q + (static_cast<uint64_t>(r) * a.heads + g * G) * HD;
-  for (uint32_t i = lane; i < G * HD / 4; i += 64)
-    qs[i / (HD / 4)][i % (HD / 4)] = reinterpret_cast<const float4*>(qg)[i];
-  __syncthreads();
+  if (t0 > pos) return;  // chunks past the query position take no part
+  const uint32_t tp = pos - t0;  // the query position within this chunk (if < 64)
+  const bool owner = FUSED && tp < kChunk;
+  const bool act = lane < P;
+  const uint32_t pl = act ? lane : 0;
+  const float* row = a.qkv + static_cast<uint64_t>(r) * a.row_stride;
 
-  const uint32_t p = t0 + lane;  // < cap (a multiple of 64)
-  const bool valid = p <= pos;
-  const float* kt = a.keys + static_cast<uint64_t>(g) * HD * a.cap + p;
-  float s[G];
+  // 1. prologue operands of this wavefront's query heads (and the new key/value)
+  [[maybe_unused]] float qx0[HPW], qx1[HPW], nq0 = 0, nq1 = 0, cs = 0, sn = 0;
+  [[maybe_unused]] float kx0 = 0, kx1 = 0, nk0 = 0, nk1 = 0, vx[DPL];
+  if constexpr (FUSED) {
 #pragma unroll
-  for (int h = 0; h < G; ++h) s[h] = 0.0f;
-#pragma unroll 4
-  for (int d4 = 0; d4 < HD / 4; ++d4) {
-    const float k0 = kt[static_cast<uint64_t>(4 * d4 + 0) * a.cap];
-    const float k1 = kt[static_cast<uint64_t>(4 * d4 + 1) * a.cap];
-    const float k2 = kt[static_cast<uint64_t>(4 * d4 + 2) * a.cap];
-    const float k3 = kt[static_cast<uint64_t>(4 * d4 + 3) * a.cap];
+    for (int i = 0; i < HPW; ++i) {
+      const uint32_t h = wave + kAttnWaves * i;
+      const uint32_t hc = h < G ? h : 0;
+      qx0[i] = row[(g * G + hc) * HD + pl];
+      qx1[i] = row[(g * G + hc) * HD + pl + P];
+    }
+    nq0 = a.q_norm[pl];
+    nq1 = a.q_norm[pl + P];
+    cs = a.rope_cos[static_cast<uint64_t>(pos) * P + pl];
+    sn = a.rope_sin[static_cast<uint64_t>(pos) * P + pl];
+    if (owner && wave == 0) {
+      const float* ksrc = row + a.heads * HD + g * HD;
+      const float* vsrc = row + (a.heads + a.kv_heads) * HD + g * HD;
+      kx0 = ksrc[pl];
+      kx1 = ksrc[pl + P];
+      nk0 = a.k_norm[pl];
+      nk1 = a.k_norm[pl + P];
 #pragma unroll
-    for (int h = 0; h < G; ++h) {
-      const float4 qv = qs[h][d4];
-      s[h] = fmaf(qv.x, k0, s[h]);
-      s[h] = fmaf(qv.y, k1, s[h]);
-      s[h] = fmaf(qv.z, k2, s[h]);
-      s[h] = fmaf(qv.w, k3, s[h]);
+      for (int j = 0; j < DPL; ++j) vx[j] = vsrc[lane * DPL + j];
     }
   }
-  float e[G], m[G], l[G];
+  // 2. the chunk into LDS, 1 KB per instruction, instructions dealt round robin
+  // to the wavefronts: keys rows 4i..4i+3 (64 positions each, rows cap apart),
+  // values 256 contiguous floats
+  {
+    const float* kt = a.keys + static_cast<uint64_t>(g) * HD * a.cap + t0;
+    const float* vchunk = a.values + (static_cast<uint64_t>(g) * a.cap + t0) * HD;
+    const uint32_t kr = lane >> 4, kc = (lane & 15) * 4;
 #pragma unroll
-  for (int h = 0; h < G; ++h) {
-    const float sc = valid ? s[h] * a.scale : -INFINITY;
-    m[h] = wave_max(sc);
-    e[h] = valid ? expf(sc - m[h]) : 0.0f;
-    l[h] = wave_sum(e[h]);
+    for (int i = static_cast<int>(wave); i < HD / 4; i += kAttnWaves) {
+      __builtin_amdgcn_global_load_lds(
+          kt + static_cast<uint64_t>(4 * i + kr) * a.cap + kc,
+          (__attribute__((address_space(3))) void*)(ks + i * 256), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(
+          vchunk + i * 256 + lane * 4, (__attribute__((address_space(3))) void*)(vs + i * 256), 16, 0,
+          0);
+    }
   }
-  // values: lane owns dimensions lane*DPL .. lane*DPL + DPL - 1
-  const uint32_t nvalid = (pos - t0 + 1) < kChunk ? (pos - t0 + 1) : kChunk;
-  const float* vb = a.values + (static_cast<uint64_t>(g) * a.cap + t0) * HD + lane * DPL;
-  float acc[G][DPL];
+  // 3. rotated queries (and the new key/value) while the chunk is in flight
+  if constexpr (FUSED) {
 #pragma unroll
-  for (int h = 0; h < G; ++h)
+    for (int i = 0; i < HPW; ++i) {
+      const uint32_t h = wave + kAttnWaves * i;
+      const float2 o =
+          norm_rope(qx0[i], qx1[i], nq0, nq1, cs, sn, static_cast<float>(HD), a.eps, act);
+      if (h < G && act) {
+        qs[h * HD + lane] = o.x;
+        qs[h * HD + lane + P] = o.y;
+      }
+    }
+    if (owner && wave == 0) {
+      const float2 o = norm_rope(kx0, kx1, nk0, nk1, cs, sn, static_cast<float>(HD), a.eps, act);
+      float* kw = a.keys_w + static_cast<uint64_t>(g) * HD * a.cap;
+      float* vw = a.values_w + (static_cast<uint64_t>(g) * a.cap + pos) * HD;
+      if (act) {
+        kn[lane] = o.x;
+        kn[lane + P] = o.y;
+        kw[static_cast<uint64_t>(lane) * a.cap + pos] = o.x;
+        kw[static_cast<uint64_t>(lane + P) * a.cap + pos] = o.y;
+      }
 #pragma unroll
-    for (int j = 0; j < DPL; ++j) acc[h][j] = 0.0f;
-  for (uint32_t t = 0; t < nvalid; ++t) {
+      for (int j = 0; j < DPL; ++j) {
+        vn[lane * DPL + j] = vx[j];
+        vw[lane * DPL + j] = vx[j];
+      }
+    }
+  } else {
+    const float* qg = a.q + (static_cast<uint64_t>(r) * a.heads + g * G) * HD;
+    for (uint32_t i = tid; i < G * HD; i += 64 * kAttnWaves) qs[i] = qg[i];
+  }
+  __syncthreads();  // LDS: queries, new key/value, and the DMA'd chunk (vmcnt drained)
+
+  // 4. this wavefront's heads: scores, softmax pieces, value sums
+  const bool valid = t0 + lane <= pos;
+  const uint32_t nvalid = tp + 1 < kChunk ? tp + 1 : kChunk;
+  const bool mine = owner && lane == tp;  // this lane's key is the new one
+  float s[HPW];
+#pragma unroll
+  for (int i = 0; i < HPW; ++i) s[i] = 0.0f;
+#pragma unroll 8
+  for (int d = 0; d < HD; ++d) {
+    const float kv = mine ? kn[d] : ks[d * kChunk + lane];
+#pragma unroll
+    for (int i = 0; i < HPW; ++i) {
+      const uint32_t h = wave + kAttnWaves * i;
+      s[i] = fmaf(qs[(h < G ? h : 0) * HD + d], kv, s[i]);
+    }
+  }
+  float e[HPW], m[HPW], l[HPW];
+#pragma unroll
+  for (int i = 0; i < HPW; ++i) {
+    const float sc = valid ? s[i] * a.scale : -INFINITY;
+    m[i] = wave_max(sc);
+    e[i] = valid ? expf(sc - m[i]) : 0.0f;
+    l[i] = wave_sum(e[i]);
+  }
+  float acc[HPW][DPL];
+#pragma unroll
+  for (int i = 0; i < HPW; ++i)
+#pragma unroll
+    for (int j = 0; j < DPL; ++j) acc[i][j] = 0.0f;
+  // all 64 positions, unrolled: weights come from lane t as scalars; positions
+  // past the query have weight 0 and their (stale) values are masked to 0
+#pragma unroll
+  for (int t = 0; t < static_cast<int>(kChunk); ++t) {
+    const bool in = static_cast<uint32_t>(t) < nvalid;
+    const bool fresh = owner && static_cast<uint32_t>(t) == tp;
     float v[DPL];
-    if constexpr (DPL == 2) {
-      const float2 v2 = *reinterpret_cast<const float2*>(vb + static_cast<uint64_t>(t) * HD);
-      v[0] = v2.x;
-      v[1] = v2.y;
-    } else {
-      v[0] = vb[static_cast<uint64_t>(t) * HD];
+#pragma unroll
+    for (int j = 0; j < DPL; ++j) {
+      const float x = fresh ? vn[lane * DPL + j] : vs[t * HD + lane * DPL + j];
+      v[j] = in ? x : 0.0f;
     }
 #pragma unroll
-    for (int h = 0; h < G; ++h) {
-      const float wt = __shfl(e[h], static_cast<int>(t));
+    for (int i = 0; i < HPW; ++i) {
+      const float wt = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e[i]), t));
 #pragma unroll
-      for (int j = 0; j < DPL; ++j) acc[h][j] = fmaf(wt, v[j], acc[h][j]);
+      for (int j = 0; j < DPL; ++j) acc[i][j] = fmaf(wt, v[j], acc[i][j]);
     }
   }
 #pragma unroll
-  for (int h = 0; h < G; ++h) {
+  for (int i = 0; i < HPW; ++i) {
+    const uint32_t h = wave + kAttnWaves * i;
+    if (h >= G) continue;
     const uint64_t idx = (static_cast<uint64_t>(rb) * a.heads + g * G + h) * a.chunks + c;
     if (lane == 0) {
-      a.pm[idx] = m[h];
-      a.pl[idx] = l[h];
+      store_coherent(a.pm + idx, m[i]);
+      store_coherent(a.pl + idx, l[i]);
     }
-    float* o = a.po + idx * HD + lane * DPL;
 #pragma unroll
-    for (int j = 0; j < DPL; ++j) o[j] = acc[h][j];
+    for (int j = 0; j < DPL; ++j) store_coherent(a.po + idx * HD + lane * DPL + j, acc[i][j]);
   }
-}
 
-template <int HD>
-__global__ __launch_bounds__(64) void attn_combine_kernel(AttnArgs a) {
-  constexpr int DPL = HD / 64;
-  const uint32_t h = blockIdx.x, rb = blockIdx.y, lane = threadIdx.x;
-  const uint32_t r = rb + a.row0;
-  const uint32_t pos = *a.len + r;
+  // 5. the last workgroup of this (row, KV head) combines its query heads
   const uint32_t nc = pos / kChunk + 1;
-  const uint64_t base = (static_cast<uint64_t>(rb) * a.heads + h) * a.chunks;
-  float mx = -INFINITY;
-  for (uint32_t c = 0; c < nc; ++c) mx = fmaxf(mx, a.pm[base + c]);
-  float denom = 0.0f, acc[DPL];
+  __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores are complete
+  __syncthreads();
+  const uint64_t ticket = static_cast<uint64_t>(rb) * a.kv_heads + g;
+  if (tid == 0) *flag = atomicAdd(&a.tickets[ticket], 1u) == nc - 1 ? 1u : 0u;
+  __syncthreads();
+  if (*flag == 0) return;
 #pragma unroll
-  for (int j = 0; j < DPL; ++j) acc[j] = 0.0f;
-  for (uint32_t c = 0; c < nc; ++c) {
-    const float f = expf(a.pm[base + c] - mx);
-    denom = fmaf(f, a.pl[base + c], denom);
-    const float* o = a.po + (base + c) * HD + lane * DPL;
+  for (int i = 0; i < HPW; ++i) {
+    const uint32_t hl = wave + kAttnWaves * i;
+    if (hl >= G) continue;
+    const uint32_t h = g * G + hl;
+    const uint64_t base = (static_cast<uint64_t>(rb) * a.heads + h) * a.chunks;
+    float mx = -INFINITY;
+    for (uint32_t c0 = 0; c0 < nc; c0 += 64)
+      if (c0 + lane < nc) mx = fmaxf(mx, load_coherent(a.pm + base + c0 + lane));
+    mx = wave_max(mx);
+    float denom = 0.0f, out[DPL];
 #pragma unroll
-    for (int j = 0; j < DPL; ++j) acc[j] = fmaf(f, o[j], acc[j]);
+    for (int j = 0; j < DPL; ++j) out[j] = 0.0f;
+    for (uint32_t c0 = 0; c0 < nc; c0 += 64) {
+      const uint32_t n = nc - c0 < 64 ? nc - c0 : 64;
+      const bool have = c0 + lane < nc;
+      const float f = have ? expf(load_coherent(a.pm + base + c0 + lane) - mx) : 0.0f;
+      denom += wave_sum(have ? f * load_coherent(a.pl + base + c0 + lane) : 0.0f);
+      const float* o = a.po + (base + c0) * HD + lane * DPL;
+      for (uint32_t cb = 0; cb < n; cb += 16) {
+        // 16 chunks unrolled; indices past the last chunk re-read it with weight 0
+#pragma unroll
+        for (int cc = 0; cc < 16; ++cc) {
+          const uint32_t ci = cb + cc < n ? cb + cc : n - 1;
+          const float fc = __int_as_float(
+              __builtin_amdgcn_readlane(__float_as_int(f), static_cast<int>((cb + cc) & 63)));
+          const float w = cb + cc < n ? fc : 0.0f;
+#pragma unroll
+          for (int j = 0; j < DPL; ++j)
+            out[j] = fmaf(w, load_coherent(o + static_cast<uint64_t>(ci) * HD + j), out[j]);
+        }
+      }
+    }
+    float* dst = a.out + (static_cast<uint64_t>(r) * a.heads + h) * HD + lane * DPL;
+#pragma unroll
+    for (int j = 0; j < DPL; ++j) dst[j] = out[j] / denom;
   }
-  float* out = a.out + (static_cast<uint64_t>(r) * a.heads + h) * HD + lane * DPL;
-#pragma unroll
-  for (int j = 0; j < DPL; ++j) out[j] = acc[j] / denom;
+  if (tid == 0) atomicExch(&a.tickets[ticket], 0u);
 }
 
 // --------------------------------------------------------------- SiLU*up
@@ -439,7 +612,8 @@ struct qi_hip_qwen3 {
   int32_t* bad = nullptr;
   hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
   qi_hip_qwen3_timing timing{};
-  bool eager = false;  // QI_HIP_QWEN3_EAGER=1: launch decode steps one by one (no graph)
+  bool eager = false;    // QI_HIP_QWEN3_EAGER=1: launch decode steps one by one (no graph)
+  bool unfused = false;  // QI_HIP_QWEN3_UNFUSED=1: decode with the separate SiLU kernel
 };
 
 struct qi_hip_kv_cache {
@@ -452,6 +626,7 @@ struct qi_hip_kv_cache {
   uint64_t len = 0;         // host mirror of *len_dev
   // attention partials for row batches of `rb` rows
   float *pm = nullptr, *pl = nullptr, *po = nullptr;
+  uint32_t* tickets = nullptr;  // [rb][kv head], zero between launches
   uint32_t rb = 0, heads = 0;
   hipGraphExec_t exec = nullptr;
   uint64_t graph_model = 0, graph_ws = 0;
@@ -557,10 +732,37 @@ qi_hip_status linear(qi_hip_qwen3* m, const Linear& l, const float* x, uint32_t 
 }
 
 // Launch the attention of `rows` query rows (positions len .. len+rows-1).
+// One row (a decode step) takes the fused path: query/key norms, RoPE and the
+// cache append happen inside the attention kernel. Several rows need the keys
+// of earlier rows of the same call, so they are appended by
+// qk_norm_rope_kernel first.
 qi_hip_status attention(qi_hip_qwen3* m, qi_hip_kv_cache* c, uint32_t layer, uint32_t rows) {
   const qi_hip_qwen3_config& k = m->cfg;
-  const uint32_t hd = k.head_dim, group = k.num_attention_heads / k.num_key_value_heads;
+  const Layer& L = m->layers[layer];
+  const uint32_t H = k.hidden_size, hd = k.head_dim;
+  const uint32_t group = k.num_attention_heads / k.num_key_value_heads;
   const uint64_t lay = static_cast<uint64_t>(k.num_key_value_heads) * hd * c->cap;
+  hipStream_t st = m->ctx->stream;
+  const bool fused = rows == 1;
+  if (!fused) {
+    HeadArgs ha;
+    ha.qkv = m->qkv;
+    ha.row_stride = (k.num_attention_heads + 2 * k.num_key_value_heads) * hd;
+    ha.heads = k.num_attention_heads;
+    ha.kv_heads = k.num_key_value_heads;
+    ha.head_dim = hd;
+    ha.q_norm = L.norms + H;
+    ha.k_norm = L.norms + H + hd;
+    ha.eps = k.rms_norm_eps;
+    ha.rope_cos = m->rope_cos;
+    ha.rope_sin = m->rope_sin;
+    ha.len = c->len_dev;
+    ha.q_out = m->q;
+    ha.keys = c->keys + layer * lay;
+    ha.values = c->values + layer * lay;
+    ha.cap = c->cap;
+    hipLaunchKernelGGL(qk_norm_rope_kernel, dim3(ha.heads + ha.kv_heads, rows), dim3(64), 0, st, ha);
+  }
   AttnArgs a;
   a.q = m->q;
   a.keys = c->keys + layer * lay;
@@ -573,18 +775,33 @@ qi_hip_status attention(qi_hip_qwen3* m, qi_hip_kv_cache* c, uint32_t layer, uin
   a.kv_heads = k.num_key_value_heads;
   a.cap = c->cap;
   a.chunks = c->cap / kChunk;
+  a.row0 = 0;
   a.scale = 1.0f / sqrtf(static_cast<float>(hd));
   a.out = m->att;
-  hipStream_t st = m->ctx->stream;
+  a.qkv = m->qkv;
+  a.row_stride = (k.num_attention_heads + 2 * k.num_key_value_heads) * hd;
+  a.q_norm = L.norms + H;
+  a.k_norm = L.norms + H + hd;
+  a.eps = k.rms_norm_eps;
+  a.rope_cos = m->rope_cos;
+  a.rope_sin = m->rope_sin;
+  a.keys_w = c->keys + layer * lay;
+  a.values_w = c->values + layer * lay;
+  a.tickets = c->tickets;
   for (uint32_t r0 = 0; r0 < rows; r0 += c->rb) {
     const uint32_t nr = rows - r0 < c->rb ? rows - r0 : c->rb;
     AttnArgs b = a;
     b.row0 = r0;
-    const dim3 pg(a.chunks, a.kv_heads, nr), cg(a.heads, nr);
-#define QI_ATTN(HD_, G_)                                                          \
-  if (hd == HD_ && group == G_) {                                                 \
-    hipLaunchKernelGGL((attn_partial_kernel<HD_, G_>), pg, dim3(64), 0, st, b);   \
-    hipLaunchKernelGGL((attn_combine_kernel<HD_>), cg, dim3(64), 0, st, b);       \
+    const dim3 pg(a.chunks, a.kv_heads, nr);
+#define QI_ATTN(HD_, G_)                                                                   \
+  if (hd == HD_ && group == G_) {                                                          \
+    const uint32_t bytes = attn_lds_bytes<HD_, G_>();                                      \
+    if (fused)                                                                             \
+      hipLaunchKernelGGL((attn_kernel<HD_, G_, true>), pg, dim3(64 * kAttnWaves), bytes,   \
+                         st, b);                                                           \
+    else                                                                                   \
+      hipLaunchKernelGGL((attn_kernel<HD_, G_, false>), pg, dim3(64 * kAttnWaves), bytes,  \
+                         st, b);                                                           \
   } else
     QI_ATTN(128, 1) QI_ATTN(128, 2) QI_ATTN(128, 4) QI_ATTN(128, 8)
     QI_ATTN(64, 1) QI_ATTN(64, 2) QI_ATTN(64, 4) QI_ATTN(64, 8)
@@ -595,6 +812,74 @@ qi_hip_status attention(qi_hip_qwen3* m, qi_hip_kv_cache* c, uint32_t layer, uin
   return QI_HIP_OK;
 }
 
+// Attention workgroups of head_dim 128 hold more than 64 KB of LDS: raise the
+// kernels' dynamic LDS limit once, outside any stream capture.
+template <int HD, int G>
+hipError_t attn_set_lds() {
+  const int bytes = static_cast<int>(attn_lds_bytes<HD, G>());
+  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(attn_kernel<HD, G, true>),
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  if (e == hipSuccess)
+    e = hipFuncSetAttribute(reinterpret_cast<const void*>(attn_kernel<HD, G, false>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  return e;
+}
+
+hipError_t attn_prepare(uint32_t hd, uint32_t group) {
+  if (hd == 128) {
+    switch (group) {
+      case 1: return attn_set_lds<128, 1>();
+      case 2: return attn_set_lds<128, 2>();
+      case 4: return attn_set_lds<128, 4>();
+      case 8: return attn_set_lds<128, 8>();
+    }
+  }
+  return hipSuccess;  // head_dim 64 stays within 64 KB
+}
+
+// x = RMSNorm(h (+ y)) for `rows` rows; the row is held in registers.
+qi_hip_status residual_norm(qi_hip_qwen3* m, bool embed, const qi_hip_kv_cache* c,
+                            uint32_t rows, const float* w) {
+  const uint32_t H = m->cfg.hidden_size;
+  const uint32_t nv = (H / 4 + 255) / 256;
+  hipStream_t st = m->ctx->stream;
+  const float eps = m->cfg.rms_norm_eps;
+#define QI_NORM(NV_)                                                                         \
+  if (nv <= NV_) {                                                                           \
+    if (embed)                                                                               \
+      hipLaunchKernelGGL((residual_norm_kernel<true, NV_>), dim3(rows), dim3(256), 0, st,    \
+                         m->h, nullptr, m->embedding, c->tok, c->len_dev, m->x, w, H, eps);  \
+    else                                                                                     \
+      hipLaunchKernelGGL((residual_norm_kernel<false, NV_>), dim3(rows), dim3(256), 0, st,   \
+                         m->h, m->y, nullptr, nullptr, nullptr, m->x, w, H, eps);            \
+  } else
+  QI_NORM(1) QI_NORM(2) QI_NORM(4) QI_NORM(8) QI_NORM(16)
+  return fail(QI_HIP_UNSUPPORTED, "hidden_size above 16384");
+#undef QI_NORM
+  QI_HIP_TRY(hipGetLastError(), "launch norm");
+  return QI_HIP_OK;
+}
+
+// One-row down projection whose activation prep computes SiLU(gate) * up from
+// the gate|up row (qi::kXSilu): one launch instead of two.
+qi_hip_status down_silu(qi_hip_qwen3* m, const Linear& l, float* y) {
+  const qi::Image& im = l.w->im;
+  qi::GemvMfmaArgs ga{qi::make_view(im, l.w->dev), nullptr, y, 1};
+  ga.xs = qi::kXSilu;
+  ga.gu = m->gu;
+  const int split = m->ctx->gemv_split > 0 ? m->ctx->gemv_split : qi::gemv_mfma_split(im.k, im.n);
+  QI_HIP_TRY(qi::launch_gemv_mfma(im.qtype, false, 1, split, ga, m->ctx->stream), "launch down gemv");
+  return QI_HIP_OK;
+}
+
+// The fused down projection needs the matrix-core GEMV (F32/AUTO modes, a
+// tiled f16-scale image).
+bool down_fusable(const qi_hip_qwen3* m, const Linear& l) {
+  if (m->unfused || (m->mode != QI_HIP_MODE_AUTO && m->mode != QI_HIP_MODE_F32)) return false;
+  const qi::Image& im = l.w->im;
+  return im.tiled && !im.wide && qi::gemv_mfma_supported(im.qtype, im.layout, im.k);
+}
+
 // Enqueue the forward of `rows` tokens tok[len .. len+rows) on the context
 // stream. With `project`, the last row goes through the final norm, the LM
 // head and the argmax (token stored at tok[len+rows]); len advances by rows.
@@ -602,43 +887,25 @@ qi_hip_status enqueue_forward(qi_hip_qwen3* m, qi_hip_kv_cache* c, uint32_t rows
   const qi_hip_qwen3_config& k = m->cfg;
   hipStream_t st = m->ctx->stream;
   const uint32_t H = k.hidden_size, I = k.intermediate_size, hd = k.head_dim;
-  const uint32_t QS = k.num_attention_heads * hd, KS = k.num_key_value_heads * hd;
-  const uint64_t lay = static_cast<uint64_t>(k.num_key_value_heads) * hd * c->cap;
   qi_hip_status s;
-  hipLaunchKernelGGL(residual_norm_kernel<true>, dim3(rows), dim3(256), 0, st, m->h, nullptr,
-                     m->embedding, c->tok, c->len_dev, m->x, m->layers[0].norms, H, k.rms_norm_eps);
+  if ((s = residual_norm(m, true, c, rows, m->layers[0].norms)) != QI_HIP_OK) return s;
   for (uint32_t l = 0; l < k.num_hidden_layers; ++l) {
     Layer& L = m->layers[l];
     if ((s = linear(m, L.qkv, m->x, rows, m->qkv)) != QI_HIP_OK) return s;
-    HeadArgs ha;
-    ha.qkv = m->qkv;
-    ha.row_stride = QS + 2 * KS;
-    ha.heads = k.num_attention_heads;
-    ha.kv_heads = k.num_key_value_heads;
-    ha.head_dim = hd;
-    ha.q_norm = L.norms + H;
-    ha.k_norm = L.norms + H + hd;
-    ha.eps = k.rms_norm_eps;
-    ha.rope_cos = m->rope_cos;
-    ha.rope_sin = m->rope_sin;
-    ha.len = c->len_dev;
-    ha.q_out = m->q;
-    ha.keys = c->keys + l * lay;
-    ha.values = c->values + l * lay;
-    ha.cap = c->cap;
-    hipLaunchKernelGGL(qk_norm_rope_kernel, dim3(ha.heads + ha.kv_heads, rows), dim3(64), 0, st, ha);
     if ((s = attention(m, c, l, rows)) != QI_HIP_OK) return s;
     if ((s = linear(m, L.o, m->att, rows, m->y)) != QI_HIP_OK) return s;
-    hipLaunchKernelGGL(residual_norm_kernel<false>, dim3(rows), dim3(256), 0, st, m->h, m->y,
-                       nullptr, nullptr, nullptr, m->x, L.norms + H + 2 * hd, H, k.rms_norm_eps);
+    if ((s = residual_norm(m, false, c, rows, L.norms + H + 2 * hd)) != QI_HIP_OK) return s;
     if ((s = linear(m, L.gate_up, m->x, rows, m->gu)) != QI_HIP_OK) return s;
-    const uint64_t total = static_cast<uint64_t>(rows) * I;
-    hipLaunchKernelGGL(silu_mul_kernel, dim3(static_cast<uint32_t>((total + 255) / 256)), dim3(256),
-                       0, st, m->gu, m->act, I, total);
-    if ((s = linear(m, L.down, m->act, rows, m->y)) != QI_HIP_OK) return s;
+    if (rows == 1 && down_fusable(m, L.down)) {
+      if ((s = down_silu(m, L.down, m->y)) != QI_HIP_OK) return s;
+    } else {
+      const uint64_t total = static_cast<uint64_t>(rows) * I;
+      hipLaunchKernelGGL(silu_mul_kernel, dim3(static_cast<uint32_t>((total + 255) / 256)),
+                         dim3(256), 0, st, m->gu, m->act, I, total);
+      if ((s = linear(m, L.down, m->act, rows, m->y)) != QI_HIP_OK) return s;
+    }
     const float* next = l + 1 < k.num_hidden_layers ? m->layers[l + 1].norms : m->final_norm;
-    hipLaunchKernelGGL(residual_norm_kernel<false>, dim3(rows), dim3(256), 0, st, m->h, m->y,
-                       nullptr, nullptr, nullptr, m->x, next, H, k.rms_norm_eps);
+    if ((s = residual_norm(m, false, c, rows, next)) != QI_HIP_OK) return s;
   }
   if (project) {
     const float* last = m->x + static_cast<uint64_t>(rows - 1) * H;
@@ -674,7 +941,9 @@ qi_hip_status ensure_partials(qi_hip_qwen3* m, qi_hip_kv_cache* c) {
   dev_free(c->pm);
   dev_free(c->pl);
   dev_free(c->po);
+  dev_free(c->tickets);
   c->pm = c->pl = c->po = nullptr;
+  c->tickets = nullptr;
   if (c->exec) (void)hipGraphExecDestroy(c->exec);
   c->exec = nullptr;
   const uint64_t chunks = c->cap / kChunk;
@@ -686,6 +955,10 @@ qi_hip_status ensure_partials(qi_hip_qwen3* m, qi_hip_kv_cache* c) {
   if ((s = dev_alloc_t(&c->pm, hc, "alloc attention partials")) != QI_HIP_OK) return s;
   if ((s = dev_alloc_t(&c->pl, hc, "alloc attention partials")) != QI_HIP_OK) return s;
   if ((s = dev_alloc_t(&c->po, hc * c->head_dim, "alloc attention partials")) != QI_HIP_OK) return s;
+  const uint64_t nt = rb * c->kv_heads;
+  if ((s = dev_alloc_t(&c->tickets, nt, "alloc attention tickets")) != QI_HIP_OK) return s;
+  QI_HIP_TRY(hipMemset(c->tickets, 0, nt * 4), "zero attention tickets");
+  QI_HIP_TRY(hipDeviceSynchronize(), "zero attention tickets");
   c->rb = static_cast<uint32_t>(rb);
   c->heads = heads;
   return QI_HIP_OK;
@@ -823,12 +1096,14 @@ qi_hip_status qi_hip_qwen3_create(qi_hip_ctx* ctx, const qi_hip_qwen3_config* cf
   const uint32_t group = k.num_attention_heads / k.num_key_value_heads;
   if (group != 1 && group != 2 && group != 4 && group != 8)
     return fail(QI_HIP_UNSUPPORTED, "the device decoder supports 1, 2, 4 or 8 query heads per KV head");
-  if (k.hidden_size % 4 != 0) return fail(QI_HIP_UNSUPPORTED, "hidden_size must be a multiple of 4");
+  if (k.hidden_size % 4 != 0 || k.hidden_size > 16384)
+    return fail(QI_HIP_UNSUPPORTED, "hidden_size must be a multiple of 4, at most 16384");
 
   qi_hip_qwen3* m = new qi_hip_qwen3();
   m->cfg = k;
   m->layers.resize(k.num_hidden_layers);
   if (const char* env = getenv("QI_HIP_QWEN3_EAGER")) m->eager = atoi(env) != 0;
+  if (const char* env = getenv("QI_HIP_QWEN3_UNFUSED")) m->unfused = atoi(env) != 0;
   std::lock_guard<std::mutex> lock(ctx->mu);
   ctx->refs.fetch_add(1, std::memory_order_relaxed);
   m->ctx = ctx;
@@ -841,6 +1116,8 @@ qi_hip_status qi_hip_qwen3_create(qi_hip_ctx* ctx, const qi_hip_qwen3_config* cf
   };
   hipError_t e = hipSetDevice(ctx->device);
   if (e != hipSuccess) return bail(hip_fail(e, "set device"));
+  e = attn_prepare(k.head_dim, group);
+  if (e != hipSuccess) return bail(hip_fail(e, "attention LDS limit"));
   // RoPE tables for every position (attention.rs:7-35, evaluated once with
   // the same f32 library functions)
   const uint32_t pairs = k.head_dim / 2;
@@ -1061,7 +1338,8 @@ void qi_hip_kv_cache_free(qi_hip_kv_cache* c) {
     if (c->exec) (void)hipGraphExecDestroy(c->exec);
     for (void* p : {static_cast<void*>(c->keys), static_cast<void*>(c->values),
                     static_cast<void*>(c->tok), static_cast<void*>(c->len_dev),
-                    static_cast<void*>(c->pm), static_cast<void*>(c->pl), static_cast<void*>(c->po)})
+                    static_cast<void*>(c->pm), static_cast<void*>(c->pl), static_cast<void*>(c->po),
+                    static_cast<void*>(c->tickets)})
       dev_free(p);
   }
   qi_abi::ctx_release(ctx);

@@ -83,6 +83,25 @@ def test_generate_tokens_identical_to_cpu(qa, small):
     dev.set_mode(qa.MODE_AUTO)
 
 
+@pytest.mark.parametrize("env", ["QI_HIP_QWEN3_UNFUSED", "QI_HIP_QWEN3_EAGER"])
+def test_decode_variants_identical_to_cpu(qa, ctx, small, env, monkeypatch):
+    """Decode steps with the separate element-wise kernels (instead of the
+    GEMV-fused ones), and steps launched one by one (instead of the replayed
+    graph), select the CPU run's tokens too."""
+    cfg, w, _ = small
+    monkeypatch.setenv(env, "1")
+    dev = w.device_model(ctx)  # the switch is read when the model is created
+    monkeypatch.delenv(env)
+    dev.set_mode(qa.MODE_F32)
+    toks = prompt(cfg, 20, seed=11)
+    print(f"qwen3 generate {env}=1 prompt=20 new=16", flush=True)
+    cache = dev.kv_cache(64)
+    got = dev.generate(cache, toks, 16)
+    want = w.oracle_model(64).generate(toks, 16)
+    assert got == want
+    dev.free()
+
+
 def test_generate_matches_forward_loop(qa, small):
     """Decode steps replayed from the captured graph select the same tokens
     as step-by-step forward calls."""
