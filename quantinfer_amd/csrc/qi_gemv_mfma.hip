@@ -52,6 +52,7 @@ constexpr uint32_t kUnitDigitBytes = 1024;
 constexpr uint32_t kUnitAuxBytes = 128;
 constexpr uint32_t kUnitRecBytes = kUnitDigitBytes + kUnitAuxBytes;
 constexpr uint32_t kMaxLds = 160 * 1024;
+constexpr uint64_t kCUs = 256;  // compute units of an MI355X (gfx950), for the work split
 
 // Byte transpose of four digit words (one per activation) into four words
 // (one per digit): out[i] byte e = in[e] byte i.
@@ -429,15 +430,29 @@ hipError_t launch_split(const GemvMfmaArgs& a, int sw, hipStream_t st) {
     else return launch4<QT, WIDE, MT, 4, 2, 1>(a, st, 8);
   } else {
     if (sw == 4) {
-      // two tiles share the activation prep where the register budget of an
-      // 8-wavefront workgroup keeps occupancy (measured: Q4_K and Q8_0 gain,
-      // Q4_0/Q5_K/Q6_K lose)
-      if constexpr (QT == kQ4_K || QT == kQ8_0) return launch4<QT, WIDE, MT, 4, 4, 2, XS>(a, st);
-      else return launch4<QT, WIDE, MT, 4, 4, 1, XS>(a, st);
+      // Two tiles share the activation prep (an 8-wavefront workgroup) where
+      // that does not raise the most tiles any CU streams, with workgroups
+      // spread evenly over the CUs: ceil(tiles / 256) one-tile workgroups
+      // against 2 ceil(tiles / 512) two-tile ones (896 tiles: 4 and 4, so
+      // the shared prep wins; 768: 3 against 4). Only Q4_K and Q8_0 keep
+      // their occupancy at 8 wavefronts (measured on MI355X: Q4_0, Q5_K and
+      // Q6_K lose), and above 1024 tiles the workgroups no longer all fit
+      // at once.
+      if constexpr (QT == kQ4_K || QT == kQ8_0) {
+        const uint64_t t = a.w.tiles;
+        const uint64_t one = (t + kCUs - 1) / kCUs, two = 2 * ((t + 2 * kCUs - 1) / (2 * kCUs));
+        if (two <= one && t <= 4 * kCUs) return launch4<QT, WIDE, MT, 4, 4, 2, XS>(a, st);
+      }
+      return launch4<QT, WIDE, MT, 4, 4, 1, XS>(a, st);
     }
     const uint32_t upw = (chunk + 7) / 8;
     if (upw <= 2) return launch4<QT, WIDE, MT, 8, 2, 1, XS>(a, st);
     if constexpr (MT == 1) {
+      // one workgroup per CU or fewer: two units in flight per wavefront,
+      // reloaded per batch, ran faster than the whole run in flight
+      // (K = 12288, N = 4096: 8.9 against 9.5 us on MI355X); more tiles
+      // than CUs: the whole run in flight (N = 14336: 21.9 against 24.1 us)
+      if (a.w.tiles <= kCUs) return launch4<QT, WIDE, MT, 8, 2, 1, XS>(a, st);
       if (upw > 4) return launch4<QT, WIDE, MT, 8, 8, 1, XS>(a, st);
     }
     return launch4<QT, WIDE, MT, 8, 4, 1, XS>(a, st);
@@ -476,12 +491,12 @@ bool gemv_mfma_supported(int32_t qtype, int32_t layout, uint64_t k) {
 }
 
 int gemv_mfma_split(uint64_t k, uint64_t n) {
-  // Wavefronts per workgroup (K parts of one 16-output tile): 4 when there
-  // are enough tiles for ~2 workgroups per CU, 8 otherwise, so that the grid
-  // keeps >= ~2048 wavefronts streaming.
-  (void)k;
-  const uint64_t tiles = (n + 15) / 16;
-  return tiles >= 512 ? 4 : 8;
+  // Wavefronts per tile (K parts of one 16-output tile): 4 up to 16 units
+  // (K <= 4096: at most 4 units per wavefront, all in flight), 8 above.
+  // Measured on MI355X at K = 4096 the 4-way split beats the 8-way one at
+  // every N tried (256 to 1536 tiles).
+  (void)n;
+  return k <= 4096 ? 4 : 8;
 }
 
 hipError_t launch_gemv_mfma(int32_t qtype, bool wide, int mt, int sw, const GemvMfmaArgs& a,
