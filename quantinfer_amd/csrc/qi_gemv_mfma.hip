@@ -148,7 +148,10 @@ __device__ __forceinline__ void store_half(const HalfX& o, const Item& it, bool 
 // PRE: the activation records were built by gemv_digits_kernel (a.digits);
 // the workgroup copies its chunk into LDS with global-to-LDS loads instead of
 // building it.
-// XS (one row only): the activation source, see XSource.
+// XS (one row only): the activation source, see XSource. kXNorm keeps each
+// thread's share of sum(v^2) in a register; the wavefront sums reach LDS only
+// in the final reduction, so the norm adds no barrier. a.radd (one row): the
+// residual add on the outputs.
 template <int QT, bool WIDE, int MT, int SW, int D, int WC, bool PRE, int XS = kXPlain>
 __global__ __launch_bounds__(64 * SW * WC) void gemv_mfma_kernel(GemvMfmaArgs a) {
   using U = Unit<QT>;
@@ -182,6 +185,7 @@ __global__ __launch_bounds__(64 * SW * WC) void gemv_mfma_kernel(GemvMfmaArgs a)
   float acc[MT];
 #pragma unroll
   for (int m = 0; m < MT; ++m) acc[m] = 0.0f;
+  [[maybe_unused]] float ssq = 0.0f;  // kXNorm: this thread's part of sum(v^2)
 
   typename U::Raw ring[D];
 
@@ -219,7 +223,7 @@ __global__ __launch_bounds__(64 * SW * WC) void gemv_mfma_kernel(GemvMfmaArgs a)
       // past the run re-read its last unit)
       HalfX xp[XP];
       Item ip[XP];
-      [[maybe_unused]] HalfX up[XP];  // kXSilu: the up halves
+      [[maybe_unused]] HalfX up[XP];  // kXSilu: the up halves; kXNorm: the norm weights
 #pragma unroll
       for (int i = 0; i < XP; ++i) {
         const uint32_t hi = tid + kThreads * i;
@@ -227,10 +231,18 @@ __global__ __launch_bounds__(64 * SW * WC) void gemv_mfma_kernel(GemvMfmaArgs a)
         if constexpr (XS == kXSilu) {
           load_half<QT>(a.gu, K, k0, ip[i], xp[i]);
           load_half<QT>(a.gu + K, K, k0, ip[i], up[i]);
+        } else if constexpr (XS == kXNorm) {
+          load_half<QT>(a.hres, K, k0, ip[i], xp[i]);
+          load_half<QT>(a.nw, K, k0, ip[i], up[i]);
         } else {
           load_half<QT>(a.x, K, k0, ip[i], xp[i]);
         }
       }
+      // fused sources: keep every activation load ahead of the weight loads
+      // (the scheduler hoisted weight scale loads above them, so the in-order
+      // wait for the activations waited for HBM); the plain source already
+      // keeps that order, and the barrier measured slower there
+      if constexpr (XS != kXPlain) __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int i = 0; i < D; ++i)
         U::template load<WIDE>(trec + min(ku0 + u_begin + i, u_last) * R.bytes, lane, ring[i]);
@@ -245,10 +257,23 @@ __global__ __launch_bounds__(64 * SW * WC) void gemv_mfma_kernel(GemvMfmaArgs a)
                            g4.z / (1.0f + expf(-g4.z)) * u4.z, g4.w / (1.0f + expf(-g4.w)) * u4.w);
         }
       };
+      // kXNorm: sum(v^2) over valid items, x = v * w
+      [[maybe_unused]] auto norm = [&](HalfX& vx, const HalfX& wx, bool valid) {
+        float s2 = 0.0f;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const float4 v = vx.v[q];
+          s2 += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+          vx.v[q] = make_float4(v.x * wx.v[q].x, v.y * wx.v[q].y, v.z * wx.v[q].z, v.w * wx.v[q].w);
+        }
+        if (valid) ssq += s2;
+      };
 #pragma unroll
       for (int i = 0; i < XP; ++i) {
+        const bool valid = tid + kThreads * i < halves;
         if constexpr (XS == kXSilu) silu(xp[i], up[i]);
-        store_half(xp[i], ip[i], tid + kThreads * i < halves, recs, cu);
+        if constexpr (XS == kXNorm) norm(xp[i], up[i], valid);
+        store_half(xp[i], ip[i], valid, recs, cu);
       }
       for (uint32_t h0 = XP * kThreads; h0 < halves; h0 += kThreads) {
         const uint32_t hi = h0 + tid;
@@ -259,6 +284,11 @@ __global__ __launch_bounds__(64 * SW * WC) void gemv_mfma_kernel(GemvMfmaArgs a)
           load_half<QT>(a.gu, K, k0, it, xh);
           load_half<QT>(a.gu + K, K, k0, it, uh);
           silu(xh, uh);
+        } else if constexpr (XS == kXNorm) {
+          HalfX wh;
+          load_half<QT>(a.hres, K, k0, it, xh);
+          load_half<QT>(a.nw, K, k0, it, wh);
+          norm(xh, wh, hi < halves);
         } else {
           load_half<QT>(a.x, K, k0, it, xh);
         }
@@ -340,12 +370,24 @@ __global__ __launch_bounds__(64 * SW * WC) void gemv_mfma_kernel(GemvMfmaArgs a)
     v += __shfl_xor(v, 32);
     acc[m] = v;
   }
-  float* red = reinterpret_cast<float*>(recs);  // [WC][SW][MT][16]
+  float* red = reinterpret_cast<float*>(recs);  // [WC][SW][MT][16], then kXNorm: [waves]
   if (g == 0) {
 #pragma unroll
     for (int m = 0; m < MT; ++m) red[((wc * SW + sw) * MT + m) * 16 + col] = acc[m];
   }
+  if constexpr (XS == kXNorm) {
+    float s2 = ssq;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) s2 += __shfl_xor(s2, o);
+    if (lane == 0) red[WC * SW * MT * 16 + wave] = s2;
+  }
   __syncthreads();
+  [[maybe_unused]] float inv = 1.0f;
+  if constexpr (XS == kXNorm) {
+    float total = 0.0f;
+    for (int w = 0; w < SW * WC; ++w) total += red[WC * SW * MT * 16 + w];
+    inv = 1.0f / sqrtf(total / static_cast<float>(K) + a.eps);
+  }
   if (sw == 0 && g == 0 && n_out < a.w.n) {
 #pragma unroll
     for (int m = 0; m < MT; ++m) {
@@ -353,6 +395,10 @@ __global__ __launch_bounds__(64 * SW * WC) void gemv_mfma_kernel(GemvMfmaArgs a)
       float v = red[(wc * SW * MT + m) * 16 + col];
 #pragma unroll
       for (int p = 1; p < SW; ++p) v += red[((wc * SW + p) * MT + m) * 16 + col];
+      if constexpr (XS == kXNorm) v *= inv;
+      if constexpr (MT == 1) {
+        if (a.radd != nullptr) v = a.radd[n_out] + v;
+      }
       a.y[static_cast<uint64_t>(m) * a.w.n + n_out] = v;
     }
   }
@@ -390,7 +436,7 @@ namespace {
 
 uint32_t lds_bytes(int mt, uint32_t chunk_units, int waves) {
   const uint32_t main = kZeroBytes + static_cast<uint32_t>(mt) * chunk_units * kUnitRecBytes;
-  const uint32_t red = kZeroBytes + static_cast<uint32_t>(waves * mt * 16 * 4);
+  const uint32_t red = kZeroBytes + static_cast<uint32_t>(waves * mt * 16 * 4 + waves * 4);
   return main > red ? main : red;
 }
 
@@ -461,13 +507,17 @@ hipError_t launch_split(const GemvMfmaArgs& a, int sw, hipStream_t st) {
 
 template <int QT, bool WIDE>
 hipError_t launch_m(const GemvMfmaArgs& a, int mt, int sw, hipStream_t st) {
+  if (a.radd != nullptr && (mt != 1 || a.m != 1)) return hipErrorInvalidValue;
   if (a.xs != kXPlain) {
-    // the decoder's fused down projection: one row, f16-scale images
+    // the decoder's fused projections: one row, f16-scale images
     if constexpr (WIDE) {
       return hipErrorInvalidValue;
     } else {
-      if (a.xs != kXSilu || a.gu == nullptr || mt != 1 || a.m != 1) return hipErrorInvalidValue;
-      return launch_split<QT, WIDE, 1, kXSilu>(a, sw, st);
+      if (mt != 1 || a.m != 1) return hipErrorInvalidValue;
+      if (a.xs == kXSilu && a.gu != nullptr) return launch_split<QT, WIDE, 1, kXSilu>(a, sw, st);
+      if (a.xs == kXNorm && a.hres != nullptr && a.nw != nullptr)
+        return launch_split<QT, WIDE, 1, kXNorm>(a, sw, st);
+      return hipErrorInvalidValue;
     }
   }
   switch (mt) {

@@ -33,7 +33,11 @@ hipError_t launch_gemv(int32_t qtype, bool wide, int mt, const GemvArgs& a, cons
 //   kXPlain  x
 //   kXSilu   x = g / (1 + exp(-g)) * u with g = gu[k], u = gu[K + k]
 //            (backends/cpu/src/backend.rs:224-237)
-enum XSource : int { kXPlain = 0, kXSilu = 2 };
+//   kXNorm   RMSNorm in front of a projection (backends/cpu/src/backend.rs:172-190):
+//            x = v * nw[k] with v = hres[k], and the outputs are scaled by
+//            1/sqrt(mean(v^2) + eps) at the end (the norm's scalar moves past
+//            the dot product)
+enum XSource : int { kXPlain = 0, kXSilu = 2, kXNorm = 3 };
 
 struct GemvMfmaArgs {
   View w;
@@ -44,6 +48,14 @@ struct GemvMfmaArgs {
   const uint8_t* digits = nullptr;  // activation records from launch_gemv_digits (2+ rows), or null
   int xs = kXPlain;  // one row, f16-scale images only
   const float* gu = nullptr;  // kXSilu: [gate | up] row
+  // kXNorm: the residual row, the norm weight and epsilon
+  const float* hres = nullptr;
+  const float* nw = nullptr;
+  float eps = 0.0f;
+  // one row: y[n] = radd[n] + (x . w_n), the residual add after a projection
+  // (runtime/src/linear.rs:129-142); y may be radd itself (each output is read
+  // and written by the one lane that computes it)
+  const float* radd = nullptr;
 };
 bool gemv_mfma_supported(int32_t qtype, int32_t layout, uint64_t k);
 // Activation records of m rows (digits + window scales, the GEMV's LDS layout)

@@ -66,7 +66,8 @@ __device__ __forceinline__ float wave_max(float v) {
 // ---------------------------------------------------------------- RMSNorm
 // backends/cpu/src/backend.rs:172-190: out = v * (1/sqrt(mean(v^2) + eps)) * w.
 // EMBED: h = embedding[tok[len + row]] (backend.rs:281-298). Otherwise h = h + y
-// (runtime/src/linear.rs:129-142). Then x = RMSNorm(h) * w. A row is held in
+// (runtime/src/linear.rs:129-142), or h unchanged when y is null (the residual
+// add already done by the projection). Then x = RMSNorm(h) * w. A row is held in
 // registers (NV float4 per thread), so every load is issued before the
 // reduction and nothing is read twice.
 template <bool EMBED, int NV>
@@ -93,11 +94,17 @@ __global__ __launch_bounds__(256) void residual_norm_kernel(
     v[j] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     g[j] = v[j];
     if (i < n4) {
-      v[j] = src[i];
       g[j] = wr[i];
-      if constexpr (!EMBED) {
+      if constexpr (EMBED) {
+        v[j] = src[i];
+      } else {
         const float4 o = hr[i];
-        v[j] = make_float4(o.x + v[j].x, o.y + v[j].y, o.z + v[j].z, o.w + v[j].w);
+        if (y != nullptr) {
+          const float4 d = src[i];
+          v[j] = make_float4(o.x + d.x, o.y + d.y, o.z + d.z, o.w + d.w);
+        } else {
+          v[j] = o;
+        }
       }
     }
   }
@@ -613,7 +620,7 @@ struct qi_hip_qwen3 {
   hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
   qi_hip_qwen3_timing timing{};
   bool eager = false;    // QI_HIP_QWEN3_EAGER=1: launch decode steps one by one (no graph)
-  bool unfused = false;  // QI_HIP_QWEN3_UNFUSED=1: decode with the separate SiLU kernel
+  bool unfused = false;  // QI_HIP_QWEN3_UNFUSED=1: decode with the separate SiLU and norm kernels
 };
 
 struct qi_hip_kv_cache {
@@ -837,9 +844,10 @@ hipError_t attn_prepare(uint32_t hd, uint32_t group) {
   return hipSuccess;  // head_dim 64 stays within 64 KB
 }
 
-// x = RMSNorm(h (+ y)) for `rows` rows; the row is held in registers.
+// x = RMSNorm(h (+ y)) for `rows` rows (h updated in place; add = false: the
+// residual add is already in h); the row is held in registers.
 qi_hip_status residual_norm(qi_hip_qwen3* m, bool embed, const qi_hip_kv_cache* c,
-                            uint32_t rows, const float* w) {
+                            uint32_t rows, const float* w, bool add = true) {
   const uint32_t H = m->cfg.hidden_size;
   const uint32_t nv = (H / 4 + 255) / 256;
   hipStream_t st = m->ctx->stream;
@@ -851,7 +859,7 @@ qi_hip_status residual_norm(qi_hip_qwen3* m, bool embed, const qi_hip_kv_cache* 
                          m->h, nullptr, m->embedding, c->tok, c->len_dev, m->x, w, H, eps);  \
     else                                                                                     \
       hipLaunchKernelGGL((residual_norm_kernel<false, NV_>), dim3(rows), dim3(256), 0, st,   \
-                         m->h, m->y, nullptr, nullptr, nullptr, m->x, w, H, eps);            \
+                         m->h, add ? m->y : nullptr, nullptr, nullptr, nullptr, m->x, w, H, eps); \
   } else
   QI_NORM(1) QI_NORM(2) QI_NORM(4) QI_NORM(8) QI_NORM(16)
   return fail(QI_HIP_UNSUPPORTED, "hidden_size above 16384");
@@ -861,12 +869,14 @@ qi_hip_status residual_norm(qi_hip_qwen3* m, bool embed, const qi_hip_kv_cache* 
 }
 
 // One-row down projection whose activation prep computes SiLU(gate) * up from
-// the gate|up row (qi::kXSilu): one launch instead of two.
-qi_hip_status down_silu(qi_hip_qwen3* m, const Linear& l, float* y) {
+// the gate|up row (qi::kXSilu): one launch instead of two. With `radd`, the
+// outputs are added to that row (the residual add).
+qi_hip_status down_silu(qi_hip_qwen3* m, const Linear& l, float* y, const float* radd = nullptr) {
   const qi::Image& im = l.w->im;
   qi::GemvMfmaArgs ga{qi::make_view(im, l.w->dev), nullptr, y, 1};
   ga.xs = qi::kXSilu;
   ga.gu = m->gu;
+  ga.radd = radd;
   const int split = m->ctx->gemv_split > 0 ? m->ctx->gemv_split : qi::gemv_mfma_split(im.k, im.n);
   QI_HIP_TRY(qi::launch_gemv_mfma(im.qtype, false, 1, split, ga, m->ctx->stream), "launch down gemv");
   return QI_HIP_OK;
@@ -880,6 +890,36 @@ bool down_fusable(const qi_hip_qwen3* m, const Linear& l) {
   return im.tiled && !im.wide && qi::gemv_mfma_supported(im.qtype, im.layout, im.k);
 }
 
+// One-row matrix-core GEMV of the decoder: activation source xs (plain x,
+// or kXNorm: x = RMSNorm(h) * w with the norm's 1/rms applied to the outputs)
+// and, with `radd`, the residual add on the outputs (out may be radd).
+qi_hip_status fused_linear(qi_hip_qwen3* m, const Linear& l, int xs, const float* x, const float* w,
+                           float* out, const float* radd) {
+  const qi::Image& im = l.w->im;
+  qi::GemvMfmaArgs ga{qi::make_view(im, l.w->dev), x, out, 1};
+  ga.xs = xs;
+  if (xs == qi::kXNorm) {
+    ga.hres = m->h;
+    ga.nw = w;
+    ga.eps = m->cfg.rms_norm_eps;
+  }
+  ga.radd = radd;
+  const int split = m->ctx->gemv_split > 0 ? m->ctx->gemv_split : qi::gemv_mfma_split(im.k, im.n);
+  QI_HIP_TRY(qi::launch_gemv_mfma(im.qtype, false, 1, split, ga, m->ctx->stream), "launch fused gemv");
+  return QI_HIP_OK;
+}
+
+// A decode step folds the residual adds into the o and down GEMVs (written
+// into h) and the RMSNorms into the activation prep of the q|k|v (from layer
+// 1) and gate|up GEMVs, when all four have matrix-core images.
+bool norm_fusable(const qi_hip_qwen3* m) {
+  for (const Layer& L : m->layers)
+    if (!down_fusable(m, L.qkv) || !down_fusable(m, L.o) || !down_fusable(m, L.gate_up) ||
+        !down_fusable(m, L.down))
+      return false;
+  return true;
+}
+
 // Enqueue the forward of `rows` tokens tok[len .. len+rows) on the context
 // stream. With `project`, the last row goes through the final norm, the LM
 // head and the argmax (token stored at tok[len+rows]); len advances by rows.
@@ -889,23 +929,41 @@ qi_hip_status enqueue_forward(qi_hip_qwen3* m, qi_hip_kv_cache* c, uint32_t rows
   const uint32_t H = k.hidden_size, I = k.intermediate_size, hd = k.head_dim;
   qi_hip_status s;
   if ((s = residual_norm(m, true, c, rows, m->layers[0].norms)) != QI_HIP_OK) return s;
-  for (uint32_t l = 0; l < k.num_hidden_layers; ++l) {
-    Layer& L = m->layers[l];
-    if ((s = linear(m, L.qkv, m->x, rows, m->qkv)) != QI_HIP_OK) return s;
-    if ((s = attention(m, c, l, rows)) != QI_HIP_OK) return s;
-    if ((s = linear(m, L.o, m->att, rows, m->y)) != QI_HIP_OK) return s;
-    if ((s = residual_norm(m, false, c, rows, L.norms + H + 2 * hd)) != QI_HIP_OK) return s;
-    if ((s = linear(m, L.gate_up, m->x, rows, m->gu)) != QI_HIP_OK) return s;
-    if (rows == 1 && down_fusable(m, L.down)) {
-      if ((s = down_silu(m, L.down, m->y)) != QI_HIP_OK) return s;
-    } else {
-      const uint64_t total = static_cast<uint64_t>(rows) * I;
-      hipLaunchKernelGGL(silu_mul_kernel, dim3(static_cast<uint32_t>((total + 255) / 256)),
-                         dim3(256), 0, st, m->gu, m->act, I, total);
-      if ((s = linear(m, L.down, m->act, rows, m->y)) != QI_HIP_OK) return s;
+  if (rows == 1 && norm_fusable(m)) {
+    // decode step: the residual row h is updated in place by the o and down
+    // GEMVs; q|k|v (from layer 1) and gate|up normalize it in their prep
+    for (uint32_t l = 0; l < k.num_hidden_layers; ++l) {
+      Layer& L = m->layers[l];
+      if (l == 0) s = fused_linear(m, L.qkv, qi::kXPlain, m->x, nullptr, m->qkv, nullptr);
+      else s = fused_linear(m, L.qkv, qi::kXNorm, nullptr, L.norms, m->qkv, nullptr);
+      if (s != QI_HIP_OK) return s;
+      if ((s = attention(m, c, l, 1)) != QI_HIP_OK) return s;
+      if ((s = fused_linear(m, L.o, qi::kXPlain, m->att, nullptr, m->h, m->h)) != QI_HIP_OK) return s;
+      if ((s = fused_linear(m, L.gate_up, qi::kXNorm, nullptr, L.norms + H + 2 * hd, m->gu, nullptr)) !=
+          QI_HIP_OK)
+        return s;
+      if ((s = down_silu(m, L.down, m->h, m->h)) != QI_HIP_OK) return s;
     }
-    const float* next = l + 1 < k.num_hidden_layers ? m->layers[l + 1].norms : m->final_norm;
-    if ((s = residual_norm(m, false, c, rows, next)) != QI_HIP_OK) return s;
+    if ((s = residual_norm(m, false, c, 1, m->final_norm, false)) != QI_HIP_OK) return s;
+  } else {
+    for (uint32_t l = 0; l < k.num_hidden_layers; ++l) {
+      Layer& L = m->layers[l];
+      if ((s = linear(m, L.qkv, m->x, rows, m->qkv)) != QI_HIP_OK) return s;
+      if ((s = attention(m, c, l, rows)) != QI_HIP_OK) return s;
+      if ((s = linear(m, L.o, m->att, rows, m->y)) != QI_HIP_OK) return s;
+      if ((s = residual_norm(m, false, c, rows, L.norms + H + 2 * hd)) != QI_HIP_OK) return s;
+      if ((s = linear(m, L.gate_up, m->x, rows, m->gu)) != QI_HIP_OK) return s;
+      if (rows == 1 && down_fusable(m, L.down)) {
+        if ((s = down_silu(m, L.down, m->y)) != QI_HIP_OK) return s;
+      } else {
+        const uint64_t total = static_cast<uint64_t>(rows) * I;
+        hipLaunchKernelGGL(silu_mul_kernel, dim3(static_cast<uint32_t>((total + 255) / 256)),
+                           dim3(256), 0, st, m->gu, m->act, I, total);
+        if ((s = linear(m, L.down, m->act, rows, m->y)) != QI_HIP_OK) return s;
+      }
+      const float* next = l + 1 < k.num_hidden_layers ? m->layers[l + 1].norms : m->final_norm;
+      if ((s = residual_norm(m, false, c, rows, next)) != QI_HIP_OK) return s;
+    }
   }
   if (project) {
     const float* last = m->x + static_cast<uint64_t>(rows - 1) * H;
