@@ -51,16 +51,35 @@ constexpr uint32_t kMaxRows = 512;    // prompt tokens per forward chunk
 constexpr uint32_t kArgBlocks = 256;  // argmax partial blocks
 constexpr uint64_t kPartialBudget = 64ull << 20;  // bytes of attention partials per row batch
 
+// Wavefront reductions on DPP lane moves (no LDS round trips): swap lanes in
+// pairs and quads, mirror within half rows and rows (every lane then holds its
+// row of 16), broadcast lane 15 into rows 1 and 3 and lane 31 into rows 2 and
+// 3; lane 63 ends with the total, read back as one value for every lane.
+// Disabled rows keep `old` (the operation's identity).
+template <int CTRL, int ROWS = 0xF>
+__device__ __forceinline__ float dpp_move(float old, float v) {
+  return __int_as_float(
+      __builtin_amdgcn_update_dpp(__float_as_int(old), __float_as_int(v), CTRL, ROWS, 0xF, false));
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-  return __shfl(v, 0);  // one value for every lane
+  v += dpp_move<0xB1>(0.0f, v);         // quad_perm [1,0,3,2]
+  v += dpp_move<0x4E>(0.0f, v);         // quad_perm [2,3,0,1]
+  v += dpp_move<0x141>(0.0f, v);        // row_half_mirror
+  v += dpp_move<0x140>(0.0f, v);        // row_mirror
+  v += dpp_move<0x142, 0xA>(0.0f, v);   // row_bcast:15
+  v += dpp_move<0x143, 0xC>(0.0f, v);   // row_bcast:31
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
-  return __shfl(v, 0);
+  v = fmaxf(v, dpp_move<0xB1>(-INFINITY, v));
+  v = fmaxf(v, dpp_move<0x4E>(-INFINITY, v));
+  v = fmaxf(v, dpp_move<0x141>(-INFINITY, v));
+  v = fmaxf(v, dpp_move<0x140>(-INFINITY, v));
+  v = fmaxf(v, dpp_move<0x142, 0xA>(-INFINITY, v));
+  v = fmaxf(v, dpp_move<0x143, 0xC>(-INFINITY, v));
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
 // ---------------------------------------------------------------- RMSNorm
@@ -248,10 +267,11 @@ __device__ __forceinline__ float load_coherent(const float* p) {
 constexpr int kAttnWaves = 4;
 
 // LDS of one attention workgroup: keys [dim][64 positions], values [64][dim],
-// the rotated queries of the group, the new position's key and value.
+// the rotated queries of the group, the new position's key and value, the
+// softmax weights [head][64 positions].
 template <int HD, int G>
 constexpr uint32_t attn_lds_bytes() {
-  return static_cast<uint32_t>((2 * HD * kChunk + G * HD + 2 * HD) * sizeof(float) + 16);
+  return static_cast<uint32_t>((2 * HD * kChunk + G * HD + 2 * HD + G * kChunk) * sizeof(float) + 16);
 }
 
 // One 4-wavefront workgroup per (chunk of 64 positions, KV head, row). The
@@ -276,7 +296,8 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attn_kernel(AttnArgs a) {
   float* qs = vs + kChunk * HD;          // [G][HD]
   float* kn = qs + G * HD;               // [HD]
   float* vn = kn + HD;                   // [HD]
-  uint32_t* flag = reinterpret_cast<uint32_t*>(vn + HD);
+  float* pe = vn + HD;                   // [G][64]
+  uint32_t* flag = reinterpret_cast<uint32_t*>(pe + G * kChunk);
   const uint32_t c = blockIdx.x, g = blockIdx.y, rb = blockIdx.z;
   const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const uint32_t r = rb + a.row0;
@@ -365,53 +386,82 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attn_kernel(AttnArgs a) {
     for (uint32_t i = tid; i < G * HD; i += 64 * kAttnWaves) qs[i] = qg[i];
   }
   __syncthreads();  // LDS: queries, new key/value, and the DMA'd chunk (vmcnt drained)
-
-  // 4. this wavefront's heads: scores, softmax pieces, value sums
-  const bool valid = t0 + lane <= pos;
-  const uint32_t nvalid = tp + 1 < kChunk ? tp + 1 : kChunk;
-  const bool mine = owner && lane == tp;  // this lane's key is the new one
-  float s[HPW];
-#pragma unroll
-  for (int i = 0; i < HPW; ++i) s[i] = 0.0f;
-#pragma unroll 8
-  for (int d = 0; d < HD; ++d) {
-    const float kv = mine ? kn[d] : ks[d * kChunk + lane];
-#pragma unroll
-    for (int i = 0; i < HPW; ++i) {
-      const uint32_t h = wave + kAttnWaves * i;
-      s[i] = fmaf(qs[(h < G ? h : 0) * HD + d], kv, s[i]);
+  if (owner) {
+    // the new position's key and value replace the chunk's stale copies
+    for (uint32_t d = tid; d < HD; d += 64 * kAttnWaves) {
+      ks[d * kChunk + tp] = kn[d];
+      vs[tp * HD + d] = vn[d];
     }
+    __syncthreads();
+  }
+
+  // 4. this wavefront's heads: scores (lane t: position t0 + t; four partial
+  // sums over the dimensions), softmax pieces, value sums. Positions past the
+  // query get weight 0; the cache holds finite values there (zeroed at
+  // creation, earlier tokens after a reset), so their products vanish.
+  const bool valid = t0 + lane <= pos;
+  float s[HPW];
+  {
+    float sp[HPW][4];
+#pragma unroll
+    for (int i = 0; i < HPW; ++i)
+#pragma unroll
+      for (int u = 0; u < 4; ++u) sp[i][u] = 0.0f;
+#pragma unroll 2
+    for (int d0 = 0; d0 < HD; d0 += 32) {
+      float kv[32];
+#pragma unroll
+      for (int u = 0; u < 32; ++u) kv[u] = ks[(d0 + u) * kChunk + lane];
+#pragma unroll
+      for (int i = 0; i < HPW; ++i) {
+        const uint32_t h = wave + kAttnWaves * i;
+        const float4* qv = reinterpret_cast<const float4*>(qs + (h < G ? h : 0) * HD + d0);
+#pragma unroll
+        for (int u4 = 0; u4 < 8; ++u4) {
+          const float4 q4 = qv[u4];
+          sp[i][0] = fmaf(q4.x, kv[4 * u4], sp[i][0]);
+          sp[i][1] = fmaf(q4.y, kv[4 * u4 + 1], sp[i][1]);
+          sp[i][2] = fmaf(q4.z, kv[4 * u4 + 2], sp[i][2]);
+          sp[i][3] = fmaf(q4.w, kv[4 * u4 + 3], sp[i][3]);
+        }
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < HPW; ++i) s[i] = (sp[i][0] + sp[i][1]) + (sp[i][2] + sp[i][3]);
   }
   float e[HPW], m[HPW], l[HPW];
 #pragma unroll
   for (int i = 0; i < HPW; ++i) {
+    const uint32_t h = wave + kAttnWaves * i;
     const float sc = valid ? s[i] * a.scale : -INFINITY;
     m[i] = wave_max(sc);
     e[i] = valid ? expf(sc - m[i]) : 0.0f;
     l[i] = wave_sum(e[i]);
+    if (h < G) pe[h * kChunk + lane] = e[i];  // read back by this wavefront only
   }
   float acc[HPW][DPL];
 #pragma unroll
   for (int i = 0; i < HPW; ++i)
 #pragma unroll
     for (int j = 0; j < DPL; ++j) acc[i][j] = 0.0f;
-  // all 64 positions, unrolled: weights come from lane t as scalars; positions
-  // past the query have weight 0 and their (stale) values are masked to 0
+  // all 64 positions: the weights come back from LDS four at a time (the same
+  // address for every lane), lane l sums value dimensions l*DPL .. l*DPL+DPL-1
+#pragma unroll 4
+  for (int t4 = 0; t4 < static_cast<int>(kChunk) / 4; ++t4) {
+    float v[4][DPL];
 #pragma unroll
-  for (int t = 0; t < static_cast<int>(kChunk); ++t) {
-    const bool in = static_cast<uint32_t>(t) < nvalid;
-    const bool fresh = owner && static_cast<uint32_t>(t) == tp;
-    float v[DPL];
+    for (int u = 0; u < 4; ++u)
 #pragma unroll
-    for (int j = 0; j < DPL; ++j) {
-      const float x = fresh ? vn[lane * DPL + j] : vs[t * HD + lane * DPL + j];
-      v[j] = in ? x : 0.0f;
-    }
+      for (int j = 0; j < DPL; ++j) v[u][j] = vs[(4 * t4 + u) * HD + lane * DPL + j];
 #pragma unroll
     for (int i = 0; i < HPW; ++i) {
-      const float wt = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e[i]), t));
+      const uint32_t h = wave + kAttnWaves * i;
+      const float4 w4 = reinterpret_cast<const float4*>(pe + (h < G ? h : 0) * kChunk)[t4];
+      const float wt[4] = {w4.x, w4.y, w4.z, w4.w};
 #pragma unroll
-      for (int j = 0; j < DPL; ++j) acc[i][j] = fmaf(wt, v[j], acc[i][j]);
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int j = 0; j < DPL; ++j) acc[i][j] = fmaf(wt[u], v[u][j], acc[i][j]);
     }
   }
 #pragma unroll
@@ -435,36 +485,59 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attn_kernel(AttnArgs a) {
   if (tid == 0) *flag = atomicAdd(&a.tickets[ticket], 1u) == nc - 1 ? 1u : 0u;
   __syncthreads();
   if (*flag == 0) return;
+  // Online combine over groups of 64 chunks: a group's maxima, sums and its
+  // first 16 chunk outputs are loaded together (one round trip for up to 16
+  // chunks), the running output and denominator are rescaled when the maximum
+  // grows: out = sum_c e^(m_c - M) o_c / sum_c e^(m_c - M) l_c.
 #pragma unroll
   for (int i = 0; i < HPW; ++i) {
     const uint32_t hl = wave + kAttnWaves * i;
     if (hl >= G) continue;
     const uint32_t h = g * G + hl;
     const uint64_t base = (static_cast<uint64_t>(rb) * a.heads + h) * a.chunks;
-    float mx = -INFINITY;
-    for (uint32_t c0 = 0; c0 < nc; c0 += 64)
-      if (c0 + lane < nc) mx = fmaxf(mx, load_coherent(a.pm + base + c0 + lane));
-    mx = wave_max(mx);
-    float denom = 0.0f, out[DPL];
+    float mx = -INFINITY, denom = 0.0f, out[DPL];
 #pragma unroll
     for (int j = 0; j < DPL; ++j) out[j] = 0.0f;
     for (uint32_t c0 = 0; c0 < nc; c0 += 64) {
       const uint32_t n = nc - c0 < 64 ? nc - c0 : 64;
-      const bool have = c0 + lane < nc;
-      const float f = have ? expf(load_coherent(a.pm + base + c0 + lane) - mx) : 0.0f;
-      denom += wave_sum(have ? f * load_coherent(a.pl + base + c0 + lane) : 0.0f);
+      const bool have = lane < n;
       const float* o = a.po + (base + c0) * HD + lane * DPL;
+      const float gm_l = have ? load_coherent(a.pm + base + c0 + lane) : -INFINITY;
+      const float gl_l = have ? load_coherent(a.pl + base + c0 + lane) : 0.0f;
+      float ov[16][DPL];
+#pragma unroll
+      for (int cc = 0; cc < 16; ++cc) {
+        const uint32_t ci = static_cast<uint32_t>(cc) < n ? static_cast<uint32_t>(cc) : n - 1;
+#pragma unroll
+        for (int j = 0; j < DPL; ++j) ov[cc][j] = load_coherent(o + static_cast<uint64_t>(ci) * HD + j);
+      }
+      // every load above is issued before the maximum needs the first of them
+      __builtin_amdgcn_sched_barrier(0);
+      const float nm = fmaxf(mx, wave_max(gm_l));
+      const float rs = expf(mx - nm);  // 0 on the first group (mx = -inf)
+      const float f = have ? expf(gm_l - nm) : 0.0f;
+      denom = denom * rs + wave_sum(f * gl_l);
+#pragma unroll
+      for (int j = 0; j < DPL; ++j) out[j] *= rs;
+      mx = nm;
       for (uint32_t cb = 0; cb < n; cb += 16) {
-        // 16 chunks unrolled; indices past the last chunk re-read it with weight 0
+        if (cb > 0) {
+          // chunks past the first 16 of the group (contexts above 1024 positions)
+#pragma unroll
+          for (int cc = 0; cc < 16; ++cc) {
+            const uint32_t ci = cb + cc < n ? cb + cc : n - 1;
+#pragma unroll
+            for (int j = 0; j < DPL; ++j) ov[cc][j] = load_coherent(o + static_cast<uint64_t>(ci) * HD + j);
+          }
+        }
+        // indices past the group's last chunk re-read it with weight 0
 #pragma unroll
         for (int cc = 0; cc < 16; ++cc) {
-          const uint32_t ci = cb + cc < n ? cb + cc : n - 1;
           const float fc = __int_as_float(
               __builtin_amdgcn_readlane(__float_as_int(f), static_cast<int>((cb + cc) & 63)));
           const float w = cb + cc < n ? fc : 0.0f;
 #pragma unroll
-          for (int j = 0; j < DPL; ++j)
-            out[j] = fmaf(w, load_coherent(o + static_cast<uint64_t>(ci) * HD + j), out[j]);
+          for (int j = 0; j < DPL; ++j) out[j] = fmaf(w, ov[cc][j], out[j]);
         }
       }
     }
