@@ -73,6 +73,7 @@ void ctx_destroy(qi_hip_ctx* c) {
   if (c->xbuf) (void)hipFree(c->xbuf);
   if (c->ybuf) (void)hipFree(c->ybuf);
   if (c->hbuf) (void)hipFree(c->hbuf);
+  if (c->sbuf) (void)hipFree(c->sbuf);
   if (c->dbuf) (void)hipFree(c->dbuf);
   if (c->stream) (void)hipStreamDestroy(c->stream);
   delete c;
@@ -116,6 +117,16 @@ qi_hip_status run_linear(qi_hip_ctx* c, const qi_hip_weights* w, const float* x,
       if (s != QI_HIP_OK) return s;
     }
     qi::GemmArgs ga{v, x, y, m, reinterpret_cast<_Float16*>(c->hbuf), m_pad};
+    ga.splits = qi::gemm_splits(im, m);
+    if (ga.splits > 1) {
+      const uint64_t need = ga.splits * m_pad * im.n;
+      if (need > c->scap) {
+        QI_HIP_TRY(hipStreamSynchronize(st), "synchronize before growing the GEMM workspace");
+        qi_hip_status s = grow(&c->sbuf, &c->scap, need, "alloc GEMM split-K workspace");
+        if (s != QI_HIP_OK) return s;
+      }
+      ga.part = c->sbuf;
+    }
     QI_HIP_TRY(qi::launch_gemm(im, ga, st), "launch gemm");
     return QI_HIP_OK;
   }

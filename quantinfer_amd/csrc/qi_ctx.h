@@ -31,6 +31,8 @@ struct qi_hip_ctx {
   uint64_t ycap = 0;
   float* hbuf = nullptr;  // f16 activations of the prefill GEMM (capacity in floats)
   uint64_t hcap = 0;
+  float* sbuf = nullptr;  // split-K partial products of the prefill GEMM (capacity in floats)
+  uint64_t scap = 0;
   float* dbuf = nullptr;  // activation records of the decode GEMV, 2+ rows (capacity in floats)
   uint64_t dcap = 0;
   int gemv_split = 0;  // QI_HIP_GEMV_SPLIT tuning override (wavefronts per GEMV workgroup: 4 or 8)

@@ -310,7 +310,9 @@ __global__ __launch_bounds__(256) void x_to_frag_kernel(const float* __restrict_
 // weights never pass through LDS. The activations of a 2-step
 // stage (16 KB, fragment order) go global -> registers (kAhead stages in
 // flight) -> one of two LDS slots, one barrier per stage; a fragment read is
-// 1 KB contiguous across the wavefront.
+// 1 KB contiguous across the wavefront. Split-K (a.splits > 1): workgroup z
+// takes units [z units / splits, (z + 1) units / splits) and writes its
+// partial tile to a.part[z].
 template <int QT, bool WIDE>
 __global__ __launch_bounds__(256) void gemm_reg_kernel(GemmArgs a) {
   using U = Unit<QT>;
@@ -326,8 +328,9 @@ __global__ __launch_bounds__(256) void gemm_reg_kernel(GemmArgs a) {
   const uint32_t cw = wave;  // column group: output tiles 4 cw .. 4 cw + 3
   constexpr uint32_t rt0 = 0;
   const uint32_t units = a.w.units;
+  const uint32_t ub = blockIdx.z * units / a.splits, ue = (blockIdx.z + 1) * units / a.splits;
   const uint64_t m0 = static_cast<uint64_t>(blockIdx.y) * kTileM;
-  const uint32_t stages = 4 * units;
+  const uint32_t stages = 4 * ue;  // one past this workgroup's last stage
   // this row tile's activation pieces (16 B each): stage s is pieces [1024 s, 1024 s + 1024)
   const u32x4* xa = reinterpret_cast<const u32x4*>(a.xh) + static_cast<uint64_t>(blockIdx.y) * units * 4096;
 
@@ -357,7 +360,7 @@ __global__ __launch_bounds__(256) void gemm_reg_kernel(GemmArgs a) {
   typename U::Raw cur[4], nxt[4];
   float sa[4][U::kWindows], sb[4][U::kWindows];
   auto b_load = [&](uint32_t u) {
-    const uint32_t ul = u < units ? u : units - 1;
+    const uint32_t ul = u < ue ? u : ue - 1;
 #pragma unroll
     for (int ct = 0; ct < 4; ++ct)
       U::template load<WIDE>(trec[ct] + static_cast<uint64_t>(ul) * R.bytes, lane, nxt[ct]);
@@ -369,19 +372,21 @@ __global__ __launch_bounds__(256) void gemm_reg_kernel(GemmArgs a) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = f4{0, 0, 0, 0};
 
-  // prologue: stage 0 into slot 0, stages 1..kAhead in registers, unit 0's
-  // weights current and unit 1's in flight
+  // prologue: stage 4 ub into slot 0, the next kAhead stages in registers,
+  // unit ub's weights current and unit ub + 1's in flight (stage parity is
+  // that of q, the stage within its unit)
 #pragma unroll
-  for (int ct = 0; ct < 4; ++ct) U::template load<WIDE>(trec[ct], lane, cur[ct]);
-  a_load(std::integral_constant<int, 0>{}, 0);
-  a_load(std::integral_constant<int, 1>{}, 1);
+  for (int ct = 0; ct < 4; ++ct)
+    U::template load<WIDE>(trec[ct] + static_cast<uint64_t>(ub) * R.bytes, lane, cur[ct]);
+  a_load(std::integral_constant<int, 0>{}, 4 * ub);
+  a_load(std::integral_constant<int, 1>{}, 4 * ub + 1);
   a_store(std::integral_constant<int, 0>{}, 0);
-  a_load(std::integral_constant<int, 0>{}, 2);
-  b_load(1);
+  a_load(std::integral_constant<int, 0>{}, 4 * ub + 2);
+  b_load(ub + 1);
 #pragma unroll
   for (int ct = 0; ct < 4; ++ct) U::template scales<WIDE>(g, cur[ct], sa[ct], sb[ct]);
 
-  for (uint32_t u = 0; u < units; ++u) {
+  for (uint32_t u = ub; u < ue; ++u) {
     // stage s = 4u + q: its activations are in slot q & 1; stages s + 1 ..
     // s + kAhead are in registers, stage s + 1 in ar[(q + 1) % kAhead]
     static_assert(4 % kAhead == 0, "the ring index below assumes kAhead divides 4");
@@ -428,7 +433,8 @@ __global__ __launch_bounds__(256) void gemm_reg_kernel(GemmArgs a) {
 
   // C[i][j]: lane j + 16 (i / 4), element i % 4
   const uint64_t ld = a.w.n;
-  float* yrow = a.y + (m0 + 16 * rt0 + 4 * g) * ld;
+  float* const out = a.splits > 1 ? a.part + static_cast<uint64_t>(blockIdx.z) * a.m_pad * ld : a.y;
+  float* yrow = out + (m0 + 16 * rt0 + 4 * g) * ld;
 #pragma unroll
   for (int ct = 0; ct < 4; ++ct) {
     const uint64_t n = static_cast<uint64_t>((blockIdx.x * 4 + cw) * 4 + ct) * 16 + c16;
@@ -444,13 +450,31 @@ __global__ __launch_bounds__(256) void gemm_reg_kernel(GemmArgs a) {
   }
 }
 
+// y = sum of the split-K partial products, in split order (deterministic).
+__global__ __launch_bounds__(256) void gemm_splitk_sum_kernel(const float* __restrict__ part, uint32_t splits,
+                                                              uint64_t count, uint64_t stride,
+                                                              float* __restrict__ y) {
+  const uint64_t i = static_cast<uint64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= count) return;
+  float v = part[i];
+  for (uint32_t s = 1; s < splits; ++s) v += part[s * stride + i];
+  y[i] = v;
+}
+
 namespace {
 
 template <int QT, bool WIDE>
 hipError_t launch_reg(const Image& im, const GemmArgs& a, hipStream_t st) {
   const uint32_t nblk = static_cast<uint32_t>((im.tiles + 15) / 16);
   const uint32_t mblk = static_cast<uint32_t>(a.m_pad / kTileM);
-  hipLaunchKernelGGL((gemm_reg_kernel<QT, WIDE>), dim3(nblk, mblk), dim3(256), 0, st, a);
+  if (a.splits < 1 || a.splits > im.k / 256 || (a.splits > 1 && a.part == nullptr)) return hipErrorInvalidValue;
+  hipLaunchKernelGGL((gemm_reg_kernel<QT, WIDE>), dim3(nblk, mblk, a.splits), dim3(256), 0, st, a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || a.splits == 1) return e;
+  // rows of y and of each partial block share the row stride n
+  const uint64_t count = a.m * im.n;
+  hipLaunchKernelGGL(gemm_splitk_sum_kernel, dim3(static_cast<uint32_t>((count + 255) / 256)), dim3(256), 0, st,
+                     a.part, a.splits, count, a.m_pad * im.n, a.y);
   return hipGetLastError();
 }
 
@@ -497,6 +521,19 @@ bool gemm_supported(int32_t qtype, int32_t layout, uint64_t k, uint64_t n) {
 }
 
 uint64_t gemm_padded_rows(uint64_t m) { return (m + kTileM - 1) / kTileM * kTileM; }
+
+uint32_t gemm_splits(const Image& im, uint64_t m) {
+  // The register-weight kernel runs one workgroup per CU (256 on MI355X),
+  // each walking its K range at the latency of one workgroup; with fewer row
+  // x column blocks than CUs, split K so the launch fills the CUs once
+  // (M = 512, N = 4096: 64 blocks x 4 splits). The Q6_K kernel does not split.
+  if (use_ws(im.qtype) || !im.tiled) return 1;
+  const uint64_t blocks = (im.tiles + 15) / 16 * (gemm_padded_rows(m) / kTileM);
+  const uint64_t units = im.k / 256;
+  uint64_t s = blocks >= 256 ? 1 : 256 / blocks;
+  if (s > units) s = units;
+  return static_cast<uint32_t>(s < 1 ? 1 : s);
+}
 
 hipError_t launch_gemm(const Image& im, const GemmArgs& a, hipStream_t st) {
   if (!im.tiled || a.xh == nullptr || a.m_pad != gemm_padded_rows(a.m)) return hipErrorInvalidValue;

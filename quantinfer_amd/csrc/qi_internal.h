@@ -80,9 +80,16 @@ struct GemmArgs {
   uint64_t m;
   _Float16* xh;    // [m_pad, k] f16 workspace (the activations rounded once)
   uint64_t m_pad;  // gemm_padded_rows(m)
+  // split-K (gemm_splits > 1): [splits][m_pad][n] f32 partial products,
+  // summed in split order into y
+  float* part = nullptr;
+  uint32_t splits = 1;
 };
 bool gemm_supported(int32_t qtype, int32_t layout, uint64_t k, uint64_t n);
 uint64_t gemm_padded_rows(uint64_t m);
+// K splits of a GEMM launch (1: no split): enough workgroups to fill the CUs
+// once when the row and column blocks alone do not.
+uint32_t gemm_splits(const Image& im, uint64_t m);
 hipError_t launch_gemm(const Image& im, const GemmArgs& a, hipStream_t st);
 
 }  // namespace qi
