@@ -150,8 +150,8 @@ __device__ __forceinline__ void store_half(const HalfX& o, const Item& it, bool 
 // building it.
 // XS (one row only): the activation source, see XSource. kXNorm keeps each
 // thread's share of sum(v^2) in a register; the wavefront sums reach LDS only
-// in the final reduction, so the norm adds no barrier. a.radd (one row): the
-// residual add on the outputs.
+// in the final reduction, so the norm adds no barrier. One row: a.radd adds
+// the residual to the outputs, a.silu_pairs combines gate/up output pairs.
 template <int QT, bool WIDE, int MT, int SW, int D, int WC, bool PRE, int XS = kXPlain>
 __global__ __launch_bounds__(64 * SW * WC) void gemv_mfma_kernel(GemvMfmaArgs a) {
   using U = Unit<QT>;
@@ -223,15 +223,12 @@ __global__ __launch_bounds__(64 * SW * WC) void gemv_mfma_kernel(GemvMfmaArgs a)
       // past the run re-read its last unit)
       HalfX xp[XP];
       Item ip[XP];
-      [[maybe_unused]] HalfX up[XP];  // kXSilu: the up halves; kXNorm: the norm weights
+      [[maybe_unused]] HalfX up[XP];  // kXNorm: the norm weights
 #pragma unroll
       for (int i = 0; i < XP; ++i) {
         const uint32_t hi = tid + kThreads * i;
         ip[i] = item_of(hi < halves ? hi : 0, units);
-        if constexpr (XS == kXSilu) {
-          load_half<QT>(a.gu, K, k0, ip[i], xp[i]);
-          load_half<QT>(a.gu + K, K, k0, ip[i], up[i]);
-        } else if constexpr (XS == kXNorm) {
+        if constexpr (XS == kXNorm) {
           load_half<QT>(a.hres, K, k0, ip[i], xp[i]);
           load_half<QT>(a.nw, K, k0, ip[i], up[i]);
         } else {
@@ -247,16 +244,6 @@ __global__ __launch_bounds__(64 * SW * WC) void gemv_mfma_kernel(GemvMfmaArgs a)
       for (int i = 0; i < D; ++i)
         U::template load<WIDE>(trec + min(ku0 + u_begin + i, u_last) * R.bytes, lane, ring[i]);
 
-      // kXSilu: x = gate / (1 + exp(-gate)) * up (backend.rs:224-237)
-      [[maybe_unused]] auto silu = [](HalfX& gx, const HalfX& ux) {
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          float4& g4 = gx.v[q];
-          const float4 u4 = ux.v[q];
-          g4 = make_float4(g4.x / (1.0f + expf(-g4.x)) * u4.x, g4.y / (1.0f + expf(-g4.y)) * u4.y,
-                           g4.z / (1.0f + expf(-g4.z)) * u4.z, g4.w / (1.0f + expf(-g4.w)) * u4.w);
-        }
-      };
       // kXNorm: sum(v^2) over valid items, x = v * w
       [[maybe_unused]] auto norm = [&](HalfX& vx, const HalfX& wx, bool valid) {
         float s2 = 0.0f;
@@ -271,7 +258,6 @@ __global__ __launch_bounds__(64 * SW * WC) void gemv_mfma_kernel(GemvMfmaArgs a)
 #pragma unroll
       for (int i = 0; i < XP; ++i) {
         const bool valid = tid + kThreads * i < halves;
-        if constexpr (XS == kXSilu) silu(xp[i], up[i]);
         if constexpr (XS == kXNorm) norm(xp[i], up[i], valid);
         store_half(xp[i], ip[i], valid, recs, cu);
       }
@@ -279,12 +265,7 @@ __global__ __launch_bounds__(64 * SW * WC) void gemv_mfma_kernel(GemvMfmaArgs a)
         const uint32_t hi = h0 + tid;
         Item it = item_of(hi < halves ? hi : 0, units);
         HalfX xh;
-        if constexpr (XS == kXSilu) {
-          HalfX uh;
-          load_half<QT>(a.gu, K, k0, it, xh);
-          load_half<QT>(a.gu + K, K, k0, it, uh);
-          silu(xh, uh);
-        } else if constexpr (XS == kXNorm) {
+        if constexpr (XS == kXNorm) {
           HalfX wh;
           load_half<QT>(a.hres, K, k0, it, xh);
           load_half<QT>(a.nw, K, k0, it, wh);
@@ -387,6 +368,20 @@ __global__ __launch_bounds__(64 * SW * WC) void gemv_mfma_kernel(GemvMfmaArgs a)
     float total = 0.0f;
     for (int w = 0; w < SW * WC; ++w) total += red[WC * SW * MT * 16 + w];
     inv = 1.0f / sqrtf(total / static_cast<float>(K) + a.eps);
+  }
+  if constexpr (MT == 1) {
+    if (a.silu_pairs) {
+      // lanes 0-7 of the tile hold gate rows, lanes 8-15 the matching up rows
+      if (sw == 0 && g == 0) {
+        float v = red[(wc * SW) * 16 + col];
+#pragma unroll
+        for (int p = 1; p < SW; ++p) v += red[(wc * SW + p) * 16 + col];
+        if constexpr (XS == kXNorm) v *= inv;
+        const float u = __shfl(v, static_cast<int>(lane) + 8, 16);
+        if (col < 8 && tile_raw < a.w.tiles) a.y[static_cast<uint64_t>(tile_raw) * 8 + col] = v / (1.0f + expf(-v)) * u;
+      }
+      return;
+    }
   }
   if (sw == 0 && g == 0 && n_out < a.w.n) {
 #pragma unroll
@@ -507,14 +502,14 @@ hipError_t launch_split(const GemvMfmaArgs& a, int sw, hipStream_t st) {
 
 template <int QT, bool WIDE>
 hipError_t launch_m(const GemvMfmaArgs& a, int mt, int sw, hipStream_t st) {
-  if (a.radd != nullptr && (mt != 1 || a.m != 1)) return hipErrorInvalidValue;
+  if ((a.radd != nullptr || a.silu_pairs) && (mt != 1 || a.m != 1)) return hipErrorInvalidValue;
+  if (a.silu_pairs && (a.radd != nullptr || a.w.n % 16 != 0)) return hipErrorInvalidValue;
   if (a.xs != kXPlain) {
     // the decoder's fused projections: one row, f16-scale images
     if constexpr (WIDE) {
       return hipErrorInvalidValue;
     } else {
       if (mt != 1 || a.m != 1) return hipErrorInvalidValue;
-      if (a.xs == kXSilu && a.gu != nullptr) return launch_split<QT, WIDE, 1, kXSilu>(a, sw, st);
       if (a.xs == kXNorm && a.hres != nullptr && a.nw != nullptr)
         return launch_split<QT, WIDE, 1, kXNorm>(a, sw, st);
       return hipErrorInvalidValue;

@@ -31,13 +31,11 @@ hipError_t launch_gemv(int32_t qtype, bool wide, int mt, const GemvArgs& a, cons
 // Activation source of a one-row GEMV. The decoder fuses the element-wise
 // step before the down projection into the GEMV's activation prep:
 //   kXPlain  x
-//   kXSilu   x = g / (1 + exp(-g)) * u with g = gu[k], u = gu[K + k]
-//            (backends/cpu/src/backend.rs:224-237)
 //   kXNorm   RMSNorm in front of a projection (backends/cpu/src/backend.rs:172-190):
 //            x = v * nw[k] with v = hres[k], and the outputs are scaled by
 //            1/sqrt(mean(v^2) + eps) at the end (the norm's scalar moves past
 //            the dot product)
-enum XSource : int { kXPlain = 0, kXSilu = 2, kXNorm = 3 };
+enum XSource : int { kXPlain = 0, kXNorm = 3 };
 
 struct GemvMfmaArgs {
   View w;
@@ -47,7 +45,6 @@ struct GemvMfmaArgs {
   uint32_t chunk_units = 0;  // set by the launcher: K units whose activation digits fit LDS
   const uint8_t* digits = nullptr;  // activation records from launch_gemv_digits (2+ rows), or null
   int xs = kXPlain;  // one row, f16-scale images only
-  const float* gu = nullptr;  // kXSilu: [gate | up] row
   // kXNorm: the residual row, the norm weight and epsilon
   const float* hres = nullptr;
   const float* nw = nullptr;
@@ -56,6 +53,10 @@ struct GemvMfmaArgs {
   // (runtime/src/linear.rs:129-142); y may be radd itself (each output is read
   // and written by the one lane that computes it)
   const float* radd = nullptr;
+  // one row, N a multiple of 16: every 16-output tile holds 8 gate rows then
+  // the 8 up rows of the same outputs, and y[8 t + c] = g / (1 + exp(-g)) * u
+  // (backends/cpu/src/backend.rs:224-237), N / 2 outputs
+  bool silu_pairs = false;
 };
 bool gemv_mfma_supported(int32_t qtype, int32_t layout, uint64_t k);
 // Activation records of m rows (digits + window scales, the GEMV's LDS layout)

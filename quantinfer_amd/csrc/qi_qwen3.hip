@@ -11,7 +11,7 @@
 //   o projection                  GEMV/GEMM
 //   residual + RMSNorm            residual_norm_kernel<ADD>
 //   gate|up projection            one fused image
-//   SiLU(gate) * up               silu_mul_kernel
+//   SiLU(gate) * up               silu_mul_kernel (one row: the gate|up GEMV epilogue)
 //   down projection               GEMV/GEMM
 //   residual + next RMSNorm       residual_norm_kernel<ADD> (the final norm after the last layer)
 //   LM head on the last row       GEMV (a Q6_K head stays quantized)
@@ -549,16 +549,19 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attn_kernel(AttnArgs a) {
 }
 
 // --------------------------------------------------------------- SiLU*up
-// backends/cpu/src/backend.rs:224-237: gate / (1 + exp(-gate)) * up, with gate
-// and up the two halves of the fused gate|up output row.
+// backends/cpu/src/backend.rs:224-237: gate / (1 + exp(-gate)) * up from the
+// fused gate|up output row: the two halves (group 0) or, for an interleaved
+// image, groups of `group` gate outputs each followed by the same up outputs.
 __global__ __launch_bounds__(256) void silu_mul_kernel(const float* __restrict__ gu,
                                                        float* __restrict__ out, uint32_t inter,
-                                                       uint64_t total) {
+                                                       uint64_t total, uint32_t group) {
   const uint64_t i = static_cast<uint64_t>(blockIdx.x) * 256 + threadIdx.x;
   if (i >= total) return;
   const uint64_t r = i / inter, j = i % inter;
-  const float g = gu[r * 2 * inter + j];
-  const float u = gu[r * 2 * inter + inter + j];
+  const uint64_t gi = group ? (j / group) * 2 * group + j % group : j;
+  const uint64_t ui = group ? gi + group : inter + j;
+  const float g = gu[r * 2 * inter + gi];
+  const float u = gu[r * 2 * inter + ui];
   out[i] = g / (1.0f + expf(-g)) * u;
 }
 
@@ -648,6 +651,7 @@ std::atomic<uint64_t> g_next_model_id{1};
 struct Linear {
   qi_hip_weights* w = nullptr;
   uint64_t k = 0, n = 0;
+  uint32_t pair_group = 0;  // two fused parts: 0 concatenated, else interleaved in groups of this many rows
 };
 
 struct Layer {
@@ -740,8 +744,12 @@ qi_hip_status upload(void* dst, const void* src, uint64_t bytes, hipStream_t st)
 // buffer and upload it as one image. Output rows: each part is [N_i][K/bs]
 // blocks, so the parts follow one another. Row-major: each part is
 // [K][N_i/bs] blocks, so row k of the result is row k of every part in turn.
+// `interleave` (two equal output-rows parts): rows alternate in groups of that
+// many, part 0's group then part 1's (a 16-output tile then holds 8 rows of
+// each, for the GEMV epilogue that pairs them).
 qi_hip_status make_linear(qi_hip_ctx* c, const qi_hip_linear_weight* const* parts, int count,
-                          uint64_t k, const uint64_t* ns, const char* name, Linear* out) {
+                          uint64_t k, const uint64_t* ns, const char* name, Linear* out,
+                          uint32_t interleave = 0) {
   const int32_t qtype = parts[0]->qtype, layout = parts[0]->layout;
   const size_t lb = logical_bytes(qtype);
   if (lb == 0) return fail(QI_HIP_INVALID_INPUT, std::string(name) + ": unknown weight type");
@@ -763,12 +771,21 @@ qi_hip_status make_linear(qi_hip_ctx* c, const qi_hip_linear_weight* const* part
   std::vector<uint8_t> joined;
   const void* blocks = parts[0]->data;
   uint64_t total = parts[0]->count;
+  const bool pair = interleave > 0 && count == 2 && rows && ns[0] == ns[1] && ns[0] % interleave == 0;
   if (count > 1) {
     total = 0;
     for (int i = 0; i < count; ++i) total += parts[i]->count;
     joined.resize(total * lb);
     uint8_t* dst = joined.data();
-    if (rows) {
+    if (pair) {
+      const uint64_t grp = static_cast<uint64_t>(interleave) * (k / bs) * lb;  // bytes of one row group
+      for (uint64_t r = 0; r < ns[0]; r += interleave) {
+        for (int i = 0; i < 2; ++i) {
+          memcpy(dst, static_cast<const uint8_t*>(parts[i]->data) + r / interleave * grp, grp);
+          dst += grp;
+        }
+      }
+    } else if (rows) {
       for (int i = 0; i < count; ++i) {
         memcpy(dst, parts[i]->data, parts[i]->count * lb);
         dst += parts[i]->count * lb;
@@ -792,6 +809,7 @@ qi_hip_status make_linear(qi_hip_ctx* c, const qi_hip_linear_weight* const* part
   if (s != QI_HIP_OK) return s;
   out->k = k;
   out->n = n;
+  out->pair_group = pair ? interleave : 0;
   return QI_HIP_OK;
 }
 
@@ -941,33 +959,20 @@ qi_hip_status residual_norm(qi_hip_qwen3* m, bool embed, const qi_hip_kv_cache* 
   return QI_HIP_OK;
 }
 
-// One-row down projection whose activation prep computes SiLU(gate) * up from
-// the gate|up row (qi::kXSilu): one launch instead of two. With `radd`, the
-// outputs are added to that row (the residual add).
-qi_hip_status down_silu(qi_hip_qwen3* m, const Linear& l, float* y, const float* radd = nullptr) {
-  const qi::Image& im = l.w->im;
-  qi::GemvMfmaArgs ga{qi::make_view(im, l.w->dev), nullptr, y, 1};
-  ga.xs = qi::kXSilu;
-  ga.gu = m->gu;
-  ga.radd = radd;
-  const int split = m->ctx->gemv_split > 0 ? m->ctx->gemv_split : qi::gemv_mfma_split(im.k, im.n);
-  QI_HIP_TRY(qi::launch_gemv_mfma(im.qtype, false, 1, split, ga, m->ctx->stream), "launch down gemv");
-  return QI_HIP_OK;
-}
-
-// The fused down projection needs the matrix-core GEMV (F32/AUTO modes, a
-// tiled f16-scale image).
-bool down_fusable(const qi_hip_qwen3* m, const Linear& l) {
+// A projection can take part in the decode fusions with the matrix-core GEMV
+// (F32/AUTO modes, a tiled f16-scale image).
+bool gemv_fusable(const qi_hip_qwen3* m, const Linear& l) {
   if (m->unfused || (m->mode != QI_HIP_MODE_AUTO && m->mode != QI_HIP_MODE_F32)) return false;
   const qi::Image& im = l.w->im;
   return im.tiled && !im.wide && qi::gemv_mfma_supported(im.qtype, im.layout, im.k);
 }
 
 // One-row matrix-core GEMV of the decoder: activation source xs (plain x,
-// or kXNorm: x = RMSNorm(h) * w with the norm's 1/rms applied to the outputs)
-// and, with `radd`, the residual add on the outputs (out may be radd).
+// or kXNorm: x = RMSNorm(h) * w with the norm's 1/rms applied to the outputs);
+// with `radd`, the residual add on the outputs (out may be radd); with
+// `pairs`, SiLU(gate) * up of an interleaved gate|up image (I outputs).
 qi_hip_status fused_linear(qi_hip_qwen3* m, const Linear& l, int xs, const float* x, const float* w,
-                           float* out, const float* radd) {
+                           float* out, const float* radd, bool pairs = false) {
   const qi::Image& im = l.w->im;
   qi::GemvMfmaArgs ga{qi::make_view(im, l.w->dev), x, out, 1};
   ga.xs = xs;
@@ -977,18 +982,21 @@ qi_hip_status fused_linear(qi_hip_qwen3* m, const Linear& l, int xs, const float
     ga.eps = m->cfg.rms_norm_eps;
   }
   ga.radd = radd;
+  ga.silu_pairs = pairs;
   const int split = m->ctx->gemv_split > 0 ? m->ctx->gemv_split : qi::gemv_mfma_split(im.k, im.n);
   QI_HIP_TRY(qi::launch_gemv_mfma(im.qtype, false, 1, split, ga, m->ctx->stream), "launch fused gemv");
   return QI_HIP_OK;
 }
 
 // A decode step folds the residual adds into the o and down GEMVs (written
-// into h) and the RMSNorms into the activation prep of the q|k|v (from layer
-// 1) and gate|up GEMVs, when all four have matrix-core images.
-bool norm_fusable(const qi_hip_qwen3* m) {
+// into h), the RMSNorms into the activation prep of the q|k|v (from layer 1)
+// and gate|up GEMVs, and SiLU(gate) * up into the gate|up GEMV epilogue, when
+// all four have matrix-core images and gate|up is interleaved by 8.
+bool decode_fusable(const qi_hip_qwen3* m) {
+  if (m->unfused) return false;
   for (const Layer& L : m->layers)
-    if (!down_fusable(m, L.qkv) || !down_fusable(m, L.o) || !down_fusable(m, L.gate_up) ||
-        !down_fusable(m, L.down))
+    if (!gemv_fusable(m, L.qkv) || !gemv_fusable(m, L.o) || !gemv_fusable(m, L.gate_up) ||
+        !gemv_fusable(m, L.down) || L.gate_up.pair_group != 8 || L.gate_up.n % 16 != 0)
       return false;
   return true;
 }
@@ -1002,7 +1010,7 @@ qi_hip_status enqueue_forward(qi_hip_qwen3* m, qi_hip_kv_cache* c, uint32_t rows
   const uint32_t H = k.hidden_size, I = k.intermediate_size, hd = k.head_dim;
   qi_hip_status s;
   if ((s = residual_norm(m, true, c, rows, m->layers[0].norms)) != QI_HIP_OK) return s;
-  if (rows == 1 && norm_fusable(m)) {
+  if (rows == 1 && decode_fusable(m)) {
     // decode step: the residual row h is updated in place by the o and down
     // GEMVs; q|k|v (from layer 1) and gate|up normalize it in their prep
     for (uint32_t l = 0; l < k.num_hidden_layers; ++l) {
@@ -1012,10 +1020,10 @@ qi_hip_status enqueue_forward(qi_hip_qwen3* m, qi_hip_kv_cache* c, uint32_t rows
       if (s != QI_HIP_OK) return s;
       if ((s = attention(m, c, l, 1)) != QI_HIP_OK) return s;
       if ((s = fused_linear(m, L.o, qi::kXPlain, m->att, nullptr, m->h, m->h)) != QI_HIP_OK) return s;
-      if ((s = fused_linear(m, L.gate_up, qi::kXNorm, nullptr, L.norms + H + 2 * hd, m->gu, nullptr)) !=
-          QI_HIP_OK)
+      if ((s = fused_linear(m, L.gate_up, qi::kXNorm, nullptr, L.norms + H + 2 * hd, m->act, nullptr,
+                            true)) != QI_HIP_OK)
         return s;
-      if ((s = down_silu(m, L.down, m->h, m->h)) != QI_HIP_OK) return s;
+      if ((s = fused_linear(m, L.down, qi::kXPlain, m->act, nullptr, m->h, m->h)) != QI_HIP_OK) return s;
     }
     if ((s = residual_norm(m, false, c, 1, m->final_norm, false)) != QI_HIP_OK) return s;
   } else {
@@ -1026,14 +1034,10 @@ qi_hip_status enqueue_forward(qi_hip_qwen3* m, qi_hip_kv_cache* c, uint32_t rows
       if ((s = linear(m, L.o, m->att, rows, m->y)) != QI_HIP_OK) return s;
       if ((s = residual_norm(m, false, c, rows, L.norms + H + 2 * hd)) != QI_HIP_OK) return s;
       if ((s = linear(m, L.gate_up, m->x, rows, m->gu)) != QI_HIP_OK) return s;
-      if (rows == 1 && down_fusable(m, L.down)) {
-        if ((s = down_silu(m, L.down, m->y)) != QI_HIP_OK) return s;
-      } else {
-        const uint64_t total = static_cast<uint64_t>(rows) * I;
-        hipLaunchKernelGGL(silu_mul_kernel, dim3(static_cast<uint32_t>((total + 255) / 256)),
-                           dim3(256), 0, st, m->gu, m->act, I, total);
-        if ((s = linear(m, L.down, m->act, rows, m->y)) != QI_HIP_OK) return s;
-      }
+      const uint64_t total = static_cast<uint64_t>(rows) * I;
+      hipLaunchKernelGGL(silu_mul_kernel, dim3(static_cast<uint32_t>((total + 255) / 256)), dim3(256), 0, st,
+                         m->gu, m->act, I, total, L.gate_up.pair_group);
+      if ((s = linear(m, L.down, m->act, rows, m->y)) != QI_HIP_OK) return s;
       const float* next = l + 1 < k.num_hidden_layers ? m->layers[l + 1].norms : m->final_norm;
       if ((s = residual_norm(m, false, c, rows, next)) != QI_HIP_OK) return s;
     }
@@ -1343,7 +1347,7 @@ qi_hip_status qi_hip_qwen3_set_layer(qi_hip_qwen3* m, uint32_t index, const qi_h
   const uint64_t nh[1] = {H};
   if ((s = make_linear(m->ctx, qkv, 3, H, nqkv, "q/k/v projection", &fresh.qkv)) != QI_HIP_OK ||
       (s = make_linear(m->ctx, o, 1, QS, nh, "o projection", &fresh.o)) != QI_HIP_OK ||
-      (s = make_linear(m->ctx, gu, 2, H, ngu, "gate/up projection", &fresh.gate_up)) != QI_HIP_OK ||
+      (s = make_linear(m->ctx, gu, 2, H, ngu, "gate/up projection", &fresh.gate_up, 8)) != QI_HIP_OK ||
       (s = make_linear(m->ctx, dn, 1, I, nh, "down projection", &fresh.down)) != QI_HIP_OK)
     return cleanup(s);
   Layer& dst = m->layers[index];
