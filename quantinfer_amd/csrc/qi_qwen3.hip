@@ -225,7 +225,8 @@ struct AttnArgs {
   float* pl;
   float* po;  // [batch row][heads][chunks][hd]
   uint32_t heads, kv_heads, cap, chunks;
-  uint32_t row0;  // first row of this batch (blockIdx row 0)
+  uint32_t row0;   // first row of this batch (blockIdx row 0)
+  uint32_t nrows;  // rows in this batch (the row-blocked prefill path)
   float scale;
   float* out;  // [rows][heads*hd]
   // fused path (one decode row): q/k/v straight from the projection
@@ -266,12 +267,19 @@ __device__ __forceinline__ float load_coherent(const float* p) {
 
 constexpr int kAttnWaves = 4;
 
-// LDS of one attention workgroup: keys [dim][64 positions], values [64][dim],
-// the rotated queries of the group, the new position's key and value, the
-// softmax weights [head][64 positions].
+// Query rows per prefill workgroup: 16 (row, head) pairs at head_dim 128 (the
+// staged queries take 8 KB and two workgroups fit a CU's LDS), 4 at head_dim
+// 64 (its fully unrolled loops keep every row's queries in registers and
+// spilled at 8 pairs).
 template <int HD, int G>
+constexpr int attn_rows() { return HD == 128 ? 16 / G : (G >= 4 ? 1 : 4 / G); }
+
+// LDS of one attention workgroup: keys [dim][64 positions], values [64][dim],
+// the rotated queries of its RB rows x G heads, the new position's key and
+// value, the softmax weights [row][head][64 positions].
+template <int HD, int G, int RB>
 constexpr uint32_t attn_lds_bytes() {
-  return static_cast<uint32_t>((2 * HD * kChunk + G * HD + 2 * HD + G * kChunk) * sizeof(float) + 16);
+  return static_cast<uint32_t>((2 * HD * kChunk + RB * G * HD + 2 * HD + RB * G * kChunk) * sizeof(float) + 16);
 }
 
 // One 4-wavefront workgroup per (chunk of 64 positions, KV head, row). The
@@ -285,25 +293,33 @@ constexpr uint32_t attn_lds_bytes() {
 // the raw projection, and the workgroup whose chunk holds the new position
 // also normalizes/rotates its key, appends key and value to the cache
 // (KvCache::append, cache.rs:96-125) and uses them for that position.
-template <int HD, int G, bool FUSED>
+// Otherwise (prompt rows, RB per workgroup): the rotated queries of RB
+// consecutive rows share the staged chunk; the ticket and the merge are per
+// (row block, KV head).
+template <int HD, int G, bool FUSED, int RB = 1>
 __global__ __launch_bounds__(64 * kAttnWaves) void attn_kernel(AttnArgs a) {
+  static_assert(!FUSED || RB == 1, "the fused decode path takes one row");
   constexpr int DPL = HD / 64;  // value dimensions per lane
   constexpr uint32_t P = HD / 2;
   constexpr int HPW = (G + kAttnWaves - 1) / kAttnWaves;  // query heads per wavefront
   extern __shared__ __attribute__((aligned(16))) float attn_lds[];
   float* ks = attn_lds;                  // [HD][64]
   float* vs = ks + HD * kChunk;          // [64][HD]
-  float* qs = vs + kChunk * HD;          // [G][HD]
-  float* kn = qs + G * HD;               // [HD]
+  float* qs = vs + kChunk * HD;          // [RB][G][HD]
+  float* kn = qs + RB * G * HD;          // [HD]
   float* vn = kn + HD;                   // [HD]
-  float* pe = vn + HD;                   // [G][64]
-  uint32_t* flag = reinterpret_cast<uint32_t*>(pe + G * kChunk);
-  const uint32_t c = blockIdx.x, g = blockIdx.y, rb = blockIdx.z;
+  float* pe = vn + HD;                   // [RB][G][64]
+  uint32_t* flag = reinterpret_cast<uint32_t*>(pe + RB * G * kChunk);
+  const uint32_t c = blockIdx.x, g = blockIdx.y;
   const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const uint32_t r = rb + a.row0;
-  const uint32_t pos = *a.len + r;
+  // rows rb0 .. rb0 + nrb - 1 of the batch (one row on the fused path)
+  const uint32_t rb0 = blockIdx.z * RB;
+  const uint32_t nrb = FUSED ? 1u : (a.nrows - rb0 < static_cast<uint32_t>(RB) ? a.nrows - rb0 : RB);
+  const uint32_t r = rb0 + a.row0;
+  const uint32_t pos = *a.len + r;        // the first row's position
+  const uint32_t pos_last = pos + nrb - 1;
   const uint32_t t0 = c * kChunk;
-  if (t0 > pos) return;  // chunks past the query position take no part
+  if (t0 > pos_last) return;  // chunks past every row's position take no part
   const uint32_t tp = pos - t0;  // the query position within this chunk (if < 64)
   const bool owner = FUSED && tp < kChunk;
   const bool act = lane < P;
@@ -382,8 +398,10 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attn_kernel(AttnArgs a) {
       }
     }
   } else {
-    const float* qg = a.q + (static_cast<uint64_t>(r) * a.heads + g * G) * HD;
-    for (uint32_t i = tid; i < G * HD; i += 64 * kAttnWaves) qs[i] = qg[i];
+    for (uint32_t i = tid; i < RB * G * HD; i += 64 * kAttnWaves) {
+      const uint32_t rr = i / (G * HD), j = i % (G * HD);
+      qs[i] = rr < nrb ? a.q[(static_cast<uint64_t>(r + rr) * a.heads + g * G) * HD + j] : 0.0f;
+    }
   }
   __syncthreads();  // LDS: queries, new key/value, and the DMA'd chunk (vmcnt drained)
   if (owner) {
@@ -395,55 +413,68 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attn_kernel(AttnArgs a) {
     __syncthreads();
   }
 
-  // 4. this wavefront's heads: scores (lane t: position t0 + t; four partial
-  // sums over the dimensions), softmax pieces, value sums. Positions past the
-  // query get weight 0; the cache holds finite values there (zeroed at
-  // creation, earlier tokens after a reset), so their products vanish.
-  const bool valid = t0 + lane <= pos;
-  float s[HPW];
+  // 4. this wavefront's heads for every row of the block at once (each key
+  // and value read from LDS serves all RB rows): scores (lane t: position
+  // t0 + t; four partial sums over the dimensions), softmax pieces, value
+  // sums. Positions past a row's query get weight 0; the cache holds finite
+  // values there (zeroed at creation, earlier tokens after a reset), so their
+  // products vanish. Rows past the block or before the chunk are not stored.
+  float s[RB][HPW];
   {
-    float sp[HPW][4];
+    float sp[RB][HPW][4];
 #pragma unroll
-    for (int i = 0; i < HPW; ++i)
+    for (int rr = 0; rr < RB; ++rr)
 #pragma unroll
-      for (int u = 0; u < 4; ++u) sp[i][u] = 0.0f;
+      for (int i = 0; i < HPW; ++i)
+#pragma unroll
+        for (int u = 0; u < 4; ++u) sp[rr][i][u] = 0.0f;
 #pragma unroll 2
     for (int d0 = 0; d0 < HD; d0 += 32) {
       float kv[32];
 #pragma unroll
       for (int u = 0; u < 32; ++u) kv[u] = ks[(d0 + u) * kChunk + lane];
 #pragma unroll
-      for (int i = 0; i < HPW; ++i) {
-        const uint32_t h = wave + kAttnWaves * i;
-        const float4* qv = reinterpret_cast<const float4*>(qs + (h < G ? h : 0) * HD + d0);
+      for (int rr = 0; rr < RB; ++rr)
 #pragma unroll
-        for (int u4 = 0; u4 < 8; ++u4) {
-          const float4 q4 = qv[u4];
-          sp[i][0] = fmaf(q4.x, kv[4 * u4], sp[i][0]);
-          sp[i][1] = fmaf(q4.y, kv[4 * u4 + 1], sp[i][1]);
-          sp[i][2] = fmaf(q4.z, kv[4 * u4 + 2], sp[i][2]);
-          sp[i][3] = fmaf(q4.w, kv[4 * u4 + 3], sp[i][3]);
+        for (int i = 0; i < HPW; ++i) {
+          const uint32_t h = wave + kAttnWaves * i;
+          const float4* qv = reinterpret_cast<const float4*>(qs + (rr * G + (h < G ? h : 0)) * HD + d0);
+#pragma unroll
+          for (int u4 = 0; u4 < 8; ++u4) {
+            const float4 q4 = qv[u4];
+            sp[rr][i][0] = fmaf(q4.x, kv[4 * u4], sp[rr][i][0]);
+            sp[rr][i][1] = fmaf(q4.y, kv[4 * u4 + 1], sp[rr][i][1]);
+            sp[rr][i][2] = fmaf(q4.z, kv[4 * u4 + 2], sp[rr][i][2]);
+            sp[rr][i][3] = fmaf(q4.w, kv[4 * u4 + 3], sp[rr][i][3]);
+          }
         }
-      }
     }
 #pragma unroll
-    for (int i = 0; i < HPW; ++i) s[i] = (sp[i][0] + sp[i][1]) + (sp[i][2] + sp[i][3]);
+    for (int rr = 0; rr < RB; ++rr)
+#pragma unroll
+      for (int i = 0; i < HPW; ++i) s[rr][i] = (sp[rr][i][0] + sp[rr][i][1]) + (sp[rr][i][2] + sp[rr][i][3]);
   }
-  float e[HPW], m[HPW], l[HPW];
+  float m[RB][HPW], l[RB][HPW];
 #pragma unroll
-  for (int i = 0; i < HPW; ++i) {
-    const uint32_t h = wave + kAttnWaves * i;
-    const float sc = valid ? s[i] * a.scale : -INFINITY;
-    m[i] = wave_max(sc);
-    e[i] = valid ? expf(sc - m[i]) : 0.0f;
-    l[i] = wave_sum(e[i]);
-    if (h < G) pe[h * kChunk + lane] = e[i];  // read back by this wavefront only
+  for (int rr = 0; rr < RB; ++rr) {
+    const bool valid = t0 + lane <= pos + rr;
+#pragma unroll
+    for (int i = 0; i < HPW; ++i) {
+      const uint32_t h = wave + kAttnWaves * i;
+      const float sc = valid ? s[rr][i] * a.scale : -INFINITY;
+      m[rr][i] = wave_max(sc);
+      const float e = valid ? expf(sc - m[rr][i]) : 0.0f;
+      l[rr][i] = wave_sum(e);
+      if (h < G) pe[(rr * G + h) * kChunk + lane] = e;  // read back by this wavefront only
+    }
   }
-  float acc[HPW][DPL];
+  float acc[RB][HPW][DPL];
 #pragma unroll
-  for (int i = 0; i < HPW; ++i)
+  for (int rr = 0; rr < RB; ++rr)
 #pragma unroll
-    for (int j = 0; j < DPL; ++j) acc[i][j] = 0.0f;
+    for (int i = 0; i < HPW; ++i)
+#pragma unroll
+      for (int j = 0; j < DPL; ++j) acc[rr][i][j] = 0.0f;
   // all 64 positions: the weights come back from LDS four at a time (the same
   // address for every lane), lane l sums value dimensions l*DPL .. l*DPL+DPL-1
 #pragma unroll 4
@@ -454,34 +485,40 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attn_kernel(AttnArgs a) {
 #pragma unroll
       for (int j = 0; j < DPL; ++j) v[u][j] = vs[(4 * t4 + u) * HD + lane * DPL + j];
 #pragma unroll
+    for (int rr = 0; rr < RB; ++rr)
+#pragma unroll
+      for (int i = 0; i < HPW; ++i) {
+        const uint32_t h = wave + kAttnWaves * i;
+        const float4 w4 = reinterpret_cast<const float4*>(pe + (rr * G + (h < G ? h : 0)) * kChunk)[t4];
+        const float wt[4] = {w4.x, w4.y, w4.z, w4.w};
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+          for (int j = 0; j < DPL; ++j) acc[rr][i][j] = fmaf(wt[u], v[u][j], acc[rr][i][j]);
+      }
+  }
+#pragma unroll
+  for (int rr = 0; rr < RB; ++rr) {
+    if (static_cast<uint32_t>(rr) >= nrb || t0 > pos + rr) continue;
+#pragma unroll
     for (int i = 0; i < HPW; ++i) {
       const uint32_t h = wave + kAttnWaves * i;
-      const float4 w4 = reinterpret_cast<const float4*>(pe + (h < G ? h : 0) * kChunk)[t4];
-      const float wt[4] = {w4.x, w4.y, w4.z, w4.w};
+      if (h >= G) continue;
+      const uint64_t idx = (static_cast<uint64_t>(rb0 + rr) * a.heads + g * G + h) * a.chunks + c;
+      if (lane == 0) {
+        store_coherent(a.pm + idx, m[rr][i]);
+        store_coherent(a.pl + idx, l[rr][i]);
+      }
 #pragma unroll
-      for (int u = 0; u < 4; ++u)
-#pragma unroll
-        for (int j = 0; j < DPL; ++j) acc[i][j] = fmaf(wt[u], v[u][j], acc[i][j]);
+      for (int j = 0; j < DPL; ++j) store_coherent(a.po + idx * HD + lane * DPL + j, acc[rr][i][j]);
     }
-  }
-#pragma unroll
-  for (int i = 0; i < HPW; ++i) {
-    const uint32_t h = wave + kAttnWaves * i;
-    if (h >= G) continue;
-    const uint64_t idx = (static_cast<uint64_t>(rb) * a.heads + g * G + h) * a.chunks + c;
-    if (lane == 0) {
-      store_coherent(a.pm + idx, m[i]);
-      store_coherent(a.pl + idx, l[i]);
-    }
-#pragma unroll
-    for (int j = 0; j < DPL; ++j) store_coherent(a.po + idx * HD + lane * DPL + j, acc[i][j]);
   }
 
-  // 5. the last workgroup of this (row, KV head) combines its query heads
-  const uint32_t nc = pos / kChunk + 1;
+  // 5. the last workgroup of this (row block, KV head) combines its query heads
+  const uint32_t nc = pos_last / kChunk + 1;
   __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores are complete
   __syncthreads();
-  const uint64_t ticket = static_cast<uint64_t>(rb) * a.kv_heads + g;
+  const uint64_t ticket = static_cast<uint64_t>(blockIdx.z) * a.kv_heads + g;
   if (tid == 0) *flag = atomicAdd(&a.tickets[ticket], 1u) == nc - 1 ? 1u : 0u;
   __syncthreads();
   if (*flag == 0) return;
@@ -489,17 +526,19 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attn_kernel(AttnArgs a) {
   // first 16 chunk outputs are loaded together (one round trip for up to 16
   // chunks), the running output and denominator are rescaled when the maximum
   // grows: out = sum_c e^(m_c - M) o_c / sum_c e^(m_c - M) l_c.
+  for (uint32_t rr = 0; rr < nrb; ++rr)
 #pragma unroll
   for (int i = 0; i < HPW; ++i) {
     const uint32_t hl = wave + kAttnWaves * i;
     if (hl >= G) continue;
     const uint32_t h = g * G + hl;
-    const uint64_t base = (static_cast<uint64_t>(rb) * a.heads + h) * a.chunks;
+    const uint32_t ncr = (pos + rr) / kChunk + 1;  // chunks this row attends to
+    const uint64_t base = (static_cast<uint64_t>(rb0 + rr) * a.heads + h) * a.chunks;
     float mx = -INFINITY, denom = 0.0f, out[DPL];
 #pragma unroll
     for (int j = 0; j < DPL; ++j) out[j] = 0.0f;
-    for (uint32_t c0 = 0; c0 < nc; c0 += 64) {
-      const uint32_t n = nc - c0 < 64 ? nc - c0 : 64;
+    for (uint32_t c0 = 0; c0 < ncr; c0 += 64) {
+      const uint32_t n = ncr - c0 < 64 ? ncr - c0 : 64;
       const bool have = lane < n;
       const float* o = a.po + (base + c0) * HD + lane * DPL;
       const float gm_l = have ? load_coherent(a.pm + base + c0 + lane) : -INFINITY;
@@ -541,7 +580,7 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attn_kernel(AttnArgs a) {
         }
       }
     }
-    float* dst = a.out + (static_cast<uint64_t>(r) * a.heads + h) * HD + lane * DPL;
+    float* dst = a.out + (static_cast<uint64_t>(r + rr) * a.heads + h) * HD + lane * DPL;
 #pragma unroll
     for (int j = 0; j < DPL; ++j) dst[j] = out[j] / denom;
   }
@@ -890,16 +929,19 @@ qi_hip_status attention(qi_hip_qwen3* m, qi_hip_kv_cache* c, uint32_t layer, uin
     const uint32_t nr = rows - r0 < c->rb ? rows - r0 : c->rb;
     AttnArgs b = a;
     b.row0 = r0;
-    const dim3 pg(a.chunks, a.kv_heads, nr);
-#define QI_ATTN(HD_, G_)                                                                   \
-  if (hd == HD_ && group == G_) {                                                          \
-    const uint32_t bytes = attn_lds_bytes<HD_, G_>();                                      \
-    if (fused)                                                                             \
-      hipLaunchKernelGGL((attn_kernel<HD_, G_, true>), pg, dim3(64 * kAttnWaves), bytes,   \
-                         st, b);                                                           \
-    else                                                                                   \
-      hipLaunchKernelGGL((attn_kernel<HD_, G_, false>), pg, dim3(64 * kAttnWaves), bytes,  \
-                         st, b);                                                           \
+    b.nrows = nr;
+#define QI_ATTN(HD_, G_)                                                                         \
+  if (hd == HD_ && group == G_) {                                                                \
+    constexpr int RB_ = attn_rows<HD_, G_>();                                                         \
+    constexpr uint32_t one_ = attn_lds_bytes<HD_, G_, 1>();                                      \
+    constexpr uint32_t blk_ = attn_lds_bytes<HD_, G_, RB_>();                                    \
+    if (fused)                                                                                   \
+      hipLaunchKernelGGL((attn_kernel<HD_, G_, true>), dim3(a.chunks, a.kv_heads, nr),           \
+                         dim3(64 * kAttnWaves), one_, st, b);                                    \
+    else                                                                                         \
+      hipLaunchKernelGGL((attn_kernel<HD_, G_, false, RB_>),                                     \
+                         dim3(a.chunks, a.kv_heads, (nr + RB_ - 1) / RB_), dim3(64 * kAttnWaves), \
+                         blk_, st, b);                                                           \
   } else
     QI_ATTN(128, 1) QI_ATTN(128, 2) QI_ATTN(128, 4) QI_ATTN(128, 8)
     QI_ATTN(64, 1) QI_ATTN(64, 2) QI_ATTN(64, 4) QI_ATTN(64, 8)
@@ -914,12 +956,13 @@ qi_hip_status attention(qi_hip_qwen3* m, qi_hip_kv_cache* c, uint32_t layer, uin
 // kernels' dynamic LDS limit once, outside any stream capture.
 template <int HD, int G>
 hipError_t attn_set_lds() {
-  const int bytes = static_cast<int>(attn_lds_bytes<HD, G>());
   hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(attn_kernel<HD, G, true>),
-                                     hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+                                     hipFuncAttributeMaxDynamicSharedMemorySize,
+                                     static_cast<int>(attn_lds_bytes<HD, G, 1>()));
   if (e == hipSuccess)
-    e = hipFuncSetAttribute(reinterpret_cast<const void*>(attn_kernel<HD, G, false>),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+    e = hipFuncSetAttribute(reinterpret_cast<const void*>(attn_kernel<HD, G, false, attn_rows<HD, G>()>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize,
+                            static_cast<int>(attn_lds_bytes<HD, G, attn_rows<HD, G>()>()));
   return e;
 }
 

@@ -186,6 +186,32 @@ def test_head_dim_128_group_4(qa, ctx):
     dev.free()
 
 
+def test_head_dim_128_prefill_row_blocks(qa, ctx):
+    """AUTO prefill at head_dim 128, 4 query heads per KV head: the prompt
+    attention runs in blocks of 4 rows per workgroup (302 rows: a partial last
+    block), then decode continues from the same cache."""
+    cfg = small_config(hidden_size=1024, intermediate_size=1024, num_hidden_layers=1,
+                       num_attention_heads=8, num_key_value_heads=2, head_dim=128,
+                       vocab_size=2048, max_position_embeddings=512)
+    w = Qwen3Weights(cfg, seed=0x5EED0105)
+    dev = w.device_model(ctx)
+    dev.set_mode(qa.MODE_AUTO)
+    toks = prompt(cfg, 302, seed=16)
+    print("qwen3 hd128 auto prompt=302", flush=True)
+    cache = dev.kv_cache(320)
+    ref = w.oracle_model(320)
+    logits, nxt = dev.forward(cache, toks)
+    want = ref.forward(toks, last_only=True)[0]
+    err = _rel(logits, want)
+    print(f"  prefill rel err {err:.2e}", flush=True)
+    assert err <= TOL_MFMA
+    assert nxt == int(np.argmax(want))
+    lg, _ = dev.forward(cache, [nxt])
+    wl = ref.forward([nxt], last_only=True)[0]
+    assert _rel(lg, wl) <= TOL_MFMA
+    dev.free()
+
+
 def test_errors(qa, ctx, small):
     cfg, w, dev = small
     cache = dev.kv_cache(16)
