@@ -161,6 +161,25 @@ qi_hip_status qi_hip_pack_weights(int32_t qtype, int32_t layout, uint64_t k, uin
                                   const void *blocks, uint64_t count, void *out, uint64_t *bytes,
                                   int32_t *f16_scales);
 
+/* Upload a GGUF tensor's block bytes directly: `wire` holds `wire_bytes` bytes
+ * of GGUF wire blocks of `qtype` (Q8_0 34 B, Q4_0 18 B, Q4_K 144 B, Q5_K 176 B,
+ * Q6_K 210 B per block; QI_HIP_F32: little-endian f32 values) in the block
+ * order of `layout`. legacy = 1 reads the files' old layout (Q4_0 nibble pairs
+ * (2j, 2j+1); Q6_K d, scales, ql, qh), which the reader selects by file
+ * version (format/src/gguf/decode.rs:168-172, 288-290); the other types ignore
+ * it. Decoding and validation are the reference's GGUF block readers
+ * (format/src/gguf/decode.rs:90-312: byte length a multiple of the block
+ * size, finite f16 scales), then as qi_hip_weights_create.
+ * Replaces: GgufFile::tensor_q8_0 / tensor_q4_0 / tensor_q4_k / tensor_q5_k /
+ * tensor_q6_k (format/src/gguf/decode.rs:90-312) followed by the upload. */
+qi_hip_status qi_hip_weights_create_gguf(qi_hip_ctx *ctx, int32_t qtype, int32_t layout, uint64_t k,
+                                         uint64_t n, const void *wire, uint64_t wire_bytes,
+                                         int32_t legacy, qi_hip_weights **out);
+/* Host-only: the device image of a GGUF tensor, as qi_hip_pack_weights. */
+qi_hip_status qi_hip_pack_gguf(int32_t qtype, int32_t layout, uint64_t k, uint64_t n,
+                               const void *wire, uint64_t wire_bytes, int32_t legacy, void *out,
+                               uint64_t *bytes, int32_t *f16_scales);
+
 /* ------------------------------------------------------------------------
  * GPU-resident Qwen3 dense decoder.
  *

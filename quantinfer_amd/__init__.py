@@ -106,6 +106,9 @@ def lib() -> ctypes.CDLL:
         l.qi_hip_dequantize_device.argtypes = [vp, vp, vp, vp]
         l.qi_hip_pack_weights.argtypes = [i32, i32, u64, u64, vp, u64, vp,
                                           ctypes.POINTER(u64), ctypes.POINTER(i32)]
+        l.qi_hip_weights_create_gguf.argtypes = [vp, i32, i32, u64, u64, vp, u64, i32, ctypes.POINTER(vp)]
+        l.qi_hip_pack_gguf.argtypes = [i32, i32, u64, u64, vp, u64, i32, vp, ctypes.POINTER(u64),
+                                       ctypes.POINTER(i32)]
         u32 = ctypes.c_uint32
         l.qi_hip_qwen3_create.argtypes = [vp, ctypes.POINTER(Qwen3Config), ctypes.POINTER(vp)]
         l.qi_hip_qwen3_set_embedding.argtypes = [vp, vp]
@@ -125,6 +128,7 @@ def lib() -> ctypes.CDLL:
         for name in ("qi_hip_open", "qi_hip_device_name", "qi_hip_weights_create",
                      "qi_hip_weights_info_get", "qi_hip_linear", "qi_hip_linear_device",
                      "qi_hip_dequantize", "qi_hip_dequantize_device", "qi_hip_pack_weights",
+                     "qi_hip_weights_create_gguf", "qi_hip_pack_gguf",
                      "qi_hip_qwen3_create", "qi_hip_qwen3_set_embedding", "qi_hip_qwen3_set_layer",
                      "qi_hip_qwen3_set_output", "qi_hip_qwen3_set_mode", "qi_hip_kv_cache_create",
                      "qi_hip_kv_cache_length", "qi_hip_kv_cache_reset", "qi_hip_qwen3_forward",
@@ -160,6 +164,21 @@ def pack_weights(qtype: int, layout: int, k: int, n: int, blocks: np.ndarray):
     return out, bool(f16.value)
 
 
+def pack_gguf(qtype: int, layout: int, k: int, n: int, wire, legacy: bool = False):
+    """Host-only device image (bytes, f16_scales) of a GGUF tensor's wire blocks,
+    exactly as weights_gguf builds it."""
+    w = np.ascontiguousarray(np.frombuffer(bytes(wire), dtype=np.uint8) if not isinstance(wire, np.ndarray)
+                             else wire.view(np.uint8).reshape(-1))
+    size = ctypes.c_uint64(0)
+    f16 = ctypes.c_int32(0)
+    _check(lib().qi_hip_pack_gguf(qtype, layout, k, n, _ptr(w), w.size, int(legacy), None,
+                                  ctypes.byref(size), ctypes.byref(f16)))
+    out = np.zeros(size.value, dtype=np.uint8)
+    _check(lib().qi_hip_pack_gguf(qtype, layout, k, n, _ptr(w), w.size, int(legacy), _ptr(out),
+                                  ctypes.byref(size), ctypes.byref(f16)))
+    return out, bool(f16.value)
+
+
 class Context:
     """An open gfx950 device (qi_hip_open)."""
 
@@ -187,9 +206,26 @@ class Context:
     def weights(self, qtype: int, layout: int, k: int, n: int, blocks: np.ndarray) -> "Weights":
         return Weights(self, qtype, layout, k, n, blocks)
 
+    def weights_gguf(self, qtype: int, layout: int, k: int, n: int, wire,
+                     legacy: bool = False) -> "Weights":
+        """A resident weight from a GGUF tensor's wire block bytes
+        (qi_hip_weights_create_gguf)."""
+        w = np.ascontiguousarray(np.frombuffer(bytes(wire), dtype=np.uint8) if not isinstance(wire, np.ndarray)
+                                 else wire.view(np.uint8).reshape(-1))
+        h = ctypes.c_void_p()
+        _check(lib().qi_hip_weights_create_gguf(self.handle, qtype, layout, k, n, _ptr(w), w.size,
+                                                int(legacy), ctypes.byref(h)))
+        return Weights._adopt(self, h, qtype, layout, k, n)
+
 
 class Weights:
     """A resident weight of logical shape [K, N] (qi_hip_weights_create)."""
+
+    @classmethod
+    def _adopt(cls, ctx: "Context", handle, qtype: int, layout: int, k: int, n: int) -> "Weights":
+        w = cls.__new__(cls)
+        w.ctx, w.handle, w.qtype, w.layout, w.k, w.n = ctx, handle, qtype, layout, k, n
+        return w
 
     def __init__(self, ctx: Context, qtype: int, layout: int, k: int, n: int, blocks: np.ndarray):
         b = np.ascontiguousarray(blocks)

@@ -13,6 +13,7 @@
 #include <atomic>
 #include <mutex>
 #include <string>
+#include <vector>
 
 #include "../../include/qi_hip.h"
 #include "qi_image.h"
@@ -290,6 +291,30 @@ qi_hip_status qi_hip_pack_weights(int32_t qtype, int32_t layout, uint64_t k, uin
   *bytes = im.bytes;
   if (f16_scales) *f16_scales = im.wide ? 0 : 1;
   return QI_HIP_OK;
+}
+
+qi_hip_status qi_hip_pack_gguf(int32_t qtype, int32_t layout, uint64_t k, uint64_t n, const void* wire,
+                               uint64_t wire_bytes, int32_t legacy, void* out, uint64_t* bytes,
+                               int32_t* f16_scales) {
+  std::vector<uint8_t> blocks;
+  uint64_t count = 0;
+  const char* why = "";
+  const qi_hip_status s = qi::gguf_decode(qtype, wire, wire_bytes, legacy, &blocks, &count, &why);
+  if (s != QI_HIP_OK) return fail(s, why);
+  return qi_hip_pack_weights(qtype, layout, k, n, blocks.data(), count, out, bytes, f16_scales);
+}
+
+qi_hip_status qi_hip_weights_create_gguf(qi_hip_ctx* c, int32_t qtype, int32_t layout, uint64_t k,
+                                         uint64_t n, const void* wire, uint64_t wire_bytes, int32_t legacy,
+                                         qi_hip_weights** out) {
+  if (c == nullptr || out == nullptr) return fail(QI_HIP_INVALID_INPUT, "null context or output");
+  *out = nullptr;
+  std::vector<uint8_t> blocks;
+  uint64_t count = 0;
+  const char* why = "";
+  const qi_hip_status s = qi::gguf_decode(qtype, wire, wire_bytes, legacy, &blocks, &count, &why);
+  if (s != QI_HIP_OK) return fail(s, why);
+  return qi_hip_weights_create(c, qtype, layout, k, n, blocks.data(), count, out);
 }
 
 qi_hip_status qi_hip_weights_create(qi_hip_ctx* c, int32_t qtype, int32_t layout, uint64_t k,

@@ -152,6 +152,12 @@ int32_t plan_image(int32_t qtype, int32_t layout, uint64_t k, uint64_t n, const 
                    uint64_t count, Image* out, const char** why);
 // Write the image into host memory of im.bytes bytes.
 void fill_image(const Image& im, const void* blocks, void* out);
+// GGUF wire blocks (`bytes` bytes) to logical blocks in `out` (resized), the
+// block count in *count; legacy selects the old Q4_0 nibble pairs and Q6_K
+// field order (others have one layout); QI_HIP_F32 passes f32 values through.
+// Returns 0 or an ABI status with a message in *why.
+int32_t gguf_decode(int32_t qtype, const void* wire, uint64_t bytes, int32_t legacy, void* out_vec,
+                    uint64_t* count, const char** why);
 
 // Tiled Q6_K record: byte position (0..15) of sub-scale i within a row's 16.
 constexpr uint32_t q6_scale_pos(uint32_t i) {

@@ -2,6 +2,8 @@
 #include <math.h>
 #include <string.h>
 
+#include <vector>
+
 #include "../../include/qi_hip.h"
 #include "qi_image.h"
 
@@ -271,6 +273,121 @@ void fill_image(const Image& im, const void* blocks, void* out) {
       }
     }
   }
+}
+
+}  // namespace qi
+
+namespace qi {
+
+namespace {
+
+// f16 little-endian to f32 (exact); false for inf/NaN, which the GGUF block
+// readers reject (format/src/gguf/decode.rs:110-116 and the other types).
+bool wire_f16(const uint8_t* p, float* out) {
+  _Float16 h;
+  memcpy(&h, p, 2);
+  *out = static_cast<float>(h);
+  return isfinite(*out);
+}
+
+}  // namespace
+
+// The GGUF block readers of format/src/gguf/decode.rs: tensor_q8_0 (:90-130),
+// tensor_q4_0 (:132-179, legacy nibble pairs :168-172), tensor_q4_k
+// (:181-227), tensor_q5_k (:229-268), tensor_q6_k (:270-312, legacy field
+// order :288-290), writing the logical blocks of include/qi_hip.h.
+int32_t gguf_decode(int32_t qtype, const void* wire, uint64_t bytes, int32_t legacy, void* out_vec,
+                    uint64_t* count, const char** why) {
+  std::vector<uint8_t>& out = *static_cast<std::vector<uint8_t>*>(out_vec);
+  const uint8_t* in = static_cast<const uint8_t*>(wire);
+  if (wire == nullptr && bytes != 0) {
+    *why = "null wire data";
+    return QI_HIP_INVALID_INPUT;
+  }
+  uint64_t wb = 0, lb = 0;
+  switch (qtype) {
+    case kF32: wb = lb = 4; break;
+    case kQ8_0: wb = 34; lb = sizeof(qi_hip_q8_0_block); break;
+    case kQ4_0: wb = 18; lb = sizeof(qi_hip_q4_0_block); break;
+    case kQ4_K: wb = 144; lb = sizeof(qi_hip_q4_k_block); break;
+    case kQ5_K: wb = 176; lb = sizeof(qi_hip_q5_k_block); break;
+    case kQ6_K: wb = 210; lb = sizeof(qi_hip_q6_k_block); break;
+    default: *why = "unknown weight type"; return QI_HIP_UNSUPPORTED;
+  }
+  if (bytes % wb != 0) {
+    *why = "GGUF tensor has an invalid byte length";
+    return QI_HIP_INVALID_INPUT;
+  }
+  const uint64_t nb = bytes / wb;
+  *count = nb;
+  out.assign(nb * lb, 0);
+  if (qtype == kF32) {
+    if (bytes) memcpy(out.data(), in, bytes);
+    return QI_HIP_OK;
+  }
+  for (uint64_t i = 0; i < nb; ++i) {
+    const uint8_t* c = in + i * wb;
+    uint8_t* o = out.data() + i * lb;
+    bool ok = true;
+    switch (qtype) {
+      case kQ8_0: {
+        qi_hip_q8_0_block b;
+        ok = wire_f16(c, &b.scale);
+        memcpy(b.values, c + 2, 32);
+        memcpy(o, &b, sizeof b);
+        break;
+      }
+      case kQ4_0: {
+        qi_hip_q4_0_block b;
+        ok = wire_f16(c, &b.scale);
+        for (int j = 0; j < 16; ++j) {
+          const uint8_t packed = c[2 + j];
+          const int lo = legacy ? 2 * j : j, hi = legacy ? 2 * j + 1 : j + 16;
+          b.values[lo] = packed & 0x0F;
+          b.values[hi] = packed >> 4;
+        }
+        memcpy(o, &b, sizeof b);
+        break;
+      }
+      case kQ4_K: {
+        qi_hip_q4_k_block b;
+        ok = wire_f16(c, &b.scale) & wire_f16(c + 2, &b.min_scale);
+        memcpy(b.scales, c + 4, 12);
+        memcpy(b.values, c + 16, 128);
+        memcpy(o, &b, sizeof b);
+        break;
+      }
+      case kQ5_K: {
+        qi_hip_q5_k_block b;
+        ok = wire_f16(c, &b.scale) & wire_f16(c + 2, &b.min_scale);
+        memcpy(b.scales, c + 4, 12);
+        memcpy(b.high_bits, c + 16, 32);
+        memcpy(b.values, c + 48, 128);
+        memcpy(o, &b, sizeof b);
+        break;
+      }
+      default: {  // kQ6_K
+        qi_hip_q6_k_block b;
+        const uint8_t *d, *sc, *ql, *qh;
+        if (legacy) {
+          d = c; sc = c + 2; ql = c + 18; qh = c + 146;
+        } else {
+          ql = c; qh = c + 128; sc = c + 192; d = c + 208;
+        }
+        ok = wire_f16(d, &b.scale);
+        memcpy(b.scales, sc, 16);
+        memcpy(b.low_bits, ql, 128);
+        memcpy(b.high_bits, qh, 64);
+        memcpy(o, &b, sizeof b);
+        break;
+      }
+    }
+    if (!ok) {
+      *why = "GGUF tensor contains a non-finite scale";
+      return QI_HIP_INVALID_INPUT;
+    }
+  }
+  return QI_HIP_OK;
 }
 
 }  // namespace qi

@@ -268,3 +268,106 @@ def test_null_arguments_are_invalid_not_crashes():
     assert lib.qi_hip_pack_weights(1, 1, 32, 1, None, 1, None, ctypes.byref(size), None) == qa.INVALID_INPUT
     lib.qi_hip_close(None)
     lib.qi_hip_weights_free(None)
+
+
+# ------------------------------------------------ direct GGUF upload (host image)
+GOLDEN = os.path.join(ROOT, "tests", "golden", "reference_known_answers.json")
+NAME_Q = {"q4_0": qa.Q4_0, "q6_k": qa.Q6_K, "q4_k": qa.Q4_K}
+
+
+def _golden_block(qtype, spec):
+    b = np.zeros(1, dtype=po.BLOCK_DTYPES[qtype])
+    for field, value in spec.items():
+        b[field][0] = value
+    return b
+
+
+def test_gguf_upload_matches_reference_wire_vectors():
+    """The reference's own standard and legacy wire bytes (format/src/gguf/
+    tests.rs:163-212) decode to the image of the block they encode."""
+    import json
+    cases = [e for e in json.load(open(GOLDEN))["wire"] if e.get("qtype") in NAME_Q and "block" in e]
+    assert {e["qtype"] for e in cases} >= {"q4_0", "q6_k"}
+    for e in cases:
+        q = NAME_Q[e["qtype"]]
+        k = po.BLOCK_ELEMS[q]
+        block = _golden_block(q, e["block"])
+        want, _ = qa.pack_weights(q, qa.OUTPUT_ROWS, k, 1, block)
+        for key, legacy in (("standard_bytes", False), ("legacy_bytes", True)):
+            if key in e:
+                got, f16 = qa.pack_gguf(q, qa.OUTPUT_ROWS, k, 1, bytes(e[key]), legacy=legacy)
+                assert f16 and got.tobytes() == want.tobytes(), (e["name"], key)
+        if "standard_bytes" not in e:
+            wire = po.wire_pack(q, block)
+            got, _ = qa.pack_gguf(q, qa.OUTPUT_ROWS, k, 1, wire)
+            assert got.tobytes() == want.tobytes(), e["name"]
+
+
+@pytest.mark.parametrize("qtype", ALL_Q, ids=lambda q: po.NAMES[q] if hasattr(po, "NAMES") else str(q))
+def test_gguf_upload_equals_logical_upload(qtype):
+    """Standard wire bytes from the oracle's GGUF writer restatement give the
+    same device image as the logical blocks, for the tiled (K % 256 == 0) and
+    the planar (K % 256 != 0, Q8_0/Q4_0) images and both layouts."""
+    shapes = [(512, 48, qa.OUTPUT_ROWS)]
+    if po.BLOCK_ELEMS[qtype] == 32:
+        shapes += [(96, 40, qa.OUTPUT_ROWS), (64, 96, qa.ROW_MAJOR)]
+    else:
+        shapes += [(256, 512, qa.ROW_MAJOR)]
+    for k, n, layout in shapes:
+        blocks = po.make_weights(qtype, k, n, seed=0x66 + qtype + k, outliers=True)
+        if layout == qa.ROW_MAJOR:
+            blocks = po.make_weights(qtype, n, k, seed=0x67 + qtype)  # [K][N/bs] blocks along N
+        want, wf16 = qa.pack_weights(qtype, layout, k, n, blocks)
+        got, gf16 = qa.pack_gguf(qtype, layout, k, n, po.wire_pack(qtype, blocks))
+        assert wf16 and gf16
+        assert got.tobytes() == want.tobytes(), (k, n, layout)
+
+
+@pytest.mark.parametrize("qtype", [qa.Q4_0, qa.Q6_K], ids=["q4_0", "q6_k"])
+def test_gguf_upload_legacy_layout(qtype):
+    """Random legacy-layout bytes with finite f16 scales: the library's reader
+    equals the oracle's restatement of decode.rs (legacy branches :168-172,
+    :288-290)."""
+    rng = np.random.default_rng(0x1E6 + qtype)
+    wb = {qa.Q4_0: 18, qa.Q6_K: 210}[qtype]
+    k, n = (64, 8) if qtype == qa.Q4_0 else (256, 8)
+    count = n * k // po.BLOCK_ELEMS[qtype]
+    raw = np.frombuffer(rng.bytes(count * wb), dtype=np.uint8).copy().reshape(count, wb)
+    scale = np.float16(rng.uniform(0.001, 0.01, count)).view(np.uint8).reshape(count, 2)
+    at = 0 if qtype == qa.Q4_0 else 0  # legacy: d first for both
+    raw[:, at:at + 2] = scale
+    logical = po.wire_unpack(qtype, raw.tobytes(), legacy=True)
+    want, _ = qa.pack_weights(qtype, qa.OUTPUT_ROWS, k, n, logical)
+    got, _ = qa.pack_gguf(qtype, qa.OUTPUT_ROWS, k, n, raw.tobytes(), legacy=True)
+    assert got.tobytes() == want.tobytes()
+    # the standard reader on the same bytes decodes something else
+    if qtype == qa.Q4_0:
+        std, _ = qa.pack_gguf(qtype, qa.OUTPUT_ROWS, k, n, raw.tobytes(), legacy=False)
+        assert std.tobytes() != want.tobytes()
+
+
+def test_gguf_upload_errors():
+    blocks = po.make_weights(po.Q8_0, 64, 2, seed=9)
+    wire = po.wire_pack(po.Q8_0, blocks)
+    for bad, what in ((wire[:-1], "byte length"), (wire[:34], "does not match")):
+        with pytest.raises(qa.QiError) as e:
+            qa.pack_gguf(qa.Q8_0, qa.OUTPUT_ROWS, 64, 2, bad)
+        assert e.value.status == qa.INVALID_INPUT
+    inf = wire.copy()
+    inf[34:36] = np.frombuffer(np.float16(np.inf).tobytes(), dtype=np.uint8)
+    with pytest.raises(qa.QiError) as e:
+        qa.pack_gguf(qa.Q8_0, qa.OUTPUT_ROWS, 64, 2, inf)
+    assert e.value.status == qa.INVALID_INPUT and "non-finite" in str(e.value)
+    k4 = po.wire_pack(po.Q4_K, po.make_weights(po.Q4_K, 256, 1, seed=10))
+    k4[2:4] = np.frombuffer(np.float16(np.nan).tobytes(), dtype=np.uint8)  # dmin
+    with pytest.raises(qa.QiError) as e:
+        qa.pack_gguf(qa.Q4_K, qa.OUTPUT_ROWS, 256, 1, k4)
+    assert e.value.status == qa.INVALID_INPUT
+    with pytest.raises(qa.QiError) as e:
+        qa.pack_gguf(9, qa.OUTPUT_ROWS, 256, 1, k4)
+    assert e.value.status == qa.UNSUPPORTED
+    # F32 passes little-endian values through
+    vals = np.arange(12, dtype=np.float32)
+    got, _ = qa.pack_gguf(qa.F32, qa.ROW_MAJOR, 3, 4, vals.tobytes())
+    want, _ = qa.pack_weights(qa.F32, qa.ROW_MAJOR, 3, 4, vals)
+    assert got.tobytes() == want.tobytes()

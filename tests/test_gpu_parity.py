@@ -364,3 +364,23 @@ def test_config_shapes_mfma_tolerance(ctx, cfg):
         comp, norm, cpu = _mfma_checks(y, x, blocks, qtype, n, cpu_rows=rows)
         print(f"mfma {NAMES[qtype]} M={m} K={k} N={n}: comp {comp:.2e} norm {norm:.2e} cpu {cpu:.2e}")
         assert comp <= MFMA_TOL and norm <= MFMA_TOL and cpu <= MFMA_TOL, (m, comp, norm, cpu)
+
+
+# ------------------------------------------------ direct GGUF upload
+@pytest.mark.parametrize("qtype", ALL_Q, ids=lambda q: NAMES[q])
+def test_gguf_upload_same_results(ctx, qtype):
+    """A weight uploaded from GGUF wire bytes (qi_hip_weights_create_gguf)
+    dequantizes bit-exactly and multiplies byte-identically to the one uploaded
+    from the logical blocks."""
+    k, n = 1024, 80
+    blocks = po.make_weights(qtype, k, n, seed=7000 + qtype, outliers=True)
+    wire = po.wire_pack(qtype, blocks)
+    wg = ctx.weights_gguf(qtype, qa.OUTPUT_ROWS, k, n, wire)
+    wl = ctx.weights(qtype, qa.OUTPUT_ROWS, k, n, blocks)
+    assert wg.info().device_bytes == wl.info().device_bytes
+    assert wg.dequantize().tobytes() == po.dequantize(qtype, blocks).tobytes()
+    x = po.fill_normal(7100 + qtype, 3 * k).reshape(3, k)
+    for mode in (qa.MODE_F32, qa.MODE_EXACT, qa.MODE_MFMA):
+        assert wg.linear(x, mode).tobytes() == wl.linear(x, mode).tobytes(), mode
+    wg.free()
+    wl.free()
