@@ -15,7 +15,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libqi_hip.so")
-SOURCES = ["qi_abi.hip", "qi_gemv.hip", "qi_gemv_mfma.hip", "qi_exact.hip", "qi_gemm.hip", "qi_qwen3.hip", "qi_pack.cpp"]
+SOURCES = ["qi_abi.hip", "qi_gemv.hip", "qi_gemv_mfma.hip", "qi_gemv_rm.hip", "qi_exact.hip", "qi_gemm.hip",
+           "qi_qwen3.hip", "qi_pack.cpp"]
 
 ARCH = "gfx950"
 FLAGS = [

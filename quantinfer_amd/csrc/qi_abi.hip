@@ -131,6 +131,28 @@ qi_hip_status run_linear(qi_hip_ctx* c, const qi_hip_weights* w, const float* x,
     QI_HIP_TRY(qi::launch_gemm(im, ga, st), "launch gemm");
     return QI_HIP_OK;
   }
+  if (mode != QI_HIP_MODE_EXACT && qi::gemv_rm_supported(im)) {
+    // row-major weights: the blocks-along-N GEMV, 4 rows per launch
+    const uint32_t chunk = m < 4 ? static_cast<uint32_t>(m) : 4u;
+    const uint32_t splits = qi::gemv_rm_splits(im, chunk);
+    if (splits > 1) {
+      const uint64_t need = static_cast<uint64_t>(splits) * chunk * im.n;
+      if (need > c->scap) {
+        QI_HIP_TRY(hipStreamSynchronize(st), "synchronize before growing the GEMV workspace");
+        qi_hip_status s = grow(&c->sbuf, &c->scap, need, "alloc row-major GEMV workspace");
+        if (s != QI_HIP_OK) return s;
+      }
+    }
+    for (uint64_t m0 = 0; m0 < m; m0 += 4) {
+      const uint32_t rows = static_cast<uint32_t>(m - m0 < 4 ? m - m0 : 4);
+      // a last chunk of one row after 4-row chunks keeps the 4-row split count
+      const uint32_t sp = rows == chunk ? splits : qi::gemv_rm_splits(im, rows);
+      QI_HIP_TRY(qi::launch_gemv_rm(im, v, x + m0 * im.k, rows, y + m0 * im.n, c->sbuf,
+                                    sp <= splits ? sp : splits, st),
+                 "launch row-major gemv");
+    }
+    return QI_HIP_OK;
+  }
   const bool fast = mode != QI_HIP_MODE_EXACT && im.qtype != qi::kF32 &&
                     im.layout == qi::kOutputRows;
   if (!fast) {

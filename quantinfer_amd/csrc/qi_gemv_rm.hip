@@ -1,0 +1,234 @@
+// Row-major (blocks along N) GEMV, F32 mode: y[m, n] = sum_k x[m, k] w(k, n)
+// for QuantInfer-layout weights (backends/cpu/src/backend.rs:62-140 ->
+// matmul.rs:14-90; element values matmul.rs:162-280). The weight image is
+// planar with flat block index k * (N / bs) + nb, so at one k the code bytes
+// of consecutive output blocks are contiguous.
+//
+// A lane owns one column unit: the outputs one 4-byte code word decodes to
+// (Q8_0: 4 outputs; Q4_0 and Q4_K/Q5_K: 8, low and high nibbles; Q6_K: 16 from
+// two ql words and one qh word). 64 consecutive column units per workgroup
+// column, the four wavefronts split the workgroup's K range, and the grid's
+// y dimension splits K further; every k a lane loads its code word(s) and its
+// block's scales (the activations are wavefront-uniform loads), forms the
+// weights in f32 and accumulates x * w for up to MT activation rows.
+// Partials of the K parts are summed in a fixed order: the four wavefronts
+// through LDS, the K splits by rm_sum_kernel. Results are deterministic; the
+// summation order differs from the reference's sequential k, so the mode is
+// judged by tolerance like the output-rows F32 GEMV.
+#include "qi_device.h"
+#include "qi_internal.h"
+
+namespace qi {
+
+namespace {
+
+template <int QT>
+struct RmGeo {
+  static constexpr uint32_t kBs = (QT == kQ8_0 || QT == kQ4_0) ? 32 : 256;   // outputs per block
+  static constexpr int kOut = QT == kQ8_0 ? 4 : QT == kQ6_K ? 16 : 8;        // outputs per lane
+  static constexpr uint32_t kCus = kBs / kOut;                              // column units per block
+};
+
+__device__ __forceinline__ uint32_t load_u32(const uint8_t* p) { return *reinterpret_cast<const uint32_t*>(p); }
+
+// Weights of column unit c of flat block blk: w[j] for the lane's outputs
+// (their positions within the block: rm_offset).
+template <int QT, bool WIDE>
+__device__ __forceinline__ void rm_weights(const View& v, uint64_t blk, uint32_t c, float w[RmGeo<QT>::kOut]) {
+  const float d = load_scale<WIDE>(v.d, blk);
+  if constexpr (QT == kQ8_0) {
+    const uint32_t q = load_u32(v.qs + blk * 32 + 4 * c);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) w[j] = d * static_cast<float>(static_cast<int8_t>(q >> (8 * j)));
+  } else if constexpr (QT == kQ4_0) {
+    const uint32_t q = load_u32(v.qs + blk * 16 + 4 * c);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      w[j] = d * (static_cast<float>((q >> (8 * j)) & 15u) - 8.0f);
+      w[4 + j] = d * (static_cast<float>((q >> (8 * j + 4)) & 15u) - 8.0f);
+    }
+  } else if constexpr (QT == kQ4_K || QT == kQ5_K) {
+    const uint32_t g = c / 8, i = c % 8;
+    const uint32_t q = load_u32(v.qs + blk * 128 + 32 * g + 4 * i);
+    const uint8_t* s = v.sc + blk * 12;
+    uint32_t sc0, m0, sc1, m1;
+    const uint32_t w0 = load_u32(s), w1 = load_u32(s + 4), w2 = load_u32(s + 8);
+    kquant_sc_m(w0, w1, w2, static_cast<int>(2 * g), sc0, m0);
+    kquant_sc_m(w0, w1, w2, static_cast<int>(2 * g + 1), sc1, m1);
+    const float dmin = load_scale<WIDE>(v.dmin, blk);
+    const float a0 = d * static_cast<float>(sc0), b0 = dmin * static_cast<float>(m0);
+    const float a1 = d * static_cast<float>(sc1), b1 = dmin * static_cast<float>(m1);
+    [[maybe_unused]] uint32_t h = 0;
+    if constexpr (QT == kQ5_K) h = load_u32(v.qh + blk * 32 + 4 * i);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      uint32_t lo = (q >> (8 * j)) & 15u, hi = (q >> (8 * j + 4)) & 15u;
+      if constexpr (QT == kQ5_K) {
+        lo += ((h >> (8 * j + 2 * g)) & 1u) << 4;
+        hi += ((h >> (8 * j + 2 * g + 1)) & 1u) << 4;
+      }
+      w[j] = a0 * static_cast<float>(lo) - b0;
+      w[4 + j] = a1 * static_cast<float>(hi) - b1;
+    }
+  } else {  // kQ6_K
+    const uint32_t ip = c / 8, i = c % 8;
+    const uint32_t A = load_u32(v.qs + blk * 128 + 64 * ip + 4 * i);
+    const uint32_t B = load_u32(v.qs + blk * 128 + 64 * ip + 32 + 4 * i);
+    const uint32_t H = load_u32(v.qh + blk * 64 + 32 * ip + 4 * i);
+    const int8_t* s = reinterpret_cast<const int8_t*>(v.sc + blk * 16) + 8 * ip + i / 4;
+#pragma unroll
+    for (int ch = 0; ch < 4; ++ch) {
+      const uint32_t src = (ch & 1) ? B : A;
+      const int sh = ch < 2 ? 0 : 4;
+      const float a = d * static_cast<float>(s[2 * ch]);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t low = (src >> (8 * j + sh)) & 15u;
+        const uint32_t high = (H >> (8 * j + 2 * ch)) & 3u;
+        w[4 * ch + j] = a * static_cast<float>(static_cast<int>(low | (high << 4)) - 32);
+      }
+    }
+  }
+}
+
+// output offset within the block of the lane's output j
+template <int QT>
+__device__ __forceinline__ uint32_t rm_offset(uint32_t c, int j) {
+  if constexpr (QT == kQ8_0) return 4 * c + j;
+  else if constexpr (QT == kQ4_0) return j < 4 ? 4 * c + j : 16 + 4 * c + (j - 4);
+  else if constexpr (QT == kQ4_K || QT == kQ5_K) return 64 * (c / 8) + 4 * (c % 8) + (j < 4 ? j : 32 + j - 4);
+  else return 128 * (c / 8) + 32 * (j / 4) + 4 * (c % 8) + (j % 4);
+}
+
+template <int QT, bool WIDE, int MT>
+__global__ __launch_bounds__(256) void gemv_rm_kernel(View v, const float* __restrict__ x, uint32_t m,
+                                                      uint32_t ksplit, float* __restrict__ out) {
+  using G = RmGeo<QT>;
+  constexpr int OUT = G::kOut;
+  __shared__ float red[3][MT][OUT][64];
+  const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const uint32_t nb_count = static_cast<uint32_t>(v.n / G::kBs);
+  const uint32_t cu = blockIdx.x * 64 + lane;  // global column unit
+  const uint32_t nb = cu / G::kCus, c = cu % G::kCus;
+  const bool live = nb < nb_count;
+  const uint32_t K = static_cast<uint32_t>(v.k);
+  // this workgroup's K range, then this wavefront's quarter of it
+  const uint32_t kb = static_cast<uint32_t>((static_cast<uint64_t>(blockIdx.y) * K) / ksplit);
+  const uint32_t ke = static_cast<uint32_t>((static_cast<uint64_t>(blockIdx.y + 1) * K) / ksplit);
+  const uint32_t k0 = kb + (ke - kb) * wave / 4, k1 = kb + (ke - kb) * (wave + 1) / 4;
+
+  float acc[MT][OUT];
+#pragma unroll
+  for (int r = 0; r < MT; ++r)
+#pragma unroll
+    for (int j = 0; j < OUT; ++j) acc[r][j] = 0.0f;
+  const uint64_t blk_nb = live ? nb : 0;  // lanes past N read block 0 and store nothing
+#pragma unroll 4
+  for (uint32_t k = k0; k < k1; ++k) {
+    float w[OUT];
+    rm_weights<QT, WIDE>(v, static_cast<uint64_t>(k) * nb_count + blk_nb, c, w);
+#pragma unroll
+    for (int r = 0; r < MT; ++r) {
+      const float xv = static_cast<uint32_t>(r) < m ? x[static_cast<uint64_t>(r) * K + k] : 0.0f;
+#pragma unroll
+      for (int j = 0; j < OUT; ++j) acc[r][j] = fmaf(xv, w[j], acc[r][j]);
+    }
+  }
+  // the four K quarters, in order
+  if (wave > 0) {
+#pragma unroll
+    for (int r = 0; r < MT; ++r)
+#pragma unroll
+      for (int j = 0; j < OUT; ++j) red[wave - 1][r][j][lane] = acc[r][j];
+  }
+  __syncthreads();
+  if (wave != 0 || !live) return;
+  float* dst = out + static_cast<uint64_t>(blockIdx.y) * m * v.n;
+#pragma unroll
+  for (int r = 0; r < MT; ++r) {
+    if (static_cast<uint32_t>(r) >= m) break;
+#pragma unroll
+    for (int j = 0; j < OUT; ++j) {
+      const float s = ((acc[r][j] + red[0][r][j][lane]) + red[1][r][j][lane]) + red[2][r][j][lane];
+      dst[static_cast<uint64_t>(r) * v.n + static_cast<uint64_t>(nb) * G::kBs + rm_offset<QT>(c, j)] = s;
+    }
+  }
+}
+
+// y = sum of the K-split partials in split order
+__global__ __launch_bounds__(256) void rm_sum_kernel(const float* __restrict__ part, uint32_t splits,
+                                                     uint64_t count, float* __restrict__ y) {
+  const uint64_t i = static_cast<uint64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= count) return;
+  // loads batched 8 at a time ahead of the in-order adds
+  float s = part[i];
+  uint32_t p = 1;
+  for (; p + 8 <= splits; p += 8) {
+    float t[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) t[j] = part[(p + j) * count + i];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) s += t[j];
+  }
+  for (; p < splits; ++p) s += part[p * count + i];
+  y[i] = s;
+}
+
+template <int QT, bool WIDE>
+hipError_t launch_rm_q(const View& v, const float* x, uint32_t m, float* y, float* part, uint32_t splits,
+                       hipStream_t st) {
+  const uint64_t cus = (v.n / RmGeo<QT>::kBs) * RmGeo<QT>::kCus;
+  float* out = splits > 1 ? part : y;
+  const dim3 grid(static_cast<uint32_t>((cus + 63) / 64), splits);
+  if (m == 1)
+    hipLaunchKernelGGL((gemv_rm_kernel<QT, WIDE, 1>), grid, dim3(256), 0, st, v, x, m, splits, out);
+  else
+    hipLaunchKernelGGL((gemv_rm_kernel<QT, WIDE, 4>), grid, dim3(256), 0, st, v, x, m, splits, out);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || splits == 1) return e;
+  const uint64_t count = static_cast<uint64_t>(m) * v.n;
+  hipLaunchKernelGGL(rm_sum_kernel, dim3(static_cast<uint32_t>((count + 255) / 256)), dim3(256), 0, st, part,
+                     splits, count, y);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+bool gemv_rm_supported(const Image& im) {
+  return im.layout == kRowMajor && !im.tiled && im.qtype >= kQ8_0 && im.qtype <= kQ6_K &&
+         im.n % block_elems(im.qtype) == 0 && im.k > 0;
+}
+
+uint32_t gemv_rm_splits(const Image& im, uint32_t m) {
+  // enough K splits for about 1024 workgroups, keeping at least 16 k per
+  // wavefront (4 wavefronts per workgroup) and at most 256 splits
+  const uint32_t be = block_elems(im.qtype);
+  (void)m;
+  const uint64_t out = im.qtype == kQ8_0 ? 4 : im.qtype == kQ6_K ? 16 : 8;
+  const uint64_t col_groups = ((im.n / be) * (be / out) + 63) / 64;
+  uint64_t s = col_groups >= 1024 ? 1 : 1024 / col_groups;
+  const uint64_t cap = im.k / 64 < 256 ? im.k / 64 : 256;
+  if (s > cap) s = cap;
+  return static_cast<uint32_t>(s < 1 ? 1 : s);
+}
+
+hipError_t launch_gemv_rm(const Image& im, const View& v, const float* x, uint32_t m, float* y, float* part,
+                          uint32_t splits, hipStream_t st) {
+  if (m < 1 || m > 4 || splits < 1 || (splits > 1 && part == nullptr)) return hipErrorInvalidValue;
+  const bool wide = im.wide != 0;
+  switch (im.qtype) {
+    case kQ8_0: return wide ? launch_rm_q<kQ8_0, true>(v, x, m, y, part, splits, st)
+                            : launch_rm_q<kQ8_0, false>(v, x, m, y, part, splits, st);
+    case kQ4_0: return wide ? launch_rm_q<kQ4_0, true>(v, x, m, y, part, splits, st)
+                            : launch_rm_q<kQ4_0, false>(v, x, m, y, part, splits, st);
+    case kQ4_K: return wide ? launch_rm_q<kQ4_K, true>(v, x, m, y, part, splits, st)
+                            : launch_rm_q<kQ4_K, false>(v, x, m, y, part, splits, st);
+    case kQ5_K: return wide ? launch_rm_q<kQ5_K, true>(v, x, m, y, part, splits, st)
+                            : launch_rm_q<kQ5_K, false>(v, x, m, y, part, splits, st);
+    case kQ6_K: return wide ? launch_rm_q<kQ6_K, true>(v, x, m, y, part, splits, st)
+                            : launch_rm_q<kQ6_K, false>(v, x, m, y, part, splits, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace qi

@@ -68,6 +68,14 @@ int gemv_mfma_split(uint64_t k, uint64_t n);
 hipError_t launch_gemv_mfma(int32_t qtype, bool wide, int mt, int split, const GemvMfmaArgs& a,
                             hipStream_t st);
 
+// Row-major (blocks along N) GEMV of up to 4 activation rows, f32
+// accumulation, K split over the grid; `part` holds splits * m * n floats when
+// splits > 1.
+bool gemv_rm_supported(const Image& im);
+uint32_t gemv_rm_splits(const Image& im, uint32_t m);
+hipError_t launch_gemv_rm(const Image& im, const View& v, const float* x, uint32_t m, float* y, float* part,
+                          uint32_t splits, hipStream_t st);
+
 // Exact-order matmul: bit-identical to CpuScalar (any M, either layout).
 hipError_t launch_exact(const Image& im, const View& w, const float* x, uint64_t m, float* y,
                         hipStream_t st);

@@ -115,9 +115,38 @@ def test_exact_mode_row_major_bit_identical(ctx, qtype):
     blocks = po.make_weights(qtype, k, n, seed=2100 + qtype)
     x = po.fill_normal(3100, m * k).reshape(m, k)
     w = ctx.weights(qtype, qa.ROW_MAJOR, k, n, blocks)
-    for mode in (qa.MODE_EXACT, qa.MODE_AUTO, qa.MODE_F32):
-        y = w.linear(x, mode)
-        assert y.tobytes() == po.matmul_row_major(qtype, x, blocks, n).tobytes()
+    y = w.linear(x, qa.MODE_EXACT)
+    assert y.tobytes() == po.matmul_row_major(qtype, x, blocks, n).tobytes()
+
+
+def _assert_f32_row_major(y, x, blocks, qtype, n, what=""):
+    """The F32-mode bars (componentwise vs f64, normwise vs CpuScalar, the
+    reference's bound) for blocks along N: the dequantized values in block
+    order are W row-major [K, N]."""
+    k = x.shape[1]
+    w = po.dequantize(qtype, blocks).reshape(k, n)
+    exact = x.astype(np.float64) @ w.astype(np.float64)
+    cpu = po.matmul_row_major(qtype, x, blocks, n)
+    comp = guarded_rel_err(y, exact, x, w.T)
+    norm = normwise_rel_err(y, cpu)
+    assert comp <= F32_TOL and norm <= F32_TOL and reference_bound_ok(y, exact), (what, comp, norm)
+
+
+@pytest.mark.parametrize("qtype", ALL_Q, ids=lambda q: NAMES[q])
+def test_f32_row_major_gemv_tolerance(ctx, qtype):
+    """Row-major (blocks along N) weights in F32/AUTO mode: the blocks-along-N
+    GEMV (K split over the grid, 4 rows per launch) within the F32 bars, and
+    deterministic."""
+    bs = po.BLOCK_ELEMS[qtype]
+    for k, n in ((96, 4 * bs), (1024, 8 * bs), (4096, 2048 if bs == 32 else 4096)):
+        blocks = po.make_weights(qtype, n, k, seed=2200 + qtype + k, outliers=qtype >= qa.Q4_K)
+        w = ctx.weights(qtype, qa.ROW_MAJOR, k, n, blocks)
+        for m in (1, 3, 6):
+            x = po.fill_normal(3200 + m + k, m * k).reshape(m, k)
+            y = w.linear(x, qa.MODE_F32)
+            _assert_f32_row_major(y, x, blocks, qtype, n, (k, n, m))
+            assert w.linear(x, qa.MODE_AUTO).tobytes() == y.tobytes()
+        w.free()
 
 
 def test_exact_mode_f32_weights_bit_identical(ctx):
