@@ -489,11 +489,12 @@ hipError_t launch_split(const GemvMfmaArgs& a, int sw, hipStream_t st) {
     const uint32_t upw = (chunk + 7) / 8;
     if (upw <= 2) return launch4<QT, WIDE, MT, 8, 2, 1, XS>(a, st);
     if constexpr (MT == 1) {
-      // one workgroup per CU or fewer: two units in flight per wavefront,
-      // reloaded per batch, ran faster than the whole run in flight
-      // (K = 12288, N = 4096: 8.9 against 9.5 us on MI355X); more tiles
-      // than CUs: the whole run in flight (N = 14336: 21.9 against 24.1 us)
-      if (a.w.tiles <= kCUs) return launch4<QT, WIDE, MT, 8, 2, 1, XS>(a, st);
+      // up to two tiles per CU: 16 wavefronts per tile with two units in
+      // flight each, reloaded per batch (K = 12288 on MI355X: N = 4096 8.5 us
+      // against 8.9 for 8 wavefronts x 2 units and 9.2-9.5 for 8 x 8; N = 6144
+      // 14.1 against 15.7); more tiles: 8 wavefronts with the whole run in
+      // flight (N = 14336: 21.9 against 24.1 us for 8 x 2)
+      if (a.w.tiles <= 2 * kCUs) return launch4<QT, WIDE, MT, 16, 2, 1, XS>(a, st);
       if (upw > 4) return launch4<QT, WIDE, MT, 8, 8, 1, XS>(a, st);
     }
     return launch4<QT, WIDE, MT, 8, 4, 1, XS>(a, st);
