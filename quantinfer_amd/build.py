@@ -3,11 +3,18 @@
 Every translation unit is compiled with -ffp-contract=off (a multiply-add is
 fused only where the source calls fmaf) and packed FP32 instructions disabled;
 f32 denormals are kept (no flush-to-zero), as on the CPU reference.
+
+The compiler's per-kernel resource report (registers, scratch, occupancy) is
+written to _build/kernel_resources.json, and a kernel that spills registers
+to scratch memory fails the build: the hot kernels run at one to four
+wavefronts per SIMD with no room for scratch traffic.
 """
 from __future__ import annotations
 
 import concurrent.futures
+import json
 import os
+import re
 import shutil
 import subprocess
 
@@ -34,21 +41,48 @@ def hipcc() -> str:
     return path
 
 
-def _compile(src: str) -> str:
+_REMARK = re.compile(r"remark:\s+(Function Name|VGPRs|AGPRs|ScratchSize \[bytes/lane\]|"
+                     r"Occupancy \[waves/SIMD\]|SGPRs Spill|VGPRs Spill|LDS Size \[bytes/block\]):\s*(\S+)")
+_KEYS = {"VGPRs": "vgpr", "AGPRs": "agpr", "ScratchSize [bytes/lane]": "scratch",
+         "Occupancy [waves/SIMD]": "waves_per_simd", "SGPRs Spill": "sgpr_spill",
+         "VGPRs Spill": "vgpr_spill", "LDS Size [bytes/block]": "lds"}
+
+
+def _resources(stderr: str) -> dict:
+    """Per-kernel figures from -Rpass-analysis=kernel-resource-usage remarks."""
+    out, cur = {}, None
+    for key, val in _REMARK.findall(stderr):
+        if key == "Function Name":
+            cur = out.setdefault(val, {})
+        elif cur is not None:
+            cur[_KEYS[key]] = int(val) if val.isdigit() else val
+    return out
+
+
+def _compile(src: str):
     obj = os.path.join(BUILD, os.path.splitext(src)[0] + ".o")
-    cmd = [hipcc(), *FLAGS, "-c", os.path.join(CSRC, src), "-o", obj]
-    if src.endswith(".cpp"):
-        cmd = [hipcc(), "-x", "hip", *FLAGS, "-c", os.path.join(CSRC, src), "-o", obj]
+    lang = ["-x", "hip"] if src.endswith(".cpp") else []
+    cmd = [hipcc(), *lang, *FLAGS, "-Rpass-analysis=kernel-resource-usage", "-c",
+           os.path.join(CSRC, src), "-o", obj]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{res.stderr}")
-    return obj
+    return obj, _resources(res.stderr)
 
 
 def build(verbose: bool = False) -> str:
     os.makedirs(BUILD, exist_ok=True)
     with concurrent.futures.ThreadPoolExecutor(max_workers=min(8, len(SOURCES))) as ex:
-        objs = list(ex.map(_compile, SOURCES))
+        done = list(ex.map(_compile, SOURCES))
+    objs = [o for o, _ in done]
+    kernels = {name: r for _, res in done for name, r in res.items()}
+    with open(os.path.join(BUILD, "kernel_resources.json"), "w") as f:
+        json.dump(kernels, f, indent=1, sort_keys=True)
+    spills = sorted(n for n, r in kernels.items()
+                    if r.get("scratch", 0) or r.get("vgpr_spill", 0) or r.get("sgpr_spill", 0))
+    if spills:
+        raise RuntimeError("kernels spill registers to scratch memory (see _build/kernel_resources.json): "
+                           + ", ".join(spills))
     tmp = LIB + ".tmp"
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]
     res = subprocess.run(cmd, capture_output=True, text=True)

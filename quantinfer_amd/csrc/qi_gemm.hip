@@ -110,6 +110,44 @@ __device__ __forceinline__ h8 weight_fragment(long codes, float a, float b) {
   }
 }
 
+// (v & mask) | pattern in one instruction: a VOP3 encoding on gfx9 holds no
+// literal and reads at most one scalar register, so the mask comes from a
+// scalar and the pattern from a vector register (the compiler otherwise
+// splits it into an and and an or).
+__device__ __forceinline__ uint32_t and_or(uint32_t v, uint32_t mask, uint32_t pattern) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(v), "s"(mask), "v"(pattern));
+  return r;
+}
+
+// Q4_K fragment straight from the record words (no byte unpacking): the
+// nibble mask and the f16 exponent pattern 0x6400 give 1024 + q per half
+// (low nibbles, steps t < 4) or 1024 + 16 q (high nibbles, t >= 4), and the
+// per-window affine (a, c) has the offset folded in (q4k_affine), so each
+// weight is one f32 fma of the exact f16 code, rounded once to f16.
+// Element order within the fragment is the natural one (bytes 0..7).
+__device__ __forceinline__ h8 q4k_fragment(const Unit<kQ4_K>::Raw& r, int t, float a, float c) {
+  const int tt = t & 3;
+  const uint4 q = r.q[tt >> 1];
+  const uint32_t lo = (tt & 1) ? q.z : q.x, hi = (tt & 1) ? q.w : q.y;
+  const uint32_t mask = t >= 4 ? 0x00F000F0u : 0x000F000Fu;
+  const h2 e0 = __builtin_bit_cast(h2, and_or(lo, mask, 0x64006400u));       // elements 0, 2
+  const h2 e1 = __builtin_bit_cast(h2, and_or(lo >> 8, mask, 0x64006400u));  // 1, 3
+  const h2 e2 = __builtin_bit_cast(h2, and_or(hi, mask, 0x64006400u));       // 4, 6
+  const h2 e3 = __builtin_bit_cast(h2, and_or(hi >> 8, mask, 0x64006400u));  // 5, 7
+  auto w = [&](_Float16 v) { return static_cast<_Float16>(fmaf(a, static_cast<float>(v), c)); };
+  return h8{w(e0[0]), w(e1[0]), w(e0[1]), w(e1[1]), w(e2[0]), w(e3[0]), w(e2[1]), w(e3[1])};
+}
+
+// (a, b) of a Q4_K window -> the (scale, offset) q4k_fragment applies to the
+// biased codes: window 0 (low nibbles, 1024 + q): (a, -(1024 a + b));
+// window 1 (high nibbles, 1024 + 16 q): (a / 16, -(64 a + b)).
+__device__ __forceinline__ void q4k_affine(float sa[2], float sb[2]) {
+  sb[0] = -fmaf(1024.0f, sa[0], sb[0]);
+  sb[1] = -fmaf(64.0f, sa[1], sb[1]);
+  sa[1] = sa[1] * 0.0625f;
+}
+
 // Warp-specialized variant: 8 wavefronts, two roles on every SIMD.
 //   compute wavefronts 0-3 own 128 rows x 64 outputs each (8 x 4 MFMA tiles)
 //     and only read fragments from LDS and issue MFMAs;
@@ -385,6 +423,10 @@ __global__ __launch_bounds__(256) void gemm_reg_kernel(GemmArgs a) {
   b_load(ub + 1);
 #pragma unroll
   for (int ct = 0; ct < 4; ++ct) U::template scales<WIDE>(g, cur[ct], sa[ct], sb[ct]);
+  if constexpr (QT == kQ4_K) {
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct) q4k_affine(sa[ct], sb[ct]);
+  }
 
   for (uint32_t u = ub; u < ue; ++u) {
     // stage s = 4u + q: its activations are in slot q & 1; stages s + 1 ..
@@ -408,7 +450,10 @@ __global__ __launch_bounds__(256) void gemm_reg_kernel(GemmArgs a) {
         for (int rt = 0; rt < RT; ++rt)
           af[rt] = *reinterpret_cast<const h8*>(A + ((tt * 8 + rt0 + rt) * 64 + lane) * 16);
 #pragma unroll
-        for (int ct = 0; ct < 4; ++ct) bf[ct] = weight_fragment<QT>(U::codes(cur[ct], g, t), sa[ct][w], sb[ct][w]);
+        for (int ct = 0; ct < 4; ++ct) {
+          if constexpr (QT == kQ4_K) bf[ct] = q4k_fragment(cur[ct], t, sa[ct][w], sb[ct][w]);
+          else bf[ct] = weight_fragment<QT>(U::codes(cur[ct], g, t), sa[ct][w], sb[ct][w]);
+        }
 #pragma unroll
         for (int ct = 0; ct < 4; ++ct)
 #pragma unroll
@@ -422,6 +467,10 @@ __global__ __launch_bounds__(256) void gemm_reg_kernel(GemmArgs a) {
         for (int ct = 0; ct < 4; ++ct) cur[ct] = nxt[ct];
 #pragma unroll
         for (int ct = 0; ct < 4; ++ct) U::template scales<WIDE>(g, cur[ct], sa[ct], sb[ct]);
+        if constexpr (QT == kQ4_K) {
+#pragma unroll
+          for (int ct = 0; ct < 4; ++ct) q4k_affine(sa[ct], sb[ct]);
+        }
         b_load(u + 2);
       }
     };
@@ -450,6 +499,221 @@ __global__ __launch_bounds__(256) void gemm_reg_kernel(GemmArgs a) {
   }
 }
 
+// s_waitcnt with vmcnt <= n (0..63) and lgkmcnt 0 (gfx9 encoding: vmcnt in
+// bits 3:0 and 15:14, expcnt 6:4 left at its maximum, lgkmcnt 11:8).
+template <int N>
+__device__ __forceinline__ void wait_vm_lgkm0() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | ((N >> 4) << 14));
+}
+
+// Q4_K (f16 scales) with both operands staged in LDS by direct global-to-LDS
+// loads, so no register holds data in flight and every vector-memory
+// instruction of the main loop is one of these copies, a known number per
+// stage, which lets a stage wait for exactly the copy it needs:
+//   activations: 2-step stages (16 KB, fragment order) in a ring of 4 LDS
+//     slots, stage s + 3 requested at the top of stage s (4 copies of 1 KB
+//     per wavefront);
+//   weights: each wavefront copies its 4 tiles' records of unit u + 1
+//     (4 x 2304 B, 12 copies) into the other of its two LDS buffers at the
+//     top of unit u, and reads its code words and scales from there when the
+//     unit becomes current.
+// Waits at the top of stage s = 4u + q (copies issued after the one needed
+// stay in flight): q = 0: the stage's activations, 8 younger copies
+// (stages s + 1, s + 2); q = 1, 2: 20 (two stages and the unit's weights);
+// q = 3: the next unit's weights, 8 younger copies. The raw s_barrier (no
+// fence) keeps the other copies in flight; the wait before it also drains
+// this wavefront's LDS reads, so the slot the new copy overwrites is free.
+// Tiling, arithmetic and split-K as gemm_reg_kernel. Each step dequantizes
+// its fragments before its matrix instructions (dequantizing one step ahead
+// measured slower here: the second fragment set costs registers).
+constexpr uint32_t kLdsSlots = 4, kLdsStage = 2 * 8 * 64 * 16;
+constexpr uint32_t kQ4kRec = record_geometry(kQ4_K, false).bytes;
+constexpr uint32_t kQ4kSc = record_geometry(kQ4_K, false).sc, kQ4kD = record_geometry(kQ4_K, false).d;
+static_assert(kQ4kRec == 2304 && kQ4kSc == 2048 && kQ4kD == 2240 &&
+                  record_geometry(kQ4_K, false).dmin == kQ4kD + 32,
+              "the record reads below hard-code the Q4_K record layout (offsets, tile stride 2304)");
+constexpr uint32_t kLdsQ4kBytes = kLdsSlots * kLdsStage + 4 * 2 * 4 * kQ4kRec;
+
+__global__ __launch_bounds__(256) void gemm_lds_q4k_kernel(GemmArgs a) {
+  using U = Unit<kQ4_K>;
+  static_assert(kQ4kRec == 2304, "the record copy below is 2 x 1 KB + 256 B");
+  constexpr int RT = 8;
+  constexpr uint32_t kWBuf = 4 * kQ4kRec;  // one wavefront's 4 records of a unit
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  uint8_t* const abuf = lds;
+
+  const uint32_t tid = threadIdx.x, lane = tid & 63;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar addressing
+  const uint32_t g = lane >> 4, c16 = lane & 15;
+  uint8_t* const wbuf = lds + kLdsSlots * kLdsStage + wave * 2 * kWBuf;
+  const uint32_t units = a.w.units;
+  const uint32_t ub = blockIdx.z * units / a.splits, ue = (blockIdx.z + 1) * units / a.splits;
+  const uint64_t m0 = static_cast<uint64_t>(blockIdx.y) * kTileM;
+  const uint32_t stages = 4 * ue;
+  const u32x4* xa = reinterpret_cast<const u32x4*>(a.xh) + static_cast<uint64_t>(blockIdx.y) * units * 4096;
+
+  const uint8_t* trec[4];
+#pragma unroll
+  for (int ct = 0; ct < 4; ++ct) {
+    const uint32_t t = min((blockIdx.x * 4 + wave) * 4 + ct, a.w.tiles - 1);
+    trec[ct] = a.w.qs + static_cast<uint64_t>(t) * units * kQ4kRec;
+  }
+
+  typedef __attribute__((address_space(3))) void* lds_ptr;
+  // stage st's activations (clamped to the last stage) into slot st % 4
+  auto copy_stage = [&](uint32_t st) {
+    const uint32_t sl = st < stages ? st : stages - 1;
+    uint8_t* dst = abuf + (st % kLdsSlots) * kLdsStage;
+    // uniform base plus a 32-bit lane offset: the scalar-base addressing form
+    const uint8_t* src = reinterpret_cast<const uint8_t*>(xa + static_cast<uint64_t>(sl) * 1024);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      __builtin_amdgcn_global_load_lds(src + static_cast<uint32_t>((tid + 256 * i) * 16),
+                                       (lds_ptr)(dst + (256 * i + 64 * wave) * 16), 16, 0, 0);
+  };
+  // this wavefront's records of unit u (clamped) into its buffer (u - ub) & 1
+  auto copy_unit = [&](uint32_t u) {
+    const uint32_t ul = u < ue ? u : ue - 1;
+    uint8_t* dst = wbuf + ((u - ub) & 1) * kWBuf;
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct) {
+      const uint8_t* src = trec[ct] + static_cast<uint64_t>(ul) * kQ4kRec;
+      __builtin_amdgcn_global_load_lds(src + static_cast<uint32_t>(lane * 16), (lds_ptr)(dst + ct * kQ4kRec), 16,
+                                       0, 0);
+      __builtin_amdgcn_global_load_lds(src + static_cast<uint32_t>(1024 + lane * 16),
+                                       (lds_ptr)(dst + ct * kQ4kRec + 1024), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(src + static_cast<uint32_t>(2048 + lane * 4),
+                                       (lds_ptr)(dst + ct * kQ4kRec + 2048), 4, 0, 0);
+    }
+  };
+
+  typename U::Raw cur[4];
+  float sa[4][U::kWindows], sb[4][U::kWindows];
+  // The records are read by inline assembly: the compiler tracks all
+  // global-to-LDS copies as one group and would otherwise wait for every copy
+  // in flight (the prefetched activation stages too) before these reads. The
+  // copy they need was waited for at the top of the stage; the closing wait
+  // passes every result through, so no use can move above it.
+  auto take_unit = [&](uint32_t u) {
+    typedef __attribute__((address_space(3))) uint8_t* lds_u8;
+    const uint32_t base = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_u8)wbuf)) + ((u - ub) & 1) * kWBuf;
+    const uint32_t aq = base + lane * 16, asc = base + kQ4kSc + c16 * 12, ad = base + kQ4kD + c16 * 2;
+    u32x4 q0[4], q1[4];
+    uint32_t sc0[4], sc1[4], sc2[4], d0[4], d1[4];
+#define QI_Q4K_TILE_READ(CT)                                                                        \
+  asm volatile("ds_read_b128 %0, %7 offset:" #CT "*2304\n\t"                                      \
+               "ds_read_b128 %1, %7 offset:" #CT "*2304+1024\n\t"                                 \
+               "ds_read_b32 %2, %8 offset:" #CT "*2304\n\t"                                       \
+               "ds_read_b32 %3, %8 offset:" #CT "*2304+4\n\t"                                     \
+               "ds_read_b32 %4, %8 offset:" #CT "*2304+8\n\t"                                     \
+               "ds_read_u16 %5, %9 offset:" #CT "*2304\n\t"                                       \
+               "ds_read_u16 %6, %9 offset:" #CT "*2304+32"                                         \
+               : "=&v"(q0[CT]), "=&v"(q1[CT]), "=&v"(sc0[CT]), "=&v"(sc1[CT]), "=&v"(sc2[CT]),    \
+                 "=&v"(d0[CT]), "=&v"(d1[CT])                                                     \
+               : "v"(aq), "v"(asc), "v"(ad))
+    QI_Q4K_TILE_READ(0);
+    QI_Q4K_TILE_READ(1);
+    QI_Q4K_TILE_READ(2);
+    QI_Q4K_TILE_READ(3);
+#undef QI_Q4K_TILE_READ
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(q0[0]), "+v"(q1[0]), "+v"(sc0[0]), "+v"(sc1[0]), "+v"(sc2[0]), "+v"(d0[0]), "+v"(d1[0]),
+                   "+v"(q0[1]), "+v"(q1[1]), "+v"(sc0[1]), "+v"(sc1[1]), "+v"(sc2[1]), "+v"(d0[1]), "+v"(d1[1]),
+                   "+v"(q0[2]), "+v"(q1[2]), "+v"(sc0[2]), "+v"(sc1[2]), "+v"(sc2[2]), "+v"(d0[2]), "+v"(d1[2]),
+                   "+v"(q0[3]), "+v"(q1[3]), "+v"(sc0[3]), "+v"(sc1[3]), "+v"(sc2[3]), "+v"(d0[3]), "+v"(d1[3]));
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct) {
+      cur[ct].q[0] = __builtin_bit_cast(uint4, q0[ct]);
+      cur[ct].q[1] = __builtin_bit_cast(uint4, q1[ct]);
+      cur[ct].sc[0] = sc0[ct];
+      cur[ct].sc[1] = sc1[ct];
+      cur[ct].sc[2] = sc2[ct];
+      cur[ct].s0 = d0[ct];
+      cur[ct].s1 = d1[ct];
+    }
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct) {
+      U::template scales<false>(g, cur[ct], sa[ct], sb[ct]);
+      q4k_affine(sa[ct], sb[ct]);
+    }
+  };
+  auto frags = [&](auto tc, h8 out[4]) {
+    constexpr int t = decltype(tc)::value, w = t / U::kSteps;
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct) out[ct] = q4k_fragment(cur[ct], t, sa[ct][w], sb[ct][w]);
+  };
+
+  f4 acc[RT][4];
+#pragma unroll
+  for (int i = 0; i < RT; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f4{0, 0, 0, 0};
+
+  // prologue: stages 4 ub .. 4 ub + 2 and unit ub, all complete
+  copy_stage(4 * ub);
+  copy_stage(4 * ub + 1);
+  copy_stage(4 * ub + 2);
+  copy_unit(ub);
+  wait_vm_lgkm0<0>();
+  __builtin_amdgcn_s_barrier();
+  take_unit(ub);
+
+  for (uint32_t u = ub; u < ue; ++u) {
+    auto step = [&](auto qc) {
+      constexpr int q = decltype(qc)::value;
+      const uint32_t s = 4 * u + q;
+      if constexpr (q == 1 || q == 2) wait_vm_lgkm0<20>();
+      else wait_vm_lgkm0<8>();
+      __builtin_amdgcn_s_barrier();
+      copy_stage(s + 3);
+      if constexpr (q == 0) copy_unit(u + 1);
+      const uint8_t* A = abuf + (s % kLdsSlots) * kLdsStage;
+      auto sub = [&](auto ttc) {
+        constexpr int tt = decltype(ttc)::value, t = 2 * q + tt;
+        h8 af[RT], bf[4];
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt)
+          af[rt] = *reinterpret_cast<const h8*>(A + ((tt * 8 + rt) * 64 + lane) * 16);
+        frags(std::integral_constant<int, t>{}, bf);
+#pragma unroll
+        for (int ct = 0; ct < 4; ++ct)
+#pragma unroll
+          for (int rt = 0; rt < RT; ++rt)
+            acc[rt][ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[rt], bf[ct], acc[rt][ct], 0, 0, 0);
+        // the next unit's records (waited for at the top of this stage)
+        if constexpr (t == 7) take_unit(u + 1);
+      };
+      sub(std::integral_constant<int, 0>{});
+      sub(std::integral_constant<int, 1>{});
+    };
+    step(std::integral_constant<int, 0>{});
+    step(std::integral_constant<int, 1>{});
+    step(std::integral_constant<int, 2>{});
+    step(std::integral_constant<int, 3>{});
+  }
+  // the clamped copies past the last stage and unit must land before the
+  // workgroup's LDS is released
+  wait_vm_lgkm0<0>();
+
+  const uint64_t ld = a.w.n;
+  float* const out = a.splits > 1 ? a.part + static_cast<uint64_t>(blockIdx.z) * a.m_pad * ld : a.y;
+  float* yrow = out + (m0 + 4 * g) * ld;
+#pragma unroll
+  for (int ct = 0; ct < 4; ++ct) {
+    const uint64_t n = static_cast<uint64_t>((blockIdx.x * 4 + wave) * 4 + ct) * 16 + c16;
+    if (n >= a.w.n) continue;
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const uint64_t m = m0 + 16 * rt + 4 * g + r;
+        if (m < a.m) yrow[(rt * 16 + r) * ld + n] = acc[rt][ct][r];
+      }
+    }
+  }
+}
+
 // y = sum of the split-K partial products, in split order (deterministic).
 __global__ __launch_bounds__(256) void gemm_splitk_sum_kernel(const float* __restrict__ part, uint32_t splits,
                                                               uint64_t count, uint64_t stride,
@@ -472,6 +736,23 @@ hipError_t launch_reg(const Image& im, const GemmArgs& a, hipStream_t st) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || a.splits == 1) return e;
   // rows of y and of each partial block share the row stride n
+  const uint64_t count = a.m * im.n;
+  hipLaunchKernelGGL(gemm_splitk_sum_kernel, dim3(static_cast<uint32_t>((count + 255) / 256)), dim3(256), 0, st,
+                     a.part, a.splits, count, a.m_pad * im.n, a.y);
+  return hipGetLastError();
+}
+
+hipError_t launch_lds_q4k(const Image& im, const GemmArgs& a, hipStream_t st) {
+  const uint32_t nblk = static_cast<uint32_t>((im.tiles + 15) / 16);
+  const uint32_t mblk = static_cast<uint32_t>(a.m_pad / kTileM);
+  if (a.splits < 1 || a.splits > im.k / 256 || (a.splits > 1 && a.part == nullptr)) return hipErrorInvalidValue;
+  auto kern = gemm_lds_q4k_kernel;
+  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kLdsQ4kBytes));
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(kern, dim3(nblk, mblk, a.splits), dim3(256), kLdsQ4kBytes, st, a);
+  e = hipGetLastError();
+  if (e != hipSuccess || a.splits == 1) return e;
   const uint64_t count = a.m * im.n;
   hipLaunchKernelGGL(gemm_splitk_sum_kernel, dim3(static_cast<uint32_t>((count + 255) / 256)), dim3(256), 0, st,
                      a.part, a.splits, count, a.m_pad * im.n, a.y);
@@ -509,6 +790,12 @@ hipError_t launch_q(const Image& im, const GemmArgs& a, hipStream_t st) {
                        static_cast<uint32_t>(im.k), pieces, a.xh);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
+    // Q4_K with f16 scales: both operands staged in LDS (faster on MI355X:
+    // 743 against 681 TFLOP/s at 2048 x 4096 x 12288); QI_HIP_GEMM_REG=1
+    // selects the register-weight kernel instead
+    if constexpr (QT == kQ4_K) {
+      if (!im.wide && getenv("QI_HIP_GEMM_REG") == nullptr) return launch_lds_q4k(im, a, st);
+    }
     return im.wide ? launch_reg<QT, true>(im, a, st) : launch_reg<QT, false>(im, a, st);
   }
 }

@@ -495,7 +495,11 @@ hipError_t launch_split(const GemvMfmaArgs& a, int sw, hipStream_t st) {
       // 14.1 against 15.7); more tiles: 8 wavefronts with the whole run in
       // flight (N = 14336: 21.9 against 24.1 us for 8 x 2)
       if (a.w.tiles <= 2 * kCUs) return launch4<QT, WIDE, MT, 16, 2, 1, XS>(a, st);
-      if (upw > 4) return launch4<QT, WIDE, MT, 8, 8, 1, XS>(a, st);
+      // (Q5_K and Q6_K with the norm prep spill registers at 8 units deep)
+      constexpr bool deep = XS != kXNorm || (QT != kQ5_K && QT != kQ6_K);
+      if constexpr (deep) {
+        if (upw > 4) return launch4<QT, WIDE, MT, 8, 8, 1, XS>(a, st);
+      }
     }
     return launch4<QT, WIDE, MT, 8, 4, 1, XS>(a, st);
   }

@@ -153,7 +153,7 @@ struct UnitQ45K {
     // bytes: one byte permute from the word pair that holds it
     const uint32_t lo = g < 2 ? r.sc[0] : r.sc[1];
     const uint32_t hi = g < 2 ? r.sc[1] : r.sc[2];
-    const uint32_t first = g == 0 ? 0 : g == 1 ? 3 : g == 2 ? 2 : 5;
+    const uint32_t first = (0x5230u >> (4 * g)) & 15u;  // g = 0..3: bytes 0, 3, 2, 5 (no branch)
     const uint32_t f = __builtin_amdgcn_perm(hi, lo, first * 0x00010101u + 0x0C020100u);
     a[0] = d * static_cast<float>(f & 63u);
     b[0] = dmin * static_cast<float>((f >> 6) & 63u);
