@@ -7,9 +7,11 @@
 // scale; the K-quants from the reference's own f32 value (d * sc) * q -
 // dmin * m (Q6_K (d * sc) * (q - 32)), so no rounding is shared by the 32
 // weights of a sub-block (rounding d * sc or dmin * m to f16 would be, and
-// cancels badly in blocks whose range an outlier stretched). Products
-// accumulate in f32 on the matrix cores. This is the tolerance-judged MFMA
-// mode (f16 operands, f32 accumulation).
+// cancels badly in blocks whose range an outlier stretched). Q4_K computes
+// that value as a * (1024 + q) + c with c = -(1024 a + b) rounded once to f32
+// per window (q4k_affine), an extra error below 2^-14 a, far under the f16
+// rounding of the weight. Products accumulate in f32 on the matrix cores.
+// This is the tolerance-judged MFMA mode (f16 operands, f32 accumulation).
 //
 // Tiling. A workgroup of 8 wavefronts owns 128 activation rows x 256
 // outputs, split by role (gemm_ws_kernel): 4 compute wavefronts each own all
