@@ -318,28 +318,50 @@ __global__ __launch_bounds__(512) void gemm_ws_kernel(GemmArgs a) {
 // window_first(l >> 4, t / 4) + 8 (t % 4) + [0, 8) of unit u, the order the
 // weight fragments of step t use. A 2-step stage is 16 KB contiguous. Rows
 // past m are zero.
+// One workgroup per (128-row tile mt, unit u, 32-row quarter rq): rows
+// mt * 128 + 32 rq + [0, 32) of unit u. Loads take 64 contiguous bytes of
+// each of 16 rows per wavefront instruction; the f16 values are placed in
+// fragment order in LDS (two-way bank conflicts at most) and leave as 1 KB
+// contiguous runs: the 16 KB of (mt, u, steps 0-7, row tiles 2 rq, 2 rq + 1).
+// Not for Q6_K, whose windows interleave differently (gemm_ws_kernel reads
+// plain f16 rows).
 template <int QT>
-__global__ __launch_bounds__(256) void x_to_frag_kernel(const float* __restrict__ x, uint64_t m,
-                                                        uint32_t K, uint64_t pieces,
+__global__ __launch_bounds__(256) void x_to_frag_kernel(const float* __restrict__ x, uint64_t m, uint32_t K,
                                                         _Float16* __restrict__ xa) {
-  const uint64_t p = static_cast<uint64_t>(blockIdx.x) * 256 + threadIdx.x;
-  if (p >= pieces) return;
-  const uint32_t lane = p & 63, rt = (p >> 6) & 7, t = (p >> 9) & 7;
-  const uint64_t rest = p >> 12;  // mt * units + u
-  const uint32_t units = K / 256;
+  static_assert(QT != kQ6_K, "Q6_K activations use x_to_f16_kernel");
+  __shared__ __attribute__((aligned(16))) uint8_t tile[16384];  // [t][rt2][lane] x 16 B
+  const uint32_t units = K / 256, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const uint32_t r = lane & 15, c = lane >> 4;
+  const uint32_t rq = blockIdx.x & 3;
+  const uint64_t rest = blockIdx.x >> 2;  // mt * units + u
   const uint64_t mt = rest / units;
   const uint32_t u = static_cast<uint32_t>(rest % units);
-  const uint64_t row = mt * kTileM + 16 * rt + (lane & 15);
-  const uint32_t k = 256 * u + window_first<QT>(lane >> 4, t >> 2) + 8 * (t & 3);
-  h8 o = h8{0, 0, 0, 0, 0, 0, 0, 0};
-  if (row < m) {
-    const float4* src = reinterpret_cast<const float4*>(x + row * K + k);
-    const float4 v0 = src[0], v1 = src[1];
-    o = h8{static_cast<_Float16>(v0.x), static_cast<_Float16>(v0.y), static_cast<_Float16>(v0.z),
-           static_cast<_Float16>(v0.w), static_cast<_Float16>(v1.x), static_cast<_Float16>(v1.y),
-           static_cast<_Float16>(v1.z), static_cast<_Float16>(v1.w)};
+  const float4* x4 = reinterpret_cast<const float4*>(x);
+  float4 v[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const uint32_t I = 4 * j + w, rt2 = I >> 4, cblk = I & 15;
+    const uint64_t row = mt * kTileM + 32 * rq + 16 * rt2 + r;
+    v[j] = row < m ? x4[(row * K + 256 * u) / 4 + 4 * cblk + c] : float4{0, 0, 0, 0};
   }
-  *reinterpret_cast<h8*>(xa + p * 8) = o;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const uint32_t I = 4 * j + w, rt2 = I >> 4, cblk = I & 15;
+    // element k = 16 cblk + 4 c of the unit: window (g, h) = (k / 64, k / 32 % 2),
+    // step t = 4 h + k / 8 % 4, half k / 4 % 2 of the 8-element piece
+    const uint32_t g = cblk >> 2, h = (cblk >> 1) & 1, t = 4 * h + (((cblk & 1) << 1) | (c >> 1));
+    const uint32_t off = ((t * 2 + rt2) * 64 + 16 * g + r) * 16 + (c & 1) * 8;
+    typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+    *reinterpret_cast<h4*>(tile + off) = h4{static_cast<_Float16>(v[j].x), static_cast<_Float16>(v[j].y),
+                                            static_cast<_Float16>(v[j].z), static_cast<_Float16>(v[j].w)};
+  }
+  __syncthreads();
+  u32x4* out = reinterpret_cast<u32x4*>(xa) + rest * 4096;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t q = 256 * i + tid, t = q >> 7, rt2 = (q >> 6) & 1, l = q & 63;
+    out[(t * 8 + 2 * rq + rt2) * 64 + l] = reinterpret_cast<const u32x4*>(tile)[q];
+  }
 }
 
 // Weights in registers: the workgroup's 128 x 256 block is split over 4
@@ -786,10 +808,9 @@ hipError_t launch_q(const Image& im, const GemmArgs& a, hipStream_t st) {
     return im.wide ? launch_ws<QT, true>(im, a, st) : launch_ws<QT, false>(im, a, st);
   } else {
     // activations in fragment order, then the register-weight kernel
-    const uint64_t pieces = a.m_pad * im.k / 8;
-    const uint32_t blocks = static_cast<uint32_t>((pieces + 255) / 256);
+    const uint32_t blocks = static_cast<uint32_t>(a.m_pad / kTileM * (im.k / 256) * 4);
     hipLaunchKernelGGL((x_to_frag_kernel<QT>), dim3(blocks), dim3(256), 0, st, a.x, a.m,
-                       static_cast<uint32_t>(im.k), pieces, a.xh);
+                       static_cast<uint32_t>(im.k), a.xh);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     // Q4_K with f16 scales: both operands staged in LDS (faster on MI355X:
