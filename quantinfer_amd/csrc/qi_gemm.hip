@@ -531,110 +531,66 @@ __device__ __forceinline__ void wait_vm_lgkm0() {
   __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | ((N >> 4) << 14));
 }
 
-// Q4_K (f16 scales) with both operands staged in LDS by direct global-to-LDS
-// loads, so no register holds data in flight and every vector-memory
-// instruction of the main loop is one of these copies, a known number per
-// stage, which lets a stage wait for exactly the copy it needs:
+// Q4_K and Q5_K (f16 scales) with both operands staged in LDS by direct
+// global-to-LDS loads, so no register holds data in flight and every
+// vector-memory instruction of the main loop is one of these copies, a known
+// number per stage, which lets a stage wait for exactly the copy it needs:
 //   activations: 2-step stages (16 KB, fragment order) in a ring of 4 LDS
 //     slots, stage s + 3 requested at the top of stage s (4 copies of 1 KB
 //     per wavefront);
 //   weights: each wavefront copies its 4 tiles' records of unit u + 1
-//     (4 x 2304 B, 12 copies) into the other of its two LDS buffers at the
-//     top of unit u, and reads its code words and scales from there when the
-//     unit becomes current.
+//     (LdsRec<QT>::kCopies instructions per record) into the other of its two
+//     LDS buffers at the top of unit u, and reads its code words and scales
+//     from there when the unit becomes current.
 // Waits at the top of stage s = 4u + q (copies issued after the one needed
 // stay in flight): q = 0: the stage's activations, 8 younger copies
-// (stages s + 1, s + 2); q = 1, 2: 20 (two stages and the unit's weights);
-// q = 3: the next unit's weights, 8 younger copies. The raw s_barrier (no
-// fence) keeps the other copies in flight; the wait before it also drains
-// this wavefront's LDS reads, so the slot the new copy overwrites is free.
+// (stages s + 1, s + 2); q = 1, 2: 8 + the unit's record copies; q = 3: the
+// next unit's records, 8 younger copies. The raw s_barrier (no fence) keeps
+// the other copies in flight; the wait before it also drains this
+// wavefront's LDS reads, so the slot the new copy overwrites is free.
 // Tiling, arithmetic and split-K as gemm_reg_kernel. Each step dequantizes
 // its fragments before its matrix instructions (dequantizing one step ahead
 // measured slower here: the second fragment set costs registers).
 constexpr uint32_t kLdsSlots = 4, kLdsStage = 2 * 8 * 64 * 16;
-constexpr uint32_t kQ4kRec = record_geometry(kQ4_K, false).bytes;
-constexpr uint32_t kQ4kSc = record_geometry(kQ4_K, false).sc, kQ4kD = record_geometry(kQ4_K, false).d;
-static_assert(kQ4kRec == 2304 && kQ4kSc == 2048 && kQ4kD == 2240 &&
-                  record_geometry(kQ4_K, false).dmin == kQ4kD + 32,
-              "the record reads below hard-code the Q4_K record layout (offsets, tile stride 2304)");
-constexpr uint32_t kLdsQ4kBytes = kLdsSlots * kLdsStage + 4 * 2 * 4 * kQ4kRec;
 
-__global__ __launch_bounds__(256) void gemm_lds_q4k_kernel(GemmArgs a) {
-  using U = Unit<kQ4_K>;
-  static_assert(kQ4kRec == 2304, "the record copy below is 2 x 1 KB + 256 B");
-  constexpr int RT = 8;
-  constexpr uint32_t kWBuf = 4 * kQ4kRec;  // one wavefront's 4 records of a unit
-  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-  uint8_t* const abuf = lds;
+typedef __attribute__((address_space(3))) void* lds_ptr;
 
-  const uint32_t tid = threadIdx.x, lane = tid & 63;
-  const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar addressing
-  const uint32_t g = lane >> 4, c16 = lane & 15;
-  uint8_t* const wbuf = lds + kLdsSlots * kLdsStage + wave * 2 * kWBuf;
-  const uint32_t units = a.w.units;
-  const uint32_t ub = blockIdx.z * units / a.splits, ue = (blockIdx.z + 1) * units / a.splits;
-  const uint64_t m0 = static_cast<uint64_t>(blockIdx.y) * kTileM;
-  const uint32_t stages = 4 * ue;
-  const u32x4* xa = reinterpret_cast<const u32x4*>(a.xh) + static_cast<uint64_t>(blockIdx.y) * units * 4096;
+template <int QT>
+struct LdsRec;  // record copy into LDS and read-back for gemm_lds_kernel
 
-  const uint8_t* trec[4];
-#pragma unroll
-  for (int ct = 0; ct < 4; ++ct) {
-    const uint32_t t = min((blockIdx.x * 4 + wave) * 4 + ct, a.w.tiles - 1);
-    trec[ct] = a.w.qs + static_cast<uint64_t>(t) * units * kQ4kRec;
+// The record reads use inline assembly: the compiler tracks all global-to-LDS
+// copies as one group and would otherwise wait for every copy in flight (the
+// prefetched activation stages too) before them. The copy they need was
+// waited for at the top of the stage; the closing wait passes every result
+// through, so no use can move above it. Tile CT's record sits at CT * kBytes.
+template <>
+struct LdsRec<kQ4_K> {
+  static constexpr Record R = record_geometry(kQ4_K, false);
+  static constexpr uint32_t kBytes = R.bytes, kCopies = 3;
+  static_assert(kBytes == 2304 && R.sc == 2048 && R.d == 2240 && R.dmin == 2272,
+                "the copies and reads below hard-code the Q4_K record layout");
+  // 2 x 1 KB + 256 B (64 lanes x 4 B)
+  __device__ static void copy(const uint8_t* src, uint8_t* dst, uint32_t lane) {
+    __builtin_amdgcn_global_load_lds(src + static_cast<uint32_t>(lane * 16), (lds_ptr)dst, 16, 0, 0);
+    __builtin_amdgcn_global_load_lds(src + static_cast<uint32_t>(1024 + lane * 16), (lds_ptr)(dst + 1024), 16, 0,
+                                     0);
+    __builtin_amdgcn_global_load_lds(src + static_cast<uint32_t>(2048 + lane * 4), (lds_ptr)(dst + 2048), 4, 0, 0);
   }
-
-  typedef __attribute__((address_space(3))) void* lds_ptr;
-  // stage st's activations (clamped to the last stage) into slot st % 4
-  auto copy_stage = [&](uint32_t st) {
-    const uint32_t sl = st < stages ? st : stages - 1;
-    uint8_t* dst = abuf + (st % kLdsSlots) * kLdsStage;
-    // uniform base plus a 32-bit lane offset: the scalar-base addressing form
-    const uint8_t* src = reinterpret_cast<const uint8_t*>(xa + static_cast<uint64_t>(sl) * 1024);
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      __builtin_amdgcn_global_load_lds(src + static_cast<uint32_t>((tid + 256 * i) * 16),
-                                       (lds_ptr)(dst + (256 * i + 64 * wave) * 16), 16, 0, 0);
-  };
-  // this wavefront's records of unit u (clamped) into its buffer (u - ub) & 1
-  auto copy_unit = [&](uint32_t u) {
-    const uint32_t ul = u < ue ? u : ue - 1;
-    uint8_t* dst = wbuf + ((u - ub) & 1) * kWBuf;
-#pragma unroll
-    for (int ct = 0; ct < 4; ++ct) {
-      const uint8_t* src = trec[ct] + static_cast<uint64_t>(ul) * kQ4kRec;
-      __builtin_amdgcn_global_load_lds(src + static_cast<uint32_t>(lane * 16), (lds_ptr)(dst + ct * kQ4kRec), 16,
-                                       0, 0);
-      __builtin_amdgcn_global_load_lds(src + static_cast<uint32_t>(1024 + lane * 16),
-                                       (lds_ptr)(dst + ct * kQ4kRec + 1024), 16, 0, 0);
-      __builtin_amdgcn_global_load_lds(src + static_cast<uint32_t>(2048 + lane * 4),
-                                       (lds_ptr)(dst + ct * kQ4kRec + 2048), 4, 0, 0);
-    }
-  };
-
-  typename U::Raw cur[4];
-  float sa[4][U::kWindows], sb[4][U::kWindows];
-  // The records are read by inline assembly: the compiler tracks all
-  // global-to-LDS copies as one group and would otherwise wait for every copy
-  // in flight (the prefetched activation stages too) before these reads. The
-  // copy they need was waited for at the top of the stage; the closing wait
-  // passes every result through, so no use can move above it.
-  auto take_unit = [&](uint32_t u) {
-    typedef __attribute__((address_space(3))) uint8_t* lds_u8;
-    const uint32_t base = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_u8)wbuf)) + ((u - ub) & 1) * kWBuf;
-    const uint32_t aq = base + lane * 16, asc = base + kQ4kSc + c16 * 12, ad = base + kQ4kD + c16 * 2;
+  __device__ static void read(uint32_t base, uint32_t lane, Unit<kQ4_K>::Raw cur[4]) {
+    const uint32_t c16 = lane & 15;
+    const uint32_t aq = base + lane * 16, asc = base + R.sc + c16 * 12, ad = base + R.d + c16 * 2;
     u32x4 q0[4], q1[4];
     uint32_t sc0[4], sc1[4], sc2[4], d0[4], d1[4];
-#define QI_Q4K_TILE_READ(CT)                                                                        \
-  asm volatile("ds_read_b128 %0, %7 offset:" #CT "*2304\n\t"                                      \
-               "ds_read_b128 %1, %7 offset:" #CT "*2304+1024\n\t"                                 \
-               "ds_read_b32 %2, %8 offset:" #CT "*2304\n\t"                                       \
-               "ds_read_b32 %3, %8 offset:" #CT "*2304+4\n\t"                                     \
-               "ds_read_b32 %4, %8 offset:" #CT "*2304+8\n\t"                                     \
-               "ds_read_u16 %5, %9 offset:" #CT "*2304\n\t"                                       \
-               "ds_read_u16 %6, %9 offset:" #CT "*2304+32"                                         \
-               : "=&v"(q0[CT]), "=&v"(q1[CT]), "=&v"(sc0[CT]), "=&v"(sc1[CT]), "=&v"(sc2[CT]),    \
-                 "=&v"(d0[CT]), "=&v"(d1[CT])                                                     \
+#define QI_Q4K_TILE_READ(CT)                                                                         \
+  asm volatile("ds_read_b128 %0, %7 offset:" #CT "*2304\n\t"                                       \
+               "ds_read_b128 %1, %7 offset:" #CT "*2304+1024\n\t"                                  \
+               "ds_read_b32 %2, %8 offset:" #CT "*2304\n\t"                                        \
+               "ds_read_b32 %3, %8 offset:" #CT "*2304+4\n\t"                                      \
+               "ds_read_b32 %4, %8 offset:" #CT "*2304+8\n\t"                                      \
+               "ds_read_u16 %5, %9 offset:" #CT "*2304\n\t"                                        \
+               "ds_read_u16 %6, %9 offset:" #CT "*2304+32"                                          \
+               : "=&v"(q0[CT]), "=&v"(q1[CT]), "=&v"(sc0[CT]), "=&v"(sc1[CT]), "=&v"(sc2[CT]),     \
+                 "=&v"(d0[CT]), "=&v"(d1[CT])                                                      \
                : "v"(aq), "v"(asc), "v"(ad))
     QI_Q4K_TILE_READ(0);
     QI_Q4K_TILE_READ(1);
@@ -656,16 +612,140 @@ __global__ __launch_bounds__(256) void gemm_lds_q4k_kernel(GemmArgs a) {
       cur[ct].s0 = d0[ct];
       cur[ct].s1 = d1[ct];
     }
+  }
+};
+
+template <>
+struct LdsRec<kQ5_K> {
+  static constexpr Record R = record_geometry(kQ5_K, false);
+  static constexpr uint32_t kBytes = R.bytes, kCopies = 5;
+  static_assert(kBytes == 2816 && R.qh == 2048 && R.sc == 2560 && R.d == 2752 && R.dmin == 2784,
+                "the copies and reads below hard-code the Q5_K record layout");
+  // 2 x 1 KB + 3 x 256 B (64 lanes x 4 B)
+  __device__ static void copy(const uint8_t* src, uint8_t* dst, uint32_t lane) {
+    __builtin_amdgcn_global_load_lds(src + static_cast<uint32_t>(lane * 16), (lds_ptr)dst, 16, 0, 0);
+    __builtin_amdgcn_global_load_lds(src + static_cast<uint32_t>(1024 + lane * 16), (lds_ptr)(dst + 1024), 16, 0,
+                                     0);
+#pragma unroll
+    for (uint32_t i = 0; i < 3; ++i)
+      __builtin_amdgcn_global_load_lds(src + static_cast<uint32_t>(2048 + 256 * i + lane * 4),
+                                       (lds_ptr)(dst + 2048 + 256 * i), 4, 0, 0);
+  }
+  __device__ static void read(uint32_t base, uint32_t lane, Unit<kQ5_K>::Raw cur[4]) {
+    const uint32_t c16 = lane & 15;
+    const uint32_t aq = base + lane * 16, ah = base + R.qh + c16 * 16, asc = base + R.sc + c16 * 12,
+                   ad = base + R.d + c16 * 2;
+    u32x4 q0[4], q1[4], h0[4], h1[4];
+    uint32_t sc0[4], sc1[4], sc2[4], d0[4], d1[4];
+#define QI_Q5K_TILE_READ(CT)                                                                         \
+  asm volatile("ds_read_b128 %0, %9 offset:" #CT "*2816\n\t"                                       \
+               "ds_read_b128 %1, %9 offset:" #CT "*2816+1024\n\t"                                  \
+               "ds_read_b128 %2, %10 offset:" #CT "*2816\n\t"                                      \
+               "ds_read_b128 %3, %10 offset:" #CT "*2816+256\n\t"                                  \
+               "ds_read_b32 %4, %11 offset:" #CT "*2816\n\t"                                       \
+               "ds_read_b32 %5, %11 offset:" #CT "*2816+4\n\t"                                     \
+               "ds_read_b32 %6, %11 offset:" #CT "*2816+8\n\t"                                     \
+               "ds_read_u16 %7, %12 offset:" #CT "*2816\n\t"                                       \
+               "ds_read_u16 %8, %12 offset:" #CT "*2816+32"                                         \
+               : "=&v"(q0[CT]), "=&v"(q1[CT]), "=&v"(h0[CT]), "=&v"(h1[CT]), "=&v"(sc0[CT]),       \
+                 "=&v"(sc1[CT]), "=&v"(sc2[CT]), "=&v"(d0[CT]), "=&v"(d1[CT])                      \
+               : "v"(aq), "v"(ah), "v"(asc), "v"(ad))
+    QI_Q5K_TILE_READ(0);
+    QI_Q5K_TILE_READ(1);
+    QI_Q5K_TILE_READ(2);
+    QI_Q5K_TILE_READ(3);
+#undef QI_Q5K_TILE_READ
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(q0[0]), "+v"(q1[0]), "+v"(h0[0]), "+v"(h1[0]), "+v"(sc0[0]), "+v"(sc1[0]), "+v"(sc2[0]),
+                   "+v"(d0[0]), "+v"(d1[0]), "+v"(q0[1]), "+v"(q1[1]), "+v"(h0[1]), "+v"(h1[1]), "+v"(sc0[1]),
+                   "+v"(sc1[1]), "+v"(sc2[1]), "+v"(d0[1]), "+v"(d1[1]), "+v"(q0[2]), "+v"(q1[2]), "+v"(h0[2]),
+                   "+v"(h1[2]), "+v"(sc0[2]), "+v"(sc1[2]), "+v"(sc2[2]), "+v"(d0[2]), "+v"(d1[2]), "+v"(q0[3]),
+                   "+v"(q1[3]), "+v"(h0[3]), "+v"(h1[3]), "+v"(sc0[3]), "+v"(sc1[3]), "+v"(sc2[3]), "+v"(d0[3]),
+                   "+v"(d1[3]));
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct) {
+      cur[ct].q[0] = __builtin_bit_cast(uint4, q0[ct]);
+      cur[ct].q[1] = __builtin_bit_cast(uint4, q1[ct]);
+      cur[ct].h[0] = __builtin_bit_cast(uint4, h0[ct]);
+      cur[ct].h[1] = __builtin_bit_cast(uint4, h1[ct]);
+      cur[ct].sc[0] = sc0[ct];
+      cur[ct].sc[1] = sc1[ct];
+      cur[ct].sc[2] = sc2[ct];
+      cur[ct].s0 = d0[ct];
+      cur[ct].s1 = d1[ct];
+    }
+  }
+};
+
+template <int QT>
+constexpr uint32_t lds_gemm_bytes() {
+  return kLdsSlots * kLdsStage + 4 * 2 * 4 * LdsRec<QT>::kBytes;
+}
+
+template <int QT>
+__global__ __launch_bounds__(256) void gemm_lds_kernel(GemmArgs a) {
+  using U = Unit<QT>;
+  using L = LdsRec<QT>;
+  static_assert(lds_gemm_bytes<QT>() <= 160 * 1024, "LDS per workgroup");
+  constexpr int RT = 8;
+  constexpr uint32_t kWBuf = 4 * L::kBytes;  // one wavefront's 4 records of a unit
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  uint8_t* const abuf = lds;
+
+  const uint32_t tid = threadIdx.x, lane = tid & 63;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar addressing
+  const uint32_t g = lane >> 4, c16 = lane & 15;
+  uint8_t* const wbuf = lds + kLdsSlots * kLdsStage + wave * 2 * kWBuf;
+  const uint32_t units = a.w.units;
+  const uint32_t ub = blockIdx.z * units / a.splits, ue = (blockIdx.z + 1) * units / a.splits;
+  const uint64_t m0 = static_cast<uint64_t>(blockIdx.y) * kTileM;
+  const uint32_t stages = 4 * ue;
+  const u32x4* xa = reinterpret_cast<const u32x4*>(a.xh) + static_cast<uint64_t>(blockIdx.y) * units * 4096;
+
+  const uint8_t* trec[4];
+#pragma unroll
+  for (int ct = 0; ct < 4; ++ct) {
+    const uint32_t t = min((blockIdx.x * 4 + wave) * 4 + ct, a.w.tiles - 1);
+    trec[ct] = a.w.qs + static_cast<uint64_t>(t) * units * L::kBytes;
+  }
+
+  // stage st's activations (clamped to the last stage) into slot st % 4
+  auto copy_stage = [&](uint32_t st) {
+    const uint32_t sl = st < stages ? st : stages - 1;
+    uint8_t* dst = abuf + (st % kLdsSlots) * kLdsStage;
+    // uniform base plus a 32-bit lane offset: the scalar-base addressing form
+    const uint8_t* src = reinterpret_cast<const uint8_t*>(xa + static_cast<uint64_t>(sl) * 1024);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      __builtin_amdgcn_global_load_lds(src + static_cast<uint32_t>((tid + 256 * i) * 16),
+                                       (lds_ptr)(dst + (256 * i + 64 * wave) * 16), 16, 0, 0);
+  };
+  // this wavefront's records of unit u (clamped) into its buffer (u - ub) & 1
+  auto copy_unit = [&](uint32_t u) {
+    const uint32_t ul = u < ue ? u : ue - 1;
+    uint8_t* dst = wbuf + ((u - ub) & 1) * kWBuf;
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct) L::copy(trec[ct] + static_cast<uint64_t>(ul) * L::kBytes, dst + ct * L::kBytes, lane);
+  };
+
+  typename U::Raw cur[4];
+  float sa[4][U::kWindows], sb[4][U::kWindows];
+  auto take_unit = [&](uint32_t u) {
+    typedef __attribute__((address_space(3))) uint8_t* lds_u8;
+    L::read(static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_u8)wbuf)) + ((u - ub) & 1) * kWBuf, lane, cur);
 #pragma unroll
     for (int ct = 0; ct < 4; ++ct) {
       U::template scales<false>(g, cur[ct], sa[ct], sb[ct]);
-      q4k_affine(sa[ct], sb[ct]);
+      if constexpr (QT == kQ4_K) q4k_affine(sa[ct], sb[ct]);
     }
   };
   auto frags = [&](auto tc, h8 out[4]) {
     constexpr int t = decltype(tc)::value, w = t / U::kSteps;
 #pragma unroll
-    for (int ct = 0; ct < 4; ++ct) out[ct] = q4k_fragment(cur[ct], t, sa[ct][w], sb[ct][w]);
+    for (int ct = 0; ct < 4; ++ct) {
+      if constexpr (QT == kQ4_K) out[ct] = q4k_fragment(cur[ct], t, sa[ct][w], sb[ct][w]);
+      else out[ct] = weight_fragment<QT>(U::codes(cur[ct], g, t), sa[ct][w], sb[ct][w]);
+    }
   };
 
   f4 acc[RT][4];
@@ -683,11 +763,12 @@ __global__ __launch_bounds__(256) void gemm_lds_q4k_kernel(GemmArgs a) {
   __builtin_amdgcn_s_barrier();
   take_unit(ub);
 
+  constexpr int kMid = 8 + 4 * static_cast<int>(L::kCopies);  // copies younger than the stage's, q = 1, 2
   for (uint32_t u = ub; u < ue; ++u) {
     auto step = [&](auto qc) {
       constexpr int q = decltype(qc)::value;
       const uint32_t s = 4 * u + q;
-      if constexpr (q == 1 || q == 2) wait_vm_lgkm0<20>();
+      if constexpr (q == 1 || q == 2) wait_vm_lgkm0<kMid>();
       else wait_vm_lgkm0<8>();
       __builtin_amdgcn_s_barrier();
       copy_stage(s + 3);
@@ -766,15 +847,17 @@ hipError_t launch_reg(const Image& im, const GemmArgs& a, hipStream_t st) {
   return hipGetLastError();
 }
 
-hipError_t launch_lds_q4k(const Image& im, const GemmArgs& a, hipStream_t st) {
+template <int QT>
+hipError_t launch_lds(const Image& im, const GemmArgs& a, hipStream_t st) {
   const uint32_t nblk = static_cast<uint32_t>((im.tiles + 15) / 16);
   const uint32_t mblk = static_cast<uint32_t>(a.m_pad / kTileM);
   if (a.splits < 1 || a.splits > im.k / 256 || (a.splits > 1 && a.part == nullptr)) return hipErrorInvalidValue;
-  auto kern = gemm_lds_q4k_kernel;
+  auto kern = gemm_lds_kernel<QT>;
+  constexpr uint32_t bytes = lds_gemm_bytes<QT>();
   hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                     hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kLdsQ4kBytes));
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(bytes));
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(kern, dim3(nblk, mblk, a.splits), dim3(256), kLdsQ4kBytes, st, a);
+  hipLaunchKernelGGL(kern, dim3(nblk, mblk, a.splits), dim3(256), bytes, st, a);
   e = hipGetLastError();
   if (e != hipSuccess || a.splits == 1) return e;
   const uint64_t count = a.m * im.n;
@@ -813,11 +896,11 @@ hipError_t launch_q(const Image& im, const GemmArgs& a, hipStream_t st) {
                        static_cast<uint32_t>(im.k), a.xh);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    // Q4_K with f16 scales: both operands staged in LDS (faster on MI355X:
-    // 743 against 681 TFLOP/s at 2048 x 4096 x 12288); QI_HIP_GEMM_REG=1
-    // selects the register-weight kernel instead
-    if constexpr (QT == kQ4_K) {
-      if (!im.wide && getenv("QI_HIP_GEMM_REG") == nullptr) return launch_lds_q4k(im, a, st);
+    // Q4_K and Q5_K with f16 scales: both operands staged in LDS (faster on
+    // MI355X: Q4_K 743 against 681 TFLOP/s at 2048 x 4096 x 12288);
+    // QI_HIP_GEMM_REG=1 selects the register-weight kernel instead
+    if constexpr (QT == kQ4_K || QT == kQ5_K) {
+      if (!im.wide && getenv("QI_HIP_GEMM_REG") == nullptr) return launch_lds<QT>(im, a, st);
     }
     return im.wide ? launch_reg<QT, true>(im, a, st) : launch_reg<QT, false>(im, a, st);
   }

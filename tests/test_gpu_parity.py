@@ -354,23 +354,24 @@ def test_mfma_gemm_tolerance_small(ctx, qtype, m):
         assert w.linear(x, qa.MODE_AUTO).tobytes() == y.tobytes()
 
 
+@pytest.mark.parametrize("qtype", [qa.Q4_K, qa.Q5_K], ids=lambda q: NAMES[q])
 @pytest.mark.parametrize("m", [5, 200, 512])
-def test_q4k_gemm_both_kernels(ctx, m, monkeypatch):
-    """Q4_K with f16 scales runs the LDS-staged GEMM; QI_HIP_GEMM_REG=1 the
-    register-weight GEMM. Both meet the MFMA bars (K = 2048 at M = 512 runs
-    8 K-splits of one unit each, the shortest per-workgroup K range), and
-    their results are identical: the same f16 fragments go through the same
-    matrix instructions in the same order."""
+def test_lds_gemm_both_kernels(ctx, qtype, m, monkeypatch):
+    """Q4_K and Q5_K with f16 scales run the LDS-staged GEMM;
+    QI_HIP_GEMM_REG=1 the register-weight GEMM. Both meet the MFMA bars
+    (K = 2048 at M = 512 runs 8 K-splits of one unit each, the shortest
+    per-workgroup K range), and their results are identical: the same f16
+    fragments go through the same matrix instructions in the same order."""
     k, n = 2048, 300
-    blocks = po.make_weights(qa.Q4_K, k, n, seed=6200 + m, outliers=True)
+    blocks = po.make_weights(qtype, k, n, seed=6200 + m + qtype, outliers=True)
     x = po.fill_normal(6300 + m, m * k).reshape(m, k)
-    w = ctx.weights(qa.Q4_K, qa.OUTPUT_ROWS, k, n, blocks)
+    w = ctx.weights(qtype, qa.OUTPUT_ROWS, k, n, blocks)
     y_lds = w.linear(x, qa.MODE_MFMA)
     monkeypatch.setenv("QI_HIP_GEMM_REG", "1")
     y_reg = w.linear(x, qa.MODE_MFMA)
     monkeypatch.delenv("QI_HIP_GEMM_REG")
     for y in (y_lds, y_reg):
-        comp, norm, cpu = _mfma_checks(y, x, blocks, qa.Q4_K, n)
+        comp, norm, cpu = _mfma_checks(y, x, blocks, qtype, n)
         assert comp <= MFMA_TOL and norm <= MFMA_TOL and cpu <= MFMA_TOL, (m, comp, norm, cpu)
     assert y_lds.tobytes() == y_reg.tobytes()
 
