@@ -587,6 +587,158 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attn_kernel(AttnArgs a) {
   if (tid == 0) atomicExch(&a.tickets[ticket], 0u);
 }
 
+// ------------------------------------------------- prompt attention (MFMA)
+// Prompt rows of head_dim 128 on the f32 matrix cores
+// (v_mfma_f32_16x16x4f32: f32 products, f32 sums, the same arithmetic class as
+// the FMA kernel). One workgroup per (16 consecutive rows, KV head), one
+// wavefront per query head of the group; the group's key/value chunks of 64
+// positions are staged in LDS (double-buffered, 2 x 64 KB) and read by every
+// wavefront. Per chunk, per 16-position tile:
+//   S^T (16 positions x 16 rows) = K (positions x 128) . Q^T: A = K from LDS
+//     (lane l: position l % 16, dimension 4 s + l / 16), B = Q^T from 32
+//     registers; lane l ends with row l % 16, positions 4 (l / 16) + i;
+//   online softmax per row (the 4 lanes of a row exchange by shuffles);
+//   O^T (128 x 16 rows) += V^T . P^T: the score registers are the B operand
+//     as they stand (k-step i pairs lane group j with position 4 j + i, and
+//     the value operand is loaded for the same positions), so P needs no
+//     transpose; output tile dt row r holds dimension 8 r + dt, which makes a
+//     lane's 8 value operands of one k-step contiguous (two 16-byte reads) and
+//     its 32 outputs contiguous.
+// LDS rows are rotated (key row d by 16 (d % 4) positions, value row p by
+// 16 ((p / 4) % 4) dimensions) so neither read pattern has bank conflicts.
+// Masked positions (past a row's position) get zero weight; the cache is
+// zeroed at creation, so positions never written hold finite values.
+constexpr uint32_t kMmaChunk = 64;
+constexpr uint32_t kMmaLds = 2 * 2 * 128 * kMmaChunk * 4;  // 2 buffers x (keys + values)
+
+template <int G>
+__global__ __launch_bounds__(64 * G) void attn_mfma_kernel(AttnArgs a) {
+  constexpr uint32_t HD = 128, C = kMmaChunk;
+  typedef float f4v __attribute__((ext_vector_type(4)));
+  typedef __attribute__((address_space(3))) void* lds_ptr;
+  extern __shared__ __attribute__((aligned(16))) float mma_lds[];
+  const uint32_t g = blockIdx.y, lane = threadIdx.x & 63;
+  const uint32_t w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint32_t h = g * G + w;
+  const uint32_t rb = blockIdx.x * 16;  // first row of the block within the call
+  const uint32_t nr = a.nrows - rb < 16u ? a.nrows - rb : 16u;
+  const uint32_t pos0 = *a.len + rb;  // position of the block's first row
+  const uint32_t nchunks = (pos0 + nr - 1) / C + 1;
+  const uint32_t myrow = lane & 15, jg = lane >> 4;
+  const bool rowok = myrow < nr;
+  const uint32_t mypos = pos0 + myrow;
+  const uint32_t ld = a.heads * HD;
+
+  // Q^T operand: lane l holds Q[row l % 16][dimension 4 s + l / 16], s = 0..31
+  float qreg[32];
+  {
+    const float* q = a.q + static_cast<uint64_t>(rb + (rowok ? myrow : 0)) * ld + h * HD + jg;
+#pragma unroll
+    for (int s = 0; s < 32; ++s) qreg[s] = q[4 * s];
+  }
+  const float* kg = a.keys + static_cast<uint64_t>(g) * HD * a.cap;
+  const float* vg = a.values + static_cast<uint64_t>(g) * a.cap * HD;
+  // chunk c into buffer b: keys [128][64] and values [64][128], rotated rows;
+  // 16-byte global-to-LDS copies (4 key rows or 2 value rows each) dealt
+  // round robin to the wavefronts
+  auto copy_chunk = [&](uint32_t c, uint32_t b) {
+    float* ks = mma_lds + b * 2 * HD * C;
+    float* vs = ks + HD * C;
+    const uint32_t t0 = c * C;
+    for (uint32_t i = w; i < HD / 4; i += G) {
+      const uint32_t jj = lane >> 4, qq = lane & 15;
+      const float* src = kg + static_cast<uint64_t>(4 * i + jj) * a.cap + t0 + 4 * ((qq - 4 * jj) & 15);
+      __builtin_amdgcn_global_load_lds(src, (lds_ptr)(ks + i * 256), 16, 0, 0);
+    }
+    for (uint32_t i = w; i < C / 2; i += G) {
+      const uint32_t p = 2 * i + (lane >> 5), qq = lane & 31;
+      const float* src = vg + static_cast<uint64_t>(t0 + p) * HD + ((4 * qq - 16 * ((p >> 2) & 3)) & 127);
+      __builtin_amdgcn_global_load_lds(src, (lds_ptr)(vs + i * 256), 16, 0, 0);
+    }
+  };
+
+  f4v o[8];
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt) o[dt] = f4v{0, 0, 0, 0};
+  float m = -INFINITY, lsum = 0.0f;
+
+  copy_chunk(0, 0);
+  for (uint32_t c = 0; c < nchunks; ++c) {
+    const uint32_t b = c & 1;
+    // chunk c landed (this wavefront's copies, then everyone's), and every
+    // wavefront is done with buffer b ^ 1 (chunk c - 1)
+    __builtin_amdgcn_s_waitcnt(0);
+    __builtin_amdgcn_s_barrier();
+    if (c + 1 < nchunks) copy_chunk(c + 1, b ^ 1);
+    const float* ks = mma_lds + b * 2 * HD * C;
+    const float* vs = ks + HD * C;
+    const uint32_t t0 = c * C;
+
+    f4v sc[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      f4v acc = f4v{0, 0, 0, 0};
+      // key row d = 4 s + jg (d % 4 = jg): position p sits at (p + 16 jg) % 64
+      const float* kr = ks + jg * C + ((16 * t + myrow + 16 * jg) & (C - 1));
+#pragma unroll
+      for (int s = 0; s < 32; ++s) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(kr[4 * s * C], qreg[s], acc, 0, 0, 0);
+      sc[t] = acc;
+    }
+    // scale and mask, then the online softmax of row myrow over this chunk
+    float mx = -INFINITY;
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t p = t0 + 16 * t + 4 * jg + i;
+        const float v = (rowok && p <= mypos) ? sc[t][i] * a.scale : -INFINITY;
+        sc[t][i] = v;
+        mx = fmaxf(mx, v);
+      }
+    mx = fmaxf(mx, __shfl_xor(mx, 16));
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const float mn = fmaxf(m, mx);
+    const float f = mn == -INFINITY ? 1.0f : expf(m - mn);  // 0 while m = -inf
+    m = mn;
+    lsum *= f;
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) o[dt] *= f;
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float e = sc[t][i] == -INFINITY ? 0.0f : expf(sc[t][i] - mn);
+        sc[t][i] = e;
+        lsum += e;
+      }
+    // O^T += V^T . P^T: k-step i of tile t takes position 16 t + 4 jg + i
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t p = 16 * t + 4 * jg + i;  // (p / 4) % 4 = jg
+        const f4v* vr = reinterpret_cast<const f4v*>(vs + p * HD + ((8 * myrow + 16 * jg) & (HD - 1)));
+        const f4v v0 = vr[0], v1 = vr[1];  // dimensions 8 myrow + 0..7
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) o[dt] = __builtin_amdgcn_mfma_f32_16x16x4f32(v0[dt], sc[t][i], o[dt], 0, 0, 0);
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt)
+          o[4 + dt] = __builtin_amdgcn_mfma_f32_16x16x4f32(v1[dt], sc[t][i], o[4 + dt], 0, 0, 0);
+      }
+  }
+  lsum += __shfl_xor(lsum, 16);
+  lsum += __shfl_xor(lsum, 32);
+  if (!rowok) return;
+  // lane l: row l % 16, dimensions 32 jg + 8 i + dt
+  const float inv = 1.0f / lsum;
+  float* out = a.out + static_cast<uint64_t>(rb + myrow) * ld + h * HD + 32 * jg;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    reinterpret_cast<f4v*>(out + 8 * i)[0] = f4v{o[0][i], o[1][i], o[2][i], o[3][i]} * inv;
+    reinterpret_cast<f4v*>(out + 8 * i)[1] = f4v{o[4][i], o[5][i], o[6][i], o[7][i]} * inv;
+  }
+}
+
 // --------------------------------------------------------------- SiLU*up
 // backends/cpu/src/backend.rs:224-237: gate / (1 + exp(-gate)) * up from the
 // fused gate|up output row: the two halves (group 0) or, for an interleaved
@@ -737,6 +889,7 @@ struct qi_hip_qwen3 {
   qi_hip_qwen3_timing timing{};
   bool eager = false;    // QI_HIP_QWEN3_EAGER=1: launch decode steps one by one (no graph)
   bool unfused = false;  // QI_HIP_QWEN3_UNFUSED=1: decode with the separate SiLU and norm kernels
+  bool attn_fma = false;  // QI_HIP_QWEN3_ATTN_FMA=1: prompt attention on the FMA kernel (head_dim 128)
 };
 
 struct qi_hip_kv_cache {
@@ -925,6 +1078,21 @@ qi_hip_status attention(qi_hip_qwen3* m, qi_hip_kv_cache* c, uint32_t layer, uin
   a.keys_w = c->keys + layer * lay;
   a.values_w = c->values + layer * lay;
   a.tickets = c->tickets;
+  if (!fused && hd == 128 && !m->attn_fma) {
+    // prompt rows on the matrix cores: every row in one launch
+    a.row0 = 0;
+    a.nrows = rows;
+    const dim3 grid((rows + 15) / 16, a.kv_heads);
+    switch (group) {
+      case 1: hipLaunchKernelGGL(attn_mfma_kernel<1>, grid, dim3(64), kMmaLds, st, a); break;
+      case 2: hipLaunchKernelGGL(attn_mfma_kernel<2>, grid, dim3(128), kMmaLds, st, a); break;
+      case 4: hipLaunchKernelGGL(attn_mfma_kernel<4>, grid, dim3(256), kMmaLds, st, a); break;
+      case 8: hipLaunchKernelGGL(attn_mfma_kernel<8>, grid, dim3(512), kMmaLds, st, a); break;
+      default: return fail(QI_HIP_UNSUPPORTED, "attention supports 1/2/4/8 query heads per KV head");
+    }
+    QI_HIP_TRY(hipGetLastError(), "launch attention");
+    return QI_HIP_OK;
+  }
   for (uint32_t r0 = 0; r0 < rows; r0 += c->rb) {
     const uint32_t nr = rows - r0 < c->rb ? rows - r0 : c->rb;
     AttnArgs b = a;
@@ -963,6 +1131,11 @@ hipError_t attn_set_lds() {
     e = hipFuncSetAttribute(reinterpret_cast<const void*>(attn_kernel<HD, G, false, attn_rows<HD, G>()>),
                             hipFuncAttributeMaxDynamicSharedMemorySize,
                             static_cast<int>(attn_lds_bytes<HD, G, attn_rows<HD, G>()>()));
+  if constexpr (HD == 128) {
+    if (e == hipSuccess)
+      e = hipFuncSetAttribute(reinterpret_cast<const void*>(attn_mfma_kernel<G>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kMmaLds));
+  }
   return e;
 }
 
@@ -1282,6 +1455,7 @@ qi_hip_status qi_hip_qwen3_create(qi_hip_ctx* ctx, const qi_hip_qwen3_config* cf
   m->layers.resize(k.num_hidden_layers);
   if (const char* env = getenv("QI_HIP_QWEN3_EAGER")) m->eager = atoi(env) != 0;
   if (const char* env = getenv("QI_HIP_QWEN3_UNFUSED")) m->unfused = atoi(env) != 0;
+  if (const char* env = getenv("QI_HIP_QWEN3_ATTN_FMA")) m->attn_fma = atoi(env) != 0;
   std::lock_guard<std::mutex> lock(ctx->mu);
   ctx->refs.fetch_add(1, std::memory_order_relaxed);
   m->ctx = ctx;

@@ -186,18 +186,23 @@ def test_head_dim_128_group_4(qa, ctx):
     dev.free()
 
 
-def test_head_dim_128_prefill_row_blocks(qa, ctx):
-    """AUTO prefill at head_dim 128, 4 query heads per KV head: the prompt
-    attention runs in blocks of 4 rows per workgroup (302 rows: a partial last
-    block), then decode continues from the same cache."""
+@pytest.mark.parametrize("kernel", ["mfma", "fma"])
+def test_head_dim_128_prefill_row_blocks(qa, ctx, kernel, monkeypatch):
+    """AUTO prefill at head_dim 128, 4 query heads per KV head, 302 rows (a
+    partial last block): the prompt attention on the matrix cores (blocks of
+    16 rows) and, with QI_HIP_QWEN3_ATTN_FMA=1, on the FMA kernel (blocks of 4
+    rows); then decode continues from the same cache."""
     cfg = small_config(hidden_size=1024, intermediate_size=1024, num_hidden_layers=1,
                        num_attention_heads=8, num_key_value_heads=2, head_dim=128,
                        vocab_size=2048, max_position_embeddings=512)
     w = Qwen3Weights(cfg, seed=0x5EED0105)
-    dev = w.device_model(ctx)
+    if kernel == "fma":
+        monkeypatch.setenv("QI_HIP_QWEN3_ATTN_FMA", "1")
+    dev = w.device_model(ctx)  # the switch is read when the model is created
+    monkeypatch.delenv("QI_HIP_QWEN3_ATTN_FMA", raising=False)
     dev.set_mode(qa.MODE_AUTO)
     toks = prompt(cfg, 302, seed=16)
-    print("qwen3 hd128 auto prompt=302", flush=True)
+    print(f"qwen3 hd128 auto prompt=302 attention={kernel}", flush=True)
     cache = dev.kv_cache(320)
     ref = w.oracle_model(320)
     logits, nxt = dev.forward(cache, toks)
@@ -209,6 +214,31 @@ def test_head_dim_128_prefill_row_blocks(qa, ctx):
     lg, _ = dev.forward(cache, [nxt])
     wl = ref.forward([nxt], last_only=True)[0]
     assert _rel(lg, wl) <= TOL_MFMA
+    dev.free()
+
+
+@pytest.mark.parametrize("group", [1, 2, 8])
+def test_head_dim_128_prompt_attention_groups(qa, ctx, group):
+    """F32 mode, head_dim 128, 1/2/8 query heads per KV head: a 100-row
+    prompt, then a 50-row chunk on top of the cached positions (rows of a
+    block attend to up to 150 positions in 3 chunks, a partial block last)."""
+    cfg = small_config(hidden_size=1024, intermediate_size=1024, num_hidden_layers=1,
+                       num_attention_heads=8, num_key_value_heads=8 // group, head_dim=128,
+                       vocab_size=2048, max_position_embeddings=256)
+    w = Qwen3Weights(cfg, seed=0x5EED0200 + group)
+    dev = w.device_model(ctx)
+    dev.set_mode(qa.MODE_F32)
+    toks = prompt(cfg, 150, seed=20 + group)
+    print(f"qwen3 hd128 group={group} prompt=100+50", flush=True)
+    cache = dev.kv_cache(192)
+    ref = w.oracle_model(192)
+    for chunk in (toks[:100], toks[100:]):
+        logits, nxt = dev.forward(cache, chunk)
+        want = ref.forward(chunk, last_only=True)[0]
+        err = _rel(logits, want)
+        print(f"  rel err {err:.2e}", flush=True)
+        assert err <= TOL_F32
+        assert nxt == int(np.argmax(logits))
     dev.free()
 
 
