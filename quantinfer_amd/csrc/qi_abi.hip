@@ -95,7 +95,8 @@ qi_hip_status check_call(qi_hip_ctx* ctx, const qi_hip_weights* w, uint64_t m) {
 }
 
 qi_hip_status run_linear(qi_hip_ctx* c, const qi_hip_weights* w, const float* x, uint64_t m,
-                         float* y, int32_t mode, hipStream_t st) {
+                         float* y, int32_t mode, hipStream_t st, float* silu_act, bool* silu_done) {
+  if (silu_done != nullptr) *silu_done = false;
   const Image& im = w->im;
   const qi::View v = qi::make_view(im, w->dev);
   if (mode < QI_HIP_MODE_AUTO || mode > QI_HIP_MODE_MFMA)
@@ -119,6 +120,10 @@ qi_hip_status run_linear(qi_hip_ctx* c, const qi_hip_weights* w, const float* x,
     }
     qi::GemmArgs ga{v, x, y, m, reinterpret_cast<_Float16*>(c->hbuf), m_pad};
     ga.splits = qi::gemm_splits(im, m);
+    if (silu_act != nullptr && silu_done != nullptr && ga.splits == 1 && qi::gemm_silu_supported(im)) {
+      ga.act = silu_act;
+      *silu_done = true;
+    }
     if (ga.splits > 1) {
       const uint64_t need = ga.splits * m_pad * im.n;
       if (need > c->scap) {

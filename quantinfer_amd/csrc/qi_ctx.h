@@ -53,8 +53,13 @@ qi_hip_status hip_fail(hipError_t e, const char* what);
 // when queued work may still read the old buffer.
 qi_hip_status grow(float** buf, uint64_t* cap, uint64_t need, const char* what);
 // One linear layer on device buffers, no locking (the caller holds c->mu).
+// With `silu_act` (an image whose 16-output tiles hold 8 gate rows then the 8
+// matching up rows): when the layer runs as one MFMA GEMM launch without a K
+// split, the GEMM writes SiLU(gate) * up of each pair to silu_act ([m][n/2])
+// instead of y and *silu_done is set; otherwise y is written as usual.
 qi_hip_status run_linear(qi_hip_ctx* c, const qi_hip_weights* w, const float* x, uint64_t m,
-                         float* y, int32_t mode, hipStream_t st);
+                         float* y, int32_t mode, hipStream_t st, float* silu_act = nullptr,
+                         bool* silu_done = nullptr);
 // Upload a planned image; the caller holds c->mu. The handle holds a context
 // reference, as one made by qi_hip_weights_create.
 qi_hip_status create_weights_locked(qi_hip_ctx* c, const qi::Image& im, const void* blocks,

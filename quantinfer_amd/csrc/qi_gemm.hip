@@ -112,6 +112,36 @@ __device__ __forceinline__ h8 weight_fragment(long codes, float a, float b) {
   }
 }
 
+// SiLU-pairs epilogue of a 128-row block (GemmArgs::act): lane (g, c16) holds
+// acc[rt][ct][r], row m0 + 16 rt + 4 g + r of output tile tile0 + ct, column
+// c16; columns c16 and c16 ^ 8 are a gate and its up value. The two lanes of
+// a pair swap their four rows and each finishes two of them (the gate lane
+// rows 0-1, the up lane rows 2-3), writing gate / (1 + e^-gate) * up
+// (backends/cpu/src/backend.rs:224-237) to act[m][8 T + c16 % 8].
+__device__ __forceinline__ void gemm_store_silu(const GemmArgs& a, const f4 (&acc)[8][4], uint32_t tile0,
+                                                uint64_t m0, uint32_t g, uint32_t c16) {
+  const uint64_t lda = a.w.n / 2;
+  const bool up = c16 >= 8;
+  const uint32_t c8 = c16 & 7;
+#pragma unroll
+  for (int ct = 0; ct < 4; ++ct) {
+    const uint64_t T = tile0 + ct;
+#pragma unroll
+    for (int rt = 0; rt < 8; ++rt) {
+      f4 other;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) other[r] = __shfl_xor(acc[rt][ct][r], 8);
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int r = up ? 2 + h : h;
+        const float gate = up ? other[r] : acc[rt][ct][r], upv = up ? acc[rt][ct][r] : other[r];
+        const uint64_t m = m0 + 16 * rt + 4 * g + r;
+        if (T * 16 < a.w.n && m < a.m) a.act[m * lda + T * 8 + c8] = gate / (1.0f + expf(-gate)) * upv;
+      }
+    }
+  }
+}
+
 // (v & mask) | pattern in one instruction: a VOP3 encoding on gfx9 holds no
 // literal and reads at most one scalar register, so the mask comes from a
 // scalar and the pattern from a vector register (the compiler otherwise
@@ -505,6 +535,11 @@ __global__ __launch_bounds__(256) void gemm_reg_kernel(GemmArgs a) {
   }
 
   // C[i][j]: lane j + 16 (i / 4), element i % 4
+  static_assert(RT == 8 && rt0 == 0, "the SiLU epilogue takes the whole 128-row block");
+  if (a.act != nullptr) {
+    gemm_store_silu(a, acc, (blockIdx.x * 4 + cw) * 4, m0, g, c16);
+    return;
+  }
   const uint64_t ld = a.w.n;
   float* const out = a.splits > 1 ? a.part + static_cast<uint64_t>(blockIdx.z) * a.m_pad * ld : a.y;
   float* yrow = out + (m0 + 16 * rt0 + 4 * g) * ld;
@@ -801,6 +836,10 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(GemmArgs a) {
   // workgroup's LDS is released
   wait_vm_lgkm0<0>();
 
+  if (a.act != nullptr) {
+    gemm_store_silu(a, acc, (blockIdx.x * 4 + wave) * 4, m0, g, c16);
+    return;
+  }
   const uint64_t ld = a.w.n;
   float* const out = a.splits > 1 ? a.part + static_cast<uint64_t>(blockIdx.z) * a.m_pad * ld : a.y;
   float* yrow = out + (m0 + 4 * g) * ld;
@@ -914,6 +953,8 @@ bool gemm_supported(int32_t qtype, int32_t layout, uint64_t k, uint64_t n) {
 }
 
 uint64_t gemm_padded_rows(uint64_t m) { return (m + kTileM - 1) / kTileM * kTileM; }
+
+bool gemm_silu_supported(const Image& im) { return im.tiled && !use_ws(im.qtype) && im.n % 16 == 0; }
 
 uint32_t gemm_splits(const Image& im, uint64_t m) {
   // The register-weight kernel runs one workgroup per CU (256 on MI355X),

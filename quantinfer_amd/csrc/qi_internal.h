@@ -93,12 +93,18 @@ struct GemmArgs {
   // summed in split order into y
   float* part = nullptr;
   uint32_t splits = 1;
+  // non-null (splits == 1 only): the epilogue pairs output 16 T + c with
+  // 16 T + 8 + c (c < 8) and writes SiLU(first) * second to act[m][8 T + c]
+  // instead of y (a gate|up image interleaved in groups of 8)
+  float* act = nullptr;
 };
 bool gemm_supported(int32_t qtype, int32_t layout, uint64_t k, uint64_t n);
 uint64_t gemm_padded_rows(uint64_t m);
 // K splits of a GEMM launch (1: no split): enough workgroups to fill the CUs
 // once when the row and column blocks alone do not.
 uint32_t gemm_splits(const Image& im, uint64_t m);
+// The GEMM kernel this image runs on has the SiLU-pairs epilogue.
+bool gemm_silu_supported(const Image& im);
 hipError_t launch_gemm(const Image& im, const GemmArgs& a, hipStream_t st);
 
 }  // namespace qi

@@ -7,11 +7,13 @@
 //   q|k|v projection              one fused GEMV/GEMM image (qi_gemv_mfma / qi_gemm)
 //   q_norm/k_norm, RoPE, KV append qk_norm_rope_kernel
 //   GQA attention                 attn_kernel (a 4-wavefront workgroup per 64 positions;
-//                                 the last workgroup of a KV head combines the chunks)
+//                                 the last workgroup of a KV head combines the chunks);
+//                                 prompt rows at head_dim 128: attn_mfma_kernel
 //   o projection                  GEMV/GEMM
 //   residual + RMSNorm            residual_norm_kernel<ADD>
 //   gate|up projection            one fused image
-//   SiLU(gate) * up               silu_mul_kernel (one row: the gate|up GEMV epilogue)
+//   SiLU(gate) * up               the gate|up GEMV epilogue (one row) or GEMM epilogue
+//                                 (an un-split GEMM); silu_mul_kernel otherwise
 //   down projection               GEMV/GEMM
 //   residual + next RMSNorm       residual_norm_kernel<ADD> (the final norm after the last layer)
 //   LM head on the last row       GEMV (a Q6_K head stays quantized)
@@ -888,7 +890,7 @@ struct qi_hip_qwen3 {
   hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
   qi_hip_qwen3_timing timing{};
   bool eager = false;    // QI_HIP_QWEN3_EAGER=1: launch decode steps one by one (no graph)
-  bool unfused = false;  // QI_HIP_QWEN3_UNFUSED=1: decode with the separate SiLU and norm kernels
+  bool unfused = false;  // QI_HIP_QWEN3_UNFUSED=1: separate SiLU and norm kernels (decode and prompt)
   bool attn_fma = false;  // QI_HIP_QWEN3_ATTN_FMA=1: prompt attention on the FMA kernel (head_dim 128)
 };
 
@@ -1249,10 +1251,18 @@ qi_hip_status enqueue_forward(qi_hip_qwen3* m, qi_hip_kv_cache* c, uint32_t rows
       if ((s = attention(m, c, l, rows)) != QI_HIP_OK) return s;
       if ((s = linear(m, L.o, m->att, rows, m->y)) != QI_HIP_OK) return s;
       if ((s = residual_norm(m, false, c, rows, L.norms + H + 2 * hd)) != QI_HIP_OK) return s;
-      if ((s = linear(m, L.gate_up, m->x, rows, m->gu)) != QI_HIP_OK) return s;
-      const uint64_t total = static_cast<uint64_t>(rows) * I;
-      hipLaunchKernelGGL(silu_mul_kernel, dim3(static_cast<uint32_t>((total + 255) / 256)), dim3(256), 0, st,
-                         m->gu, m->act, I, total, L.gate_up.pair_group);
+      // SiLU(gate) * up in the GEMM epilogue when the layer runs as one
+      // un-split GEMM over an image interleaved in groups of 8; else a pass
+      bool silu_done = false;
+      float* act = L.gate_up.pair_group == 8 && !m->unfused ? m->act : nullptr;
+      if ((s = qi_abi::run_linear(m->ctx, L.gate_up.w, m->x, rows, m->gu, m->mode, st, act, &silu_done)) !=
+          QI_HIP_OK)
+        return s;
+      if (!silu_done) {
+        const uint64_t total = static_cast<uint64_t>(rows) * I;
+        hipLaunchKernelGGL(silu_mul_kernel, dim3(static_cast<uint32_t>((total + 255) / 256)), dim3(256), 0, st,
+                           m->gu, m->act, I, total, L.gate_up.pair_group);
+      }
       if ((s = linear(m, L.down, m->act, rows, m->y)) != QI_HIP_OK) return s;
       const float* next = l + 1 < k.num_hidden_layers ? m->layers[l + 1].norms : m->final_norm;
       if ((s = residual_norm(m, false, c, rows, next)) != QI_HIP_OK) return s;

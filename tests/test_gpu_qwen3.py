@@ -152,6 +152,36 @@ def test_prefill_gemm_and_chunked_prompt(qa, small):
     assert cache.length == 605
 
 
+def test_prompt_silu_in_gemm_epilogue(qa, ctx, monkeypatch):
+    """AUTO prefill of 512 rows with intermediate 8192: the gate|up GEMM
+    (K = 256, N = 16384: 64 x 4 blocks, no K split) writes SiLU(gate) * up in
+    its epilogue. Its logits are identical to the run with the separate SiLU
+    kernel (QI_HIP_QWEN3_UNFUSED=1: the same GEMM accumulators and the same
+    f32 expression), and the greedy token matches the CPU oracle's."""
+    cfg = small_config(hidden_size=256, intermediate_size=8192, num_hidden_layers=1,
+                       num_attention_heads=2, num_key_value_heads=1, head_dim=128,
+                       vocab_size=512, max_position_embeddings=512)
+    w = Qwen3Weights(cfg, seed=0x5EED0300)
+    toks = prompt(cfg, 512, seed=30)
+    print("qwen3 prompt=512 intermediate=8192 fused vs unfused SiLU", flush=True)
+    got = {}
+    for variant in ("fused", "unfused"):
+        if variant == "unfused":
+            monkeypatch.setenv("QI_HIP_QWEN3_UNFUSED", "1")
+        dev = w.device_model(ctx)
+        monkeypatch.delenv("QI_HIP_QWEN3_UNFUSED", raising=False)
+        dev.set_mode(qa.MODE_AUTO)
+        cache = dev.kv_cache(512)
+        got[variant] = dev.forward(cache, toks)
+        dev.free()
+    assert got["fused"][0].tobytes() == got["unfused"][0].tobytes()
+    want = w.oracle_model(512).forward(toks, last_only=True)[0]
+    err = _rel(got["fused"][0], want)
+    print(f"  rel err {err:.2e}", flush=True)
+    assert err <= TOL_MFMA
+    assert got["fused"][1] == int(np.argmax(want))
+
+
 def test_eos_stops_generation(qa, small):
     cfg, w, dev = small
     dev.set_mode(qa.MODE_F32)
