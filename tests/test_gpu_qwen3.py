@@ -155,9 +155,11 @@ def test_prefill_gemm_and_chunked_prompt(qa, small):
 def test_prompt_silu_in_gemm_epilogue(qa, ctx, monkeypatch):
     """AUTO prefill of 512 rows with intermediate 8192: the gate|up GEMM
     (K = 256, N = 16384: 64 x 4 blocks, no K split) writes SiLU(gate) * up in
-    its epilogue. Its logits are identical to the run with the separate SiLU
-    kernel (QI_HIP_QWEN3_UNFUSED=1: the same GEMM accumulators and the same
-    f32 expression), and the greedy token matches the CPU oracle's."""
+    its epilogue, on the LDS-staged kernel and (QI_HIP_GEMM_REG=1, read at
+    each GEMM call) on the register-weight kernel. The logits are identical
+    to the run with the separate SiLU kernel (QI_HIP_QWEN3_UNFUSED=1: the same
+    GEMM accumulators and the same f32 expression), and the greedy token
+    matches the CPU oracle's."""
     cfg = small_config(hidden_size=256, intermediate_size=8192, num_hidden_layers=1,
                        num_attention_heads=2, num_key_value_heads=1, head_dim=128,
                        vocab_size=512, max_position_embeddings=512)
@@ -165,16 +167,20 @@ def test_prompt_silu_in_gemm_epilogue(qa, ctx, monkeypatch):
     toks = prompt(cfg, 512, seed=30)
     print("qwen3 prompt=512 intermediate=8192 fused vs unfused SiLU", flush=True)
     got = {}
-    for variant in ("fused", "unfused"):
+    for variant in ("fused", "fused-register-kernel", "unfused"):
         if variant == "unfused":
             monkeypatch.setenv("QI_HIP_QWEN3_UNFUSED", "1")
         dev = w.device_model(ctx)
         monkeypatch.delenv("QI_HIP_QWEN3_UNFUSED", raising=False)
         dev.set_mode(qa.MODE_AUTO)
         cache = dev.kv_cache(512)
+        if variant == "fused-register-kernel":
+            monkeypatch.setenv("QI_HIP_GEMM_REG", "1")
         got[variant] = dev.forward(cache, toks)
+        monkeypatch.delenv("QI_HIP_GEMM_REG", raising=False)
         dev.free()
     assert got["fused"][0].tobytes() == got["unfused"][0].tobytes()
+    assert got["fused-register-kernel"][0].tobytes() == got["unfused"][0].tobytes()
     want = w.oracle_model(512).forward(toks, last_only=True)[0]
     err = _rel(got["fused"][0], want)
     print(f"  rel err {err:.2e}", flush=True)
