@@ -113,6 +113,17 @@ def gpu_measure(qtype: int, steps: int, warmup: int, copies_mb: float = 512.0):
     stream.synchronize()
     region_ms = start.elapsed_ms(end)
 
+    # PCIe-inclusive rate, never `value`: the synchronous KernelBackend call
+    # (qi_hip_linear: host x in, host y out, copies and the launch on the
+    # context's stream), timed on the host per call
+    xh = normal(0x5EED1000, M * K).reshape(M, K)
+    abi_times = []
+    for i in range(max(10, min(steps, 100))):
+        t = time.perf_counter()
+        weights[i % copies].linear(xh, qa.MODE_F32)
+        abi_times.append(time.perf_counter() - t)
+    abi_ms = statistics.median(abi_times) * 1e3
+
     name = ctx.device_name()
     start.destroy()
     end.destroy()
@@ -122,7 +133,8 @@ def gpu_measure(qtype: int, steps: int, warmup: int, copies_mb: float = 512.0):
     y.free()
     stream.destroy()
     ctx.close()
-    return {"region_ms": region_ms, "copies": copies, "device": name}
+    return {"region_ms": region_ms, "copies": copies, "device": name, "abi_ms": abi_ms,
+            "abi_calls": len(abi_times)}
 
 
 def copy_calibration(steps: int, mib: int = 256) -> None:
@@ -199,6 +211,24 @@ def gemm_bench(qtype: int, m: int, k: int, n: int, steps: int, warmup: int) -> d
     }
 
 
+def host_cpu() -> str:
+    """The host CPU model and the logical CPU count this process may use."""
+    model = "unknown CPU"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for ln in f:
+                if ln.startswith("model name"):
+                    model = ln.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        avail = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        avail = os.cpu_count() or 0
+    return f"{model} ({avail} CPUs available)"
+
+
 def cpu_baseline(qtype: int, repeats: int = 3):
     """The oracle's port of CpuScalar::matmul_q4_k_output_rows (single-threaded,
     as the reference's output-row kernels are), pinned to one host core."""
@@ -225,7 +255,8 @@ def cpu_baseline(qtype: int, repeats: int = 3):
         "value": round(algorithmic_bytes(qtype, K, N, M) / sec / 1e9, 3),
         "unit": "GB/s", "cores": 1, "kind": "port",
         "sample": f"full workload (M=1, K={K}, N={N}) x{repeats}, median {sec * 1e3:.1f} ms; "
-                  f"oracle C port of CpuScalar output-row kernel, 1 pinned core",
+                  f"oracle C port of CpuScalar output-row kernel, 1 pinned core of "
+                  f"{host_cpu()}; Q4_K has no cpu-simd path in the reference",
     }
 
 
@@ -373,7 +404,7 @@ def e2e_cpu_baseline(cfg) -> dict:
     return {"value": round(1.0 / sec, 4), "unit": "tok/s", "cores": 1, "kind": "port",
             "sample": f"one layer's 7 Q4_K projections ({t_layer:.2f} s) x36 + f32 LM head "
                       f"({t_head:.2f} s) at M=1: {sec:.1f} s per decode token; oracle C port of "
-                      f"CpuScalar (matmul.rs:282-332, :92-117), 1 pinned core"}
+                      f"CpuScalar (matmul.rs:282-332, :92-117), 1 pinned core of {host_cpu()}"}
 
 
 def main():
@@ -442,6 +473,12 @@ def main():
             "traffic": traffic_from_profile("q4_k_gemv_4096x14336_traffic.md"),
         },
         "cpu_baseline": None if args.no_cpu else cpu_baseline(qtype),
+        "through_abi": {
+            "value": round(abytes / (g["abi_ms"] * 1e-3) / 1e9, 2), "unit": "GB/s",
+            "ms_per_call": round(g["abi_ms"], 5), "calls": g["abi_calls"],
+            "note": "qi_hip_linear with host x and y (H2D, GEMV, D2H, synchronous): the "
+                    "PCIe-inclusive KernelBackend call, median over calls; not `value`",
+        },
     }
     if not args.no_e2e:
         line["e2e"] = e2e_bench(with_cpu=not args.no_cpu)

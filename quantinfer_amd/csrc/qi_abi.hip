@@ -53,6 +53,19 @@ qi_hip_status grow(float** buf, uint64_t* cap, uint64_t need, const char* what) 
   return QI_HIP_OK;
 }
 
+// Pinned host staging buffer of at least `need` floats. Every qi_hip_linear
+// call ends with a stream synchronize, so no copy still reads the old one.
+qi_hip_status grow_pinned(float** buf, uint64_t* cap, uint64_t need) {
+  if (need <= *cap) return QI_HIP_OK;
+  if (*buf) (void)hipHostFree(*buf);
+  *buf = nullptr;
+  *cap = 0;
+  QI_HIP_TRY(hipHostMalloc(reinterpret_cast<void**>(buf), need * sizeof(float), hipHostMallocDefault),
+             "alloc pinned staging");
+  *cap = need;
+  return QI_HIP_OK;
+}
+
 qi_hip_status ensure_tickets(qi_hip_ctx* c, uint64_t need) {
   if (need <= c->tickets_cap) return QI_HIP_OK;
   QI_HIP_TRY(hipStreamSynchronize(c->stream), "synchronize before growing tickets");
@@ -73,6 +86,8 @@ void ctx_destroy(qi_hip_ctx* c) {
   if (c->tickets) (void)hipFree(c->tickets);
   if (c->xbuf) (void)hipFree(c->xbuf);
   if (c->ybuf) (void)hipFree(c->ybuf);
+  if (c->hx) (void)hipHostFree(c->hx);
+  if (c->hy) (void)hipHostFree(c->hy);
   if (c->hbuf) (void)hipFree(c->hbuf);
   if (c->sbuf) (void)hipFree(c->sbuf);
   if (c->dbuf) (void)hipFree(c->dbuf);
@@ -384,6 +399,8 @@ qi_hip_status qi_hip_weights_info_get(const qi_hip_weights* w, qi_hip_weights_in
   return QI_HIP_OK;
 }
 
+constexpr uint64_t kStageFloats = 16ull << 20;  // 64 MiB
+
 qi_hip_status qi_hip_linear(qi_hip_ctx* c, const qi_hip_weights* w, const float* x_host, uint64_t m,
                             float* y_host, int32_t mode) {
   qi_hip_status s = check_call(c, w, m);
@@ -394,11 +411,23 @@ qi_hip_status qi_hip_linear(qi_hip_ctx* c, const qi_hip_weights* w, const float*
   const uint64_t xn = m * w->im.k, yn = m * w->im.n;
   if ((s = grow(&c->xbuf, &c->xcap, xn + 64, "alloc activations")) != QI_HIP_OK) return s;
   if ((s = grow(&c->ybuf, &c->ycap, yn, "alloc outputs")) != QI_HIP_OK) return s;
-  QI_HIP_TRY(hipMemcpyAsync(c->xbuf, x_host, xn * 4, hipMemcpyHostToDevice, c->stream), "copy x");
+  // Activations up to 64 MiB each way are staged through pinned host buffers
+  // (a host memcpy, then an asynchronous DMA); larger ones are copied from the
+  // caller's pageable memory directly.
+  const bool staged = xn <= kStageFloats && yn <= kStageFloats;
+  if (staged) {
+    if ((s = grow_pinned(&c->hx, &c->hxcap, xn)) != QI_HIP_OK) return s;
+    if ((s = grow_pinned(&c->hy, &c->hycap, yn)) != QI_HIP_OK) return s;
+    memcpy(c->hx, x_host, xn * 4);
+  }
+  QI_HIP_TRY(hipMemcpyAsync(c->xbuf, staged ? c->hx : x_host, xn * 4, hipMemcpyHostToDevice, c->stream),
+             "copy x");
   s = run_linear(c, w, c->xbuf, m, c->ybuf, mode, c->stream);
   if (s != QI_HIP_OK) return s;
-  QI_HIP_TRY(hipMemcpyAsync(y_host, c->ybuf, yn * 4, hipMemcpyDeviceToHost, c->stream), "copy y");
+  QI_HIP_TRY(hipMemcpyAsync(staged ? c->hy : y_host, c->ybuf, yn * 4, hipMemcpyDeviceToHost, c->stream),
+             "copy y");
   QI_HIP_TRY(hipStreamSynchronize(c->stream), "synchronize");
+  if (staged) memcpy(y_host, c->hy, yn * 4);
   return QI_HIP_OK;
 }
 

@@ -29,6 +29,12 @@ struct qi_hip_ctx {
   uint64_t xcap = 0;  // floats
   float* ybuf = nullptr;
   uint64_t ycap = 0;
+  // pinned host staging of qi_hip_linear (hipHostMalloc), so that its copies
+  // are asynchronous DMA transfers instead of pageable-memory copies
+  float* hx = nullptr;
+  uint64_t hxcap = 0;  // floats
+  float* hy = nullptr;
+  uint64_t hycap = 0;
   float* hbuf = nullptr;  // f16 activations of the prefill GEMM (capacity in floats)
   uint64_t hcap = 0;
   float* sbuf = nullptr;  // split-K partial products of the prefill GEMM (capacity in floats)
