@@ -400,6 +400,7 @@ qi_hip_status qi_hip_weights_info_get(const qi_hip_weights* w, qi_hip_weights_in
 }
 
 constexpr uint64_t kStageFloats = 16ull << 20;  // 64 MiB
+constexpr uint64_t kDirectFloats = 1ull << 20;  // 4 MiB
 
 qi_hip_status qi_hip_linear(qi_hip_ctx* c, const qi_hip_weights* w, const float* x_host, uint64_t m,
                             float* y_host, int32_t mode) {
@@ -422,10 +423,15 @@ qi_hip_status qi_hip_linear(qi_hip_ctx* c, const qi_hip_weights* w, const float*
   }
   QI_HIP_TRY(hipMemcpyAsync(c->xbuf, staged ? c->hx : x_host, xn * 4, hipMemcpyHostToDevice, c->stream),
              "copy x");
-  s = run_linear(c, w, c->xbuf, m, c->ybuf, mode, c->stream);
+  // Outputs up to 4 MiB go from the kernels straight into the pinned buffer
+  // (device-mapped host memory, visible to the host once the stream is
+  // synchronized), which saves the device-to-host copy.
+  const bool direct = staged && yn <= kDirectFloats;
+  s = run_linear(c, w, c->xbuf, m, direct ? c->hy : c->ybuf, mode, c->stream);
   if (s != QI_HIP_OK) return s;
-  QI_HIP_TRY(hipMemcpyAsync(staged ? c->hy : y_host, c->ybuf, yn * 4, hipMemcpyDeviceToHost, c->stream),
-             "copy y");
+  if (!direct)
+    QI_HIP_TRY(hipMemcpyAsync(staged ? c->hy : y_host, c->ybuf, yn * 4, hipMemcpyDeviceToHost, c->stream),
+               "copy y");
   QI_HIP_TRY(hipStreamSynchronize(c->stream), "synchronize");
   if (staged) memcpy(y_host, c->hy, yn * 4);
   return QI_HIP_OK;
