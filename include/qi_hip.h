@@ -135,7 +135,9 @@ qi_hip_status qi_hip_weights_info_get(const qi_hip_weights *w, qi_hip_weights_in
  * (lib.rs:97-99), matmul_q8_0_output_rows / matmul_q4_0_output_rows
  * (lib.rs:102-113), matmul_q4_k / q5_k / q6_k (lib.rs:115-119) and
  * matmul_q{4,5,6}_k_output_rows (lib.rs:122-140): the variant is selected by the
- * handle's qtype and layout. */
+ * handle's qtype and layout. x and y pass through pinned host buffers the
+ * context keeps (grown to the largest call up to 64 MiB each way, freed at
+ * close); larger ones are copied from and to the caller's memory directly. */
 qi_hip_status qi_hip_linear(qi_hip_ctx *ctx, const qi_hip_weights *w, const float *x_host,
                             uint64_t m, float *y_host, int32_t mode);
 
