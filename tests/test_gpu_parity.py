@@ -297,6 +297,37 @@ def test_linear_device_matches_host_path(ctx):
     stream.destroy()
 
 
+@pytest.mark.parametrize("qtype,m,k,n,note", [
+    (qa.Q4_K, 128, 256, 4096, "y 2 MiB: the kernels write into the pinned host buffer"),
+    (qa.Q4_K, 128, 256, 16384, "y 8 MiB: pinned staging and a device-to-host copy"),
+    (qa.Q8_0, 4200, 4096, 256, "x 66 MiB: copies from and to the caller's memory"),
+    (qa.Q4_K, 2, 4096, 512, "small again after the buffers grew"),
+])
+def test_host_path_copy_regimes(ctx, qtype, m, k, n, note):
+    """qi_hip_linear moves x and y through pinned buffers, writes outputs up
+    to 4 MiB from the kernels into pinned host memory, and copies larger ones
+    directly: every regime returns the device-buffer entry point's result bit
+    for bit (AUTO mode: GEMV or GEMM by M)."""
+    from quantinfer_amd import hiprt
+    print(f"host path {m}x{k}x{n}: {note}", flush=True)
+    blocks = po.make_weights(qtype, k, n, seed=21, outliers=False)
+    w = ctx.weights(qtype, qa.OUTPUT_ROWS, k, n, blocks)
+    x = po.fill_normal(22, m * k).reshape(m, k)
+    xd = hiprt.DeviceBuffer.from_array(x)
+    yd = hiprt.DeviceBuffer(m * n * 4)
+    stream = hiprt.Stream()
+    w.linear_device(xd.ptr, m, yd.ptr, qa.MODE_AUTO, stream.handle)
+    stream.synchronize()
+    want = yd.to_array(np.float32, (m, n))
+    got = w.linear(x, qa.MODE_AUTO)
+    assert got.tobytes() == want.tobytes()
+    assert np.isfinite(got).all()
+    stream.destroy()
+    xd.free()
+    yd.free()
+    w.free()
+
+
 def test_gpu_error_paths(ctx):
     blocks = po.make_weights(qa.Q8_0, 64, 4, seed=1)
     w = ctx.weights(qa.Q8_0, qa.OUTPUT_ROWS, 64, 4, blocks)
