@@ -260,6 +260,46 @@ def cpu_baseline(qtype: int, repeats: int = 3):
     }
 
 
+def cpu_simd_table(repeats: int = 3) -> dict:
+    """The reference's two CPU kernels for Q8_0/Q4_0 output rows, one pinned
+    core each: the scalar CpuScalar order (matmul.rs:119-160) and the cpu-simd
+    per-block dot (cpu-simd lib.rs:179-204; AVX-512 where the host has it, else
+    AVX2), on BASELINE configs[0] (Q8_0, K = N = 4096) and a configs[1] shape
+    (Q4_0, K = 4096, N = 12288), M = 1. GB/s of algorithmic bytes."""
+    from oracle import pyoracle as po
+
+    isa = 2 if po.simd_available(2) else (1 if po.simd_available(1) else 0)
+    rows = []
+    try:
+        old = os.sched_getaffinity(0)
+        os.sched_setaffinity(0, {min(old)})
+    except (AttributeError, OSError):
+        old = None
+    try:
+        for qtype, name, k, n in ((1, "q8_0", 4096, 4096), (2, "q4_0", 4096, 12288)):
+            blocks = synth_blocks(qtype, n * (k // BLOCK[qtype]), seed=0x5EED0000 + qtype)
+            x = normal(0x5EED1000, k).reshape(1, k)
+            row = {"qtype": name, "k": k, "n": n, "m": 1}
+            legs = [("scalar", lambda: po.matmul_output_rows(qtype, x, blocks, n))]
+            if isa:
+                legs.append(("simd", lambda: po.matmul_output_rows_simd(qtype, isa, x, blocks, n)))
+            for leg, fn in legs:
+                times = []
+                for _ in range(repeats):
+                    t = time.perf_counter()
+                    fn()
+                    times.append(time.perf_counter() - t)
+                sec = statistics.median(times)
+                row[leg + "_ms"] = round(sec * 1e3, 3)
+                row[leg + "_gbps"] = round(algorithmic_bytes(qtype, k, n, 1) / sec / 1e9, 3)
+            rows.append(row)
+    finally:
+        if old is not None:
+            os.sched_setaffinity(0, old)
+    return {"cpu_simd_table": rows, "isa": {0: "none", 1: "avx2", 2: "avx512f"}[isa], "cores": 1,
+            "host": host_cpu(), "kind": "port"}
+
+
 # --------------------------------------------------------------- e2e decode
 
 QWEN3_8B = dict(vocab_size=151936, hidden_size=4096, intermediate_size=12288, num_hidden_layers=36,
@@ -419,6 +459,8 @@ def main():
                     help="gemv: the headline decode GEMV, with the e2e decode line embedded "
                          "(default); gemm: the MFMA prefill GEMM; e2e: Qwen3-8B-shape decode only")
     ap.add_argument("--no-e2e", action="store_true", help="gemv: leave out the e2e decode run")
+    ap.add_argument("--cpu-simd", action="store_true",
+                    help="only the CPU table: scalar and cpu-simd Q8_0/Q4_0 kernels, one core")
     ap.add_argument("--qtype", default="q4_k", help="gemm only: q8_0, q4_0, q4_k, q5_k or q6_k")
     ap.add_argument("--mkn", default="2048,4096,12288", help="gemm only: M,K,N")
     args = ap.parse_args()
@@ -429,6 +471,9 @@ def main():
 
     if args.copy_calibration:
         copy_calibration(args.steps)
+        return
+    if args.cpu_simd:
+        print(json.dumps(cpu_simd_table()))
         return
     if args.workload == "gemm":
         qt = {"q8_0": 1, "q4_0": 2, "q4_k": 3, "q5_k": 4, "q6_k": 5}[args.qtype]
