@@ -213,7 +213,7 @@ __global__ __launch_bounds__(64 * SW * WC) void gemv_mfma_kernel(GemvMfmaArgs a)
       }
 #pragma unroll
       for (int i = 0; i < D; ++i)
-        U::template load<WIDE>(trec + min(ku0 + u_begin + i, u_last) * R.bytes, lane, ring[i]);
+        U::template load<WIDE, true>(trec + min(ku0 + u_begin + i, u_last) * R.bytes, lane, ring[i]);
       (void)halves;
       (void)K;
       (void)k0;
@@ -242,7 +242,7 @@ __global__ __launch_bounds__(64 * SW * WC) void gemv_mfma_kernel(GemvMfmaArgs a)
       if constexpr (XS != kXPlain) __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int i = 0; i < D; ++i)
-        U::template load<WIDE>(trec + min(ku0 + u_begin + i, u_last) * R.bytes, lane, ring[i]);
+        U::template load<WIDE, true>(trec + min(ku0 + u_begin + i, u_last) * R.bytes, lane, ring[i]);
 
       // kXNorm: sum(v^2) over valid items, x = v * w
       [[maybe_unused]] auto norm = [&](HalfX& vx, const HalfX& wx, bool valid) {
@@ -337,7 +337,7 @@ __global__ __launch_bounds__(64 * SW * WC) void gemv_mfma_kernel(GemvMfmaArgs a)
     for (uint32_t j = D; j < u_count; j += D) {
 #pragma unroll
       for (int i = 0; i < D; ++i)
-        U::template load<WIDE>(trec + min(ku0 + u_begin + j + i, u_last) * R.bytes, lane, ring[i]);
+        U::template load<WIDE, true>(trec + min(ku0 + u_begin + j + i, u_last) * R.bytes, lane, ring[i]);
       consume(j);
     }
     __syncthreads();  // LDS reused by the next chunk / the reduction

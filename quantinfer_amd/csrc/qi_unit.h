@@ -8,6 +8,18 @@
 #include "qi_device.h"
 
 namespace qi {
+// 16 bytes of weight codes. NT: a non-temporal (streaming) load, for kernels
+// that read every weight byte once (the GEMV: 3.97-4.02 against 3.73-3.84
+// TB/s at Q4_K 4096 x 14336 on MI355X, alternating runs); the GEMMs re-read a
+// weight tile for every row block and keep ordinary loads.
+template <bool NT>
+__device__ __forceinline__ uint4 ld_codes(const uint4* p) {
+  static_assert(NT, "ordinary loads index the record directly");
+  typedef unsigned int v4 __attribute__((ext_vector_type(4)));
+  const v4 v = __builtin_nontemporal_load(reinterpret_cast<const v4*>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
 
 template <int QT>
 struct Unit;  // per-format code/scale access for one (output n, lane group g, unit u)
@@ -24,11 +36,16 @@ struct Unit<kQ8_0> {
     uint4 q[4];
     uint32_t s0, s1;  // f16 pair in s0, or two f32 scales
   };
-  template <bool W>
+  template <bool W, bool NT = false>
   __device__ static void load(const uint8_t* rec, uint32_t lane, Raw& r) {
     constexpr Record R = record_geometry(kQ8_0, W);
     const uint4* p = reinterpret_cast<const uint4*>(rec + R.qs) + lane;
-    r.q[0] = p[0]; r.q[1] = p[64]; r.q[2] = p[128]; r.q[3] = p[192];
+    if constexpr (NT) {
+      r.q[0] = ld_codes<true>(p); r.q[1] = ld_codes<true>(p + 64);
+      r.q[2] = ld_codes<true>(p + 128); r.q[3] = ld_codes<true>(p + 192);
+    } else {
+      r.q[0] = p[0]; r.q[1] = p[64]; r.q[2] = p[128]; r.q[3] = p[192];
+    }
     const uint32_t e = (lane & 15) * 8 + 2 * (lane >> 4);  // blocks 2g, 2g+1 of row c
     if constexpr (W) {
       const uint2 d = *reinterpret_cast<const uint2*>(rec + R.d + e * 4);
@@ -65,11 +82,15 @@ struct Unit<kQ4_0> {
     uint4 q[2];
     uint32_t s0, s1;
   };
-  template <bool W>
+  template <bool W, bool NT = false>
   __device__ static void load(const uint8_t* rec, uint32_t lane, Raw& r) {
     constexpr Record R = record_geometry(kQ4_0, W);
     const uint4* p = reinterpret_cast<const uint4*>(rec + R.qs) + lane;
-    r.q[0] = p[0]; r.q[1] = p[64];
+    if constexpr (NT) {
+      r.q[0] = ld_codes<true>(p); r.q[1] = ld_codes<true>(p + 64);
+    } else {
+      r.q[0] = p[0]; r.q[1] = p[64];
+    }
     const uint32_t e = (lane & 15) * 8 + 2 * (lane >> 4);
     if constexpr (W) {
       const uint2 d = *reinterpret_cast<const uint2*>(rec + R.d + e * 4);
@@ -118,12 +139,16 @@ struct UnitQ45K {
     uint32_t sc[3];
     uint32_t s0, s1;  // d and dmin: f16 bits (zero-extended) or f32 bits
   };
-  template <bool W>
+  template <bool W, bool NT = false>
   __device__ static void load(const uint8_t* rec, uint32_t lane, Raw& r) {
     constexpr Record R = record_geometry(kQT, W);
     const uint32_t col = lane & 15;
     const uint4* p = reinterpret_cast<const uint4*>(rec + R.qs) + lane;
-    r.q[0] = p[0]; r.q[1] = p[64];
+    if constexpr (NT) {
+      r.q[0] = ld_codes<true>(p); r.q[1] = ld_codes<true>(p + 64);
+    } else {
+      r.q[0] = p[0]; r.q[1] = p[64];
+    }
     if constexpr (FIVE) {
       const uint4* h = reinterpret_cast<const uint4*>(rec + R.qh) + col;
       r.h[0] = h[0]; r.h[1] = h[16];
@@ -197,12 +222,16 @@ struct Unit<kQ6_K> {
     uint32_t sc;  // this lane group's four int8 sub-scales
     uint32_t d;   // f16 in the low half, or f32
   };
-  template <bool W>
+  template <bool W, bool NT = false>
   __device__ static void load(const uint8_t* rec, uint32_t lane, Raw& r) {
     constexpr Record R = record_geometry(kQ6_K, W);
     const uint32_t col = lane & 15, ip = lane >> 5;
     const uint4* p = reinterpret_cast<const uint4*>(rec + R.qs) + lane;
-    r.q[0] = p[0]; r.q[1] = p[64];
+    if constexpr (NT) {
+      r.q[0] = ld_codes<true>(p); r.q[1] = ld_codes<true>(p + 64);
+    } else {
+      r.q[0] = p[0]; r.q[1] = p[64];
+    }
     const uint4* h = reinterpret_cast<const uint4*>(rec + R.qh) + 32 * ip + col;
     r.h[0] = h[0]; r.h[1] = h[16];
     r.sc = *reinterpret_cast<const uint32_t*>(rec + R.sc + col * 16 + 4 * (lane >> 4));
