@@ -198,3 +198,77 @@ def test_block_validation_matches_core():
     c["scale"] = np.inf  # core quantized/q8.rs:34-38
     assert not po.validate_blocks(po.Q8_0, c, 32)
     assert not po.validate_blocks(po.Q8_0, np.zeros(1, dtype=po.BLOCK_DTYPES[po.Q8_0]), 64)
+
+
+# ----------------------------------------------------------------- Q5_K pin
+#
+# The dequantizer's fifth-bit decode (quant/src/schemes/q5_k.rs:96-135,
+# backends/cpu/src/matmul.rs:217-258) is pinned twice, without retyping it:
+#  - by the quantizer: its placement of the fifth bit is held by the
+#    reference's own nearest-codebook test above (k_grid_tests.rs:82-113 reads
+#    the bit as 2*group + within/32), so dequantize(quantize(x)) must land on
+#    the nearest point of each sub-block's grid {d*sc*c - dmin*m : c = 0..31},
+#    which is computed here from the block's scales alone;
+#  - by a hand-worked block whose low and high nibbles differ and whose high
+#    bits form a checkerboard, so that reading bit 2g+1 for the low half (or
+#    2g for the high half) changes every element by 16*d*sc.
+
+
+@pytest.mark.parametrize("seed", [11, 12])
+def test_q5_k_dequantize_lands_on_nearest_grid_point(seed):
+    # N(0, 0.02^2) with 0.5% N(0, 0.2^2) outliers, as BASELINE configs[2]
+    x = po.fill_normal(seed, 256 * 96, 0.02, 0.005, 0.2)
+    blocks = po.quantize(po.Q5_K, x)
+    deq = po.dequantize(po.Q5_K, blocks).astype(np.float64)
+    codes = np.arange(32, dtype=np.float64)
+    checked = 0
+    for bi, blk in enumerate(blocks):
+        d, dmin = float(blk["scale"]), float(blk["min_scale"])
+        for sub in range(8):
+            s, m = _sc_m(blk["scales"].astype(int), sub)
+            a, b = d * s, dmin * m
+            grid = a * codes - b
+            lo = bi * 256 + sub * 32
+            xs = x[lo:lo + 32].astype(np.float64)
+            nearest = np.min(np.abs(grid[None, :] - xs[:, None]), axis=1)
+            err = np.abs(deq[lo:lo + 32] - xs)
+            # f32 evaluation of (d*sc)*q - dmin*m: a few ulps of its operands
+            tol = (abs(a) * 32.0 + abs(b)) * 4.0 * float(np.finfo(f32).eps) + 1e-30
+            assert np.all(err <= nearest + tol), (bi, sub)
+            # inside the grid the nearest point is at most half a step away
+            inside = (xs >= -b) & (xs <= a * 31.0 - b)
+            assert np.all(err[inside] <= 0.5 * a + tol), (bi, sub)
+            checked += int(inside.sum())
+    assert checked > 0.9 * x.size
+
+
+def test_q5_k_dequantize_hand_worked_block():
+    b = np.zeros(1, dtype=po.BLOCK_DTYPES[po.Q5_K])
+    b["scale"] = 0.5
+    b["min_scale"] = 0.25
+    # sc0..3 = 1, 2, 3, 4 and m0..3 = 5, 6, 7, 8 (6-bit fields, top bits 0);
+    # bytes 8..11 = 0x21: sc4..7 = 1, m4..7 = 2
+    b["scales"][0] = [1, 2, 3, 4, 5, 6, 7, 8, 0x21, 0x21, 0x21, 0x21]
+    b["values"] = 0x3A     # low nibble 10, high nibble 3
+    b["high_bits"] = 0x55  # bits 0, 2, 4, 6: the low half's fifth bit only
+    sc = [1, 2, 3, 4, 1, 1, 1, 1]
+    mn = [5, 6, 7, 8, 2, 2, 2, 2]
+    deq = po.dequantize(po.Q5_K, b)
+    # sub-block j = 2g (elements 64g + [0, 32)): q = 10 + 16 = 26;
+    # sub-block j = 2g + 1 (elements 64g + [32, 64)): q = 3
+    expected = np.empty(256, dtype=np.float64)
+    for j in range(8):
+        q = 26 if j % 2 == 0 else 3
+        expected[32 * j:32 * (j + 1)] = 0.5 * sc[j] * q - 0.25 * mn[j]
+    # e.g. element 0: 0.5*1*26 - 0.25*5 = 11.75; element 32: 0.5*2*3 - 0.25*6 = 1.5
+    assert expected[0] == 11.75 and expected[32] == 1.5 and expected[255] == 1.0
+    assert np.array_equal(deq.astype(np.float64), expected)
+    # the checkerboard the other way round: the high half's bit only
+    b["high_bits"] = 0xAA
+    deq = po.dequantize(po.Q5_K, b)
+    for j in range(8):
+        q = 10 if j % 2 == 0 else 19
+        expected[32 * j:32 * (j + 1)] = 0.5 * sc[j] * q - 0.25 * mn[j]
+    assert np.array_equal(deq.astype(np.float64), expected)
+    for i in (0, 37, 100, 255):
+        assert po.value(po.Q5_K, b, i) == expected[i]
