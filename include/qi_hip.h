@@ -182,6 +182,20 @@ qi_hip_status qi_hip_pack_gguf(int32_t qtype, int32_t layout, uint64_t k, uint64
                                const void *wire, uint64_t wire_bytes, int32_t legacy, void *out,
                                uint64_t *bytes, int32_t *f16_scales);
 
+/* Host-only: quantize n f32 values (a multiple of 32 for Q8_0/Q4_0, of 256
+ * for the K-quants) into out_count = n / block-size logical blocks of `qtype`,
+ * bit for bit as the reference's quantizers: quantize_q8_0 / q4_0 / q4_k /
+ * q5_k / q6_k (crates/quantinfer-quant/src/schemes/q8.rs:8-31, q4.rs:8-33,
+ * q4_k.rs:8-88, q5_k.rs:8-94, q6_k.rs:8-72). storage_f16 = 1 then rounds every
+ * scale to its f16 storage value as QuantizedData::with_storage_precision
+ * (quant/src/providers/storage.rs:28-87; the K-quant scales already are).
+ * Blocks are split over `threads` host threads (<= 0: one per hardware
+ * thread); the result does not depend on the count. QI_HIP_INVALID_INPUT for a
+ * non-finite value, a bad count or a scale f16 cannot hold finitely (the
+ * reference's QuantizationError::InvalidInput); `out` is then unspecified. */
+qi_hip_status qi_hip_quantize(int32_t qtype, const float *values, uint64_t n, int32_t storage_f16,
+                              void *out, uint64_t out_count, int32_t threads);
+
 /* ------------------------------------------------------------------------
  * GPU-resident Qwen3 dense decoder.
  *

@@ -109,6 +109,7 @@ def lib() -> ctypes.CDLL:
         l.qi_hip_weights_create_gguf.argtypes = [vp, i32, i32, u64, u64, vp, u64, i32, ctypes.POINTER(vp)]
         l.qi_hip_pack_gguf.argtypes = [i32, i32, u64, u64, vp, u64, i32, vp, ctypes.POINTER(u64),
                                        ctypes.POINTER(i32)]
+        l.qi_hip_quantize.argtypes = [i32, vp, u64, i32, vp, u64, i32]
         u32 = ctypes.c_uint32
         l.qi_hip_qwen3_create.argtypes = [vp, ctypes.POINTER(Qwen3Config), ctypes.POINTER(vp)]
         l.qi_hip_qwen3_set_embedding.argtypes = [vp, vp]
@@ -128,7 +129,7 @@ def lib() -> ctypes.CDLL:
         for name in ("qi_hip_open", "qi_hip_device_name", "qi_hip_weights_create",
                      "qi_hip_weights_info_get", "qi_hip_linear", "qi_hip_linear_device",
                      "qi_hip_dequantize", "qi_hip_dequantize_device", "qi_hip_pack_weights",
-                     "qi_hip_weights_create_gguf", "qi_hip_pack_gguf",
+                     "qi_hip_weights_create_gguf", "qi_hip_pack_gguf", "qi_hip_quantize",
                      "qi_hip_qwen3_create", "qi_hip_qwen3_set_embedding", "qi_hip_qwen3_set_layer",
                      "qi_hip_qwen3_set_output", "qi_hip_qwen3_set_mode", "qi_hip_kv_cache_create",
                      "qi_hip_kv_cache_length", "qi_hip_kv_cache_reset", "qi_hip_qwen3_forward",
@@ -177,6 +178,16 @@ def pack_gguf(qtype: int, layout: int, k: int, n: int, wire, legacy: bool = Fals
     _check(lib().qi_hip_pack_gguf(qtype, layout, k, n, _ptr(w), w.size, int(legacy), _ptr(out),
                                   ctypes.byref(size), ctypes.byref(f16)))
     return out, bool(f16.value)
+
+
+def quantize(qtype: int, values, storage_f16: bool = False, threads: int = 0) -> np.ndarray:
+    """Host-only: the reference quantizer's logical blocks of `values`
+    (qi_hip_quantize), optionally with f16 storage rounding of the scales."""
+    v = np.ascontiguousarray(values, dtype=np.float32).reshape(-1)
+    out = np.zeros(v.size // BLOCK_ELEMS[qtype], dtype=BLOCK_DTYPES[qtype])
+    _check(lib().qi_hip_quantize(qtype, _ptr(v), v.size, int(storage_f16), _ptr(out), out.size,
+                                 threads))
+    return out
 
 
 class Context:

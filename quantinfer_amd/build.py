@@ -23,7 +23,7 @@ CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libqi_hip.so")
 SOURCES = ["qi_abi.hip", "qi_gemv.hip", "qi_gemv_mfma.hip", "qi_gemv_rm.hip", "qi_exact.hip", "qi_gemm.hip",
-           "qi_qwen3.hip", "qi_pack.cpp"]
+           "qi_qwen3.hip", "qi_pack.cpp", "qi_quant.cpp"]
 
 ARCH = "gfx950"
 FLAGS = [

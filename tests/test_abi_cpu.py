@@ -371,3 +371,60 @@ def test_gguf_upload_errors():
     got, _ = qa.pack_gguf(qa.F32, qa.ROW_MAJOR, 3, 4, vals.tobytes())
     want, _ = qa.pack_weights(qa.F32, qa.ROW_MAJOR, 3, 4, vals)
     assert got.tobytes() == want.tobytes()
+
+
+# ------------------------------------------------------ host quantizer
+
+def _quantizer_inputs():
+    from tests.test_oracle_quantizers import _k_grid_input
+    yield "normal_outliers", po.fill_normal(0x5EED0002, 256 * 200, 0.02, 0.005, 0.2)
+    yield "k_grid", _k_grid_input()
+    yield "unit_normal", po.fill_normal(3, 256 * 40, 1.0)
+    yield "zeros_and_tiny", np.concatenate([np.zeros(256, np.float32), np.full(256, 1e-8, np.float32),
+                                            np.full(256, -3e-39, np.float32)])
+    yield "large", po.fill_normal(4, 256 * 8, 300.0)
+
+
+@pytest.mark.parametrize("qtype", ALL_Q)
+@pytest.mark.parametrize("storage_f16", [False, True])
+def test_quantize_equals_oracle_quantizer(qtype, storage_f16):
+    """qi_hip_quantize produces the oracle's (the reference quantizer's) blocks
+    byte for byte, with and without f16 storage rounding, for any thread count."""
+    for name, x in _quantizer_inputs():
+        ref = po.quantize(qtype, x)
+        if storage_f16:
+            ref = po.storage_precision(qtype, ref)
+        for threads in (1, 3, 0):
+            ours = qa.quantize(qtype, x, storage_f16=storage_f16, threads=threads)
+            assert ours.tobytes() == ref.tobytes(), (name, threads)
+
+
+@pytest.mark.parametrize("qtype", ALL_Q)
+def test_quantize_rejects_what_the_reference_rejects(qtype):
+    bs = qa.BLOCK_ELEMS[qtype]
+    x = np.ones(bs, dtype=np.float32)
+    x[3] = np.nan
+    with pytest.raises(qa.QiError) as e:
+        qa.quantize(qtype, x)
+    assert e.value.status == qa.INVALID_INPUT
+    x[3] = np.inf
+    with pytest.raises(qa.QiError):
+        qa.quantize(qtype, x)
+    # element count not a multiple of the block size; output count mismatch
+    out = np.zeros(1, qa.BLOCK_DTYPES[qtype])
+    x[3] = 1.0
+    assert qa.lib().qi_hip_quantize(qtype, x.ctypes.data, bs - 1, 0, out.ctypes.data, 0, 1) == qa.INVALID_INPUT
+    assert qa.lib().qi_hip_quantize(qtype, x.ctypes.data, bs, 0, out.ctypes.data, 2, 1) == qa.INVALID_INPUT
+    assert qa.lib().qi_hip_quantize(qtype, x.ctypes.data, bs, 0, out.ctypes.data, 1, 1) == qa.OK
+    # f32::MAX input: the K-quant super-block scale overflows f16
+    # (k_grid_tests.rs:148-155); Q8_0/Q4_0 keep f32 scales unless stored as f16
+    big = np.full(bs, np.finfo(np.float32).max, dtype=np.float32)
+    if qtype in (qa.Q4_K, qa.Q5_K, qa.Q6_K):
+        with pytest.raises(qa.QiError):
+            qa.quantize(qtype, big)
+        with pytest.raises(po.OracleError):
+            po.quantize(qtype, big)
+    else:
+        assert qa.quantize(qtype, big).tobytes() == po.quantize(qtype, big).tobytes()
+        with pytest.raises(qa.QiError):
+            qa.quantize(qtype, big, storage_f16=True)
