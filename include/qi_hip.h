@@ -196,6 +196,15 @@ qi_hip_status qi_hip_pack_gguf(int32_t qtype, int32_t layout, uint64_t k, uint64
 qi_hip_status qi_hip_quantize(int32_t qtype, const float *values, uint64_t n, int32_t storage_f16,
                               void *out, uint64_t out_count, int32_t threads);
 
+/* Host-only synthetic inputs (no counterpart in the reference; used to build
+ * benchmark weights and activations of a stated distribution): out[i] =
+ * z_i * s_i for n elements, z_i standard normal by Box-Muller from
+ * counter-based SplitMix64 draws 3i and 3i+1 of `seed`, s_i = outlier_std when
+ * draw 3i+2 (uniform on (0, 1]) is <= outlier_rate, else std. Independent of
+ * the thread count (<= 0: one per hardware thread). */
+qi_hip_status qi_hip_synth_normal(uint64_t seed, uint64_t n, double std, double outlier_rate,
+                                  double outlier_std, float *out, int32_t threads);
+
 /* ------------------------------------------------------------------------
  * GPU-resident Qwen3 dense decoder.
  *

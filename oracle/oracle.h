@@ -133,24 +133,39 @@ int qo_argmax(const float *logits, size_t n, int32_t *out);
 int qo_linear_rows(const float *x, size_t m, size_t k, const float *w, size_t n, float *y,
                    int threads);
 
+/* One projection of logical shape [k, n] as the runtime holds it: QO_F32 with
+ * `data` f32 output rows w[n][k], or the logical blocks of a quantized type in
+ * output-rows order (output n owns blocks n*(k/bs) .. +k/bs). */
+typedef struct {
+  int qtype;
+  const void *data;
+} qo_weight;
+/* qo_linear_rows on a qo_weight. For blocks, each output's weights w(k) are
+ * the dequantized values (bit-identical to the per-element value()), so this is
+ * the CpuScalar output-row matmul (backends/cpu/src/matmul.rs:282-332,
+ * 119-160) with its per-output operation sequence. */
+int qo_linear(const float *x, size_t m, size_t k, qo_weight w, size_t n, float *y, int threads);
+
 typedef struct {
   uint32_t vocab, hidden, intermediate, layers, heads, kv_heads, head_dim, max_positions;
   float eps, theta;
 } qo_qwen3_config;
 
-/* Projections are dequantized f32 output rows w[n][k]: q [heads*hd][hidden],
- * k and v [kv_heads*hd][hidden], o [hidden][heads*hd], gate and up
- * [intermediate][hidden], down [hidden][intermediate]. Norms are f32 vectors.
- * The model borrows every pointer. */
+/* Projections (qo_weight: f32 output rows or output-rows blocks) of logical
+ * shape [in, out]: q [hidden, heads*hd], k and v [hidden, kv_heads*hd],
+ * o [heads*hd, hidden], gate and up [hidden, intermediate], down
+ * [intermediate, hidden]. Norms are f32 vectors. The model borrows every
+ * pointer. */
 typedef struct {
-  const float *input_norm, *q, *k, *v, *q_norm, *k_norm, *o, *post_norm, *gate, *up, *down;
+  const float *input_norm, *q_norm, *k_norm, *post_norm;
+  qo_weight q, k, v, o, gate, up, down;
 } qo_qwen3_layer;
 
 typedef struct qo_qwen3 qo_qwen3;
-/* embedding [vocab][hidden]; head [vocab][hidden] (output rows); capacity =
+/* embedding [vocab][hidden]; head [hidden, vocab] (output rows); capacity =
  * KV cache positions. */
 qo_qwen3 *qo_qwen3_new(const qo_qwen3_config *cfg, const float *embedding,
-                       const qo_qwen3_layer *layers, const float *final_norm, const float *head,
+                       const qo_qwen3_layer *layers, const float *final_norm, qo_weight head,
                        size_t capacity, int threads);
 void qo_qwen3_free(qo_qwen3 *m);
 size_t qo_qwen3_length(const qo_qwen3 *m);

@@ -31,6 +31,11 @@ BLOCK_DTYPES = {
                     ("high_bits", "u1", (64,))]),
 }
 BLOCK_ELEMS = {Q8_0: 32, Q4_0: 32, Q4_K: 256, Q5_K: 256, Q6_K: 256}
+
+
+class _Weight(ctypes.Structure):
+    """qo_weight: a projection as f32 output rows (qtype F32) or output-rows blocks."""
+    _fields_ = [("qtype", ctypes.c_int), ("data", ctypes.c_void_p)]
 WIRE_BYTES = {Q8_0: 34, Q4_0: 18, Q4_K: 144, Q5_K: 176, Q6_K: 210}
 
 
@@ -96,7 +101,8 @@ def _declare(l: ctypes.CDLL) -> None:
     l.qo_gqa_attention.argtypes = [fp, sz, sz, sz, sz, fp, fp, sz, sz, fp]
     l.qo_argmax.argtypes = [fp, sz, vp]
     l.qo_linear_rows.argtypes = [fp, sz, sz, fp, sz, fp, i32]
-    l.qo_qwen3_new.argtypes = [vp, fp, vp, fp, fp, sz, i32]
+    l.qo_linear.argtypes = [fp, sz, sz, _Weight, sz, fp, i32]
+    l.qo_qwen3_new.argtypes = [vp, fp, vp, fp, _Weight, sz, i32]
     l.qo_qwen3_new.restype = vp
     l.qo_qwen3_free.argtypes = [vp]
     l.qo_qwen3_free.restype = None
@@ -360,33 +366,63 @@ class Qwen3Config(ctypes.Structure):
                 ("eps", ctypes.c_float), ("theta", ctypes.c_float)]
 
 
-LAYER_FIELDS = ("input_norm", "q", "k", "v", "q_norm", "k_norm", "o", "post_norm", "gate",
-                "up", "down")
+NORM_FIELDS = ("input_norm", "q_norm", "k_norm", "post_norm")
+PROJ_FIELDS = ("q", "k", "v", "o", "gate", "up", "down")
+LAYER_FIELDS = NORM_FIELDS + PROJ_FIELDS
 
 
 class _Layer(ctypes.Structure):
-    _fields_ = [(f, ctypes.c_void_p) for f in LAYER_FIELDS]
+    _fields_ = [(f, ctypes.c_void_p) for f in NORM_FIELDS] + [(f, _Weight) for f in PROJ_FIELDS]
+
+
+def _weight(w, keep: list) -> "_Weight":
+    """A projection as f32 output rows [n, k], or a (qtype, blocks) pair of
+    output-rows logical blocks."""
+    if isinstance(w, tuple):
+        qtype, blocks = w
+        b = np.ascontiguousarray(blocks)
+        if b.dtype != BLOCK_DTYPES[qtype]:
+            raise ValueError("blocks do not match the block type")
+        keep.append(b)
+        return _Weight(qtype, b.ctypes.data)
+    a = _f32(w)
+    keep.append(a)
+    return _Weight(F32, a.ctypes.data)
+
+
+def linear(x, w, n: int, threads: int = 1) -> np.ndarray:
+    """qo_linear: y[m, n] = x . w with w f32 output rows [n, k] or (qtype, blocks)."""
+    x = _f32(x)
+    m, k = x.shape
+    keep = []
+    y = np.empty((m, n), dtype=np.float32)
+    _check(lib().qo_linear(_ptr(x), m, k, _weight(w, keep), n, _ptr(y), threads), "linear")
+    return y
 
 
 class Qwen3:
-    """The oracle decoder. `layers` is a list of dicts of f32 arrays keyed by
-    LAYER_FIELDS (projections as dequantized output rows [n, k]); `head` is
-    [vocab, hidden] output rows. Arrays are kept alive by this object."""
+    """The oracle decoder. `layers` is a list of dicts keyed by LAYER_FIELDS:
+    f32 norm vectors, and projections as dequantized f32 output rows [n, k] or
+    as (qtype, blocks) pairs of output-rows logical blocks; `head` likewise
+    ([vocab, hidden] output rows). Arrays are kept alive by this object."""
 
     def __init__(self, cfg: dict, embedding, layers, final_norm, head, capacity: int,
                  threads: int = 1):
         self.cfg = Qwen3Config(**cfg)
-        self._keep = [_f32(embedding), _f32(final_norm), _f32(head)]
+        self._keep = [_f32(embedding), _f32(final_norm)]
+        head_w = _weight(head, self._keep)
         lay = (_Layer * len(layers))()
         for i, d in enumerate(layers):
-            for f in LAYER_FIELDS:
+            for f in NORM_FIELDS:
                 a = _f32(d[f])
                 self._keep.append(a)
                 setattr(lay[i], f, a.ctypes.data)
+            for f in PROJ_FIELDS:
+                setattr(lay[i], f, _weight(d[f], self._keep))
         self._layers = lay
         self.vocab = cfg["vocab"]
         h = lib().qo_qwen3_new(ctypes.byref(self.cfg), _ptr(self._keep[0]), lay,
-                               _ptr(self._keep[1]), _ptr(self._keep[2]), capacity, threads)
+                               _ptr(self._keep[1]), head_w, capacity, threads)
         if not h:
             raise OracleError("qo_qwen3_new rejected its configuration")
         self._h = h

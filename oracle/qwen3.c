@@ -20,12 +20,15 @@
  * acc = acc + x[k] * w(k) in ascending k (backends/cpu/src/matmul.rs:146-157,
  * 319-330 for output rows; :92-117 for the f32 LM head). The per-element
  * weight w(k) equals the dequantized value bit for bit (matmul.rs:162-280 vs
- * quant/src/schemes), so the model takes dequantized f32 weights, stored as
- * output rows w[n][k], and keeps that exact per-output operation sequence.
- * Several rows (or outputs) are computed side by side in vector registers
- * and outputs are split over OpenMP threads; neither changes any output's
- * operation sequence, so the result is bit-identical to the scalar loop (the
- * threading is this oracle's, not the reference's).
+ * quant/src/schemes), so a projection is given either as f32 output rows
+ * w[n][k] or as its quantized blocks, whose rows are dequantized a few at a
+ * time just before use (the 8B shape then needs its 4.6 GB of blocks, not
+ * 30 GB of f32); either way the per-output operation sequence is the same.
+ * Several rows (or outputs) are computed side by side in vector registers,
+ * and outputs (and attention's (token, head) pairs) are split over OpenMP
+ * threads; neither changes any output's operation sequence, so the result is
+ * bit-identical to the scalar loop (the threading is this oracle's, not the
+ * reference's).
  *
  * f32 functions expf, powf, cosf, sinf, sqrtf are the C library's; Rust's
  * f32::exp/powf/cos/sin lower to the same libm calls. Sums start from 0.0 and
@@ -141,20 +144,29 @@ int qo_embedding(const float *table, size_t vocab, size_t hidden, const int32_t 
 
 /* runtime/src/attention.rs:37-141. q [q_tokens][q_heads][head_dim]; keys and
  * values [key_tokens][kv_heads][head_dim]; query token t sees keys
- * 0..=start+t. */
-int qo_gqa_attention(const float *q, size_t q_tokens, size_t q_heads, size_t kv_heads,
-                     size_t head_dim, const float *keys, const float *values, size_t key_tokens,
-                     size_t start, float *out) {
+ * 0..=start+t. Every (token, head) pair is independent; they are split over
+ * `threads` OpenMP threads (bit-identical to one thread). */
+static int gqa_attention(const float *q, size_t q_tokens, size_t q_heads, size_t kv_heads,
+                         size_t head_dim, const float *keys, const float *values, size_t key_tokens,
+                         size_t start, float *out, int threads) {
   if (kv_heads == 0 || key_tokens == 0 || q_heads % kv_heads != 0) return QO_INVALID;
   if (key_tokens < start + q_tokens) return QO_INVALID;
   size_t group = q_heads / kv_heads;
   float scale = 1.0f / sqrtf((float)head_dim);
-  float *scores = (float *)malloc(key_tokens * sizeof(float));
-  if (scores == NULL) return QO_INVALID;
+  int status = QO_OK;
   memset(out, 0, q_tokens * q_heads * head_dim * sizeof(float));
-  for (size_t t = 0; t < q_tokens; ++t) {
-    size_t last = start + t;
-    for (size_t h = 0; h < q_heads; ++h) {
+#pragma omp parallel num_threads(threads < 1 ? 1 : threads)
+  {
+    float *scores = (float *)malloc(key_tokens * sizeof(float));
+    if (scores == NULL) {
+#pragma omp atomic write
+      status = QO_INVALID;
+    }
+#pragma omp for schedule(dynamic, 4)
+    for (size_t th = 0; th < q_tokens * q_heads; ++th) {
+      if (scores == NULL) continue;
+      size_t t = th / q_heads, h = th % q_heads;
+      size_t last = start + t;
       size_t g = h / group;
       const float *qv = q + (t * q_heads + h) * head_dim;
       for (size_t j = 0; j <= last; ++j) {
@@ -174,9 +186,16 @@ int qo_gqa_attention(const float *q, size_t q_tokens, size_t q_heads, size_t kv_
         for (size_t d = 0; d < head_dim; ++d) o[d] += weight * vv[d];
       }
     }
+    free(scores);
   }
-  free(scores);
-  return QO_OK;
+  return status;
+}
+
+int qo_gqa_attention(const float *q, size_t q_tokens, size_t q_heads, size_t kv_heads,
+                     size_t head_dim, const float *keys, const float *values, size_t key_tokens,
+                     size_t start, float *out) {
+  return gqa_attention(q, q_tokens, q_heads, kv_heads, head_dim, keys, values, key_tokens, start,
+                       out, 1);
 }
 
 /* generation.rs:58-76: the first index of the maximum; non-finite logits are
@@ -218,10 +237,21 @@ static void lin_rows8(const float *xt, size_t mp, size_t k, const float *w0, con
   }
 }
 
-static void lin_row1(const float *x, size_t k, const float *w, size_t n0, size_t n1, float *y) {
+/* Source of output n's weights: f32 rows are used in place; quantized rows
+ * are dequantized into `buf` (k floats) by the bit-exact dequantizer. */
+static const float *weight_row(qo_weight w, size_t k, size_t n, float *buf) {
+  if (w.qtype == QO_F32) return (const float *)w.data + n * k;
+  size_t bs = qo_block_elems(w.qtype), bb = qo_block_bytes(w.qtype);
+  qo_dequantize(w.qtype, (const uint8_t *)w.data + n * (k / bs) * bb, k / bs, buf);
+  return buf;
+}
+
+static void lin_row1(const float *x, size_t k, qo_weight w, size_t n0, size_t n1, float *buf,
+                     float *y) {
   size_t n = n0;
   for (; n + 4 <= n1; n += 4) {
-    const float *w0 = w + n * k, *w1 = w0 + k, *w2 = w1 + k, *w3 = w2 + k;
+    const float *w0 = weight_row(w, k, n, buf), *w1 = weight_row(w, k, n + 1, buf + k);
+    const float *w2 = weight_row(w, k, n + 2, buf + 2 * k), *w3 = weight_row(w, k, n + 3, buf + 3 * k);
     float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
     for (size_t i = 0; i < k; ++i) {
       a0 = a0 + x[i] * w0[i];
@@ -235,25 +265,40 @@ static void lin_row1(const float *x, size_t k, const float *w, size_t n0, size_t
     y[n + 3] = a3;
   }
   for (; n < n1; ++n) {
-    const float *wr = w + n * k;
+    const float *wr = weight_row(w, k, n, buf);
     float a = 0.0f;
     for (size_t i = 0; i < k; ++i) a = a + x[i] * wr[i];
     y[n] = a;
   }
 }
 
-int qo_linear_rows(const float *x, size_t m, size_t k, const float *w, size_t n, float *y,
-                   int threads) {
-  if (m == 0 || k == 0 || n == 0) return QO_INVALID;
+int qo_linear(const float *x, size_t m, size_t k, qo_weight w, size_t n, float *y, int threads) {
+  if (m == 0 || k == 0 || n == 0 || w.data == NULL) return QO_INVALID;
+  if (w.qtype != QO_F32) {
+    size_t bs = qo_block_elems(w.qtype);
+    if (bs == 0 || k % bs != 0) return QO_INVALID;
+  }
   int nt = threads < 1 ? 1 : threads;
+  int status = QO_OK;
   if (m == 1) {
-    size_t chunk = (n + (size_t)nt * 4 - 1) / ((size_t)nt * 4) * 4;
-#pragma omp parallel for num_threads(nt) schedule(static)
-    for (size_t c = 0; c < (n + chunk - 1) / chunk; ++c) {
-      size_t n0 = c * chunk, n1 = n0 + chunk < n ? n0 + chunk : n;
-      lin_row1(x, k, w, n0, n1, y);
+    size_t chunk = (n + (size_t)nt * 64 - 1) / ((size_t)nt * 64) * 4;
+    size_t chunks = (n + chunk - 1) / chunk;
+#pragma omp parallel num_threads(nt)
+    {
+      float *buf = (float *)malloc(4 * k * sizeof(float));
+      if (buf == NULL) {
+#pragma omp atomic write
+        status = QO_INVALID;
+      }
+#pragma omp for schedule(dynamic, 1)
+      for (size_t c = 0; c < chunks; ++c) {
+        if (buf == NULL) continue;
+        size_t n0 = c * chunk, n1 = n0 + chunk < n ? n0 + chunk : n;
+        lin_row1(x, k, w, n0, n1, buf, y);
+      }
+      free(buf);
     }
-    return QO_OK;
+    return status;
   }
   size_t mp = (m + ROWS - 1) / ROWS * ROWS;
   float *xt = (float *)calloc(mp * k, sizeof(float));
@@ -261,22 +306,38 @@ int qo_linear_rows(const float *x, size_t m, size_t k, const float *w, size_t n,
   for (size_t r = 0; r < m; ++r)
     for (size_t i = 0; i < k; ++i) xt[i * mp + r] = x[r * k + i];
   size_t groups = (n + 3) / 4;
-#pragma omp parallel for num_threads(nt) schedule(dynamic, 8)
-  for (size_t g = 0; g < groups; ++g) {
-    size_t nb = g * 4;
-    const float *wr[4];
-    for (int j = 0; j < 4; ++j) wr[j] = w + (nb + j < n ? nb + j : n - 1) * k;
-    float acc[4][ROWS];
-    for (size_t r0 = 0; r0 < m; r0 += ROWS) {
-      lin_rows8(xt + r0, mp, k, wr[0], wr[1], wr[2], wr[3], acc);
-      for (int j = 0; j < 4; ++j) {
-        if (nb + j >= n) break;
-        for (int r = 0; r < ROWS && r0 + r < m; ++r) y[(r0 + r) * n + nb + j] = acc[j][r];
+#pragma omp parallel num_threads(nt)
+  {
+    float *buf = (float *)malloc(4 * k * sizeof(float));
+    if (buf == NULL) {
+#pragma omp atomic write
+      status = QO_INVALID;
+    }
+#pragma omp for schedule(dynamic, 8)
+    for (size_t g = 0; g < groups; ++g) {
+      if (buf == NULL) continue;
+      size_t nb = g * 4;
+      const float *wr[4];
+      for (int j = 0; j < 4; ++j) wr[j] = weight_row(w, k, nb + j < n ? nb + j : n - 1, buf + j * k);
+      float acc[4][ROWS];
+      for (size_t r0 = 0; r0 < m; r0 += ROWS) {
+        lin_rows8(xt + r0, mp, k, wr[0], wr[1], wr[2], wr[3], acc);
+        for (int j = 0; j < 4; ++j) {
+          if (nb + j >= n) break;
+          for (int r = 0; r < ROWS && r0 + r < m; ++r) y[(r0 + r) * n + nb + j] = acc[j][r];
+        }
       }
     }
+    free(buf);
   }
   free(xt);
-  return QO_OK;
+  return status;
+}
+
+int qo_linear_rows(const float *x, size_t m, size_t k, const float *w, size_t n, float *y,
+                   int threads) {
+  qo_weight f = {QO_F32, w};
+  return qo_linear(x, m, k, f, n, y, threads);
 }
 
 /* ---------------------------------------------------------------- model */
@@ -286,7 +347,7 @@ struct qo_qwen3 {
   const float *embedding;
   qo_qwen3_layer *layers;
   const float *final_norm;
-  const float *head;
+  qo_weight head;
   int threads;
   size_t capacity;
   size_t length;
@@ -295,7 +356,7 @@ struct qo_qwen3 {
 };
 
 qo_qwen3 *qo_qwen3_new(const qo_qwen3_config *cfg, const float *embedding,
-                       const qo_qwen3_layer *layers, const float *final_norm, const float *head,
+                       const qo_qwen3_layer *layers, const float *final_norm, qo_weight head,
                        size_t capacity, int threads) {
   if (cfg == NULL || cfg->layers == 0 || cfg->heads == 0 || cfg->kv_heads == 0 ||
       cfg->heads % cfg->kv_heads != 0 || cfg->head_dim == 0 || cfg->head_dim % 2 != 0 ||
@@ -374,32 +435,32 @@ int qo_qwen3_forward(qo_qwen3 *m, const int32_t *tokens, size_t n, int last_only
   for (uint32_t l = 0; l < c->layers; ++l) {
     const qo_qwen3_layer *L = &m->layers[l];
     qo_rms_norm(hidden, n, H, L->input_norm, c->eps, norm);
-    qo_linear_rows(norm, n, H, L->q, QS, q, m->threads);
-    qo_linear_rows(norm, n, H, L->k, KS, k, m->threads);
-    qo_linear_rows(norm, n, H, L->v, KS, v, m->threads);
+    if (qo_linear(norm, n, H, L->q, QS, q, m->threads) != QO_OK) goto done;
+    if (qo_linear(norm, n, H, L->k, KS, k, m->threads) != QO_OK) goto done;
+    if (qo_linear(norm, n, H, L->v, KS, v, m->threads) != QO_OK) goto done;
     qo_rms_norm(q, n * c->heads, hd, L->q_norm, c->eps, q);
     qo_rms_norm(k, n * c->kv_heads, hd, L->k_norm, c->eps, k);
     qo_apply_rope(q, n, c->heads, hd, cs, sn, n, q);
     qo_apply_rope(k, n, c->kv_heads, hd, cs, sn, n, k);
     memcpy(m->keys[l] + start * KS, k, n * KS * sizeof(float));
     memcpy(m->values[l] + start * KS, v, n * KS * sizeof(float));
-    if (qo_gqa_attention(q, n, c->heads, c->kv_heads, hd, m->keys[l], m->values[l], start + n,
-                         start, att) != QO_OK)
+    if (gqa_attention(q, n, c->heads, c->kv_heads, hd, m->keys[l], m->values[l], start + n,
+                      start, att, m->threads) != QO_OK)
       goto done;
-    qo_linear_rows(att, n, QS, L->o, H, proj, m->threads);
+    if (qo_linear(att, n, QS, L->o, H, proj, m->threads) != QO_OK) goto done;
     add_into(hidden, proj, n * H);
     qo_rms_norm(hidden, n, H, L->post_norm, c->eps, norm);
-    qo_linear_rows(norm, n, H, L->gate, I, gate, m->threads);
-    qo_linear_rows(norm, n, H, L->up, I, up, m->threads);
+    if (qo_linear(norm, n, H, L->gate, I, gate, m->threads) != QO_OK) goto done;
+    if (qo_linear(norm, n, H, L->up, I, up, m->threads) != QO_OK) goto done;
     qo_silu_mul(gate, up, n * I, gate);
-    qo_linear_rows(gate, n, I, L->down, H, proj, m->threads);
+    if (qo_linear(gate, n, I, L->down, H, proj, m->threads) != QO_OK) goto done;
     add_into(hidden, proj, n * H);
   }
   m->length = start + n;
   {
     size_t first = last_only ? n - 1 : 0, rows = n - first;
     qo_rms_norm(hidden + first * H, rows, H, m->final_norm, c->eps, norm);
-    qo_linear_rows(norm, rows, H, m->head, c->vocab, logits, m->threads);
+    if (qo_linear(norm, rows, H, m->head, c->vocab, logits, m->threads) != QO_OK) goto done;
   }
   status = QO_OK;
 done:

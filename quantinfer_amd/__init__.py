@@ -110,6 +110,8 @@ def lib() -> ctypes.CDLL:
         l.qi_hip_pack_gguf.argtypes = [i32, i32, u64, u64, vp, u64, i32, vp, ctypes.POINTER(u64),
                                        ctypes.POINTER(i32)]
         l.qi_hip_quantize.argtypes = [i32, vp, u64, i32, vp, u64, i32]
+        l.qi_hip_synth_normal.argtypes = [u64, u64, ctypes.c_double, ctypes.c_double, ctypes.c_double,
+                                          vp, i32]
         u32 = ctypes.c_uint32
         l.qi_hip_qwen3_create.argtypes = [vp, ctypes.POINTER(Qwen3Config), ctypes.POINTER(vp)]
         l.qi_hip_qwen3_set_embedding.argtypes = [vp, vp]
@@ -129,7 +131,7 @@ def lib() -> ctypes.CDLL:
         for name in ("qi_hip_open", "qi_hip_device_name", "qi_hip_weights_create",
                      "qi_hip_weights_info_get", "qi_hip_linear", "qi_hip_linear_device",
                      "qi_hip_dequantize", "qi_hip_dequantize_device", "qi_hip_pack_weights",
-                     "qi_hip_weights_create_gguf", "qi_hip_pack_gguf", "qi_hip_quantize",
+                     "qi_hip_weights_create_gguf", "qi_hip_pack_gguf", "qi_hip_quantize", "qi_hip_synth_normal",
                      "qi_hip_qwen3_create", "qi_hip_qwen3_set_embedding", "qi_hip_qwen3_set_layer",
                      "qi_hip_qwen3_set_output", "qi_hip_qwen3_set_mode", "qi_hip_kv_cache_create",
                      "qi_hip_kv_cache_length", "qi_hip_kv_cache_reset", "qi_hip_qwen3_forward",
@@ -187,6 +189,15 @@ def quantize(qtype: int, values, storage_f16: bool = False, threads: int = 0) ->
     out = np.zeros(v.size // BLOCK_ELEMS[qtype], dtype=BLOCK_DTYPES[qtype])
     _check(lib().qi_hip_quantize(qtype, _ptr(v), v.size, int(storage_f16), _ptr(out), out.size,
                                  threads))
+    return out
+
+
+def synth_normal(seed: int, n: int, std: float = 1.0, outlier_rate: float = 0.0,
+                 outlier_std: float = 0.0, threads: int = 0) -> np.ndarray:
+    """Host-only seeded synthetic values (qi_hip_synth_normal): N(0, std^2), a
+    fraction `outlier_rate` drawn with outlier_std instead."""
+    out = np.empty(n, dtype=np.float32)
+    _check(lib().qi_hip_synth_normal(seed, n, std, outlier_rate, outlier_std, _ptr(out), threads))
     return out
 
 

@@ -1,11 +1,12 @@
 // C ABI of the MI355X quantized-linear backend (include/qi_hip.h).
 //
-// The context owns one HIP stream (default priority), a split-K workspace
-// (partial sums + per-row-tile tickets, zeroed once at open) and grow-only
-// staging buffers for the synchronous host entry points. A mutex serializes
-// calls on one context; device-side work of two calls on one context must not
-// overlap (they share the workspace), which holds for every entry point here
-// because each enqueues on a single stream.
+// The context owns one HIP stream (default priority), grow-only device
+// workspaces (f16 activations and split-K partials of the prefill GEMM, the
+// activation records of the multi-row GEMV) and the staging buffers of the
+// synchronous host entry point. A mutex serializes calls on one context.
+// Calls may enqueue on different caller streams; the device work of calls
+// that use a workspace is ordered by an event (ws_before / ws_after), so two
+// such calls never use a workspace at the same time.
 #include <hip/hip_runtime.h>
 #include <stdlib.h>
 #include <string.h>
@@ -37,10 +38,35 @@ qi_hip_status hip_fail(hipError_t e, const char* what) {
 }
 
 
-constexpr uint64_t kPartialsFloats = 8ull << 20;  // 32 MiB of split-K partials
-constexpr uint64_t kTickets = 1ull << 20;
-
 uint64_t workspace_version() { return g_ws_version.load(std::memory_order_relaxed); }
+
+bool capturing(hipStream_t st) {
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  return hipStreamIsCapturing(st, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone;
+}
+
+qi_hip_status ws_before(qi_hip_ctx* c, hipStream_t st) {
+  // A stream under capture records only its own work; the decoder captures
+  // on the context stream after an eager step, so nothing else is pending.
+  if (!c->ws_used || c->ws_stream == st || capturing(st)) return QI_HIP_OK;
+  QI_HIP_TRY(hipStreamWaitEvent(st, c->ws_event, 0), "order workspace use across streams");
+  return QI_HIP_OK;
+}
+
+qi_hip_status ws_after(qi_hip_ctx* c, hipStream_t st) {
+  if (capturing(st)) return QI_HIP_OK;
+  QI_HIP_TRY(hipEventRecord(c->ws_event, st), "record workspace use");
+  c->ws_stream = st;
+  c->ws_used = true;
+  return QI_HIP_OK;
+}
+
+// Wait until no queued work uses a workspace (before one is reallocated).
+qi_hip_status ws_drain(qi_hip_ctx* c, hipStream_t st) {
+  if (c->ws_used) QI_HIP_TRY(hipEventSynchronize(c->ws_event), "wait for workspace users");
+  QI_HIP_TRY(hipStreamSynchronize(st), "synchronize before growing a workspace");
+  return QI_HIP_OK;
+}
 
 qi_hip_status grow(float** buf, uint64_t* cap, uint64_t need, const char* what) {
   if (need <= *cap) return QI_HIP_OK;
@@ -66,24 +92,13 @@ qi_hip_status grow_pinned(float** buf, uint64_t* cap, uint64_t need) {
   return QI_HIP_OK;
 }
 
-qi_hip_status ensure_tickets(qi_hip_ctx* c, uint64_t need) {
-  if (need <= c->tickets_cap) return QI_HIP_OK;
-  QI_HIP_TRY(hipStreamSynchronize(c->stream), "synchronize before growing tickets");
-  if (c->tickets) (void)hipFree(c->tickets);
-  c->tickets = nullptr;
-  c->tickets_cap = 0;
-  QI_HIP_TRY(hipMalloc(reinterpret_cast<void**>(&c->tickets), need * sizeof(uint32_t)), "alloc tickets");
-  QI_HIP_TRY(hipMemset(c->tickets, 0, need * sizeof(uint32_t)), "zero tickets");
-  QI_HIP_TRY(hipDeviceSynchronize(), "zero tickets");
-  c->tickets_cap = need;
-  return QI_HIP_OK;
-}
-
 void ctx_destroy(qi_hip_ctx* c) {
   (void)hipSetDevice(c->device);
   if (c->stream) (void)hipStreamSynchronize(c->stream);
-  if (c->partials) (void)hipFree(c->partials);
-  if (c->tickets) (void)hipFree(c->tickets);
+  if (c->ws_event) {
+    if (c->ws_used) (void)hipEventSynchronize(c->ws_event);
+    (void)hipEventDestroy(c->ws_event);
+  }
   if (c->xbuf) (void)hipFree(c->xbuf);
   if (c->ybuf) (void)hipFree(c->ybuf);
   if (c->hx) (void)hipHostFree(c->hx);
@@ -109,6 +124,15 @@ qi_hip_status check_call(qi_hip_ctx* ctx, const qi_hip_weights* w, uint64_t m) {
   return QI_HIP_OK;
 }
 
+// Grow workspace `buf` to `need` floats, after every queued user is done.
+qi_hip_status grow_ws(qi_hip_ctx* c, hipStream_t st, float** buf, uint64_t* cap, uint64_t need,
+                      const char* what) {
+  if (need <= *cap) return QI_HIP_OK;
+  qi_hip_status s = ws_drain(c, st);
+  if (s != QI_HIP_OK) return s;
+  return grow(buf, cap, need, what);
+}
+
 qi_hip_status run_linear(qi_hip_ctx* c, const qi_hip_weights* w, const float* x, uint64_t m,
                          float* y, int32_t mode, hipStream_t st, float* silu_act, bool* silu_done) {
   if (silu_done != nullptr) *silu_done = false;
@@ -120,19 +144,19 @@ qi_hip_status run_linear(qi_hip_ctx* c, const qi_hip_weights* w, const float* x,
   if (mode == QI_HIP_MODE_MFMA) {
     if (!qi::gemm_supported(im.qtype, im.layout, im.k, im.n))
       return fail(QI_HIP_UNSUPPORTED, "MFMA GEMM does not support this weight type/layout/shape");
+    if (!im.f16_gemm)
+      return fail(QI_HIP_UNSUPPORTED,
+                  "MFMA GEMM: the weight values or scales lie outside the range f16 operands hold");
     use_gemm = true;
   } else if (mode == QI_HIP_MODE_AUTO) {
-    use_gemm = m >= 128 && qi::gemm_supported(im.qtype, im.layout, im.k, im.n);
+    use_gemm = m >= 128 && im.f16_gemm && qi::gemm_supported(im.qtype, im.layout, im.k, im.n);
   }
+  qi_hip_status s = QI_HIP_OK;
   if (use_gemm) {
     const uint64_t m_pad = qi::gemm_padded_rows(m);
     const uint64_t halves = m_pad * im.k;
-    if (halves > c->hcap * 2) {
-      // the workspace may still be read by queued work of this context
-      QI_HIP_TRY(hipStreamSynchronize(st), "synchronize before growing the GEMM workspace");
-      qi_hip_status s = grow(&c->hbuf, &c->hcap, (halves + 1) / 2, "alloc GEMM workspace");
-      if (s != QI_HIP_OK) return s;
-    }
+    if ((s = grow_ws(c, st, &c->hbuf, &c->hcap, (halves + 1) / 2, "alloc GEMM workspace")) != QI_HIP_OK)
+      return s;
     qi::GemmArgs ga{v, x, y, m, reinterpret_cast<_Float16*>(c->hbuf), m_pad};
     ga.splits = qi::gemm_splits(im, m);
     if (silu_act != nullptr && silu_done != nullptr && ga.splits == 1 && qi::gemm_silu_supported(im)) {
@@ -141,15 +165,13 @@ qi_hip_status run_linear(qi_hip_ctx* c, const qi_hip_weights* w, const float* x,
     }
     if (ga.splits > 1) {
       const uint64_t need = ga.splits * m_pad * im.n;
-      if (need > c->scap) {
-        QI_HIP_TRY(hipStreamSynchronize(st), "synchronize before growing the GEMM workspace");
-        qi_hip_status s = grow(&c->sbuf, &c->scap, need, "alloc GEMM split-K workspace");
-        if (s != QI_HIP_OK) return s;
-      }
+      if ((s = grow_ws(c, st, &c->sbuf, &c->scap, need, "alloc GEMM split-K workspace")) != QI_HIP_OK)
+        return s;
       ga.part = c->sbuf;
     }
+    if ((s = ws_before(c, st)) != QI_HIP_OK) return s;
     QI_HIP_TRY(qi::launch_gemm(im, ga, st), "launch gemm");
-    return QI_HIP_OK;
+    return ws_after(c, st);
   }
   if (mode != QI_HIP_MODE_EXACT && qi::gemv_rm_supported(im)) {
     // row-major weights: the blocks-along-N GEMV, 4 rows per launch
@@ -157,11 +179,9 @@ qi_hip_status run_linear(qi_hip_ctx* c, const qi_hip_weights* w, const float* x,
     const uint32_t splits = qi::gemv_rm_splits(im, chunk);
     if (splits > 1) {
       const uint64_t need = static_cast<uint64_t>(splits) * chunk * im.n;
-      if (need > c->scap) {
-        QI_HIP_TRY(hipStreamSynchronize(st), "synchronize before growing the GEMV workspace");
-        qi_hip_status s = grow(&c->sbuf, &c->scap, need, "alloc row-major GEMV workspace");
-        if (s != QI_HIP_OK) return s;
-      }
+      if ((s = grow_ws(c, st, &c->sbuf, &c->scap, need, "alloc row-major GEMV workspace")) != QI_HIP_OK)
+        return s;
+      if ((s = ws_before(c, st)) != QI_HIP_OK) return s;
     }
     for (uint64_t m0 = 0; m0 < m; m0 += 4) {
       const uint32_t rows = static_cast<uint32_t>(m - m0 < 4 ? m - m0 : 4);
@@ -171,28 +191,29 @@ qi_hip_status run_linear(qi_hip_ctx* c, const qi_hip_weights* w, const float* x,
                                     sp <= splits ? sp : splits, st),
                  "launch row-major gemv");
     }
-    return QI_HIP_OK;
+    return splits > 1 ? ws_after(c, st) : QI_HIP_OK;
   }
-  const bool fast = mode != QI_HIP_MODE_EXACT && im.qtype != qi::kF32 &&
-                    im.layout == qi::kOutputRows;
-  if (!fast) {
+  const bool mfma = mode != QI_HIP_MODE_EXACT && qi::gemv_mfma_supported(im.qtype, im.layout, im.k);
+  const bool planar = mode != QI_HIP_MODE_EXACT && !mfma && qi::gemv_supported(im.qtype, im.layout, im.k);
+  if (!mfma && !planar) {
     QI_HIP_TRY(qi::launch_exact(im, v, x, m, y, st), "launch exact matmul");
     return QI_HIP_OK;
   }
-  const bool mfma = qi::gemv_mfma_supported(im.qtype, im.layout, im.k);
+  // two or more rows: activation records built once per 16-row chunk into
+  // the context workspace
+  const bool records = mfma && m >= 2;
+  if (records) {
+    const uint32_t rows = static_cast<uint32_t>(m < 16 ? m : 16);
+    const uint64_t need = (qi::gemv_digits_bytes(im.k, rows) + 3) / 4;
+    if ((s = grow_ws(c, st, &c->dbuf, &c->dcap, need, "alloc GEMV workspace")) != QI_HIP_OK) return s;
+    if ((s = ws_before(c, st)) != QI_HIP_OK) return s;
+  }
   for (uint64_t m0 = 0; m0 < m; m0 += 16) {
     const int rows = static_cast<int>(m - m0 < 16 ? m - m0 : 16);
     const int mt = rows == 1 ? 1 : rows == 2 ? 2 : rows <= 4 ? 4 : rows <= 8 ? 8 : 16;
     if (mfma) {
       qi::GemvMfmaArgs ga{v, x + m0 * im.k, y + m0 * im.n, rows};
       if (rows >= 2) {
-        // activation records built once for the whole call
-        const uint64_t need = (qi::gemv_digits_bytes(im.k, static_cast<uint32_t>(rows)) + 3) / 4;
-        if (need > c->dcap) {
-          QI_HIP_TRY(hipStreamSynchronize(st), "synchronize before growing the GEMV workspace");
-          qi_hip_status s = grow(&c->dbuf, &c->dcap, need, "alloc GEMV workspace");
-          if (s != QI_HIP_OK) return s;
-        }
         QI_HIP_TRY(qi::launch_gemv_digits(im.qtype, ga.x, im.k, static_cast<uint32_t>(rows),
                                           reinterpret_cast<uint8_t*>(c->dbuf), st),
                    "launch gemv activation records");
@@ -202,22 +223,10 @@ qi_hip_status run_linear(qi_hip_ctx* c, const qi_hip_weights* w, const float* x,
       QI_HIP_TRY(qi::launch_gemv_mfma(im.qtype, im.wide != 0, mt, split, ga, st), "launch gemv");
       continue;
     }
-    qi::GemvPlan plan = qi::plan_gemv(im.qtype, im.k, im.n, mt, c->partials_cap);
-    if (plan.splits > 1) {
-      qi_hip_status s = ensure_tickets(c, plan.row_tiles);
-      if (s != QI_HIP_OK) return s;
-    }
-    qi::GemvArgs ga;
-    ga.w = v;
-    ga.x = x + m0 * im.k;
-    ga.y = y + m0 * im.n;
-    ga.m = rows;
-    ga.slots_per_split = plan.slots_per_split;
-    ga.partials = c->partials;
-    ga.tickets = c->tickets;
-    QI_HIP_TRY(qi::launch_gemv(im.qtype, im.wide != 0, mt, ga, plan, st), "launch gemv");
+    qi::GemvArgs ga{v, x + m0 * im.k, y + m0 * im.n, rows};
+    QI_HIP_TRY(qi::launch_gemv(im.qtype, im.wide != 0, mt, ga, st), "launch gemv");
   }
-  return QI_HIP_OK;
+  return records ? ws_after(c, st) : QI_HIP_OK;
 }
 
 qi_hip_status create_weights_locked(qi_hip_ctx* c, const Image& im, const void* blocks,
@@ -283,16 +292,7 @@ qi_hip_status qi_hip_open(int32_t device, qi_hip_ctx** out) {
   if (const char* env = getenv("QI_HIP_GEMV_SPLIT")) c->gemv_split = atoi(env);
   c->name = prop.name[0] ? std::string(prop.name) : std::string("AMD ") + prop.gcnArchName;
   e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
-  if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&c->partials), kPartialsFloats * 4);
-  if (e == hipSuccess) {
-    c->partials_cap = kPartialsFloats;
-    e = hipMalloc(reinterpret_cast<void**>(&c->tickets), kTickets * 4);
-  }
-  if (e == hipSuccess) {
-    c->tickets_cap = kTickets;
-    e = hipMemset(c->tickets, 0, kTickets * 4);
-  }
-  if (e == hipSuccess) e = hipDeviceSynchronize();
+  if (e == hipSuccess) e = hipEventCreateWithFlags(&c->ws_event, hipEventDisableTiming);
   if (e != hipSuccess) {
     ctx_destroy(c);
     return hip_fail(e, "context setup");

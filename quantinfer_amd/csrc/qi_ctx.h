@@ -21,10 +21,14 @@ struct qi_hip_ctx {
   hipStream_t stream = nullptr;
   std::mutex mu;
   std::string name;
-  float* partials = nullptr;
-  uint64_t partials_cap = 0;  // floats
-  uint32_t* tickets = nullptr;
-  uint64_t tickets_cap = 0;
+  // Order of work that uses the workspaces below (hbuf, sbuf, dbuf): calls
+  // may enqueue on different caller streams, so the launches of a call that
+  // uses a workspace wait (hipStreamWaitEvent) for ws_event, recorded after
+  // the previous such call's launches on ws_stream. A workspace is
+  // reallocated only after ws_event has completed.
+  hipEvent_t ws_event = nullptr;
+  hipStream_t ws_stream = nullptr;
+  bool ws_used = false;
   float* xbuf = nullptr;
   uint64_t xcap = 0;  // floats
   float* ybuf = nullptr;
@@ -77,6 +81,11 @@ void ctx_release(qi_hip_ctx* c);
 // Number of workspace reallocations so far (any context): a captured graph
 // that reads a workspace is stale once this changes.
 uint64_t workspace_version();
+// Before enqueueing work that uses a context workspace on `st`: make st wait
+// for the previous workspace user (another stream). After enqueueing it:
+// record it as the last user. No-ops while st is under graph capture.
+qi_hip_status ws_before(qi_hip_ctx* c, hipStream_t st);
+qi_hip_status ws_after(qi_hip_ctx* c, hipStream_t st);
 
 }  // namespace qi_abi
 

@@ -201,6 +201,39 @@ struct Exact<kQ6_K, WIDE> {
   }
 };
 
+// The CpuScalar sum of output n for one activation row x (k elements):
+// acc = acc + x[k] * w(k) in f32, k ascending, no FMA (backends/cpu/src/
+// matmul.rs:146-157, 319-330 output rows; :25-31 row major). The fast
+// kernels call it for an output whose fast result is not finite: a NaN or
+// infinite activation (or an overflow) then yields exactly the reference's
+// value, where the fast arithmetic (digit splits, affine pieces, f16
+// operands) cannot reproduce which outputs are NaN and which +-Inf.
+template <int QT, bool WIDE>
+__device__ __forceinline__ float exact_output_row(const View& w, const float* x, uint64_t n) {
+  constexpr uint32_t bs = (QT == kQ8_0 || QT == kQ4_0) ? 32 : 256;
+  float sum = 0.0f;
+  for (uint32_t b = 0; b < w.nb; ++b) {
+    const BlockLoc L = locate<QT>(w, n, b);
+    const float* lb = x + static_cast<uint64_t>(b) * bs;
+    // (a partial unroll: where n is wave-uniform, a full one would load a
+    // whole block through scalar registers)
+#pragma unroll 8
+    for (uint32_t l = 0; l < bs; ++l) sum += lb[l] * Exact<QT, WIDE>::value(w, L, l);
+  }
+  return sum;
+}
+
+template <int QT, bool WIDE>
+__device__ __forceinline__ float exact_row_major_col(const View& w, const float* x, uint64_t n) {
+  constexpr uint32_t bs = (QT == kQ8_0 || QT == kQ4_0) ? 32 : 256;
+  float sum = 0.0f;
+  for (uint64_t k = 0; k < w.k; ++k) {
+    const uint64_t f = k * w.n + n;  // flat index of element (k, n)
+    sum += x[k] * Exact<QT, WIDE>::value(w, locate<QT>(w, 0, f / bs), static_cast<uint32_t>(f % bs));
+  }
+  return sum;
+}
+
 // ---------------------------------------------------------------------------
 // Fast-path slot decoders (GEMV). A slot is the unit one lane handles per
 // output row: 32 elements (Q8_0/Q4_0: one block) or 64 elements (K-quants:

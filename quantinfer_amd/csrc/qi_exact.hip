@@ -48,15 +48,7 @@ __global__ __launch_bounds__(256) void exact_output_rows_kernel(View w, const fl
   const uint64_t n = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   const uint64_t r = blockIdx.y;
   if (n >= w.n || r >= m) return;
-  constexpr uint32_t bs = (QT == kQ8_0 || QT == kQ4_0) ? 32 : 256;
-  const float* left = x + r * w.k;
-  float sum = 0.0f;
-  for (uint32_t b = 0; b < w.nb; ++b) {
-    const BlockLoc L = locate<QT>(w, n, b);
-    const float* lb = left + static_cast<uint64_t>(b) * bs;
-    for (uint32_t l = 0; l < bs; ++l) sum += lb[l] * Exact<QT, WIDE>::value(w, L, l);
-  }
-  y[r * w.n + n] = sum;
+  y[r * w.n + n] = exact_output_row<QT, WIDE>(w, x + r * w.k, n);
 }
 
 // --------------------------------------------------------- exact: row major
@@ -67,14 +59,7 @@ __global__ __launch_bounds__(256) void exact_row_major_kernel(View w, const floa
   const uint64_t n = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   const uint64_t r = blockIdx.y;
   if (n >= w.n || r >= m) return;
-  constexpr uint32_t bs = (QT == kQ8_0 || QT == kQ4_0) ? 32 : 256;
-  const float* left = x + r * w.k;
-  float sum = 0.0f;
-  for (uint64_t k = 0; k < w.k; ++k) {
-    const uint64_t f = k * w.n + n;  // flat index of element (k, n)
-    sum += left[k] * Exact<QT, WIDE>::value(w, locate<QT>(w, 0, f / bs), static_cast<uint32_t>(f % bs));
-  }
-  y[r * w.n + n] = sum;
+  y[r * w.n + n] = exact_row_major_col<QT, WIDE>(w, x + r * w.k, n);
 }
 
 // ------------------------------------------------------------------ F32 W

@@ -112,6 +112,23 @@ __device__ __forceinline__ h8 weight_fragment(long codes, float a, float b) {
   }
 }
 
+// Outputs of a lane's tile whose f16 result is not finite (a NaN or infinite
+// activation, |x| beyond f16's range) are recomputed in the reference's order
+// (exact_output_row), which decides which are NaN and which +-Inf. The lane
+// owns rows row0 + 16 rt + r (rt < rts, r < 4) of columns col0 + 16 ct
+// (ct < 4); its values are already stored in y.
+template <int QT, bool WIDE>
+__device__ __forceinline__ void gemm_fix_nonfinite(const GemmArgs& a, uint64_t row0, int rts, uint64_t col0) {
+#pragma unroll 1
+  for (int i = 0; i < 16 * rts; ++i) {
+    const uint64_t n = col0 + 16 * static_cast<uint64_t>(i / (4 * rts));
+    const uint64_t m = row0 + 16 * static_cast<uint64_t>((i / 4) % rts) + (i % 4);
+    if (n >= a.w.n || m >= a.m) continue;
+    float* const p = a.y + m * a.w.n + n;
+    if (!__builtin_isfinite(*p)) *p = exact_output_row<QT, WIDE>(a.w, a.x + m * a.w.k, n);
+  }
+}
+
 // SiLU-pairs epilogue of a 128-row block (GemmArgs::act): lane (g, c16) holds
 // acc[rt][ct][r], row m0 + 16 rt + 4 g + r of output tile tile0 + ct, column
 // c16; columns c16 and c16 ^ 8 are a gate and its up value. The two lanes of
@@ -235,6 +252,7 @@ __global__ __launch_bounds__(512) void gemm_ws_kernel(GemmArgs a) {
     // C[i][j]: lane j + 16 (i / 4), element i % 4
     const uint64_t ld = a.w.n;
     float* yrow = a.y + (m0 + 4 * g) * ld;
+    bool bad = false;
 #pragma unroll
     for (int ct = 0; ct < 4; ++ct) {
       const uint64_t n = static_cast<uint64_t>((blockIdx.x * 4 + wave) * 4 + ct) * 16 + c16;
@@ -244,10 +262,14 @@ __global__ __launch_bounds__(512) void gemm_ws_kernel(GemmArgs a) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const uint64_t m = m0 + rt * 16 + 4 * g + r;
-          if (m < a.m) yrow[(rt * 16 + r) * ld + n] = acc[rt][ct][r];
+          if (m < a.m) {
+            yrow[(rt * 16 + r) * ld + n] = acc[rt][ct][r];
+            bad |= !__builtin_isfinite(acc[rt][ct][r]);
+          }
         }
       }
     }
+    if (bad) gemm_fix_nonfinite<QT, WIDE>(a, m0 + 4 * g, 8, static_cast<uint64_t>((blockIdx.x * 4 + wave) * 4) * 16 + c16);
     return;
   }
 
@@ -543,6 +565,7 @@ __global__ __launch_bounds__(256) void gemm_reg_kernel(GemmArgs a) {
   const uint64_t ld = a.w.n;
   float* const out = a.splits > 1 ? a.part + static_cast<uint64_t>(blockIdx.z) * a.m_pad * ld : a.y;
   float* yrow = out + (m0 + 16 * rt0 + 4 * g) * ld;
+  bool bad = false;
 #pragma unroll
   for (int ct = 0; ct < 4; ++ct) {
     const uint64_t n = static_cast<uint64_t>((blockIdx.x * 4 + cw) * 4 + ct) * 16 + c16;
@@ -552,10 +575,17 @@ __global__ __launch_bounds__(256) void gemm_reg_kernel(GemmArgs a) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const uint64_t m = m0 + 16 * (rt0 + rt) + 4 * g + r;
-        if (m < a.m) yrow[(rt * 16 + r) * ld + n] = acc[rt][ct][r];
+        if (m < a.m) {
+          yrow[(rt * 16 + r) * ld + n] = acc[rt][ct][r];
+          bad |= !__builtin_isfinite(acc[rt][ct][r]);
+        }
       }
     }
   }
+  // with a K split the partial sums are checked by gemm_splitk_sum_kernel
+  if (bad && a.splits == 1)
+    gemm_fix_nonfinite<QT, WIDE>(a, m0 + 16 * rt0 + 4 * g, RT,
+                                 static_cast<uint64_t>((blockIdx.x * 4 + cw) * 4) * 16 + c16);
 }
 
 // s_waitcnt with vmcnt <= n (0..63) and lgkmcnt 0 (gfx9 encoding: vmcnt in
@@ -843,6 +873,7 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(GemmArgs a) {
   const uint64_t ld = a.w.n;
   float* const out = a.splits > 1 ? a.part + static_cast<uint64_t>(blockIdx.z) * a.m_pad * ld : a.y;
   float* yrow = out + (m0 + 4 * g) * ld;
+  bool bad = false;
 #pragma unroll
   for (int ct = 0; ct < 4; ++ct) {
     const uint64_t n = static_cast<uint64_t>((blockIdx.x * 4 + wave) * 4 + ct) * 16 + c16;
@@ -852,20 +883,30 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(GemmArgs a) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const uint64_t m = m0 + 16 * rt + 4 * g + r;
-        if (m < a.m) yrow[(rt * 16 + r) * ld + n] = acc[rt][ct][r];
+        if (m < a.m) {
+          yrow[(rt * 16 + r) * ld + n] = acc[rt][ct][r];
+          bad |= !__builtin_isfinite(acc[rt][ct][r]);
+        }
       }
     }
   }
+  // with a K split the partial sums are checked by gemm_splitk_sum_kernel
+  if (bad && a.splits == 1)
+    gemm_fix_nonfinite<QT, false>(a, m0 + 4 * g, RT, static_cast<uint64_t>((blockIdx.x * 4 + wave) * 4) * 16 + c16);
 }
 
-// y = sum of the split-K partial products, in split order (deterministic).
+// y = sum of the split-K partial products, in split order (deterministic);
+// a sum that is not finite is recomputed in the reference's order.
+template <int QT, bool WIDE>
 __global__ __launch_bounds__(256) void gemm_splitk_sum_kernel(const float* __restrict__ part, uint32_t splits,
                                                               uint64_t count, uint64_t stride,
-                                                              float* __restrict__ y) {
+                                                              float* __restrict__ y, View w,
+                                                              const float* __restrict__ x) {
   const uint64_t i = static_cast<uint64_t>(blockIdx.x) * 256 + threadIdx.x;
   if (i >= count) return;
   float v = part[i];
   for (uint32_t s = 1; s < splits; ++s) v += part[s * stride + i];
+  if (!__builtin_isfinite(v)) v = exact_output_row<QT, WIDE>(w, x + (i / w.n) * w.k, i % w.n);
   y[i] = v;
 }
 
@@ -881,8 +922,8 @@ hipError_t launch_reg(const Image& im, const GemmArgs& a, hipStream_t st) {
   if (e != hipSuccess || a.splits == 1) return e;
   // rows of y and of each partial block share the row stride n
   const uint64_t count = a.m * im.n;
-  hipLaunchKernelGGL(gemm_splitk_sum_kernel, dim3(static_cast<uint32_t>((count + 255) / 256)), dim3(256), 0, st,
-                     a.part, a.splits, count, a.m_pad * im.n, a.y);
+  hipLaunchKernelGGL((gemm_splitk_sum_kernel<QT, WIDE>), dim3(static_cast<uint32_t>((count + 255) / 256)),
+                     dim3(256), 0, st, a.part, a.splits, count, a.m_pad * im.n, a.y, a.w, a.x);
   return hipGetLastError();
 }
 
@@ -900,8 +941,8 @@ hipError_t launch_lds(const Image& im, const GemmArgs& a, hipStream_t st) {
   e = hipGetLastError();
   if (e != hipSuccess || a.splits == 1) return e;
   const uint64_t count = a.m * im.n;
-  hipLaunchKernelGGL(gemm_splitk_sum_kernel, dim3(static_cast<uint32_t>((count + 255) / 256)), dim3(256), 0, st,
-                     a.part, a.splits, count, a.m_pad * im.n, a.y);
+  hipLaunchKernelGGL((gemm_splitk_sum_kernel<QT, false>), dim3(static_cast<uint32_t>((count + 255) / 256)),
+                     dim3(256), 0, st, a.part, a.splits, count, a.m_pad * im.n, a.y, a.w, a.x);
   return hipGetLastError();
 }
 

@@ -114,10 +114,15 @@ __device__ __forceinline__ void store_half(const HalfX& o, const Item& it, bool 
   }
   mx = fmaxf(mx, __shfl_xor(mx, 1));
   const float other = __shfl_xor(sum, 1);
+  // A NaN or infinite activation makes the window sum non-finite. Its scale
+  // is then NaN, so every output of the row comes out NaN and the GEMV's
+  // epilogue recomputes it in the reference's order; the digits are built
+  // from zeros (no float-to-int conversion of a non-finite value).
+  const bool finite = __builtin_isfinite(sum + other);
   // 2^s with max|x| * 2^s < 2^29: F = rint(x * 2^s) keeps 30 bits with headroom
-  const int e = mx > 0.0f ? __builtin_amdgcn_frexp_expf(mx) : 0;
+  const int e = finite && mx > 0.0f ? __builtin_amdgcn_frexp_expf(mx) : 0;
   const int sh = 29 - e;
-  const float inv = mx > 0.0f ? ldexpf(1.0f, e - 29) : 0.0f;
+  const float inv = !finite ? __builtin_nanf("") : mx > 0.0f ? ldexpf(1.0f, e - 29) : 0.0f;
   if (!valid) return;
   const uint32_t t0 = 4 * it.h + 2 * it.half;
   uint8_t* const rec = recs + (static_cast<uint64_t>(it.m) * cu + it.u) * kUnitRecBytes;
@@ -127,7 +132,7 @@ __device__ __forceinline__ void store_half(const HalfX& o, const Item& it, bool 
     uint32_t dig[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const int F = static_cast<int>(rintf(ldexpf(xs[8 * tt + j], sh)));
+      const int F = finite ? static_cast<int>(rintf(ldexpf(xs[8 * tt + j], sh))) : 0;
       // signed base-256 digits: byte i of (F + 0x808080) ^ 0x808080
       dig[j] = (static_cast<uint32_t>(F) + 0x00808080u) ^ 0x00808080u;
     }
@@ -384,6 +389,8 @@ __global__ __launch_bounds__(64 * SW * WC) void gemv_mfma_kernel(GemvMfmaArgs a)
     }
   }
   if (sw == 0 && g == 0 && n_out < a.w.n) {
+    [[maybe_unused]] uint32_t bad = 0;  // rows whose result is not finite
+    [[maybe_unused]] float rv = 0.0f;
 #pragma unroll
     for (int m = 0; m < MT; ++m) {
       if (m >= M) break;
@@ -392,9 +399,26 @@ __global__ __launch_bounds__(64 * SW * WC) void gemv_mfma_kernel(GemvMfmaArgs a)
       for (int p = 1; p < SW; ++p) v += red[((wc * SW + p) * MT + m) * 16 + col];
       if constexpr (XS == kXNorm) v *= inv;
       if constexpr (MT == 1) {
-        if (a.radd != nullptr) v = a.radd[n_out] + v;
+        if (a.radd != nullptr) {
+          rv = a.radd[n_out];
+          v = rv + v;
+        }
       }
+      if constexpr (XS == kXPlain) bad |= static_cast<uint32_t>(!__builtin_isfinite(v)) << m;
       a.y[static_cast<uint64_t>(m) * a.w.n + n_out] = v;
+    }
+    if constexpr (XS == kXPlain) {
+      // NaN or infinite activations (or an overflow): the reference's own
+      // order decides which outputs are NaN and which +-Inf
+      if (bad) {
+#pragma unroll 1
+        for (int m = 0; m < M; ++m) {
+          if (!((bad >> m) & 1u)) continue;
+          float v = exact_output_row<QT, WIDE>(a.w, a.x + static_cast<uint64_t>(m) * K, n_out);
+          if (MT == 1 && a.radd != nullptr) v = rv + v;
+          a.y[static_cast<uint64_t>(m) * a.w.n + n_out] = v;
+        }
+      }
     }
   }
 }

@@ -149,15 +149,22 @@ __global__ __launch_bounds__(256) void gemv_rm_kernel(View v, const float* __res
     if (static_cast<uint32_t>(r) >= m) break;
 #pragma unroll
     for (int j = 0; j < OUT; ++j) {
-      const float s = ((acc[r][j] + red[0][r][j][lane]) + red[1][r][j][lane]) + red[2][r][j][lane];
-      dst[static_cast<uint64_t>(r) * v.n + static_cast<uint64_t>(nb) * G::kBs + rm_offset<QT>(c, j)] = s;
+      float s = ((acc[r][j] + red[0][r][j][lane]) + red[1][r][j][lane]) + red[2][r][j][lane];
+      const uint64_t col = static_cast<uint64_t>(nb) * G::kBs + rm_offset<QT>(c, j);
+      // a NaN or infinite activation: the reference's order decides NaN or
+      // +-Inf (with a K split, rm_sum_kernel checks the sum instead)
+      if (ksplit == 1 && !__builtin_isfinite(s)) s = exact_row_major_col<QT, WIDE>(v, x + static_cast<uint64_t>(r) * K, col);
+      dst[static_cast<uint64_t>(r) * v.n + col] = s;
     }
   }
 }
 
-// y = sum of the K-split partials in split order
+// y = sum of the K-split partials in split order; a sum that is not finite
+// is recomputed in the reference's order
+template <int QT, bool WIDE>
 __global__ __launch_bounds__(256) void rm_sum_kernel(const float* __restrict__ part, uint32_t splits,
-                                                     uint64_t count, float* __restrict__ y) {
+                                                     uint64_t count, float* __restrict__ y, View v,
+                                                     const float* __restrict__ x) {
   const uint64_t i = static_cast<uint64_t>(blockIdx.x) * 256 + threadIdx.x;
   if (i >= count) return;
   // loads batched 8 at a time ahead of the in-order adds
@@ -171,6 +178,7 @@ __global__ __launch_bounds__(256) void rm_sum_kernel(const float* __restrict__ p
     for (int j = 0; j < 8; ++j) s += t[j];
   }
   for (; p < splits; ++p) s += part[p * count + i];
+  if (!__builtin_isfinite(s)) s = exact_row_major_col<QT, WIDE>(v, x + (i / v.n) * v.k, i % v.n);
   y[i] = s;
 }
 
@@ -187,8 +195,8 @@ hipError_t launch_rm_q(const View& v, const float* x, uint32_t m, float* y, floa
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || splits == 1) return e;
   const uint64_t count = static_cast<uint64_t>(m) * v.n;
-  hipLaunchKernelGGL(rm_sum_kernel, dim3(static_cast<uint32_t>((count + 255) / 256)), dim3(256), 0, st, part,
-                     splits, count, y);
+  hipLaunchKernelGGL((rm_sum_kernel<QT, WIDE>), dim3(static_cast<uint32_t>((count + 255) / 256)), dim3(256), 0,
+                     st, part, splits, count, y, v, x);
   return hipGetLastError();
 }
 

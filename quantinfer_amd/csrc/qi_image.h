@@ -106,6 +106,9 @@ struct Image {
   uint64_t k = 0, n = 0, nblocks = 0;
   int32_t wide = 0;   // 1: f32 scale entries
   int32_t tiled = 0;  // 1: tiled arrangement
+  // 1: every weight value and scale fits the f16 operands of the matrix-core
+  // GEMM (no overflow, no scale in f16's subnormal range; see plan_image)
+  int32_t f16_gemm = 1;
   uint64_t off_qs = 0, off_qh = 0, off_sc = 0, off_d = 0, off_dmin = 0;  // planar
   uint64_t tiles = 0, units = 0;  // tiled: 16-row tiles, 256-element units per row
   Record rec;

@@ -7,25 +7,16 @@
 
 namespace qi {
 
+// Planar decode GEMV (Q8_0/Q4_0 output rows, K a multiple of 32 but not of
+// 256), up to 16 rows per launch.
 struct GemvArgs {
   View w;
-  const float* x;       // [m, k] device
-  float* y;             // [m, n] device
-  int m;                // activation rows in this launch (<= compile-time tile)
-  uint32_t slots_per_split;
-  float* partials;      // [splits, m, n] workspace (split-K only)
-  uint32_t* tickets;    // one per row tile, zero between launches
+  const float* x;  // [m, k] device
+  float* y;        // [m, n] device
+  int m;           // activation rows in this launch (<= compile-time tile)
 };
-
-struct GemvPlan {
-  uint32_t row_tiles = 0, splits = 1, slots_per_split = 0;
-};
-
-int gemv_tile_rows(int mt);
-int gemv_slot_elems(int32_t qtype);
-GemvPlan plan_gemv(int32_t qtype, uint64_t k, uint64_t n, int mt, uint64_t max_partials);
-hipError_t launch_gemv(int32_t qtype, bool wide, int mt, const GemvArgs& a, const GemvPlan& plan,
-                       hipStream_t st);
+bool gemv_supported(int32_t qtype, int32_t layout, uint64_t k);
+hipError_t launch_gemv(int32_t qtype, bool wide, int mt, const GemvArgs& a, hipStream_t st);
 
 // Matrix-core decode GEMV (int8 digits of the activations x raw weight codes).
 // Activation source of a one-row GEMV. The decoder fuses the element-wise

@@ -84,11 +84,32 @@ int32_t plan_image(int32_t qtype, int32_t layout, uint64_t k, uint64_t n, const 
     *why = "invalid quantized output rows: K is not a multiple of the block size";
     return QI_HIP_INVALID_INPUT;
   }
-  bool all_f16 = true;
+  // The matrix-core GEMM rounds every weight (Q8_0/Q4_0: code times the f16
+  // scale) to an f16 operand. It is used only when that loses nothing beyond
+  // f16's relative precision: the largest possible weight magnitude stays
+  // below 2^15 (no overflow to infinity), Q8_0/Q4_0 scales are f16 normals
+  // (>= 2^-14; a subnormal scale would be rounded with an error of up to 2^-25
+  // absolute, hundreds of times f16's relative step for such a scale), and the
+  // K-quant weights are not all below 2^-10 (so their f16 subnormal floor of
+  // 2^-25 stays far below the tensor's scale). Other weights take the f32
+  // kernels in AUTO mode.
+  bool all_f16 = true, f16_gemm = true;
+  float wmax = 0.0f;
   for (uint64_t i = 0; i < count; ++i) {
     float d, dmin;
     if (!block_scales(qtype, blocks, i, &d, &dmin)) { *why = "block scales must be finite"; return QI_HIP_INVALID_INPUT; }
     if (all_f16 && !(f16_exact(d) && f16_exact(dmin))) all_f16 = false;
+    const float ad = fabsf(d), am = fabsf(dmin);
+    switch (qtype) {
+      case kQ8_0:
+      case kQ4_0:
+        if (ad != 0.0f && (ad < 0x1p-14f || ad > 256.0f)) f16_gemm = false;
+        wmax = fmaxf(wmax, ad * 128.0f);
+        break;
+      case kQ4_K: wmax = fmaxf(wmax, ad * (63.0f * 15.0f) + am * 63.0f); break;
+      case kQ5_K: wmax = fmaxf(wmax, ad * (63.0f * 31.0f) + am * 63.0f); break;
+      case kQ6_K: wmax = fmaxf(wmax, ad * (127.0f * 32.0f)); break;
+    }
     if (qtype == kQ4_0) {
       const uint8_t* v = as_blocks<qi_hip_q4_0_block>(blocks)[i].values;
       for (int j = 0; j < 32; ++j)
@@ -97,8 +118,11 @@ int32_t plan_image(int32_t qtype, int32_t layout, uint64_t k, uint64_t n, const 
   }
   const PlaneSizes ps = plane_sizes(qtype);
   const uint64_t scale_bytes = all_f16 ? 2 : 4;
+  if (qtype >= kQ4_K && wmax < 0x1p-10f) f16_gemm = false;
+  if (wmax > 32768.0f) f16_gemm = false;
   im.nblocks = count;
   im.wide = all_f16 ? 0 : 1;
+  im.f16_gemm = f16_gemm ? 1 : 0;
   if (layout == kOutputRows && k % 256 == 0) {
     // tiled records: 16-output tiles x 256-element units
     im.tiled = 1;

@@ -261,3 +261,47 @@ extern "C" qi_hip_status qi_hip_quantize(int32_t qtype, const float* values, uin
                 "quantize: input values must be finite and every scale representable as a finite f16");
   return QI_HIP_OK;
 }
+
+// Synthetic inputs for benchmarks: normal draws from counter-based SplitMix64
+// (Steele, Lea and Flood 2014, with Vigna's published constants) and
+// Box-Muller in double precision. Element i uses draws 3i, 3i + 1 (the
+// normal) and 3i + 2 (outlier or not), so the tensor does not depend on how
+// the elements are split over threads.
+namespace {
+
+uint64_t mix64(uint64_t seed, uint64_t draw) {
+  uint64_t z = seed + (draw + 1) * 0x9E3779B97F4A7C15ull;
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+
+// uniform on (0, 1]: the top 53 bits, plus one, times 2^-53
+double uniform(uint64_t seed, uint64_t draw) {
+  return (static_cast<double>(mix64(seed, draw) >> 11) + 1.0) * 0x1p-53;
+}
+
+}  // namespace
+
+extern "C" qi_hip_status qi_hip_synth_normal(uint64_t seed, uint64_t n, double std, double outlier_rate,
+                                             double outlier_std, float* out, int32_t threads) {
+  if (out == nullptr && n > 0) return qi_abi::fail(QI_HIP_INVALID_INPUT, "synth_normal: null output");
+  const uint64_t hw = std::max(1u, std::thread::hardware_concurrency());
+  uint64_t nt = threads > 0 ? static_cast<uint64_t>(threads) : hw;
+  nt = std::min<uint64_t>(std::min<uint64_t>(nt, 64), std::max<uint64_t>(1, n >> 16));
+  auto work = [&](uint64_t t) {
+    const double two_pi = 6.283185307179586476925286766559;
+    const uint64_t i0 = n * t / nt, i1 = n * (t + 1) / nt;
+    for (uint64_t i = i0; i < i1; ++i) {
+      const double u1 = uniform(seed, 3 * i), u2 = uniform(seed, 3 * i + 1), u3 = uniform(seed, 3 * i + 2);
+      const double z = sqrt(-2.0 * log(u1)) * cos(two_pi * u2);
+      const double s = outlier_rate > 0.0 && u3 <= outlier_rate ? outlier_std : std;
+      out[i] = static_cast<float>(z * s);
+    }
+  };
+  std::vector<std::thread> pool;
+  for (uint64_t t = 1; t < nt; ++t) pool.emplace_back(work, t);
+  work(0);
+  for (auto& th : pool) th.join();
+  return QI_HIP_OK;
+}

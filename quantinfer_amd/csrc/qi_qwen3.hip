@@ -1396,8 +1396,11 @@ qi_hip_status decode_step(qi_hip_qwen3* m, qi_hip_kv_cache* c) {
     c->graph_ws = ws;
     return QI_HIP_OK;  // the eager step was this step
   }
+  // the step's graph may read the context workspaces (MFMA mode)
+  qi_hip_status s = qi_abi::ws_before(m->ctx, st);
+  if (s != QI_HIP_OK) return s;
   QI_HIP_TRY(hipGraphLaunch(c->exec, st), "launch decode graph");
-  return QI_HIP_OK;
+  return qi_abi::ws_after(m->ctx, st);
 }
 
 void model_destroy(qi_hip_qwen3* m) {

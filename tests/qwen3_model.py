@@ -1,19 +1,22 @@
 """Seeded random-init Qwen3 weights for the decoder tests.
 
-Each projection is drawn from N(0, 0.02^2) as f32 output rows [N, K], quantized
-with the oracle's restatement of the reference quantizer (Q4_K by default; the
-LM head Q6_K, as in the end-to-end config) and dequantized again, so the same
-weights feed the device decoder (as logical blocks) and the CPU oracle (as
-the bit-identical f32 values the CpuScalar matmuls multiply by). Norm weights
-are N(1, 0.05^2) and the embedding N(0, 0.02^2), both f32.
+The recipe is quantinfer_amd.synth.qwen3_weights (projections N(0, 0.02^2)
+quantized to Q4_K, the LM head to Q6_K; embedding N(0, 0.02^2) and norm
+weights N(1, 0.05^2), f32), built here with the oracle's generator and
+quantizer. The same blocks feed the device decoder; the CPU oracle gets the
+dequantized rows (the bit-identical f32 values the CpuScalar matmuls multiply
+by) or the blocks themselves.
 """
 from __future__ import annotations
 
 import numpy as np
 
 from oracle import pyoracle as po
+from quantinfer_amd import synth
 
 OUTPUT_ROWS = 1
+ORACLE_NAMES = {"q_proj": "q", "k_proj": "k", "v_proj": "v", "o_proj": "o",
+                "gate_proj": "gate", "up_proj": "up", "down_proj": "down"}
 
 
 def small_config(**kw) -> dict:
@@ -32,49 +35,40 @@ def oracle_config(cfg: dict) -> dict:
                 eps=cfg["rms_norm_eps"], theta=cfg["rope_theta"])
 
 
-def _proj(qtype: int, n: int, k: int, seed: int):
-    w = po.fill_normal(seed, n * k, 0.02)
-    blocks = po.storage_precision(qtype, po.quantize(qtype, w))
-    deq = po.dequantize(qtype, blocks).reshape(n, k)
-    return blocks, deq
+def oracle_fns():
+    """The oracle's generator and quantizer (with f16 storage rounding), for
+    quantinfer_amd.synth.qwen3_weights."""
+    return (lambda seed, n, std: po.fill_normal(seed, n, std),
+            lambda qtype, v: po.storage_precision(qtype, po.quantize(qtype, v)))
 
 
 class Qwen3Weights:
-    """Weights of one random model: `device_layers` for quantinfer_amd.Qwen3,
-    `oracle_layers` for oracle.pyoracle.Qwen3."""
+    """Weights of one random model (the recipe of quantinfer_amd.synth, built
+    with the oracle's generator and quantizer): `device_layers` for
+    quantinfer_amd.Qwen3, `oracle_layers` (dequantized f32 rows) for
+    oracle.pyoracle.Qwen3."""
 
     def __init__(self, cfg: dict, seed: int = 0x5EED0004, qtype: int = po.Q4_K,
-                 head_qtype: int = po.Q6_K):
+                 head_qtype: int = po.Q6_K, dequantized: bool = True):
         self.cfg = cfg
-        H, I = cfg["hidden_size"], cfg["intermediate_size"]
-        hd = cfg["head_dim"]
-        QS, KS = cfg["num_attention_heads"] * hd, cfg["num_key_value_heads"] * hd
-        rng = np.random.default_rng(seed)
-        s = seed
-        self.embedding = po.fill_normal(s, cfg["vocab_size"] * H, 0.02).reshape(cfg["vocab_size"], H)
-        self.device_layers, self.oracle_layers = [], []
-        shapes = {"q_proj": (QS, H), "k_proj": (KS, H), "v_proj": (KS, H), "o_proj": (H, QS),
-                  "gate_proj": (I, H), "up_proj": (I, H), "down_proj": (H, I)}
-        oracle_names = {"q_proj": "q", "k_proj": "k", "v_proj": "v", "o_proj": "o",
-                        "gate_proj": "gate", "up_proj": "up", "down_proj": "down"}
-        for _ in range(cfg["num_hidden_layers"]):
-            norms = {n: (1.0 + 0.05 * rng.standard_normal(d)).astype(np.float32)
-                     for n, d in (("input_layernorm", H), ("q_norm", hd), ("k_norm", hd),
-                                  ("post_attention_layernorm", H))}
-            dev = dict(norms)
-            orc = {"input_norm": norms["input_layernorm"], "q_norm": norms["q_norm"],
-                   "k_norm": norms["k_norm"], "post_norm": norms["post_attention_layernorm"]}
-            for name, (n, k) in shapes.items():
-                s += 1
-                blocks, deq = _proj(qtype, n, k, s)
-                dev[name] = (qtype, OUTPUT_ROWS, blocks)
-                orc[oracle_names[name]] = deq
-            self.device_layers.append(dev)
+        normal, quantize = oracle_fns()
+        w = synth.qwen3_weights(cfg, seed, qtype, head_qtype, normal=normal, quantize=quantize)
+        self.embedding = w["embedding"]
+        self.device_layers = w["layers"]
+        self.final_norm = w["final_norm"]
+        self.head_qtype, _, self.head_blocks = w["head"]
+        shapes = synth.projection_shapes(cfg)
+        self.oracle_layers = []
+        for dev in self.device_layers:
+            orc = {"input_norm": dev["input_layernorm"], "q_norm": dev["q_norm"],
+                   "k_norm": dev["k_norm"], "post_norm": dev["post_attention_layernorm"]}
+            for name, short in ORACLE_NAMES.items():
+                q, _, blocks = dev[name]
+                orc[short] = (po.dequantize(q, blocks).reshape(shapes[name]) if dequantized
+                              else (q, blocks))
             self.oracle_layers.append(orc)
-        self.final_norm = (1.0 + 0.05 * rng.standard_normal(H)).astype(np.float32)
-        s += 1
-        self.head_blocks, self.head = _proj(head_qtype, cfg["vocab_size"], H, s)
-        self.head_qtype = head_qtype
+        self.head = (po.dequantize(self.head_qtype, self.head_blocks).reshape(cfg["vocab_size"], -1)
+                     if dequantized else (self.head_qtype, self.head_blocks))
 
     def device_model(self, ctx):
         import quantinfer_amd as qa
@@ -85,9 +79,21 @@ class Qwen3Weights:
         m.set_output(self.final_norm, (self.head_qtype, OUTPUT_ROWS, self.head_blocks))
         return m
 
-    def oracle_model(self, capacity: int, threads: int = 4):
-        return po.Qwen3(oracle_config(self.cfg), self.embedding, self.oracle_layers,
-                        self.final_norm, self.head, capacity, threads)
+    def oracle_model(self, capacity: int, threads: int = 4, blocks: bool = False):
+        """The oracle decoder on the dequantized f32 rows, or (blocks=True) on
+        the same quantized blocks the device holds."""
+        if not blocks:
+            return po.Qwen3(oracle_config(self.cfg), self.embedding, self.oracle_layers,
+                            self.final_norm, self.head, capacity, threads)
+        layers = []
+        for dev, orc in zip(self.device_layers, self.oracle_layers):
+            d = {f: orc[f] for f in po.NORM_FIELDS}
+            for name, short in ORACLE_NAMES.items():
+                qtype, _, blk = dev[name]
+                d[short] = (qtype, blk)
+            layers.append(d)
+        return po.Qwen3(oracle_config(self.cfg), self.embedding, layers, self.final_norm,
+                        (self.head_qtype, self.head_blocks), capacity, threads)
 
 
 def prompt(cfg: dict, n: int, seed: int = 7) -> np.ndarray:

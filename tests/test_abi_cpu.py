@@ -428,3 +428,11 @@ def test_quantize_rejects_what_the_reference_rejects(qtype):
         assert qa.quantize(qtype, big).tobytes() == po.quantize(qtype, big).tobytes()
         with pytest.raises(qa.QiError):
             qa.quantize(qtype, big, storage_f16=True)
+
+
+def test_synth_normal_equals_oracle_generator():
+    for args in ((0x5EED0002, 1 << 21, 0.02, 0.005, 0.2), (7, 1000, 1.0, 0.0, 0.0),
+                 (1, 300001, 0.02, 0.5, 0.2)):
+        ref = po.fill_normal(*args)
+        for threads in (1, 5, 0):
+            assert qa.synth_normal(*args, threads=threads).tobytes() == ref.tobytes()

@@ -11,6 +11,7 @@ import os
 import numpy as np
 import pytest
 
+from oracle import pyoracle as po
 from tests import numpy_ref
 from tests.qwen3_model import Qwen3Weights, oracle_config, prompt, small_config
 
@@ -239,3 +240,31 @@ def test_generate_is_forward_then_argmax_loop(oracle, small):
     m4 = w.oracle_model(8)
     with pytest.raises(oracle.OracleError):
         m4.forward(prompt(cfg, 9))
+
+
+@pytest.mark.parametrize("qtype", [po.Q8_0, po.Q4_0, po.Q4_K, po.Q5_K, po.Q6_K])
+def test_linear_on_blocks_is_the_output_row_matmul(oracle, qtype):
+    """qo_linear on quantized blocks equals the CpuScalar output-row matmul
+    (matmul.rs:119-160, 282-332) bit for bit, for any row count and thread
+    count, and equals qo_linear_rows on the dequantized rows."""
+    k, n = 512, 40
+    blocks = po.quantize(qtype, po.fill_normal(21 + qtype, n * k, 0.02, 0.005, 0.2))
+    deq = po.dequantize(qtype, blocks).reshape(n, k)
+    for m in (1, 5, 9):
+        x = po.fill_normal(m, m * k)
+        ref = po.matmul_output_rows(qtype, x.reshape(m, k), blocks, n)
+        for threads in (1, 3):
+            y = po.linear(x.reshape(m, k), (qtype, blocks), n, threads)
+            assert y.tobytes() == ref.tobytes(), (m, threads)
+        assert po.linear_rows(x.reshape(m, k), deq, threads=2).tobytes() == ref.tobytes()
+
+
+def test_decoder_on_blocks_equals_decoder_on_dequantized_rows(oracle, small):
+    cfg, w = small
+    p = prompt(cfg, 11)
+    a = w.oracle_model(32, threads=3).forward(p)
+    b = w.oracle_model(32, threads=2, blocks=True).forward(p)
+    assert a.tobytes() == b.tobytes()
+    ga = w.oracle_model(32, threads=1).generate(p, 6)
+    gb = w.oracle_model(32, threads=4, blocks=True).generate(p, 6)
+    assert ga == gb
