@@ -2,22 +2,32 @@
 
 Workload (the shape the metric is quoted on):
 Q4_K output-rows weight, K=4096, N=14336, M=1 f32 activation row, F32 mode.
-A step is one GEMV over the whole weight. Inputs are resident in HBM before
-the timed region; 16 distinct weight copies (530 MB, above the 256 MB
-Infinity Cache) are rotated so every step streams its weight from HBM.
+Inputs are resident in HBM before the timed region. The weight is held in C
+copies (C x 33 MB >= 512 MB, above the 256 MB Infinity Cache) and a step is
+one GEMV over each copy in turn (C launches, back to back), so every launch
+streams its weight from HBM and the event region's fixed cost is spread over
+C x steps launches; the region's own cost (events with no launch between
+them) is measured and reported beside it.
 
 Prints ONE JSON line (the driver's contract) with a `roofline` object for the
-GEMV kernel (algorithmic bytes / measured average kernel duration vs 8 TB/s)
-and a `cpu_baseline` object (the oracle's CpuScalar port on one host core).
-The line also carries `e2e`, the second half of the metric: Qwen3-8B-shape
-decode tokens/s of the GPU-resident decoder (36
-Q4_K layers, Q6_K head, 512-token prompt, 128 greedy decode steps), with its
-own roofline (bytes one decode step moves vs 8 TB/s) and CPU baseline.
+GEMV kernel (algorithmic bytes per launch / the average launch duration from
+HIP events on the launch stream, vs 8 TB/s) and a `cpu_baseline` object (the
+oracle's CpuScalar port on one host core). The line also carries:
+- `gemv_q8_0`: the same measurement for Q8_0 at 4096 x 14336 (the north
+  star's GEMV target names Q4_K and Q8_0);
+- `gemm`: the prefill GEMM at M=2048, K=4096, N=12288 for Q4_K and Q8_0,
+  TFLOP/s against the dense f16 matrix-core peak (the north star's GEMM
+  target);
+- `e2e`: Qwen3-8B-shape decode tokens/s of the GPU-resident decoder
+  with its own roofline and CPU baseline, and
+  whether its greedy ids equal the CPU run's (tests/golden/qwen3_8b_greedy.json).
 
-Inputs are synthetic. Weight blocks are drawn directly (synth_blocks): uniform
-random codes and sub-scales with f16-exact scales of the size the reference
-quantizer gives N(0, 0.02^2) weights. Kernel time does not depend on the
-values, and nothing in the measured legs touches the test oracle.
+Inputs are synthetic, drawn by the library's own host functions: N(0, 0.02^2)
+weights (configs[2] and [3]: 0.5% N(0, 0.2^2) outliers for the K-quants) from
+qi_hip_synth_normal, quantized by qi_hip_quantize (the reference quantizer,
+f16 storage rounding), activations N(0, 1). The e2e model is the recipe of
+quantinfer_amd.synth. Nothing in the measured legs touches the test oracle;
+it is loaded only for the cpu_baseline legs.
 """
 from __future__ import annotations
 
@@ -36,6 +46,7 @@ HBM_PEAK_GBPS = 8000.0
 K, N, M = 4096, 14336, 1
 WIRE = {1: 34, 2: 18, 3: 144, 4: 176, 5: 210}
 BLOCK = {1: 32, 2: 32, 3: 256, 4: 256, 5: 256}
+QNAME = {1: "q8_0", 2: "q4_0", 3: "q4_k", 4: "q5_k", 5: "q6_k"}
 
 
 def algorithmic_bytes(qtype: int, k: int, n: int, m: int) -> int:
@@ -52,79 +63,76 @@ def traffic_from_profile(name: str):
     return float(m.group(1)) if m else None
 
 
-# f16-exact scale magnitudes of quantized N(0, 0.02^2) blocks: (d, dmin)
-SCALE_SIZE = {1: (0.05 / 127, 0.0), 2: (0.05 / 7, 0.0), 3: (1.7e-4, 1.3e-3), 4: (8.5e-5, 1.3e-3),
-              5: (2.4e-5, 0.0)}
-
-
-def synth_blocks(qtype: int, count: int, seed: int):
-    """`count` random valid logical blocks (bench input only): random bytes in
-    every code and sub-scale field, f16-exact d (and dmin) of the quantizer's
-    magnitude, Q4_0 codes masked to four bits."""
-    import numpy as np
+def weight_blocks(qtype: int, k: int, n: int, seed: int):
+    """Output-rows blocks of an f32 [N, K] weight drawn from N(0, 0.02^2), with
+    0.5% N(0, 0.2^2) outliers for the K-quants,
+    quantized by the reference quantizer with f16 storage rounding
+    (qi_hip_synth_normal, qi_hip_quantize)."""
     import quantinfer_amd as qa
-
-    dt = qa.BLOCK_DTYPES[qtype]
-    rng = np.random.default_rng(seed)
-    b = np.frombuffer(rng.bytes(count * dt.itemsize), dtype=np.uint8).copy().view(dt)
-    d, dmin = SCALE_SIZE[qtype]
-    f16 = lambda v: v.astype(np.float16).astype(np.float32)  # noqa: E731
-    b["scale"] = f16(rng.uniform(0.7, 1.3, count) * d)
-    if dmin:
-        b["min_scale"] = f16(rng.uniform(0.7, 1.3, count) * dmin)
-    if qtype == 2:
-        b["values"] &= 15
-    return b
+    outliers = 0.005 if qtype >= 3 else 0.0
+    w = qa.synth_normal(seed, n * k, 0.02, outliers, 0.2)
+    return qa.quantize(qtype, w, storage_f16=True)
 
 
 def normal(seed: int, n: int, std: float = 1.0):
-    import numpy as np
-    return (np.random.default_rng(seed).standard_normal(n, dtype=np.float32) * np.float32(std))
+    import quantinfer_amd as qa
+    return qa.synth_normal(seed, n, std)
 
 
-def gpu_measure(qtype: int, steps: int, warmup: int, copies_mb: float = 512.0):
+def gemv_bench(qtype: int, k: int, n: int, m: int, steps: int, warmup: int, copies_mb: float = 512.0,
+               with_abi: bool = False) -> dict:
+    """`steps` passes over C resident weight copies, one launch per copy,
+    event-timed on the launch stream; plus the event region's own cost."""
     import quantinfer_amd as qa
     from quantinfer_amd import hiprt
 
     ctx = qa.Context(0)
-    blocks = synth_blocks(qtype, N * (K // BLOCK[qtype]), seed=0x5EED0000 + qtype)
-    wbytes = N * (K // BLOCK[qtype]) * WIRE[qtype]
+    blocks = weight_blocks(qtype, k, n, seed=0x5EED0000 + qtype)
+    wbytes = n * (k // BLOCK[qtype]) * WIRE[qtype]
     copies = max(1, int(-(-copies_mb * 1e6 // wbytes)))
-    weights = [ctx.weights(qtype, qa.OUTPUT_ROWS, K, N, blocks) for _ in range(copies)]
-    x = hiprt.DeviceBuffer.from_array(normal(0x5EED1000, M * K).reshape(M, K))
-    y = hiprt.DeviceBuffer(M * N * 4)
+    weights = [ctx.weights(qtype, qa.OUTPUT_ROWS, k, n, blocks) for _ in range(copies)]
+    x = hiprt.DeviceBuffer.from_array(normal(0x5EED1000, m * k).reshape(m, k))
+    y = hiprt.DeviceBuffer(m * n * 4)
     stream = hiprt.Stream()
 
-    def step(i):
-        weights[i % copies].linear_device(x.ptr, M, y.ptr, qa.MODE_F32, stream.handle)
+    def step():
+        for w in weights:
+            w.linear_device(x.ptr, m, y.ptr, qa.MODE_F32, stream.handle)
 
-    for i in range(warmup):
-        step(i)
+    for _ in range(warmup):
+        step()
     stream.synchronize()
-
-    # timed region: `steps` back-to-back GEMVs, bracketed by HIP events on the
-    # stream the kernels are launched on
     start, end = hiprt.Event(), hiprt.Event()
+    # the event region's fixed cost: the two events with nothing between them
+    empty = []
+    for _ in range(5):
+        start.record(stream)
+        end.record(stream)
+        stream.synchronize()
+        empty.append(start.elapsed_ms(end))
+    # timed region: `steps` passes over the copies, bracketed by HIP events on
+    # the stream the kernels are launched on
     hiprt.synchronize()
     start.record(stream)
-    for i in range(steps):
-        step(i)
+    for _ in range(steps):
+        step()
     end.record(stream)
     stream.synchronize()
     region_ms = start.elapsed_ms(end)
+    out = {"region_ms": region_ms, "copies": copies, "launches": steps * copies,
+           "empty_region_us": statistics.median(empty) * 1e3, "device": ctx.device_name()}
 
-    # PCIe-inclusive rate, never `value`: the synchronous KernelBackend call
-    # (qi_hip_linear: host x in, host y out, copies and the launch on the
-    # context's stream), timed on the host per call
-    xh = normal(0x5EED1000, M * K).reshape(M, K)
-    abi_times = []
-    for i in range(max(10, min(steps, 100))):
-        t = time.perf_counter()
-        weights[i % copies].linear(xh, qa.MODE_F32)
-        abi_times.append(time.perf_counter() - t)
-    abi_ms = statistics.median(abi_times) * 1e3
-
-    name = ctx.device_name()
+    if with_abi:
+        # PCIe-inclusive rate, never `value`: the synchronous KernelBackend
+        # call (qi_hip_linear: host x in, host y out), timed on the host
+        xh = normal(0x5EED1000, m * k).reshape(m, k)
+        abi_times = []
+        for i in range(100):
+            t = time.perf_counter()
+            weights[i % copies].linear(xh, qa.MODE_F32)
+            abi_times.append(time.perf_counter() - t)
+        out["abi_ms"] = statistics.median(abi_times) * 1e3
+        out["abi_calls"] = len(abi_times)
     start.destroy()
     end.destroy()
     for w in weights:
@@ -133,8 +141,31 @@ def gpu_measure(qtype: int, steps: int, warmup: int, copies_mb: float = 512.0):
     y.free()
     stream.destroy()
     ctx.close()
-    return {"region_ms": region_ms, "copies": copies, "device": name, "abi_ms": abi_ms,
-            "abi_calls": len(abi_times)}
+    return out
+
+
+def gemv_line(qtype: int, k: int, n: int, m: int, g: dict, steps: int, warmup: int) -> dict:
+    """The JSON object of one GEMV measurement."""
+    abytes = algorithmic_bytes(qtype, k, n, m)
+    us_launch = g["region_ms"] * 1e3 / g["launches"]
+    gbps = abytes / (us_launch * 1e-6) / 1e9
+    q = QNAME[qtype]
+    return {
+        "metric": f"quant GEMV GB/s (% of HBM peak) at {k}x{n}",
+        "value": round(gbps, 2), "unit": "GB/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
+        "ms_per_step": round(g["region_ms"] / steps, 5), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": f"synthetic: N(0,0.02^2) weights{' with 0.5% N(0,0.2^2) outliers' if qtype >= 3 else ''}"
+                f" quantized to {q} (qi_hip_quantize, f16 storage); x ~ N(0,1)",
+        "config": {"workload": f"{q}_gemv_output_rows_m{m}_k{k}_n{n}", "qtype": q, "m": m, "k": k,
+                   "n": n, "mode": "f32", "weight_copies": g["copies"],
+                   "step": f"one GEMV launch over each of the {g['copies']} resident weight copies",
+                   "launches": g["launches"], "us_per_launch": round(us_launch, 3),
+                   "event_region_overhead_us": round(g["empty_region_us"], 2), "device": g["device"]},
+        "roofline": {"bound": "hbm", "achieved": round(gbps, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(gbps / HBM_PEAK_GBPS, 4),
+                     "traffic": traffic_from_profile(f"{q}_gemv_{k}x{n}_traffic.md")},
+    }
 
 
 def copy_calibration(steps: int, mib: int = 256) -> None:
@@ -167,13 +198,14 @@ MFMA_F16_PEAK_TFLOPS = 2500.0
 
 def gemm_bench(qtype: int, m: int, k: int, n: int, steps: int, warmup: int) -> dict:
     """Prefill GEMM (MFMA mode, f16 operands, f32 accumulation): `steps`
-    back-to-back linear calls on resident inputs, event-timed on the launch
-    stream (each call is the f16 activation conversion plus the GEMM)."""
+    back-to-back linear calls on resident inputs (two weight copies
+    alternating), event-timed on the launch stream; each call is the f16
+    activation conversion plus the GEMM."""
     import quantinfer_amd as qa
     from quantinfer_amd import hiprt
 
     ctx = qa.Context(0)
-    blocks = synth_blocks(qtype, n * (k // BLOCK[qtype]), seed=0x5EED0010 + qtype)
+    blocks = weight_blocks(qtype, k, n, seed=0x5EED0010 + qtype)
     weights = [ctx.weights(qtype, qa.OUTPUT_ROWS, k, n, blocks) for _ in range(2)]
     x = hiprt.DeviceBuffer.from_array(normal(0x5EED3000, m * k).reshape(m, k))
     y = hiprt.DeviceBuffer(m * n * 4)
@@ -196,15 +228,17 @@ def gemm_bench(qtype: int, m: int, k: int, n: int, steps: int, warmup: int) -> d
     stream.destroy()
     ctx.close()
     tflops = 2.0 * m * n * k / (ms * 1e-3) / 1e12
-    qname = {1: "q8_0", 2: "q4_0", 3: "q4_k", 4: "q5_k", 5: "q6_k"}[qtype]
+    qname = QNAME[qtype]
     return {
         "metric": "prefill GEMM TFLOP/s (% of dense f16 MFMA peak)",
         "value": round(tflops, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": steps,
         "warmup": warmup, "ms_per_step": round(ms, 5), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "f16 operands, f32 accumulation",
-        "data": "synthetic: random Q-format blocks with f16-exact scales (synth_blocks); x ~ N(0,1)",
+        "data": f"synthetic: N(0,0.02^2) weights{' with 0.5% outliers' if qtype >= 3 else ''} quantized "
+                f"to {qname} (qi_hip_quantize); x ~ N(0,1)",
         "config": {"workload": f"{qname}_gemm_output_rows_m{m}_k{k}_n{n}", "qtype": qname,
-                   "m": m, "k": k, "n": n, "mode": "mfma", "device": name},
+                   "m": m, "k": k, "n": n, "mode": "mfma",
+                   "step": "one linear call: f16 activation conversion + GEMM", "device": name},
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": MFMA_F16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4),
                      "traffic": None},
@@ -234,7 +268,7 @@ def cpu_baseline(qtype: int, repeats: int = 3):
     as the reference's output-row kernels are), pinned to one host core."""
     from oracle import pyoracle as po
 
-    blocks = synth_blocks(qtype, N * (K // BLOCK[qtype]), seed=0x5EED0000 + qtype)
+    blocks = weight_blocks(qtype, K, N, seed=0x5EED0000 + qtype)
     x = normal(0x5EED1000, M * K).reshape(M, K)
     try:
         old = os.sched_getaffinity(0)
@@ -277,7 +311,7 @@ def cpu_simd_table(repeats: int = 3) -> dict:
         old = None
     try:
         for qtype, name, k, n in ((1, "q8_0", 4096, 4096), (2, "q4_0", 4096, 12288)):
-            blocks = synth_blocks(qtype, n * (k // BLOCK[qtype]), seed=0x5EED0000 + qtype)
+            blocks = weight_blocks(qtype, k, n, seed=0x5EED0000 + qtype)
             x = normal(0x5EED1000, k).reshape(1, k)
             row = {"qtype": name, "k": k, "n": n, "m": 1}
             legs = [("scalar", lambda: po.matmul_output_rows(qtype, x, blocks, n))]
@@ -302,10 +336,8 @@ def cpu_simd_table(repeats: int = 3) -> dict:
 
 # --------------------------------------------------------------- e2e decode
 
-QWEN3_8B = dict(vocab_size=151936, hidden_size=4096, intermediate_size=12288, num_hidden_layers=36,
-                num_attention_heads=32, num_key_value_heads=8, head_dim=128,
-                max_position_embeddings=40960, rms_norm_eps=1e-6, rope_theta=1e6)
 E2E_PROMPT, E2E_NEW = 512, 128
+E2E_GOLDEN = os.path.join(ROOT, "tests", "golden", "qwen3_8b_greedy.json")
 
 
 def e2e_shapes(cfg):
@@ -315,18 +347,6 @@ def e2e_shapes(cfg):
     KS = cfg["num_key_value_heads"] * cfg["head_dim"]
     return [("q_proj", H, QS), ("k_proj", H, KS), ("v_proj", H, KS), ("o_proj", QS, H),
             ("gate_proj", H, I), ("up_proj", H, I), ("down_proj", I, H)]
-
-
-def e2e_layer(cfg, index: int):
-    import numpy as np
-    rng = np.random.default_rng(0x5EED4000 + index)
-    H, hd = cfg["hidden_size"], cfg["head_dim"]
-    layer = {n: (1.0 + 0.05 * rng.standard_normal(d)).astype(np.float32)
-             for n, d in (("input_layernorm", H), ("q_norm", hd), ("k_norm", hd),
-                          ("post_attention_layernorm", H))}
-    for j, (name, k, n) in enumerate(e2e_shapes(cfg)):
-        layer[name] = (3, 1, synth_blocks(3, n * (k // 256), seed=(index << 4) + j + 0x5EED5000))
-    return layer
 
 
 def e2e_step_bytes(cfg, position: int) -> int:
@@ -343,26 +363,26 @@ def e2e_step_bytes(cfg, position: int) -> int:
 
 
 def e2e_bench(repeats: int = 3, with_cpu: bool = True) -> dict:
-    """Qwen3-8B-shape decode tokens/s: build the random-init model on the
-    device, then `repeats` x (reset cache, 512-token prompt, 128 greedy decode
-    steps); the decode time is the HIP-event time of the decode steps."""
+    """Qwen3-8B-shape decode tokens/s: build the random-init model of
+    quantinfer_amd.synth on the device, then `repeats` x (reset cache,
+    512-token prompt, 128 greedy decode steps) in AUTO mode; the decode time is
+    the HIP-event time of the decode steps. One more run in F32 mode (f32
+    prompt linears). Both runs' ids are compared with the CPU run's."""
     import numpy as np
     import quantinfer_amd as qa
+    from quantinfer_amd import synth
 
-    cfg = dict(QWEN3_8B)
+    cfg = dict(synth.QWEN3_8B)
     t0 = time.perf_counter()
+    w = synth.qwen3_weights(cfg, synth.DEFAULT_SEED, 3, 5)
+    cpu_layer = {name: w["layers"][0][name][2] for name, _, _ in e2e_shapes(cfg)}
+    cpu_head = w["head"][2]
     ctx = qa.Context(0)
-    model = qa.Qwen3(ctx, cfg)
-    model.set_embedding(normal(0x5EED6000, cfg["vocab_size"] * cfg["hidden_size"], 0.02))
-    for i in range(cfg["num_hidden_layers"]):
-        model.set_layer(i, e2e_layer(cfg, i))
-    head = synth_blocks(5, cfg["vocab_size"] * (cfg["hidden_size"] // 256), seed=0x5EED7000)
-    final_norm = (1.0 + 0.05 * np.random.default_rng(0x5EED7001)
-                  .standard_normal(cfg["hidden_size"])).astype(np.float32)
-    model.set_output(final_norm, (5, 1, head))
+    model = synth.device_model(ctx, cfg, w)
+    del w
     build_s = time.perf_counter() - t0
     cache = model.kv_cache(E2E_PROMPT + E2E_NEW)
-    prompt = np.random.default_rng(0x5EED7002).integers(0, cfg["vocab_size"], E2E_PROMPT)
+    prompt = synth.prompt(cfg, E2E_PROMPT)
     model.generate(cache, prompt, E2E_NEW)  # warm-up: workspaces and the decode graph
     runs, tokens = [], None
     for _ in range(repeats):
@@ -373,10 +393,28 @@ def e2e_bench(repeats: int = 3, with_cpu: bool = True) -> dict:
             raise RuntimeError("decode is not deterministic across runs")
         tokens = out
         runs.append((t.decode_ms, t.prefill_ms, t.decode_steps))
+    model.set_mode(qa.MODE_F32)
+    cache.reset()
+    tokens_f32 = model.generate(cache, prompt, E2E_NEW)
+    f32_timing = model.last_timing()
     device = ctx.device_name()
     cache.free()
     model.free()
     ctx.close()
+    golden = None
+    if os.path.exists(E2E_GOLDEN):
+        with open(E2E_GOLDEN) as f:
+            g = json.load(f)
+        if g["prompt"] == [int(v) for v in prompt] and g["seed"] == synth.DEFAULT_SEED:
+            golden = g["tokens"]
+
+    def match(ids):
+        if golden is None:
+            return None
+        first = next((i for i, (a, b) in enumerate(zip(ids, golden)) if a != b), None)
+        return {"equal": first is None and len(ids) == len(golden), "first_difference": first,
+                "equal_ids": sum(a == b for a, b in zip(ids, golden)), "of": len(golden)}
+
     decode_ms = statistics.median(r[0] for r in runs)
     prefill_ms = statistics.median(r[1] for r in runs)
     steps = runs[0][2]
@@ -390,8 +428,9 @@ def e2e_bench(repeats: int = 3, with_cpu: bool = True) -> dict:
         "warmup": 1, "ms_per_step": round(ms_tok, 5), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None,
         "dtype": "f32 activations, Q4_K linears (Q6_K head), f32 KV cache",
-        "data": "synthetic random-init model: random Q4_K/Q6_K blocks with f16-exact scales, "
-                "N(0,0.02^2) f32 embedding, N(1,0.05^2) norms; uniform random prompt ids",
+        "data": "synthetic random-init model (quantinfer_amd.synth): N(0,0.02^2) weights quantized to "
+                "Q4_K (head Q6_K) by qi_hip_quantize, N(0,0.02^2) f32 embedding, N(1,0.05^2) norms; "
+                "uniform random prompt ids",
         "config": {"workload": "qwen3_8b_shape_decode_prompt512_new128", "layers": 36,
                    "hidden": 4096, "heads": 32, "kv_heads": 8, "head_dim": 128,
                    "intermediate": 12288, "vocab": 151936, "prompt_tokens": E2E_PROMPT,
@@ -400,26 +439,28 @@ def e2e_bench(repeats: int = 3, with_cpu: bool = True) -> dict:
         "prefill_tok_s": round(E2E_PROMPT / (prefill_ms * 1e-3), 1),
         "prefill_ms": round(prefill_ms, 3),
         "model_build_s": round(build_s, 1),
+        "tokens_vs_cpu_run": {"auto": match(tokens), "f32": match(tokens_f32),
+                              "f32_prefill_ms": round(f32_timing.prefill_ms, 3),
+                              "f32_decode_tok_s": round(1e3 * f32_timing.decode_steps / f32_timing.decode_ms, 2),
+                              "reference": "tests/golden/qwen3_8b_greedy.json (oracle CpuScalar run)"},
         "roofline": {"bound": "hbm", "scope": "one whole decode step (all kernels of a token)",
                      "achieved": round(achieved, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBPS, 4),
                      "bytes_per_step": int(avg_bytes), "traffic": None},
-        "cpu_baseline": e2e_cpu_baseline(cfg) if with_cpu else None,
+        "cpu_baseline": e2e_cpu_baseline(cfg, cpu_layer, cpu_head) if with_cpu else None,
     }
 
 
-def e2e_cpu_baseline(cfg) -> dict:
+def e2e_cpu_baseline(cfg, layer: dict, head_blocks) -> dict:
     """The oracle's CpuScalar port on one pinned core, on a bounded sample:
     the seven Q4_K output-row matmuls of one layer at M=1 and the f32 LM head
     (the reference dequantizes a Q6_K head to f32 at load,
     runtime/src/qwen3/loader.rs:47-61), scaled to 36 layers per token.
     Attention and the norms (under 1% of the work) are left out."""
-    import numpy as np
     from oracle import pyoracle as po
 
-    layer = e2e_layer(cfg, 0)
     H, V = cfg["hidden_size"], cfg["vocab_size"]
-    head = po.dequantize(5, synth_blocks(5, V * (H // 256), seed=0x5EED7000)).reshape(V, H)
+    head = po.dequantize(5, head_blocks).reshape(V, H)
     try:
         old = os.sched_getaffinity(0)
         os.sched_setaffinity(0, {min(old)})
@@ -430,7 +471,7 @@ def e2e_cpu_baseline(cfg) -> dict:
         for name, k, n in e2e_shapes(cfg):
             x = normal(0x5EED8000, k).reshape(1, k)
             t = time.perf_counter()
-            po.matmul_output_rows(3, x, layer[name][2], n)
+            po.matmul_output_rows(3, x, layer[name], n)
             t_layer += time.perf_counter() - t
         x = normal(0x5EED8001, H).reshape(1, H)
         t = time.perf_counter()
@@ -450,19 +491,23 @@ def e2e_cpu_baseline(cfg) -> dict:
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--steps", type=int, default=20,
+                    help="timed steps (a step is one GEMV over each resident weight copy)")
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="time device-to-device copies of 256 MiB instead (counter calibration)")
     ap.add_argument("--workload", choices=["gemv", "gemm", "e2e"], default="gemv",
-                    help="gemv: the headline decode GEMV, with the e2e decode line embedded "
-                         "(default); gemm: the MFMA prefill GEMM; e2e: Qwen3-8B-shape decode only")
+                    help="gemv: the headline decode GEMV with the Q8_0 GEMV, the GEMMs and the e2e "
+                         "decode line embedded (default); gemm: one MFMA prefill GEMM; e2e: "
+                         "Qwen3-8B-shape decode only")
     ap.add_argument("--no-e2e", action="store_true", help="gemv: leave out the e2e decode run")
+    ap.add_argument("--no-gemm", action="store_true", help="gemv: leave out the GEMM objects")
     ap.add_argument("--cpu-simd", action="store_true",
                     help="only the CPU table: scalar and cpu-simd Q8_0/Q4_0 kernels, one core")
-    ap.add_argument("--qtype", default="q4_k", help="gemm only: q8_0, q4_0, q4_k, q5_k or q6_k")
-    ap.add_argument("--mkn", default="2048,4096,12288", help="gemm only: M,K,N")
+    ap.add_argument("--qtype", default="q4_k", help="gemv/gemm: q8_0, q4_0, q4_k, q5_k or q6_k")
+    ap.add_argument("--mkn", default=None,
+                    help="M,K,N (gemm default 2048,4096,12288; gemv default 1,4096,14336)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for {args.gpus}); "
@@ -475,58 +520,35 @@ def main():
     if args.cpu_simd:
         print(json.dumps(cpu_simd_table()))
         return
+    qt = {"q8_0": 1, "q4_0": 2, "q4_k": 3, "q5_k": 4, "q6_k": 5}[args.qtype]
     if args.workload == "gemm":
-        qt = {"q8_0": 1, "q4_0": 2, "q4_k": 3, "q5_k": 4, "q6_k": 5}[args.qtype]
-        m, k, n = (int(v) for v in args.mkn.split(","))
-        print(json.dumps(gemm_bench(qt, m, k, n, min(args.steps, 50), min(args.warmup, 5))))
+        m, k, n = (int(v) for v in (args.mkn or "2048,4096,12288").split(","))
+        print(json.dumps(gemm_bench(qt, m, k, n, max(args.steps, 20), args.warmup)))
         return
-
     if args.workload == "e2e":
         print(json.dumps(e2e_bench(with_cpu=not args.no_cpu)))
         return
 
-    qtype = 3  # Q4_K
-    g = gpu_measure(qtype, args.steps, args.warmup)
-    abytes = algorithmic_bytes(qtype, K, N, M)
-    # every step is one launch of the GEMV kernel, so the event-timed region
-    # average is the kernel's average launch duration (back-to-back launches)
-    ms_per_step = g["region_ms"] / args.steps
-    value = abytes / (ms_per_step * 1e-3) / 1e9
-    achieved = value
-    line = {
-        "metric": "quant GEMV GB/s (% of HBM peak) at 4096x14336; Qwen3-8B-shape decode tok/s",
-        "value": round(value, 2),
-        "unit": "GB/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(ms_per_step, 5),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "f32",
-        "data": "synthetic: random Q4_K blocks with f16-exact d/dmin (synth_blocks); x ~ N(0,1)",
-        "config": {"workload": "q4_k_gemv_output_rows_m1_k4096_n14336", "qtype": "q4_k",
-                   "m": M, "k": K, "n": N, "mode": "f32", "weight_copies": g["copies"],
-                   "device": g["device"]},
-        "roofline": {
-            "bound": "hbm",
-            "achieved": round(achieved, 2),
-            "peak": HBM_PEAK_GBPS,
-            "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBPS, 4),
-            "traffic": traffic_from_profile("q4_k_gemv_4096x14336_traffic.md"),
-        },
-        "cpu_baseline": None if args.no_cpu else cpu_baseline(qtype),
-        "through_abi": {
-            "value": round(abytes / (g["abi_ms"] * 1e-3) / 1e9, 2), "unit": "GB/s",
-            "ms_per_call": round(g["abi_ms"], 5), "calls": g["abi_calls"],
-            "note": "qi_hip_linear with host x and y (H2D, GEMV, D2H, synchronous): the "
-                    "PCIe-inclusive KernelBackend call, median over calls; not `value`",
-        },
+    m, k, n = (int(v) for v in (args.mkn or f"{M},{K},{N}").split(","))
+    g = gemv_bench(qt, k, n, m, args.steps, args.warmup, with_abi=True)
+    line = gemv_line(qt, k, n, m, g, args.steps, args.warmup)
+    line["metric"] = "quant GEMV GB/s (% of HBM peak) at 4096x14336; Qwen3-8B-shape decode tok/s"
+    line["cpu_baseline"] = None if args.no_cpu or (m, k, n) != (M, K, N) else cpu_baseline(qt)
+    abytes = algorithmic_bytes(qt, k, n, m)
+    line["through_abi"] = {
+        "value": round(abytes / (g["abi_ms"] * 1e-3) / 1e9, 2), "unit": "GB/s",
+        "ms_per_call": round(g["abi_ms"], 5), "calls": g["abi_calls"],
+        "note": "qi_hip_linear with host x and y (H2D, GEMV, D2H, synchronous): the "
+                "PCIe-inclusive KernelBackend call, median over calls; not `value`",
     }
-    if not args.no_e2e:
-        line["e2e"] = e2e_bench(with_cpu=not args.no_cpu)
+    if (qt, m, k, n) == (3, M, K, N):
+        g8 = gemv_bench(1, K, N, M, args.steps, args.warmup)
+        line["gemv_q8_0"] = gemv_line(1, K, N, M, g8, args.steps, args.warmup)
+        if not args.no_gemm:
+            line["gemm"] = {QNAME[q]: gemm_bench(q, 2048, 4096, 12288, max(args.steps, 20), args.warmup)
+                            for q in (3, 1)}
+        if not args.no_e2e:
+            line["e2e"] = e2e_bench(with_cpu=not args.no_cpu)
     print(json.dumps(line))
 
 

@@ -22,8 +22,15 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libqi_hip.so")
-SOURCES = ["qi_abi.hip", "qi_gemv.hip", "qi_gemv_mfma.hip", "qi_gemv_rm.hip", "qi_exact.hip", "qi_gemm.hip",
-           "qi_qwen3.hip", "qi_pack.cpp", "qi_quant.cpp"]
+
+def read_sources() -> list:
+    """The translation units, from csrc/sources.txt (shared with the Rust
+    crate's build.rs, backends/hip/build.rs)."""
+    with open(os.path.join(CSRC, "sources.txt")) as f:
+        return [ln.strip() for ln in f if ln.strip() and not ln.lstrip().startswith("#")]
+
+
+SOURCES = read_sources()
 
 ARCH = "gfx950"
 FLAGS = [

@@ -436,3 +436,40 @@ def test_synth_normal_equals_oracle_generator():
         ref = po.fill_normal(*args)
         for threads in (1, 5, 0):
             assert qa.synth_normal(*args, threads=threads).tobytes() == ref.tobytes()
+
+
+# ------------------------------------------- the Rust crate (backends/hip)
+
+def test_rust_crate_builds_the_same_sources_and_flags():
+    """backends/hip/build.rs compiles the translation units listed in
+    quantinfer_amd/csrc/sources.txt (the list build.py builds), with build.py's
+    code-generation flags."""
+    from quantinfer_amd import build as qb
+    rs = open(os.path.join(ROOT, "backends", "hip", "build.rs")).read()
+    assert 'join("sources.txt")' in rs and "quantinfer_amd/csrc" in rs
+    listed = [ln.strip() for ln in open(os.path.join(ROOT, "quantinfer_amd", "csrc", "sources.txt"))
+              if ln.strip() and not ln.startswith("#")]
+    assert listed == qb.SOURCES
+    for f in listed:
+        assert os.path.exists(os.path.join(ROOT, "quantinfer_amd", "csrc", f)), f
+    # every file under csrc that defines code is listed
+    code = sorted(f for f in os.listdir(os.path.join(ROOT, "quantinfer_amd", "csrc"))
+                  if f.endswith((".hip", ".cpp")))
+    assert sorted(listed) == code
+    flags = re.search(r"const FLAGS: &\[&str\] = &\[(.*?)\];", rs, re.S).group(1)
+    rs_flags = re.findall(r'"([^"]+)"', flags)
+    codegen = [f for f in qb.FLAGS if not f.startswith("-W")]
+    assert rs_flags == codegen
+
+
+def test_rust_ffi_declares_every_header_function():
+    ffi = open(os.path.join(ROOT, "backends", "hip", "src", "ffi.rs")).read()
+    declared = sorted(set(re.findall(r"pub fn (qi_hip_[a-z_0-9]+)\s*\(", ffi)))
+    assert declared == declared_symbols()
+    # block structs: the header's field order and sizes
+    for name, fields in (("Q8_0", ["scale", "values"]), ("Q4_0", ["scale", "values"]),
+                         ("Q4K", ["scale", "min_scale", "scales", "values"]),
+                         ("Q5K", ["scale", "min_scale", "scales", "high_bits", "values"]),
+                         ("Q6K", ["scale", "scales", "low_bits", "high_bits"])):
+        body = re.search(r"pub struct %s \{(.*?)\}" % name, ffi, re.S).group(1)
+        assert re.findall(r"pub (\w+):", body) == fields, name

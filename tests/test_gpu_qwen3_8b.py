@@ -1,0 +1,96 @@
+"""Greedy token identity on the end-to-end config at its real size.
+
+the random-init Qwen3-8B-architecture decoder (36
+layers, hidden 4096, 32 query / 8 KV heads of 128, SwiGLU 12288, vocab
+151936; every linear Q4_K, the head Q6_K; f32 embedding and norms) of
+quantinfer_amd.synth's recipe, a 512-token uniform random prompt, then 128
+greedy decode steps with the KV cache on the GPU. "Token ids must match the
+CPU run": the CPU run is the oracle's (CpuScalar linears on the same blocks,
+oracle/qwen3.c), committed as tests/golden/qwen3_8b_greedy.json by
+tests/golden/make_qwen3_8b_golden.py (about 20 minutes on 8 cores, so it is
+not recomputed here).
+
+The weights are rebuilt on the box with the library's own generator and
+quantizer (qi_hip_synth_normal, qi_hip_quantize), which equal the oracle's
+byte for byte (tests/test_abi_cpu.py); the test first checks the rebuilt
+weights' digest against the fixture's, so a mismatch in the inputs cannot
+pass for a mismatch in the decoder.
+
+F32 mode (f32 GEMV linears for the prompt and the steps) must give the CPU
+run's ids exactly. AUTO mode (the f16-operand GEMM for the 512-row prompt)
+is reported beside it; its ids are asserted too, with the per-step top-2 logit
+gaps of the CPU run printed so that a flip can be judged against them.
+"""
+import json
+import os
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "qwen3_8b_greedy.json")
+
+
+@pytest.fixture(scope="module")
+def golden():
+    if not os.path.exists(GOLDEN):
+        pytest.skip("tests/golden/qwen3_8b_greedy.json not generated")
+    with open(GOLDEN) as f:
+        return json.load(f)
+
+
+@pytest.fixture(scope="module")
+def model(golden):
+    import quantinfer_amd as qa
+    from quantinfer_amd import synth
+    from tests.golden.make_qwen3_8b_golden import weights_digest
+    cfg = dict(golden["config"])
+    print("building the Qwen3-8B-shape weights (synth_normal + quantize)", flush=True)
+    w = synth.qwen3_weights(cfg, golden["seed"], qa.Q4_K, qa.Q6_K)
+    digest = weights_digest(w)
+    print(f"weights digest {digest}", flush=True)
+    assert digest == golden["weights_digest_blake2b128"]
+    ctx = qa.Context(0)
+    dev = synth.device_model(ctx, cfg, w)
+    del w
+    yield cfg, ctx, dev
+    dev.free()
+    ctx.close()
+
+
+def _generate(qa, dev, golden, mode):
+    dev.set_mode(mode)
+    prompt = np.array(golden["prompt"], dtype=np.int32)
+    cache = dev.kv_cache(len(prompt) + len(golden["tokens"]))
+    got = dev.generate(cache, prompt, len(golden["tokens"]))
+    t = dev.last_timing()
+    cache.free()
+    return got, t
+
+
+def _report(name, got, want, gaps):
+    first = next((i for i, (a, b) in enumerate(zip(got, want)) if a != b), None)
+    print(f"{name}: {sum(a == b for a, b in zip(got, want))}/{len(want)} ids equal; first difference "
+          f"{first}; smallest CPU top-2 gap {min(gaps):.3e} at step {int(np.argmin(gaps))}", flush=True)
+    return first
+
+
+def test_f32_mode_greedy_ids_equal_cpu_run(model, golden):
+    import quantinfer_amd as qa
+    cfg, ctx, dev = model
+    got, t = _generate(qa, dev, golden, qa.MODE_F32)
+    first = _report("f32", got, golden["tokens"], golden["top2_gap"])
+    print(f"  prefill {t.prefill_ms:.1f} ms, decode {t.decode_ms:.1f} ms", flush=True)
+    assert first is None and len(got) == len(golden["tokens"])
+
+
+def test_auto_mode_greedy_ids_equal_cpu_run(model, golden):
+    """AUTO: the prompt's linears run on the f16-operand GEMM (normwise error
+    up to 2e-3 per layer), the decode steps on the f32 GEMV."""
+    import quantinfer_amd as qa
+    cfg, ctx, dev = model
+    got, t = _generate(qa, dev, golden, qa.MODE_AUTO)
+    first = _report("auto", got, golden["tokens"], golden["top2_gap"])
+    print(f"  prefill {t.prefill_ms:.1f} ms, decode {t.decode_ms:.1f} ms", flush=True)
+    assert first is None and len(got) == len(golden["tokens"])
