@@ -133,11 +133,17 @@ qi_hip_status grow_ws(qi_hip_ctx* c, hipStream_t st, float** buf, uint64_t* cap,
   return grow(buf, cap, need, what);
 }
 
-qi_hip_status run_linear(qi_hip_ctx* c, const qi_hip_weights* w, const float* x, uint64_t m,
-                         float* y, int32_t mode, hipStream_t st, float* silu_act, bool* silu_done) {
-  if (silu_done != nullptr) *silu_done = false;
-  const Image& im = w->im;
-  const qi::View v = qi::make_view(im, w->dev);
+// Which kernels a linear call runs and the workspace floats they need. One
+// function decides, so that the growing path (run_linear) and the scratch
+// path (qi_hip_linear_device_noalloc) take the same kernels.
+struct LinearPlan {
+  enum Kind { kGemm, kRowMajor, kMfma, kPlanar, kExact } kind = kExact;
+  uint64_t m_pad = 0;
+  uint32_t splits = 1;  // GEMM K splits, or row-major GEMV K splits for 4-row chunks
+  uint64_t h_floats = 0, s_floats = 0, d_floats = 0;  // f16 activations, partials, records
+};
+
+qi_hip_status plan_linear(const Image& im, uint64_t m, int32_t mode, LinearPlan* p) {
   if (mode < QI_HIP_MODE_AUTO || mode > QI_HIP_MODE_MFMA)
     return fail(QI_HIP_INVALID_INPUT, "unknown arithmetic mode");
   bool use_gemm = false;
@@ -151,82 +157,110 @@ qi_hip_status run_linear(qi_hip_ctx* c, const qi_hip_weights* w, const float* x,
   } else if (mode == QI_HIP_MODE_AUTO) {
     use_gemm = m >= 128 && im.f16_gemm && qi::gemm_supported(im.qtype, im.layout, im.k, im.n);
   }
-  qi_hip_status s = QI_HIP_OK;
+  *p = LinearPlan{};
   if (use_gemm) {
-    const uint64_t m_pad = qi::gemm_padded_rows(m);
-    const uint64_t halves = m_pad * im.k;
-    if ((s = grow_ws(c, st, &c->hbuf, &c->hcap, (halves + 1) / 2, "alloc GEMM workspace")) != QI_HIP_OK)
-      return s;
-    qi::GemmArgs ga{v, x, y, m, reinterpret_cast<_Float16*>(c->hbuf), m_pad};
-    ga.splits = qi::gemm_splits(im, m);
-    if (silu_act != nullptr && silu_done != nullptr && ga.splits == 1 && qi::gemm_silu_supported(im)) {
-      ga.act = silu_act;
-      *silu_done = true;
-    }
-    if (ga.splits > 1) {
-      const uint64_t need = ga.splits * m_pad * im.n;
-      if ((s = grow_ws(c, st, &c->sbuf, &c->scap, need, "alloc GEMM split-K workspace")) != QI_HIP_OK)
-        return s;
-      ga.part = c->sbuf;
-    }
-    if ((s = ws_before(c, st)) != QI_HIP_OK) return s;
-    QI_HIP_TRY(qi::launch_gemm(im, ga, st), "launch gemm");
-    return ws_after(c, st);
-  }
-  if (mode != QI_HIP_MODE_EXACT && qi::gemv_rm_supported(im)) {
-    // row-major weights: the blocks-along-N GEMV, 4 rows per launch
-    const uint32_t chunk = m < 4 ? static_cast<uint32_t>(m) : 4u;
-    const uint32_t splits = qi::gemv_rm_splits(im, chunk);
-    if (splits > 1) {
-      const uint64_t need = static_cast<uint64_t>(splits) * chunk * im.n;
-      if ((s = grow_ws(c, st, &c->sbuf, &c->scap, need, "alloc row-major GEMV workspace")) != QI_HIP_OK)
-        return s;
-      if ((s = ws_before(c, st)) != QI_HIP_OK) return s;
-    }
-    for (uint64_t m0 = 0; m0 < m; m0 += 4) {
-      const uint32_t rows = static_cast<uint32_t>(m - m0 < 4 ? m - m0 : 4);
-      // a last chunk of one row after 4-row chunks keeps the 4-row split count
-      const uint32_t sp = rows == chunk ? splits : qi::gemv_rm_splits(im, rows);
-      QI_HIP_TRY(qi::launch_gemv_rm(im, v, x + m0 * im.k, rows, y + m0 * im.n, c->sbuf,
-                                    sp <= splits ? sp : splits, st),
-                 "launch row-major gemv");
-    }
-    return splits > 1 ? ws_after(c, st) : QI_HIP_OK;
-  }
-  const bool mfma = mode != QI_HIP_MODE_EXACT && qi::gemv_mfma_supported(im.qtype, im.layout, im.k);
-  const bool planar = mode != QI_HIP_MODE_EXACT && !mfma && qi::gemv_supported(im.qtype, im.layout, im.k);
-  if (!mfma && !planar) {
-    QI_HIP_TRY(qi::launch_exact(im, v, x, m, y, st), "launch exact matmul");
+    p->kind = LinearPlan::kGemm;
+    p->m_pad = qi::gemm_padded_rows(m);
+    p->h_floats = (p->m_pad * im.k + 1) / 2;
+    p->splits = qi::gemm_splits(im, m);
+    if (p->splits > 1) p->s_floats = p->splits * p->m_pad * im.n;
     return QI_HIP_OK;
   }
-  // two or more rows: activation records built once per 16-row chunk into
-  // the context workspace
-  const bool records = mfma && m >= 2;
-  if (records) {
-    const uint32_t rows = static_cast<uint32_t>(m < 16 ? m : 16);
-    const uint64_t need = (qi::gemv_digits_bytes(im.k, rows) + 3) / 4;
-    if ((s = grow_ws(c, st, &c->dbuf, &c->dcap, need, "alloc GEMV workspace")) != QI_HIP_OK) return s;
-    if ((s = ws_before(c, st)) != QI_HIP_OK) return s;
+  if (mode != QI_HIP_MODE_EXACT && qi::gemv_rm_supported(im)) {
+    p->kind = LinearPlan::kRowMajor;
+    const uint32_t chunk = m < 4 ? static_cast<uint32_t>(m) : 4u;
+    p->splits = qi::gemv_rm_splits(im, chunk);
+    if (p->splits > 1) p->s_floats = static_cast<uint64_t>(p->splits) * chunk * im.n;
+    return QI_HIP_OK;
   }
-  for (uint64_t m0 = 0; m0 < m; m0 += 16) {
-    const int rows = static_cast<int>(m - m0 < 16 ? m - m0 : 16);
-    const int mt = rows == 1 ? 1 : rows == 2 ? 2 : rows <= 4 ? 4 : rows <= 8 ? 8 : 16;
-    if (mfma) {
-      qi::GemvMfmaArgs ga{v, x + m0 * im.k, y + m0 * im.n, rows};
-      if (rows >= 2) {
-        QI_HIP_TRY(qi::launch_gemv_digits(im.qtype, ga.x, im.k, static_cast<uint32_t>(rows),
-                                          reinterpret_cast<uint8_t*>(c->dbuf), st),
-                   "launch gemv activation records");
-        ga.digits = reinterpret_cast<const uint8_t*>(c->dbuf);
+  if (mode != QI_HIP_MODE_EXACT && qi::gemv_mfma_supported(im.qtype, im.layout, im.k)) {
+    p->kind = LinearPlan::kMfma;
+    // two or more rows: activation records built once per 16-row chunk
+    if (m >= 2) p->d_floats = (qi::gemv_digits_bytes(im.k, static_cast<uint32_t>(m < 16 ? m : 16)) + 3) / 4;
+    return QI_HIP_OK;
+  }
+  if (mode != QI_HIP_MODE_EXACT && qi::gemv_supported(im.qtype, im.layout, im.k)) {
+    p->kind = LinearPlan::kPlanar;
+    return QI_HIP_OK;
+  }
+  p->kind = LinearPlan::kExact;
+  return QI_HIP_OK;
+}
+
+// Enqueue the kernels of `p` on `st` with the given workspaces (each at least
+// the plan's size).
+qi_hip_status enqueue_linear(const qi_hip_weights* w, const LinearPlan& p, const float* x, uint64_t m,
+                             float* y, hipStream_t st, float* hws, float* sws, float* dws,
+                             float* silu_act, bool* silu_done) {
+  const Image& im = w->im;
+  const qi::View v = qi::make_view(im, w->dev);
+  switch (p.kind) {
+    case LinearPlan::kGemm: {
+      qi::GemmArgs ga{v, x, y, m, reinterpret_cast<_Float16*>(hws), p.m_pad};
+      ga.splits = p.splits;
+      if (silu_act != nullptr && silu_done != nullptr && ga.splits == 1 && qi::gemm_silu_supported(im)) {
+        ga.act = silu_act;
+        *silu_done = true;
       }
-      const int split = c->gemv_split > 0 ? c->gemv_split : qi::gemv_mfma_split(im.k, im.n);
-      QI_HIP_TRY(qi::launch_gemv_mfma(im.qtype, im.wide != 0, mt, split, ga, st), "launch gemv");
-      continue;
+      if (ga.splits > 1) ga.part = sws;
+      QI_HIP_TRY(qi::launch_gemm(im, ga, st), "launch gemm");
+      return QI_HIP_OK;
     }
-    qi::GemvArgs ga{v, x + m0 * im.k, y + m0 * im.n, rows};
-    QI_HIP_TRY(qi::launch_gemv(im.qtype, im.wide != 0, mt, ga, st), "launch gemv");
+    case LinearPlan::kRowMajor: {
+      // the blocks-along-N GEMV, 4 rows per launch; a last chunk of fewer
+      // rows keeps at most the 4-row split count
+      for (uint64_t m0 = 0; m0 < m; m0 += 4) {
+        const uint32_t rows = static_cast<uint32_t>(m - m0 < 4 ? m - m0 : 4);
+        const uint32_t chunk = m < 4 ? static_cast<uint32_t>(m) : 4u;
+        const uint32_t sp = rows == chunk ? p.splits : qi::gemv_rm_splits(im, rows);
+        QI_HIP_TRY(qi::launch_gemv_rm(im, v, x + m0 * im.k, rows, y + m0 * im.n, sws,
+                                      sp <= p.splits ? sp : p.splits, st),
+                   "launch row-major gemv");
+      }
+      return QI_HIP_OK;
+    }
+    case LinearPlan::kMfma:
+    case LinearPlan::kPlanar:
+      for (uint64_t m0 = 0; m0 < m; m0 += 16) {
+        const int rows = static_cast<int>(m - m0 < 16 ? m - m0 : 16);
+        const int mt = rows == 1 ? 1 : rows == 2 ? 2 : rows <= 4 ? 4 : rows <= 8 ? 8 : 16;
+        if (p.kind == LinearPlan::kMfma) {
+          qi::GemvMfmaArgs ga{v, x + m0 * im.k, y + m0 * im.n, rows};
+          if (rows >= 2) {
+            QI_HIP_TRY(qi::launch_gemv_digits(im.qtype, ga.x, im.k, static_cast<uint32_t>(rows),
+                                              reinterpret_cast<uint8_t*>(dws), st),
+                       "launch gemv activation records");
+            ga.digits = reinterpret_cast<const uint8_t*>(dws);
+          }
+          const int split = w->ctx->gemv_split > 0 ? w->ctx->gemv_split : qi::gemv_mfma_split(im.k, im.n);
+          QI_HIP_TRY(qi::launch_gemv_mfma(im.qtype, im.wide != 0, mt, split, ga, st), "launch gemv");
+        } else {
+          qi::GemvArgs ga{v, x + m0 * im.k, y + m0 * im.n, rows};
+          QI_HIP_TRY(qi::launch_gemv(im.qtype, im.wide != 0, mt, ga, st), "launch gemv");
+        }
+      }
+      return QI_HIP_OK;
+    case LinearPlan::kExact:
+      QI_HIP_TRY(qi::launch_exact(im, v, x, m, y, st), "launch exact matmul");
+      return QI_HIP_OK;
   }
-  return records ? ws_after(c, st) : QI_HIP_OK;
+  return fail(QI_HIP_RUNTIME_ERROR, "unknown linear plan");
+}
+
+qi_hip_status run_linear(qi_hip_ctx* c, const qi_hip_weights* w, const float* x, uint64_t m,
+                         float* y, int32_t mode, hipStream_t st, float* silu_act, bool* silu_done) {
+  if (silu_done != nullptr) *silu_done = false;
+  LinearPlan p;
+  qi_hip_status s = plan_linear(w->im, m, mode, &p);
+  if (s != QI_HIP_OK) return s;
+  if ((s = grow_ws(c, st, &c->hbuf, &c->hcap, p.h_floats, "alloc GEMM workspace")) != QI_HIP_OK) return s;
+  if ((s = grow_ws(c, st, &c->sbuf, &c->scap, p.s_floats, "alloc split-K workspace")) != QI_HIP_OK) return s;
+  if ((s = grow_ws(c, st, &c->dbuf, &c->dcap, p.d_floats, "alloc GEMV workspace")) != QI_HIP_OK) return s;
+  const bool uses_ws = p.h_floats + p.s_floats + p.d_floats > 0;
+  if (uses_ws && (s = ws_before(c, st)) != QI_HIP_OK) return s;
+  if ((s = enqueue_linear(w, p, x, m, y, st, c->hbuf, c->sbuf, c->dbuf, silu_act, silu_done)) != QI_HIP_OK)
+    return s;
+  return uses_ws ? ws_after(c, st) : QI_HIP_OK;
 }
 
 qi_hip_status create_weights_locked(qi_hip_ctx* c, const Image& im, const void* blocks,
@@ -293,6 +327,7 @@ qi_hip_status qi_hip_open(int32_t device, qi_hip_ctx** out) {
   c->name = prop.name[0] ? std::string(prop.name) : std::string("AMD ") + prop.gcnArchName;
   e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
   if (e == hipSuccess) e = hipEventCreateWithFlags(&c->ws_event, hipEventDisableTiming);
+
   if (e != hipSuccess) {
     ctx_destroy(c);
     return hip_fail(e, "context setup");

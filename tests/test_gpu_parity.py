@@ -428,29 +428,30 @@ def test_mfma_gemm_wide_scales(ctx):
         assert normwise_rel_err(y, exact) <= MFMA_TOL, NAMES[qtype]
 
 
-GEMM_CONFIGS = [
-    # Q8_0 and Q4_K, K=4096 N in {4096, 12288}, K=12288 N=4096
-    (qa.Q8_0, 4096, 4096, [128, 512]),
-    (qa.Q4_K, 4096, 4096, [128, 512]),
-    (qa.Q8_0, 4096, 12288, [2048]),
-    (qa.Q4_K, 4096, 12288, [2048]),
-    (qa.Q4_K, 12288, 4096, [2048]),
-]
+# BASELINE.json configs[3], the full cross product: Q8_0 and Q4_K weights x
+# (K=4096, N=4096), (K=4096, N=12288), (K=12288, N=4096) x M in {128, 512,
+# 2048} (18 points; M=128 and 512 run K-split GEMMs, M=2048 none).
+GEMM_SHAPES = [(qt, k, n) for qt in (qa.Q8_0, qa.Q4_K)
+               for k, n in ((4096, 4096), (4096, 12288), (12288, 4096))]
+GEMM_MS = (128, 512, 2048)
 
 
-@pytest.mark.parametrize("cfg", GEMM_CONFIGS, ids=lambda c: f"{NAMES[c[0]]}-K{c[1]}-N{c[2]}")
+@pytest.mark.parametrize("cfg", GEMM_SHAPES, ids=lambda c: f"{NAMES[c[0]]}-K{c[1]}-N{c[2]}")
 def test_config_shapes_mfma_tolerance(ctx, cfg):
-    qtype, k, n, ms = cfg
+    qtype, k, n = cfg
     blocks = po.make_weights(qtype, k, n, seed=0x5EED0010 + qtype, outliers=qtype != qa.Q8_0)
     w = ctx.weights(qtype, qa.OUTPUT_ROWS, k, n, blocks)
     rng = np.random.default_rng(3)
-    for m in ms:
+    for m in GEMM_MS:
         x = po.fill_normal(0x5EED3000 + m, m * k).reshape(m, k)
         y = w.linear(x, qa.MODE_MFMA)
+        # the CPU reference (CpuScalar) on 32 sampled rows, the f64 product on all
         rows = np.sort(rng.choice(m, size=min(m, 32), replace=False))
         comp, norm, cpu = _mfma_checks(y, x, blocks, qtype, n, cpu_rows=rows)
-        print(f"mfma {NAMES[qtype]} M={m} K={k} N={n}: comp {comp:.2e} norm {norm:.2e} cpu {cpu:.2e}")
+        print(f"mfma {NAMES[qtype]} M={m} K={k} N={n}: comp {comp:.2e} norm {norm:.2e} cpu {cpu:.2e}",
+              flush=True)
         assert comp <= MFMA_TOL and norm <= MFMA_TOL and cpu <= MFMA_TOL, (m, comp, norm, cpu)
+        assert w.linear(x, qa.MODE_AUTO).tobytes() == y.tobytes()  # AUTO picks the GEMM here
 
 
 # ------------------------------------------------ direct GGUF upload
