@@ -165,6 +165,8 @@ extern "C" {
                          y_host: *mut f32, mode: i32) -> i32;
     pub fn qi_hip_linear_device(ctx: *mut Ctx, w: *const Weights, x_dev: *const f32, m: u64,
                                 y_dev: *mut f32, mode: i32, stream: *mut c_void) -> i32;
+    pub fn qi_hip_linear_device_noalloc(ctx: *mut Ctx, w: *const Weights, x_dev: *const f32, m: u64,
+                                        y_dev: *mut f32, mode: i32, stream: *mut c_void) -> i32;
     pub fn qi_hip_dequantize(ctx: *mut Ctx, w: *const Weights, out_host: *mut f32) -> i32;
     pub fn qi_hip_dequantize_device(ctx: *mut Ctx, w: *const Weights, out_dev: *mut f32,
                                     stream: *mut c_void) -> i32;

@@ -147,6 +147,22 @@ qi_hip_status qi_hip_linear(qi_hip_ctx *ctx, const qi_hip_weights *w, const floa
 qi_hip_status qi_hip_linear_device(qi_hip_ctx *ctx, const qi_hip_weights *w, const float *x_dev,
                                    uint64_t m, float *y_dev, int32_t mode, void *stream);
 
+/* qi_hip_linear_device for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). No counterpart in the reference. Same kernels and results as
+ * qi_hip_linear_device, but every workspace (the GEMM's f16 activations and
+ * split-K partials, the multi-row GEMV's activation records) is carved out of
+ * a fixed 64 MiB scratch array the library holds on each GPU until the
+ * process ends; no call allocates or frees. A call whose workspaces exceed
+ * 64 MiB is refused with QI_HIP_INVALID_INPUT (the GEMM takes 2*M*K bytes of
+ * f16 activations, M rounded up to 128, plus split-K partials when fewer than
+ * 256 row x column blocks: every BASELINE GEMM shape fits). Every call on one GPU
+ * shares that GPU's array: calls that overlap on one GPU (other streams, other
+ * threads, other contexts on the same device) race, and the caller must order
+ * them. Nothing in the array needs clearing between calls. */
+qi_hip_status qi_hip_linear_device_noalloc(qi_hip_ctx *ctx, const qi_hip_weights *w, const float *x_dev,
+                                           uint64_t m, float *y_dev, int32_t mode, void *stream);
+
 /* Bit-exact f32 dequantization in block order (K*N floats).
  * Replaces: dequantize_q8_0 / q4_0 / q4_k / q5_k / q6_k
  * (crates/quantinfer-quant/src/schemes/q8.rs:33-45, q4.rs:35-47, q4_k.rs:90-121,

@@ -102,6 +102,7 @@ def lib() -> ctypes.CDLL:
         l.qi_hip_weights_info_get.argtypes = [vp, ctypes.POINTER(WeightsInfo)]
         l.qi_hip_linear.argtypes = [vp, vp, vp, u64, vp, i32]
         l.qi_hip_linear_device.argtypes = [vp, vp, vp, u64, vp, i32, vp]
+        l.qi_hip_linear_device_noalloc.argtypes = [vp, vp, vp, u64, vp, i32, vp]
         l.qi_hip_dequantize.argtypes = [vp, vp, vp]
         l.qi_hip_dequantize_device.argtypes = [vp, vp, vp, vp]
         l.qi_hip_pack_weights.argtypes = [i32, i32, u64, u64, vp, u64, vp,
@@ -130,6 +131,7 @@ def lib() -> ctypes.CDLL:
         l.qi_hip_qwen3_last_timing.argtypes = [vp, ctypes.POINTER(Qwen3Timing)]
         for name in ("qi_hip_open", "qi_hip_device_name", "qi_hip_weights_create",
                      "qi_hip_weights_info_get", "qi_hip_linear", "qi_hip_linear_device",
+                     "qi_hip_linear_device_noalloc",
                      "qi_hip_dequantize", "qi_hip_dequantize_device", "qi_hip_pack_weights",
                      "qi_hip_weights_create_gguf", "qi_hip_pack_gguf", "qi_hip_quantize", "qi_hip_synth_normal",
                      "qi_hip_qwen3_create", "qi_hip_qwen3_set_embedding", "qi_hip_qwen3_set_layer",

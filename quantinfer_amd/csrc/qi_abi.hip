@@ -23,7 +23,24 @@
 
 using qi::Image;
 
+// Scratch memory of qi_hip_linear_device_noalloc: the workspaces of one call
+// (the GEMM's f16 activations and split-K partials, the multi-row GEMV's
+// activation records) carved out of this file-scope array instead of
+// allocated. Each GPU the library runs on holds its own copy, at its own
+// address, until the process ends. In host code `scratch` is a host-side
+// stand-in, never a device address: qi_hip_open resolves the device address
+// once per device (hipGetSymbolAddress) and only that address is used.
+constexpr uint64_t kScratchBytes = 64ull << 20;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
 namespace qi_abi {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch[kMaxDevices] = {};  // device address of `scratch`, per device ordinal
+
+// With `device` current: the device address of its `scratch`, resolved once.
+qi_hip_status scratch_setup(int device, void** out);
 
 thread_local std::string g_last_error;
 std::atomic<uint64_t> g_ws_version{0};
@@ -89,6 +106,19 @@ qi_hip_status grow_pinned(float** buf, uint64_t* cap, uint64_t need) {
   QI_HIP_TRY(hipHostMalloc(reinterpret_cast<void**>(buf), need * sizeof(float), hipHostMallocDefault),
              "alloc pinned staging");
   *cap = need;
+  return QI_HIP_OK;
+}
+
+qi_hip_status scratch_setup(int device, void** out) {
+  if (device < 0 || device >= kMaxDevices) return fail(QI_HIP_UNSUPPORTED, "HIP device ordinal beyond 63");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch[device] == nullptr) {
+    void* ptr = nullptr;
+    QI_HIP_TRY(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)), "device address of the scratch array");
+    if (ptr == nullptr) return fail(QI_HIP_RUNTIME_ERROR, "device address of the scratch array is null");
+    g_scratch[device] = ptr;
+  }
+  *out = g_scratch[device];
   return QI_HIP_OK;
 }
 
@@ -327,7 +357,13 @@ qi_hip_status qi_hip_open(int32_t device, qi_hip_ctx** out) {
   c->name = prop.name[0] ? std::string(prop.name) : std::string("AMD ") + prop.gcnArchName;
   e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
   if (e == hipSuccess) e = hipEventCreateWithFlags(&c->ws_event, hipEventDisableTiming);
-
+  if (e == hipSuccess) {
+    const qi_hip_status st = scratch_setup(device, &c->scratch);
+    if (st != QI_HIP_OK) {
+      ctx_destroy(c);
+      return st;
+    }
+  }
   if (e != hipSuccess) {
     ctx_destroy(c);
     return hip_fail(e, "context setup");
@@ -484,6 +520,32 @@ qi_hip_status qi_hip_linear_device(qi_hip_ctx* c, const qi_hip_weights* w, const
   QI_HIP_TRY(hipSetDevice(c->device), "set device");
   hipStream_t st = stream ? static_cast<hipStream_t>(stream) : c->stream;
   return run_linear(c, w, x_dev, m, y_dev, mode, st);
+}
+
+qi_hip_status qi_hip_linear_device_noalloc(qi_hip_ctx* c, const qi_hip_weights* w, const float* x_dev,
+                                           uint64_t m, float* y_dev, int32_t mode, void* stream) {
+  qi_hip_status s = check_call(c, w, m);
+  if (s != QI_HIP_OK) return s;
+  if (x_dev == nullptr || y_dev == nullptr) return fail(QI_HIP_INVALID_INPUT, "null activation buffer");
+  if ((reinterpret_cast<uintptr_t>(x_dev) | reinterpret_cast<uintptr_t>(y_dev)) & 15u)
+    return fail(QI_HIP_INVALID_INPUT, "device activation and output buffers must be 16-byte aligned");
+  std::lock_guard<std::mutex> lock(c->mu);
+  QI_HIP_TRY(hipSetDevice(c->device), "set device");
+  LinearPlan p;
+  if ((s = plan_linear(w->im, m, mode, &p)) != QI_HIP_OK) return s;
+  auto a256 = [](uint64_t floats) { return (floats * 4 + 255) & ~static_cast<uint64_t>(255); };
+  const uint64_t hb = a256(p.h_floats), sb = a256(p.s_floats), db = a256(p.d_floats);
+  if (hb + sb + db > kScratchBytes)
+    return fail(QI_HIP_INVALID_INPUT, "this call needs " + std::to_string(hb + sb + db) +
+                                          " bytes of scratch; the no-allocation entry point holds " +
+                                          std::to_string(kScratchBytes));
+  // every workspace is written in full before it is read: nothing to clear
+  uint8_t* base = static_cast<uint8_t*>(c->scratch);
+  float* hws = reinterpret_cast<float*>(base);
+  float* sws = reinterpret_cast<float*>(base + hb);
+  float* dws = reinterpret_cast<float*>(base + hb + sb);
+  hipStream_t st = stream ? static_cast<hipStream_t>(stream) : c->stream;
+  return enqueue_linear(w, p, x_dev, m, y_dev, st, hws, sws, dws, nullptr, nullptr);
 }
 
 qi_hip_status qi_hip_dequantize_device(qi_hip_ctx* c, const qi_hip_weights* w, float* out_dev,

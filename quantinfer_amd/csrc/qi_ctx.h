@@ -46,6 +46,7 @@ struct qi_hip_ctx {
   float* dbuf = nullptr;  // activation records of the decode GEMV, 2+ rows (capacity in floats)
   uint64_t dcap = 0;
   int gemv_split = 0;  // QI_HIP_GEMV_SPLIT tuning override (wavefronts per GEMV workgroup: 4 or 8)
+  void* scratch = nullptr;  // device address of this device's scratch array (qi_abi.hip)
 };
 
 struct qi_hip_weights {
