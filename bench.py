@@ -245,6 +245,69 @@ def gemm_bench(qtype: int, m: int, k: int, n: int, steps: int, warmup: int) -> d
     }
 
 
+MFMA_F32_PEAK_TFLOPS = 157.3
+
+
+def f32_head_bench(steps: int, warmup: int) -> dict:
+    """F32 weights through the dense `matmul` (backends/cpu/src/backend.rs:48-60):
+    the unchanged runtime's LM head, [4096, 151936] f32 (a Q6_K head is
+    dequantized at load, runtime/src/qwen3/loader.rs:47-61). One decode row
+    (the streaming F32 GEMV, HBM-bound on 2.49 GB), the 512-row prompt's
+    logits (rocBLAS sgemm, against the f32 matrix-core peak), and the
+    synchronous per-token call with host buffers as the runtime makes it."""
+    import quantinfer_amd as qa
+    from quantinfer_amd import hiprt
+
+    k, n = 4096, 151936
+    ctx = qa.Context(0)
+    w = ctx.weights(qa.F32, qa.ROW_MAJOR, k, n, normal(0x5EED9000, k * n, 0.02))
+    stream = hiprt.Stream()
+    out = {}
+    for m in (1, 512):
+        x = hiprt.DeviceBuffer.from_array(normal(0x5EED9001, m * k).reshape(m, k))
+        y = hiprt.DeviceBuffer(m * n * 4)
+        reps = steps if m == 1 else max(steps // 4, 5)
+        for _ in range(warmup):
+            w.linear_device(x.ptr, m, y.ptr, qa.MODE_AUTO, stream.handle)
+        stream.synchronize()
+        start, end = hiprt.Event(), hiprt.Event()
+        start.record(stream)
+        for _ in range(reps):
+            w.linear_device(x.ptr, m, y.ptr, qa.MODE_AUTO, stream.handle)
+        end.record(stream)
+        stream.synchronize()
+        out[m] = start.elapsed_ms(end) / reps
+        x.free()
+        y.free()
+    xh = normal(0x5EED9001, k).reshape(1, k)
+    times = []
+    for _ in range(20):
+        t = time.perf_counter()
+        w.linear(xh, qa.MODE_AUTO)
+        times.append(time.perf_counter() - t)
+    abi_ms = statistics.median(times) * 1e3
+    stream.destroy()
+    w.free()
+    ctx.close()
+    gemv_bytes = k * n * 4 + k * 4 + n * 4
+    gbps = gemv_bytes / (out[1] * 1e-3) / 1e9
+    tflops = 2.0 * 512 * k * n / (out[512] * 1e-3) / 1e12
+    return {
+        "metric": "F32 matmul (unchanged runtime's LM head) GB/s at M=1",
+        "value": round(gbps, 2), "unit": "GB/s", "dtype": "f32",
+        "config": {"workload": "f32_matmul_row_major_k4096_n151936", "k": k, "n": n, "mode": "auto"},
+        "m1_ms": round(out[1], 4),
+        "roofline": {"bound": "hbm", "achieved": round(gbps, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None},
+        "m512": {"ms": round(out[512], 3), "tflops": round(tflops, 2), "kernel": "rocBLAS sgemm",
+                 "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": MFMA_F32_PEAK_TFLOPS,
+                              "unit": "TFLOP/s", "frac": round(tflops / MFMA_F32_PEAK_TFLOPS, 4)}},
+        "through_abi_m1_ms": round(abi_ms, 4),
+        "note": "through_abi: qi_hip_linear with host x and y (H2D 16 KB, GEMV, D2H 608 KB), the "
+                "per-token cost of the head when the unchanged runtime calls KernelBackend::matmul",
+    }
+
+
 def host_cpu() -> str:
     """The host CPU model and the logical CPU count this process may use."""
     model = "unknown CPU"
@@ -507,7 +570,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="time device-to-device copies of 256 MiB instead (counter calibration)")
-    ap.add_argument("--workload", choices=["gemv", "gemm", "e2e"], default="gemv",
+    ap.add_argument("--workload", choices=["gemv", "gemm", "e2e", "f32head"], default="gemv",
                     help="gemv: the headline decode GEMV with the Q8_0 GEMV, the GEMMs and the e2e "
                          "decode line embedded (default); gemm: one MFMA prefill GEMM; e2e: "
                          "Qwen3-8B-shape decode only")
@@ -538,6 +601,9 @@ def main():
     if args.workload == "e2e":
         print(json.dumps(e2e_bench(with_cpu=not args.no_cpu)))
         return
+    if args.workload == "f32head":
+        print(json.dumps(f32_head_bench(args.steps, args.warmup)))
+        return
 
     m, k, n = (int(v) for v in (args.mkn or f"{M},{K},{N}").split(","))
     g = gemv_bench(qt, k, n, m, args.steps, args.warmup, with_abi=True)
@@ -554,6 +620,7 @@ def main():
     if (qt, m, k, n) == (3, M, K, N):
         g8 = gemv_bench(1, K, N, M, args.steps, args.warmup)
         line["gemv_q8_0"] = gemv_line(1, K, N, M, g8, args.steps, args.warmup)
+        line["f32_matmul_head"] = f32_head_bench(args.steps, args.warmup)
         if not args.no_gemm:
             # the GEMM objects take their own counts: 20 warm-up calls (about
             # 6 ms, so that the clocks settle) and 50 timed ones

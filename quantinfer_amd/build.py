@@ -33,6 +33,8 @@ def read_sources() -> list:
 SOURCES = read_sources()
 
 ARCH = "gfx950"
+# rocBLAS: the plain f32 GEMM of F32 weights at 17+ rows (qi_f32.hip)
+LINK = ["-L/opt/rocm/lib", "-lrocblas", "-Wl,-rpath,/opt/rocm/lib"]
 FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-Wall",
     "-ffp-contract=off", "-fno-fast-math", "-fno-gpu-flush-denormals-to-zero",
@@ -91,7 +93,7 @@ def build(verbose: bool = False) -> str:
         raise RuntimeError("kernels spill registers to scratch memory (see _build/kernel_resources.json): "
                            + ", ".join(spills))
     tmp = LIB + ".tmp"
-    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs, *LINK]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stderr}")

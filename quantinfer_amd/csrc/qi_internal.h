@@ -67,6 +67,19 @@ uint32_t gemv_rm_splits(const Image& im, uint32_t m);
 hipError_t launch_gemv_rm(const Image& im, const View& v, const float* x, uint32_t m, float* y, float* part,
                           uint32_t splits, hipStream_t st);
 
+// F32 weights (row-major [K, N] f32, N a multiple of 4): the streaming GEMV
+// for up to 8 rows per launch (K split over the grid; `part` holds splits * m * n floats
+// when splits > 1), and rocBLAS sgemm for more rows through a handle made by
+// f32w_blas_create (0 on success, else a rocBLAS status).
+bool f32w_gemv_supported(const Image& im);
+uint32_t f32w_splits(const Image& im);
+hipError_t launch_f32w_gemv(const Image& im, const View& v, const float* x, uint32_t m, float* y, float* part,
+                            uint32_t splits, hipStream_t st);
+int f32w_blas_create(void** handle);
+void f32w_blas_destroy(void* handle);
+int f32w_sgemm(void* handle, const Image& im, const View& v, const float* x, uint64_t m, float* y,
+               hipStream_t st);
+
 // Exact-order matmul: bit-identical to CpuScalar (any M, either layout).
 hipError_t launch_exact(const Image& im, const View& w, const float* x, uint64_t m, float* y,
                         hipStream_t st);

@@ -150,12 +150,19 @@ def test_f32_row_major_gemv_tolerance(ctx, qtype):
 
 
 def test_exact_mode_f32_weights_bit_identical(ctx):
-    k, n = 300, 1000
-    wt = po.fill_normal(5, k * n, 0.02).reshape(k, n)
-    for m in (1, 3, 17):
-        x = po.fill_normal(6 + m, m * k).reshape(m, k)
+    """EXACT mode on F32 weights is CpuScalar's sequential-k matmul bit for
+    bit (N = 1001 is not a multiple of 4, the width the streaming GEMV needs:
+    AUTO falls back to the same exact kernel there)."""
+    k = 300
+    for n in (1000, 1001):
+        wt = po.fill_normal(5, k * n, 0.02).reshape(k, n)
         w = ctx.weights(qa.F32, qa.ROW_MAJOR, k, n, wt)
-        assert w.linear(x, qa.MODE_AUTO).tobytes() == po.matmul_f32(x, wt).tobytes()
+        for m in (1, 3, 17):
+            x = po.fill_normal(6 + m, m * k).reshape(m, k)
+            ref = po.matmul_f32(x, wt).tobytes()
+            assert w.linear(x, qa.MODE_EXACT).tobytes() == ref
+            if n % 4:
+                assert w.linear(x, qa.MODE_AUTO).tobytes() == ref
 
 
 def test_exact_mode_wide_scales_bit_identical(ctx):
@@ -472,3 +479,69 @@ def test_gguf_upload_same_results(ctx, qtype):
         assert wg.linear(x, mode).tobytes() == wl.linear(x, mode).tobytes(), mode
     wg.free()
     wl.free()
+
+
+# ------------------------------------------- F32 weights (the dense matmul)
+#
+# backends/cpu/src/backend.rs:48-60 -> matmul.rs:92-117: W row-major [K, N]
+# f32. F32/AUTO mode: the streaming GEMV up to 16 rows, rocBLAS sgemm above;
+# both judged by the F32 bars against CpuScalar's sequential f32 sums and the
+# f64 product.
+
+def _f32w_checks(y, x, w, rows=None):
+    rows = np.arange(x.shape[0]) if rows is None else rows
+    xs = np.ascontiguousarray(x[rows])
+    cpu = po.matmul_f32(xs, w)
+    exact = xs.astype(np.float64) @ w.astype(np.float64)
+    return (guarded_rel_err(y[rows], exact, xs, np.ascontiguousarray(w.T)),
+            normwise_rel_err(y[rows], cpu))
+
+
+@pytest.mark.parametrize("m", [1, 2, 3, 8, 11, 16, 17, 128, 300])
+def test_f32_weights_tolerance(ctx, m):
+    k, n = 2048, 1000
+    w = po.fill_normal(9800, k * n, 0.02).reshape(k, n)
+    x = po.fill_normal(9801 + m, m * k).reshape(m, k)
+    wt = ctx.weights(qa.F32, qa.ROW_MAJOR, k, n, w)
+    y = wt.linear(x, qa.MODE_F32)
+    comp, norm = _f32w_checks(y, x, w)
+    assert comp <= F32_TOL and norm <= F32_TOL, (m, comp, norm)
+    assert wt.linear(x, qa.MODE_AUTO).tobytes() == y.tobytes()
+    assert wt.linear(x, qa.MODE_F32).tobytes() == y.tobytes()  # deterministic
+
+
+def test_f32_weights_lm_head_shape(ctx):
+    """The unchanged runtime's LM head: [4096, 151936] f32 (a Q6_K head
+    dequantized at load, runtime/src/qwen3/loader.rs:47-61), one decode row
+    (GEMV) and a 128-row prompt (sgemm), on sampled outputs rows."""
+    k, n = 4096, 151936
+    w = po.fill_normal(9810, k * n, 0.02).reshape(k, n)
+    wt = ctx.weights(qa.F32, qa.ROW_MAJOR, k, n, w)
+    for m in (1, 128):
+        x = po.fill_normal(9811 + m, m * k).reshape(m, k)
+        y = wt.linear(x, qa.MODE_AUTO)
+        rows = np.array([0, m // 2, m - 1]) if m > 1 else np.array([0])
+        cols = np.random.default_rng(m).choice(n, 4096, replace=False)
+        ws = np.ascontiguousarray(w[:, cols])
+        comp, norm = _f32w_checks(np.ascontiguousarray(y[:, cols]), x, ws, rows)
+        print(f"f32 head M={m}: comp {comp:.2e} norm {norm:.2e}", flush=True)
+        assert comp <= F32_TOL and norm <= F32_TOL, (m, comp, norm)
+
+
+def test_f32_weights_nonfinite_activations(ctx):
+    k, n = 1024, 512
+    w = po.fill_normal(9820, k * n, 0.02).reshape(k, n)
+    w[:, 7] = 0.0  # Inf * 0 is NaN in the reference
+    wt = ctx.weights(qa.F32, qa.ROW_MAJOR, k, n, w)
+    for m in (1, 5, 40):
+        x = po.fill_normal(9821, m * k).reshape(m, k)
+        x[0, 3] = np.inf
+        if m > 1:
+            x[1, 9] = np.nan
+        y = wt.linear(x, qa.MODE_F32)
+        ref = po.matmul_f32(x, w)
+        bad = [0, 1] if m > 1 else [0]
+        assert np.array_equal(y[bad], ref[bad], equal_nan=True), m
+        assert np.isnan(y[0, 7]) and np.isinf(y[0, 0])
+        if m > 2:
+            assert normwise_rel_err(y[2:], ref[2:]) <= F32_TOL
