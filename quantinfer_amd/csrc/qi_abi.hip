@@ -11,6 +11,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <algorithm>
 #include <atomic>
 #include <mutex>
 #include <string>
@@ -219,8 +220,17 @@ qi_hip_status plan_linear(const Image& im, uint64_t m, int32_t mode, LinearPlan*
   }
   if (mode != QI_HIP_MODE_EXACT && qi::gemv_mfma_supported(im.qtype, im.layout, im.k)) {
     p->kind = LinearPlan::kMfma;
-    // two or more rows: activation records built once per 16-row chunk
-    if (m >= 2) p->d_floats = (qi::gemv_digits_bytes(im.k, static_cast<uint32_t>(m < 16 ? m : 16)) + 3) / 4;
+    // two or more rows: activation records built once per 16-row chunk, and
+    // K parts over the grid whose partial sums are added in order
+    if (m >= 2) {
+      const uint32_t rows = static_cast<uint32_t>(m < 16 ? m : 16);
+      p->d_floats = (qi::gemv_digits_bytes(im.k, rows) + 3) / 4;
+      // partial sums [parts][rows][n] of a 16-row chunk; a shorter last
+      // chunk (2..8 rows) may take more parts, so size for the larger count
+      const uint32_t parts = std::max(qi::gemv_pre_splits(im.k, 16), qi::gemv_pre_splits(im.k, 8));
+      p->splits = parts;
+      if (parts > 1) p->s_floats = static_cast<uint64_t>(parts) * rows * im.n;
+    }
     return QI_HIP_OK;
   }
   if (mode != QI_HIP_MODE_EXACT && qi::gemv_supported(im.qtype, im.layout, im.k)) {
@@ -275,9 +285,16 @@ qi_hip_status enqueue_linear(const qi_hip_weights* w, const LinearPlan& p, const
                                               reinterpret_cast<uint8_t*>(dws), st),
                        "launch gemv activation records");
             ga.digits = reinterpret_cast<const uint8_t*>(dws);
+            ga.ksplit = qi::gemv_pre_splits(im.k, static_cast<uint32_t>(mt));
+            ga.part = sws;
           }
           const int split = w->ctx->gemv_split > 0 ? w->ctx->gemv_split : qi::gemv_mfma_split(im.k, im.n);
           QI_HIP_TRY(qi::launch_gemv_mfma(im.qtype, im.wide != 0, mt, split, ga, st), "launch gemv");
+          if (ga.ksplit > 1) {
+            const uint64_t count = static_cast<uint64_t>(rows) * im.n;
+            QI_HIP_TRY(qi::launch_splitk_sum(im, v, sws, ga.ksplit, count, count, ga.y, ga.x, st),
+                       "launch gemv split-K sum");
+          }
         } else {
           qi::GemvArgs ga{v, x + m0 * im.k, y + m0 * im.n, rows};
           QI_HIP_TRY(qi::launch_gemv(im.qtype, im.wide != 0, mt, ga, st), "launch gemv");

@@ -988,6 +988,24 @@ hipError_t launch_q(const Image& im, const GemmArgs& a, hipStream_t st) {
 
 }  // namespace
 
+hipError_t launch_splitk_sum(const Image& im, const View& v, const float* part, uint32_t splits,
+                             uint64_t count, uint64_t stride, float* y, const float* x, hipStream_t st) {
+  const dim3 grid(static_cast<uint32_t>((count + 255) / 256));
+  auto go = [&](auto kern) {
+    hipLaunchKernelGGL(kern, grid, dim3(256), 0, st, part, splits, count, stride, y, v, x);
+    return hipGetLastError();
+  };
+  const bool w = im.wide != 0;
+  switch (im.qtype) {
+    case kQ8_0: return w ? go(gemm_splitk_sum_kernel<kQ8_0, true>) : go(gemm_splitk_sum_kernel<kQ8_0, false>);
+    case kQ4_0: return w ? go(gemm_splitk_sum_kernel<kQ4_0, true>) : go(gemm_splitk_sum_kernel<kQ4_0, false>);
+    case kQ4_K: return w ? go(gemm_splitk_sum_kernel<kQ4_K, true>) : go(gemm_splitk_sum_kernel<kQ4_K, false>);
+    case kQ5_K: return w ? go(gemm_splitk_sum_kernel<kQ5_K, true>) : go(gemm_splitk_sum_kernel<kQ5_K, false>);
+    case kQ6_K: return w ? go(gemm_splitk_sum_kernel<kQ6_K, true>) : go(gemm_splitk_sum_kernel<kQ6_K, false>);
+    default: return hipErrorInvalidValue;
+  }
+}
+
 bool gemm_supported(int32_t qtype, int32_t layout, uint64_t k, uint64_t n) {
   (void)n;
   return layout == kOutputRows && qtype >= kQ8_0 && qtype <= kQ6_K && k % 256 == 0 && k > 0;

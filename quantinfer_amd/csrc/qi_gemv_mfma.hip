@@ -15,14 +15,17 @@
 //   y += a * 2^-s * combine(C) - b * sum_k x_k.
 // This reorders the reference arithmetic and is judged by tolerance.
 //
-// Operand layout (16x16x32: A[i][k] lane i+16*(k/8), B[k][j] lane j+16*(k/8),
-// C[i][j] lane j+16*(i/4) element i%4). For a tile of 16 outputs (B columns)
-// the 4 lane groups g = lane/16 each stream their own 8 codes per step; A row
-// i = 4*sigma + digit carries digit `digit` of lane group sigma's 8
-// activations and is zero elsewhere, so C row 4*sigma + digit holds lane
-// group sigma's own digit sums: after a window of steps, lane (n, g) holds
-// the four digit sums of its own codes in its four C registers, next to its
-// own scale. A 256-element unit is 8 steps x 4 groups x 8 codes.
+// Operand layout (v_mfma_i32_16x16x64_i8: A[i][k] lane i+16*(k/16), B[k][j]
+// lane j+16*(k/16), 16 bytes per lane; C[i][j] lane j+16*(i/4) element i%4).
+// For a tile of 16 outputs (B columns) the 4 lane groups g = lane/16 each
+// stream their own codes: a step is 8 codes per lane group and one matrix
+// instruction takes a pair of steps (16 codes). A row i = 4*sigma + digit
+// carries digit `digit` of lane group sigma's 16 activations and is zero
+// elsewhere, so C row 4*sigma + digit holds lane group sigma's own digit sums:
+// after a window of steps, lane (n, g) holds the four digit sums of its own
+// codes in its four C registers, next to its own scale. A 256-element unit is
+// 8 steps x 4 groups x 8 codes, 4 instructions. (The 16x16x32 instruction
+// takes as many cycles for half the products on gfx950.)
 //
 // Work split: WC tiles of 16 outputs per workgroup, SW wavefronts per tile
 // splitting its K range (contiguous runs of units, reduced through LDS at the
@@ -44,9 +47,9 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 
 constexpr uint32_t kZeroBytes = 1024;  // zero A operand for the lanes of other lane groups
 // Activation record of one (row, unit): 256 activations x 4 digits (1024 B,
-// [step t][lane group g] x 32 B, digit d of the 8 activations at byte 8 d),
-// then 8 windows x float4 {2^-s, sum of elements 0-15, of 16-31, 0} (128 B,
-// [g][h]). Built in LDS by the workgroup, or once per call in global memory
+// [step pair p][lane group g][digit d] x 16 B: digit d of the pair's 16
+// activations, steps 2p and 2p + 1), then 8 windows x float4 {2^-s, sum of
+// elements 0-15, of 16-31, 0} (128 B, [g][h]). Built in LDS by the workgroup, or once per call in global memory
 // by gemv_digits_kernel and copied into LDS.
 constexpr uint32_t kUnitDigitBytes = 1024;
 constexpr uint32_t kUnitAuxBytes = 128;
@@ -124,9 +127,10 @@ __device__ __forceinline__ void store_half(const HalfX& o, const Item& it, bool 
   const int sh = 29 - e;
   const float inv = !finite ? __builtin_nanf("") : mx > 0.0f ? ldexpf(1.0f, e - 29) : 0.0f;
   if (!valid) return;
-  const uint32_t t0 = 4 * it.h + 2 * it.half;
+  // this half window is the step pair p = 2h + half (steps 2p and 2p + 1)
+  const uint32_t p = 2 * it.h + it.half;
   uint8_t* const rec = recs + (static_cast<uint64_t>(it.m) * cu + it.u) * kUnitRecBytes;
-  uint8_t* dst0 = rec + (t0 * 4 + it.g) * 32;
+  uint32_t lo[2][4], hi[2][4];
 #pragma unroll
   for (int tt = 0; tt < 2; ++tt) {
     uint32_t dig[8];
@@ -136,13 +140,13 @@ __device__ __forceinline__ void store_half(const HalfX& o, const Item& it, bool 
       // signed base-256 digits: byte i of (F + 0x808080) ^ 0x808080
       dig[j] = (static_cast<uint32_t>(F) + 0x00808080u) ^ 0x00808080u;
     }
-    uint32_t lo[4], hi[4];
-    transpose4(dig, lo);
-    transpose4(dig + 4, hi);
-    uint8_t* dst = dst0 + tt * 128;
-    *reinterpret_cast<uint4*>(dst) = make_uint4(lo[0], hi[0], lo[1], hi[1]);
-    *reinterpret_cast<uint4*>(dst + 16) = make_uint4(lo[2], hi[2], lo[3], hi[3]);
+    transpose4(dig, lo[tt]);
+    transpose4(dig + 4, hi[tt]);
   }
+  // digit d of the pair's 16 activations: 16 contiguous bytes
+  uint4* const dst = reinterpret_cast<uint4*>(rec + (p * 4 + it.g) * 64);
+#pragma unroll
+  for (int d = 0; d < 4; ++d) dst[d] = make_uint4(lo[0][d], hi[0][d], lo[1][d], hi[1][d]);
   if (it.half == 0)
     reinterpret_cast<float4*>(rec + kUnitDigitBytes)[it.g * 2 + it.h] = make_float4(inv, sum, other, 0.0f);
 }
@@ -194,8 +198,12 @@ __global__ __launch_bounds__(64 * SW * WC) void gemv_mfma_kernel(GemvMfmaArgs a)
 
   typename U::Raw ring[D];
 
-  for (uint32_t ku0 = 0; ku0 < units_total; ku0 += cu) {
-    const uint32_t units = min(cu, units_total - ku0);
+  // K split over the grid's y dimension (two or more rows): this workgroup's
+  // units [u_lo, u_hi); its partial sums go to a.part[blockIdx.y]
+  const uint32_t u_lo = a.ksplit > 1 ? blockIdx.y * a.split_units : 0;
+  const uint32_t u_hi = a.ksplit > 1 ? min(units_total, u_lo + a.split_units) : units_total;
+  for (uint32_t ku0 = u_lo; ku0 < u_hi; ku0 += cu) {
+    const uint32_t units = min(cu, u_hi - ku0);
     const uint32_t k0 = ku0 * 256;
     const uint32_t halves = static_cast<uint32_t>(M) * units * 16;
     // this wavefront's contiguous run of the chunk's units (balanced split)
@@ -303,7 +311,7 @@ __global__ __launch_bounds__(64 * SW * WC) void gemv_mfma_kernel(GemvMfmaArgs a)
 #pragma unroll
         for (int m = 0; m < MT; ++m) {
           const uint8_t* rec = recs + (m * cu + u) * kUnitRecBytes;
-          abase[m] = a_live ? rec + g * 32 + digit * 8 : lds;
+          abase[m] = a_live ? rec + g * 64 + digit * 16 : lds;
           ax[m] = reinterpret_cast<const float4*>(rec + kUnitDigitBytes) + g * 2;
         }
 #pragma unroll
@@ -312,14 +320,18 @@ __global__ __launch_bounds__(64 * SW * WC) void gemv_mfma_kernel(GemvMfmaArgs a)
 #pragma unroll
           for (int m = 0; m < MT; ++m) c[m] = v4i{0, 0, 0, 0};
 #pragma unroll
-          for (int s = 0; s < U::kSteps; ++s) {
+          for (int s = 0; s < U::kSteps; s += 2) {
+            // one 16x16x64 instruction per step pair: 16 activations (digit
+            // bytes) and 16 codes per lane
             const int t = w * U::kSteps + s;
-            long av[MT];
+            v4i av[MT];
 #pragma unroll
-            for (int m = 0; m < MT; ++m) av[m] = *reinterpret_cast<const long*>(abase[m] + t * 128);
-            const long cb = U::codes(ring[i], g, t);
+            for (int m = 0; m < MT; ++m) av[m] = *reinterpret_cast<const v4i*>(abase[m] + (t >> 1) * 256);
+            const long c0 = U::codes(ring[i], g, t), c1 = U::codes(ring[i], g, t + 1);
+            const v4i cb = {static_cast<int>(c0), static_cast<int>(c0 >> 32), static_cast<int>(c1),
+                            static_cast<int>(c1 >> 32)};
 #pragma unroll
-            for (int m = 0; m < MT; ++m) c[m] = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[m], cb, c[m], 0, 0, 0);
+            for (int m = 0; m < MT; ++m) c[m] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[m], cb, c[m], 0, 0, 0);
           }
           const int h = U::kSteps == 4 ? w : (w >> 1);
 #pragma unroll
@@ -391,6 +403,8 @@ __global__ __launch_bounds__(64 * SW * WC) void gemv_mfma_kernel(GemvMfmaArgs a)
   if (sw == 0 && g == 0 && n_out < a.w.n) {
     [[maybe_unused]] uint32_t bad = 0;  // rows whose result is not finite
     [[maybe_unused]] float rv = 0.0f;
+    // a K part's partial sums (checked for non-finite values when summed)
+    float* const yout = a.ksplit > 1 ? a.part + static_cast<uint64_t>(blockIdx.y) * M * a.w.n : a.y;
 #pragma unroll
     for (int m = 0; m < MT; ++m) {
       if (m >= M) break;
@@ -405,12 +419,12 @@ __global__ __launch_bounds__(64 * SW * WC) void gemv_mfma_kernel(GemvMfmaArgs a)
         }
       }
       if constexpr (XS == kXPlain) bad |= static_cast<uint32_t>(!__builtin_isfinite(v)) << m;
-      a.y[static_cast<uint64_t>(m) * a.w.n + n_out] = v;
+      yout[static_cast<uint64_t>(m) * a.w.n + n_out] = v;
     }
     if constexpr (XS == kXPlain) {
       // NaN or infinite activations (or an overflow): the reference's own
       // order decides which outputs are NaN and which +-Inf
-      if (bad) {
+      if (bad && a.ksplit == 1) {
 #pragma unroll 1
         for (int m = 0; m < M; ++m) {
           if (!((bad >> m) & 1u)) continue;
@@ -473,7 +487,8 @@ hipError_t launch4(GemvMfmaArgs a, hipStream_t st, uint32_t chunk_target = 0) {
                                        hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(bytes));
     if (e != hipSuccess) return e;
   }
-  hipLaunchKernelGGL(kern, dim3((a.w.tiles + WC - 1) / WC), dim3(64 * SW * WC), bytes, st, a);
+  if (a.ksplit > 1 && (!kPre || a.part == nullptr || a.split_units != a.chunk_units)) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(kern, dim3((a.w.tiles + WC - 1) / WC, a.ksplit), dim3(64 * SW * WC), bytes, st, a);
   return hipGetLastError();
 }
 
@@ -484,15 +499,20 @@ hipError_t launch_split(const GemvMfmaArgs& a, int sw, hipStream_t st) {
   const uint32_t cap = (kMaxLds - kZeroBytes) / (MT * kUnitRecBytes);
   const uint32_t chunk = a.w.units < cap ? a.w.units : cap;
   if constexpr (MT >= 2) {
-    // Two or more rows copy prebuilt activation records, so small K chunks
-    // cost little: chunks of 8 units (4 at 16 rows), 4 wavefronts of one tile
-    // each holding 2 (1 at 8+ rows) units per chunk, so that several
-    // workgroups fit a CU's LDS.
+    // Two or more rows read activation records built once per call. Every
+    // tile needs all of them, so the records a workgroup copies into LDS are
+    // shared by four tiles (one wavefront each), and K is split over the
+    // grid's y dimension in parts of gemv_pre_units(MT) units: a workgroup
+    // copies its part's records once and each wavefront holds its tile's
+    // whole part in flight; the parts' partial sums are added in order by the
+    // split-K sum (a.part, a.ksplit set by the caller: gemv_pre_splits).
     (void)sw;
     (void)chunk;
-    if constexpr (MT >= 16) return launch4<QT, WIDE, MT, 4, 1, 1>(a, st, 4);
-    else if constexpr (MT >= 8) return launch4<QT, WIDE, MT, 4, 1, 1>(a, st, 4);
-    else return launch4<QT, WIDE, MT, 4, 2, 1>(a, st, 8);
+    constexpr uint32_t kUs = MT >= 16 ? 2 : 4;
+    GemvMfmaArgs b = a;
+    b.split_units = kUs;
+    if (b.ksplit != (b.w.units + kUs - 1) / kUs) return hipErrorInvalidValue;
+    return launch4<QT, WIDE, MT, 1, kUs, 4>(b, st, kUs);
   } else {
     if (sw == 4) {
       // Two tiles share the activation prep (an 8-wavefront workgroup) where
@@ -519,8 +539,8 @@ hipError_t launch_split(const GemvMfmaArgs& a, int sw, hipStream_t st) {
       // 14.1 against 15.7); more tiles: 8 wavefronts with the whole run in
       // flight (N = 14336: 21.9 against 24.1 us for 8 x 2)
       if (a.w.tiles <= 2 * kCUs) return launch4<QT, WIDE, MT, 16, 2, 1, XS>(a, st);
-      // (Q5_K and Q6_K with the norm prep spill registers at 8 units deep)
-      constexpr bool deep = XS != kXNorm || (QT != kQ5_K && QT != kQ6_K);
+      // (Q5_K, and Q6_K with the norm prep, spill registers at 8 units deep)
+      constexpr bool deep = QT != kQ5_K && (XS != kXNorm || QT != kQ6_K);
       if constexpr (deep) {
         if (upw > 4) return launch4<QT, WIDE, MT, 8, 8, 1, XS>(a, st);
       }
@@ -562,6 +582,11 @@ hipError_t launch_w(const GemvMfmaArgs& a, bool wide, int mt, int sw, hipStream_
 
 bool gemv_mfma_supported(int32_t qtype, int32_t layout, uint64_t k) {
   return layout == kOutputRows && qtype >= kQ8_0 && qtype <= kQ6_K && k % 256 == 0 && k > 0;
+}
+
+uint32_t gemv_pre_splits(uint64_t k, uint32_t m) {
+  const uint64_t us = m >= 9 ? 2 : 4;  // units per K part (the MT >= 16 kernel takes 2)
+  return static_cast<uint32_t>((k / 256 + us - 1) / us);
 }
 
 int gemv_mfma_split(uint64_t k, uint64_t n) {

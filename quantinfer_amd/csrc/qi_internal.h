@@ -48,6 +48,11 @@ struct GemvMfmaArgs {
   // the 8 up rows of the same outputs, and y[8 t + c] = g / (1 + exp(-g)) * u
   // (backends/cpu/src/backend.rs:224-237), N / 2 outputs
   bool silu_pairs = false;
+  // two or more rows: K parts over the grid (gemv_pre_splits), partial sums
+  // [ksplit][m][n] in `part` when ksplit > 1, added by launch_splitk_sum
+  float* part = nullptr;
+  uint32_t ksplit = 1;
+  uint32_t split_units = 0;  // set by the launcher
 };
 bool gemv_mfma_supported(int32_t qtype, int32_t layout, uint64_t k);
 // Activation records of m rows (digits + window scales, the GEMV's LDS layout)
@@ -56,6 +61,12 @@ hipError_t launch_gemv_digits(int32_t qtype, const float* x, uint64_t k, uint32_
                               hipStream_t st);
 uint64_t gemv_digits_bytes(uint64_t k, uint32_t m);
 int gemv_mfma_split(uint64_t k, uint64_t n);
+// K parts of a 2..16-row GEMV launch (its partial sums: parts * m * n floats)
+uint32_t gemv_pre_splits(uint64_t k, uint32_t m);
+// y[i] = sum over s of part[s * stride + i] (i < count = m * n) in split order;
+// a non-finite sum is recomputed in the reference's order
+hipError_t launch_splitk_sum(const Image& im, const View& v, const float* part, uint32_t splits,
+                             uint64_t count, uint64_t stride, float* y, const float* x, hipStream_t st);
 hipError_t launch_gemv_mfma(int32_t qtype, bool wide, int mt, int split, const GemvMfmaArgs& a,
                             hipStream_t st);
 
