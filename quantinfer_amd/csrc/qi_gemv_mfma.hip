@@ -162,7 +162,8 @@ __device__ __forceinline__ void store_half(const HalfX& o, const Item& it, bool 
 // in the final reduction, so the norm adds no barrier. One row: a.radd adds
 // the residual to the outputs, a.silu_pairs combines gate/up output pairs.
 template <int QT, bool WIDE, int MT, int SW, int D, int WC, bool PRE, int XS = kXPlain>
-__global__ __launch_bounds__(64 * SW * WC) void gemv_mfma_kernel(GemvMfmaArgs a) {
+__global__ __launch_bounds__(64 * SW * WC, (QT == kQ4_K && MT == 1 && SW == 4) ? 4 : 1)
+void gemv_mfma_kernel(GemvMfmaArgs a) {
   using U = Unit<QT>;
   constexpr int kThreads = 64 * SW * WC;
   constexpr int XP = SW == 8 ? 2 : 1;
@@ -519,14 +520,20 @@ hipError_t launch_split(const GemvMfmaArgs& a, int sw, hipStream_t st) {
       // that does not raise the most tiles any CU streams, with workgroups
       // spread evenly over the CUs: ceil(tiles / 256) one-tile workgroups
       // against 2 ceil(tiles / 512) two-tile ones (896 tiles: 4 and 4, so
-      // the shared prep wins; 768: 3 against 4). Only Q4_K and Q8_0 keep
-      // their occupancy at 8 wavefronts (measured on MI355X: Q4_0, Q5_K and
-      // Q6_K lose), and above 1024 tiles the workgroups no longer all fit
-      // at once.
-      if constexpr (QT == kQ4_K || QT == kQ8_0) {
-        const uint64_t t = a.w.tiles;
-        const uint64_t one = (t + kCUs - 1) / kCUs, two = 2 * ((t + 2 * kCUs - 1) / (2 * kCUs));
-        if (two <= one && t <= 4 * kCUs) return launch4<QT, WIDE, MT, 4, 4, 2, XS>(a, st);
+      // the shared prep wins; 768: 3 against 4); above 1024 tiles the
+      // workgroups no longer all fit at once. With two workgroups on a CU
+      // the second one's activation loads queue behind the first one's
+      // weight loads, so the 4-bit K-quants then keep two units in flight per
+      // wavefront, not four (measured on MI355X at 896 tiles: Q4_K 7.9
+      // against 8.2 us, Q5_K 10.0 against 10.6, Q6_K 10.7 against 11.4; the
+      // 8-bit and Q4_0 codes do not gain).
+      const uint64_t t = a.w.tiles;
+      const uint64_t one = (t + kCUs - 1) / kCUs, two = 2 * ((t + 2 * kCUs - 1) / (2 * kCUs));
+      if (two <= one && t <= 4 * kCUs) {
+        if constexpr (QT == kQ4_K || QT == kQ5_K || QT == kQ6_K) {
+          if (t > 2 * kCUs) return launch4<QT, WIDE, MT, 4, 2, 2, XS>(a, st);
+        }
+        return launch4<QT, WIDE, MT, 4, 4, 2, XS>(a, st);
       }
       return launch4<QT, WIDE, MT, 4, 4, 1, XS>(a, st);
     }
