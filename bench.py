@@ -195,6 +195,169 @@ def copy_calibration(steps: int, mib: int = 256) -> None:
 
 MFMA_F16_PEAK_TFLOPS = 2500.0
 
+# Sizes of the streaming-read calibration: the decode GEMV weights at the
+# Qwen3-8B projection shapes (Q4_K 4096x4096, 4096x6144, 12288x4096,
+# 4096x14336, 4096x24576; Q8_0 4096x14336), then 512 MB and 1 GiB.
+CALIB_BYTES = [9437184, 14155776, 28311552, 33030144, 56623104, 62390272, 509607936, 1073741824]
+
+
+def calib_bench(steps: int = 10) -> dict:
+    """Plain streaming reads (quantinfer_amd/calib, not the product library)
+    at the GEMV weight sizes, timed as gemv_bench times the GEMV: back to
+    back over resident zero-filled buffers (at least 512 MB in all), HIP
+    events on the launch stream, best of three regions. The ceiling a kernel
+    that reads each byte once reaches at that size with this launch pattern."""
+    import ctypes
+
+    from quantinfer_amd import build as qb, hiprt
+
+    if not os.path.exists(qb.CALIB_LIB):
+        raise RuntimeError(f"{qb.CALIB_LIB} is not built (python quantinfer_amd/build.py)")
+    cal = ctypes.CDLL(qb.CALIB_LIB)
+    cal.qi_calib_stream_read.argtypes = [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_int32, ctypes.c_uint64,
+                                         ctypes.c_void_p, ctypes.c_void_p]
+    sink = hiprt.DeviceBuffer(4096)
+    stream = hiprt.Stream()
+    patterns = [("grid-stride", 0, w) for w in (512, 1024, 2048, 4096)] + \
+               [("chunk", 1, c) for c in (36864, 73728)]
+    rows = []
+    for nbytes in CALIB_BYTES:
+        copies = max(1, -(-512_000_000 // nbytes))
+        bufs = [hiprt.DeviceBuffer(nbytes) for _ in range(copies)]
+        for b in bufs:
+            b.zero()
+        for name, pat, param in patterns:
+            def step():
+                for b in bufs:
+                    err = cal.qi_calib_stream_read(b.ptr, nbytes, pat, param, sink.ptr, stream.handle)
+                    if err:
+                        raise RuntimeError(f"qi_calib_stream_read: HIP error {err}")
+            for _ in range(3):
+                step()
+            stream.synchronize()
+            n = max(steps, -(-2_000_000_000 // (nbytes * copies)))
+            best = None
+            for _ in range(3):
+                a, b = hiprt.Event(), hiprt.Event()
+                a.record(stream)
+                for _ in range(n):
+                    step()
+                b.record(stream)
+                us = a.elapsed_ms(b) * 1e3 / (n * copies)
+                best = us if best is None else min(best, us)
+                a.destroy()
+                b.destroy()
+            rows.append({"bytes": nbytes, "pattern": name,
+                         "param": f"{param} workgroups" if pat == 0 else f"{param} B per workgroup",
+                         "us_per_read": round(best, 3), "gb_s": round(nbytes / best / 1e3, 1)})
+        for b in bufs:
+            b.free()
+    sink.free()
+    stream.destroy()
+    best = {}
+    for r in rows:
+        if r["bytes"] not in best or r["gb_s"] > best[r["bytes"]]["gb_s"]:
+            best[r["bytes"]] = r
+    return {"calibration": "streaming_read", "unit": "GB/s", "peak": HBM_PEAK_GBPS,
+            "note": "plain non-temporal 16-byte loads, event-timed back to back like the GEMV; "
+                    "best pattern per size below, every pattern in `rows`",
+            "best": [{"bytes": b, "gb_s": r["gb_s"], "frac": round(r["gb_s"] / HBM_PEAK_GBPS, 4),
+                      "us_per_read": r["us_per_read"], "pattern": f"{r['pattern']} ({r['param']})"}
+                     for b, r in sorted(best.items())],
+            "rows": rows}
+
+
+def timeline_bench(qtype: int, k: int, n: int) -> dict:
+    """Workgroup timeline of the M=1 GEMV from the profiling build
+    (libqi_hip_timeline.so, python quantinfer_amd/build.py --timeline): the
+    launch stream runs passes over resident weight copies as gemv_bench does;
+    the stamps of the last launch are read back. Times are microseconds from
+    the first workgroup's start (100 MHz clock), as percentiles over
+    workgroups."""
+    import ctypes
+
+    import numpy as np
+
+    import quantinfer_amd as qa
+    from quantinfer_amd import build as qb, hiprt
+
+    if not os.path.exists(qb.TIMELINE_LIB):
+        raise RuntimeError(f"{qb.TIMELINE_LIB} is not built (python quantinfer_amd/build.py --timeline)")
+    qa.LIB_PATH = qb.TIMELINE_LIB
+    lib = qa.lib()
+    lib.qi_timeline_read.argtypes = [ctypes.c_void_p, ctypes.c_uint64]
+    ctx = qa.Context(0)
+    blocks = weight_blocks(qtype, k, n, seed=0x5EED0000 + qtype)
+    wbytes = n * (k // BLOCK[qtype]) * WIRE[qtype]
+    copies = max(2, -(-512_000_000 // wbytes))
+    weights = [ctx.weights(qtype, qa.OUTPUT_ROWS, k, n, blocks) for _ in range(copies)]
+    x = hiprt.DeviceBuffer.from_array(normal(0x5EED1000, k).reshape(1, k))
+    y = hiprt.DeviceBuffer(n * 4)
+    stream = hiprt.Stream()
+    for _ in range(4):
+        for w in weights:
+            w.linear_device(x.ptr, 1, y.ptr, qa.MODE_F32, stream.handle)
+    stream.synchronize()
+    if lib.qi_timeline_clear() != 0:
+        raise RuntimeError("qi_timeline_clear failed")
+    for w in weights:
+        w.linear_device(x.ptr, 1, y.ptr, qa.MODE_F32, stream.handle)
+    stream.synchronize()
+    ts = np.zeros(8192 * 8, dtype=np.uint64)
+    if lib.qi_timeline_read(ts.ctypes.data, ts.size) != 0:
+        raise RuntimeError("qi_timeline_read failed")
+    ts = ts.reshape(8192, 8)
+    used = ts[:, 0] > 0
+    t = ts[used].astype(np.int64)
+    rel = (t[:, :5] - t[:, 0].min()) / 100.0  # 100 MHz ticks -> us
+    # HW_ID bits 8-11 CU, 12 shader array, 13-15 shader engine; plus the XCD
+    cus = {(int(r[6]), int(r[5]) >> 8 & 0xFF) for r in ts[used]}
+    pct = (0, 10, 50, 90, 100)
+
+    def dist(v):
+        return {f"p{p}": round(float(np.percentile(v, p)), 3) for p in pct}
+
+    for w in weights:
+        w.free()
+    x.free()
+    y.free()
+    stream.destroy()
+    ctx.close()
+    return {
+        "timeline": f"{QNAME[qtype]}_gemv_output_rows_m1_k{k}_n{n}", "workgroups": int(used.sum()),
+        "compute_units": len(cus), "weight_bytes": wbytes, "unit": "us from the first workgroup's start",
+        "start": dist(rel[:, 0]), "records_in_lds": dist(rel[:, 1]), "first_batch_done": dist(rel[:, 2]),
+        "units_done": dist(rel[:, 3]), "epilogue": dist(rel[:, 4]),
+        "prep_wait": dist(rel[:, 1] - rel[:, 0]), "after_prep_to_first_batch": dist(rel[:, 2] - rel[:, 1]),
+    }
+
+
+def library_f16_gemm(m: int, k: int, n: int, steps: int = 20) -> dict:
+    """The same GEMM shape as a plain f16 library GEMM (torch.matmul, which
+    calls hipBLASLt), operands resident, no dequantization: what a vendor
+    GEMM reaches at this shape on this box, for scale. Its own process
+    (--workload libgemm): torch bundles its own HIP runtime, and the second
+    runtime to start in a process finds no device."""
+    import torch
+
+    x = torch.randn(m, k, device="cuda", dtype=torch.float16)
+    w = torch.randn(n, k, device="cuda", dtype=torch.float16) * 0.02
+    for _ in range(5):
+        x @ w.t()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(steps):
+        x @ w.t()
+    b.record()
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / steps
+    tflops = 2.0 * m * n * k / (ms * 1e-3) / 1e12
+    del x, w
+    torch.cuda.empty_cache()
+    return {"what": "torch.matmul f16 (hipBLASLt), x[m,k] @ w[n,k]^T", "value": round(tflops, 1),
+            "unit": "TFLOP/s", "frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4), "ms": round(ms, 5)}
+
 
 def gemm_bench(qtype: int, m: int, k: int, n: int, steps: int, warmup: int) -> dict:
     """Prefill GEMM (MFMA mode, f16 operands, f32 accumulation): `steps`
@@ -570,10 +733,13 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="time device-to-device copies of 256 MiB instead (counter calibration)")
-    ap.add_argument("--workload", choices=["gemv", "gemm", "e2e", "f32head"], default="gemv",
+    ap.add_argument("--workload", choices=["gemv", "gemm", "e2e", "f32head", "calib", "timeline", "libgemm"],
+                    default="gemv",
                     help="gemv: the headline decode GEMV with the Q8_0 GEMV, the GEMMs and the e2e "
                          "decode line embedded (default); gemm: one MFMA prefill GEMM; e2e: "
-                         "Qwen3-8B-shape decode only")
+                         "Qwen3-8B-shape decode only; calib: streaming-read ceilings (measurement "
+                         "aid); timeline: the M=1 GEMV's workgroup timeline (profiling build); "
+                         "libgemm: the GEMM shape as a plain f16 library GEMM, for scale")
     ap.add_argument("--no-e2e", action="store_true", help="gemv: leave out the e2e decode run")
     ap.add_argument("--no-gemm", action="store_true", help="gemv: leave out the GEMM objects")
     ap.add_argument("--cpu-simd", action="store_true",
@@ -603,6 +769,21 @@ def main():
         return
     if args.workload == "f32head":
         print(json.dumps(f32_head_bench(args.steps, args.warmup)))
+        return
+    if args.workload == "libgemm":
+        m, k, n = (int(v) for v in (args.mkn or "2048,4096,12288").split(","))
+        out = library_f16_gemm(m, k, n, max(args.steps, 20))
+        out.update({"m": m, "k": k, "n": n})
+        print(json.dumps(out))
+        return
+    if args.workload == "calib":
+        print(json.dumps(calib_bench(args.steps)))
+        return
+    if args.workload == "timeline":
+        m, k, n = (int(v) for v in (args.mkn or f"{M},{K},{N}").split(","))
+        if m != 1:
+            sys.exit("bench.py --workload timeline: the stamps cover the one-row GEMV (M=1)")
+        print(json.dumps(timeline_bench(qt, k, n)))
         return
 
     m, k, n = (int(v) for v in (args.mkn or f"{M},{K},{N}").split(","))

@@ -17,11 +17,17 @@ import os
 import re
 import shutil
 import subprocess
+import sys
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libqi_hip.so")
+# profiling build: the same sources with the GEMV's timeline stamps compiled in
+TIMELINE_LIB = os.path.join(HERE, "libqi_hip_timeline.so")
+# measurement aid (bench.py --workload calib): plain streaming reads
+CALIB_SRC = os.path.join(HERE, "calib", "stream_read.hip")
+CALIB_LIB = os.path.join(HERE, "calib", "libqi_calib.so")
 
 def read_sources() -> list:
     """The translation units, from csrc/sources.txt (shared with the Rust
@@ -68,10 +74,11 @@ def _resources(stderr: str) -> dict:
     return out
 
 
-def _compile(src: str):
-    obj = os.path.join(BUILD, os.path.splitext(src)[0] + ".o")
+def _compile(src: str, timeline: bool = False):
+    obj = os.path.join(BUILD, ("timeline_" if timeline else "") + os.path.splitext(src)[0] + ".o")
     lang = ["-x", "hip"] if src.endswith(".cpp") else []
-    cmd = [hipcc(), *lang, *FLAGS, "-Rpass-analysis=kernel-resource-usage", "-c",
+    defs = ["-DQI_TIMELINE"] if timeline else []
+    cmd = [hipcc(), *lang, *FLAGS, *defs, "-Rpass-analysis=kernel-resource-usage", "-c",
            os.path.join(CSRC, src), "-o", obj]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
@@ -79,29 +86,48 @@ def _compile(src: str):
     return obj, _resources(res.stderr)
 
 
-def build(verbose: bool = False) -> str:
+def build_calib(verbose: bool = False) -> str:
+    """libqi_calib.so, the streaming-read calibration of bench.py --workload calib."""
+    tmp = CALIB_LIB + ".tmp"
+    cmd = [hipcc(), *FLAGS, "-shared", CALIB_SRC, "-o", tmp]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc failed for {CALIB_SRC}:\n{res.stderr}")
+    os.replace(tmp, CALIB_LIB)
+    if verbose:
+        print(CALIB_LIB)
+    return CALIB_LIB
+
+
+def build(verbose: bool = False, timeline: bool = False) -> str:
+    """libqi_hip.so (and the calibration library), or with timeline=True the
+    profiling build libqi_hip_timeline.so."""
     os.makedirs(BUILD, exist_ok=True)
     with concurrent.futures.ThreadPoolExecutor(max_workers=min(8, len(SOURCES))) as ex:
-        done = list(ex.map(_compile, SOURCES))
+        done = list(ex.map(lambda src: _compile(src, timeline), SOURCES))
     objs = [o for o, _ in done]
     kernels = {name: r for _, res in done for name, r in res.items()}
-    with open(os.path.join(BUILD, "kernel_resources.json"), "w") as f:
-        json.dump(kernels, f, indent=1, sort_keys=True)
+    if not timeline:
+        with open(os.path.join(BUILD, "kernel_resources.json"), "w") as f:
+            json.dump(kernels, f, indent=1, sort_keys=True)
     spills = sorted(n for n, r in kernels.items()
                     if r.get("scratch", 0) or r.get("vgpr_spill", 0) or r.get("sgpr_spill", 0))
     if spills:
         raise RuntimeError("kernels spill registers to scratch memory (see _build/kernel_resources.json): "
                            + ", ".join(spills))
-    tmp = LIB + ".tmp"
+    out = TIMELINE_LIB if timeline else LIB
+    tmp = out + ".tmp"
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs, *LINK]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stderr}")
-    os.replace(tmp, LIB)
+    os.replace(tmp, out)
     if verbose:
-        print(LIB)
-    return LIB
+        print(out)
+    if not timeline:
+        build_calib(verbose)
+    return out
 
 
 if __name__ == "__main__":
-    build(verbose=True)
+    build(verbose=True, timeline="--timeline" in sys.argv[1:])

@@ -57,6 +57,30 @@ constexpr uint32_t kUnitRecBytes = kUnitDigitBytes + kUnitAuxBytes;
 constexpr uint32_t kMaxLds = 160 * 1024;
 constexpr uint64_t kCUs = 256;  // compute units of an MI355X (gfx950), for the work split
 
+// Profiling build only (quantinfer_amd/build.py --timeline makes
+// libqi_hip_timeline.so with QI_TIMELINE defined): per workgroup of the last
+// GEMV launch, the 100 MHz constant clock at kernel entry, once the
+// activation records are in LDS, after the first batch of units, after the
+// last unit and before the epilogue, plus the hardware and XCD ids; read back
+// with qi_timeline_read. In the product build the stamps compile to nothing.
+#ifdef QI_TIMELINE
+constexpr uint32_t kTimelineSlots = 8192;
+__device__ uint64_t g_timeline[kTimelineSlots * 8];
+__device__ __forceinline__ void stamp(uint32_t slot, int i) {
+  g_timeline[(slot % kTimelineSlots) * 8 + i] = __builtin_amdgcn_s_memrealtime();
+}
+__device__ __forceinline__ void stamp_where(uint32_t slot) {
+  uint32_t hw, xcc;
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID)" : "=s"(hw));
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+  g_timeline[(slot % kTimelineSlots) * 8 + 5] = hw;
+  g_timeline[(slot % kTimelineSlots) * 8 + 6] = xcc;
+}
+#else
+__device__ __forceinline__ void stamp(uint32_t, int) {}
+__device__ __forceinline__ void stamp_where(uint32_t) {}
+#endif
+
 // Byte transpose of four digit words (one per activation) into four words
 // (one per digit): out[i] byte e = in[e] byte i.
 __device__ __forceinline__ void transpose4(const uint32_t in[4], uint32_t out[4]) {
@@ -175,6 +199,11 @@ void gemv_mfma_kernel(GemvMfmaArgs a) {
 
   const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const uint32_t sw = wave % SW, wc = wave / SW;
+  const uint32_t slot = blockIdx.y * gridDim.x + blockIdx.x;
+  if (tid == 0) {
+    stamp(slot, 0);
+    stamp_where(slot);
+  }
   const uint32_t col = lane & 15, g = lane >> 4;
   // the grid's last workgroup may hold a tile past the end: it streams the
   // last tile again and stores nothing
@@ -291,6 +320,7 @@ void gemv_mfma_kernel(GemvMfmaArgs a) {
       }
     }
     __syncthreads();
+    if (tid == 0) stamp(slot, 1);
 
     // ---- main: this wavefront's units, D in flight ----
     // The first batch is straight-line code on the registers loaded above (a
@@ -352,6 +382,7 @@ void gemv_mfma_kernel(GemvMfmaArgs a) {
       }
     };
     consume(0);
+    if (tid == 0) stamp(slot, 2);
     for (uint32_t j = D; j < u_count; j += D) {
 #pragma unroll
       for (int i = 0; i < D; ++i)
@@ -361,6 +392,7 @@ void gemv_mfma_kernel(GemvMfmaArgs a) {
     __syncthreads();  // LDS reused by the next chunk / the reduction
   }
 
+  if (tid == 0) stamp(slot, 3);
   // ---- reduce: 4 lane groups of a column, then the SW K-parts ----
 #pragma unroll
   for (int m = 0; m < MT; ++m) {
@@ -401,6 +433,7 @@ void gemv_mfma_kernel(GemvMfmaArgs a) {
       return;
     }
   }
+  if (tid == 0) stamp(slot, 4);
   if (sw == 0 && g == 0 && n_out < a.w.n) {
     [[maybe_unused]] uint32_t bad = 0;  // rows whose result is not finite
     [[maybe_unused]] float rv = 0.0f;
@@ -619,3 +652,15 @@ hipError_t launch_gemv_mfma(int32_t qtype, bool wide, int mt, int sw, const Gemv
 }
 
 }  // namespace qi
+
+#ifdef QI_TIMELINE
+// Copy the first n words of the timeline ([slot][8]) to host memory, or zero it.
+extern "C" int qi_timeline_read(uint64_t* host, uint64_t n) {
+  if (n > qi::kTimelineSlots * 8) return static_cast<int>(hipErrorInvalidValue);
+  return static_cast<int>(hipMemcpyFromSymbol(host, HIP_SYMBOL(qi::g_timeline), n * 8, 0, hipMemcpyDeviceToHost));
+}
+extern "C" int qi_timeline_clear(void) {
+  static uint64_t zeros[qi::kTimelineSlots * 8];
+  return static_cast<int>(hipMemcpyToSymbol(HIP_SYMBOL(qi::g_timeline), zeros, sizeof(zeros), 0, hipMemcpyHostToDevice));
+}
+#endif

@@ -71,6 +71,9 @@ class DeviceBuffer:
         _ok(hip().hipMemcpy(out.ctypes.data, self.ptr, out.nbytes, D2H), "hipMemcpy D2H")
         return out
 
+    def zero(self) -> None:
+        _ok(hip().hipMemset(self.ptr, 0, self.nbytes), "hipMemset")
+
     def copy_from(self, src: "DeviceBuffer", nbytes: int, stream: "Stream") -> None:
         """Device-to-device copy on `stream` (the HIP runtime's copy kernel)."""
         _ok(hip().hipMemcpyAsync(self.ptr, src.ptr, nbytes, D2D, stream.handle), "hipMemcpyAsync D2D")

@@ -31,6 +31,20 @@ def test_library_exports_every_declared_symbol():
     assert lib.qi_hip_abi_version() == 1
 
 
+def test_measurement_libraries_stay_out_of_the_product():
+    """The streaming-read calibration lives in its own library and the
+    timeline stamps only in the profiling build: the product library exports
+    neither."""
+    from quantinfer_amd import build as qb
+    lib_syms = open(qa.LIB_PATH, "rb").read()
+    assert b"qi_timeline_read" not in lib_syms and b"qi_calib_stream_read" not in lib_syms
+    cal = ctypes.CDLL(qb.CALIB_LIB)
+    assert hasattr(cal, "qi_calib_stream_read")
+    if os.path.exists(qb.TIMELINE_LIB):
+        tl = ctypes.CDLL(qb.TIMELINE_LIB)
+        assert hasattr(tl, "qi_timeline_read") and hasattr(tl, "qi_timeline_clear")
+
+
 def test_block_structs_match_reference_layout():
     for q in ALL_Q:
         assert qa.BLOCK_DTYPES[q] == po.BLOCK_DTYPES[q]
