@@ -267,13 +267,15 @@ def calib_bench(steps: int = 10) -> dict:
             "rows": rows}
 
 
-def timeline_bench(qtype: int, k: int, n: int) -> dict:
-    """Workgroup timeline of the M=1 GEMV from the profiling build
+def timeline_bench(qtype: int, k: int, n: int, m: int = 1) -> dict:
+    """Workgroup timeline of the decode GEMV kernel from the profiling build
     (libqi_hip_timeline.so, python quantinfer_amd/build.py --timeline): the
     launch stream runs passes over resident weight copies as gemv_bench does;
     the stamps of the last launch are read back. Times are microseconds from
     the first workgroup's start (100 MHz clock), as percentiles over
-    workgroups."""
+    workgroups. With two or more rows the stamps cover the GEMV kernel
+    between the activation-record and split-K-sum kernels; "activations in
+    LDS" is then the records' copy into LDS."""
     import ctypes
 
     import numpy as np
@@ -291,17 +293,17 @@ def timeline_bench(qtype: int, k: int, n: int) -> dict:
     wbytes = n * (k // BLOCK[qtype]) * WIRE[qtype]
     copies = max(2, -(-512_000_000 // wbytes))
     weights = [ctx.weights(qtype, qa.OUTPUT_ROWS, k, n, blocks) for _ in range(copies)]
-    x = hiprt.DeviceBuffer.from_array(normal(0x5EED1000, k).reshape(1, k))
-    y = hiprt.DeviceBuffer(n * 4)
+    x = hiprt.DeviceBuffer.from_array(normal(0x5EED1000, m * k).reshape(m, k))
+    y = hiprt.DeviceBuffer(m * n * 4)
     stream = hiprt.Stream()
     for _ in range(4):
         for w in weights:
-            w.linear_device(x.ptr, 1, y.ptr, qa.MODE_F32, stream.handle)
+            w.linear_device(x.ptr, m, y.ptr, qa.MODE_F32, stream.handle)
     stream.synchronize()
     if lib.qi_timeline_clear() != 0:
         raise RuntimeError("qi_timeline_clear failed")
     for w in weights:
-        w.linear_device(x.ptr, 1, y.ptr, qa.MODE_F32, stream.handle)
+        w.linear_device(x.ptr, m, y.ptr, qa.MODE_F32, stream.handle)
     stream.synchronize()
     ts = np.zeros(8192 * 8, dtype=np.uint64)
     if lib.qi_timeline_read(ts.ctypes.data, ts.size) != 0:
@@ -324,7 +326,7 @@ def timeline_bench(qtype: int, k: int, n: int) -> dict:
     stream.destroy()
     ctx.close()
     return {
-        "timeline": f"{QNAME[qtype]}_gemv_output_rows_m1_k{k}_n{n}", "workgroups": int(used.sum()),
+        "timeline": f"{QNAME[qtype]}_gemv_output_rows_m{m}_k{k}_n{n}", "workgroups": int(used.sum()),
         "compute_units": len(cus), "weight_bytes": wbytes, "unit": "us from the first workgroup's start",
         "start": dist(rel[:, 0]), "records_in_lds": dist(rel[:, 1]), "first_batch_done": dist(rel[:, 2]),
         "units_done": dist(rel[:, 3]), "epilogue": dist(rel[:, 4]),
@@ -781,9 +783,9 @@ def main():
         return
     if args.workload == "timeline":
         m, k, n = (int(v) for v in (args.mkn or f"{M},{K},{N}").split(","))
-        if m != 1:
-            sys.exit("bench.py --workload timeline: the stamps cover the one-row GEMV (M=1)")
-        print(json.dumps(timeline_bench(qt, k, n)))
+        if not 1 <= m <= 16:
+            sys.exit("bench.py --workload timeline: the stamps cover the decode GEMV (M <= 16)")
+        print(json.dumps(timeline_bench(qtype=qt, k=k, n=n, m=m)))
         return
 
     m, k, n = (int(v) for v in (args.mkn or f"{M},{K},{N}").split(","))
