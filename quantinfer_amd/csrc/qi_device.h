@@ -311,7 +311,10 @@ struct Fast<kQ8_0, WIDE> {
 template <bool WIDE>
 struct Fast<kQ4_0, WIDE> {
   static constexpr int kSlotElems = 32, kPieces = 2;
-  static constexpr bool kHasMin = true;
+  // the offset enters the codes (q - 8, exact small integers), not a separate
+  // -8d * sum(x) term: a*sum(x q) - 8a*sum(x) cancels when the codes sit near
+  // 8, which costs f32 bits the reference's sum of x * d(q - 8) keeps
+  static constexpr bool kHasMin = false;
   struct Slot {
     uint4 q;
     float a;
@@ -323,9 +326,13 @@ struct Fast<kQ4_0, WIDE> {
   }
   // byte j holds element j (low nibble) and j+16 (high nibble)
   __device__ static uint32_t x_offset(uint32_t s, int p) { return s * 32 + 16 * p; }
-  __device__ static void codes(const Slot& o, int p, float q[16]) { nibbles16(o.q, p ? 4 : 0, q); }
+  __device__ static void codes(const Slot& o, int p, float q[16]) {
+    nibbles16(o.q, p ? 4 : 0, q);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) q[j] -= 8.0f;
+  }
   __device__ static float a(const Slot& o, int) { return o.a; }
-  __device__ static float b(const Slot& o, int) { return 8.0f * o.a; }
+  __device__ static float b(const Slot&, int) { return 0.0f; }
 };
 
 // Q4_K / Q5_K slot s = (super-block s/4, group g = s%4): 32 code bytes

@@ -1,4 +1,4 @@
-// Decode GEMV on the int8 matrix cores (v_mfma_i32_16x16x32_i8), output-rows
+// Decode GEMV on the int8 matrix cores (v_mfma_i32_16x16x64_i8), output-rows
 // layout, M <= 16 activation rows, K a multiple of 256.
 //
 // Arithmetic. The activations are cut into windows of 32 consecutive
@@ -34,8 +34,10 @@
 // from the neighbouring lane: a single barrier).
 // Each wavefront issues its activation loads, then the loads of up to D
 // units, before it waits for anything (vector loads complete in order, so
-// waiting for the activations never waits for the weights); a workgroup's
-// whole weight slice is in flight at once.
+// waiting for the activations never waits for the weights). Two or more
+// rows: a small kernel builds the activation records once per call, the
+// workgroups copy their K part's records into LDS, and the K parts' partial
+// sums are added in order by a separate kernel.
 // No state is shared between workgroups, so there are no device-scope fences.
 #include "qi_device.h"
 #include "qi_internal.h"

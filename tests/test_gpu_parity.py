@@ -226,6 +226,28 @@ def test_f32_gemv_split_k_deterministic(ctx, qtype):
             assert w.linear(x, qa.MODE_F32).tobytes() == y.tobytes()
 
 
+@pytest.mark.parametrize("qtype", [qa.Q8_0, qa.Q4_0], ids=lambda q: NAMES[q])
+@pytest.mark.parametrize("k", [96, 288, 4000])
+def test_planar_gemv_tolerance(ctx, qtype, k):
+    """K a multiple of 32 but not of 256: the planar image and its GEMV
+    (qi_gemv.hip), ragged N, 1 to 16 rows (one launch per 16-row chunk) and
+    17 (a second chunk)."""
+    for n in (1, 17, 100):
+        blocks = po.make_weights(qtype, k, n, seed=4300 + k + n + qtype, outliers=True)
+        w = ctx.weights(qtype, qa.OUTPUT_ROWS, k, n, blocks)
+        assert w.info().f16_scales == 1
+        for m in (1, 3, 16, 17):
+            x = po.fill_normal(4400 + m + n, m * k).reshape(m, k)
+            y = w.linear(x, qa.MODE_F32)
+            comp, norm, ok = _f32_checks(y, x, blocks, qtype, n)
+            # with one output per row the normwise check (1) is the elementwise
+            # relative error the tolerance section rules out for cancelled dot
+            # products (the CPU result's own error dominates); (2) and (3) hold
+            assert comp <= F32_TOL and ok and (n == 1 or norm <= F32_TOL), ((k, n, m), comp, norm, ok)
+            assert w.linear(x, qa.MODE_F32).tobytes() == y.tobytes()
+        w.free()
+
+
 def test_f32_gemv_unrounded_scales(ctx):
     # quantize_q8_0 output without storage rounding keeps f32 scales
     for qtype in (qa.Q8_0, qa.Q4_0):
