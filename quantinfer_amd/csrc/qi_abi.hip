@@ -225,11 +225,19 @@ qi_hip_status plan_linear(const Image& im, uint64_t m, int32_t mode, LinearPlan*
     if (m >= 2) {
       const uint32_t rows = static_cast<uint32_t>(m < 16 ? m : 16);
       p->d_floats = (qi::gemv_digits_bytes(im.k, rows) + 3) / 4;
-      // partial sums [parts][rows][n] of a 16-row chunk; a shorter last
-      // chunk (2..8 rows) may take more parts, so size for the larger count
-      const uint32_t parts = std::max(qi::gemv_pre_splits(im.k, 16), qi::gemv_pre_splits(im.k, 8));
+      // partial sums [parts][rows][n] of each 16-row chunk and of a shorter
+      // last chunk, which may take more parts
+      auto mt_of = [](uint64_t r) { return r == 1 ? 1 : r == 2 ? 2 : r <= 4 ? 4 : r <= 8 ? 8 : 16; };
+      uint64_t floats = 0;
+      uint32_t parts = 1;
+      for (uint64_t r : {static_cast<uint64_t>(rows), m > 16 ? m % 16 : 0}) {
+        if (r < 2) continue;
+        const uint32_t pr = qi::gemv_pre_splits(im.qtype, im.wide != 0, im.k, im.n, mt_of(r));
+        parts = std::max(parts, pr);
+        if (pr > 1) floats = std::max(floats, static_cast<uint64_t>(pr) * r * im.n);
+      }
       p->splits = parts;
-      if (parts > 1) p->s_floats = static_cast<uint64_t>(parts) * rows * im.n;
+      p->s_floats = floats;
     }
     return QI_HIP_OK;
   }
@@ -285,7 +293,7 @@ qi_hip_status enqueue_linear(const qi_hip_weights* w, const LinearPlan& p, const
                                               reinterpret_cast<uint8_t*>(dws), st),
                        "launch gemv activation records");
             ga.digits = reinterpret_cast<const uint8_t*>(dws);
-            ga.ksplit = qi::gemv_pre_splits(im.k, static_cast<uint32_t>(mt));
+            ga.ksplit = qi::gemv_pre_splits(im.qtype, im.wide != 0, im.k, im.n, mt);
             ga.part = sws;
           }
           const int split = w->ctx->gemv_split > 0 ? w->ctx->gemv_split : qi::gemv_mfma_split(im.k, im.n);

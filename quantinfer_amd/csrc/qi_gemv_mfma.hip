@@ -39,6 +39,9 @@
 // workgroups copy their K part's records into LDS, and the K parts' partial
 // sums are added in order by a separate kernel.
 // No state is shared between workgroups, so there are no device-scope fences.
+#include <atomic>
+#include <type_traits>
+
 #include "qi_device.h"
 #include "qi_internal.h"
 #include "qi_unit.h"
@@ -521,11 +524,75 @@ hipError_t launch4(GemvMfmaArgs a, hipStream_t st, uint32_t chunk_target = 0) {
   if (bytes > 65536) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(bytes));
-    if (e != hipSuccess) return e;
+    if (e != hipSuccess) {
+      (void)hipGetLastError();  // the next launch's check must not see this call's error
+      return e;
+    }
   }
   if (a.ksplit > 1 && (!kPre || a.part == nullptr || a.split_units != a.chunk_units)) return hipErrorInvalidValue;
   hipLaunchKernelGGL(kern, dim3((a.w.tiles + WC - 1) / WC, a.ksplit), dim3(64 * SW * WC), bytes, st, a);
   return hipGetLastError();
+}
+
+// Two or more rows: units in flight per wavefront (the K part is streamed in
+// batches of that many).
+template <int MT>
+constexpr int pre_depth() { return MT >= 16 ? 2 : 4; }
+
+// Workgroups of the 2-16 row kernel that fit a CU at once with K parts of
+// `chunk` units (registers and LDS; the HIP occupancy calculator), cached.
+template <int QT, bool WIDE, int MT>
+uint32_t pre_groups_per_cu(uint32_t chunk) {
+  static std::atomic<int> cache[17];
+  if (chunk > 16) return 0;
+  int n = cache[chunk].load(std::memory_order_relaxed);
+  if (n > 0) return static_cast<uint32_t>(n);
+  const uint32_t bytes = lds_bytes(MT, chunk, 4);
+  if (bytes > kMaxLds) return 0;
+  auto kern = gemv_mfma_kernel<QT, WIDE, MT, 1, pre_depth<MT>(), 4, true, kXPlain>;
+  if (bytes > 65536 && hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize,
+                                           static_cast<int>(bytes)) != hipSuccess) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, reinterpret_cast<const void*>(kern), 256, bytes) !=
+          hipSuccess || n < 1) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  cache[chunk].store(n, std::memory_order_relaxed);
+  return static_cast<uint32_t>(n);
+}
+
+// Units per K part of a 2-16 row launch. Every workgroup copies its part's
+// activation records into LDS and then streams its part, so a launch costs
+// about (rounds of resident workgroups) x (part length + one unit of copy
+// latency per round); the part length in {2, 4, 8, 16} units that minimizes
+// it is taken, ties to the longer part (fewer rounds, fewer partials).
+// Measured on MI355X (records kernel and split-K sum included): Q4_K
+// 4096x14336 M=8 30.4 -> 29.0 us (8 units), M=16 69.7 -> 61.5 (8), 14336x4096
+// M=8 33.5 -> 30.6 (8), Q6_K 4096x14336 M=8 49.8 -> 41.4 (16), Q4_0
+// 4096x12288 M=16 60.1 -> 53.1 (4).
+template <int QT, bool WIDE, int MT>
+uint32_t pre_units(uint64_t units, uint64_t tiles) {
+  const uint64_t groups = (tiles + 3) / 4;
+  uint64_t best = 0, best_cost = ~0ull;
+  for (uint32_t us : {2u, 4u, 8u, 16u}) {
+    const uint64_t chunk = us < units ? us : units;
+    const uint32_t per_cu = pre_groups_per_cu<QT, WIDE, MT>(static_cast<uint32_t>(chunk));
+    if (per_cu == 0) continue;
+    const uint64_t parts = (units + chunk - 1) / chunk;
+    const uint64_t slots = per_cu * kCUs;
+    const uint64_t rounds = (groups * parts + slots - 1) / slots;
+    const uint64_t cost = rounds * (chunk + 1);
+    if (cost <= best_cost) {
+      best_cost = cost;
+      best = chunk;
+    }
+    if (chunk == units) break;
+  }
+  return static_cast<uint32_t>(best ? best : 1);
 }
 
 // (wavefronts per workgroup, units in flight per wavefront) for `sw` and the
@@ -538,17 +605,17 @@ hipError_t launch_split(const GemvMfmaArgs& a, int sw, hipStream_t st) {
     // Two or more rows read activation records built once per call. Every
     // tile needs all of them, so the records a workgroup copies into LDS are
     // shared by four tiles (one wavefront each), and K is split over the
-    // grid's y dimension in parts of gemv_pre_units(MT) units: a workgroup
-    // copies its part's records once and each wavefront holds its tile's
-    // whole part in flight; the parts' partial sums are added in order by the
-    // split-K sum (a.part, a.ksplit set by the caller: gemv_pre_splits).
+    // grid's y dimension in parts of pre_units units: a workgroup copies its
+    // part's records once and each wavefront streams its tile's part; the
+    // parts' partial sums are added in order by the split-K sum (a.part,
+    // a.ksplit set by the caller: gemv_pre_splits).
     (void)sw;
     (void)chunk;
-    constexpr uint32_t kUs = MT >= 16 ? 2 : 4;
+    const uint32_t us = pre_units<QT, WIDE, MT>(a.w.units, a.w.tiles);
     GemvMfmaArgs b = a;
-    b.split_units = kUs;
-    if (b.ksplit != (b.w.units + kUs - 1) / kUs) return hipErrorInvalidValue;
-    return launch4<QT, WIDE, MT, 1, kUs, 4>(b, st, kUs);
+    b.split_units = us;
+    if (b.ksplit != (b.w.units + us - 1) / us) return hipErrorInvalidValue;
+    return launch4<QT, WIDE, MT, 1, pre_depth<MT>(), 4>(b, st, us);
   } else {
     if (sw == 4) {
       // Two tiles share the activation prep (an 8-wavefront workgroup) where
@@ -626,9 +693,30 @@ bool gemv_mfma_supported(int32_t qtype, int32_t layout, uint64_t k) {
   return layout == kOutputRows && qtype >= kQ8_0 && qtype <= kQ6_K && k % 256 == 0 && k > 0;
 }
 
-uint32_t gemv_pre_splits(uint64_t k, uint32_t m) {
-  const uint64_t us = m >= 9 ? 2 : 4;  // units per K part (the MT >= 16 kernel takes 2)
-  return static_cast<uint32_t>((k / 256 + us - 1) / us);
+uint32_t gemv_pre_splits(int32_t qtype, bool wide, uint64_t k, uint64_t n, int mt) {
+  const uint64_t units = k / 256, tiles = (n + 15) / 16;
+  auto by_mt = [&](auto qc, auto wc) -> uint32_t {
+    constexpr int QT = decltype(qc)::value;
+    constexpr bool W = decltype(wc)::value;
+    switch (mt) {
+      case 2: return pre_units<QT, W, 2>(units, tiles);
+      case 4: return pre_units<QT, W, 4>(units, tiles);
+      case 8: return pre_units<QT, W, 8>(units, tiles);
+      default: return pre_units<QT, W, 16>(units, tiles);
+    }
+  };
+  auto by_w = [&](auto qc) -> uint32_t {
+    return wide ? by_mt(qc, std::true_type{}) : by_mt(qc, std::false_type{});
+  };
+  uint32_t us = 1;
+  switch (qtype) {
+    case kQ8_0: us = by_w(std::integral_constant<int, kQ8_0>{}); break;
+    case kQ4_0: us = by_w(std::integral_constant<int, kQ4_0>{}); break;
+    case kQ4_K: us = by_w(std::integral_constant<int, kQ4_K>{}); break;
+    case kQ5_K: us = by_w(std::integral_constant<int, kQ5_K>{}); break;
+    default: us = by_w(std::integral_constant<int, kQ6_K>{}); break;
+  }
+  return static_cast<uint32_t>((units + us - 1) / us);
 }
 
 int gemv_mfma_split(uint64_t k, uint64_t n) {

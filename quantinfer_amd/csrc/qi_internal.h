@@ -62,7 +62,7 @@ hipError_t launch_gemv_digits(int32_t qtype, const float* x, uint64_t k, uint32_
 uint64_t gemv_digits_bytes(uint64_t k, uint32_t m);
 int gemv_mfma_split(uint64_t k, uint64_t n);
 // K parts of a 2..16-row GEMV launch (its partial sums: parts * m * n floats)
-uint32_t gemv_pre_splits(uint64_t k, uint32_t m);
+uint32_t gemv_pre_splits(int32_t qtype, bool wide, uint64_t k, uint64_t n, int mt);
 // y[i] = sum over s of part[s * stride + i] (i < count = m * n) in split order;
 // a non-finite sum is recomputed in the reference's order
 hipError_t launch_splitk_sum(const Image& im, const View& v, const float* part, uint32_t splits,
