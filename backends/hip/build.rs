@@ -4,7 +4,9 @@
 //! (`QI_HIP_SRC`, default `../../quantinfer_amd/csrc` from this crate), the
 //! list quantinfer_amd/build.py builds from, so the two builds compile the
 //! same files. The flags are build.py's: gfx950 only, no FMA contraction, no
-//! fast-math, f32 denormals kept, packed FP32 instructions off.
+//! fast-math, f32 denormals kept, packed FP32 instructions off, and the same
+//! per-file additions (the GEMV keeps its matrix-instruction results in
+//! ordinary VGPRs).
 use std::{env, fs, path::PathBuf, process::Command};
 
 const FLAGS: &[&str] = &[
@@ -20,6 +22,8 @@ const FLAGS: &[&str] = &[
     "-Xclang",
     "-packed-fp32-ops",
 ];
+
+const FILE_FLAGS: &[(&str, &[&str])] = &[("qi_gemv_mfma.hip", &["-mllvm", "-amdgpu-mfma-vgpr-form"])];
 
 fn main() {
     let manifest = PathBuf::from(env::var("CARGO_MANIFEST_DIR").unwrap());
@@ -42,8 +46,13 @@ fn main() {
             // host code in the same HIP translation model
             cmd.args(["-x", "hip"]);
         }
+        cmd.args(FLAGS);
+        for (name, extra) in FILE_FLAGS {
+            if name == file {
+                cmd.args(*extra);
+            }
+        }
         let status = cmd
-            .args(FLAGS)
             .arg("-c")
             .arg(src.join(file))
             .arg("-o")

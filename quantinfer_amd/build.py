@@ -49,6 +49,13 @@ FLAGS = [
 ]
 
 
+# Per-file code generation: the GEMV keeps its matrix-instruction results in
+# ordinary VGPRs (the accumulator-register form cost four moves per digit
+# sum read in its combine; its accumulators are small). The GEMMs keep the
+# default: their 128-register accumulator tiles need the accumulator file.
+FILE_FLAGS = {"qi_gemv_mfma.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+
+
 def hipcc() -> str:
     path = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
     if not os.path.exists(path):
@@ -78,8 +85,8 @@ def _compile(src: str, timeline: bool = False):
     obj = os.path.join(BUILD, ("timeline_" if timeline else "") + os.path.splitext(src)[0] + ".o")
     lang = ["-x", "hip"] if src.endswith(".cpp") else []
     defs = ["-DQI_TIMELINE"] if timeline else []
-    cmd = [hipcc(), *lang, *FLAGS, *defs, "-Rpass-analysis=kernel-resource-usage", "-c",
-           os.path.join(CSRC, src), "-o", obj]
+    cmd = [hipcc(), *lang, *FLAGS, *FILE_FLAGS.get(src, []), *defs, "-Rpass-analysis=kernel-resource-usage",
+           "-c", os.path.join(CSRC, src), "-o", obj]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{res.stderr}")

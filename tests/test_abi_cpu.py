@@ -474,6 +474,10 @@ def test_rust_crate_builds_the_same_sources_and_flags():
     rs_flags = re.findall(r'"([^"]+)"', flags)
     codegen = [f for f in qb.FLAGS if not f.startswith("-W")]
     assert rs_flags == codegen
+    per_file = re.search(r"const FILE_FLAGS: &\[\(&str, &\[&str\]\)\] = &\[(.*?)\];", rs, re.S).group(1)
+    rs_per_file = {m.group(1): re.findall(r'"([^"]+)"', m.group(2))
+                   for m in re.finditer(r'\("([^"]+)",\s*&\[(.*?)\]\)', per_file, re.S)}
+    assert rs_per_file == qb.FILE_FLAGS
 
 
 def test_rust_ffi_declares_every_header_function():
