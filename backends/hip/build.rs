@@ -23,7 +23,10 @@ const FLAGS: &[&str] = &[
     "-packed-fp32-ops",
 ];
 
-const FILE_FLAGS: &[(&str, &[&str])] = &[("qi_gemv_mfma.hip", &["-mllvm", "-amdgpu-mfma-vgpr-form"])];
+const FILE_FLAGS: &[(&str, &[&str])] = &[
+    ("qi_gemv_mfma.hip", &["-mllvm", "-amdgpu-mfma-vgpr-form"]),
+    ("qi_gemv_rows.hip", &["-mllvm", "-amdgpu-mfma-vgpr-form"]),
+];
 
 fn main() {
     let manifest = PathBuf::from(env::var("CARGO_MANIFEST_DIR").unwrap());

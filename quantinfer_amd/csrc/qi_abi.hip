@@ -220,8 +220,15 @@ qi_hip_status plan_linear(const Image& im, uint64_t m, int32_t mode, LinearPlan*
   }
   if (mode != QI_HIP_MODE_EXACT && qi::gemv_mfma_supported(im.qtype, im.layout, im.k)) {
     p->kind = LinearPlan::kMfma;
-    // two or more rows: activation records built once per 16-row chunk, and
-    // K parts over the grid whose partial sums are added in order
+    if (m >= 2 && qi::gemv_rows_supported(im.qtype, im.layout, im.k)) {
+      // two or more rows, dense operands: one kernel per 16-row chunk; K parts
+      // (the same count for every chunk) only for shapes with few tiles
+      p->splits = qi::gemv_rows_splits(im.k, im.n);
+      if (p->splits > 1) p->s_floats = static_cast<uint64_t>(p->splits) * (m < 16 ? m : 16) * im.n;
+      return QI_HIP_OK;
+    }
+    // two or more rows (Q6_K): activation records built once per 16-row chunk,
+    // and K parts over the grid whose partial sums are added in order
     if (m >= 2) {
       const uint32_t rows = static_cast<uint32_t>(m < 16 ? m : 16);
       p->d_floats = (qi::gemv_digits_bytes(im.k, rows) + 3) / 4;
@@ -286,7 +293,17 @@ qi_hip_status enqueue_linear(const qi_hip_weights* w, const LinearPlan& p, const
       for (uint64_t m0 = 0; m0 < m; m0 += 16) {
         const int rows = static_cast<int>(m - m0 < 16 ? m - m0 : 16);
         const int mt = rows == 1 ? 1 : rows == 2 ? 2 : rows <= 4 ? 4 : rows <= 8 ? 8 : 16;
-        if (p.kind == LinearPlan::kMfma) {
+        if (p.kind == LinearPlan::kMfma && rows >= 2 && qi::gemv_rows_supported(im.qtype, im.layout, im.k)) {
+          const float* xc = x + m0 * im.k;
+          float* const yc = y + m0 * im.n;
+          QI_HIP_TRY(qi::launch_gemv_rows(im.qtype, im.wide != 0, v, xc, rows, yc, sws, p.splits, st),
+                     "launch gemv rows");
+          if (p.splits > 1) {
+            const uint64_t count = static_cast<uint64_t>(rows) * im.n;
+            QI_HIP_TRY(qi::launch_splitk_sum(im, v, sws, p.splits, count, count, yc, xc, st),
+                       "launch gemv split-K sum");
+          }
+        } else if (p.kind == LinearPlan::kMfma) {
           qi::GemvMfmaArgs ga{v, x + m0 * im.k, y + m0 * im.n, rows};
           if (rows >= 2) {
             QI_HIP_TRY(qi::launch_gemv_digits(im.qtype, ga.x, im.k, static_cast<uint32_t>(rows),
