@@ -682,6 +682,16 @@ hipError_t launch_split(const GemvMfmaArgs& a, int sw, hipStream_t st) {
         }
         return launch4<QT, WIDE, MT, 4, 4, 2, XS>(a, st);
       }
+      if constexpr (QT == kQ4_K && MT == 1) {
+        // 1281-1536 tiles (the decoder's fused gate|up, N = 24576): four
+        // one-tile workgroups fit a CU at once, so the one-tile launch runs
+        // in two rounds and the second pays the activation round trip again.
+        // Six tiles per workgroup with two wavefronts each (8 units per
+        // wavefront, two in flight; 12 wavefronts, one workgroup per CU) run
+        // in one. Measured on MI355X: decode step of the Qwen3-8B-shape
+        // decoder 1.671 -> 1.626 ms; plain 4096 x 24576 11.6-11.9 -> 11.4 us.
+        if (t > 5 * kCUs && t <= 6 * kCUs) return launch4<QT, WIDE, MT, 2, 2, 6, XS>(a, st);
+      }
       return launch4<QT, WIDE, MT, 4, 4, 1, XS>(a, st);
     }
     const uint32_t upw = (chunk + 7) / 8;

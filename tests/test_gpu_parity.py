@@ -296,6 +296,20 @@ def test_config_shapes_f32_tolerance(ctx, cfg):
         assert reference_bound_ok(y, exact)
 
 
+@pytest.mark.parametrize("n", [20496, 20500, 24576, 24580])
+def test_q4_k_gemv_six_tile_workgroups(ctx, n):
+    """One row, K=4096, 1281-1536 output tiles: the six-tile, two-wavefront
+    launch (the decoder's fused gate|up shape, N=24576), a ragged last tile
+    (20500) and the one-tile launch just past its range (24580)."""
+    k = 4096
+    blocks = po.make_weights(qa.Q4_K, k, n, seed=0x5EED6000 + n, outliers=True)
+    w = ctx.weights(qa.Q4_K, qa.OUTPUT_ROWS, k, n, blocks)
+    x = po.fill_normal(0x5EED6100, k).reshape(1, k)
+    y = w.linear(x, qa.MODE_F32)
+    w.free()
+    _assert_f32(y, x, blocks, qa.Q4_K, n, f"N={n}")
+
+
 def test_config_q4_k_exact_mode_full_size(ctx):
     k, n = 4096, 14336
     blocks = po.make_weights(qa.Q4_K, k, n, seed=0x5EED0003, outliers=True)
