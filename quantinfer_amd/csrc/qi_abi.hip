@@ -222,9 +222,16 @@ qi_hip_status plan_linear(const Image& im, uint64_t m, int32_t mode, LinearPlan*
     p->kind = LinearPlan::kMfma;
     if (m >= 2 && qi::gemv_rows_supported(im.qtype, im.layout, im.k)) {
       // two or more rows, dense operands: one kernel per 16-row chunk; K parts
-      // (the same count for every chunk) only for shapes with few tiles
-      p->splits = qi::gemv_rows_splits(im.k, im.n);
-      if (p->splits > 1) p->s_floats = static_cast<uint64_t>(p->splits) * (m < 16 ? m : 16) * im.n;
+      // only for shapes with few tiles, by the chunk's row count (a shorter
+      // last chunk may take a different count; enqueue_linear asks again)
+      uint64_t floats = 0;
+      for (uint64_t r : {static_cast<uint64_t>(m < 16 ? m : 16), m > 16 ? m % 16 : 0}) {
+        if (r < 2) continue;
+        const uint32_t pr = qi::gemv_rows_splits(im.k, im.n, static_cast<uint32_t>(r));
+        if (pr > 1) floats = std::max(floats, static_cast<uint64_t>(pr) * r * im.n);
+      }
+      p->splits = 1;
+      p->s_floats = floats;
       return QI_HIP_OK;
     }
     // two or more rows (Q6_K): activation records built once per 16-row chunk,
@@ -296,11 +303,12 @@ qi_hip_status enqueue_linear(const qi_hip_weights* w, const LinearPlan& p, const
         if (p.kind == LinearPlan::kMfma && rows >= 2 && qi::gemv_rows_supported(im.qtype, im.layout, im.k)) {
           const float* xc = x + m0 * im.k;
           float* const yc = y + m0 * im.n;
-          QI_HIP_TRY(qi::launch_gemv_rows(im.qtype, im.wide != 0, v, xc, rows, yc, sws, p.splits, st),
+          const uint32_t parts = qi::gemv_rows_splits(im.k, im.n, static_cast<uint32_t>(rows));
+          QI_HIP_TRY(qi::launch_gemv_rows(im.qtype, im.wide != 0, v, xc, rows, yc, sws, parts, st),
                      "launch gemv rows");
-          if (p.splits > 1) {
+          if (parts > 1) {
             const uint64_t count = static_cast<uint64_t>(rows) * im.n;
-            QI_HIP_TRY(qi::launch_splitk_sum(im, v, sws, p.splits, count, count, yc, xc, st),
+            QI_HIP_TRY(qi::launch_splitk_sum(im, v, sws, parts, count, count, yc, xc, st),
                        "launch gemv split-K sum");
           }
         } else if (p.kind == LinearPlan::kMfma) {

@@ -27,7 +27,8 @@
 // are broadcast to the others the same way.
 //
 // Work split: a workgroup is 16 wavefronts, 4 tiles of 16 outputs x 4 K
-// slices. The workgroup builds the digits of its K range for all rows into
+// slices (or, for shapes of up to one tile per CU, one tile x 16 K slices,
+// so that no K part leaves the workgroup). The workgroup builds the digits of its K range for all rows into
 // LDS (chunk by chunk when they do not fit), each wavefront streams its
 // tile's units of its slice, and the slices are summed in order through LDS.
 // Weight loads are issued before the activation prep so that the HBM latency
@@ -48,8 +49,7 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 
 constexpr int kRowsThreads = 1024;   // 16 wavefronts
-constexpr int kRowsTiles = 4;        // tiles per workgroup
-constexpr int kRowsSlices = 4;       // K slices per tile
+constexpr int kRowsWaves = 16;      // wavefronts per workgroup: TL tiles x (16 / TL) K slices
 constexpr uint32_t kBlock = 512;     // LDS bytes per (row group, window) digit block
 constexpr uint32_t kRowsCUs = 256;   // compute units of an MI355X (gfx950)
 
@@ -340,9 +340,12 @@ __device__ __forceinline__ void prep_item(uint32_t t, uint32_t cw, uint32_t cwin
   }
 }
 
-// MG row groups (M <= 4 MG), D units of weights in flight per wavefront.
-template <int QT, bool WIDE, int MG, int D>
+// MG row groups (M <= 4 MG), D units of weights in flight per wavefront, TL
+// tiles per workgroup (4, or 1 with 16 K slices for shapes of up to one tile
+// per CU).
+template <int QT, bool WIDE, int MG, int D, int TL>
 __global__ __launch_bounds__(kRowsThreads) void gemv_rows_kernel(RowsArgs a) {
+  constexpr int SL = kRowsWaves / TL;  // K slices per tile
   using U = RowsUnit<QT>;
   static_assert(QT != kQ6_K, "Q6_K windows are 16 elements");
   constexpr Record R = record_geometry(QT, WIDE);
@@ -353,9 +356,9 @@ __global__ __launch_bounds__(kRowsThreads) void gemv_rows_kernel(RowsArgs a) {
   float* const xsum = xsc + 4 * MG * cw;
 
   const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const uint32_t sw = wave % kRowsSlices, wc = wave / kRowsSlices;
+  const uint32_t sw = wave % SL, wc = wave / SL;
   const uint32_t col = lane & 15, g = lane >> 4;
-  const uint32_t tile_raw = blockIdx.x * kRowsTiles + wc;
+  const uint32_t tile_raw = blockIdx.x * TL + wc;
   const uint32_t tile = min(tile_raw, a.w.tiles - 1);
   const uint32_t units_total = a.w.units;
   const uint8_t* const trec = a.w.qs + static_cast<uint64_t>(tile) * units_total * R.bytes;
@@ -379,8 +382,8 @@ __global__ __launch_bounds__(kRowsThreads) void gemv_rows_kernel(RowsArgs a) {
     const uint32_t units = min(cu, u_hi - ku0);
     const uint32_t cwin = 8 * units;  // windows of this chunk (records use the chunk stride cw)
     // this wavefront's contiguous run of the chunk's units
-    const uint32_t u_begin = (units * sw) / kRowsSlices;
-    const uint32_t u_count = (units * (sw + 1)) / kRowsSlices - u_begin;
+    const uint32_t u_begin = (units * sw) / SL;
+    const uint32_t u_count = (units * (sw + 1)) / SL - u_begin;
 
     // the previous chunk's records are consumed before its blocks are reused
     if (ku0 != u_lo) __syncthreads();
@@ -468,7 +471,7 @@ __global__ __launch_bounds__(kRowsThreads) void gemv_rows_kernel(RowsArgs a) {
   for (int q = 0; q < MG; ++q) {
     float v = acc[q];
     if constexpr (U::kMin) v -= cmin[q];
-    red[((wc * kRowsSlices + sw) * MG + q) * 64 + lane] = v;
+    red[((wc * SL + sw) * MG + q) * 64 + lane] = v;
   }
   __syncthreads();
   if (sw != 0) return;
@@ -479,9 +482,9 @@ __global__ __launch_bounds__(kRowsThreads) void gemv_rows_kernel(RowsArgs a) {
   for (int q = 0; q < MG; ++q) {
     const int m = 4 * q + static_cast<int>(g);
     if (m >= M) continue;
-    float v = red[((wc * kRowsSlices) * MG + q) * 64 + lane];
+    float v = red[((wc * SL) * MG + q) * 64 + lane];
 #pragma unroll
-    for (int p = 1; p < kRowsSlices; ++p) v += red[((wc * kRowsSlices + p) * MG + q) * 64 + lane];
+    for (int p = 1; p < SL; ++p) v += red[((wc * SL + p) * MG + q) * 64 + lane];
     // NaN or infinite activations (or an overflow): the reference's own order
     // decides which outputs are NaN and which +-Inf
     if (!__builtin_isfinite(v) && gridDim.y == 1)
@@ -490,14 +493,14 @@ __global__ __launch_bounds__(kRowsThreads) void gemv_rows_kernel(RowsArgs a) {
   }
 }
 
-template <int QT, bool WIDE, int MG, int D>
+template <int QT, bool WIDE, int MG, int D, int TL>
 hipError_t launch_rows_t(RowsArgs a, uint32_t ksplit, hipStream_t st) {
   const uint32_t cap = rows_chunk_cap(MG);
   a.chunk_units = a.part_units < cap ? a.part_units : cap;
   const uint32_t main = rows_lds(MG, a.chunk_units);
-  const uint32_t red = kRowsTiles * kRowsSlices * MG * 64 * 4;
+  const uint32_t red = kRowsWaves * MG * 64 * 4;
   const uint32_t bytes = main > red ? main : red;
-  auto kern = gemv_rows_kernel<QT, WIDE, MG, D>;
+  auto kern = gemv_rows_kernel<QT, WIDE, MG, D, TL>;
   if (bytes > 65536) {
     const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                              hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(bytes));
@@ -507,19 +510,42 @@ hipError_t launch_rows_t(RowsArgs a, uint32_t ksplit, hipStream_t st) {
     }
   }
   if (ksplit > 1 && a.part == nullptr) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(kern, dim3((a.w.tiles + kRowsTiles - 1) / kRowsTiles, ksplit), dim3(kRowsThreads), bytes, st,
+  hipLaunchKernelGGL(kern, dim3((a.w.tiles + TL - 1) / TL, ksplit), dim3(kRowsThreads), bytes, st,
                      a);
   return hipGetLastError();
 }
 
-template <int QT, bool WIDE>
-hipError_t launch_rows_w(const RowsArgs& a, uint32_t ksplit, hipStream_t st) {
+template <int QT, bool WIDE, int TL>
+hipError_t launch_rows_tl(const RowsArgs& a, uint32_t ksplit, hipStream_t st) {
   // two units in flight per wavefront: what the 128-register budget of a
   // 16-wavefront workgroup holds
-  if (a.m <= 4) return launch_rows_t<QT, WIDE, 1, 2>(a, ksplit, st);
-  if (a.m <= 8) return launch_rows_t<QT, WIDE, 2, 2>(a, ksplit, st);
+  if (a.m <= 4) return launch_rows_t<QT, WIDE, 1, 2, TL>(a, ksplit, st);
+  if (a.m <= 8) return launch_rows_t<QT, WIDE, 2, 2, TL>(a, ksplit, st);
   // (Q5_K with 16 rows exceeds the budget at two units in flight)
-  return launch_rows_t<QT, WIDE, 4, QT == kQ5_K ? 1 : 2>(a, ksplit, st);
+  return launch_rows_t<QT, WIDE, 4, QT == kQ5_K ? 1 : 2, TL>(a, ksplit, st);
+}
+
+// One-tile workgroups (16 K slices, no K split) for shapes of up to one tile
+// per CU whose whole K range of activation digits fits one LDS chunk: every
+// workgroup then builds its digits once and streams straight through. With
+// more K (more chunks, each built and consumed in turn) the four-tile
+// workgroups with K parts over the grid build less per workgroup. Measured on
+// MI355X (Q4_0, one launch plus the split-K sum where there is one): 4096 x
+// 1024 M=4 13.9 -> 7.1 us, M=8 13.7 -> 10.8; 4096 x 4096 M=4 13.3 -> 7.4,
+// M=8 13.0 -> 11.1; slower with two chunks or more (4096 x 4096 M=16 15.5 ->
+// 21.7, 12288 x 4096 M=4 16.7 -> 18.7).
+bool rows_one_tile(uint64_t k, uint64_t n, uint32_t m) {
+  const int mg = m <= 4 ? 1 : m <= 8 ? 2 : 4;
+  return (n + 15) / 16 <= kRowsCUs && k / 256 <= rows_chunk_cap(mg);
+}
+
+template <int QT, bool WIDE>
+hipError_t launch_rows_w(const RowsArgs& a, uint32_t ksplit, hipStream_t st) {
+  if (rows_one_tile(a.w.k, a.w.n, static_cast<uint32_t>(a.m))) {
+    if (ksplit != 1) return hipErrorInvalidValue;
+    return launch_rows_tl<QT, WIDE, 1>(a, ksplit, st);
+  }
+  return launch_rows_tl<QT, WIDE, 4>(a, ksplit, st);
 }
 
 }  // namespace
@@ -529,11 +555,14 @@ bool gemv_rows_supported(int32_t qtype, int32_t layout, uint64_t k) {
          k % 256 == 0 && k > 0;
 }
 
-uint32_t gemv_rows_splits(uint64_t k, uint64_t n) {
-  // one workgroup per CU (LDS and registers); split K only when the tile
-  // groups leave most CUs idle, keeping at least 4 units (one per K slice)
-  // per part
-  const uint64_t units = k / 256, groups = ((n + 15) / 16 + kRowsTiles - 1) / kRowsTiles;
+uint32_t gemv_rows_splits(uint64_t k, uint64_t n, uint32_t m) {
+  // one-tile workgroups: no K split (launch_rows_w)
+  if (rows_one_tile(k, n, m)) return 1;
+  const uint64_t tiles = (n + 15) / 16;
+  // one four-tile workgroup per CU (LDS and registers); split K only when the
+  // tile groups leave most CUs idle, keeping at least 4 units (one per K
+  // slice) per part
+  const uint64_t units = k / 256, groups = (tiles + 3) / 4;
   uint64_t s = kRowsCUs / (groups ? groups : 1);
   const uint64_t most = units / 4 ? units / 4 : 1;
   if (s > most) s = most;

@@ -71,11 +71,11 @@ hipError_t launch_gemv_mfma(int32_t qtype, bool wide, int mt, int split, const G
                             hipStream_t st);
 
 // Matrix-core decode GEMV of 2-16 rows with dense operands (qi_gemv_rows.hip):
-// one kernel, K parts over the grid (gemv_rows_splits) only for shapes with few
-// tiles; with ksplit > 1 the partial sums [ksplit][m][n] go to `part` and
-// launch_splitk_sum adds them.
+// one kernel, K parts over the grid (gemv_rows_splits, by shape and row count)
+// only for shapes with few tiles; with ksplit > 1 the partial sums
+// [ksplit][m][n] go to `part` and launch_splitk_sum adds them.
 bool gemv_rows_supported(int32_t qtype, int32_t layout, uint64_t k);
-uint32_t gemv_rows_splits(uint64_t k, uint64_t n);
+uint32_t gemv_rows_splits(uint64_t k, uint64_t n, uint32_t m);
 hipError_t launch_gemv_rows(int32_t qtype, bool wide, const View& w, const float* x, int m, float* y, float* part,
                             uint32_t ksplit, hipStream_t st);
 

@@ -263,8 +263,9 @@ def test_f32_gemv_unrounded_scales(ctx):
 CONFIGS = [
     # (qtype, K, N, M list, outliers) -- configs[0..2] of BASELINE.json
     (qa.Q8_0, 4096, 4096, [1], False),
-    (qa.Q4_0, 4096, 4096, [1, 4, 16], False),
-    (qa.Q4_0, 4096, 1024, [1, 4, 16], False),
+    (qa.Q4_0, 4096, 4096, [1, 4, 8, 16], False),
+    # 20 rows: a 16-row chunk with K parts and a 4-row chunk of one-tile workgroups
+    (qa.Q4_0, 4096, 1024, [1, 4, 16, 20], False),
     (qa.Q4_0, 4096, 12288, [1, 4, 16], False),
     (qa.Q4_0, 12288, 4096, [1, 4, 16], False),
     (qa.Q4_K, 4096, 14336, [1, 8], True),
