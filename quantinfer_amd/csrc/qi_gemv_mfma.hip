@@ -6,13 +6,18 @@
 // integer F = rint(x * 2^s), with one power of two 2^s per (activation row,
 // window) chosen from the window's max |x|, written as four signed 8-bit
 // digits F = d0 + d1*2^8 + d2*2^16 + d3*2^24. The weight codes enter the
-// matrix cores unchanged (Q8_0 int8 codes, Q4_0/Q4_K/Q5_K/Q6_K unsigned
-// codes), so every product digit*code is exact in int32, and over a window
-//   sum_k x_k q_k = 2^-s * (C0 + C1*2^8 + C2*2^16 + C3*2^24),  Ci = sum_k di_k q_k
-// up to the 2^-30-of-window-max rounding of x. The sub-block scale a and
-// offset b of the format (w = a*q - b) are applied in f32 once per window
-// (Q6_K: per 16-element half window, one int8 sub-scale each):
-//   y += a * 2^-s * combine(C) - b * sum_k x_k.
+// matrix cores as signed bytes centred on the middle of their range (Q8_0's
+// int8 codes as they are; Q4_0 and Q4_K as 16 (q - 8), Q5_K as 8 (q - 16),
+// Q6_K as 4 (q - 32); qi_unit.h), so every product digit*code is exact in
+// int32, and over a window
+//   sum_k x_k (q_k - z) = 2^-s * (C0 + C1*2^8 + C2*2^16 + C3*2^24),  Ci = sum_k di_k (q_k - z)
+// up to the 2^-30-of-window-max rounding of x. The sub-block scale a and the
+// offset left, b' = b - z a, of the format (w = a*q - b) are applied in f32
+// once per window (Q6_K: per 16-element half window, one int8 sub-scale
+// each): y += a * 2^-s * combine(C) - b' * sum_k x_k, with b' = 0 for Q4_0
+// and Q6_K; the sums are scaled back by the codes' 1/16, 1/8 or 1/4 once at
+// the end. Centring keeps a sum x q and b sum x, of similar size, from
+// cancelling in f32.
 // This reorders the reference arithmetic and is judged by tolerance.
 //
 // Operand layout (v_mfma_i32_16x16x64_i8: A[i][k] lane i+16*(k/16), B[k][j]
@@ -53,9 +58,9 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 constexpr uint32_t kZeroBytes = 1024;  // zero A operand for the lanes of other lane groups
 // Activation record of one (row, unit): 256 activations x 4 digits (1024 B,
 // [step pair p][lane group g][digit d] x 16 B: digit d of the pair's 16
-// activations, steps 2p and 2p + 1), then 8 windows x float4 {2^-s, sum of
-// elements 0-15, of 16-31, 0} (128 B, [g][h]). Built in LDS by the workgroup, or once per call in global memory
-// by gemv_digits_kernel and copied into LDS.
+// activations, steps 2p and 2p + 1), then 8 windows x float4 {2^-s, window
+// sum, 0, 0} (128 B, [g][h]). Built in LDS by the workgroup, or once per call
+// in global memory by gemv_digits_kernel and copied into LDS.
 constexpr uint32_t kUnitDigitBytes = 1024;
 constexpr uint32_t kUnitAuxBytes = 128;
 constexpr uint32_t kUnitRecBytes = kUnitDigitBytes + kUnitAuxBytes;
@@ -138,12 +143,16 @@ __device__ __forceinline__ void store_half(const HalfX& o, const Item& it, bool 
                                            uint32_t cu) {
   const float xs[16] = {o.v[0].x, o.v[0].y, o.v[0].z, o.v[0].w, o.v[1].x, o.v[1].y, o.v[1].z, o.v[1].w,
                         o.v[2].x, o.v[2].y, o.v[2].z, o.v[2].w, o.v[3].x, o.v[3].y, o.v[3].z, o.v[3].w};
-  float mx = 0.0f, sum = 0.0f;
+  float mx = 0.0f;
 #pragma unroll
-  for (int j = 0; j < 16; ++j) {
-    mx = fmaxf(mx, fabsf(xs[j]));
-    sum += xs[j];
-  }
+  for (int j = 0; j < 16; ++j) mx = fmaxf(mx, fabsf(xs[j]));
+  // the half window's sum, pairwise (the offset term's error scales with it)
+  float ps[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) ps[j] = xs[2 * j] + xs[2 * j + 1];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) ps[j] = ps[2 * j] + ps[2 * j + 1];
+  const float sum = (ps[0] + ps[1]) + (ps[2] + ps[3]);
   mx = fmaxf(mx, __shfl_xor(mx, 1));
   const float other = __shfl_xor(sum, 1);
   // A NaN or infinite activation makes the window sum non-finite. Its scale
@@ -177,7 +186,7 @@ __device__ __forceinline__ void store_half(const HalfX& o, const Item& it, bool 
 #pragma unroll
   for (int d = 0; d < 4; ++d) dst[d] = make_uint4(lo[0][d], hi[0][d], lo[1][d], hi[1][d]);
   if (it.half == 0)
-    reinterpret_cast<float4*>(rec + kUnitDigitBytes)[it.g * 2 + it.h] = make_float4(inv, sum, other, 0.0f);
+    reinterpret_cast<float4*>(rec + kUnitDigitBytes)[it.g * 2 + it.h] = make_float4(inv, sum + other, 0.0f, 0.0f);
 }
 
 // WC tiles of 16 outputs per workgroup, SW wavefronts per tile splitting its
@@ -338,6 +347,13 @@ void gemv_mfma_kernel(GemvMfmaArgs a) {
         const uint32_t u = u_begin + j + i;  // chunk-relative unit
         float sa[U::kWindows], sb[U::kWindows];
         U::template scales<WIDE>(g, ring[i], sa, sb);
+        // Q4_K / Q5_K: the offsets left by the centred codes, b - z a
+        // (exactly rounded), in the codes' scale (times a power of two)
+        if constexpr (window_centered<QT>()) {
+#pragma unroll
+          for (int w = 0; w < U::kWindows; ++w)
+            sb[w] = fmaf(-static_cast<float>(code_centre<QT>()), sa[w], sb[w]) * static_cast<float>(code_scale<QT>());
+        }
         if constexpr (MT >= 8) {
           // Eight or more rows: a window's codes are decoded once, then the
           // rows go one after another (two matrix instructions and the combine
@@ -357,7 +373,7 @@ void gemv_mfma_kernel(GemvMfmaArgs a) {
 #pragma unroll
             for (int sp = 0; sp < kPairs; ++sp) {
               const int t = w * U::kSteps + 2 * sp;
-              const long c0 = U::codes(ring[i], g, t), c1 = U::codes(ring[i], g, t + 1);
+              const long c0 = gemv_codes<QT>(ring[i], g, t), c1 = gemv_codes<QT>(ring[i], g, t + 1);
               cb[sp] = v4i{static_cast<int>(c0), static_cast<int>(c0 >> 32), static_cast<int>(c1),
                            static_cast<int>(c1 >> 32)};
             }
@@ -375,10 +391,7 @@ void gemv_mfma_kernel(GemvMfmaArgs a) {
                                       static_cast<float>(c[0] + c[1] * 256));
               const float4 wx = x0[m * xstride + h];
               acc[m] = fmaf(sa[w] * wx.x, comb, acc[m]);
-              if constexpr (U::kMin) {
-                const float xs = U::kSteps == 4 ? wx.y + wx.z : ((w & 1) ? wx.z : wx.y);
-                acc[m] = fmaf(-sb[w], xs, acc[m]);
-              }
+              if constexpr (window_centered<QT>()) acc[m] = fmaf(-sb[w], wx.y, acc[m]);
             }
           }
           continue;
@@ -408,7 +421,7 @@ void gemv_mfma_kernel(GemvMfmaArgs a) {
             v4i av[MT];
 #pragma unroll
             for (int m = 0; m < MT; ++m) av[m] = *reinterpret_cast<const v4i*>(abase[m] + (t >> 1) * 256);
-            const long c0 = U::codes(ring[i], g, t), c1 = U::codes(ring[i], g, t + 1);
+            const long c0 = gemv_codes<QT>(ring[i], g, t), c1 = gemv_codes<QT>(ring[i], g, t + 1);
             const v4i cb = {static_cast<int>(c0), static_cast<int>(c0 >> 32), static_cast<int>(c1),
                             static_cast<int>(c1 >> 32)};
 #pragma unroll
@@ -423,10 +436,7 @@ void gemv_mfma_kernel(GemvMfmaArgs a) {
                                     static_cast<float>(c[m][0] + c[m][1] * 256));
             const float4 wx = ax[m][h];
             acc[m] = fmaf(sa[w] * wx.x, comb, acc[m]);
-            if constexpr (U::kMin) {
-              const float xs = U::kSteps == 4 ? wx.y + wx.z : ((w & 1) ? wx.z : wx.y);
-              acc[m] = fmaf(-sb[w], xs, acc[m]);
-            }
+            if constexpr (window_centered<QT>()) acc[m] = fmaf(-sb[w], wx.y, acc[m]);
           }
         }
       }
@@ -446,7 +456,7 @@ void gemv_mfma_kernel(GemvMfmaArgs a) {
   // ---- reduce: 4 lane groups of a column, then the SW K-parts ----
 #pragma unroll
   for (int m = 0; m < MT; ++m) {
-    float v = acc[m];
+    float v = acc[m] * (1.0f / code_scale<QT>());  // centred codes' scale (exact)
     v += __shfl_xor(v, 16);
     v += __shfl_xor(v, 32);
     acc[m] = v;

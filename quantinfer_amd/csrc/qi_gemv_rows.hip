@@ -5,12 +5,14 @@
 // Arithmetic: as the one-row kernel (qi_gemv_mfma.hip). Each activation row
 // is cut into windows of 32 elements; an element becomes the 30-bit integer
 // F = rint(x * 2^s) (2^s per (row, window) from the window's max |x|), held
-// as four signed 8-bit digits; weight codes enter the matrix cores unchanged,
+// as four signed 8-bit digits; weight codes enter the matrix cores as bytes,
+// centred as there (Q4_0 as 16 (q - 8); Q4_K and Q5_K as q - z with a zero
+// point z per window, by a second matrix instruction with -z in every B byte),
 // so every digit sum is exact in int32, and per (row, window, output)
-//   sum_k x_k w_k = a * 2^-s * (C0 + C1*2^8 + C2*2^16 + C3*2^24) - b * sum_k x_k
-// with the format's sub-block scale a and offset b (w = a*q - b). The offset
-// terms of all windows go through f32 matrix instructions
-// (v_mfma_f32_16x16x4_f32: window sums x per-output offsets).
+//   sum_k x_k w_k = a * 2^-s * (C0 + C1*2^8 + C2*2^16 + C3*2^24) - b' * sum_k x_k
+// with the format's sub-block scale a and the offset left, b' = b - z a
+// (w = a*q - b). The offset terms of all windows go through f32 matrix
+// instructions (v_mfma_f32_16x16x4_f32: window sums x per-output offsets).
 //
 // Dense operands. One 16x16x32 instruction covers one window for four
 // activation rows and the tile's 16 outputs: A row 4r + d holds digit d of
@@ -108,6 +110,7 @@ struct Dense<kQ8_0> {
   struct T {
     uint32_t lo[2][4], hi[2][4];
   };
+  template <bool C>
   __device__ static void prepare(const Unit<kQ8_0>::Raw& r, uint32_t, T& t) {
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
@@ -124,32 +127,39 @@ template <>
 struct Dense<kQ4_0> {
   // lane group g: block 2g + b in q[b] (byte i = element i | element i+16 << 4).
   // Slice s as one word of 8 nibbles (byte k = element 8s+k | element 8s+4+k << 4)
-  // before the transpose, so a lane group sends four words per block.
+  // before the transpose, so a lane group sends four words per block. The
+  // codes go out centred, 16 (q - 8) as signed bytes (Unit<kQ4_0>::centred_codes,
+  // qi_unit.h): bit 3 of every nibble flipped, each nibble moved to the high
+  // half of its byte.
   static constexpr uint32_t kM = 0x0F0F0F0Fu;
   struct T {
     uint32_t w[2][4];
   };
+  template <bool C>
   __device__ static void prepare(const Unit<kQ4_0>::Raw& r, uint32_t, T& t) {
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
       const uint4 q = r.q[b];
-      t.w[b][0] = (q.x & kM) | ((q.y << 4) & ~kM);
-      t.w[b][1] = (q.z & kM) | ((q.w << 4) & ~kM);
-      t.w[b][2] = ((q.x >> 4) & kM) | (q.y & ~kM);
-      t.w[b][3] = ((q.z >> 4) & kM) | (q.w & ~kM);
+      t.w[b][0] = ((q.x & kM) | ((q.y << 4) & ~kM)) ^ 0x88888888u;
+      t.w[b][1] = ((q.z & kM) | ((q.w << 4) & ~kM)) ^ 0x88888888u;
+      t.w[b][2] = (((q.x >> 4) & kM) | (q.y & ~kM)) ^ 0x88888888u;
+      t.w[b][3] = (((q.z >> 4) & kM) | (q.w & ~kM)) ^ 0x88888888u;
       xpose4(t.w[b]);
     }
   }
   __device__ static long b(const T& t, int w) {
     const uint32_t v = t.w[w & 1][w >> 1];
-    return pack2(v & kM, (v >> 4) & kM);
+    return pack2((v << 4) & ~kM, v & ~kM);
   }
 };
 
 // Q4_K / Q5_K: lane group g holds code bytes [32g, 32g+32) of the
 // super-block, bytes 8s..8s+7 (dwords 2s, 2s+1) carrying slice s of window
 // 2g (low nibbles) and of window 2g+1 (high nibbles); Q5_K adds bit w of
-// qh byte e as bit 4 of element e of window w.
+// qh byte e as bit 4 of element e of window w. b() gives the codes as they
+// are, bc() centred on the middle of their range as the one-row kernel takes
+// them (qi_unit.h): Q4_K 16 (q - 8) (nibble bit 3 flipped, the nibble in the
+// byte's high half; prepare() flips the bits when C), Q5_K 8 (q - 16).
 template <bool FIVE>
 struct DenseQ45K {
   static constexpr uint32_t kM = 0x0F0F0F0Fu;
@@ -157,10 +167,17 @@ struct DenseQ45K {
     uint32_t lo[4], hi[4];
     uint32_t hl, hh;  // Q5_K: qh bytes 8g..8g+7 of this output
   };
-  template <typename Raw>
+  template <bool C, typename Raw>
   __device__ static void prepare(const Raw& r, uint32_t, T& t) {
     t.lo[0] = r.q[0].x; t.lo[1] = r.q[0].z; t.lo[2] = r.q[1].x; t.lo[3] = r.q[1].z;
     t.hi[0] = r.q[0].y; t.hi[1] = r.q[0].w; t.hi[2] = r.q[1].y; t.hi[3] = r.q[1].w;
+    if constexpr (C && !FIVE) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        t.lo[i] ^= 0x88888888u;
+        t.hi[i] ^= 0x88888888u;
+      }
+    }
     xpose4(t.lo);
     xpose4(t.hi);
     if constexpr (FIVE) {
@@ -180,6 +197,21 @@ struct DenseQ45K {
       c |= (w <= 4 ? t.hh << (4 - w) : t.hh >> (w - 4)) & 0x10101010u;
     }
     return pack2(a, c);
+  }
+  __device__ static long bc(const T& t, int w) {
+    const int gp = w >> 1, h = w & 1;
+    if constexpr (FIVE) {
+      // nibble to bits 3-6, bit w of the qh byte to bit 7, bit 7 flipped
+      const uint32_t a = ((h ? t.lo[gp] >> 1 : t.lo[gp] << 3) & 0x78787878u) ^
+                         ((t.hl << (7 - w)) & 0x80808080u) ^ 0x80808080u;
+      const uint32_t c = ((h ? t.hi[gp] >> 1 : t.hi[gp] << 3) & 0x78787878u) ^
+                         ((t.hh << (7 - w)) & 0x80808080u) ^ 0x80808080u;
+      return pack2(a, c);
+    } else {
+      const uint32_t a = (h ? t.lo[gp] : t.lo[gp] << 4) & ~kM;
+      const uint32_t c = (h ? t.hi[gp] : t.hi[gp] << 4) & ~kM;
+      return pack2(a, c);
+    }
   }
 };
 template <>
@@ -342,9 +374,13 @@ __device__ __forceinline__ void prep_item(uint32_t t, uint32_t cw, uint32_t cwin
 
 // MG row groups (M <= 4 MG), D units of weights in flight per wavefront, TL
 // tiles per workgroup (4, or 1 with 16 K slices for shapes of up to one tile
-// per CU).
-template <int QT, bool WIDE, int MG, int D, int TL>
+// per CU). ZP (Q4_K / Q5_K): the codes centred on a zero point per window
+// (rows_zero_points); otherwise on the middle of their range.
+template <int QT, bool WIDE, int MG, int D, int TL, bool ZP>
 __global__ __launch_bounds__(kRowsThreads) void gemv_rows_kernel(RowsArgs a) {
+  // codes centred on the middle of their range, and their scale
+  constexpr bool kFixed = QT == kQ4_0 || (window_centered<QT>() && !ZP);
+  constexpr float kInvScale = kFixed ? 1.0f / static_cast<float>(code_scale<QT>()) : 1.0f;
   constexpr int SL = kRowsWaves / TL;  // K slices per tile
   using U = RowsUnit<QT>;
   static_assert(QT != kQ6_K, "Q6_K windows are 16 elements");
@@ -425,8 +461,38 @@ __global__ __launch_bounds__(kRowsThreads) void gemv_rows_kernel(RowsArgs a) {
           for (int gp = 0; gp < 4; ++gp) sa[2 * gp + 1] = t[gp];
         }
         typename Dense<QT>::T ct;
-        Dense<QT>::prepare(ring[i], g, ct);
-        if constexpr (U::kMin) {
+        Dense<QT>::template prepare<kFixed>(ring[i], g, ct);
+        if constexpr (window_centered<QT>() && !ZP) {
+          // the offsets left by the centred codes, b - z a (exactly rounded),
+          // of windows 2k + h (k = lane group) of this unit for the tile's
+          // outputs, times the rows' window sums
+          constexpr float z = static_cast<float>(code_centre<QT>());
+          const float2 sx = mrow < 4 * MG
+                                ? *reinterpret_cast<const float2*>(xsum + mrow * cw + u * 8 + 2 * g)
+                                : make_float2(0.0f, 0.0f);
+          cmin = __builtin_amdgcn_mfma_f32_16x16x4f32(sx.x, fmaf(-z, sa_own[0], sb_own[0]), cmin, 0, 0, 0);
+          cmin = __builtin_amdgcn_mfma_f32_16x16x4f32(sx.y, fmaf(-z, sa_own[1], sb_own[1]), cmin, 0, 0, 0);
+        }
+        // ZP: -z of window w of this output in every byte of zb[w]
+        [[maybe_unused]] uint32_t zb[8];
+        if constexpr (window_centered<QT>() && ZP) {
+          // zero points of windows 2g, 2g + 1 (window_zero_point) and the
+          // offsets left, b - z a (exactly rounded); -z of both as bytes 0
+          // and 1 of one word, gathered from the other lane groups
+          const float z0 = window_zero_point(sa_own[0], sb_own[0]);
+          const float z1 = window_zero_point(sa_own[1], sb_own[1]);
+          sb_own[0] = fmaf(-z0, sa_own[0], sb_own[0]);
+          sb_own[1] = fmaf(-z1, sa_own[1], sb_own[1]);
+          const uint32_t nz = (static_cast<uint32_t>(-static_cast<int>(z0)) & 0xFFu) |
+                              ((static_cast<uint32_t>(-static_cast<int>(z1)) & 0xFFu) << 8);
+          float t[4];
+          gather4(__builtin_bit_cast(float, nz), t);
+#pragma unroll
+          for (int gp = 0; gp < 4; ++gp) {
+            const uint32_t v = __builtin_bit_cast(uint32_t, t[gp]);
+            zb[2 * gp] = __builtin_amdgcn_perm(0u, v, 0x00000000u);      // byte 0 everywhere
+            zb[2 * gp + 1] = __builtin_amdgcn_perm(0u, v, 0x01010101u);  // byte 1 everywhere
+          }
           // offsets of windows 2k + h (k = lane group) of this unit for the
           // tile's outputs, times the rows' window sums
           const float2 sx = mrow < 4 * MG
@@ -437,13 +503,17 @@ __global__ __launch_bounds__(kRowsThreads) void gemv_rows_kernel(RowsArgs a) {
         }
 #pragma unroll
         for (int w = 0; w < 8; ++w) {
-          const long bw = Dense<QT>::b(ct, w);
+          long bw;
+          if constexpr (window_centered<QT>() && !ZP) bw = Dense<QT>::bc(ct, w);
+          else bw = Dense<QT>::b(ct, w);
 #pragma unroll
           for (int q = 0; q < MG; ++q) {
             const uint32_t qw = q * cw + u * 8 + w;  // (row group, chunk window)
             const long av = *reinterpret_cast<const long*>(dig + qw * kBlock + lane * 8);
             const float xw = xsc[(4 * q + g) * cw + u * 8 + w];
-            const v4i c = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, bw, v4i{0, 0, 0, 0}, 0, 0, 0);
+            v4i c = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, bw, v4i{0, 0, 0, 0}, 0, 0, 0);
+            if constexpr (window_centered<QT>() && ZP)
+              c = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, pack2(zb[w], zb[w]), c, 0, 0, 0);
             // pairs exactly in int32 (|C0| < 2^20, |C1 * 256| < 2^28), halves in f32
             const float comb = fmaf(static_cast<float>(c[2] + c[3] * 256), 65536.0f,
                                     static_cast<float>(c[0] + c[1] * 256));
@@ -469,8 +539,8 @@ __global__ __launch_bounds__(kRowsThreads) void gemv_rows_kernel(RowsArgs a) {
   float* red = reinterpret_cast<float*>(lds);  // [tile][slice][q][64]
 #pragma unroll
   for (int q = 0; q < MG; ++q) {
-    float v = acc[q];
-    if constexpr (U::kMin) v -= cmin[q];
+    float v = acc[q] * kInvScale;  // centred codes' scale (exact)
+    if constexpr (window_centered<QT>()) v -= cmin[q];
     red[((wc * SL + sw) * MG + q) * 64 + lane] = v;
   }
   __syncthreads();
@@ -493,14 +563,14 @@ __global__ __launch_bounds__(kRowsThreads) void gemv_rows_kernel(RowsArgs a) {
   }
 }
 
-template <int QT, bool WIDE, int MG, int D, int TL>
+template <int QT, bool WIDE, int MG, int D, int TL, bool ZP>
 hipError_t launch_rows_t(RowsArgs a, uint32_t ksplit, hipStream_t st) {
   const uint32_t cap = rows_chunk_cap(MG);
   a.chunk_units = a.part_units < cap ? a.part_units : cap;
   const uint32_t main = rows_lds(MG, a.chunk_units);
   const uint32_t red = kRowsWaves * MG * 64 * 4;
   const uint32_t bytes = main > red ? main : red;
-  auto kern = gemv_rows_kernel<QT, WIDE, MG, D, TL>;
+  auto kern = gemv_rows_kernel<QT, WIDE, MG, D, TL, ZP>;
   if (bytes > 65536) {
     const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                              hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(bytes));
@@ -515,14 +585,33 @@ hipError_t launch_rows_t(RowsArgs a, uint32_t ksplit, hipStream_t st) {
   return hipGetLastError();
 }
 
-template <int QT, bool WIDE, int TL>
-hipError_t launch_rows_tl(const RowsArgs& a, uint32_t ksplit, hipStream_t st) {
+template <int QT, bool WIDE, int TL, bool ZP>
+hipError_t launch_rows_tz(const RowsArgs& a, uint32_t ksplit, hipStream_t st) {
   // two units in flight per wavefront: what the 128-register budget of a
   // 16-wavefront workgroup holds
-  if (a.m <= 4) return launch_rows_t<QT, WIDE, 1, 2, TL>(a, ksplit, st);
-  if (a.m <= 8) return launch_rows_t<QT, WIDE, 2, 2, TL>(a, ksplit, st);
+  if (a.m <= 4) return launch_rows_t<QT, WIDE, 1, 2, TL, ZP>(a, ksplit, st);
+  if (a.m <= 8) return launch_rows_t<QT, WIDE, 2, 2, TL, ZP>(a, ksplit, st);
   // (Q5_K with 16 rows exceeds the budget at two units in flight)
-  return launch_rows_t<QT, WIDE, 4, QT == kQ5_K ? 1 : 2, TL>(a, ksplit, st);
+  return launch_rows_t<QT, WIDE, 4, QT == kQ5_K ? 1 : 2, TL, ZP>(a, ksplit, st);
+}
+
+// Q4_K / Q5_K centring. The offsets of all windows are summed apart from the
+// code products and subtracted once at the end, so what the centring leaves
+// of them cancels there; centred on the middle of the code range, the
+// leftover of outlier windows (b / a far from the middle) still cancels to
+// 1.7e-5 of sum |x w| at K = 256 (16 rows; a CPU model of this kernel's
+// arithmetic, and MI355X). The cancellation error grows like sqrt(K) and
+// sum |x w| like K, so zero points (window_zero_point, subtracted by a second
+// matrix instruction per window: 10-16% slower at 4-16 rows) are taken for
+// K <= 2048, where the fixed centre would leave more than 6e-6.
+constexpr uint64_t kRowsZeroPointUnits = 8;
+
+template <int QT, bool WIDE, int TL>
+hipError_t launch_rows_tl(const RowsArgs& a, uint32_t ksplit, hipStream_t st) {
+  if constexpr (window_centered<QT>()) {
+    if (a.w.units <= kRowsZeroPointUnits) return launch_rows_tz<QT, WIDE, TL, true>(a, ksplit, st);
+  }
+  return launch_rows_tz<QT, WIDE, TL, false>(a, ksplit, st);
 }
 
 // One-tile workgroups (16 K slices, no K split) for shapes of up to one tile

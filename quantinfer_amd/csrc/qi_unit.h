@@ -122,6 +122,16 @@ struct Unit<kQ4_0> {
     const uint32_t l2 = (lo >> sh) & 0x0F0F0F0Fu, h2 = (hi >> sh) & 0x0F0F0F0Fu;
     return static_cast<long>((static_cast<uint64_t>(h2) << 32) | l2);
   }
+  // the same codes as 16 (q - 8), signed bytes: with bit 3 of each nibble
+  // flipped, the nibble is q - 8 in 4-bit two's complement, and in the high
+  // half of a byte it reads as 16 times that
+  __device__ static long centred_codes(const Raw& r, uint32_t, int t) {
+    const uint4 q = r.q[t >> 2];
+    const int qq = t & 3;
+    const uint32_t lo = ((qq & 1) ? q.z : q.x) ^ 0x88888888u, hi = ((qq & 1) ? q.w : q.y) ^ 0x88888888u;
+    const uint32_t l2 = (qq >= 2 ? lo : lo << 4) & 0xF0F0F0F0u, h2 = (qq >= 2 ? hi : hi << 4) & 0xF0F0F0F0u;
+    return static_cast<long>((static_cast<uint64_t>(h2) << 32) | l2);
+  }
 };
 
 // Q4_K / Q5_K: lane group g holds code bytes [32g, 32g+32) of the super-block:
@@ -200,6 +210,29 @@ struct UnitQ45K {
     }
     return static_cast<long>((static_cast<uint64_t>(h2) << 32) | l2);
   }
+  // The same codes centred, as signed bytes. Q4_K: 16 (q - 8), the nibble
+  // with bit 3 flipped (q - 8 in 4-bit two's complement) in the byte's high
+  // half. Q5_K: 8 (q - 16), the nibble in bits 3-6 and the high bit in bit 7
+  // (disjoint, so joined by xor), bit 7 flipped (subtracting 128 = 8 * 16).
+  __device__ static long centred_codes(const Raw& r, uint32_t g, int t) {
+    const int tt = t & 3;
+    const uint4 q = r.q[tt >> 1];
+    const uint32_t lo = (tt & 1) ? q.z : q.x, hi = (tt & 1) ? q.w : q.y;
+    uint32_t l2, h2;
+    if constexpr (FIVE) {
+      const uint4 h = r.h[tt >> 1];
+      const uint32_t hl = (tt & 1) ? h.z : h.x, hh = (tt & 1) ? h.w : h.y;
+      const int up = 7 - static_cast<int>(2 * g) - (t >= 4 ? 1 : 0);  // 7 - (bit of the pair)
+      const uint32_t nl = (t >= 4 ? lo >> 1 : lo << 3) & 0x78787878u, nh = (t >= 4 ? hi >> 1 : hi << 3) & 0x78787878u;
+      l2 = nl ^ ((hl << up) & 0x80808080u) ^ 0x80808080u;
+      h2 = nh ^ ((hh << up) & 0x80808080u) ^ 0x80808080u;
+    } else {
+      const uint32_t fl = lo ^ 0x88888888u, fh = hi ^ 0x88888888u;
+      l2 = (t >= 4 ? fl : fl << 4) & 0xF0F0F0F0u;
+      h2 = (t >= 4 ? fh : fh << 4) & 0xF0F0F0F0u;
+    }
+    return static_cast<long>((static_cast<uint64_t>(h2) << 32) | l2);
+  }
 };
 
 template <>
@@ -262,6 +295,21 @@ struct Unit<kQ6_K> {
     const uint32_t h2 = ((hi >> sh) & 0x0F0F0F0Fu) | (((hh >> hs) & 0x03030303u) << 4);
     return static_cast<long>((static_cast<uint64_t>(h2) << 32) | l2);
   }
+  // the same codes as 4 (q - 32), signed bytes: 4q = the low nibble in bits
+  // 2-5 and the two high bits in bits 6-7 (disjoint, so joined by xor), and
+  // flipping bit 7 subtracts 128 = 4 * 32
+  __device__ static long centred_codes(const Raw& r, uint32_t g, int t) {
+    const int tt = t & 3;
+    const uint4 q = r.q[tt >> 1];
+    const uint4 h = r.h[tt >> 1];
+    const uint32_t lo = (tt & 1) ? q.z : q.x, hi = (tt & 1) ? q.w : q.y;
+    const uint32_t hl = (tt & 1) ? h.z : h.x, hh = (tt & 1) ? h.w : h.y;
+    const int hs = 6 - 2 * static_cast<int>(g & 1) - (t >= 4 ? 4 : 0);  // 6 - (bit of the pair)
+    const uint32_t ll = (t >= 4 ? lo >> 2 : lo << 2) & 0x3C3C3C3Cu, lh = (t >= 4 ? hi >> 2 : hi << 2) & 0x3C3C3C3Cu;
+    const uint32_t l2 = ll ^ ((hl << hs) & 0xC0C0C0C0u) ^ 0x80808080u;
+    const uint32_t h2 = lh ^ ((hh << hs) & 0xC0C0C0C0u) ^ 0x80808080u;
+    return static_cast<long>((static_cast<uint64_t>(h2) << 32) | l2);
+  }
 };
 
 // First unit element of window (g, h): Q6_K lane group g = 2*ip + c holds
@@ -271,6 +319,49 @@ template <int QT>
 __device__ __forceinline__ uint32_t window_first(uint32_t g, uint32_t h) {
   if constexpr (QT == kQ6_K) return 128 * (g >> 1) + 32 * (g & 1) + 64 * h;
   return 64 * g + 32 * h;
+}
+
+// Code centring of the decode GEMVs. With w = a q - b they compute
+// a * sum x (q - z) - (b - a z) * sum x with the integer dot products of
+// (q - z) exact, so that a sum x q and b sum x, of similar size, do not cancel
+// in f32 (they cancelled to below their own rounding at small K).
+// - The one-row kernel takes the codes centred on the middle of their range,
+//   z = code_centre, as c (q - z) in signed bytes (centred_codes, c =
+//   code_scale: 16 for Q4_0 and Q4_K, 8 for Q5_K, 4 for Q6_K), and scales
+//   its sums back by 1 / c at the end (a power of two: exact). Q4_0 (b = 8a)
+//   and Q6_K (b = 32a) are left with no offset; Q4_K and Q5_K with b - z a,
+//   over a window sum added pairwise.
+// - The 2-16 row kernel, which subtracts all offsets once at the end, centres
+//   Q4_0 the same way and Q4_K / Q5_K on a zero point per output and window
+//   (window_zero_point), subtracted by the matrix cores themselves: a second
+//   instruction on the same activations with -z in every byte of B.
+// - Q8_0: signed codes, no offset.
+template <int QT>
+constexpr int code_centre() {
+  return QT == kQ4_0 || QT == kQ4_K ? 8 : QT == kQ5_K ? 16 : QT == kQ6_K ? 32 : 0;
+}
+template <int QT>
+constexpr int code_scale() {
+  return QT == kQ4_0 || QT == kQ4_K ? 16 : QT == kQ5_K ? 8 : QT == kQ6_K ? 4 : 1;
+}
+template <int QT>
+constexpr bool window_centered() {
+  return QT == kQ4_K || QT == kQ5_K;
+}
+// The codes of step t as the GEMV's matrix instructions take them.
+template <int QT>
+__device__ __forceinline__ long gemv_codes(const typename Unit<QT>::Raw& r, uint32_t g, int t) {
+  if constexpr (code_scale<QT>() != 1) return Unit<QT>::centred_codes(r, g, t);
+  else return Unit<QT>::codes(r, g, t);
+}
+// Zero point of an affine window (w = a q - b), as a float holding an
+// integer: the integer nearest b / a, clamped to [-127, 127] (so that -z is
+// an int8). Any integer keeps the centring exact; the nearest leaves an
+// offset b - z a of at most a / 2. (a = 0 gives an infinite or NaN quotient;
+// the clamps, which return their other operand for NaN, map both into the
+// range.)
+__device__ __forceinline__ float window_zero_point(float a, float b) {
+  return fminf(fmaxf(rintf(b * __builtin_amdgcn_rcpf(a)), -127.0f), 127.0f);
 }
 
 }  // namespace qi

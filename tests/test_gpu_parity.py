@@ -248,6 +248,42 @@ def test_planar_gemv_tolerance(ctx, qtype, k):
         w.free()
 
 
+@pytest.mark.parametrize("qtype", [qa.Q4_K, qa.Q5_K, qa.Q6_K], ids=lambda q: NAMES[q])
+def test_f32_gemv_wide_scales_k_quants(ctx, qtype):
+    """K-quant images with f32 d/dmin (not f16-exact): the one-row GEMV and
+    the 2-16 row kernels in their f32-scale form, at 3 tiles (one-tile
+    workgroups) and 257 tiles (four-tile workgroups), within the F32 bars."""
+    for k, n, ms in ((1024, 48, (1, 2, 5, 8, 16)), (1024, 4112, (1, 8, 16))):
+        # quantized N(0, 0.02^2) weights whose super-block scales are moved
+        # off the f16 grid (realistic magnitudes, f32 scale planes)
+        blocks = po.make_weights(qtype, k, n, seed=90 + qtype + n, outliers=True)
+        blocks["scale"] *= np.float32(1.0001)
+        if "min_scale" in blocks.dtype.names:
+            blocks["min_scale"] *= np.float32(1.0001)
+        w = ctx.weights(qtype, qa.OUTPUT_ROWS, k, n, blocks)
+        assert w.info().f16_scales == 0
+        for m in ms:
+            x = po.fill_normal(4400 + m, m * k).reshape(m, k)
+            _assert_f32(w.linear(x, qa.MODE_F32), x, blocks, qtype, n, (n, m))
+        w.free()
+
+
+@pytest.mark.parametrize("qtype", [qa.Q4_0, qa.Q4_K, qa.Q5_K, qa.Q6_K], ids=lambda q: NAMES[q])
+def test_f32_gemv_offset_cancellation(ctx, qtype):
+    """The formats with an offset (w = a q - b) at few windows per output,
+    where a sum x q and b sum x of uncentred codes cancel in f32 to about
+    3.5e-5 of sum |x w| (Q4_K, K = 256, 16 rows): centred codes keep every
+    kernel within 1e-5. K = 256 and 2048 take the 2-16 row kernel's zero
+    points, K = 2304 its fixed centre; 1 row is the one-row kernel."""
+    for k, n in ((256, 8192), (2048, 2048), (2304, 2048)):
+        blocks = po.make_weights(qtype, k, n, seed=77 + qtype + k, outliers=True)
+        w = ctx.weights(qtype, qa.OUTPUT_ROWS, k, n, blocks)
+        for m in (1, 8, 16):
+            x = po.fill_normal(4500 + m + k, m * k).reshape(m, k)
+            _assert_f32(w.linear(x, qa.MODE_F32), x, blocks, qtype, n, (k, n, m))
+        w.free()
+
+
 def test_f32_gemv_unrounded_scales(ctx):
     # quantize_q8_0 output without storage rounding keeps f32 scales
     for qtype in (qa.Q8_0, qa.Q4_0):
