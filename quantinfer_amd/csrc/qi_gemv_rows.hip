@@ -501,6 +501,15 @@ __global__ __launch_bounds__(kRowsThreads) void gemv_rows_kernel(RowsArgs a) {
           cmin = __builtin_amdgcn_mfma_f32_16x16x4f32(sx.x, sb_own[0], cmin, 0, 0, 0);
           cmin = __builtin_amdgcn_mfma_f32_16x16x4f32(sx.y, sb_own[1], cmin, 0, 0, 0);
         }
+        // this unit's digit blocks and activation scales per row group; the
+        // windows are then constant offsets from them
+        const uint8_t* dq[MG];
+        const float* xq[MG];
+#pragma unroll
+        for (int q = 0; q < MG; ++q) {
+          dq[q] = dig + (q * cw + u * 8) * kBlock + lane * 8;
+          xq[q] = xsc + (4 * q + g) * cw + u * 8;
+        }
 #pragma unroll
         for (int w = 0; w < 8; ++w) {
           long bw;
@@ -508,9 +517,8 @@ __global__ __launch_bounds__(kRowsThreads) void gemv_rows_kernel(RowsArgs a) {
           else bw = Dense<QT>::b(ct, w);
 #pragma unroll
           for (int q = 0; q < MG; ++q) {
-            const uint32_t qw = q * cw + u * 8 + w;  // (row group, chunk window)
-            const long av = *reinterpret_cast<const long*>(dig + qw * kBlock + lane * 8);
-            const float xw = xsc[(4 * q + g) * cw + u * 8 + w];
+            const long av = *reinterpret_cast<const long*>(dq[q] + w * kBlock);
+            const float xw = xq[q][w];
             v4i c = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, bw, v4i{0, 0, 0, 0}, 0, 0, 0);
             if constexpr (window_centered<QT>() && ZP)
               c = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, pack2(zb[w], zb[w]), c, 0, 0, 0);
