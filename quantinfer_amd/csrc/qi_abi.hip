@@ -224,14 +224,16 @@ qi_hip_status plan_linear(const Image& im, uint64_t m, int32_t mode, LinearPlan*
       // two or more rows, dense operands: one kernel per 16-row chunk; K parts
       // only for shapes with few tiles, by the chunk's row count (a shorter
       // last chunk may take a different count; enqueue_linear asks again)
-      uint64_t floats = 0;
+      uint64_t floats = 0, records = 0;
       for (uint64_t r : {static_cast<uint64_t>(m < 16 ? m : 16), m > 16 ? m % 16 : 0}) {
         if (r < 2) continue;
         const uint32_t pr = qi::gemv_rows_splits(im.k, im.n, static_cast<uint32_t>(r));
         if (pr > 1) floats = std::max(floats, static_cast<uint64_t>(pr) * r * im.n);
+        records = std::max(records, qi::gemv_rows_records_bytes(im.k, im.n, static_cast<uint32_t>(r)));
       }
       p->splits = 1;
       p->s_floats = floats;
+      p->d_floats = (records + 3) / 4;
       return QI_HIP_OK;
     }
     // two or more rows (Q6_K): activation records built once per 16-row chunk,
@@ -304,7 +306,13 @@ qi_hip_status enqueue_linear(const qi_hip_weights* w, const LinearPlan& p, const
           const float* xc = x + m0 * im.k;
           float* const yc = y + m0 * im.n;
           const uint32_t parts = qi::gemv_rows_splits(im.k, im.n, static_cast<uint32_t>(rows));
-          QI_HIP_TRY(qi::launch_gemv_rows(im.qtype, im.wide != 0, v, xc, rows, yc, sws, parts, st),
+          const uint8_t* records = nullptr;
+          if (qi::gemv_rows_records(im.k, im.n, static_cast<uint32_t>(rows))) {
+            QI_HIP_TRY(qi::launch_gemv_rows_records(xc, im.k, rows, reinterpret_cast<uint8_t*>(dws), st),
+                       "launch gemv rows activation records");
+            records = reinterpret_cast<const uint8_t*>(dws);
+          }
+          QI_HIP_TRY(qi::launch_gemv_rows(im.qtype, im.wide != 0, v, xc, rows, yc, sws, parts, records, st),
                      "launch gemv rows");
           if (parts > 1) {
             const uint64_t count = static_cast<uint64_t>(rows) * im.n;

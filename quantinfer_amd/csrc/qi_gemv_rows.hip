@@ -277,6 +277,7 @@ struct RowsArgs {
   uint32_t chunk_units;  // units per LDS chunk
   uint32_t part_units;   // units per K part (grid.y)
   float* part;           // [grid.y][m][n] when grid.y > 1
+  const uint8_t* rec;    // the call's activation records (rows_records_kernel), or null
 };
 
 // Activation prep, in place. Item (q, W, s, r) is slice s (elements 8s..8s+7)
@@ -301,20 +302,13 @@ __device__ __forceinline__ void stage_x(const float* x, uint32_t K, uint32_t k0,
   }
 }
 
-// Convert item t in place: window max and sum over its four slices (lanes 4
-// apart), the power of two 2^-s, the digits; slice 0 stores the window's
-// scale and sum. Items of rows >= M become zero digits.
-__device__ __forceinline__ void prep_item(uint32_t t, uint32_t cw, uint32_t cwin, int M, bool in_range,
-                                          uint8_t* dig, float* xsc, float* xsum) {
-  const uint32_t W = (t >> 4) % cw, q = (t >> 4) / cw, s = (t >> 2) & 3, m = 4 * q + (t & 3);
-  const bool valid = in_range && W < cwin;
-  const bool live = valid && static_cast<int>(m) < M;
-  float4 v0 = make_float4(0.0f, 0.0f, 0.0f, 0.0f), v1 = v0;
-  if (live) {
-    const float4* p = reinterpret_cast<const float4*>(dig + 32 * t);
-    v0 = p[0];
-    v1 = p[1];
-  }
+// Convert item t (activations v0, v1; zeros for rows >= M): window max and
+// sum over its four slices (lanes 4 apart), the power of two 2^-s, the
+// digits, at 32 * t of `dig`; slice 0 stores the window's scale and sum.
+// Every lane takes part (the shuffles); only `valid` items store.
+__device__ __forceinline__ void prep_convert(float4 v0, float4 v1, uint32_t t, uint32_t cw, bool valid,
+                                             uint8_t* dig, float* xsc, float* xsum) {
+  const uint32_t W = (t >> 4) % cw, s = (t >> 2) & 3, m = 4 * ((t >> 4) / cw) + (t & 3);
   const float xs[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
   float mx = 0.0f, sum = 0.0f;
 #pragma unroll
@@ -372,10 +366,86 @@ __device__ __forceinline__ void prep_item(uint32_t t, uint32_t cw, uint32_t cwin
   }
 }
 
+// Convert item t of a chunk in place (its floats staged by stage_x).
+__device__ __forceinline__ void prep_item(uint32_t t, uint32_t cw, uint32_t cwin, int M, bool in_range,
+                                          uint8_t* dig, float* xsc, float* xsum) {
+  const uint32_t W = (t >> 4) % cw, q = (t >> 4) / cw, m = 4 * q + (t & 3);
+  const bool valid = in_range && W < cwin;
+  float4 v0 = make_float4(0.0f, 0.0f, 0.0f, 0.0f), v1 = v0;
+  if (valid && static_cast<int>(m) < M) {
+    const float4* p = reinterpret_cast<const float4*>(dig + 32 * t);
+    v0 = p[0];
+    v1 = p[1];
+  }
+  prep_convert(v0, v1, t, cw, valid, dig, xsc, xsum);
+}
+
+// Four row groups (9-16 rows): the activation records of the whole call,
+// built once into global memory by a kernel of their own, since every
+// workgroup otherwise converts all of them (at 16 rows a quarter of the GEMV,
+// Q4_K 4096 x 14336; the records kernel and its launch cost about a third of
+// that back: 30.0 -> 29.2 us on MI355X; at 8 rows they cost more than they
+// save, 18.8 -> 21.9 us). The layout is the LDS one with the whole K range
+// as one chunk, cw = K / 32 windows: digit
+// blocks [q][window] of kBlock bytes, then the scales [row][window] and the
+// window sums [row][window] as f32, rows 4 MG (zero digits past M).
+constexpr uint64_t rows_records_size(uint64_t k, int mg) {
+  return static_cast<uint64_t>(mg) * (k / 32) * kBlock + 2 * 4 * static_cast<uint64_t>(mg) * (k / 32) * 4;
+}
+
+__global__ __launch_bounds__(256) void rows_records_kernel(const float* x, uint32_t K, int M, int mg, uint8_t* out) {
+  const uint32_t cw = K / 32, items = 16u * static_cast<uint32_t>(mg) * cw;
+  const uint32_t t = blockIdx.x * 256 + threadIdx.x;
+  const bool valid = t < items;
+  const uint32_t W = (t >> 4) % cw, m = 4 * ((t >> 4) / cw) + (t & 3), s = (t >> 2) & 3;
+  float4 v0 = make_float4(0.0f, 0.0f, 0.0f, 0.0f), v1 = v0;
+  if (valid && static_cast<int>(m) < M) {
+    const float4* p = reinterpret_cast<const float4*>(x + static_cast<uint64_t>(m) * K + 32 * W + 8 * s);
+    v0 = p[0];
+    v1 = p[1];
+  }
+  float* const xsc = reinterpret_cast<float*>(out + static_cast<uint64_t>(mg) * cw * kBlock);
+  prep_convert(v0, v1, t, cw, valid, out, xsc, xsc + 4 * mg * cw);
+}
+
+// Copy a chunk's records (windows [w0, w0 + cwin) of every row group) into
+// the LDS layout of chunk stride cw: the digit blocks by global-to-LDS copies
+// (each row group's run is contiguous in both), the scales and sums by one
+// 16-byte load per thread (at most 2 x 4 MG x cwin / 4 = 512 of them), issued
+// with the copies; the caller writes them to LDS (RecordTail) once they land.
+struct RecordTail {
+  float4 v;
+  float* dst;
+};
+__device__ __forceinline__ RecordTail stage_records(const uint8_t* rec, uint32_t wtot, uint32_t w0, uint32_t cwin,
+                                                    uint32_t cw, int mg, uint8_t* dig, float* xsc, uint32_t tid) {
+  const uint32_t wave = tid >> 6, lane = tid & 63;
+  const uint32_t per_q = cwin * kBlock / 1024;  // 1 KB copies per row group
+  for (uint32_t j = wave; j < static_cast<uint32_t>(mg) * per_q; j += kRowsThreads / 64) {
+    const uint32_t q = j / per_q, pc = j % per_q;
+    __builtin_amdgcn_global_load_lds(rec + (static_cast<uint64_t>(q) * wtot + w0) * kBlock + pc * 1024 + lane * 16,
+                                     (__attribute__((address_space(3))) void*)(dig + q * cw * kBlock + pc * 1024),
+                                     16, 0, 0);
+  }
+  RecordTail r{make_float4(0.0f, 0.0f, 0.0f, 0.0f), nullptr};
+  const uint32_t rows = 4 * static_cast<uint32_t>(mg), per_row = cwin / 4;
+  if (tid < 2 * rows * per_row) {
+    const uint32_t which = tid / (rows * per_row), rem = tid % (rows * per_row);
+    const uint32_t row = rem / per_row, i = rem % per_row;
+    const float* src = reinterpret_cast<const float*>(rec + static_cast<uint64_t>(mg) * wtot * kBlock) +
+                       (static_cast<uint64_t>(which) * rows + row) * wtot + w0 + 4 * i;
+    r.v = *reinterpret_cast<const float4*>(src);
+    r.dst = xsc + (which * rows + row) * cw + 4 * i;
+  }
+  return r;
+}
+
 // MG row groups (M <= 4 MG), D units of weights in flight per wavefront, TL
 // tiles per workgroup (4, or 1 with 16 K slices for shapes of up to one tile
 // per CU). ZP (Q4_K / Q5_K): the codes centred on a zero point per window
-// (rows_zero_points); otherwise on the middle of their range.
+// (window_zero_point, kRowsZeroPointUnits); otherwise on the middle of their
+// range. Given the call's activation records (a.rec; four row groups), the
+// workgroups copy them; otherwise each converts its activations itself.
 template <int QT, bool WIDE, int MG, int D, int TL, bool ZP>
 __global__ __launch_bounds__(kRowsThreads) void gemv_rows_kernel(RowsArgs a) {
   // codes centred on the middle of their range, and their scale
@@ -429,19 +499,33 @@ __global__ __launch_bounds__(kRowsThreads) void gemv_rows_kernel(RowsArgs a) {
     // global-to-LDS copy, and vector memory completes in order, so a copy
     // waited for after the weight loads would wait for the weights. The
     // weights' HBM latency then overlaps the prep instead.
-    stage_x(a.x, K, ku0 * 256, M, MG, cw, cwin, dig, wave, lane);
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    if (MG >= 4 && !ZP && a.rec != nullptr) {
+      // the call's records (rows_records_kernel): copies, then the weights
+      const RecordTail rt = stage_records(a.rec, K / 32, ku0 * 8, cwin, cw, MG, dig, xsc, tid);
+      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+      if (rt.dst != nullptr) *reinterpret_cast<float4*>(rt.dst) = rt.v;
 #pragma unroll
-    for (int i = 0; i < D; ++i)
-      if (i < static_cast<int>(u_count))
-        U::template load<WIDE, true>(trec + (ku0 + u_begin + i) * R.bytes, lane, ring[i]);
-    // every wavefront's copies have landed; a bare barrier (a fenced one
-    // would wait for the weight loads)
-    __builtin_amdgcn_s_barrier();
-    const uint32_t items = 16u * MG * cw;
-    for (uint32_t t = tid; t < items; t += kRowsThreads) prep_item(t, cw, cwin, M, true, dig, xsc, xsum);
-    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wavefront's records are written
-    __builtin_amdgcn_s_barrier();
+      for (int i = 0; i < D; ++i)
+        if (i < static_cast<int>(u_count))
+          U::template load<WIDE, true>(trec + (ku0 + u_begin + i) * R.bytes, lane, ring[i]);
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wavefront's scale and sum stores
+      __builtin_amdgcn_s_barrier();
+    } else {
+      // this workgroup's own conversion of its activations
+      stage_x(a.x, K, ku0 * 256, M, MG, cw, cwin, dig, wave, lane);
+      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+#pragma unroll
+      for (int i = 0; i < D; ++i)
+        if (i < static_cast<int>(u_count))
+          U::template load<WIDE, true>(trec + (ku0 + u_begin + i) * R.bytes, lane, ring[i]);
+      // every wavefront's copies have landed; a bare barrier (a fenced one
+      // would wait for the weight loads)
+      __builtin_amdgcn_s_barrier();
+      const uint32_t items = 16u * MG * cw;
+      for (uint32_t t = tid; t < items; t += kRowsThreads) prep_item(t, cw, cwin, M, true, dig, xsc, xsum);
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wavefront's records are written
+      __builtin_amdgcn_s_barrier();
+    }
 
     auto consume = [&](uint32_t j) {
 #pragma unroll
@@ -473,8 +557,8 @@ __global__ __launch_bounds__(kRowsThreads) void gemv_rows_kernel(RowsArgs a) {
           cmin = __builtin_amdgcn_mfma_f32_16x16x4f32(sx.x, fmaf(-z, sa_own[0], sb_own[0]), cmin, 0, 0, 0);
           cmin = __builtin_amdgcn_mfma_f32_16x16x4f32(sx.y, fmaf(-z, sa_own[1], sb_own[1]), cmin, 0, 0, 0);
         }
-        // ZP: -z of window w of this output in every byte of zb[w]
-        [[maybe_unused]] uint32_t zb[8];
+        // ZP: -z of windows 2k and 2k + 1 of this output as bytes 0 and 1 of zg[k]
+        [[maybe_unused]] uint32_t zg[4];
         if constexpr (window_centered<QT>() && ZP) {
           // zero points of windows 2g, 2g + 1 (window_zero_point) and the
           // offsets left, b - z a (exactly rounded); -z of both as bytes 0
@@ -488,11 +572,7 @@ __global__ __launch_bounds__(kRowsThreads) void gemv_rows_kernel(RowsArgs a) {
           float t[4];
           gather4(__builtin_bit_cast(float, nz), t);
 #pragma unroll
-          for (int gp = 0; gp < 4; ++gp) {
-            const uint32_t v = __builtin_bit_cast(uint32_t, t[gp]);
-            zb[2 * gp] = __builtin_amdgcn_perm(0u, v, 0x00000000u);      // byte 0 everywhere
-            zb[2 * gp + 1] = __builtin_amdgcn_perm(0u, v, 0x01010101u);  // byte 1 everywhere
-          }
+          for (int gp = 0; gp < 4; ++gp) zg[gp] = __builtin_bit_cast(uint32_t, t[gp]);
           // offsets of windows 2k + h (k = lane group) of this unit for the
           // tile's outputs, times the rows' window sums
           const float2 sx = mrow < 4 * MG
@@ -520,8 +600,11 @@ __global__ __launch_bounds__(kRowsThreads) void gemv_rows_kernel(RowsArgs a) {
             const long av = *reinterpret_cast<const long*>(dq[q] + w * kBlock);
             const float xw = xq[q][w];
             v4i c = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, bw, v4i{0, 0, 0, 0}, 0, 0, 0);
-            if constexpr (window_centered<QT>() && ZP)
-              c = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, pack2(zb[w], zb[w]), c, 0, 0, 0);
+            if constexpr (window_centered<QT>() && ZP) {
+              // byte (w & 1) of zg[w / 2] everywhere
+              const uint32_t zb = __builtin_amdgcn_perm(0u, zg[w >> 1], (w & 1) ? 0x01010101u : 0u);
+              c = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, pack2(zb, zb), c, 0, 0, 0);
+            }
             // pairs exactly in int32 (|C0| < 2^20, |C1 * 256| < 2^28), halves in f32
             const float comb = fmaf(static_cast<float>(c[2] + c[3] * 256), 65536.0f,
                                     static_cast<float>(c[0] + c[1] * 256));
@@ -667,10 +750,34 @@ uint32_t gemv_rows_splits(uint64_t k, uint64_t n, uint32_t m) {
   return static_cast<uint32_t>(s);
 }
 
+bool gemv_rows_records(uint64_t k, uint64_t n, uint32_t m) {
+  // where every workgroup would convert more than 8 units of K (per K part);
+  // below that the records kernel and its launch cost more than they save
+  // (Q4_0 4096 x 4096 M=12, four parts of 4 units: 15.7 -> 17.6 us). The
+  // zero-point kernels (at most 8 units) thus always convert their own.
+  if (m <= 8 || m > 16) return false;
+  const uint64_t units = k / 256, parts = gemv_rows_splits(k, n, m);
+  return (units + parts - 1) / parts > kRowsZeroPointUnits;
+}
+
+uint64_t gemv_rows_records_bytes(uint64_t k, uint64_t n, uint32_t m) {
+  return gemv_rows_records(k, n, m) ? rows_records_size(k, 4) : 0;
+}
+
+hipError_t launch_gemv_rows_records(const float* x, uint64_t k, int m, uint8_t* out, hipStream_t st) {
+  if (m <= 8 || m > 16 || k % 256 != 0 || out == nullptr) return hipErrorInvalidValue;
+  const int mg = 4;
+  const uint64_t items = 16ull * static_cast<uint64_t>(mg) * (k / 32);
+  hipLaunchKernelGGL(rows_records_kernel, dim3(static_cast<uint32_t>((items + 255) / 256)), dim3(256), 0, st, x,
+                     static_cast<uint32_t>(k), m, mg, out);
+  return hipGetLastError();
+}
+
 hipError_t launch_gemv_rows(int32_t qtype, bool wide, const View& w, const float* x, int m, float* y, float* part,
-                            uint32_t ksplit, hipStream_t st) {
+                            uint32_t ksplit, const uint8_t* records, hipStream_t st) {
   if (m < 1 || m > 16 || ksplit < 1) return hipErrorInvalidValue;
-  RowsArgs a{w, x, y, m, 0, 0, part};
+  if ((records != nullptr) != gemv_rows_records(w.k, w.n, static_cast<uint32_t>(m))) return hipErrorInvalidValue;
+  RowsArgs a{w, x, y, m, 0, 0, part, records};
   const uint32_t units = w.units;
   a.part_units = (units + ksplit - 1) / ksplit;
   const uint32_t parts = (units + a.part_units - 1) / a.part_units;

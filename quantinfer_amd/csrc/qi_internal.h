@@ -73,11 +73,17 @@ hipError_t launch_gemv_mfma(int32_t qtype, bool wide, int mt, int split, const G
 // Matrix-core decode GEMV of 2-16 rows with dense operands (qi_gemv_rows.hip):
 // one kernel, K parts over the grid (gemv_rows_splits, by shape and row count)
 // only for shapes with few tiles; with ksplit > 1 the partial sums
-// [ksplit][m][n] go to `part` and launch_splitk_sum adds them.
+// [ksplit][m][n] go to `part` and launch_splitk_sum adds them. Where
+// gemv_rows_records (9-16 rows, no K parts) the GEMV reads the activation
+// records that launch_gemv_rows_records builds into `records`
+// (gemv_rows_records_bytes bytes, 0 elsewhere; null records elsewhere).
 bool gemv_rows_supported(int32_t qtype, int32_t layout, uint64_t k);
 uint32_t gemv_rows_splits(uint64_t k, uint64_t n, uint32_t m);
+bool gemv_rows_records(uint64_t k, uint64_t n, uint32_t m);
+uint64_t gemv_rows_records_bytes(uint64_t k, uint64_t n, uint32_t m);
+hipError_t launch_gemv_rows_records(const float* x, uint64_t k, int m, uint8_t* out, hipStream_t st);
 hipError_t launch_gemv_rows(int32_t qtype, bool wide, const View& w, const float* x, int m, float* y, float* part,
-                            uint32_t ksplit, hipStream_t st);
+                            uint32_t ksplit, const uint8_t* records, hipStream_t st);
 
 // Row-major (blocks along N) GEMV of up to 4 activation rows, f32
 // accumulation, K split over the grid; `part` holds splits * m * n floats when
