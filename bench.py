@@ -164,7 +164,8 @@ def gemv_line(qtype: int, k: int, n: int, m: int, g: dict, steps: int, warmup: i
                    "event_region_overhead_us": round(g["empty_region_us"], 2), "device": g["device"]},
         "roofline": {"bound": "hbm", "achieved": round(gbps, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(gbps / HBM_PEAK_GBPS, 4),
-                     "traffic": traffic_from_profile(f"{q}_gemv_{k}x{n}_traffic.md")},
+                     "traffic": traffic_from_profile(f"{q}_gemv_{k}x{n}_traffic.md" if m == 1
+                                                     else f"{q}_gemv_m{m}_{k}x{n}_counters.md")},
     }
 
 
