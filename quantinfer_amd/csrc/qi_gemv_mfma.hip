@@ -153,8 +153,8 @@ __device__ __forceinline__ void store_half(const HalfX& o, const Item& it, bool 
 #pragma unroll
   for (int j = 0; j < 4; ++j) ps[j] = ps[2 * j] + ps[2 * j + 1];
   const float sum = (ps[0] + ps[1]) + (ps[2] + ps[3]);
-  mx = fmaxf(mx, __shfl_xor(mx, 1));
-  const float other = __shfl_xor(sum, 1);
+  mx = fmaxf(mx, dpp_move<kDppSwap1>(mx));
+  const float other = dpp_move<kDppSwap1>(sum);
   // A NaN or infinite activation makes the window sum non-finite. Its scale
   // is then NaN, so every output of the row comes out NaN and the GEMV's
   // epilogue recomputes it in the reference's order; the digits are built

@@ -302,13 +302,14 @@ __device__ __forceinline__ void stage_x(const float* x, uint32_t K, uint32_t k0,
   }
 }
 
-// Convert item t (activations v0, v1; zeros for rows >= M): window max and
-// sum over its four slices (lanes 4 apart), the power of two 2^-s, the
-// digits, at 32 * t of `dig`; slice 0 stores the window's scale and sum.
-// Every lane takes part (the shuffles); only `valid` items store.
-__device__ __forceinline__ void prep_convert(float4 v0, float4 v1, uint32_t t, uint32_t cw, bool valid,
-                                             uint8_t* dig, float* xsc, float* xsum) {
-  const uint32_t W = (t >> 4) % cw, s = (t >> 2) & 3, m = 4 * ((t >> 4) / cw) + (t & 3);
+// Convert item t (activations v0, v1; zeros for rows >= M) of row group q,
+// window W: window max and sum over its four slices (lanes 4, 8 and 12
+// apart), the power of two 2^-s, the digits, at 32 * t of `dig`; slice 0
+// stores the window's scale and sum. Every lane of the wavefront takes part
+// (the lane moves); only `valid` items store.
+__device__ __forceinline__ void prep_convert(float4 v0, float4 v1, uint32_t t, uint32_t q, uint32_t W, uint32_t cw,
+                                             bool valid, uint8_t* dig, float* xsc, float* xsum) {
+  const uint32_t s = (t >> 2) & 3, m = 4 * q + (t & 3);
   const float xs[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
   float mx = 0.0f, sum = 0.0f;
 #pragma unroll
@@ -316,10 +317,11 @@ __device__ __forceinline__ void prep_convert(float4 v0, float4 v1, uint32_t t, u
     mx = fmaxf(mx, fabsf(xs[j]));
     sum += xs[j];
   }
-  mx = fmaxf(mx, __shfl_xor(mx, 4));
-  mx = fmaxf(mx, __shfl_xor(mx, 8));
-  sum += __shfl_xor(sum, 4);
-  sum += __shfl_xor(sum, 8);
+  // the four slices of a window are lanes r, r + 4, r + 8, r + 12 of a row of 16
+  mx = fmaxf(mx, dpp_move<kDppRor4>(mx));
+  mx = fmaxf(mx, dpp_move<kDppRor8>(mx));
+  sum += dpp_move<kDppRor4>(sum);
+  sum += dpp_move<kDppRor8>(sum);
   // A NaN or infinite activation makes the window sum non-finite: the scale
   // is then NaN (every output of the row comes out NaN and the epilogue
   // recomputes it in the reference's order) and the digits are zero.
@@ -328,12 +330,14 @@ __device__ __forceinline__ void prep_convert(float4 v0, float4 v1, uint32_t t, u
   const int sh = 29 - e;  // max|x| * 2^sh < 2^29
   const float inv = !finite ? __builtin_nanf("") : mx > 0.0f ? ldexpf(1.0f, e - 29) : 0.0f;
   if (!valid) return;
-  uint32_t dg[8];
+  uint32_t dg[8] = {0, 0, 0, 0, 0, 0, 0, 0};  // zero digits for a non-finite window
+  if (finite) {
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int F = finite ? static_cast<int>(rintf(ldexpf(xs[j], sh))) : 0;
-    // signed base-256 digits: byte i of (F + 0x808080) ^ 0x808080
-    dg[j] = (static_cast<uint32_t>(F) + 0x00808080u) ^ 0x00808080u;
+    for (int j = 0; j < 8; ++j) {
+      const int F = static_cast<int>(rintf(ldexpf(xs[j], sh)));
+      // signed base-256 digits: byte i of (F + 0x808080) ^ 0x808080
+      dg[j] = (static_cast<uint32_t>(F) + 0x00808080u) ^ 0x00808080u;
+    }
   }
   // digit d of the 8 elements: byte d of dg[0..3] (low word), of dg[4..7] (high word)
   uint32_t lo[4], hi[4];
@@ -366,18 +370,19 @@ __device__ __forceinline__ void prep_convert(float4 v0, float4 v1, uint32_t t, u
   }
 }
 
-// Convert item t of a chunk in place (its floats staged by stage_x).
-__device__ __forceinline__ void prep_item(uint32_t t, uint32_t cw, uint32_t cwin, int M, bool in_range,
+// Convert item t (row group q, window W) of a chunk in place (its floats
+// staged by stage_x).
+__device__ __forceinline__ void prep_item(uint32_t t, uint32_t q, uint32_t W, uint32_t cw, uint32_t cwin, int M,
                                           uint8_t* dig, float* xsc, float* xsum) {
-  const uint32_t W = (t >> 4) % cw, q = (t >> 4) / cw, m = 4 * q + (t & 3);
-  const bool valid = in_range && W < cwin;
+  const uint32_t m = 4 * q + (t & 3);
+  const bool valid = W < cwin;
   float4 v0 = make_float4(0.0f, 0.0f, 0.0f, 0.0f), v1 = v0;
   if (valid && static_cast<int>(m) < M) {
     const float4* p = reinterpret_cast<const float4*>(dig + 32 * t);
     v0 = p[0];
     v1 = p[1];
   }
-  prep_convert(v0, v1, t, cw, valid, dig, xsc, xsum);
+  prep_convert(v0, v1, t, q, W, cw, valid, dig, xsc, xsum);
 }
 
 // Four row groups (9-16 rows): the activation records of the whole call,
@@ -405,7 +410,7 @@ __global__ __launch_bounds__(256) void rows_records_kernel(const float* x, uint3
     v1 = p[1];
   }
   float* const xsc = reinterpret_cast<float*>(out + static_cast<uint64_t>(mg) * cw * kBlock);
-  prep_convert(v0, v1, t, cw, valid, out, xsc, xsc + 4 * mg * cw);
+  prep_convert(v0, v1, t, (t >> 4) / cw, W, cw, valid, out, xsc, xsc + 4 * mg * cw);
 }
 
 // Copy a chunk's records (windows [w0, w0 + cwin) of every row group) into
@@ -521,8 +526,18 @@ __global__ __launch_bounds__(kRowsThreads) void gemv_rows_kernel(RowsArgs a) {
       // every wavefront's copies have landed; a bare barrier (a fenced one
       // would wait for the weight loads)
       __builtin_amdgcn_s_barrier();
+      // items t = tid + 1024 i: block t / 16 advances by 64 windows a step,
+      // (row group, window) kept without a division per item
       const uint32_t items = 16u * MG * cw;
-      for (uint32_t t = tid; t < items; t += kRowsThreads) prep_item(t, cw, cwin, M, true, dig, xsc, xsum);
+      uint32_t q = (tid >> 4) / cw, W = (tid >> 4) % cw;
+      for (uint32_t t = tid; t < items; t += kRowsThreads) {
+        prep_item(t, q, W, cw, cwin, M, dig, xsc, xsum);
+        W += kRowsThreads / 16;
+        while (W >= cw) {
+          W -= cw;
+          ++q;
+        }
+      }
       __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wavefront's records are written
       __builtin_amdgcn_s_barrier();
     }

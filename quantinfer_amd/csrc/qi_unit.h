@@ -354,6 +354,18 @@ __device__ __forceinline__ long gemv_codes(const typename Unit<QT>::Raw& r, uint
   if constexpr (code_scale<QT>() != 1) return Unit<QT>::centred_codes(r, g, t);
   else return Unit<QT>::codes(r, g, t);
 }
+// A lane's value moved by a DPP pattern (all lanes of the wavefront active):
+// kDppSwap1 from lane i ^ 1, kDppRor4 / kDppRor8 from lane (i + 4) / (i + 8)
+// mod 16 within each row of 16 lanes. VALU operand modifiers, no LDS round
+// trip (unlike __shfl_xor).
+constexpr int kDppSwap1 = 0xB1;  // quad_perm [1, 0, 3, 2]
+constexpr int kDppRor4 = 0x124;  // row_ror:4
+constexpr int kDppRor8 = 0x128;  // row_ror:8
+template <int CTRL>
+__device__ __forceinline__ float dpp_move(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
 // Zero point of an affine window (w = a q - b), as a float holding an
 // integer: the integer nearest b / a, clamped to [-127, 127] (so that -z is
 // an int8). Any integer keeps the centring exact; the nearest leaves an
