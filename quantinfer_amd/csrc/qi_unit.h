@@ -367,11 +367,11 @@ __device__ __forceinline__ float dpp_move(float v) {
 }
 
 // Zero point of an affine window (w = a q - b), as a float holding an
-// integer: the integer nearest b / a, clamped to [-127, 127] (so that -z is
-// an int8). Any integer keeps the centring exact; the nearest leaves an
-// offset b - z a of at most a / 2. (a = 0 gives an infinite or NaN quotient;
-// the clamps, which return their other operand for NaN, map both into the
-// range.)
+// integer: the integer nearest b / a (by the hardware reciprocal, so within
+// one of it), clamped to [-127, 127] so that -z is an int8. Any integer keeps
+// the centring exact; one near b / a leaves an offset b - z a of about a / 2
+// at most. (a = 0 gives an infinite or NaN quotient; the clamps, which return
+// their other operand for NaN, map both into the range.)
 __device__ __forceinline__ float window_zero_point(float a, float b) {
   return fminf(fmaxf(rintf(b * __builtin_amdgcn_rcpf(a)), -127.0f), 127.0f);
 }
