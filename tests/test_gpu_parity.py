@@ -304,10 +304,12 @@ CONFIGS = [
     (qa.Q4_0, 4096, 1024, [1, 4, 16, 20], False),
     (qa.Q4_0, 4096, 12288, [1, 4, 16], False),
     (qa.Q4_0, 12288, 4096, [1, 4, 16], False),
-    (qa.Q4_K, 4096, 14336, [1, 8], True),
-    (qa.Q4_K, 14336, 4096, [1, 8], True),
+    # 12 and 16 rows: activation records built once per call (more than 8
+    # units per K part), also with K parts (14336 x 4096)
+    (qa.Q4_K, 4096, 14336, [1, 8, 12], True),
+    (qa.Q4_K, 14336, 4096, [1, 8, 16], True),
     (qa.Q5_K, 4096, 14336, [1, 8], True),
-    (qa.Q5_K, 14336, 4096, [1, 8], True),
+    (qa.Q5_K, 14336, 4096, [1, 8, 16], True),
     (qa.Q6_K, 4096, 14336, [1, 8], True),
     (qa.Q6_K, 14336, 4096, [1, 8], True),
     (qa.Q8_0, 4096, 14336, [1], False),
