@@ -6,13 +6,16 @@
 // is cut into windows of 32 elements; an element becomes the 30-bit integer
 // F = rint(x * 2^s) (2^s per (row, window) from the window's max |x|), held
 // as four signed 8-bit digits; weight codes enter the matrix cores as bytes,
-// centred as there (Q4_0 as 16 (q - 8); Q4_K and Q5_K as q - z with a zero
-// point z per window, by a second matrix instruction with -z in every B byte),
-// so every digit sum is exact in int32, and per (row, window, output)
+// centred as there (Q4_0 as 16 (q - 8), Q6_K as 4 (q - 32); Q4_K and Q5_K as
+// q - z with a zero point z per window, by a second matrix instruction with -z
+// in every B byte), so every digit sum is exact in int32, and per (row,
+// window, output)
 //   sum_k x_k w_k = a * 2^-s * (C0 + C1*2^8 + C2*2^16 + C3*2^24) - b' * sum_k x_k
 // with the format's sub-block scale a and the offset left, b' = b - z a
 // (w = a*q - b). The offset terms of all windows go through f32 matrix
 // instructions (v_mfma_f32_16x16x4_f32: window sums x per-output offsets).
+// Q6_K's windows hold two 16-element sub-blocks of their own scales, whose
+// digit sums two instructions per window keep apart (consume_q6).
 //
 // Dense operands. One 16x16x32 instruction covers one window for four
 // activation rows and the tile's 16 outputs: A row 4r + d holds digit d of
@@ -219,6 +222,39 @@ struct Dense<kQ4_K> : DenseQ45K<false> {};
 template <>
 struct Dense<kQ5_K> : DenseQ45K<true> {};
 
+// Q6_K: lane group g' = 2ip + c holds ql bytes [64ip + 32c, +32) of the
+// super-block, window w = 4ip + 2hf + c (elements 32w..32w+31) being the low
+// (hf = 0) or high (hf = 1) nibbles of them, so the ql words cross the lane
+// groups as Q4_K's do. Slice g of window w takes its two high bits from bits
+// 2c + 4hf of qh bytes 32ip + 8g..8g+7, which each lane group loads for itself
+// (h[2ip], h[2ip + 1]; RowsUnit<kQ6_K>). The codes go out as the one-row
+// kernel takes them (Unit<kQ6_K>::centred_codes): 4 (q - 32) as signed bytes.
+template <>
+struct Dense<kQ6_K> {
+  struct T {
+    uint32_t lo[4], hi[4];
+    uint32_t h[4];
+  };
+  template <bool C, typename Raw>
+  __device__ static void prepare(const Raw& r, uint32_t, T& t) {
+    t.lo[0] = r.q[0].x; t.lo[1] = r.q[0].z; t.lo[2] = r.q[1].x; t.lo[3] = r.q[1].z;
+    t.hi[0] = r.q[0].y; t.hi[1] = r.q[0].w; t.hi[2] = r.q[1].y; t.hi[3] = r.q[1].w;
+    xpose4(t.lo);
+    xpose4(t.hi);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) t.h[i] = r.h[i];
+  }
+  __device__ static long bc(const T& t, int w) {
+    const int ip = w >> 2, hf = (w >> 1) & 1, c = w & 1, gp = 2 * ip + c;
+    const int up = 6 - 2 * c - 4 * hf;  // qh bits 2c + 4hf to bits 6-7
+    const uint32_t nl = (hf ? t.lo[gp] >> 2 : t.lo[gp] << 2) & 0x3C3C3C3Cu;
+    const uint32_t nh = (hf ? t.hi[gp] >> 2 : t.hi[gp] << 2) & 0x3C3C3C3Cu;
+    const uint32_t a = nl ^ ((t.h[2 * ip] << up) & 0xC0C0C0C0u) ^ 0x80808080u;
+    const uint32_t b = nh ^ ((t.h[2 * ip + 1] << up) & 0xC0C0C0C0u) ^ 0x80808080u;
+    return pack2(a, b);
+  }
+};
+
 // Weight access of one unit: the one-row kernel's (qi_unit.h), except that
 // Q5_K loads only the 8 qh bytes of slice g (not all 32 of the output), which
 // keeps the 16-wavefront register budget.
@@ -266,6 +302,48 @@ struct RowsUnit<kQ5_K> {
     u.s0 = r.s0;
     u.s1 = r.s1;
     Unit<kQ5_K>::template scales<W>(g, u, a, b);
+  }
+};
+
+// Q6_K: the ql chunks as the one-row kernel loads them; the qh bytes of slice
+// g of both halves (bytes 8g..8g+7 of 32ip + [0, 32), ip = 0, 1) instead of
+// the lane group's own 32, and the row's 16 sub-scales (tiled order,
+// q6_scale_pos: window w's two at bytes 2hf, 2hf + 1 of word 2ip + c).
+template <>
+struct RowsUnit<kQ6_K> {
+  struct Raw {
+    uint4 q[2];
+    uint32_t h[4];
+    uint4 sc;
+    uint32_t d;  // f16 in the low half, or f32
+  };
+  template <bool W, bool NT>
+  __device__ static void load(const uint8_t* rec, uint32_t lane, Raw& r) {
+    constexpr Record R = record_geometry(kQ6_K, W);
+    const uint32_t col = lane & 15, g = lane >> 4;
+    const uint4* p = reinterpret_cast<const uint4*>(rec + R.qs) + lane;
+    r.q[0] = ld_codes<true>(p);
+    r.q[1] = ld_codes<true>(p + 64);
+    // 16-byte chunk 2ip + g / 2 of row col's qh, its half g % 2
+#pragma unroll
+    for (int ip = 0; ip < 2; ++ip) {
+      const uint2 h = *reinterpret_cast<const uint2*>(rec + R.qh + (2 * ip + (g >> 1)) * 256 + col * 16 + (g & 1) * 8);
+      r.h[2 * ip] = h.x;
+      r.h[2 * ip + 1] = h.y;
+    }
+    r.sc = *reinterpret_cast<const uint4*>(rec + R.sc + col * 16);
+    if constexpr (W) r.d = reinterpret_cast<const uint32_t*>(rec + R.d)[col];
+    else r.d = reinterpret_cast<const uint16_t*>(rec + R.d)[col];
+  }
+  template <bool W>
+  __device__ static float d(const Raw& r) {
+    if constexpr (W) return __builtin_bit_cast(float, r.d);
+    else return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(r.d)));
+  }
+  // the sub-scales of window w, word 2ip + c of the row's 16
+  __device__ static uint32_t window_scales(const Raw& r, int w) {
+    const int word = 2 * (w >> 2) + (w & 1);
+    return word == 0 ? r.sc.x : word == 1 ? r.sc.y : word == 2 ? r.sc.z : r.sc.w;
   }
 };
 
@@ -454,11 +532,10 @@ __device__ __forceinline__ RecordTail stage_records(const uint8_t* rec, uint32_t
 template <int QT, bool WIDE, int MG, int D, int TL, bool ZP>
 __global__ __launch_bounds__(kRowsThreads) void gemv_rows_kernel(RowsArgs a) {
   // codes centred on the middle of their range, and their scale
-  constexpr bool kFixed = QT == kQ4_0 || (window_centered<QT>() && !ZP);
+  constexpr bool kFixed = QT == kQ4_0 || QT == kQ6_K || (window_centered<QT>() && !ZP);
   constexpr float kInvScale = kFixed ? 1.0f / static_cast<float>(code_scale<QT>()) : 1.0f;
   constexpr int SL = kRowsWaves / TL;  // K slices per tile
   using U = RowsUnit<QT>;
-  static_assert(QT != kQ6_K, "Q6_K windows are 16 elements");
   constexpr Record R = record_geometry(QT, WIDE);
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   const uint32_t cu = a.chunk_units, cw = 8 * cu;
@@ -542,92 +619,149 @@ __global__ __launch_bounds__(kRowsThreads) void gemv_rows_kernel(RowsArgs a) {
       __builtin_amdgcn_s_barrier();
     }
 
+    // Q6_K: each 32-element window holds two 16-element sub-blocks of their
+    // own scales. The window's codes go in twice, in one instruction with
+    // lane groups 0-1 (elements 0-15) and in one with lane groups 2-3
+    // (elements 16-31), the others zero, so each sub-block's digit sums come
+    // out apart; the int8 sub-scales weight them per window and d per unit.
+    [[maybe_unused]] auto consume_q6 = [&](uint32_t u, const typename U::Raw& r) __attribute__((always_inline)) {
+      if constexpr (QT == kQ6_K) {
+        typename Dense<QT>::T ct;
+        Dense<QT>::template prepare<true>(r, g, ct);
+        const uint32_t keep = g < 2 ? ~0u : 0u;  // this lane group's slice in the first sub-block
+        const uint8_t* dq[MG];
+        const float* xq[MG];
+        float accu[MG];
+#pragma unroll
+        for (int q = 0; q < MG; ++q) {
+          dq[q] = dig + (q * cw + u * 8) * kBlock + lane * 8;
+          xq[q] = xsc + (4 * q + g) * cw + u * 8;
+          accu[q] = 0.0f;
+        }
+#pragma unroll
+        for (int w = 0; w < 8; ++w) {
+          const long bw = Dense<QT>::bc(ct, w);
+          const uint32_t b_lo = static_cast<uint32_t>(bw), b_hi = static_cast<uint32_t>(static_cast<uint64_t>(bw) >> 32);
+          const long b0 = pack2(b_lo & keep, b_hi & keep);
+          const long b1 = pack2(b_lo & ~keep, b_hi & ~keep);
+          const uint32_t sw = U::window_scales(r, w);
+          const int hf = (w >> 1) & 1;
+          const float s0 = static_cast<float>(static_cast<int32_t>(sw << (24 - 16 * hf)) >> 24);
+          const float s1 = static_cast<float>(static_cast<int32_t>(sw << (16 - 16 * hf)) >> 24);
+#pragma unroll
+          for (int q = 0; q < MG; ++q) {
+            const long av = *reinterpret_cast<const long*>(dq[q] + w * kBlock);
+            const float xw = xq[q][w];
+            const v4i c0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, b0, v4i{0, 0, 0, 0}, 0, 0, 0);
+            const v4i c1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, b1, v4i{0, 0, 0, 0}, 0, 0, 0);
+            // pairs exactly in int32 (|C0| < 2^19, |C1 * 256| < 2^27), halves in f32
+            const float comb0 = fmaf(static_cast<float>(c0[2] + c0[3] * 256), 65536.0f,
+                                     static_cast<float>(c0[0] + c0[1] * 256));
+            const float comb1 = fmaf(static_cast<float>(c1[2] + c1[3] * 256), 65536.0f,
+                                     static_cast<float>(c1[0] + c1[1] * 256));
+            accu[q] = fmaf(xw, fmaf(s1, comb1, s0 * comb0), accu[q]);
+            // the window's sums are combined here, not after the last window
+            // (the compiler would otherwise keep every window's digit sums live)
+            asm volatile("" : "+v"(accu[q]));
+          }
+          __builtin_amdgcn_sched_barrier(0);
+        }
+        const float d = U::template d<WIDE>(r);
+#pragma unroll
+        for (int q = 0; q < MG; ++q) acc[q] = fmaf(d, accu[q], acc[q]);
+      }
+    };
+
     auto consume = [&](uint32_t j) {
 #pragma unroll
       for (int i = 0; i < D; ++i) {
         if (j + i >= u_count) break;
         const uint32_t u = u_begin + j + i;  // chunk-relative unit
-        float sa_own[2], sb_own[2];
-        U::template scales<WIDE>(g, ring[i], sa_own, sb_own);
-        float sa[8];
-        {
-          float t[4];
-          gather4(sa_own[0], t);
+        if constexpr (QT == kQ6_K) {
+          consume_q6(u, ring[i]);
+        } else {
+          float sa_own[2], sb_own[2];
+          U::template scales<WIDE>(g, ring[i], sa_own, sb_own);
+          float sa[8];
+          {
+            float t[4];
+            gather4(sa_own[0], t);
 #pragma unroll
-          for (int gp = 0; gp < 4; ++gp) sa[2 * gp] = t[gp];
-          gather4(sa_own[1], t);
+            for (int gp = 0; gp < 4; ++gp) sa[2 * gp] = t[gp];
+            gather4(sa_own[1], t);
 #pragma unroll
-          for (int gp = 0; gp < 4; ++gp) sa[2 * gp + 1] = t[gp];
-        }
-        typename Dense<QT>::T ct;
-        Dense<QT>::template prepare<kFixed>(ring[i], g, ct);
-        if constexpr (window_centered<QT>() && !ZP) {
-          // the offsets left by the centred codes, b - z a (exactly rounded),
-          // of windows 2k + h (k = lane group) of this unit for the tile's
-          // outputs, times the rows' window sums
-          constexpr float z = static_cast<float>(code_centre<QT>());
-          const float2 sx = mrow < 4 * MG
-                                ? *reinterpret_cast<const float2*>(xsum + mrow * cw + u * 8 + 2 * g)
-                                : make_float2(0.0f, 0.0f);
-          cmin = __builtin_amdgcn_mfma_f32_16x16x4f32(sx.x, fmaf(-z, sa_own[0], sb_own[0]), cmin, 0, 0, 0);
-          cmin = __builtin_amdgcn_mfma_f32_16x16x4f32(sx.y, fmaf(-z, sa_own[1], sb_own[1]), cmin, 0, 0, 0);
-        }
-        // ZP: -z of windows 2k and 2k + 1 of this output as bytes 0 and 1 of zg[k]
-        [[maybe_unused]] uint32_t zg[4];
-        if constexpr (window_centered<QT>() && ZP) {
-          // zero points of windows 2g, 2g + 1 (window_zero_point) and the
-          // offsets left, b - z a (exactly rounded); -z of both as bytes 0
-          // and 1 of one word, gathered from the other lane groups
-          const float z0 = window_zero_point(sa_own[0], sb_own[0]);
-          const float z1 = window_zero_point(sa_own[1], sb_own[1]);
-          sb_own[0] = fmaf(-z0, sa_own[0], sb_own[0]);
-          sb_own[1] = fmaf(-z1, sa_own[1], sb_own[1]);
-          const uint32_t nz = (static_cast<uint32_t>(-static_cast<int>(z0)) & 0xFFu) |
-                              ((static_cast<uint32_t>(-static_cast<int>(z1)) & 0xFFu) << 8);
-          float t[4];
-          gather4(__builtin_bit_cast(float, nz), t);
+            for (int gp = 0; gp < 4; ++gp) sa[2 * gp + 1] = t[gp];
+          }
+          typename Dense<QT>::T ct;
+          Dense<QT>::template prepare<kFixed>(ring[i], g, ct);
+          if constexpr (window_centered<QT>() && !ZP) {
+            // the offsets left by the centred codes, b - z a (exactly rounded),
+            // of windows 2k + h (k = lane group) of this unit for the tile's
+            // outputs, times the rows' window sums
+            constexpr float z = static_cast<float>(code_centre<QT>());
+            const float2 sx = mrow < 4 * MG
+                                  ? *reinterpret_cast<const float2*>(xsum + mrow * cw + u * 8 + 2 * g)
+                                  : make_float2(0.0f, 0.0f);
+            cmin = __builtin_amdgcn_mfma_f32_16x16x4f32(sx.x, fmaf(-z, sa_own[0], sb_own[0]), cmin, 0, 0, 0);
+            cmin = __builtin_amdgcn_mfma_f32_16x16x4f32(sx.y, fmaf(-z, sa_own[1], sb_own[1]), cmin, 0, 0, 0);
+          }
+          // ZP: -z of windows 2k and 2k + 1 of this output as bytes 0 and 1 of zg[k]
+          [[maybe_unused]] uint32_t zg[4];
+          if constexpr (window_centered<QT>() && ZP) {
+            // zero points of windows 2g, 2g + 1 (window_zero_point) and the
+            // offsets left, b - z a (exactly rounded); -z of both as bytes 0
+            // and 1 of one word, gathered from the other lane groups
+            const float z0 = window_zero_point(sa_own[0], sb_own[0]);
+            const float z1 = window_zero_point(sa_own[1], sb_own[1]);
+            sb_own[0] = fmaf(-z0, sa_own[0], sb_own[0]);
+            sb_own[1] = fmaf(-z1, sa_own[1], sb_own[1]);
+            const uint32_t nz = (static_cast<uint32_t>(-static_cast<int>(z0)) & 0xFFu) |
+                                ((static_cast<uint32_t>(-static_cast<int>(z1)) & 0xFFu) << 8);
+            float t[4];
+            gather4(__builtin_bit_cast(float, nz), t);
 #pragma unroll
-          for (int gp = 0; gp < 4; ++gp) zg[gp] = __builtin_bit_cast(uint32_t, t[gp]);
-          // offsets of windows 2k + h (k = lane group) of this unit for the
-          // tile's outputs, times the rows' window sums
-          const float2 sx = mrow < 4 * MG
-                                ? *reinterpret_cast<const float2*>(xsum + mrow * cw + u * 8 + 2 * g)
-                                : make_float2(0.0f, 0.0f);
-          cmin = __builtin_amdgcn_mfma_f32_16x16x4f32(sx.x, sb_own[0], cmin, 0, 0, 0);
-          cmin = __builtin_amdgcn_mfma_f32_16x16x4f32(sx.y, sb_own[1], cmin, 0, 0, 0);
-        }
-        // this unit's digit blocks and activation scales per row group; the
-        // windows are then constant offsets from them
-        const uint8_t* dq[MG];
-        const float* xq[MG];
-#pragma unroll
-        for (int q = 0; q < MG; ++q) {
-          dq[q] = dig + (q * cw + u * 8) * kBlock + lane * 8;
-          xq[q] = xsc + (4 * q + g) * cw + u * 8;
-        }
-#pragma unroll
-        for (int w = 0; w < 8; ++w) {
-          long bw;
-          if constexpr (window_centered<QT>() && !ZP) bw = Dense<QT>::bc(ct, w);
-          else bw = Dense<QT>::b(ct, w);
+            for (int gp = 0; gp < 4; ++gp) zg[gp] = __builtin_bit_cast(uint32_t, t[gp]);
+            // offsets of windows 2k + h (k = lane group) of this unit for the
+            // tile's outputs, times the rows' window sums
+            const float2 sx = mrow < 4 * MG
+                                  ? *reinterpret_cast<const float2*>(xsum + mrow * cw + u * 8 + 2 * g)
+                                  : make_float2(0.0f, 0.0f);
+            cmin = __builtin_amdgcn_mfma_f32_16x16x4f32(sx.x, sb_own[0], cmin, 0, 0, 0);
+            cmin = __builtin_amdgcn_mfma_f32_16x16x4f32(sx.y, sb_own[1], cmin, 0, 0, 0);
+          }
+          // this unit's digit blocks and activation scales per row group; the
+          // windows are then constant offsets from them
+          const uint8_t* dq[MG];
+          const float* xq[MG];
 #pragma unroll
           for (int q = 0; q < MG; ++q) {
-            const long av = *reinterpret_cast<const long*>(dq[q] + w * kBlock);
-            const float xw = xq[q][w];
-            v4i c = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, bw, v4i{0, 0, 0, 0}, 0, 0, 0);
-            if constexpr (window_centered<QT>() && ZP) {
-              // byte (w & 1) of zg[w / 2] everywhere
-              const uint32_t zb = __builtin_amdgcn_perm(0u, zg[w >> 1], (w & 1) ? 0x01010101u : 0u);
-              c = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, pack2(zb, zb), c, 0, 0, 0);
-            }
-            // pairs exactly in int32 (|C0| < 2^20, |C1 * 256| < 2^28), halves in f32
-            const float comb = fmaf(static_cast<float>(c[2] + c[3] * 256), 65536.0f,
-                                    static_cast<float>(c[0] + c[1] * 256));
-            acc[q] = fmaf(sa[w] * xw, comb, acc[q]);
+            dq[q] = dig + (q * cw + u * 8) * kBlock + lane * 8;
+            xq[q] = xsc + (4 * q + g) * cw + u * 8;
           }
-          // one window at a time: the scheduler would otherwise hoist every
-          // window's operand reads and keep their results live
-          __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+          for (int w = 0; w < 8; ++w) {
+            long bw;
+            if constexpr (window_centered<QT>() && !ZP) bw = Dense<QT>::bc(ct, w);
+            else bw = Dense<QT>::b(ct, w);
+#pragma unroll
+            for (int q = 0; q < MG; ++q) {
+              const long av = *reinterpret_cast<const long*>(dq[q] + w * kBlock);
+              const float xw = xq[q][w];
+              v4i c = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, bw, v4i{0, 0, 0, 0}, 0, 0, 0);
+              if constexpr (window_centered<QT>() && ZP) {
+                // byte (w & 1) of zg[w / 2] everywhere
+                const uint32_t zb = __builtin_amdgcn_perm(0u, zg[w >> 1], (w & 1) ? 0x01010101u : 0u);
+                c = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, pack2(zb, zb), c, 0, 0, 0);
+              }
+              // pairs exactly in int32 (|C0| < 2^20, |C1 * 256| < 2^28), halves in f32
+              const float comb = fmaf(static_cast<float>(c[2] + c[3] * 256), 65536.0f,
+                                      static_cast<float>(c[0] + c[1] * 256));
+              acc[q] = fmaf(sa[w] * xw, comb, acc[q]);
+            }
+            // one window at a time: the scheduler would otherwise hoist every
+            // window's operand reads and keep their results live
+            __builtin_amdgcn_sched_barrier(0);
+          }
         }
       }
     };
@@ -746,8 +880,9 @@ hipError_t launch_rows_w(const RowsArgs& a, uint32_t ksplit, hipStream_t st) {
 }  // namespace
 
 bool gemv_rows_supported(int32_t qtype, int32_t layout, uint64_t k) {
-  return layout == kOutputRows && (qtype == kQ8_0 || qtype == kQ4_0 || qtype == kQ4_K || qtype == kQ5_K) &&
-         k % 256 == 0 && k > 0;
+  return layout == kOutputRows &&
+         (qtype == kQ8_0 || qtype == kQ4_0 || qtype == kQ4_K || qtype == kQ5_K || qtype == kQ6_K) && k % 256 == 0 &&
+         k > 0;
 }
 
 uint32_t gemv_rows_splits(uint64_t k, uint64_t n, uint32_t m) {
@@ -802,6 +937,7 @@ hipError_t launch_gemv_rows(int32_t qtype, bool wide, const View& w, const float
     case kQ4_0: return wide ? launch_rows_w<kQ4_0, true>(a, ksplit, st) : launch_rows_w<kQ4_0, false>(a, ksplit, st);
     case kQ4_K: return wide ? launch_rows_w<kQ4_K, true>(a, ksplit, st) : launch_rows_w<kQ4_K, false>(a, ksplit, st);
     case kQ5_K: return wide ? launch_rows_w<kQ5_K, true>(a, ksplit, st) : launch_rows_w<kQ5_K, false>(a, ksplit, st);
+    case kQ6_K: return wide ? launch_rows_w<kQ6_K, true>(a, ksplit, st) : launch_rows_w<kQ6_K, false>(a, ksplit, st);
     default: return hipErrorInvalidValue;
   }
 }
