@@ -220,8 +220,9 @@ qi_hip_status plan_linear(const Image& im, uint64_t m, int32_t mode, LinearPlan*
   }
   if (mode != QI_HIP_MODE_EXACT && qi::gemv_mfma_supported(im.qtype, im.layout, im.k)) {
     p->kind = LinearPlan::kMfma;
-    if (m >= 2 && qi::gemv_rows_supported(im.qtype, im.layout, im.k)) {
-      // two or more rows, dense operands: one kernel per 16-row chunk; K parts
+    if (m >= 2) {
+      // two or more rows, dense operands (launch_gemv_rows, the same formats
+      // and shapes as the one-row kernel): one kernel per 16-row chunk; K parts
       // only for shapes with few tiles, by the chunk's row count (a shorter
       // last chunk may take a different count; enqueue_linear asks again)
       uint64_t floats = 0, records = 0;
@@ -234,26 +235,6 @@ qi_hip_status plan_linear(const Image& im, uint64_t m, int32_t mode, LinearPlan*
       p->splits = 1;
       p->s_floats = floats;
       p->d_floats = (records + 3) / 4;
-      return QI_HIP_OK;
-    }
-    // two or more rows (Q6_K): activation records built once per 16-row chunk,
-    // and K parts over the grid whose partial sums are added in order
-    if (m >= 2) {
-      const uint32_t rows = static_cast<uint32_t>(m < 16 ? m : 16);
-      p->d_floats = (qi::gemv_digits_bytes(im.k, rows) + 3) / 4;
-      // partial sums [parts][rows][n] of each 16-row chunk and of a shorter
-      // last chunk, which may take more parts
-      auto mt_of = [](uint64_t r) { return r == 1 ? 1 : r == 2 ? 2 : r <= 4 ? 4 : r <= 8 ? 8 : 16; };
-      uint64_t floats = 0;
-      uint32_t parts = 1;
-      for (uint64_t r : {static_cast<uint64_t>(rows), m > 16 ? m % 16 : 0}) {
-        if (r < 2) continue;
-        const uint32_t pr = qi::gemv_pre_splits(im.qtype, im.wide != 0, im.k, im.n, mt_of(r));
-        parts = std::max(parts, pr);
-        if (pr > 1) floats = std::max(floats, static_cast<uint64_t>(pr) * r * im.n);
-      }
-      p->splits = parts;
-      p->s_floats = floats;
     }
     return QI_HIP_OK;
   }
@@ -301,8 +282,7 @@ qi_hip_status enqueue_linear(const qi_hip_weights* w, const LinearPlan& p, const
     case LinearPlan::kPlanar:
       for (uint64_t m0 = 0; m0 < m; m0 += 16) {
         const int rows = static_cast<int>(m - m0 < 16 ? m - m0 : 16);
-        const int mt = rows == 1 ? 1 : rows == 2 ? 2 : rows <= 4 ? 4 : rows <= 8 ? 8 : 16;
-        if (p.kind == LinearPlan::kMfma && rows >= 2 && qi::gemv_rows_supported(im.qtype, im.layout, im.k)) {
+        if (p.kind == LinearPlan::kMfma && rows >= 2) {
           const float* xc = x + m0 * im.k;
           float* const yc = y + m0 * im.n;
           const uint32_t parts = qi::gemv_rows_splits(im.k, im.n, static_cast<uint32_t>(rows));
@@ -320,23 +300,12 @@ qi_hip_status enqueue_linear(const qi_hip_weights* w, const LinearPlan& p, const
                        "launch gemv split-K sum");
           }
         } else if (p.kind == LinearPlan::kMfma) {
-          qi::GemvMfmaArgs ga{v, x + m0 * im.k, y + m0 * im.n, rows};
-          if (rows >= 2) {
-            QI_HIP_TRY(qi::launch_gemv_digits(im.qtype, ga.x, im.k, static_cast<uint32_t>(rows),
-                                              reinterpret_cast<uint8_t*>(dws), st),
-                       "launch gemv activation records");
-            ga.digits = reinterpret_cast<const uint8_t*>(dws);
-            ga.ksplit = qi::gemv_pre_splits(im.qtype, im.wide != 0, im.k, im.n, mt);
-            ga.part = sws;
-          }
+          // one row
+          const qi::GemvMfmaArgs ga{v, x + m0 * im.k, y + m0 * im.n, rows};
           const int split = w->ctx->gemv_split > 0 ? w->ctx->gemv_split : qi::gemv_mfma_split(im.k, im.n);
-          QI_HIP_TRY(qi::launch_gemv_mfma(im.qtype, im.wide != 0, mt, split, ga, st), "launch gemv");
-          if (ga.ksplit > 1) {
-            const uint64_t count = static_cast<uint64_t>(rows) * im.n;
-            QI_HIP_TRY(qi::launch_splitk_sum(im, v, sws, ga.ksplit, count, count, ga.y, ga.x, st),
-                       "launch gemv split-K sum");
-          }
+          QI_HIP_TRY(qi::launch_gemv_mfma(im.qtype, im.wide != 0, split, ga, st), "launch gemv");
         } else {
+          const int mt = rows == 1 ? 1 : rows == 2 ? 2 : rows <= 4 ? 4 : rows <= 8 ? 8 : 16;
           qi::GemvArgs ga{v, x + m0 * im.k, y + m0 * im.n, rows};
           QI_HIP_TRY(qi::launch_gemv(im.qtype, im.wide != 0, mt, ga, st), "launch gemv");
         }

@@ -1,5 +1,5 @@
 // Decode GEMV on the int8 matrix cores (v_mfma_i32_16x16x64_i8), output-rows
-// layout, M <= 16 activation rows, K a multiple of 256.
+// layout, one activation row, K a multiple of 256.
 //
 // Arithmetic. The activations are cut into windows of 32 consecutive
 // elements. Each activation x of a window becomes a 30-bit fixed-point
@@ -39,12 +39,9 @@
 // from the neighbouring lane: a single barrier).
 // Each wavefront issues its activation loads, then the loads of up to D
 // units, before it waits for anything (vector loads complete in order, so
-// waiting for the activations never waits for the weights). Two or more
-// rows: a small kernel builds the activation records once per call, the
-// workgroups copy their K part's records into LDS, and the K parts' partial
-// sums are added in order by a separate kernel.
+// waiting for the activations never waits for the weights). Two to sixteen
+// rows run in the dense-operand kernel of qi_gemv_rows.hip.
 // No state is shared between workgroups, so there are no device-scope fences.
-#include <atomic>
 #include <type_traits>
 
 #include "qi_device.h"
@@ -59,8 +56,7 @@ constexpr uint32_t kZeroBytes = 1024;  // zero A operand for the lanes of other 
 // Activation record of one (row, unit): 256 activations x 4 digits (1024 B,
 // [step pair p][lane group g][digit d] x 16 B: digit d of the pair's 16
 // activations, steps 2p and 2p + 1), then 8 windows x float4 {2^-s, window
-// sum, 0, 0} (128 B, [g][h]). Built in LDS by the workgroup, or once per call
-// in global memory by gemv_digits_kernel and copied into LDS.
+// sum, 0, 0} (128 B, [g][h]), built in LDS by the workgroup.
 constexpr uint32_t kUnitDigitBytes = 1024;
 constexpr uint32_t kUnitAuxBytes = 128;
 constexpr uint32_t kUnitRecBytes = kUnitDigitBytes + kUnitAuxBytes;
@@ -192,15 +188,12 @@ __device__ __forceinline__ void store_half(const HalfX& o, const Item& it, bool 
 // WC tiles of 16 outputs per workgroup, SW wavefronts per tile splitting its
 // K range, D units in flight per wavefront, XP half windows of activations
 // preloaded per thread (the WC tiles share one activation prep).
-// PRE: the activation records were built by gemv_digits_kernel (a.digits);
-// the workgroup copies its chunk into LDS with global-to-LDS loads instead of
-// building it.
-// XS (one row only): the activation source, see XSource. kXNorm keeps each
+// XS: the activation source, see XSource. kXNorm keeps each
 // thread's share of sum(v^2) in a register; the wavefront sums reach LDS only
-// in the final reduction, so the norm adds no barrier. One row: a.radd adds
-// the residual to the outputs, a.silu_pairs combines gate/up output pairs.
-template <int QT, bool WIDE, int MT, int SW, int D, int WC, bool PRE, int XS = kXPlain>
-__global__ __launch_bounds__(64 * SW * WC, (QT == kQ4_K && MT == 1 && SW == 4) ? 4 : 1)
+// in the final reduction, so the norm adds no barrier. a.radd adds the
+// residual to the outputs, a.silu_pairs combines gate/up output pairs.
+template <int QT, bool WIDE, int SW, int D, int WC, int XS = kXPlain>
+__global__ __launch_bounds__(64 * SW * WC, (QT == kQ4_K && SW == 4) ? 4 : 1)
 void gemv_mfma_kernel(GemvMfmaArgs a) {
   using U = Unit<QT>;
   constexpr int kThreads = 64 * SW * WC;
@@ -227,7 +220,6 @@ void gemv_mfma_kernel(GemvMfmaArgs a) {
   const uint32_t units_total = a.w.units;
   const uint8_t* trec = a.w.qs + static_cast<uint64_t>(tile) * units_total * R.bytes;
   const uint32_t K = static_cast<uint32_t>(a.w.k);
-  const int M = a.m;
 
   // A-operand lane role: row (sigma, digit) is live for lane group g == sigma
   const uint32_t arow = lane & 15, sigma = arow >> 2, digit = arow & 3;
@@ -235,103 +227,76 @@ void gemv_mfma_kernel(GemvMfmaArgs a) {
 
   for (uint32_t i = tid; i < kZeroBytes / 4; i += kThreads) reinterpret_cast<uint32_t*>(lds)[i] = 0;
 
-  float acc[MT];
-#pragma unroll
-  for (int m = 0; m < MT; ++m) acc[m] = 0.0f;
+  float acc = 0.0f;
   [[maybe_unused]] float ssq = 0.0f;  // kXNorm: this thread's part of sum(v^2)
 
   typename U::Raw ring[D];
 
-  // K split over the grid's y dimension (two or more rows): this workgroup's
-  // units [u_lo, u_hi); its partial sums go to a.part[blockIdx.y]
-  const uint32_t u_lo = a.ksplit > 1 ? blockIdx.y * a.split_units : 0;
-  const uint32_t u_hi = a.ksplit > 1 ? min(units_total, u_lo + a.split_units) : units_total;
-  for (uint32_t ku0 = u_lo; ku0 < u_hi; ku0 += cu) {
-    const uint32_t units = min(cu, u_hi - ku0);
+  for (uint32_t ku0 = 0; ku0 < units_total; ku0 += cu) {
+    const uint32_t units = min(cu, units_total - ku0);
     const uint32_t k0 = ku0 * 256;
-    const uint32_t halves = static_cast<uint32_t>(M) * units * 16;
+    const uint32_t halves = units * 16;
     // this wavefront's contiguous run of the chunk's units (balanced split)
     const uint32_t u_begin = (units * sw) / SW;
     const uint32_t u_count = (units * (sw + 1)) / SW - u_begin;
     const uint32_t u_last = ku0 + (u_count ? u_begin + u_count - 1 : 0);
 
-    if constexpr (PRE) {
-      // copy the chunk's records: row m's units [ku0, ku0 + units) are
-      // contiguous in both places; one global-to-LDS load per wavefront
-      // moves 1 KB (lanes past the end of a row's run stay idle)
-      const uint32_t bytes = units * kUnitRecBytes, pieces = (bytes + 1023) / 1024;
-      for (uint32_t pi = wave; pi < static_cast<uint32_t>(M) * pieces; pi += kThreads / 64) {
-        const uint32_t m = pi / pieces, p = pi % pieces, off = p * 1024 + lane * 16;
-        if (off < bytes)
-          __builtin_amdgcn_global_load_lds(
-              a.digits + (static_cast<uint64_t>(m) * units_total + ku0) * kUnitRecBytes + off,
-              (__attribute__((address_space(3))) void*)(recs + (m * cu) * kUnitRecBytes + p * 1024), 16, 0,
-              0);
+    // activations first (so that waiting for them never waits for the
+    // weights), then this wavefront's first D units, unconditionally (slots
+    // past the run re-read its last unit)
+    HalfX xp[XP];
+    Item ip[XP];
+    [[maybe_unused]] HalfX up[XP];  // kXNorm: the norm weights
+#pragma unroll
+    for (int i = 0; i < XP; ++i) {
+      const uint32_t hi = tid + kThreads * i;
+      ip[i] = item_of(hi < halves ? hi : 0, units);
+      if constexpr (XS == kXNorm) {
+        load_half<QT>(a.hres, K, k0, ip[i], xp[i]);
+        load_half<QT>(a.nw, K, k0, ip[i], up[i]);
+      } else {
+        load_half<QT>(a.x, K, k0, ip[i], xp[i]);
       }
+    }
+    // fused sources: keep every activation load ahead of the weight loads
+    // (the scheduler hoisted weight scale loads above them, so the in-order
+    // wait for the activations waited for HBM); the plain source already
+    // keeps that order, and the barrier measured slower there
+    if constexpr (XS != kXPlain) __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int i = 0; i < D; ++i)
-        U::template load<WIDE, true>(trec + min(ku0 + u_begin + i, u_last) * R.bytes, lane, ring[i]);
-      (void)halves;
-      (void)K;
-      (void)k0;
-    } else {
-      // activations first (so that waiting for them never waits for the
-      // weights), then this wavefront's first D units, unconditionally (slots
-      // past the run re-read its last unit)
-      HalfX xp[XP];
-      Item ip[XP];
-      [[maybe_unused]] HalfX up[XP];  // kXNorm: the norm weights
-#pragma unroll
-      for (int i = 0; i < XP; ++i) {
-        const uint32_t hi = tid + kThreads * i;
-        ip[i] = item_of(hi < halves ? hi : 0, units);
-        if constexpr (XS == kXNorm) {
-          load_half<QT>(a.hres, K, k0, ip[i], xp[i]);
-          load_half<QT>(a.nw, K, k0, ip[i], up[i]);
-        } else {
-          load_half<QT>(a.x, K, k0, ip[i], xp[i]);
-        }
-      }
-      // fused sources: keep every activation load ahead of the weight loads
-      // (the scheduler hoisted weight scale loads above them, so the in-order
-      // wait for the activations waited for HBM); the plain source already
-      // keeps that order, and the barrier measured slower there
-      if constexpr (XS != kXPlain) __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int i = 0; i < D; ++i)
-        U::template load<WIDE, true>(trec + min(ku0 + u_begin + i, u_last) * R.bytes, lane, ring[i]);
+    for (int i = 0; i < D; ++i)
+      U::template load<WIDE, true>(trec + min(ku0 + u_begin + i, u_last) * R.bytes, lane, ring[i]);
 
-      // kXNorm: sum(v^2) over valid items, x = v * w
-      [[maybe_unused]] auto norm = [&](HalfX& vx, const HalfX& wx, bool valid) {
-        float s2 = 0.0f;
+    // kXNorm: sum(v^2) over valid items, x = v * w
+    [[maybe_unused]] auto norm = [&](HalfX& vx, const HalfX& wx, bool valid) {
+      float s2 = 0.0f;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const float4 v = vx.v[q];
-          s2 += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
-          vx.v[q] = make_float4(v.x * wx.v[q].x, v.y * wx.v[q].y, v.z * wx.v[q].z, v.w * wx.v[q].w);
-        }
-        if (valid) ssq += s2;
-      };
+      for (int q = 0; q < 4; ++q) {
+        const float4 v = vx.v[q];
+        s2 += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+        vx.v[q] = make_float4(v.x * wx.v[q].x, v.y * wx.v[q].y, v.z * wx.v[q].z, v.w * wx.v[q].w);
+      }
+      if (valid) ssq += s2;
+    };
 #pragma unroll
-      for (int i = 0; i < XP; ++i) {
-        const bool valid = tid + kThreads * i < halves;
-        if constexpr (XS == kXNorm) norm(xp[i], up[i], valid);
-        store_half(xp[i], ip[i], valid, recs, cu);
+    for (int i = 0; i < XP; ++i) {
+      const bool valid = tid + kThreads * i < halves;
+      if constexpr (XS == kXNorm) norm(xp[i], up[i], valid);
+      store_half(xp[i], ip[i], valid, recs, cu);
+    }
+    for (uint32_t h0 = XP * kThreads; h0 < halves; h0 += kThreads) {
+      const uint32_t hi = h0 + tid;
+      Item it = item_of(hi < halves ? hi : 0, units);
+      HalfX xh;
+      if constexpr (XS == kXNorm) {
+        HalfX wh;
+        load_half<QT>(a.hres, K, k0, it, xh);
+        load_half<QT>(a.nw, K, k0, it, wh);
+        norm(xh, wh, hi < halves);
+      } else {
+        load_half<QT>(a.x, K, k0, it, xh);
       }
-      for (uint32_t h0 = XP * kThreads; h0 < halves; h0 += kThreads) {
-        const uint32_t hi = h0 + tid;
-        Item it = item_of(hi < halves ? hi : 0, units);
-        HalfX xh;
-        if constexpr (XS == kXNorm) {
-          HalfX wh;
-          load_half<QT>(a.hres, K, k0, it, xh);
-          load_half<QT>(a.nw, K, k0, it, wh);
-          norm(xh, wh, hi < halves);
-        } else {
-          load_half<QT>(a.x, K, k0, it, xh);
-        }
-        store_half(xh, it, hi < halves, recs, cu);
-      }
+      store_half(xh, it, hi < halves, recs, cu);
     }
     __syncthreads();
     if (tid == 0) stamp(slot, 1);
@@ -354,90 +319,31 @@ void gemv_mfma_kernel(GemvMfmaArgs a) {
           for (int w = 0; w < U::kWindows; ++w)
             sb[w] = fmaf(-static_cast<float>(code_centre<QT>()), sa[w], sb[w]) * static_cast<float>(code_scale<QT>());
         }
-        if constexpr (MT >= 8) {
-          // Eight or more rows: a window's codes are decoded once, then the
-          // rows go one after another (two matrix instructions and the combine
-          // each), so only one row's operands and digit sums are live: fewer
-          // registers, more wavefronts per SIMD to hide the latencies (Q4_K
-          // 4096x14336 M=16 61.5 -> 44.2 us, Q6_K M=8 41.5 -> 34.9 on MI355X;
-          // at 4 rows the interleaved form below measured faster). Rows past M
-          // compute on stale records and are never stored.
-          const uint8_t* const a0 = a_live ? recs + u * kUnitRecBytes + g * 64 + digit * 16 : lds;
-          const uint32_t astride = a_live ? cu * kUnitRecBytes : 0;
-          const float4* const x0 = reinterpret_cast<const float4*>(recs + u * kUnitRecBytes + kUnitDigitBytes) + g * 2;
-          const uint32_t xstride = cu * kUnitRecBytes / 16;
-#pragma unroll
-          for (int w = 0; w < U::kWindows; ++w) {
-            constexpr int kPairs = U::kSteps / 2;
-            v4i cb[kPairs];
-#pragma unroll
-            for (int sp = 0; sp < kPairs; ++sp) {
-              const int t = w * U::kSteps + 2 * sp;
-              const long c0 = gemv_codes<QT>(ring[i], g, t), c1 = gemv_codes<QT>(ring[i], g, t + 1);
-              cb[sp] = v4i{static_cast<int>(c0), static_cast<int>(c0 >> 32), static_cast<int>(c1),
-                           static_cast<int>(c1 >> 32)};
-            }
-            const int h = U::kSteps == 4 ? w : (w >> 1);
-#pragma unroll
-            for (int m = 0; m < MT; ++m) {
-              v4i c = {0, 0, 0, 0};
-#pragma unroll
-              for (int sp = 0; sp < kPairs; ++sp) {
-                const int t = w * U::kSteps + 2 * sp;
-                const v4i av = *reinterpret_cast<const v4i*>(a0 + m * astride + (t >> 1) * 256);
-                c = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, cb[sp], c, 0, 0, 0);
-              }
-              const float comb = fmaf(static_cast<float>(c[2] + c[3] * 256), 65536.0f,
-                                      static_cast<float>(c[0] + c[1] * 256));
-              const float4 wx = x0[m * xstride + h];
-              acc[m] = fmaf(sa[w] * wx.x, comb, acc[m]);
-              if constexpr (window_centered<QT>()) acc[m] = fmaf(-sb[w], wx.y, acc[m]);
-            }
-          }
-          continue;
-        }
-        // Rows are independent: per step, all rows' activation words are read
-        // together and their MFMAs issued together (one LDS latency per step,
-        // not one per row). Rows past M compute on stale records and are never
-        // stored.
-        const uint8_t* abase[MT];
-        const float4* ax[MT];
-#pragma unroll
-        for (int m = 0; m < MT; ++m) {
-          const uint8_t* rec = recs + (m * cu + u) * kUnitRecBytes;
-          abase[m] = a_live ? rec + g * 64 + digit * 16 : lds;
-          ax[m] = reinterpret_cast<const float4*>(rec + kUnitDigitBytes) + g * 2;
-        }
+        const uint8_t* const rec = recs + u * kUnitRecBytes;
+        const uint8_t* const abase = a_live ? rec + g * 64 + digit * 16 : lds;
+        const float4* const ax = reinterpret_cast<const float4*>(rec + kUnitDigitBytes) + g * 2;
 #pragma unroll
         for (int w = 0; w < U::kWindows; ++w) {
-          v4i c[MT];
-#pragma unroll
-          for (int m = 0; m < MT; ++m) c[m] = v4i{0, 0, 0, 0};
+          v4i c = {0, 0, 0, 0};
 #pragma unroll
           for (int s = 0; s < U::kSteps; s += 2) {
             // one 16x16x64 instruction per step pair: 16 activations (digit
             // bytes) and 16 codes per lane
             const int t = w * U::kSteps + s;
-            v4i av[MT];
-#pragma unroll
-            for (int m = 0; m < MT; ++m) av[m] = *reinterpret_cast<const v4i*>(abase[m] + (t >> 1) * 256);
+            const v4i av = *reinterpret_cast<const v4i*>(abase + (t >> 1) * 256);
             const long c0 = gemv_codes<QT>(ring[i], g, t), c1 = gemv_codes<QT>(ring[i], g, t + 1);
             const v4i cb = {static_cast<int>(c0), static_cast<int>(c0 >> 32), static_cast<int>(c1),
                             static_cast<int>(c1 >> 32)};
-#pragma unroll
-            for (int m = 0; m < MT; ++m) c[m] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[m], cb, c[m], 0, 0, 0);
+            c = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, cb, c, 0, 0, 0);
           }
           const int h = U::kSteps == 4 ? w : (w >> 1);
-#pragma unroll
-          for (int m = 0; m < MT; ++m) {
-            // combine the digit sums: pairs exactly in int32 (|C0| < 2^20,
-            // |C1 * 256| < 2^28), the two halves in f32
-            const float comb = fmaf(static_cast<float>(c[m][2] + c[m][3] * 256), 65536.0f,
-                                    static_cast<float>(c[m][0] + c[m][1] * 256));
-            const float4 wx = ax[m][h];
-            acc[m] = fmaf(sa[w] * wx.x, comb, acc[m]);
-            if constexpr (window_centered<QT>()) acc[m] = fmaf(-sb[w], wx.y, acc[m]);
-          }
+          // combine the digit sums: pairs exactly in int32 (|C0| < 2^20,
+          // |C1 * 256| < 2^28), the two halves in f32
+          const float comb = fmaf(static_cast<float>(c[2] + c[3] * 256), 65536.0f,
+                                  static_cast<float>(c[0] + c[1] * 256));
+          const float4 wx = ax[h];
+          acc = fmaf(sa[w] * wx.x, comb, acc);
+          if constexpr (window_centered<QT>()) acc = fmaf(-sb[w], wx.y, acc);
         }
       }
     };
@@ -454,128 +360,71 @@ void gemv_mfma_kernel(GemvMfmaArgs a) {
 
   if (tid == 0) stamp(slot, 3);
   // ---- reduce: 4 lane groups of a column, then the SW K-parts ----
-#pragma unroll
-  for (int m = 0; m < MT; ++m) {
-    float v = acc[m] * (1.0f / code_scale<QT>());  // centred codes' scale (exact)
-    v += __shfl_xor(v, 16);
-    v += __shfl_xor(v, 32);
-    acc[m] = v;
-  }
-  float* red = reinterpret_cast<float*>(recs);  // [WC][SW][MT][16], then kXNorm: [waves]
-  if (g == 0) {
-#pragma unroll
-    for (int m = 0; m < MT; ++m) red[((wc * SW + sw) * MT + m) * 16 + col] = acc[m];
-  }
+  acc *= 1.0f / code_scale<QT>();  // centred codes' scale (exact)
+  acc += __shfl_xor(acc, 16);
+  acc += __shfl_xor(acc, 32);
+  float* red = reinterpret_cast<float*>(recs);  // [WC][SW][16], then kXNorm: [waves]
+  if (g == 0) red[(wc * SW + sw) * 16 + col] = acc;
   if constexpr (XS == kXNorm) {
     float s2 = ssq;
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) s2 += __shfl_xor(s2, o);
-    if (lane == 0) red[WC * SW * MT * 16 + wave] = s2;
+    if (lane == 0) red[WC * SW * 16 + wave] = s2;
   }
   __syncthreads();
   [[maybe_unused]] float inv = 1.0f;
   if constexpr (XS == kXNorm) {
     float total = 0.0f;
-    for (int w = 0; w < SW * WC; ++w) total += red[WC * SW * MT * 16 + w];
+    for (int w = 0; w < SW * WC; ++w) total += red[WC * SW * 16 + w];
     inv = 1.0f / sqrtf(total / static_cast<float>(K) + a.eps);
   }
-  if constexpr (MT == 1) {
-    if (a.silu_pairs) {
-      // lanes 0-7 of the tile hold gate rows, lanes 8-15 the matching up rows
-      if (sw == 0 && g == 0) {
-        float v = red[(wc * SW) * 16 + col];
+  if (a.silu_pairs) {
+    // lanes 0-7 of the tile hold gate rows, lanes 8-15 the matching up rows
+    if (sw == 0 && g == 0) {
+      float v = red[(wc * SW) * 16 + col];
 #pragma unroll
-        for (int p = 1; p < SW; ++p) v += red[(wc * SW + p) * 16 + col];
-        if constexpr (XS == kXNorm) v *= inv;
-        const float u = __shfl(v, static_cast<int>(lane) + 8, 16);
-        if (col < 8 && tile_raw < a.w.tiles) a.y[static_cast<uint64_t>(tile_raw) * 8 + col] = v / (1.0f + expf(-v)) * u;
-      }
-      return;
+      for (int p = 1; p < SW; ++p) v += red[(wc * SW + p) * 16 + col];
+      if constexpr (XS == kXNorm) v *= inv;
+      const float u = __shfl(v, static_cast<int>(lane) + 8, 16);
+      if (col < 8 && tile_raw < a.w.tiles) a.y[static_cast<uint64_t>(tile_raw) * 8 + col] = v / (1.0f + expf(-v)) * u;
     }
+    return;
   }
   if (tid == 0) stamp(slot, 4);
   if (sw == 0 && g == 0 && n_out < a.w.n) {
-    [[maybe_unused]] uint32_t bad = 0;  // rows whose result is not finite
-    [[maybe_unused]] float rv = 0.0f;
-    // a K part's partial sums (checked for non-finite values when summed)
-    float* const yout = a.ksplit > 1 ? a.part + static_cast<uint64_t>(blockIdx.y) * M * a.w.n : a.y;
+    float v = red[(wc * SW) * 16 + col];
 #pragma unroll
-    for (int m = 0; m < MT; ++m) {
-      if (m >= M) break;
-      float v = red[(wc * SW * MT + m) * 16 + col];
-#pragma unroll
-      for (int p = 1; p < SW; ++p) v += red[((wc * SW + p) * MT + m) * 16 + col];
-      if constexpr (XS == kXNorm) v *= inv;
-      if constexpr (MT == 1) {
-        if (a.radd != nullptr) {
-          rv = a.radd[n_out];
-          v = rv + v;
-        }
-      }
-      if constexpr (XS == kXPlain) bad |= static_cast<uint32_t>(!__builtin_isfinite(v)) << m;
-      yout[static_cast<uint64_t>(m) * a.w.n + n_out] = v;
-    }
+    for (int p = 1; p < SW; ++p) v += red[(wc * SW + p) * 16 + col];
+    if constexpr (XS == kXNorm) v *= inv;
+    const float rv = a.radd != nullptr ? a.radd[n_out] : 0.0f;
+    if (a.radd != nullptr) v = rv + v;
+    // NaN or infinite activations (or an overflow): the reference's own order
+    // decides which outputs are NaN and which +-Inf
     if constexpr (XS == kXPlain) {
-      // NaN or infinite activations (or an overflow): the reference's own
-      // order decides which outputs are NaN and which +-Inf
-      if (bad && a.ksplit == 1) {
-#pragma unroll 1
-        for (int m = 0; m < M; ++m) {
-          if (!((bad >> m) & 1u)) continue;
-          float v = exact_output_row<QT, WIDE>(a.w, a.x + static_cast<uint64_t>(m) * K, n_out);
-          if (MT == 1 && a.radd != nullptr) v = rv + v;
-          a.y[static_cast<uint64_t>(m) * a.w.n + n_out] = v;
-        }
+      if (!__builtin_isfinite(v)) {
+        v = exact_output_row<QT, WIDE>(a.w, a.x, n_out);
+        if (a.radd != nullptr) v = rv + v;
       }
     }
+    a.y[n_out] = v;
   }
 }
 
-// Activation records of all M rows and K units, once per call (gemv_mfma
-// kernels with PRE copy them instead of building them per workgroup).
-template <int QT>
-__global__ __launch_bounds__(256) void gemv_digits_kernel(const float* x, uint32_t K, uint32_t units,
-                                                          uint32_t m, uint8_t* out) {
-  const uint32_t hi = blockIdx.x * 256 + threadIdx.x;  // half windows, [m][unit][16]
-  const bool valid = hi < m * units * 16;
-  const Item it = item_of(valid ? hi : 0, units);
-  HalfX xh;
-  load_half<QT>(x, K, 0, it, xh);
-  store_half(xh, it, valid, out, units);
-}
-
-hipError_t launch_gemv_digits(int32_t qtype, const float* x, uint64_t k, uint32_t m, uint8_t* out,
-                              hipStream_t st) {
-  const uint32_t units = static_cast<uint32_t>(k / 256);
-  const uint32_t blocks = (m * units * 16 + 255) / 256;
-  if (qtype == kQ6_K)
-    hipLaunchKernelGGL(gemv_digits_kernel<kQ6_K>, dim3(blocks), dim3(256), 0, st, x, static_cast<uint32_t>(k),
-                       units, m, out);
-  else
-    hipLaunchKernelGGL(gemv_digits_kernel<kQ4_K>, dim3(blocks), dim3(256), 0, st, x, static_cast<uint32_t>(k),
-                       units, m, out);
-  return hipGetLastError();
-}
-
-uint64_t gemv_digits_bytes(uint64_t k, uint32_t m) { return (k / 256) * m * kUnitRecBytes; }
 
 namespace {
 
-uint32_t lds_bytes(int mt, uint32_t chunk_units, int waves) {
-  const uint32_t main = kZeroBytes + static_cast<uint32_t>(mt) * chunk_units * kUnitRecBytes;
-  const uint32_t red = kZeroBytes + static_cast<uint32_t>(waves * mt * 16 * 4 + waves * 4);
+uint32_t lds_bytes(uint32_t chunk_units, int waves) {
+  const uint32_t main = kZeroBytes + chunk_units * kUnitRecBytes;
+  const uint32_t red = kZeroBytes + static_cast<uint32_t>(waves * 16 * 4 + waves * 4);
   return main > red ? main : red;
 }
 
-template <int QT, bool WIDE, int MT, int SW, int D, int WC, int XS = kXPlain>
-hipError_t launch4(GemvMfmaArgs a, hipStream_t st, uint32_t chunk_target = 0) {
-  const uint32_t cap = chunk_target ? chunk_target : (kMaxLds - kZeroBytes) / (MT * kUnitRecBytes);
+template <int QT, bool WIDE, int SW, int D, int WC, int XS = kXPlain>
+hipError_t launch4(GemvMfmaArgs a, hipStream_t st) {
+  const uint32_t cap = (kMaxLds - kZeroBytes) / kUnitRecBytes;
   a.chunk_units = a.w.units < cap ? a.w.units : cap;
-  const uint32_t bytes = lds_bytes(MT, a.chunk_units, SW * WC);
-  // two or more activation rows read records built once per call
-  constexpr bool kPre = MT >= 2;
-  if (kPre && a.digits == nullptr) return hipErrorInvalidValue;
-  auto kern = gemv_mfma_kernel<QT, WIDE, MT, SW, D, WC, kPre, XS>;
+  const uint32_t bytes = lds_bytes(a.chunk_units, SW * WC);
+  auto kern = gemv_mfma_kernel<QT, WIDE, SW, D, WC, XS>;
   if (bytes > 65536) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(bytes));
@@ -584,204 +433,89 @@ hipError_t launch4(GemvMfmaArgs a, hipStream_t st, uint32_t chunk_target = 0) {
       return e;
     }
   }
-  if (a.ksplit > 1 && (!kPre || a.part == nullptr || a.split_units != a.chunk_units)) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(kern, dim3((a.w.tiles + WC - 1) / WC, a.ksplit), dim3(64 * SW * WC), bytes, st, a);
+  hipLaunchKernelGGL(kern, dim3((a.w.tiles + WC - 1) / WC), dim3(64 * SW * WC), bytes, st, a);
   return hipGetLastError();
-}
-
-// Two or more rows: units in flight per wavefront (the K part is streamed in
-// batches of that many).
-template <int MT>
-constexpr int pre_depth() { return MT >= 16 ? 2 : 4; }
-
-// Workgroups of the 2-16 row kernel that fit a CU at once with K parts of
-// `chunk` units (registers and LDS; the HIP occupancy calculator), cached.
-template <int QT, bool WIDE, int MT>
-uint32_t pre_groups_per_cu(uint32_t chunk) {
-  static std::atomic<int> cache[17];
-  if (chunk > 16) return 0;
-  int n = cache[chunk].load(std::memory_order_relaxed);
-  if (n > 0) return static_cast<uint32_t>(n);
-  const uint32_t bytes = lds_bytes(MT, chunk, 4);
-  if (bytes > kMaxLds) return 0;
-  auto kern = gemv_mfma_kernel<QT, WIDE, MT, 1, pre_depth<MT>(), 4, true, kXPlain>;
-  if (bytes > 65536 && hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize,
-                                           static_cast<int>(bytes)) != hipSuccess) {
-    (void)hipGetLastError();
-    return 0;
-  }
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, reinterpret_cast<const void*>(kern), 256, bytes) !=
-          hipSuccess || n < 1) {
-    (void)hipGetLastError();
-    return 0;
-  }
-  cache[chunk].store(n, std::memory_order_relaxed);
-  return static_cast<uint32_t>(n);
-}
-
-// Units per K part of a 2-16 row launch. Every workgroup copies its part's
-// activation records into LDS and then streams its part, so a launch costs
-// about (rounds of resident workgroups) x (part length + one unit of copy
-// latency per round); the part length in {2, 4, 8, 16} units that minimizes
-// it is taken, ties to the longer part (fewer rounds, fewer partials).
-// Measured on MI355X (records kernel and split-K sum included): Q4_K
-// 4096x14336 M=8 30.4 -> 29.0 us (8 units), M=16 69.7 -> 61.5 (8), 14336x4096
-// M=8 33.5 -> 30.6 (8), Q6_K 4096x14336 M=8 49.8 -> 41.4 (16), Q4_0
-// 4096x12288 M=16 60.1 -> 53.1 (4).
-template <int QT, bool WIDE, int MT>
-uint32_t pre_units(uint64_t units, uint64_t tiles) {
-  const uint64_t groups = (tiles + 3) / 4;
-  uint64_t best = 0, best_cost = ~0ull;
-  for (uint32_t us : {2u, 4u, 8u, 16u}) {
-    const uint64_t chunk = us < units ? us : units;
-    const uint32_t per_cu = pre_groups_per_cu<QT, WIDE, MT>(static_cast<uint32_t>(chunk));
-    if (per_cu == 0) continue;
-    const uint64_t parts = (units + chunk - 1) / chunk;
-    const uint64_t slots = per_cu * kCUs;
-    const uint64_t rounds = (groups * parts + slots - 1) / slots;
-    const uint64_t cost = rounds * (chunk + 1);
-    if (cost <= best_cost) {
-      best_cost = cost;
-      best = chunk;
-    }
-    if (chunk == units) break;
-  }
-  return static_cast<uint32_t>(best ? best : 1);
 }
 
 // (wavefronts per workgroup, units in flight per wavefront) for `sw` and the
 // units each wavefront holds
-template <int QT, bool WIDE, int MT, int XS = kXPlain>
+template <int QT, bool WIDE, int XS = kXPlain>
 hipError_t launch_split(const GemvMfmaArgs& a, int sw, hipStream_t st) {
-  const uint32_t cap = (kMaxLds - kZeroBytes) / (MT * kUnitRecBytes);
+  const uint32_t cap = (kMaxLds - kZeroBytes) / kUnitRecBytes;
   const uint32_t chunk = a.w.units < cap ? a.w.units : cap;
-  if constexpr (MT >= 2) {
-    // Two or more rows read activation records built once per call. Every
-    // tile needs all of them, so the records a workgroup copies into LDS are
-    // shared by four tiles (one wavefront each), and K is split over the
-    // grid's y dimension in parts of pre_units units: a workgroup copies its
-    // part's records once and each wavefront streams its tile's part; the
-    // parts' partial sums are added in order by the split-K sum (a.part,
-    // a.ksplit set by the caller: gemv_pre_splits).
-    (void)sw;
-    (void)chunk;
-    const uint32_t us = pre_units<QT, WIDE, MT>(a.w.units, a.w.tiles);
-    GemvMfmaArgs b = a;
-    b.split_units = us;
-    if (b.ksplit != (b.w.units + us - 1) / us) return hipErrorInvalidValue;
-    return launch4<QT, WIDE, MT, 1, pre_depth<MT>(), 4>(b, st, us);
-  } else {
-    if (sw == 4) {
-      // Two tiles share the activation prep (an 8-wavefront workgroup) where
-      // that does not raise the most tiles any CU streams, with workgroups
-      // spread evenly over the CUs: ceil(tiles / 256) one-tile workgroups
-      // against 2 ceil(tiles / 512) two-tile ones (896 tiles: 4 and 4, so
-      // the shared prep wins; 768: 3 against 4); above 1024 tiles the
-      // workgroups no longer all fit at once. With two workgroups on a CU
-      // the second one's activation loads queue behind the first one's
-      // weight loads, so the 4-bit K-quants then keep two units in flight per
-      // wavefront, not four (measured on MI355X at 896 tiles: Q4_K 7.9
-      // against 8.2 us, Q5_K 10.0 against 10.6, Q6_K 10.7 against 11.4; the
-      // 8-bit and Q4_0 codes do not gain).
-      const uint64_t t = a.w.tiles;
-      const uint64_t one = (t + kCUs - 1) / kCUs, two = 2 * ((t + 2 * kCUs - 1) / (2 * kCUs));
-      if (two <= one && t <= 4 * kCUs) {
-        if constexpr (QT == kQ4_K || QT == kQ5_K || QT == kQ6_K) {
-          if (t > 2 * kCUs) return launch4<QT, WIDE, MT, 4, 2, 2, XS>(a, st);
-        }
-        return launch4<QT, WIDE, MT, 4, 4, 2, XS>(a, st);
+  if (sw == 4) {
+    // Two tiles share the activation prep (an 8-wavefront workgroup) where
+    // that does not raise the most tiles any CU streams, with workgroups
+    // spread evenly over the CUs: ceil(tiles / 256) one-tile workgroups
+    // against 2 ceil(tiles / 512) two-tile ones (896 tiles: 4 and 4, so
+    // the shared prep wins; 768: 3 against 4); above 1024 tiles the
+    // workgroups no longer all fit at once. With two workgroups on a CU
+    // the second one's activation loads queue behind the first one's
+    // weight loads, so the 4-bit K-quants then keep two units in flight per
+    // wavefront, not four (measured on MI355X at 896 tiles: Q4_K 7.9
+    // against 8.2 us, Q5_K 10.0 against 10.6, Q6_K 10.7 against 11.4; the
+    // 8-bit and Q4_0 codes do not gain).
+    const uint64_t t = a.w.tiles;
+    const uint64_t one = (t + kCUs - 1) / kCUs, two = 2 * ((t + 2 * kCUs - 1) / (2 * kCUs));
+    if (two <= one && t <= 4 * kCUs) {
+      if constexpr (QT == kQ4_K || QT == kQ5_K || QT == kQ6_K) {
+        if (t > 2 * kCUs) return launch4<QT, WIDE, 4, 2, 2, XS>(a, st);
       }
-      if constexpr (QT == kQ4_K && MT == 1) {
-        // 1281-1536 tiles (the decoder's fused gate|up, N = 24576): four
-        // one-tile workgroups fit a CU at once, so the one-tile launch runs
-        // in two rounds and the second pays the activation round trip again.
-        // Six tiles per workgroup with two wavefronts each (8 units per
-        // wavefront, two in flight; 12 wavefronts, one workgroup per CU) run
-        // in one. Measured on MI355X: decode step of the Qwen3-8B-shape
-        // decoder 1.671 -> 1.626 ms; plain 4096 x 24576 11.6-11.9 -> 11.4 us.
-        if (t > 5 * kCUs && t <= 6 * kCUs) return launch4<QT, WIDE, MT, 2, 2, 6, XS>(a, st);
-      }
-      return launch4<QT, WIDE, MT, 4, 4, 1, XS>(a, st);
+      return launch4<QT, WIDE, 4, 4, 2, XS>(a, st);
     }
-    const uint32_t upw = (chunk + 7) / 8;
-    if (upw <= 2) return launch4<QT, WIDE, MT, 8, 2, 1, XS>(a, st);
-    if constexpr (MT == 1) {
-      // up to two tiles per CU: 16 wavefronts per tile with two units in
-      // flight each, reloaded per batch (K = 12288 on MI355X: N = 4096 8.5 us
-      // against 8.9 for 8 wavefronts x 2 units and 9.2-9.5 for 8 x 8; N = 6144
-      // 14.1 against 15.7); more tiles: 8 wavefronts with the whole run in
-      // flight (N = 14336: 21.9 against 24.1 us for 8 x 2)
-      if (a.w.tiles <= 2 * kCUs) return launch4<QT, WIDE, MT, 16, 2, 1, XS>(a, st);
-      // (Q5_K, and Q6_K with the norm prep, spill registers at 8 units deep)
-      constexpr bool deep = QT != kQ5_K && (XS != kXNorm || QT != kQ6_K);
-      if constexpr (deep) {
-        if (upw > 4) return launch4<QT, WIDE, MT, 8, 8, 1, XS>(a, st);
-      }
+    if constexpr (QT == kQ4_K) {
+      // 1281-1536 tiles (the decoder's fused gate|up, N = 24576): four
+      // one-tile workgroups fit a CU at once, so the one-tile launch runs
+      // in two rounds and the second pays the activation round trip again.
+      // Six tiles per workgroup with two wavefronts each (8 units per
+      // wavefront, two in flight; 12 wavefronts, one workgroup per CU) run
+      // in one. Measured on MI355X: decode step of the Qwen3-8B-shape
+      // decoder 1.671 -> 1.626 ms; plain 4096 x 24576 11.6-11.9 -> 11.4 us.
+      if (t > 5 * kCUs && t <= 6 * kCUs) return launch4<QT, WIDE, 2, 2, 6, XS>(a, st);
     }
-    return launch4<QT, WIDE, MT, 8, 4, 1, XS>(a, st);
+    return launch4<QT, WIDE, 4, 4, 1, XS>(a, st);
   }
+  const uint32_t upw = (chunk + 7) / 8;
+  if (upw <= 2) return launch4<QT, WIDE, 8, 2, 1, XS>(a, st);
+  // up to two tiles per CU: 16 wavefronts per tile with two units in
+  // flight each, reloaded per batch (K = 12288 on MI355X: N = 4096 8.5 us
+  // against 8.9 for 8 wavefronts x 2 units and 9.2-9.5 for 8 x 8; N = 6144
+  // 14.1 against 15.7); more tiles: 8 wavefronts with the whole run in
+  // flight (N = 14336: 21.9 against 24.1 us for 8 x 2)
+  if (a.w.tiles <= 2 * kCUs) return launch4<QT, WIDE, 16, 2, 1, XS>(a, st);
+  // (Q5_K, and Q6_K with the norm prep, spill registers at 8 units deep)
+  constexpr bool deep = QT != kQ5_K && (XS != kXNorm || QT != kQ6_K);
+  if constexpr (deep) {
+    if (upw > 4) return launch4<QT, WIDE, 8, 8, 1, XS>(a, st);
+  }
+  return launch4<QT, WIDE, 8, 4, 1, XS>(a, st);
 }
 
 template <int QT, bool WIDE>
-hipError_t launch_m(const GemvMfmaArgs& a, int mt, int sw, hipStream_t st) {
-  if ((a.radd != nullptr || a.silu_pairs) && (mt != 1 || a.m != 1)) return hipErrorInvalidValue;
+hipError_t launch_m(const GemvMfmaArgs& a, int sw, hipStream_t st) {
+  if (a.m != 1) return hipErrorInvalidValue;
   if (a.silu_pairs && (a.radd != nullptr || a.w.n % 16 != 0)) return hipErrorInvalidValue;
   if (a.xs != kXPlain) {
-    // the decoder's fused projections: one row, f16-scale images
+    // the decoder's fused projections: f16-scale images
     if constexpr (WIDE) {
       return hipErrorInvalidValue;
     } else {
-      if (mt != 1 || a.m != 1) return hipErrorInvalidValue;
-      if (a.xs == kXNorm && a.hres != nullptr && a.nw != nullptr)
-        return launch_split<QT, WIDE, 1, kXNorm>(a, sw, st);
+      if (a.xs == kXNorm && a.hres != nullptr && a.nw != nullptr) return launch_split<QT, WIDE, kXNorm>(a, sw, st);
       return hipErrorInvalidValue;
     }
   }
-  switch (mt) {
-    case 1: return launch_split<QT, WIDE, 1>(a, sw, st);
-    case 2: return launch_split<QT, WIDE, 2>(a, sw, st);
-    case 4: return launch_split<QT, WIDE, 4>(a, sw, st);
-    case 8: return launch_split<QT, WIDE, 8>(a, sw, st);
-    default: return launch_split<QT, WIDE, 16>(a, sw, st);
-  }
+  return launch_split<QT, WIDE>(a, sw, st);
 }
 
 template <int QT>
-hipError_t launch_w(const GemvMfmaArgs& a, bool wide, int mt, int sw, hipStream_t st) {
-  return wide ? launch_m<QT, true>(a, mt, sw, st) : launch_m<QT, false>(a, mt, sw, st);
+hipError_t launch_w(const GemvMfmaArgs& a, bool wide, int sw, hipStream_t st) {
+  return wide ? launch_m<QT, true>(a, sw, st) : launch_m<QT, false>(a, sw, st);
 }
 
 }  // namespace
 
 bool gemv_mfma_supported(int32_t qtype, int32_t layout, uint64_t k) {
   return layout == kOutputRows && qtype >= kQ8_0 && qtype <= kQ6_K && k % 256 == 0 && k > 0;
-}
-
-uint32_t gemv_pre_splits(int32_t qtype, bool wide, uint64_t k, uint64_t n, int mt) {
-  const uint64_t units = k / 256, tiles = (n + 15) / 16;
-  auto by_mt = [&](auto qc, auto wc) -> uint32_t {
-    constexpr int QT = decltype(qc)::value;
-    constexpr bool W = decltype(wc)::value;
-    switch (mt) {
-      case 2: return pre_units<QT, W, 2>(units, tiles);
-      case 4: return pre_units<QT, W, 4>(units, tiles);
-      case 8: return pre_units<QT, W, 8>(units, tiles);
-      default: return pre_units<QT, W, 16>(units, tiles);
-    }
-  };
-  auto by_w = [&](auto qc) -> uint32_t {
-    return wide ? by_mt(qc, std::true_type{}) : by_mt(qc, std::false_type{});
-  };
-  uint32_t us = 1;
-  switch (qtype) {
-    case kQ8_0: us = by_w(std::integral_constant<int, kQ8_0>{}); break;
-    case kQ4_0: us = by_w(std::integral_constant<int, kQ4_0>{}); break;
-    case kQ4_K: us = by_w(std::integral_constant<int, kQ4_K>{}); break;
-    case kQ5_K: us = by_w(std::integral_constant<int, kQ5_K>{}); break;
-    default: us = by_w(std::integral_constant<int, kQ6_K>{}); break;
-  }
-  return static_cast<uint32_t>((units + us - 1) / us);
 }
 
 int gemv_mfma_split(uint64_t k, uint64_t n) {
@@ -793,15 +527,14 @@ int gemv_mfma_split(uint64_t k, uint64_t n) {
   return k <= 4096 ? 4 : 8;
 }
 
-hipError_t launch_gemv_mfma(int32_t qtype, bool wide, int mt, int sw, const GemvMfmaArgs& a,
-                            hipStream_t st) {
+hipError_t launch_gemv_mfma(int32_t qtype, bool wide, int sw, const GemvMfmaArgs& a, hipStream_t st) {
   if (sw != 4 && sw != 8) return hipErrorInvalidValue;
   switch (qtype) {
-    case kQ8_0: return launch_w<kQ8_0>(a, wide, mt, sw, st);
-    case kQ4_0: return launch_w<kQ4_0>(a, wide, mt, sw, st);
-    case kQ4_K: return launch_w<kQ4_K>(a, wide, mt, sw, st);
-    case kQ5_K: return launch_w<kQ5_K>(a, wide, mt, sw, st);
-    case kQ6_K: return launch_w<kQ6_K>(a, wide, mt, sw, st);
+    case kQ8_0: return launch_w<kQ8_0>(a, wide, sw, st);
+    case kQ4_0: return launch_w<kQ4_0>(a, wide, sw, st);
+    case kQ4_K: return launch_w<kQ4_K>(a, wide, sw, st);
+    case kQ5_K: return launch_w<kQ5_K>(a, wide, sw, st);
+    case kQ6_K: return launch_w<kQ6_K>(a, wide, sw, st);
     default: return hipErrorInvalidValue;
   }
 }

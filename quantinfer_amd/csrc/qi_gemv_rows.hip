@@ -879,12 +879,6 @@ hipError_t launch_rows_w(const RowsArgs& a, uint32_t ksplit, hipStream_t st) {
 
 }  // namespace
 
-bool gemv_rows_supported(int32_t qtype, int32_t layout, uint64_t k) {
-  return layout == kOutputRows &&
-         (qtype == kQ8_0 || qtype == kQ4_0 || qtype == kQ4_K || qtype == kQ5_K || qtype == kQ6_K) && k % 256 == 0 &&
-         k > 0;
-}
-
 uint32_t gemv_rows_splits(uint64_t k, uint64_t n, uint32_t m) {
   // one-tile workgroups: no K split (launch_rows_w)
   if (rows_one_tile(k, n, m)) return 1;
@@ -925,7 +919,7 @@ hipError_t launch_gemv_rows_records(const float* x, uint64_t k, int m, uint8_t* 
 
 hipError_t launch_gemv_rows(int32_t qtype, bool wide, const View& w, const float* x, int m, float* y, float* part,
                             uint32_t ksplit, const uint8_t* records, hipStream_t st) {
-  if (m < 1 || m > 16 || ksplit < 1) return hipErrorInvalidValue;
+  if (m < 1 || m > 16 || ksplit < 1 || w.k == 0 || w.k % 256 != 0) return hipErrorInvalidValue;
   if ((records != nullptr) != gemv_rows_records(w.k, w.n, static_cast<uint32_t>(m))) return hipErrorInvalidValue;
   RowsArgs a{w, x, y, m, 0, 0, part, records};
   const uint32_t units = w.units;

@@ -32,9 +32,8 @@ struct GemvMfmaArgs {
   View w;
   const float* x;  // [m, k] device, 16-byte aligned rows
   float* y;        // [m, n]
-  int m;           // rows in this launch (<= compile-time tile)
+  int m;           // rows in this launch: 1 (2-16 rows: launch_gemv_rows)
   uint32_t chunk_units = 0;  // set by the launcher: K units whose activation digits fit LDS
-  const uint8_t* digits = nullptr;  // activation records from launch_gemv_digits (2+ rows), or null
   int xs = kXPlain;  // one row, f16-scale images only
   // kXNorm: the residual row, the norm weight and epsilon
   const float* hres = nullptr;
@@ -48,27 +47,14 @@ struct GemvMfmaArgs {
   // the 8 up rows of the same outputs, and y[8 t + c] = g / (1 + exp(-g)) * u
   // (backends/cpu/src/backend.rs:224-237), N / 2 outputs
   bool silu_pairs = false;
-  // two or more rows: K parts over the grid (gemv_pre_splits), partial sums
-  // [ksplit][m][n] in `part` when ksplit > 1, added by launch_splitk_sum
-  float* part = nullptr;
-  uint32_t ksplit = 1;
-  uint32_t split_units = 0;  // set by the launcher
 };
 bool gemv_mfma_supported(int32_t qtype, int32_t layout, uint64_t k);
-// Activation records of m rows (digits + window scales, the GEMV's LDS layout)
-// into `out` of gemv_digits_bytes(k, m) bytes.
-hipError_t launch_gemv_digits(int32_t qtype, const float* x, uint64_t k, uint32_t m, uint8_t* out,
-                              hipStream_t st);
-uint64_t gemv_digits_bytes(uint64_t k, uint32_t m);
 int gemv_mfma_split(uint64_t k, uint64_t n);
-// K parts of a 2..16-row GEMV launch (its partial sums: parts * m * n floats)
-uint32_t gemv_pre_splits(int32_t qtype, bool wide, uint64_t k, uint64_t n, int mt);
 // y[i] = sum over s of part[s * stride + i] (i < count = m * n) in split order;
 // a non-finite sum is recomputed in the reference's order
 hipError_t launch_splitk_sum(const Image& im, const View& v, const float* part, uint32_t splits,
                              uint64_t count, uint64_t stride, float* y, const float* x, hipStream_t st);
-hipError_t launch_gemv_mfma(int32_t qtype, bool wide, int mt, int split, const GemvMfmaArgs& a,
-                            hipStream_t st);
+hipError_t launch_gemv_mfma(int32_t qtype, bool wide, int split, const GemvMfmaArgs& a, hipStream_t st);
 
 // Matrix-core decode GEMV of 2-16 rows with dense operands (qi_gemv_rows.hip):
 // one kernel, K parts over the grid (gemv_rows_splits, by shape and row count)
@@ -77,7 +63,8 @@ hipError_t launch_gemv_mfma(int32_t qtype, bool wide, int mt, int split, const G
 // gemv_rows_records (9-16 rows, no K parts) the GEMV reads the activation
 // records that launch_gemv_rows_records builds into `records`
 // (gemv_rows_records_bytes bytes, 0 elsewhere; null records elsewhere).
-bool gemv_rows_supported(int32_t qtype, int32_t layout, uint64_t k);
+// Shapes: those of gemv_mfma_supported (every format, output rows, K a
+// multiple of 256).
 uint32_t gemv_rows_splits(uint64_t k, uint64_t n, uint32_t m);
 bool gemv_rows_records(uint64_t k, uint64_t n, uint32_t m);
 uint64_t gemv_rows_records_bytes(uint64_t k, uint64_t n, uint32_t m);

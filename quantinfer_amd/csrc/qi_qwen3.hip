@@ -1202,7 +1202,7 @@ qi_hip_status fused_linear(qi_hip_qwen3* m, const Linear& l, int xs, const float
   ga.radd = radd;
   ga.silu_pairs = pairs;
   const int split = m->ctx->gemv_split > 0 ? m->ctx->gemv_split : qi::gemv_mfma_split(im.k, im.n);
-  QI_HIP_TRY(qi::launch_gemv_mfma(im.qtype, false, 1, split, ga, m->ctx->stream), "launch fused gemv");
+  QI_HIP_TRY(qi::launch_gemv_mfma(im.qtype, false, split, ga, m->ctx->stream), "launch fused gemv");
   return QI_HIP_OK;
 }
 
