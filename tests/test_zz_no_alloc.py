@@ -31,11 +31,12 @@ def ctx():
 
 CASES = [
     # (qtype, layout, K, N, first M, second M, mode): what the plan uses
-    (qa.Q4_K, qa.OUTPUT_ROWS, 4096, 4096, 512, 8, qa.MODE_AUTO),     # GEMM + split-K partials, then GEMV records
+    (qa.Q4_K, qa.OUTPUT_ROWS, 4096, 4096, 512, 8, qa.MODE_AUTO),     # GEMM + split-K partials, then 8-row GEMV K parts
     (qa.Q8_0, qa.OUTPUT_ROWS, 4096, 12288, 2048, 130, qa.MODE_AUTO),  # GEMM without, then with a K split
     (qa.Q6_K, qa.OUTPUT_ROWS, 4096, 1024, 200, 1, qa.MODE_MFMA),     # the Q6_K GEMM, then one row
     (qa.Q5_K, qa.OUTPUT_ROWS, 1024, 512, 16, 3, qa.MODE_F32),        # 2-16 row GEMV with K parts
     (qa.Q4_0, qa.OUTPUT_ROWS, 4096, 12288, 16, 9, qa.MODE_F32),      # 2-16 row GEMV, activation records
+    (qa.Q6_K, qa.OUTPUT_ROWS, 14336, 4096, 16, 9, qa.MODE_F32),      # Q6_K 2-16 rows: records and K parts
     (qa.Q4_0, qa.ROW_MAJOR, 4096, 4096, 9, 1, qa.MODE_F32),          # row-major GEMV with K-split partials
     (qa.Q4_K, qa.OUTPUT_ROWS, 512, 64, 5, 2, qa.MODE_EXACT),         # no workspace
 ]
