@@ -247,10 +247,8 @@ struct Dense<kQ6_K> {
   __device__ static long bc(const T& t, int w) {
     const int ip = w >> 2, hf = (w >> 1) & 1, c = w & 1, gp = 2 * ip + c;
     const int up = 6 - 2 * c - 4 * hf;  // qh bits 2c + 4hf to bits 6-7
-    const uint32_t nl = (hf ? t.lo[gp] >> 2 : t.lo[gp] << 2) & 0x3C3C3C3Cu;
-    const uint32_t nh = (hf ? t.hi[gp] >> 2 : t.hi[gp] << 2) & 0x3C3C3C3Cu;
-    const uint32_t a = nl ^ ((t.h[2 * ip] << up) & 0xC0C0C0C0u) ^ 0x80808080u;
-    const uint32_t b = nh ^ ((t.h[2 * ip + 1] << up) & 0xC0C0C0C0u) ^ 0x80808080u;
+    const uint32_t a = q6_centred(hf ? t.lo[gp] >> 2 : t.lo[gp] << 2, t.h[2 * ip] << up);
+    const uint32_t b = q6_centred(hf ? t.hi[gp] >> 2 : t.hi[gp] << 2, t.h[2 * ip + 1] << up);
     return pack2(a, b);
   }
 };

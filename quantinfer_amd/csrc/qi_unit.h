@@ -240,6 +240,16 @@ struct Unit<kQ4_K> : UnitQ45K<false> {};
 template <>
 struct Unit<kQ5_K> : UnitQ45K<true> {};
 
+// Four Q6_K codes as 4 (q - 32) in signed bytes, from the low nibbles placed
+// in bits 2-5 of `n` and the two high bits in bits 6-7 of `h` (the other bits
+// of both are ignored): 4q takes bits 2-5 from n and 6-7 from h (one bit
+// select), and clearing bits 0-1 while flipping bit 7 (subtracting 128 =
+// 4 * 32) is one more bitwise operation.
+__device__ __forceinline__ uint32_t q6_centred(uint32_t n, uint32_t h) {
+  const uint32_t v = (n & 0x3C3C3C3Cu) | (h & ~0x3C3C3C3Cu);
+  return (v & 0xFCFCFCFCu) ^ 0x80808080u;
+}
+
 // Q6_K: lane group g = 2*ip + c holds ql bytes [64ip + 32c, +32) and qh bytes
 // [32ip, +32). Step t < 4: low nibbles of ql bytes 8t.. with qh bits 2c (elements
 // 128ip + 32c + 8t + j); t >= 4: high nibbles of ql bytes 8(t-4).. with qh bits
@@ -295,9 +305,7 @@ struct Unit<kQ6_K> {
     const uint32_t h2 = ((hi >> sh) & 0x0F0F0F0Fu) | (((hh >> hs) & 0x03030303u) << 4);
     return static_cast<long>((static_cast<uint64_t>(h2) << 32) | l2);
   }
-  // the same codes as 4 (q - 32), signed bytes: 4q = the low nibble in bits
-  // 2-5 and the two high bits in bits 6-7 (disjoint, so joined by xor), and
-  // flipping bit 7 subtracts 128 = 4 * 32
+  // the same codes as 4 (q - 32), signed bytes (q6_centred)
   __device__ static long centred_codes(const Raw& r, uint32_t g, int t) {
     const int tt = t & 3;
     const uint4 q = r.q[tt >> 1];
@@ -305,9 +313,8 @@ struct Unit<kQ6_K> {
     const uint32_t lo = (tt & 1) ? q.z : q.x, hi = (tt & 1) ? q.w : q.y;
     const uint32_t hl = (tt & 1) ? h.z : h.x, hh = (tt & 1) ? h.w : h.y;
     const int hs = 6 - 2 * static_cast<int>(g & 1) - (t >= 4 ? 4 : 0);  // 6 - (bit of the pair)
-    const uint32_t ll = (t >= 4 ? lo >> 2 : lo << 2) & 0x3C3C3C3Cu, lh = (t >= 4 ? hi >> 2 : hi << 2) & 0x3C3C3C3Cu;
-    const uint32_t l2 = ll ^ ((hl << hs) & 0xC0C0C0C0u) ^ 0x80808080u;
-    const uint32_t h2 = lh ^ ((hh << hs) & 0xC0C0C0C0u) ^ 0x80808080u;
+    const uint32_t l2 = q6_centred(t >= 4 ? lo >> 2 : lo << 2, hl << hs);
+    const uint32_t h2 = q6_centred(t >= 4 ? hi >> 2 : hi << 2, hh << hs);
     return static_cast<long>((static_cast<uint64_t>(h2) << 32) | l2);
   }
 };
