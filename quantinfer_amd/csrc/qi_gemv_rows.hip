@@ -658,10 +658,11 @@ __global__ __launch_bounds__(kRowsThreads) void gemv_rows_kernel(RowsArgs a) {
             const float comb1 = fmaf(static_cast<float>(c1[2] + c1[3] * 256), 65536.0f,
                                      static_cast<float>(c1[0] + c1[1] * 256));
             accu[q] = fmaf(xw, fmaf(s1, comb1, s0 * comb0), accu[q]);
-            // the window's sums are combined here, not after the last window
-            // (the compiler would otherwise keep every window's digit sums live)
-            asm volatile("" : "+v"(accu[q]));
           }
+          // the window's sums are combined here, not after the last window
+          // (the compiler would otherwise keep every window's digit sums live)
+#pragma unroll
+          for (int q = 0; q < MG; ++q) asm volatile("" : "+v"(accu[q]));
           __builtin_amdgcn_sched_barrier(0);
         }
         const float d = U::template d<WIDE>(r);
