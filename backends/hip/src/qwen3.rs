@@ -7,7 +7,8 @@ use std::sync::Arc;
 
 use quantinfer_core::Tensor;
 use quantinfer_kernel::{KernelError, Result};
-use quantinfer_runtime::{LinearWeight, Qwen3Config, Qwen3LayerWeights};
+use quantinfer_model::Qwen3Config;
+use quantinfer_runtime::{LinearWeight, Qwen3LayerWeights};
 
 use crate::{ffi, status, Context, HipBackend};
 

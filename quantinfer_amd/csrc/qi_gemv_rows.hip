@@ -890,7 +890,11 @@ uint32_t gemv_rows_splits(uint64_t k, uint64_t n, uint32_t m) {
   const uint64_t most = units / 4 ? units / 4 : 1;
   if (s > most) s = most;
   if (s < 1) s = 1;
-  return static_cast<uint32_t>(s);
+  // the launch gives every part ceil(units / s) units; with that part length
+  // fewer parts may cover K (8960 / 256 = 35 units over s = 8 gives parts of
+  // 5, so 7 parts): return the count the launch will actually run
+  const uint64_t part_units = (units + s - 1) / s;
+  return static_cast<uint32_t>((units + part_units - 1) / part_units);
 }
 
 bool gemv_rows_records(uint64_t k, uint64_t n, uint32_t m) {

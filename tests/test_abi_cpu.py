@@ -491,3 +491,68 @@ def test_rust_ffi_declares_every_header_function():
                          ("Q6K", ["scale", "scales", "low_bits", "high_bits"])):
         body = re.search(r"pub struct %s \{(.*?)\}" % name, ffi, re.S).group(1)
         assert re.findall(r"pub (\w+):", body) == fields, name
+
+
+# ------------------------------------------- planner arithmetic (host only)
+
+def _planner(name, *argtypes):
+    fn = getattr(qa.lib(), name)
+    fn.argtypes = list(argtypes)
+    fn.restype = ctypes.c_uint32
+    return fn
+
+
+def test_gemv_rows_split_count_gives_every_part_units():
+    """The 2-16 row GEMV's launch gives each of its `s` K parts ceil(units/s)
+    units and refuses a split count whose parts would not all hold units.
+    The planner (qi::gemv_rows_splits, host code in the library) must return
+    a count the launch accepts for every shape: K = 8960, N = 1536 at 2-4
+    rows once asked for 8 parts of 5 units (7 parts cover K)."""
+    splits = _planner("_ZN2qi16gemv_rows_splitsEmmj", ctypes.c_uint64, ctypes.c_uint64, ctypes.c_uint32)
+    seen = set()
+    for units in range(1, 129):
+        k = 256 * units
+        for n in list(range(16, 4097, 16)) + [4100, 12288, 14336]:
+            for m in range(2, 17):
+                s = splits(k, n, m)
+                assert 1 <= s <= units, (k, n, m, s)
+                part = -(-units // s)
+                assert -(-units // part) == s, (k, n, m, s)
+                seen.add(s)
+    assert len(seen) > 8  # the sweep reaches many split counts
+    assert splits(8960, 1536, 2) == 7 and splits(6400, 1024, 8) == 5
+
+
+def _rust_paths():
+    """Every (crate, name) that backends/hip/src/*.rs takes from a
+    quantinfer crate: `use quantinfer_x::{a, b}`, `use quantinfer_x::a` and
+    qualified paths `quantinfer_x::Name` in the code."""
+    src = os.path.join(ROOT, "backends", "hip", "src")
+    used = set()
+    for f in sorted(os.listdir(src)):
+        text = open(os.path.join(src, f)).read()
+        text = re.sub(r"//[^\n]*", "", text)  # comments name crates too
+        for crate, body in re.findall(r"\buse\s+(quantinfer_\w+)::\{([^}]*)\}", text):
+            used.update((crate, n.strip()) for n in body.split(",") if n.strip())
+        for crate, name in re.findall(r"\buse\s+(quantinfer_\w+)::(\w+)\s*;", text):
+            used.add((crate, name))
+        for crate, name in re.findall(r"(?<!use )\b(quantinfer_\w+)::(\w+)\b(?!::\{)", text):
+            used.add((crate, name))
+    return used
+
+
+def test_rust_crate_imports_exist_in_the_reference():
+    """Each name the crate imports is public in the reference crate it is
+    taken from (the committed list cites the line that exports it), and each
+    crate it uses is a dependency in its Cargo.toml."""
+    import json
+    ref = json.load(open(os.path.join(ROOT, "tests", "golden", "reference_rust_exports.json")))
+    used = _rust_paths()
+    assert ("quantinfer_model", "Qwen3Config") in used
+    for crate, name in sorted(used):
+        assert name in ref["exports"].get(crate, {}), f"{crate}::{name} is not a public export"
+        assert name not in ref["not_exported"].get(crate, {}), f"{crate}::{name}"
+    cargo = open(os.path.join(ROOT, "backends", "hip", "Cargo.toml")).read()
+    deps = set(re.findall(r"^([a-z0-9-]+)\s*=\s*\{\s*workspace\s*=\s*true", cargo, re.M))
+    for crate in sorted({c for c, _ in used}):
+        assert ref["packages"][crate] in deps, crate

@@ -335,6 +335,22 @@ def test_config_shapes_f32_tolerance(ctx, cfg):
         assert reference_bound_ok(y, exact)
 
 
+@pytest.mark.parametrize("qtype,k,n,ms", [
+    (qa.Q4_K, 8960, 1536, [2, 3, 4]),   # 35 units: 7 K parts of 5
+    (qa.Q4_0, 6400, 1024, [5, 8, 16]),  # 25 units: 5 K parts of 5
+    (qa.Q6_K, 6400, 1024, [8]),
+], ids=["q4_k-K8960-N1536", "q4_0-K6400-N1024", "q6_k-K6400-N1024"])
+def test_gemv_rows_uneven_k_parts(ctx, qtype, k, n, ms):
+    """2-16 rows on shapes whose unit count does not divide into the first
+    split count tried: the planner returns the count the launch runs."""
+    blocks = po.make_weights(qtype, k, n, seed=0x5EED6200 + k + qtype, outliers=True)
+    w = ctx.weights(qtype, qa.OUTPUT_ROWS, k, n, blocks)
+    for m in ms:
+        x = po.fill_normal(0x5EED6300 + m, m * k).reshape(m, k)
+        _assert_f32(w.linear(x, qa.MODE_F32), x, blocks, qtype, n, f"K={k} N={n} M={m}")
+    w.free()
+
+
 @pytest.mark.parametrize("n", [20496, 20500, 24576, 24580])
 def test_q4_k_gemv_six_tile_workgroups(ctx, n):
     """One row, K=4096, 1281-1536 output tiles: the six-tile, two-wavefront
