@@ -71,14 +71,11 @@ fn main() {
         .args(["--offload-arch=gfx950", "-shared", "-fPIC", "-o"])
         .arg(&lib)
         .args(&objects)
-        .args(["-L/opt/rocm/lib", "-lrocblas", "-Wl,-rpath,/opt/rocm/lib"])
+        .args(["-Wl,-rpath,/opt/rocm/lib"])
         .status()
         .expect("hipcc link");
     assert!(status.success(), "linking libqi_hip.so failed");
     println!("cargo:rerun-if-changed={}", src.join("sources.txt").display());
     println!("cargo:rustc-link-search=native={}", out.display());
     println!("cargo:rustc-link-lib=dylib=qi_hip");
-    // the F32-weight GEMM of 17+ rows calls rocBLAS
-    println!("cargo:rustc-link-search=native=/opt/rocm/lib");
-    println!("cargo:rustc-link-lib=dylib=rocblas");
 }

@@ -419,7 +419,8 @@ def f32_head_bench(steps: int, warmup: int) -> dict:
     the unchanged runtime's LM head, [4096, 151936] f32 (a Q6_K head is
     dequantized at load, runtime/src/qwen3/loader.rs:47-61). One decode row
     (the streaming F32 GEMV, HBM-bound on 2.49 GB), the 512-row prompt's
-    logits (rocBLAS sgemm, against the f32 matrix-core peak), and the
+    logits (the f32 matrix-core GEMM, f32w_gemm_kernel, against the f32
+    matrix-core peak), and the
     synchronous per-token call with host buffers as the runtime makes it."""
     import quantinfer_amd as qa
     from quantinfer_amd import hiprt
@@ -465,7 +466,7 @@ def f32_head_bench(steps: int, warmup: int) -> dict:
         "m1_ms": round(out[1], 4),
         "roofline": {"bound": "hbm", "achieved": round(gbps, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None},
-        "m512": {"ms": round(out[512], 3), "tflops": round(tflops, 2), "kernel": "rocBLAS sgemm",
+        "m512": {"ms": round(out[512], 3), "tflops": round(tflops, 2), "kernel": "f32w_gemm_kernel (v_mfma_f32_16x16x4f32)",
                  "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": MFMA_F32_PEAK_TFLOPS,
                               "unit": "TFLOP/s", "frac": round(tflops / MFMA_F32_PEAK_TFLOPS, 4)}},
         "through_abi_m1_ms": round(abi_ms, 4),

@@ -39,8 +39,7 @@ def read_sources() -> list:
 SOURCES = read_sources()
 
 ARCH = "gfx950"
-# rocBLAS: the plain f32 GEMM of F32 weights at 17+ rows (qi_f32.hip)
-LINK = ["-L/opt/rocm/lib", "-lrocblas", "-Wl,-rpath,/opt/rocm/lib"]
+LINK = ["-Wl,-rpath,/opt/rocm/lib"]
 FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-Wall",
     "-ffp-contract=off", "-fno-fast-math", "-fno-gpu-flush-denormals-to-zero",

@@ -130,7 +130,6 @@ void ctx_destroy(qi_hip_ctx* c) {
     if (c->ws_used) (void)hipEventSynchronize(c->ws_event);
     (void)hipEventDestroy(c->ws_event);
   }
-  qi::f32w_blas_destroy(c->blas);
   if (c->xbuf) (void)hipFree(c->xbuf);
   if (c->ybuf) (void)hipFree(c->ybuf);
   if (c->hx) (void)hipHostFree(c->hx);
@@ -169,15 +168,13 @@ qi_hip_status grow_ws(qi_hip_ctx* c, hipStream_t st, float** buf, uint64_t* cap,
 // function decides, so that the growing path (run_linear) and the scratch
 // path (qi_hip_linear_device_noalloc) take the same kernels.
 struct LinearPlan {
-  enum Kind { kGemm, kRowMajor, kMfma, kPlanar, kF32Gemv, kF32Blas, kExact } kind = kExact;
+  enum Kind { kGemm, kRowMajor, kMfma, kPlanar, kF32Gemv, kF32Gemm, kExact } kind = kExact;
   uint64_t m_pad = 0;
   uint32_t splits = 1;  // GEMM K splits, or row-major GEMV K splits for 4-row chunks
   uint64_t h_floats = 0, s_floats = 0, d_floats = 0;  // f16 activations, partials, records
 };
 
-// allow_library: the call may use rocBLAS (which allocates its own memory)
-qi_hip_status plan_linear(const Image& im, uint64_t m, int32_t mode, LinearPlan* p,
-                          bool allow_library = true) {
+qi_hip_status plan_linear(const Image& im, uint64_t m, int32_t mode, LinearPlan* p) {
   if (mode < QI_HIP_MODE_AUTO || mode > QI_HIP_MODE_MFMA)
     return fail(QI_HIP_INVALID_INPUT, "unknown arithmetic mode");
   bool use_gemm = false;
@@ -201,9 +198,9 @@ qi_hip_status plan_linear(const Image& im, uint64_t m, int32_t mode, LinearPlan*
     return QI_HIP_OK;
   }
   if (mode != QI_HIP_MODE_EXACT && qi::f32w_gemv_supported(im)) {
-    // F32 weights: the streaming GEMV in 16-row chunks, rocBLAS sgemm above
-    if (m > 16 && allow_library) {
-      p->kind = LinearPlan::kF32Blas;
+    // F32 weights: the streaming GEMV in 8-row chunks, the matrix-core GEMM above
+    if (m > qi::kF32GemvMaxRows && qi::f32w_gemm_supported(im)) {
+      p->kind = LinearPlan::kF32Gemm;
       return QI_HIP_OK;
     }
     p->kind = LinearPlan::kF32Gemv;
@@ -318,16 +315,9 @@ qi_hip_status enqueue_linear(const qi_hip_weights* w, const LinearPlan& p, const
                    "launch f32 gemv");
       }
       return QI_HIP_OK;
-    case LinearPlan::kF32Blas: {
-      qi_hip_ctx* c = w->ctx;
-      if (c->blas == nullptr) {
-        const int e = qi::f32w_blas_create(&c->blas);
-        if (e != 0) return fail(QI_HIP_RUNTIME_ERROR, "rocBLAS handle: status " + std::to_string(e));
-      }
-      const int e = qi::f32w_sgemm(c->blas, im, v, x, m, y, st);
-      if (e != 0) return fail(QI_HIP_RUNTIME_ERROR, "rocBLAS sgemm: status " + std::to_string(e));
+    case LinearPlan::kF32Gemm:
+      QI_HIP_TRY(qi::launch_f32w_gemm(im, v, x, m, y, st), "launch f32 gemm");
       return QI_HIP_OK;
-    }
     case LinearPlan::kExact:
       QI_HIP_TRY(qi::launch_exact(im, v, x, m, y, st), "launch exact matmul");
       return QI_HIP_OK;
@@ -590,7 +580,7 @@ qi_hip_status qi_hip_linear_device_noalloc(qi_hip_ctx* c, const qi_hip_weights* 
   std::lock_guard<std::mutex> lock(c->mu);
   QI_HIP_TRY(hipSetDevice(c->device), "set device");
   LinearPlan p;
-  if ((s = plan_linear(w->im, m, mode, &p, false)) != QI_HIP_OK) return s;
+  if ((s = plan_linear(w->im, m, mode, &p)) != QI_HIP_OK) return s;
   auto a256 = [](uint64_t floats) { return (floats * 4 + 255) & ~static_cast<uint64_t>(255); };
   const uint64_t hb = a256(p.h_floats), sb = a256(p.s_floats), db = a256(p.d_floats);
   if (hb + sb + db > kScratchBytes)

@@ -47,7 +47,6 @@ struct qi_hip_ctx {
   uint64_t dcap = 0;
   int gemv_split = 0;  // QI_HIP_GEMV_SPLIT tuning override (wavefronts per GEMV workgroup: 4 or 8)
   void* scratch = nullptr;  // device address of this device's scratch array (qi_abi.hip)
-  void* blas = nullptr;     // rocBLAS handle of the F32-weight GEMM, made on first use
 };
 
 struct qi_hip_weights {

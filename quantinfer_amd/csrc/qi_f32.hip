@@ -5,21 +5,20 @@
 // of it). Two throughput paths, judged by the F32 tolerance (EXACT mode keeps
 // the sequential-k kernel of qi_exact.hip):
 //
-// * up to 16 activation rows: a streaming GEMV, 8 rows per launch. A lane owns 4 consecutive
+// * up to 8 activation rows: a streaming GEMV (in 8-row launches for any
+//   row count when K is not a multiple of 4). A lane owns 4 consecutive
 //   columns and reads them with one 16-byte load per k (a wavefront reads
 //   1 KB of a row), the activations are wavefront-uniform loads, and each k
 //   adds x * w for every row with an FMA. The four wavefronts of a workgroup
 //   split its K range and the grid's y dimension splits K further; the parts
 //   are summed in a fixed order (through LDS, then f32w_sum_kernel), so
 //   results do not depend on scheduling. HBM-bound: K * N * 4 bytes.
-// * more rows: rocBLAS sgemm (a plain f32 library GEMM on the matrix cores;
-//   there is nothing to fuse into it).
+// * more rows: a GEMM on the f32 matrix cores (f32w_gemm_kernel below),
+//   LDS-staged tiles of 32 to 128 rows by 128 or 256 columns.
 //
 // An output whose sum is not finite (a NaN or infinite activation, or an
 // overflow) is recomputed in the reference's order, which fixes which outputs
 // are NaN and which +-Inf.
-#include <rocblas/rocblas.h>
-
 #include "qi_device.h"
 #include "qi_internal.h"
 
@@ -170,33 +169,164 @@ hipError_t launch_f32w_gemv(const Image& im, const View& v, const float* x, uint
   return hipGetLastError();
 }
 
-// y[M, N] = x[M, K] W[K, N], all row-major: in rocBLAS's column-major terms
-// y^T (N x M, ld N) = W^T (N x K, ld N) * x^T (K x M, ld K).
-int f32w_sgemm(void* handle, const Image& im, const View& v, const float* x, uint64_t m, float* y,
-               hipStream_t st) {
-  rocblas_handle h = static_cast<rocblas_handle>(handle);
-  if (rocblas_set_stream(h, st) != rocblas_status_success) return -1;
-  const float one = 1.0f, zero = 0.0f;
-  const rocblas_int n = static_cast<rocblas_int>(im.n), k = static_cast<rocblas_int>(im.k);
-  const rocblas_int mm = static_cast<rocblas_int>(m);
-  const rocblas_status s = rocblas_sgemm(h, rocblas_operation_none, rocblas_operation_none, n, mm, k, &one,
-                                         reinterpret_cast<const float*>(v.qs), n, x, k, &zero, y, n);
-  return s == rocblas_status_success ? 0 : static_cast<int>(s);
+// ---------------------------------------------------------------- GEMM
+//
+// More rows: y[M, N] = x[M, K] W[K, N] on the f32 matrix cores
+// (v_mfma_f32_16x16x4f32: f32 products, f32 sums). A workgroup owns an
+// MT x NT tile of y (MT = WM*TM*16 rows, NT = WN*TN*16 columns), wavefront
+// (wm, wn) a TM x TN grid of 16 x 16 blocks of it. K advances in stages of 32:
+// the x stage (MT rows x 32, row stride 36 floats) and the W stage (32 rows x
+// NT, row stride NT + 4) are loaded from HBM into registers with 16-byte
+// loads while the previous stage is multiplied out of LDS, then stored into
+// the other LDS buffer; one barrier per stage.
+//
+// Operands: for k-step s (0..3) of a 16-wide k slice, lane l (row or column
+// l % 16, lane group g = l / 16) supplies k = 16 kk + 4 g + s. So an A operand
+// for four k-steps is one 16-byte LDS read (x[row][16 kk + 4 g .. + 3]), and
+// a B operand one 4-byte read of W[16 kk + 4 g + s][col]; the row strides put
+// the four lane groups' rows in different LDS banks. Rows past M, k past K
+// and columns past N load as zeros (K and N are multiples of 4, so a 16-byte
+// load is all in or all out) and are never stored.
+//
+// Block order is XCD-aware: the hardware deals workgroups round-robin over
+// the 8 XCDs, so workgroup b takes logical tile (b % 8) * ceil(B / 8) + b / 8
+// and each XCD runs a contiguous run of logical tiles; M tiles vary fastest,
+// so the workgroups sharing a W column panel run on one XCD's L2.
+namespace {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr uint32_t kF32Kt = 32;
+
+template <int WM, int WN, int TM, int TN>
+__global__ __launch_bounds__(WM * WN * 64) void f32w_gemm_kernel(const float* __restrict__ W, uint32_t K,
+                                                                  uint32_t N, const float* __restrict__ x,
+                                                                  uint32_t M, uint32_t mtiles,
+                                                                  uint32_t ntiles, float* __restrict__ y) {
+  constexpr int MT = WM * TM * 16, NT = WN * TN * 16, KT = kF32Kt, THREADS = WM * WN * 64;
+  constexpr int XS = KT + 4, WS = NT + 4;
+  constexpr int XL = MT * KT / 4 / THREADS, WL = KT * NT / 4 / THREADS;  // 16-byte loads per thread
+  static_assert(XL >= 1 && WL >= 1 && MT * KT / 4 % THREADS == 0 && KT * NT / 4 % THREADS == 0, "tile");
+  __shared__ __align__(16) float xs[2][MT * XS];
+  __shared__ __align__(16) float ws[2][KT * WS];
+
+  const uint32_t tiles = mtiles * ntiles;
+  const uint32_t per = (tiles + 7) / 8;
+  const uint32_t logical = (blockIdx.x % 8) * per + blockIdx.x / 8;
+  if (logical >= tiles) return;
+  const uint32_t m0 = (logical % mtiles) * MT, n0 = (logical / mtiles) * NT;
+  const uint32_t t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const uint32_t wm = wave / WN, wn = wave % WN, r16 = lane & 15, g = lane >> 4;
+
+  f32x4 xr[XL], wr[WL];
+  auto load = [&](uint32_t k0) {
+#pragma unroll
+    for (int i = 0; i < XL; ++i) {
+      const uint32_t e = t + i * THREADS, row = e / (KT / 4), k = k0 + (e % (KT / 4)) * 4;
+      xr[i] = (m0 + row < M && k < K)
+                  ? *reinterpret_cast<const f32x4*>(x + static_cast<uint64_t>(m0 + row) * K + k)
+                  : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+#pragma unroll
+    for (int i = 0; i < WL; ++i) {
+      const uint32_t e = t + i * THREADS, kr = e / (NT / 4), n = n0 + (e % (NT / 4)) * 4;
+      wr[i] = (k0 + kr < K && n < N)
+                  ? __builtin_nontemporal_load(
+                        reinterpret_cast<const f32x4*>(W + static_cast<uint64_t>(k0 + kr) * N + n))
+                  : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+  };
+  auto store = [&](int b) {
+#pragma unroll
+    for (int i = 0; i < XL; ++i) {
+      const uint32_t e = t + i * THREADS;
+      *reinterpret_cast<f32x4*>(&xs[b][(e / (KT / 4)) * XS + (e % (KT / 4)) * 4]) = xr[i];
+    }
+#pragma unroll
+    for (int i = 0; i < WL; ++i) {
+      const uint32_t e = t + i * THREADS;
+      *reinterpret_cast<f32x4*>(&ws[b][(e / (NT / 4)) * WS + (e % (NT / 4)) * 4]) = wr[i];
+    }
+  };
+
+  f32x4 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  const uint32_t stages = (K + KT - 1) / KT;
+  load(0);
+  store(0);
+  __syncthreads();
+  for (uint32_t s = 0; s < stages; ++s) {
+    const int b = s & 1;
+    if (s + 1 < stages) load((s + 1) * KT);
+    const float* xb = &xs[b][(wm * TM * 16 + r16) * XS + 4 * g];
+    const float* wb = &ws[b][(4 * g) * WS + wn * TN * 16 + r16];
+#pragma unroll
+    for (int kk = 0; kk < KT / 16; ++kk) {
+      f32x4 a[TM];
+#pragma unroll
+      for (int i = 0; i < TM; ++i) a[i] = *reinterpret_cast<const f32x4*>(xb + i * 16 * XS + kk * 16);
+#pragma unroll
+      for (int st = 0; st < 4; ++st) {
+        float bv[TN];
+#pragma unroll
+        for (int j = 0; j < TN; ++j) bv[j] = wb[(kk * 16 + st) * WS + j * 16];
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+          for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i][st], bv[j], acc[i][j], 0, 0, 0);
+      }
+    }
+    if (s + 1 < stages) store(b ^ 1);
+    __syncthreads();
+  }
+
+  // lane l holds rows 4 g + 0..3 of each block, column l % 16
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const uint32_t n = n0 + wn * TN * 16 + j * 16 + r16;
+      if (n >= N) continue;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const uint32_t m = m0 + wm * TM * 16 + i * 16 + 4 * g + q;
+        if (m >= M) continue;
+        float v = acc[i][j][q];
+        if (!__builtin_isfinite(v)) v = f32w_exact(W, K, N, x + static_cast<uint64_t>(m) * K, n);
+        y[static_cast<uint64_t>(m) * N + n] = v;
+      }
+    }
 }
 
-int f32w_blas_create(void** handle) {
-  rocblas_handle h = nullptr;
-  const rocblas_status s = rocblas_create_handle(&h);
-  if (s != rocblas_status_success) return static_cast<int>(s);
-  // host-side alpha/beta, default (non-atomic, deterministic) kernels
-  rocblas_set_pointer_mode(h, rocblas_pointer_mode_host);
-  rocblas_set_atomics_mode(h, rocblas_atomics_not_allowed);
-  *handle = h;
-  return 0;
+template <int WM, int WN, int TM, int TN>
+hipError_t launch_f32w_gemm_t(const float* W, uint32_t K, uint32_t N, const float* x, uint32_t M, float* y,
+                              hipStream_t st) {
+  constexpr uint32_t MT = WM * TM * 16, NT = WN * TN * 16;
+  const uint32_t mtiles = (M + MT - 1) / MT, ntiles = (N + NT - 1) / NT;
+  const uint64_t tiles = static_cast<uint64_t>(mtiles) * ntiles;
+  if (tiles > 0x7fffffffull) return hipErrorInvalidValue;
+  const uint32_t grid = static_cast<uint32_t>((tiles + 7) / 8 * 8);
+  hipLaunchKernelGGL((f32w_gemm_kernel<WM, WN, TM, TN>), dim3(grid), dim3(WM * WN * 64), 0, st, W, K, N, x, M,
+                     mtiles, ntiles, y);
+  return hipGetLastError();
 }
 
-void f32w_blas_destroy(void* handle) {
-  if (handle) rocblas_destroy_handle(static_cast<rocblas_handle>(handle));
+}  // namespace
+
+bool f32w_gemm_supported(const Image& im) { return f32w_gemv_supported(im) && im.k % 4 == 0; }
+
+hipError_t launch_f32w_gemm(const Image& im, const View& v, const float* x, uint64_t m, float* y, hipStream_t st) {
+  if (!f32w_gemm_supported(im) || m < 1 || m > 0x7fffffffull || im.k > 0x7fffffffull || im.n > 0x7fffffffull)
+    return hipErrorInvalidValue;
+  const float* W = reinterpret_cast<const float*>(v.qs);
+  const uint32_t K = static_cast<uint32_t>(im.k), N = static_cast<uint32_t>(im.n), M = static_cast<uint32_t>(m);
+  if (M <= 32) return launch_f32w_gemm_t<1, 4, 2, 4>(W, K, N, x, M, y, st);
+  if (M <= 64) return launch_f32w_gemm_t<1, 4, 4, 4>(W, K, N, x, M, y, st);
+  return launch_f32w_gemm_t<2, 2, 4, 4>(W, K, N, x, M, y, st);
 }
 
 }  // namespace qi

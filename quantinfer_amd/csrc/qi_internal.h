@@ -82,16 +82,18 @@ hipError_t launch_gemv_rm(const Image& im, const View& v, const float* x, uint32
 
 // F32 weights (row-major [K, N] f32, N a multiple of 4): the streaming GEMV
 // for up to 8 rows per launch (K split over the grid; `part` holds splits * m * n floats
-// when splits > 1), and rocBLAS sgemm for more rows through a handle made by
-// f32w_blas_create (0 on success, else a rocBLAS status).
+// when splits > 1), and the matrix-core GEMM for more rows (K a multiple of
+// 4; no workspace).
+// rows above which F32 weights take the GEMM: at the LM head shape
+// (4096 x 151936) 9-16 rows take 0.55-0.64 ms on the 32-row GEMM tiles
+// against 0.97-1.11 ms for two GEMV launches; 8 rows 0.56 ms on one GEMV
+constexpr uint64_t kF32GemvMaxRows = 8;
 bool f32w_gemv_supported(const Image& im);
 uint32_t f32w_splits(const Image& im);
 hipError_t launch_f32w_gemv(const Image& im, const View& v, const float* x, uint32_t m, float* y, float* part,
                             uint32_t splits, hipStream_t st);
-int f32w_blas_create(void** handle);
-void f32w_blas_destroy(void* handle);
-int f32w_sgemm(void* handle, const Image& im, const View& v, const float* x, uint64_t m, float* y,
-               hipStream_t st);
+bool f32w_gemm_supported(const Image& im);
+hipError_t launch_f32w_gemm(const Image& im, const View& v, const float* x, uint64_t m, float* y, hipStream_t st);
 
 // Exact-order matmul: bit-identical to CpuScalar (any M, either layout).
 hipError_t launch_exact(const Image& im, const View& w, const float* x, uint64_t m, float* y,

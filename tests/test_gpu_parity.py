@@ -575,7 +575,7 @@ def test_gguf_upload_same_results(ctx, qtype):
 # ------------------------------------------- F32 weights (the dense matmul)
 #
 # backends/cpu/src/backend.rs:48-60 -> matmul.rs:92-117: W row-major [K, N]
-# f32. F32/AUTO mode: the streaming GEMV up to 16 rows, rocBLAS sgemm above;
+# f32. F32/AUTO mode: the streaming GEMV up to 16 rows, the f32 matrix-core GEMM above;
 # both judged by the F32 bars against CpuScalar's sequential f32 sums and the
 # f64 product.
 
@@ -601,14 +601,30 @@ def test_f32_weights_tolerance(ctx, m):
     assert wt.linear(x, qa.MODE_F32).tobytes() == y.tobytes()  # deterministic
 
 
+@pytest.mark.parametrize("k,n", [(1022, 1000), (4096, 260), (256, 4100)])
+def test_f32_weights_gemm_edges(ctx, k, n):
+    """K not a multiple of 4 (the GEMM's 16-byte x loads): 8-row GEMV chunks
+    instead; N past a tile boundary by 4 columns; 17-128 rows across the
+    GEMM's three tile heights."""
+    w = po.fill_normal(9830 + k, k * n, 0.02).reshape(k, n)
+    wt = ctx.weights(qa.F32, qa.ROW_MAJOR, k, n, w)
+    for m in (17, 33, 65, 128):
+        x = po.fill_normal(9831 + m, m * k).reshape(m, k)
+        y = wt.linear(x, qa.MODE_F32)
+        comp, norm = _f32w_checks(y, x, w)
+        assert comp <= F32_TOL and norm <= F32_TOL, (k, n, m, comp, norm)
+    wt.free()
+
+
 def test_f32_weights_lm_head_shape(ctx):
     """The unchanged runtime's LM head: [4096, 151936] f32 (a Q6_K head
     dequantized at load, runtime/src/qwen3/loader.rs:47-61), one decode row
-    (GEMV) and a 128-row prompt (sgemm), on sampled outputs rows."""
+    (GEMV) and 17, 128 and 512 rows (GEMM: the 32-, 128- and 128-row tiles),
+    on sampled outputs rows."""
     k, n = 4096, 151936
     w = po.fill_normal(9810, k * n, 0.02).reshape(k, n)
     wt = ctx.weights(qa.F32, qa.ROW_MAJOR, k, n, w)
-    for m in (1, 128):
+    for m in (1, 17, 128, 512):
         x = po.fill_normal(9811 + m, m * k).reshape(m, k)
         y = wt.linear(x, qa.MODE_AUTO)
         rows = np.array([0, m // 2, m - 1]) if m > 1 else np.array([0])

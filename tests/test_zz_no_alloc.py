@@ -39,6 +39,7 @@ CASES = [
     (qa.Q6_K, qa.OUTPUT_ROWS, 14336, 4096, 16, 9, qa.MODE_F32),      # Q6_K 2-16 rows: records and K parts
     (qa.Q4_0, qa.ROW_MAJOR, 4096, 4096, 9, 1, qa.MODE_F32),          # row-major GEMV with K-split partials
     (qa.Q4_K, qa.OUTPUT_ROWS, 512, 64, 5, 2, qa.MODE_EXACT),         # no workspace
+    (qa.F32, qa.ROW_MAJOR, 1024, 2000, 40, 12, qa.MODE_F32),          # F32 weights: GEMM, then GEMV K parts
 ]
 
 
@@ -47,8 +48,12 @@ def test_noalloc_equals_linear_device(ctx, case):
     from quantinfer_amd import hiprt
     qtype, layout, k, n, m1, m2, mode = case
     print(f"no-alloc case {case}", flush=True)
-    blocks = po.make_weights(qtype, k, n, seed=9500 + qtype, outliers=qtype >= qa.Q4_K) if layout == qa.OUTPUT_ROWS \
-        else po.make_weights(qtype, n, k, seed=9500 + qtype)
+    if qtype == qa.F32:
+        blocks = po.fill_normal(9500, k * n, 0.02).reshape(k, n)
+    elif layout == qa.OUTPUT_ROWS:
+        blocks = po.make_weights(qtype, k, n, seed=9500 + qtype, outliers=qtype >= qa.Q4_K)
+    else:
+        blocks = po.make_weights(qtype, n, k, seed=9500 + qtype)
     w = ctx.weights(qtype, layout, k, n, blocks)
     stream = hiprt.Stream()
     f = _noalloc()
