@@ -564,6 +564,167 @@ def cpu_simd_table(repeats: int = 3) -> dict:
             "host": host_cpu(), "kind": "port"}
 
 
+# ------------------------------------------------ every BASELINE config point
+
+# (BASELINE.json configs index, qtype, K, N, row counts) of the decode GEMV
+# points: configs[0] Q8_0 4096^2; configs[1] Q4_0 at the four Qwen3-8B
+# projection shapes; configs[2] Q4_K / Q5_K / Q6_K in both FFN orientations.
+GEMV_POINTS = ([(0, 1, 4096, 4096, (1,))] +
+               [(1, 2, k, n, (1, 4, 16)) for k, n in ((4096, 4096), (4096, 1024), (4096, 12288), (12288, 4096))] +
+               [(2, q, k, n, (1, 8)) for q in (3, 4, 5) for k, n in ((4096, 14336), (14336, 4096))])
+# the prefill GEMM, Q8_0 and Q4_K, M x (K, N)
+GEMM_POINTS = [(3, q, k, n, (128, 512, 2048)) for q in (1, 3)
+               for k, n in ((4096, 4096), (4096, 12288), (12288, 4096))]
+RIDGE_FLOP_PER_BYTE = MFMA_F16_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBPS * 1e9)
+
+
+class _OneCore:
+    """Pin this process to one host core for the CPU legs (the reference's
+    output-row kernels are single-threaded, backends/cpu/src/config.rs:59-67)."""
+
+    def __enter__(self):
+        try:
+            self.old = os.sched_getaffinity(0)
+            os.sched_setaffinity(0, {min(self.old)})
+        except (AttributeError, OSError):
+            self.old = None
+        return self
+
+    def __exit__(self, *exc):
+        if self.old is not None:
+            os.sched_setaffinity(0, self.old)
+
+
+def _median_s(fn, repeats: int) -> float:
+    times = []
+    for _ in range(repeats):
+        t = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t)
+    return statistics.median(times)
+
+
+def _cpu_point(qtype: int, k: int, n: int, m: int, blocks, unit: str, work: float) -> dict:
+    """CpuScalar (and, for Q8_0/Q4_0, the cpu-simd per-block dot, cpu-simd
+    lib.rs:179-204) on one pinned core over `rows` <= m activation rows,
+    scaled linearly to m rows (rows are independent, matmul.rs:146-158).
+    `work` is the point's bytes (GB/s) or flops (TFLOP/s)."""
+    from oracle import pyoracle as po
+
+    rows = m if m <= 4 else 2
+    x = normal(0x5EED8100 + m, rows * k).reshape(rows, k)
+    isa = 2 if po.simd_available(2) else (1 if po.simd_available(1) else 0)
+    legs = [("scalar", lambda: po.matmul_output_rows(qtype, x, blocks, n))]
+    if qtype in (1, 2) and isa:
+        legs.append(("simd", lambda: po.matmul_output_rows_simd(qtype, isa, x, blocks, n)))
+    out = {"unit": unit, "cores": 1, "kind": "port"}
+    with _OneCore():
+        for leg, fn in legs:
+            sec = _median_s(fn, 3 if rows * k * n <= 64 << 20 else 1) * m / rows
+            out[leg] = round(work / sec / (1e9 if unit == "GB/s" else 1e12), 6 if unit == "TFLOP/s" else 3)
+            out[leg + "_ms"] = round(sec * 1e3, 2)
+    if "simd" not in out:
+        out["simd"] = None
+    out["value"] = out["scalar"]
+    out["sample"] = (f"{rows} of {m} rows, scaled x{m // rows}" if rows < m else f"all {m} rows") + \
+        f"; oracle C port of CpuScalar (matmul.rs:119-160, :282-332)" + \
+        (f" and the cpu-simd {['', 'avx2', 'avx512f'][isa]} block dot" if len(legs) > 1 else
+         ("; no cpu-simd path for K-quants in the reference" if qtype >= 3 else "")) + \
+        f"; 1 pinned core of {host_cpu()}"
+    return out
+
+
+def _time_rotating(weights, m: int, k: int, n: int, mode: int, steps: int, warmup: int) -> float:
+    """Microseconds per linear_device call, rotating over resident weight
+    copies, HIP events on the launch stream."""
+    import quantinfer_amd as qa
+    from quantinfer_amd import hiprt
+
+    x = hiprt.DeviceBuffer.from_array(normal(0x5EED1000, m * k).reshape(m, k))
+    y = hiprt.DeviceBuffer(m * n * 4)
+    stream = hiprt.Stream()
+    calls = 0
+    for _ in range(warmup):
+        for w in weights:
+            w.linear_device(x.ptr, m, y.ptr, mode, stream.handle)
+    stream.synchronize()
+    start, end = hiprt.Event(), hiprt.Event()
+    start.record(stream)
+    for _ in range(steps):
+        for w in weights:
+            w.linear_device(x.ptr, m, y.ptr, mode, stream.handle)
+            calls += 1
+    end.record(stream)
+    stream.synchronize()
+    us = start.elapsed_ms(end) * 1e3 / calls
+    for b in (start, end):
+        b.destroy()
+    x.free()
+    y.free()
+    stream.destroy()
+    return us
+
+
+def configs_table(steps: int, warmup: int, with_cpu: bool) -> dict:
+    """Every BASELINE.json config point of the linear path, each with its
+    time per call, its rate against its roofline and (unless with_cpu is
+    false) the CPU kernels beside it. GEMV points: F32 mode, one call per
+    resident weight copy (copies >= 512 MB), GB/s of algorithmic bytes
+    against 8 TB/s. GEMM points: MFMA mode (f16 operands, f32 accumulation),
+    TFLOP/s against the attainable roofline min(2.5 PFLOP/s, intensity x
+    8 TB/s); weight copies rotated the same way."""
+    import quantinfer_amd as qa
+
+    ctx = qa.Context(0)
+    out = {"gemv": [], "gemm": []}
+    for kind, points in (("gemv", GEMV_POINTS), ("gemm", GEMM_POINTS)):
+        for cfg_i, qtype, k, n, ms in points:
+            blocks = weight_blocks(qtype, k, n, seed=0x5EED0000 + qtype)
+            wbytes = n * (k // BLOCK[qtype]) * WIRE[qtype]
+            copies = max(2, int(-(-512e6 // wbytes)))
+            weights = [ctx.weights(qtype, qa.OUTPUT_ROWS, k, n, blocks) for _ in range(copies)]
+            for m in ms:
+                abytes = algorithmic_bytes(qtype, k, n, m)
+                if kind == "gemv":
+                    us = _time_rotating(weights, m, k, n, qa.MODE_F32, steps, warmup)
+                    gbps = abytes / (us * 1e-6) / 1e9
+                    entry = {"config": cfg_i, "qtype": QNAME[qtype], "m": m, "k": k, "n": n,
+                             "us": round(us, 3), "gbps": round(gbps, 1),
+                             "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS,
+                                          "unit": "GB/s", "frac": round(gbps / HBM_PEAK_GBPS, 4),
+                                          "algorithmic_bytes": abytes}}
+                    if with_cpu:
+                        entry["cpu_baseline"] = _cpu_point(qtype, k, n, m, blocks, "GB/s", abytes)
+                else:
+                    reps = max(3, steps // 2) if m >= 2048 else steps
+                    us = _time_rotating(weights, m, k, n, qa.MODE_MFMA, reps, max(2, warmup))
+                    flops = 2.0 * m * n * k
+                    tflops = flops / (us * 1e-6) / 1e12
+                    intensity = flops / abytes
+                    attainable = min(MFMA_F16_PEAK_TFLOPS, intensity * HBM_PEAK_GBPS / 1e3)
+                    entry = {"config": cfg_i, "qtype": QNAME[qtype], "m": m, "k": k, "n": n,
+                             "us": round(us, 2), "tflops": round(tflops, 1),
+                             "roofline": {"bound": "mfma" if intensity >= RIDGE_FLOP_PER_BYTE else "hbm",
+                                          "achieved": round(tflops, 1), "peak": round(attainable, 1),
+                                          "unit": "TFLOP/s", "frac": round(tflops / attainable, 4),
+                                          "frac_of_f16_peak": round(tflops / MFMA_F16_PEAK_TFLOPS, 4),
+                                          "intensity_flop_per_byte": round(intensity, 1)}}
+                    if with_cpu:
+                        entry["cpu_baseline"] = _cpu_point(qtype, k, n, m, blocks, "TFLOP/s", flops)
+                out[kind].append(entry)
+                print(f"bench configs: {kind} {QNAME[qtype]} M={m} K={k} N={n}: "
+                      f"{entry['us']} us, frac {entry['roofline']['frac']}", file=sys.stderr, flush=True)
+            for w in weights:
+                w.free()
+    out["device"] = ctx.device_name()
+    ctx.close()
+    out["note"] = ("GEMV: F32 mode, us per call over resident weight copies (>= 512 MB); GEMM: MFMA mode, "
+                   "f16 activation conversion + GEMM per call; roofline.frac of the GEMM is against "
+                   "min(f16 peak, intensity x HBM peak); cpu_baseline: scalar CpuScalar port and, for "
+                   "Q8_0/Q4_0, the cpu-simd block dot, one pinned core, in the unit of the point")
+    return out
+
+
 # --------------------------------------------------------------- e2e decode
 
 E2E_PROMPT, E2E_NEW = 512, 128
@@ -737,7 +898,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="time device-to-device copies of 256 MiB instead (counter calibration)")
-    ap.add_argument("--workload", choices=["gemv", "gemm", "e2e", "f32head", "calib", "timeline", "libgemm"],
+    ap.add_argument("--workload", choices=["gemv", "gemm", "e2e", "f32head", "configs", "calib", "timeline",
+                                           "libgemm"],
                     default="gemv",
                     help="gemv: the headline decode GEMV with the Q8_0 GEMV, the GEMMs and the e2e "
                          "decode line embedded (default); gemm: one MFMA prefill GEMM; e2e: "
@@ -746,6 +908,12 @@ def main():
                          "libgemm: the GEMM shape as a plain f16 library GEMM, for scale")
     ap.add_argument("--no-e2e", action="store_true", help="gemv: leave out the e2e decode run")
     ap.add_argument("--no-gemm", action="store_true", help="gemv: leave out the GEMM objects")
+    ap.add_argument("--no-abi", action="store_true",
+                    help="gemv: leave out the through-ABI calls (host buffers), so a kernel trace holds "
+                         "only the timed device launches")
+    ap.add_argument("--no-f32head", action="store_true", help="gemv: leave out the F32 LM-head object")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="gemv: leave out the table of every BASELINE config point")
     ap.add_argument("--cpu-simd", action="store_true",
                     help="only the CPU table: scalar and cpu-simd Q8_0/Q4_0 kernels, one core")
     ap.add_argument("--qtype", default="q4_k", help="gemv/gemm: q8_0, q4_0, q4_k, q5_k or q6_k")
@@ -771,6 +939,9 @@ def main():
     if args.workload == "e2e":
         print(json.dumps(e2e_bench(with_cpu=not args.no_cpu)))
         return
+    if args.workload == "configs":
+        print(json.dumps(configs_table(args.steps, args.warmup, not args.no_cpu)))
+        return
     if args.workload == "f32head":
         print(json.dumps(f32_head_bench(args.steps, args.warmup)))
         return
@@ -791,12 +962,12 @@ def main():
         return
 
     m, k, n = (int(v) for v in (args.mkn or f"{M},{K},{N}").split(","))
-    g = gemv_bench(qt, k, n, m, args.steps, args.warmup, with_abi=True)
+    g = gemv_bench(qt, k, n, m, args.steps, args.warmup, with_abi=not args.no_abi)
     line = gemv_line(qt, k, n, m, g, args.steps, args.warmup)
     line["metric"] = "quant GEMV GB/s (% of HBM peak) at 4096x14336; Qwen3-8B-shape decode tok/s"
     line["cpu_baseline"] = None if args.no_cpu or (m, k, n) != (M, K, N) else cpu_baseline(qt)
     abytes = algorithmic_bytes(qt, k, n, m)
-    line["through_abi"] = {
+    line["through_abi"] = None if args.no_abi else {
         "value": round(abytes / (g["abi_ms"] * 1e-3) / 1e9, 2), "unit": "GB/s",
         "ms_per_call": round(g["abi_ms"], 5), "calls": g["abi_calls"],
         "note": "qi_hip_linear with host x and y (H2D, GEMV, D2H, synchronous): the "
@@ -805,11 +976,17 @@ def main():
     if (qt, m, k, n) == (3, M, K, N):
         g8 = gemv_bench(1, K, N, M, args.steps, args.warmup)
         line["gemv_q8_0"] = gemv_line(1, K, N, M, g8, args.steps, args.warmup)
-        line["f32_matmul_head"] = f32_head_bench(args.steps, args.warmup)
+        if not args.no_cpu:
+            line["gemv_q8_0"]["cpu_baseline"] = _cpu_point(1, K, N, M, weight_blocks(1, K, N, seed=0x5EED0001),
+                                                           "GB/s", algorithmic_bytes(1, K, N, M))
+        if not args.no_f32head:
+            line["f32_matmul_head"] = f32_head_bench(args.steps, args.warmup)
         if not args.no_gemm:
             # the GEMM objects take their own counts: 20 warm-up calls (about
             # 6 ms, so that the clocks settle) and 50 timed ones
             line["gemm"] = {QNAME[q]: gemm_bench(q, 2048, 4096, 12288, 50, 20) for q in (3, 1)}
+        if not args.no_configs:
+            line["configs"] = configs_table(min(args.steps, 10), min(args.warmup, 3), not args.no_cpu)
         if not args.no_e2e:
             line["e2e"] = e2e_bench(with_cpu=not args.no_cpu)
     print(json.dumps(line))
