@@ -174,6 +174,16 @@ struct LinearPlan {
   uint64_t h_floats = 0, s_floats = 0, d_floats = 0;  // f16 activations, partials, records
 };
 
+// Rows of a chunk at which the 2-16 row GEMV switches from the int8-digit
+// kernel (qi_gemv_rows.hip) to the split-half kernel (qi_gemv_half.hip): the
+// digit kernel's work grows with the row count (a matrix instruction and a
+// combine per four rows and window), the split-half kernel's does not (all 16
+// rows in one f16 instruction per window half). Measured on MI355X, us per
+// call, digit / split-half: Q4_K 4096x14336 M=2 12.5 / 14.8, M=8 17.7 / 17.1,
+// M=16 29.5 / 23.8; Q4_0 12288x4096 M=4 16.6 / 18.0, M=16 28.1 / 22.9; Q4_K
+// 4096x24576 M=16 49.6 / 38.3.
+constexpr uint32_t kHalfMinRows = 9;
+
 qi_hip_status plan_linear(const Image& im, uint64_t m, int32_t mode, LinearPlan* p) {
   if (mode < QI_HIP_MODE_AUTO || mode > QI_HIP_MODE_MFMA)
     return fail(QI_HIP_INVALID_INPUT, "unknown arithmetic mode");
@@ -218,16 +228,18 @@ qi_hip_status plan_linear(const Image& im, uint64_t m, int32_t mode, LinearPlan*
   if (mode != QI_HIP_MODE_EXACT && qi::gemv_mfma_supported(im.qtype, im.layout, im.k)) {
     p->kind = LinearPlan::kMfma;
     if (m >= 2) {
-      // two or more rows, dense operands (launch_gemv_rows, the same formats
-      // and shapes as the one-row kernel): one kernel per 16-row chunk; K parts
-      // only for shapes with few tiles, by the chunk's row count (a shorter
-      // last chunk may take a different count; enqueue_linear asks again)
+      // two or more rows (launch_gemv_half, the same formats and shapes as
+      // the one-row kernel): one kernel per 16-row chunk; K parts only for
+      // shapes with few tiles, by the chunk's row count (a shorter last chunk
+      // may take a different count; enqueue_linear asks again)
       uint64_t floats = 0, records = 0;
       for (uint64_t r : {static_cast<uint64_t>(m < 16 ? m : 16), m > 16 ? m % 16 : 0}) {
         if (r < 2) continue;
-        const uint32_t pr = qi::gemv_rows_splits(im.k, im.n, static_cast<uint32_t>(r));
+        const uint32_t rr = static_cast<uint32_t>(r);
+        const bool half = rr >= kHalfMinRows;
+        const uint32_t pr = half ? qi::gemv_half_splits(im.k, im.n, rr) : qi::gemv_rows_splits(im.k, im.n, rr);
         if (pr > 1) floats = std::max(floats, static_cast<uint64_t>(pr) * r * im.n);
-        records = std::max(records, qi::gemv_rows_records_bytes(im.k, im.n, static_cast<uint32_t>(r)));
+        if (half) records = std::max(records, qi::gemv_half_records_bytes(im.k));
       }
       p->splits = 1;
       p->s_floats = floats;
@@ -282,14 +294,23 @@ qi_hip_status enqueue_linear(const qi_hip_weights* w, const LinearPlan& p, const
         if (p.kind == LinearPlan::kMfma && rows >= 2) {
           const float* xc = x + m0 * im.k;
           float* const yc = y + m0 * im.n;
-          const uint32_t parts = qi::gemv_rows_splits(im.k, im.n, static_cast<uint32_t>(rows));
-          const uint8_t* records = nullptr;
-          if (qi::gemv_rows_records(im.k, im.n, static_cast<uint32_t>(rows))) {
-            QI_HIP_TRY(qi::launch_gemv_rows_records(xc, im.k, rows, reinterpret_cast<uint8_t*>(dws), st),
+          const uint32_t rr = static_cast<uint32_t>(rows);
+          if (rr >= kHalfMinRows) {
+            const uint32_t parts = qi::gemv_half_splits(im.k, im.n, rr);
+            QI_HIP_TRY(qi::launch_gemv_half_records(xc, im.k, rows, reinterpret_cast<uint8_t*>(dws), st),
                        "launch gemv rows activation records");
-            records = reinterpret_cast<const uint8_t*>(dws);
+            QI_HIP_TRY(qi::launch_gemv_half(im.qtype, im.wide != 0, v, xc, rows, yc, sws, parts,
+                                            reinterpret_cast<const uint8_t*>(dws), st),
+                       "launch gemv rows");
+            if (parts > 1) {
+              const uint64_t count = static_cast<uint64_t>(rows) * im.n;
+              QI_HIP_TRY(qi::launch_splitk_sum(im, v, sws, parts, count, count, yc, xc, st),
+                         "launch gemv split-K sum");
+            }
+            continue;
           }
-          QI_HIP_TRY(qi::launch_gemv_rows(im.qtype, im.wide != 0, v, xc, rows, yc, sws, parts, records, st),
+          const uint32_t parts = qi::gemv_rows_splits(im.k, im.n, rr);
+          QI_HIP_TRY(qi::launch_gemv_rows(im.qtype, im.wide != 0, v, xc, rows, yc, sws, parts, st),
                      "launch gemv rows");
           if (parts > 1) {
             const uint64_t count = static_cast<uint64_t>(rows) * im.n;

@@ -1,0 +1,672 @@
+// Decode GEMV of 2-16 activation rows on the f16 matrix cores
+// (v_mfma_f32_16x16x32_f16), output-rows layout, K a multiple of 256; one
+// kernel per call (K parts over the grid only for shapes with few tiles).
+//
+// Arithmetic ("split halves"). Per (row, unit of 256 elements) the
+// activations are scaled by a power of two 2^s that brings the unit's largest
+// |x| just under 2^15, and each scaled value x' is held as two f16 numbers,
+// hi = f16(x') and lo = f16(x' - hi), which carry 22 significant bits of it.
+// The weight codes enter the matrix cores as exact small f16 integers,
+// centred: q - z with z the middle of the code range (Q4_0 8, Q6_K 32), a
+// zero point per (output, window) for Q4_K / Q5_K (the integer nearest b / a),
+// Q8_0's signed codes as they are. All products are exact in f32; per
+// (row, window of 32, output), with w = a q - b,
+//   sum_k x'_k w_k = a * (C_hi + C_lo) - (b - z a) * sum_k x'_k,
+// where C_hi / C_lo are the matrix-core sums of the two halves against the
+// centred codes. The window scale a is applied by one f32 fma per window and
+// output; the offsets (b - z a) * sum x' of a unit's eight windows go through
+// two f32 matrix instructions (v_mfma_f32_16x16x4_f32: window sums x
+// per-output offsets); the unit's sum is multiplied by 2^-s once. Q6_K's
+// 16-element sub-blocks (two per window) take two instructions per half, each
+// with the other sub-block's codes zeroed, weighted by their own int8 scales.
+// The rounding is that of f32 sums of exact products, plus x to 22 bits:
+// within the 1e-5 bars of the f32 GEMV at every K (no cancellation: the
+// centred codes leave an offset of at most a / 2 for the K-quants).
+//
+// Operands. One 16x16x32 instruction covers one window for all 16 rows (A:
+// lane (m, g) = lane m + 16 g supplies 8 values of row m, k-slots 8g..8g+7)
+// and the tile's 16 outputs (B: lane (n, g) supplies output n's codes of the
+// same slots); lane (n, g) receives rows 4g..4g+3 of output n. The weight
+// record gives lane group g two whole windows of its output; the B operand
+// needs slice g of every window, so the code words are transposed across the
+// four lane groups with v_permlane32_swap / v_permlane16_swap, and the window
+// scales and zero points, decoded by their owning lane group, are gathered the
+// same way. A 16-bit pair of the B operand is made from two code bytes with
+// one v_and_or_b32 (the code in the low mantissa bits under the exponent of
+// 1024: 1024 + q, or 1024 + 16 q for a high nibble) and centred with one
+// packed f16 add or fma (exact: integers below 2048); the slots of a lane
+// group hold elements (0, 2), (1, 3), (4, 6), (5, 7) of its slice in that
+// order, and the activation halves are stored in the same order.
+//
+// Work split: a workgroup is 16 wavefronts, 4 tiles of 16 outputs x 4 K
+// slices (or, for shapes of up to one tile per CU, one tile x 16 K slices,
+// so that no K part leaves the workgroup). The workgroup converts the
+// activations of its K range for all rows into LDS (chunk by chunk when they
+// do not fit), each wavefront streams its tile's units of its slice, and the
+// slices are summed in order through LDS. The activation loads are waited for
+// before the weight loads are issued (vector loads complete in order), so the
+// weights' HBM latency overlaps the conversion. No state is shared between
+// workgroups. Rows past M hold zeros and are never stored. A NaN or infinite
+// activation (or a sum of |x| that overflows) makes its (row, unit) scale NaN,
+// so every output of the row comes out non-finite and is recomputed in the
+// reference's order.
+#include "qi_device.h"
+#include "qi_internal.h"
+#include "qi_unit.h"
+
+namespace qi {
+
+namespace {
+
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+
+constexpr int kHThreads = 1024;  // 16 wavefronts
+constexpr int kHWaves = 16;
+constexpr uint32_t kHCUs = 256;  // compute units of an MI355X (gfx950)
+constexpr int kHRows = 16;      // rows of the A operand (9-16 activation rows)
+
+// LDS of a chunk of `cu` units for MR rows: the halves [unit][window][half]
+// [row][lane group] x 16 B, then the window sums [unit][row][window] and the
+// unscales 2^-s [unit][row] as f32.
+constexpr uint32_t half_lds(int mr, uint32_t cu) { return cu * static_cast<uint32_t>(mr) * (1024 + 32 + 4); }
+constexpr uint32_t half_chunk_cap(int mr) { return 128 / static_cast<uint32_t>(mr); }
+static_assert(half_lds(16, 8) <= 160 * 1024 && half_lds(4, 32) <= 160 * 1024, "chunks fit LDS");
+
+__device__ __forceinline__ void xpose4(uint32_t r[4]) {
+  const auto a = __builtin_amdgcn_permlane32_swap(r[0], r[2], false, false);
+  const auto b = __builtin_amdgcn_permlane32_swap(r[1], r[3], false, false);
+  const auto c = __builtin_amdgcn_permlane16_swap(a[0], b[0], false, false);
+  const auto d = __builtin_amdgcn_permlane16_swap(a[1], b[1], false, false);
+  r[0] = c[0];
+  r[1] = c[1];
+  r[2] = d[0];
+  r[3] = d[1];
+}
+
+// All-gather across the lane groups: v is V[g] in lane group g; out[g'] = V[g'].
+__device__ __forceinline__ void gather4u(uint32_t u, uint32_t out[4]) {
+  const auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  const auto b = __builtin_amdgcn_permlane32_swap(a[0], a[0], false, false);
+  const auto c = __builtin_amdgcn_permlane32_swap(a[1], a[1], false, false);
+  out[0] = b[0];
+  out[1] = c[0];
+  out[2] = b[1];
+  out[3] = c[1];
+}
+
+__device__ __forceinline__ uint32_t h2u(h2 v) { return __builtin_bit_cast(uint32_t, v); }
+__device__ __forceinline__ h2 u2h(uint32_t v) { return __builtin_bit_cast(h2, v); }
+// (a & m) | o in one v_and_or_b32: m from a scalar register, o from a vector
+// register (gfx950 reads one scalar operand per VALU instruction, so with both
+// constants scalar the compiler splits it in two)
+__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t m, uint32_t o) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "s"(m), "v"(o));
+  return r;
+}
+// centre a pair: v + c (exact on the integers these hold)
+__device__ __forceinline__ uint32_t pk_add(uint32_t v, h2 c) { return h2u(u2h(v) + c); }
+// centre a pair of 1024 + 16 q / 1024 + 4 q: v * s + c (exact likewise)
+__device__ __forceinline__ uint32_t pk_fma(uint32_t v, h2 s, h2 c) {
+  return h2u(__builtin_elementwise_fma(u2h(v), s, c));
+}
+// keep a value computed where it stands (an empty asm the compiler cannot move work across)
+__device__ __forceinline__ void pin(v4f& v) {
+  float a = v[0], b = v[1], c = v[2], d = v[3];
+  asm volatile("" : "+v"(a), "+v"(b), "+v"(c), "+v"(d));
+  v = v4f{a, b, c, d};
+}
+__device__ __forceinline__ h2 splat(float f) { return h2{static_cast<_Float16>(f), static_cast<_Float16>(f)}; }
+
+constexpr uint32_t kExp1024 = 0x64006400u;  // f16 1024.0 in both halves
+
+// B operand of one window from a slice's two code words: lo (elements 0..3),
+// hi (elements 4..7), one code per byte in its low nibble (kMaskLo) or high
+// nibble (kMaskHi), or as a whole byte (kMaskByte).
+constexpr uint32_t kMaskLo = 0x000F000Fu, kMaskHi = 0x00F000F0u, kMaskByte = 0x00FF00FFu;
+template <uint32_t MASK>
+__device__ __forceinline__ void raw_pairs(uint32_t lo, uint32_t hi, uint32_t lo8, uint32_t hi8, uint32_t out[4]) {
+  out[0] = and_or(lo, MASK, kExp1024);   // elements 0, 2
+  out[1] = and_or(lo8, MASK, kExp1024);  // 1, 3
+  out[2] = and_or(hi, MASK, kExp1024);   // 4, 6
+  out[3] = and_or(hi8, MASK, kExp1024);  // 5, 7
+}
+
+// Per-format weight access of one unit: load() the record bytes (the
+// one-row kernel's loaders), prepare() the transposes, then for window w the
+// centred f16 codes of slice g and, from the scales, the window's factor and
+// offset.
+template <int QT>
+struct Half;
+
+template <>
+struct Half<kQ8_0> {
+  using U = Unit<kQ8_0>;
+  static constexpr bool kOffset = false;
+  struct T {
+    uint32_t lo[2][4], hi[2][4];
+  };
+  __device__ static void prepare(const U::Raw& r, T& t) {
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      t.lo[b][0] = r.q[2 * b].x; t.lo[b][1] = r.q[2 * b].z; t.lo[b][2] = r.q[2 * b + 1].x; t.lo[b][3] = r.q[2 * b + 1].z;
+      t.hi[b][0] = r.q[2 * b].y; t.hi[b][1] = r.q[2 * b].w; t.hi[b][2] = r.q[2 * b + 1].y; t.hi[b][3] = r.q[2 * b + 1].w;
+      xpose4(t.lo[b]);
+      xpose4(t.hi[b]);
+    }
+  }
+  // signed bytes s: 1024 + (s ^ 128) - 1152 = s
+  __device__ static void codes(const T& t, int w, uint32_t out[4]) {
+    const uint32_t lo = t.lo[w & 1][w >> 1] ^ 0x80808080u, hi = t.hi[w & 1][w >> 1] ^ 0x80808080u;
+    raw_pairs<kMaskByte>(lo, hi, lo >> 8, hi >> 8, out);
+    const h2 c = splat(-1152.0f);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) out[i] = pk_add(out[i], c);
+  }
+};
+
+template <>
+struct Half<kQ4_0> {
+  using U = Unit<kQ4_0>;
+  static constexpr bool kOffset = false;
+  static constexpr uint32_t kM = 0x0F0F0F0Fu;
+  struct T {
+    uint32_t w[2][4];
+  };
+  // block 2g + b in q[b] (byte i = element i | element i+16 << 4); slice s as
+  // one word, byte k = element 8s+k | element 8s+4+k << 4
+  __device__ static void prepare(const U::Raw& r, T& t) {
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      const uint4 q = r.q[b];
+      t.w[b][0] = (q.x & kM) | ((q.y << 4) & ~kM);
+      t.w[b][1] = (q.z & kM) | ((q.w << 4) & ~kM);
+      t.w[b][2] = ((q.x >> 4) & kM) | (q.y & ~kM);
+      t.w[b][3] = ((q.z >> 4) & kM) | (q.w & ~kM);
+      xpose4(t.w[b]);
+    }
+  }
+  __device__ static void codes(const T& t, int w, uint32_t out[4]) {
+    const uint32_t v = t.w[w & 1][w >> 1], v8 = v >> 8;
+    out[0] = pk_add(and_or(v, kMaskLo, kExp1024), splat(-1032.0f));                     // elements 0, 2: q - 8
+    out[1] = pk_add(and_or(v8, kMaskLo, kExp1024), splat(-1032.0f));                    // 1, 3
+    out[2] = pk_fma(and_or(v, kMaskHi, kExp1024), splat(0.0625f), splat(-72.0f));       // 4, 6: (1024 + 16q) / 16 - 72
+    out[3] = pk_fma(and_or(v8, kMaskHi, kExp1024), splat(0.0625f), splat(-72.0f));      // 5, 7
+  }
+};
+
+// Q4_K / Q5_K: lane group g holds code bytes [32g, 32g+32) of the super-block,
+// bytes 8s..8s+7 carrying slice s of window 2g (low nibbles) and 2g+1 (high
+// nibbles); Q5_K adds bit w of qh byte e as bit 4 of element e of window w
+// (RowsUnit<kQ5_K> loads qh bytes 8g..8g+7: slice g of every window).
+template <bool FIVE>
+struct HalfQ45K {
+  using U = RowsUnit<FIVE ? kQ5_K : kQ4_K>;
+  static constexpr bool kOffset = true;
+  struct T {
+    uint32_t lo[4], hi[4];
+    uint32_t hl, hh;
+  };
+  __device__ static void prepare(const typename U::Raw& r, T& t) {
+    t.lo[0] = r.q[0].x; t.lo[1] = r.q[0].z; t.lo[2] = r.q[1].x; t.lo[3] = r.q[1].z;
+    t.hi[0] = r.q[0].y; t.hi[1] = r.q[0].w; t.hi[2] = r.q[1].y; t.hi[3] = r.q[1].w;
+    xpose4(t.lo);
+    xpose4(t.hi);
+    if constexpr (FIVE) {
+      t.hl = r.hl;
+      t.hh = r.hh;
+    } else {
+      t.hl = t.hh = 0;
+    }
+  }
+  // c0 = -(1024 + z) (low-nibble windows), c1 = -(64 + z) (high): codes q - z
+  __device__ static void codes(const T& t, int w, h2 c, uint32_t out[4]) {
+    const int gp = w >> 1;
+    const uint32_t lo = t.lo[gp], hi = t.hi[gp];
+    if ((w & 1) == 0) {
+      raw_pairs<kMaskLo>(lo, hi, lo >> 8, hi >> 8, out);
+      if constexpr (FIVE) {
+        // bit w of each qh byte to bit 4 of its half (1024 + q + 16 * bit)
+        const uint32_t l = t.hl >> w, h = t.hh >> w;
+        out[0] |= (l << 4) & 0x00100010u;
+        out[1] |= (l >> 4) & 0x00100010u;
+        out[2] |= (h << 4) & 0x00100010u;
+        out[3] |= (h >> 4) & 0x00100010u;
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) out[i] = pk_add(out[i], c);
+    } else {
+      raw_pairs<kMaskHi>(lo, hi, lo >> 8, hi >> 8, out);
+      if constexpr (FIVE) {
+        // bit w to bit 8 (1024 + 16 (q + 16 * bit))
+        const uint32_t l = t.hl >> w, h = t.hh >> w;
+        out[0] |= (l << 8) & 0x01000100u;
+        out[1] |= l & 0x01000100u;
+        out[2] |= (h << 8) & 0x01000100u;
+        out[3] |= h & 0x01000100u;
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) out[i] = pk_fma(out[i], splat(0.0625f), c);
+    }
+  }
+};
+template <>
+struct Half<kQ4_K> : HalfQ45K<false> {};
+template <>
+struct Half<kQ5_K> : HalfQ45K<true> {};
+
+// Q6_K: lane group g' = 2ip + c holds ql bytes [64ip + 32c, +32); window
+// w = 4ip + 2hf + c is their low (hf = 0) or high (hf = 1) nibbles, its two
+// high bits bits 2c + 4hf of qh bytes 32ip + 8g..8g+7 (RowsUnit<kQ6_K>).
+template <>
+struct Half<kQ6_K> {
+  using U = RowsUnit<kQ6_K>;
+  struct T {
+    uint32_t lo[4], hi[4];
+    uint32_t h[4];
+  };
+  __device__ static void prepare(const U::Raw& r, T& t) {
+    t.lo[0] = r.q[0].x; t.lo[1] = r.q[0].z; t.lo[2] = r.q[1].x; t.lo[3] = r.q[1].z;
+    t.hi[0] = r.q[0].y; t.hi[1] = r.q[0].w; t.hi[2] = r.q[1].y; t.hi[3] = r.q[1].w;
+    xpose4(t.lo);
+    xpose4(t.hi);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) t.h[i] = r.h[i];
+  }
+  // 4q in each byte (nibble to bits 2-5, high bits to 6-7), as 1024 + 4q pairs
+  __device__ static void raw(const T& t, int w, uint32_t out[4]) {
+    const int ip = w >> 2, hf = (w >> 1) & 1, c = w & 1, gp = 2 * ip + c;
+    const int up = 6 - 2 * c - 4 * hf;
+    const uint32_t lo = (((hf ? t.lo[gp] >> 2 : t.lo[gp] << 2)) & 0x3C3C3C3Cu) | ((t.h[2 * ip] << up) & 0xC0C0C0C0u);
+    const uint32_t hi = (((hf ? t.hi[gp] >> 2 : t.hi[gp] << 2)) & 0x3C3C3C3Cu) | ((t.h[2 * ip + 1] << up) & 0xC0C0C0C0u);
+    raw_pairs<kMaskByte>(lo, hi, lo >> 8, hi >> 8, out);
+  }
+};
+
+struct HalfArgs {
+  View w;
+  const float* x;  // [m, k]
+  float* y;        // [m, n]
+  int m;
+  uint32_t chunk_units;  // units per LDS chunk
+  uint32_t part_units;   // units per K part (grid.y)
+  float* part;           // [grid.y][m][n] when grid.y > 1
+  const uint8_t* rec;    // the call's activation records (half_prep_kernel)
+  const float* rsum;     // their window sums, then unscales
+};
+
+// Convert one item (window w, slice g of one (row, unit)) of the values v[8]
+// (zeros past M): the (row, unit) scale from its 32 items (the 32 lanes of a
+// half wavefront), the window sum from its 4 items (adjacent lanes), the
+// halves in the operand order. Every lane takes part.
+__device__ __forceinline__ void half_convert(const float v[8], uint8_t* hi_slot, uint8_t* lo_slot, float* xsum_w,
+                                             float* unsc_mu, uint32_t w, uint32_t g) {
+  // the (row, unit) max over the 32 lanes: 16-lane rows by DPP, then the
+  // pair of rows (a NaN is passed over here; it reaches the sums below)
+  float mx = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) mx = fmaxf(mx, fabsf(v[j]));
+  mx = fmaxf(mx, dpp_move<0x121>(mx));  // row_ror:1
+  mx = fmaxf(mx, dpp_move<0x122>(mx));  // row_ror:2
+  mx = fmaxf(mx, dpp_move<kDppRor4>(mx));
+  mx = fmaxf(mx, dpp_move<kDppRor8>(mx));
+  {
+    const auto p = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, mx), __builtin_bit_cast(uint32_t, mx),
+                                                    false, false);
+    mx = fmaxf(__builtin_bit_cast(float, static_cast<uint32_t>(p[0])), __builtin_bit_cast(float, static_cast<uint32_t>(p[1])));
+  }
+  // max |x| * 2^sh < 2^15, bounded so that 2^-sh stays a normal f32. A NaN
+  // or infinite activation is not caught here: it stays non-finite through
+  // the halves and the matrix sums (inf * 0 is NaN), so every output of its
+  // row is non-finite and the epilogue recomputes it in the reference's order.
+  const int e = __builtin_isfinite(mx) && mx > 0.0f ? __builtin_amdgcn_frexp_expf(mx) : 0;
+  const int sh = min(15 - e, 125);
+  const float scale = __builtin_bit_cast(float, static_cast<uint32_t>(127 + sh) << 23);  // 2^sh
+  // hi: x' truncated to 11 significant bits (exact in f16 in this range); lo:
+  // the rest, exactly x' - hi in f32, rounded to f16
+  constexpr int kOrd[8] = {0, 2, 1, 3, 4, 6, 5, 7};  // operand order: (0, 2), (1, 3), (4, 6), (5, 7)
+  float xh[8], xl[8], sum = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const float xs = v[kOrd[j]] * scale;
+    xh[j] = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, xs) & 0xFFFFE000u);
+    xl[j] = xs - xh[j];
+    sum += xs;
+  }
+  uint32_t hi[4], lo[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    hi[j] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(xh[2 * j], xh[2 * j + 1]));  // exact
+    lo[j] = h2u(h2{static_cast<_Float16>(xl[2 * j]), static_cast<_Float16>(xl[2 * j + 1])});
+  }
+  // the window's four slices are lanes 4w'..4w'+3
+  sum += dpp_move<kDppSwap1>(sum);
+  sum += dpp_move<0x4E>(sum);  // quad_perm [2, 3, 0, 1]
+  *reinterpret_cast<uint4*>(hi_slot) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+  *reinterpret_cast<uint4*>(lo_slot) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+  if (g == 0) *xsum_w = sum;
+  if (g == 0 && w == 0) *unsc_mu = __builtin_bit_cast(float, static_cast<uint32_t>(127 - sh) << 23);  // 2^-sh
+}
+
+// The call's activation records, built once by half_prep_kernel: for all
+// K / 256 units, the halves [unit][window][half][row < MR][lane group] x 16 B,
+// then the window sums [unit][row][window] and the unscales [unit][row] (f32)
+// -- the LDS layout of a chunk, so that a chunk is three contiguous copies.
+constexpr uint64_t half_records_size(uint64_t units, int mr) {
+  return units * static_cast<uint64_t>(mr) * (1024 + 32 + 4);
+}
+
+// One (row, unit) per 32 threads: item r = 4 w + g of the 32.
+template <int MR>
+__global__ __launch_bounds__(256) void half_prep_kernel(const float* __restrict__ x, uint32_t K, int M,
+                                                        uint8_t* __restrict__ rec) {
+  const uint32_t units = K / 256;
+  const uint32_t pair = blockIdx.x * 8 + (threadIdx.x >> 5);  // u * MR + m
+  const uint32_t r = threadIdx.x & 31, w = r >> 2, g = r & 3;
+  // whole half-wavefronts are in or out (the lane moves stay within them)
+  if (pair >= units * MR) return;
+  const uint32_t u = pair / MR, m = pair % MR;
+  float4 v0 = make_float4(0.0f, 0.0f, 0.0f, 0.0f), v1 = v0;
+  if (static_cast<int>(m) < M) {
+    const float4* p = reinterpret_cast<const float4*>(x + static_cast<uint64_t>(m) * K + u * 256 + 32 * w + 8 * g);
+    v0 = p[0];
+    v1 = p[1];
+  }
+  const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+  uint8_t* const hs = rec + ((((u * 8 + w) * 2) * MR + m) * 4 + g) * 16;
+  float* const xsum = reinterpret_cast<float*>(rec + static_cast<uint64_t>(units) * MR * 1024);
+  float* const unsc = xsum + units * MR * 8;
+  half_convert(v, hs, hs + MR * 64, xsum + pair * 8 + w, unsc + pair, w, g);
+}
+
+// MR rows held (M <= MR), D units of weights in flight per wavefront, TL
+// tiles per workgroup (4, or 1 with 16 K slices).
+template <int QT, bool WIDE, int MR, int D, int TL>
+__global__ __launch_bounds__(kHThreads) void gemv_half_kernel(HalfArgs a) {
+  constexpr int SL = kHWaves / TL;  // K slices per tile
+  using H = Half<QT>;
+  using U = typename H::U;
+  constexpr Record R = record_geometry(QT, WIDE);
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  const uint32_t cu = a.chunk_units;
+  uint8_t* const planes = lds;
+  float* const xsum = reinterpret_cast<float*>(lds + cu * MR * 1024);
+  float* const unsc = xsum + cu * MR * 8;
+
+  const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const uint32_t sw = wave % SL, wc = wave / SL;
+  const uint32_t col = lane & 15, g = lane >> 4;
+  const uint32_t tile_raw = blockIdx.x * TL + wc;
+  const uint32_t tile = min(tile_raw, a.w.tiles - 1);
+  const uint32_t units_total = a.w.units;
+  const uint8_t* const trec = a.w.qs + static_cast<uint64_t>(tile) * units_total * R.bytes;
+  const uint32_t K = static_cast<uint32_t>(a.w.k);
+  const int M = a.m;
+  const uint32_t u_lo = blockIdx.y * a.part_units;
+  const uint32_t u_hi = min(units_total, u_lo + a.part_units);
+
+  v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  typename U::Raw ring[D];
+
+  for (uint32_t ku0 = u_lo; ku0 < u_hi; ku0 += cu) {
+    const uint32_t units = min(cu, u_hi - ku0);
+    const uint32_t u_begin = (units * sw) / SL;
+    const uint32_t u_count = (units * (sw + 1)) / SL - u_begin;
+    if (ku0 != u_lo) __syncthreads();  // the previous chunk is consumed
+
+    // ---- the chunk's activation records (half_prep_kernel): the halves
+    // by 1 KB global-to-LDS copies, the window sums and unscales by 256 B
+    // ones
+    const uint8_t* const src = a.rec + static_cast<uint64_t>(ku0) * MR * 1024;
+    const uint32_t kb = units * MR;  // KB of halves
+    for (uint32_t j = wave; j < kb; j += kHWaves)
+      __builtin_amdgcn_global_load_lds(src + 1024 * j + 16 * lane,
+                                       (__attribute__((address_space(3))) void*)(planes + 1024 * j), 16, 0, 0);
+    const float* const ssrc = a.rsum + static_cast<uint64_t>(ku0) * MR * 8;
+    const float* const usrc = a.rsum + static_cast<uint64_t>(units_total) * MR * 8 + ku0 * MR;
+    const uint32_t nsum = units * MR * 8, nun = units * MR;  // floats
+    for (uint32_t j = wave; j * 64 < nsum; j += kHWaves)
+      if (j * 64 + lane < nsum)
+        __builtin_amdgcn_global_load_lds(ssrc + 64 * j + lane,
+                                         (__attribute__((address_space(3))) void*)(xsum + 64 * j), 4, 0, 0);
+    for (uint32_t j = wave; j * 64 < nun; j += kHWaves)
+      if (j * 64 + lane < nun)
+        __builtin_amdgcn_global_load_lds(usrc + 64 * j + lane,
+                                         (__attribute__((address_space(3))) void*)(unsc + 64 * j), 4, 0, 0);
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the weights queue behind nothing
+#pragma unroll
+    for (int i = 0; i < D; ++i)
+      if (i < static_cast<int>(u_count))
+        U::template load<WIDE, true>(trec + (ku0 + u_begin + i) * R.bytes, lane, ring[i]);
+    // every wavefront's copies have landed; a bare barrier (a fenced one
+    // would wait for the weight loads)
+    __builtin_amdgcn_s_barrier();
+    auto consume = [&](uint32_t j) {
+#pragma unroll
+      for (int i = 0; i < D; ++i) {
+        if (j + i >= u_count) break;
+        const uint32_t u = u_begin + j + i;  // chunk-relative unit
+        const typename U::Raw& r = ring[i];
+        typename H::T ct;
+        H::prepare(r, ct);
+        v4f ua = {0.0f, 0.0f, 0.0f, 0.0f};
+        // rows past MR read row MR - 1 (their sums are never stored)
+        const uint32_t arow = col < static_cast<uint32_t>(MR) ? col : MR - 1;
+        const uint8_t* const ab = planes + ((u * 16) * MR + arow) * 64 + g * 16;  // window 0, hi
+        if constexpr (QT == kQ6_K) {
+          const float d = U::template d<WIDE>(r);
+          const h2 k0 = splat(g < 2 ? 0.25f : 0.0f), c0 = splat(g < 2 ? -288.0f : 0.0f);
+          const h2 k1 = splat(g < 2 ? 0.0f : 0.25f), c1 = splat(g < 2 ? 0.0f : -288.0f);
+#pragma unroll
+          for (int w = 0; w < 8; ++w) {
+            uint32_t raw[4], b0[4], b1[4];
+            H::raw(ct, w, raw);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              b0[q] = pk_fma(raw[q], k0, c0);
+              b1[q] = pk_fma(raw[q], k1, c1);
+            }
+            const uint32_t swd = U::window_scales(r, w);
+            const int hf = (w >> 1) & 1;
+            const float a0 = d * static_cast<float>(static_cast<int32_t>(swd << (24 - 16 * hf)) >> 24);
+            const float a1 = d * static_cast<float>(static_cast<int32_t>(swd << (16 - 16 * hf)) >> 24);
+            const h8 ahi = *reinterpret_cast<const h8*>(ab + w * 2 * MR * 64);
+            const h8 alo = *reinterpret_cast<const h8*>(ab + (w * 2 + 1) * MR * 64);
+            const h8 bb0 = __builtin_bit_cast(h8, make_uint4(b0[0], b0[1], b0[2], b0[3]));
+            const h8 bb1 = __builtin_bit_cast(h8, make_uint4(b1[0], b1[1], b1[2], b1[3]));
+            v4f c0v = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, bb0, v4f{0, 0, 0, 0}, 0, 0, 0);
+            c0v = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, bb0, c0v, 0, 0, 0);
+            v4f c1v = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, bb1, v4f{0, 0, 0, 0}, 0, 0, 0);
+            c1v = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, bb1, c1v, 0, 0, 0);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) ua[q] = fmaf(a1, c1v[q], fmaf(a0, c0v[q], ua[q]));
+            // the window's sums are combined here, not after the last window
+            // (the compiler would otherwise keep every window's sums live)
+            pin(ua);
+            __builtin_amdgcn_sched_barrier(0);
+          }
+        } else {
+          // window factors (and for Q4_K / Q5_K zero points and offsets) of
+          // this lane group's windows 2g, 2g + 1, gathered for all eight:
+          // the windows of one h (w = 2g' + h) at a time
+          float sa_own[2], sb_own[2];
+          U::template scales<WIDE>(g, r, sa_own, sb_own);
+          [[maybe_unused]] uint32_t zown[2];
+          if constexpr (H::kOffset) {
+            // zero points z (window_zero_point) and what they leave, b - z a
+            // (exactly rounded); the centring constants -(1024 + z) for the
+            // low-nibble window 2g and -(64 + z) for the high-nibble 2g + 1
+            const float z0 = window_zero_point(sa_own[0], sb_own[0]);
+            const float z1 = window_zero_point(sa_own[1], sb_own[1]);
+            const float o0 = fmaf(-z0, sa_own[0], sb_own[0]);
+            const float o1 = fmaf(-z1, sa_own[1], sb_own[1]);
+            zown[0] = h2u(splat(-(1024.0f + z0)));
+            zown[1] = h2u(splat(-(64.0f + z1)));
+            // offsets: the rows' sums of windows 2g + h against -(b - z a)
+            const float2 sx = *reinterpret_cast<const float2*>(xsum + (u * MR + arow) * 8 + 2 * g);
+            ua = __builtin_amdgcn_mfma_f32_16x16x4f32(sx.x, -o0, ua, 0, 0, 0);
+            ua = __builtin_amdgcn_mfma_f32_16x16x4f32(sx.y, -o1, ua, 0, 0, 0);
+          }
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            uint32_t fa[4];
+            gather4u(__builtin_bit_cast(uint32_t, sa_own[h]), fa);
+            [[maybe_unused]] uint32_t zc[4];
+            if constexpr (H::kOffset) gather4u(zown[h], zc);
+            // two windows at a time, their instruction chains interleaved
+#pragma unroll
+            for (int pp = 0; pp < 2; ++pp) {
+              h8 ahi[2], alo[2], bb[2];
+#pragma unroll
+              for (int e = 0; e < 2; ++e) {
+                const int w = 2 * (2 * pp + e) + h;
+                ahi[e] = *reinterpret_cast<const h8*>(ab + w * 2 * MR * 64);
+                alo[e] = *reinterpret_cast<const h8*>(ab + (w * 2 + 1) * MR * 64);
+              }
+#pragma unroll
+              for (int e = 0; e < 2; ++e) {
+                const int w = 2 * (2 * pp + e) + h;
+                uint32_t bq[4];
+                if constexpr (H::kOffset) H::codes(ct, w, u2h(zc[2 * pp + e]), bq);
+                else H::codes(ct, w, bq);
+                bb[e] = __builtin_bit_cast(h8, make_uint4(bq[0], bq[1], bq[2], bq[3]));
+              }
+              v4f c0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi[0], bb[0], v4f{0, 0, 0, 0}, 0, 0, 0);
+              v4f c1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi[1], bb[1], v4f{0, 0, 0, 0}, 0, 0, 0);
+              c0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo[0], bb[0], c0, 0, 0, 0);
+              c1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo[1], bb[1], c1, 0, 0, 0);
+              const float f0 = __builtin_bit_cast(float, fa[2 * pp]), f1 = __builtin_bit_cast(float, fa[2 * pp + 1]);
+#pragma unroll
+              for (int q = 0; q < 4; ++q) ua[q] = fmaf(f1, c1[q], fmaf(f0, c0[q], ua[q]));
+              // the pair's sums are combined here, not after the last window
+              // (the compiler would otherwise keep every window's sums live)
+              pin(ua);
+              __builtin_amdgcn_sched_barrier(0);
+            }
+          }
+        }
+        // the unit's sums of rows 4g..4g+3, unscaled
+        const float4 us = *reinterpret_cast<const float4*>(unsc + u * MR + min(4 * g, static_cast<uint32_t>(MR) - 4));
+        acc[0] = fmaf(us.x, ua[0], acc[0]);
+        acc[1] = fmaf(us.y, ua[1], acc[1]);
+        acc[2] = fmaf(us.z, ua[2], acc[2]);
+        acc[3] = fmaf(us.w, ua[3], acc[3]);
+      }
+    };
+    consume(0);
+    for (uint32_t j = D; j < u_count; j += D) {
+#pragma unroll
+      for (int i = 0; i < D; ++i)
+        if (j + i < u_count) U::template load<WIDE, true>(trec + (ku0 + u_begin + j + i) * R.bytes, lane, ring[i]);
+      consume(j);
+    }
+  }
+
+  // ---- the K slices of each tile, in order ----
+  __syncthreads();  // the chunk is no longer read
+  float* red = reinterpret_cast<float*>(lds);  // [tile][slice][4][64]
+#pragma unroll
+  for (int q = 0; q < 4; ++q) red[((wc * SL + sw) * 4 + q) * 64 + lane] = acc[q];
+  __syncthreads();
+  if (sw != 0) return;
+  const uint64_t n_out = static_cast<uint64_t>(tile_raw) * 16 + col;
+  if (tile_raw >= a.w.tiles || n_out >= a.w.n) return;
+  float* const yout = gridDim.y > 1 ? a.part + static_cast<uint64_t>(blockIdx.y) * M * a.w.n : a.y;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int m = 4 * static_cast<int>(g) + q;
+    if (m >= M) continue;
+    float v = red[((wc * SL) * 4 + q) * 64 + lane];
+#pragma unroll
+    for (int p = 1; p < SL; ++p) v += red[((wc * SL + p) * 4 + q) * 64 + lane];
+    // NaN or infinite activations (or an overflow): the reference's own order
+    // decides which outputs are NaN and which +-Inf
+    if (!__builtin_isfinite(v) && gridDim.y == 1)
+      v = exact_output_row<QT, WIDE>(a.w, a.x + static_cast<uint64_t>(m) * K, n_out);
+    yout[static_cast<uint64_t>(m) * a.w.n + n_out] = v;
+  }
+}
+
+template <int QT, bool WIDE, int MR, int TL>
+hipError_t launch_half_t(HalfArgs a, uint32_t ksplit, hipStream_t st) {
+  constexpr int D = 2;
+  const uint32_t cap = half_chunk_cap(MR);
+  a.chunk_units = a.part_units < cap ? a.part_units : cap;
+  const uint32_t main = half_lds(MR, a.chunk_units);
+  const uint32_t red = kHWaves * 4 * 64 * 4;
+  const uint32_t bytes = main > red ? main : red;
+  auto kern = gemv_half_kernel<QT, WIDE, MR, D, TL>;
+  if (bytes > 65536) {
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(bytes));
+    if (e != hipSuccess) {
+      (void)hipGetLastError();
+      return e;
+    }
+  }
+  if (ksplit > 1 && a.part == nullptr) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(kern, dim3((a.w.tiles + TL - 1) / TL, ksplit), dim3(kHThreads), bytes, st, a);
+  return hipGetLastError();
+}
+
+// One-tile workgroups (16 K slices, no K split) for shapes of up to one tile
+// per CU whose whole K range fits one LDS chunk.
+bool half_one_tile(uint64_t k, uint64_t n) {
+  return (n + 15) / 16 <= kHCUs && k / 256 <= half_chunk_cap(kHRows);
+}
+
+template <int QT, bool WIDE>
+hipError_t launch_half_w(const HalfArgs& a, uint32_t ksplit, hipStream_t st) {
+  const bool one = half_one_tile(a.w.k, a.w.n);
+  if (one && ksplit != 1) return hipErrorInvalidValue;
+  return one ? launch_half_t<QT, WIDE, kHRows, 1>(a, ksplit, st) : launch_half_t<QT, WIDE, kHRows, 4>(a, ksplit, st);
+}
+
+}  // namespace
+
+uint32_t gemv_half_splits(uint64_t k, uint64_t n, uint32_t m) {
+  (void)m;
+  if (half_one_tile(k, n)) return 1;
+  // one four-tile workgroup per CU; split K only when the tile groups leave
+  // most CUs idle, keeping at least 4 units (one per K slice) per part, and
+  // return the count the launch runs (every part holds units)
+  const uint64_t tiles = (n + 15) / 16, units = k / 256, groups = (tiles + 3) / 4;
+  uint64_t s = kHCUs / (groups ? groups : 1);
+  const uint64_t most = units / 4 ? units / 4 : 1;
+  if (s > most) s = most;
+  if (s < 1) s = 1;
+  const uint64_t part_units = (units + s - 1) / s;
+  return static_cast<uint32_t>((units + part_units - 1) / part_units);
+}
+
+uint64_t gemv_half_records_bytes(uint64_t k) { return half_records_size(k / 256, kHRows); }
+
+hipError_t launch_gemv_half_records(const float* x, uint64_t k, int m, uint8_t* rec, hipStream_t st) {
+  if (m < 9 || m > 16 || k == 0 || k % 256 != 0 || rec == nullptr) return hipErrorInvalidValue;
+  const uint32_t pairs = static_cast<uint32_t>(k / 256) * kHRows;
+  hipLaunchKernelGGL(half_prep_kernel<kHRows>, dim3((pairs + 7) / 8), dim3(256), 0, st, x,
+                     static_cast<uint32_t>(k), m, rec);
+  return hipGetLastError();
+}
+
+hipError_t launch_gemv_half(int32_t qtype, bool wide, const View& w, const float* x, int m, float* y, float* part,
+                            uint32_t ksplit, const uint8_t* rec, hipStream_t st) {
+  if (m < 9 || m > 16 || ksplit < 1 || w.k == 0 || w.k % 256 != 0 || rec == nullptr) return hipErrorInvalidValue;
+  HalfArgs a{w, x, y, m, 0, 0, part, rec, nullptr};
+  const uint32_t units = w.units;
+  a.rsum = reinterpret_cast<const float*>(rec + static_cast<uint64_t>(units) * kHRows * 1024);
+  a.part_units = (units + ksplit - 1) / ksplit;
+  if ((units + a.part_units - 1) / a.part_units != ksplit) return hipErrorInvalidValue;  // every K part holds units
+  switch (qtype) {
+    case kQ8_0: return wide ? launch_half_w<kQ8_0, true>(a, ksplit, st) : launch_half_w<kQ8_0, false>(a, ksplit, st);
+    case kQ4_0: return wide ? launch_half_w<kQ4_0, true>(a, ksplit, st) : launch_half_w<kQ4_0, false>(a, ksplit, st);
+    case kQ4_K: return wide ? launch_half_w<kQ4_K, true>(a, ksplit, st) : launch_half_w<kQ4_K, false>(a, ksplit, st);
+    case kQ5_K: return wide ? launch_half_w<kQ5_K, true>(a, ksplit, st) : launch_half_w<kQ5_K, false>(a, ksplit, st);
+    case kQ6_K: return wide ? launch_half_w<kQ6_K, true>(a, ksplit, st) : launch_half_w<kQ6_K, false>(a, ksplit, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace qi

@@ -1,6 +1,7 @@
-// Decode GEMV of 2-16 activation rows on the int8 matrix cores
+// Decode GEMV of 2-8 activation rows on the int8 matrix cores
 // (v_mfma_i32_16x16x32_i8), output-rows layout, K a multiple of 256; one
-// kernel per call (K parts over the grid only for shapes with few tiles).
+// kernel per call (K parts over the grid only for shapes with few tiles);
+// 9-16 rows take the split-half kernel (qi_gemv_half.hip).
 //
 // Arithmetic: as the one-row kernel (qi_gemv_mfma.hip). Each activation row
 // is cut into windows of 32 elements; an element becomes the 30-bit integer
@@ -253,98 +254,6 @@ struct Dense<kQ6_K> {
   }
 };
 
-// Weight access of one unit: the one-row kernel's (qi_unit.h), except that
-// Q5_K loads only the 8 qh bytes of slice g (not all 32 of the output), which
-// keeps the 16-wavefront register budget.
-template <int QT>
-struct RowsUnit : Unit<QT> {};
-
-template <>
-struct RowsUnit<kQ5_K> {
-  static constexpr bool kMin = true;
-  struct Raw {
-    uint4 q[2];
-    uint32_t hl, hh;  // qh bytes 8g..8g+7 of this output
-    uint32_t sc[3];
-    uint32_t s0, s1;
-  };
-  template <bool W, bool NT>
-  __device__ static void load(const uint8_t* rec, uint32_t lane, Raw& r) {
-    constexpr Record R = record_geometry(kQ5_K, W);
-    const uint32_t col = lane & 15, g = lane >> 4;
-    const uint4* p = reinterpret_cast<const uint4*>(rec + R.qs) + lane;
-    r.q[0] = ld_codes<true>(p);
-    r.q[1] = ld_codes<true>(p + 64);
-    // 16-byte chunk g / 2 of row col's qh, its half g % 2
-    const uint2 h = *reinterpret_cast<const uint2*>(rec + R.qh + (g >> 1) * 256 + col * 16 + (g & 1) * 8);
-    r.hl = h.x;
-    r.hh = h.y;
-    const uint32_t* s = reinterpret_cast<const uint32_t*>(rec + R.sc + col * 12);
-    r.sc[0] = s[0];
-    r.sc[1] = s[1];
-    r.sc[2] = s[2];
-    if constexpr (W) {
-      r.s0 = reinterpret_cast<const uint32_t*>(rec + R.d)[col];
-      r.s1 = reinterpret_cast<const uint32_t*>(rec + R.dmin)[col];
-    } else {
-      r.s0 = reinterpret_cast<const uint16_t*>(rec + R.d)[col];
-      r.s1 = reinterpret_cast<const uint16_t*>(rec + R.dmin)[col];
-    }
-  }
-  template <bool W>
-  __device__ static void scales(uint32_t g, const Raw& r, float a[2], float b[2]) {
-    typename Unit<kQ5_K>::Raw u;
-    u.sc[0] = r.sc[0];
-    u.sc[1] = r.sc[1];
-    u.sc[2] = r.sc[2];
-    u.s0 = r.s0;
-    u.s1 = r.s1;
-    Unit<kQ5_K>::template scales<W>(g, u, a, b);
-  }
-};
-
-// Q6_K: the ql chunks as the one-row kernel loads them; the qh bytes of slice
-// g of both halves (bytes 8g..8g+7 of 32ip + [0, 32), ip = 0, 1) instead of
-// the lane group's own 32, and the row's 16 sub-scales (tiled order,
-// q6_scale_pos: window w's two at bytes 2hf, 2hf + 1 of word 2ip + c).
-template <>
-struct RowsUnit<kQ6_K> {
-  struct Raw {
-    uint4 q[2];
-    uint32_t h[4];
-    uint4 sc;
-    uint32_t d;  // f16 in the low half, or f32
-  };
-  template <bool W, bool NT>
-  __device__ static void load(const uint8_t* rec, uint32_t lane, Raw& r) {
-    constexpr Record R = record_geometry(kQ6_K, W);
-    const uint32_t col = lane & 15, g = lane >> 4;
-    const uint4* p = reinterpret_cast<const uint4*>(rec + R.qs) + lane;
-    r.q[0] = ld_codes<true>(p);
-    r.q[1] = ld_codes<true>(p + 64);
-    // 16-byte chunk 2ip + g / 2 of row col's qh, its half g % 2
-#pragma unroll
-    for (int ip = 0; ip < 2; ++ip) {
-      const uint2 h = *reinterpret_cast<const uint2*>(rec + R.qh + (2 * ip + (g >> 1)) * 256 + col * 16 + (g & 1) * 8);
-      r.h[2 * ip] = h.x;
-      r.h[2 * ip + 1] = h.y;
-    }
-    r.sc = *reinterpret_cast<const uint4*>(rec + R.sc + col * 16);
-    if constexpr (W) r.d = reinterpret_cast<const uint32_t*>(rec + R.d)[col];
-    else r.d = reinterpret_cast<const uint16_t*>(rec + R.d)[col];
-  }
-  template <bool W>
-  __device__ static float d(const Raw& r) {
-    if constexpr (W) return __builtin_bit_cast(float, r.d);
-    else return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(r.d)));
-  }
-  // the sub-scales of window w, word 2ip + c of the row's 16
-  __device__ static uint32_t window_scales(const Raw& r, int w) {
-    const int word = 2 * (w >> 2) + (w & 1);
-    return word == 0 ? r.sc.x : word == 1 ? r.sc.y : word == 2 ? r.sc.z : r.sc.w;
-  }
-};
-
 struct RowsArgs {
   View w;
   const float* x;  // [m, k]
@@ -353,7 +262,6 @@ struct RowsArgs {
   uint32_t chunk_units;  // units per LDS chunk
   uint32_t part_units;   // units per K part (grid.y)
   float* part;           // [grid.y][m][n] when grid.y > 1
-  const uint8_t* rec;    // the call's activation records (rows_records_kernel), or null
 };
 
 // Activation prep, in place. Item (q, W, s, r) is slice s (elements 8s..8s+7)
@@ -461,66 +369,6 @@ __device__ __forceinline__ void prep_item(uint32_t t, uint32_t q, uint32_t W, ui
   prep_convert(v0, v1, t, q, W, cw, valid, dig, xsc, xsum);
 }
 
-// Four row groups (9-16 rows): the activation records of the whole call,
-// built once into global memory by a kernel of their own, since every
-// workgroup otherwise converts all of them (at 16 rows a quarter of the GEMV,
-// Q4_K 4096 x 14336; the records kernel and its launch cost about a third of
-// that back: 30.0 -> 29.2 us on MI355X; at 8 rows they cost more than they
-// save, 18.8 -> 21.9 us). The layout is the LDS one with the whole K range
-// as one chunk, cw = K / 32 windows: digit
-// blocks [q][window] of kBlock bytes, then the scales [row][window] and the
-// window sums [row][window] as f32, rows 4 MG (zero digits past M).
-constexpr uint64_t rows_records_size(uint64_t k, int mg) {
-  return static_cast<uint64_t>(mg) * (k / 32) * kBlock + 2 * 4 * static_cast<uint64_t>(mg) * (k / 32) * 4;
-}
-
-__global__ __launch_bounds__(256) void rows_records_kernel(const float* x, uint32_t K, int M, int mg, uint8_t* out) {
-  const uint32_t cw = K / 32, items = 16u * static_cast<uint32_t>(mg) * cw;
-  const uint32_t t = blockIdx.x * 256 + threadIdx.x;
-  const bool valid = t < items;
-  const uint32_t W = (t >> 4) % cw, m = 4 * ((t >> 4) / cw) + (t & 3), s = (t >> 2) & 3;
-  float4 v0 = make_float4(0.0f, 0.0f, 0.0f, 0.0f), v1 = v0;
-  if (valid && static_cast<int>(m) < M) {
-    const float4* p = reinterpret_cast<const float4*>(x + static_cast<uint64_t>(m) * K + 32 * W + 8 * s);
-    v0 = p[0];
-    v1 = p[1];
-  }
-  float* const xsc = reinterpret_cast<float*>(out + static_cast<uint64_t>(mg) * cw * kBlock);
-  prep_convert(v0, v1, t, (t >> 4) / cw, W, cw, valid, out, xsc, xsc + 4 * mg * cw);
-}
-
-// Copy a chunk's records (windows [w0, w0 + cwin) of every row group) into
-// the LDS layout of chunk stride cw: the digit blocks by global-to-LDS copies
-// (each row group's run is contiguous in both), the scales and sums by one
-// 16-byte load per thread (at most 2 x 4 MG x cwin / 4 = 512 of them), issued
-// with the copies; the caller writes them to LDS (RecordTail) once they land.
-struct RecordTail {
-  float4 v;
-  float* dst;
-};
-__device__ __forceinline__ RecordTail stage_records(const uint8_t* rec, uint32_t wtot, uint32_t w0, uint32_t cwin,
-                                                    uint32_t cw, int mg, uint8_t* dig, float* xsc, uint32_t tid) {
-  const uint32_t wave = tid >> 6, lane = tid & 63;
-  const uint32_t per_q = cwin * kBlock / 1024;  // 1 KB copies per row group
-  for (uint32_t j = wave; j < static_cast<uint32_t>(mg) * per_q; j += kRowsThreads / 64) {
-    const uint32_t q = j / per_q, pc = j % per_q;
-    __builtin_amdgcn_global_load_lds(rec + (static_cast<uint64_t>(q) * wtot + w0) * kBlock + pc * 1024 + lane * 16,
-                                     (__attribute__((address_space(3))) void*)(dig + q * cw * kBlock + pc * 1024),
-                                     16, 0, 0);
-  }
-  RecordTail r{make_float4(0.0f, 0.0f, 0.0f, 0.0f), nullptr};
-  const uint32_t rows = 4 * static_cast<uint32_t>(mg), per_row = cwin / 4;
-  if (tid < 2 * rows * per_row) {
-    const uint32_t which = tid / (rows * per_row), rem = tid % (rows * per_row);
-    const uint32_t row = rem / per_row, i = rem % per_row;
-    const float* src = reinterpret_cast<const float*>(rec + static_cast<uint64_t>(mg) * wtot * kBlock) +
-                       (static_cast<uint64_t>(which) * rows + row) * wtot + w0 + 4 * i;
-    r.v = *reinterpret_cast<const float4*>(src);
-    r.dst = xsc + (which * rows + row) * cw + 4 * i;
-  }
-  return r;
-}
-
 // MG row groups (M <= 4 MG), D units of weights in flight per wavefront, TL
 // tiles per workgroup (4, or 1 with 16 K slices for shapes of up to one tile
 // per CU). ZP (Q4_K / Q5_K): the codes centred on a zero point per window
@@ -579,43 +427,30 @@ __global__ __launch_bounds__(kRowsThreads) void gemv_rows_kernel(RowsArgs a) {
     // global-to-LDS copy, and vector memory completes in order, so a copy
     // waited for after the weight loads would wait for the weights. The
     // weights' HBM latency then overlaps the prep instead.
-    if (MG >= 4 && !ZP && a.rec != nullptr) {
-      // the call's records (rows_records_kernel): copies, then the weights
-      const RecordTail rt = stage_records(a.rec, K / 32, ku0 * 8, cwin, cw, MG, dig, xsc, tid);
-      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
-      if (rt.dst != nullptr) *reinterpret_cast<float4*>(rt.dst) = rt.v;
+    // this workgroup's own conversion of its activations
+    stage_x(a.x, K, ku0 * 256, M, MG, cw, cwin, dig, wave, lane);
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
 #pragma unroll
-      for (int i = 0; i < D; ++i)
-        if (i < static_cast<int>(u_count))
-          U::template load<WIDE, true>(trec + (ku0 + u_begin + i) * R.bytes, lane, ring[i]);
-      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wavefront's scale and sum stores
-      __builtin_amdgcn_s_barrier();
-    } else {
-      // this workgroup's own conversion of its activations
-      stage_x(a.x, K, ku0 * 256, M, MG, cw, cwin, dig, wave, lane);
-      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
-#pragma unroll
-      for (int i = 0; i < D; ++i)
-        if (i < static_cast<int>(u_count))
-          U::template load<WIDE, true>(trec + (ku0 + u_begin + i) * R.bytes, lane, ring[i]);
-      // every wavefront's copies have landed; a bare barrier (a fenced one
-      // would wait for the weight loads)
-      __builtin_amdgcn_s_barrier();
-      // items t = tid + 1024 i: block t / 16 advances by 64 windows a step,
-      // (row group, window) kept without a division per item
-      const uint32_t items = 16u * MG * cw;
-      uint32_t q = (tid >> 4) / cw, W = (tid >> 4) % cw;
-      for (uint32_t t = tid; t < items; t += kRowsThreads) {
-        prep_item(t, q, W, cw, cwin, M, dig, xsc, xsum);
-        W += kRowsThreads / 16;
-        while (W >= cw) {
-          W -= cw;
-          ++q;
-        }
+    for (int i = 0; i < D; ++i)
+      if (i < static_cast<int>(u_count))
+        U::template load<WIDE, true>(trec + (ku0 + u_begin + i) * R.bytes, lane, ring[i]);
+    // every wavefront's copies have landed; a bare barrier (a fenced one
+    // would wait for the weight loads)
+    __builtin_amdgcn_s_barrier();
+    // items t = tid + 1024 i: block t / 16 advances by 64 windows a step,
+    // (row group, window) kept without a division per item
+    const uint32_t items = 16u * MG * cw;
+    uint32_t q = (tid >> 4) / cw, W = (tid >> 4) % cw;
+    for (uint32_t t = tid; t < items; t += kRowsThreads) {
+      prep_item(t, q, W, cw, cwin, M, dig, xsc, xsum);
+      W += kRowsThreads / 16;
+      while (W >= cw) {
+        W -= cw;
+        ++q;
       }
-      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wavefront's records are written
-      __builtin_amdgcn_s_barrier();
     }
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wavefront's records are written
+    __builtin_amdgcn_s_barrier();
 
     // Q6_K: each 32-element window holds two 16-element sub-blocks of their
     // own scales. The window's codes go in twice, in one instruction with
@@ -829,9 +664,7 @@ hipError_t launch_rows_tz(const RowsArgs& a, uint32_t ksplit, hipStream_t st) {
   // two units in flight per wavefront: what the 128-register budget of a
   // 16-wavefront workgroup holds
   if (a.m <= 4) return launch_rows_t<QT, WIDE, 1, 2, TL, ZP>(a, ksplit, st);
-  if (a.m <= 8) return launch_rows_t<QT, WIDE, 2, 2, TL, ZP>(a, ksplit, st);
-  // (Q5_K with 16 rows exceeds the budget at two units in flight)
-  return launch_rows_t<QT, WIDE, 4, QT == kQ5_K ? 1 : 2, TL, ZP>(a, ksplit, st);
+  return launch_rows_t<QT, WIDE, 2, 2, TL, ZP>(a, ksplit, st);
 }
 
 // Q4_K / Q5_K centring. The offsets of all windows are summed apart from the
@@ -863,7 +696,7 @@ hipError_t launch_rows_tl(const RowsArgs& a, uint32_t ksplit, hipStream_t st) {
 // M=8 13.0 -> 11.1; slower with two chunks or more (4096 x 4096 M=16 15.5 ->
 // 21.7, 12288 x 4096 M=4 16.7 -> 18.7).
 bool rows_one_tile(uint64_t k, uint64_t n, uint32_t m) {
-  const int mg = m <= 4 ? 1 : m <= 8 ? 2 : 4;
+  const int mg = m <= 4 ? 1 : 2;
   return (n + 15) / 16 <= kRowsCUs && k / 256 <= rows_chunk_cap(mg);
 }
 
@@ -897,34 +730,10 @@ uint32_t gemv_rows_splits(uint64_t k, uint64_t n, uint32_t m) {
   return static_cast<uint32_t>((units + part_units - 1) / part_units);
 }
 
-bool gemv_rows_records(uint64_t k, uint64_t n, uint32_t m) {
-  // where every workgroup would convert more than 8 units of K (per K part);
-  // below that the records kernel and its launch cost more than they save
-  // (Q4_0 4096 x 4096 M=12, four parts of 4 units: 15.7 -> 17.6 us). The
-  // zero-point kernels (at most 8 units) thus always convert their own.
-  if (m <= 8 || m > 16) return false;
-  const uint64_t units = k / 256, parts = gemv_rows_splits(k, n, m);
-  return (units + parts - 1) / parts > kRowsZeroPointUnits;
-}
-
-uint64_t gemv_rows_records_bytes(uint64_t k, uint64_t n, uint32_t m) {
-  return gemv_rows_records(k, n, m) ? rows_records_size(k, 4) : 0;
-}
-
-hipError_t launch_gemv_rows_records(const float* x, uint64_t k, int m, uint8_t* out, hipStream_t st) {
-  if (m <= 8 || m > 16 || k % 256 != 0 || out == nullptr) return hipErrorInvalidValue;
-  const int mg = 4;
-  const uint64_t items = 16ull * static_cast<uint64_t>(mg) * (k / 32);
-  hipLaunchKernelGGL(rows_records_kernel, dim3(static_cast<uint32_t>((items + 255) / 256)), dim3(256), 0, st, x,
-                     static_cast<uint32_t>(k), m, mg, out);
-  return hipGetLastError();
-}
-
 hipError_t launch_gemv_rows(int32_t qtype, bool wide, const View& w, const float* x, int m, float* y, float* part,
-                            uint32_t ksplit, const uint8_t* records, hipStream_t st) {
-  if (m < 1 || m > 16 || ksplit < 1 || w.k == 0 || w.k % 256 != 0) return hipErrorInvalidValue;
-  if ((records != nullptr) != gemv_rows_records(w.k, w.n, static_cast<uint32_t>(m))) return hipErrorInvalidValue;
-  RowsArgs a{w, x, y, m, 0, 0, part, records};
+                            uint32_t ksplit, hipStream_t st) {
+  if (m < 1 || m > 8 || ksplit < 1 || w.k == 0 || w.k % 256 != 0) return hipErrorInvalidValue;
+  RowsArgs a{w, x, y, m, 0, 0, part};
   const uint32_t units = w.units;
   a.part_units = (units + ksplit - 1) / ksplit;
   const uint32_t parts = (units + a.part_units - 1) / a.part_units;

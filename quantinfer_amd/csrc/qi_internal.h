@@ -56,20 +56,27 @@ hipError_t launch_splitk_sum(const Image& im, const View& v, const float* part, 
                              uint64_t count, uint64_t stride, float* y, const float* x, hipStream_t st);
 hipError_t launch_gemv_mfma(int32_t qtype, bool wide, int split, const GemvMfmaArgs& a, hipStream_t st);
 
-// Matrix-core decode GEMV of 2-16 rows with dense operands (qi_gemv_rows.hip):
-// one kernel, K parts over the grid (gemv_rows_splits, by shape and row count)
-// only for shapes with few tiles; with ksplit > 1 the partial sums
-// [ksplit][m][n] go to `part` and launch_splitk_sum adds them. Where
-// gemv_rows_records (9-16 rows, no K parts) the GEMV reads the activation
-// records that launch_gemv_rows_records builds into `records`
-// (gemv_rows_records_bytes bytes, 0 elsewhere; null records elsewhere).
-// Shapes: those of gemv_mfma_supported (every format, output rows, K a
-// multiple of 256).
+// Matrix-core decode GEMV of 2-8 rows with dense operands and int8
+// activation digits (qi_gemv_rows.hip): one kernel, K parts over the grid
+// (gemv_rows_splits, by shape and row count) only for shapes with few tiles;
+// with ksplit > 1 the partial sums [ksplit][m][n] go to `part` and
+// launch_splitk_sum adds them. Shapes: those of gemv_mfma_supported (every
+// format, output rows, K a multiple of 256).
 uint32_t gemv_rows_splits(uint64_t k, uint64_t n, uint32_t m);
-bool gemv_rows_records(uint64_t k, uint64_t n, uint32_t m);
-uint64_t gemv_rows_records_bytes(uint64_t k, uint64_t n, uint32_t m);
-hipError_t launch_gemv_rows_records(const float* x, uint64_t k, int m, uint8_t* out, hipStream_t st);
 hipError_t launch_gemv_rows(int32_t qtype, bool wide, const View& w, const float* x, int m, float* y, float* part,
+                            uint32_t ksplit, hipStream_t st);
+
+// Decode GEMV of 9-16 rows on the f16 matrix cores with split-half
+// activations (qi_gemv_half.hip): launch_gemv_half_records converts the
+// activations once per call into `records` (gemv_half_records_bytes bytes),
+// which the GEMV workgroups copy; one GEMV kernel, K parts over the grid
+// (gemv_half_splits) only for shapes with few tiles; with ksplit > 1 the
+// partial sums [ksplit][m][n] go to `part` and launch_splitk_sum adds them.
+// Shapes: those of gemv_mfma_supported.
+uint32_t gemv_half_splits(uint64_t k, uint64_t n, uint32_t m);
+uint64_t gemv_half_records_bytes(uint64_t k);
+hipError_t launch_gemv_half_records(const float* x, uint64_t k, int m, uint8_t* records, hipStream_t st);
+hipError_t launch_gemv_half(int32_t qtype, bool wide, const View& w, const float* x, int m, float* y, float* part,
                             uint32_t ksplit, const uint8_t* records, hipStream_t st);
 
 // Row-major (blocks along N) GEMV of up to 4 activation rows, f32

@@ -383,4 +383,96 @@ __device__ __forceinline__ float window_zero_point(float a, float b) {
   return fminf(fmaxf(rintf(b * __builtin_amdgcn_rcpf(a)), -127.0f), 127.0f);
 }
 
+// Weight access of one unit for the 2-16 row GEMVs: the one-row loaders,
+// except that Q5_K loads only the 8 qh bytes of slice g (not all 32 of the
+// output), which keeps the 16-wavefront register budget, and Q6_K (below).
+template <int QT>
+struct RowsUnit : Unit<QT> {};
+
+template <>
+struct RowsUnit<kQ5_K> {
+  static constexpr bool kMin = true;
+  struct Raw {
+    uint4 q[2];
+    uint32_t hl, hh;  // qh bytes 8g..8g+7 of this output
+    uint32_t sc[3];
+    uint32_t s0, s1;
+  };
+  template <bool W, bool NT>
+  __device__ static void load(const uint8_t* rec, uint32_t lane, Raw& r) {
+    constexpr Record R = record_geometry(kQ5_K, W);
+    const uint32_t col = lane & 15, g = lane >> 4;
+    const uint4* p = reinterpret_cast<const uint4*>(rec + R.qs) + lane;
+    r.q[0] = ld_codes<true>(p);
+    r.q[1] = ld_codes<true>(p + 64);
+    // 16-byte chunk g / 2 of row col's qh, its half g % 2
+    const uint2 h = *reinterpret_cast<const uint2*>(rec + R.qh + (g >> 1) * 256 + col * 16 + (g & 1) * 8);
+    r.hl = h.x;
+    r.hh = h.y;
+    const uint32_t* s = reinterpret_cast<const uint32_t*>(rec + R.sc + col * 12);
+    r.sc[0] = s[0];
+    r.sc[1] = s[1];
+    r.sc[2] = s[2];
+    if constexpr (W) {
+      r.s0 = reinterpret_cast<const uint32_t*>(rec + R.d)[col];
+      r.s1 = reinterpret_cast<const uint32_t*>(rec + R.dmin)[col];
+    } else {
+      r.s0 = reinterpret_cast<const uint16_t*>(rec + R.d)[col];
+      r.s1 = reinterpret_cast<const uint16_t*>(rec + R.dmin)[col];
+    }
+  }
+  template <bool W>
+  __device__ static void scales(uint32_t g, const Raw& r, float a[2], float b[2]) {
+    typename Unit<kQ5_K>::Raw u;
+    u.sc[0] = r.sc[0];
+    u.sc[1] = r.sc[1];
+    u.sc[2] = r.sc[2];
+    u.s0 = r.s0;
+    u.s1 = r.s1;
+    Unit<kQ5_K>::template scales<W>(g, u, a, b);
+  }
+};
+
+// Q6_K: the ql chunks as the one-row kernel loads them; the qh bytes of slice
+// g of both halves (bytes 8g..8g+7 of 32ip + [0, 32), ip = 0, 1) instead of
+// the lane group's own 32, and the row's 16 sub-scales (tiled order,
+// q6_scale_pos: window w's two at bytes 2hf, 2hf + 1 of word 2ip + c).
+template <>
+struct RowsUnit<kQ6_K> {
+  struct Raw {
+    uint4 q[2];
+    uint32_t h[4];
+    uint4 sc;
+    uint32_t d;  // f16 in the low half, or f32
+  };
+  template <bool W, bool NT>
+  __device__ static void load(const uint8_t* rec, uint32_t lane, Raw& r) {
+    constexpr Record R = record_geometry(kQ6_K, W);
+    const uint32_t col = lane & 15, g = lane >> 4;
+    const uint4* p = reinterpret_cast<const uint4*>(rec + R.qs) + lane;
+    r.q[0] = ld_codes<true>(p);
+    r.q[1] = ld_codes<true>(p + 64);
+    // 16-byte chunk 2ip + g / 2 of row col's qh, its half g % 2
+#pragma unroll
+    for (int ip = 0; ip < 2; ++ip) {
+      const uint2 h = *reinterpret_cast<const uint2*>(rec + R.qh + (2 * ip + (g >> 1)) * 256 + col * 16 + (g & 1) * 8);
+      r.h[2 * ip] = h.x;
+      r.h[2 * ip + 1] = h.y;
+    }
+    r.sc = *reinterpret_cast<const uint4*>(rec + R.sc + col * 16);
+    if constexpr (W) r.d = reinterpret_cast<const uint32_t*>(rec + R.d)[col];
+    else r.d = reinterpret_cast<const uint16_t*>(rec + R.d)[col];
+  }
+  template <bool W>
+  __device__ static float d(const Raw& r) {
+    if constexpr (W) return __builtin_bit_cast(float, r.d);
+    else return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(r.d)));
+  }
+  // the sub-scales of window w, word 2ip + c of the row's 16
+  __device__ static uint32_t window_scales(const Raw& r, int w) {
+    const int word = 2 * (w >> 2) + (w & 1);
+    return word == 0 ? r.sc.x : word == 1 ? r.sc.y : word == 2 ? r.sc.z : r.sc.w;
+  }
+};
+
 }  // namespace qi

@@ -503,24 +503,26 @@ def _planner(name, *argtypes):
 
 
 def test_gemv_rows_split_count_gives_every_part_units():
-    """The 2-16 row GEMV's launch gives each of its `s` K parts ceil(units/s)
-    units and refuses a split count whose parts would not all hold units.
-    The planner (qi::gemv_rows_splits, host code in the library) must return
-    a count the launch accepts for every shape: K = 8960, N = 1536 at 2-4
-    rows once asked for 8 parts of 5 units (7 parts cover K)."""
-    splits = _planner("_ZN2qi16gemv_rows_splitsEmmj", ctypes.c_uint64, ctypes.c_uint64, ctypes.c_uint32)
-    seen = set()
-    for units in range(1, 129):
-        k = 256 * units
-        for n in list(range(16, 4097, 16)) + [4100, 12288, 14336]:
-            for m in range(2, 17):
-                s = splits(k, n, m)
-                assert 1 <= s <= units, (k, n, m, s)
-                part = -(-units // s)
-                assert -(-units // part) == s, (k, n, m, s)
-                seen.add(s)
-    assert len(seen) > 8  # the sweep reaches many split counts
-    assert splits(8960, 1536, 2) == 7 and splits(6400, 1024, 8) == 5
+    """The 2-16 row GEMVs' launches give each of their `s` K parts
+    ceil(units/s) units and refuse a split count whose parts would not all
+    hold units. The planners (qi::gemv_rows_splits for 2-8 rows,
+    qi::gemv_half_splits for 9-16, host code in the library) must return a
+    count the launch accepts for every shape: K = 8960, N = 1536 at 2-4 rows
+    once asked for 8 parts of 5 units (7 parts cover K)."""
+    for name, rows in (("_ZN2qi16gemv_rows_splitsEmmj", range(2, 9)), ("_ZN2qi16gemv_half_splitsEmmj", range(9, 17))):
+        splits = _planner(name, ctypes.c_uint64, ctypes.c_uint64, ctypes.c_uint32)
+        seen = set()
+        for units in range(1, 129):
+            k = 256 * units
+            for n in list(range(16, 4097, 16)) + [4100, 12288, 14336]:
+                for m in rows:
+                    s = splits(k, n, m)
+                    assert 1 <= s <= units, (name, k, n, m, s)
+                    part = -(-units // s)
+                    assert -(-units // part) == s, (name, k, n, m, s)
+                    seen.add(s)
+        assert len(seen) > 8  # the sweep reaches many split counts
+        assert splits(8960, 1536, 2) == 7 and splits(6400, 1024, 8) == 5
 
 
 def _rust_paths():
