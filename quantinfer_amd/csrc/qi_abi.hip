@@ -168,7 +168,7 @@ qi_hip_status grow_ws(qi_hip_ctx* c, hipStream_t st, float** buf, uint64_t* cap,
 // function decides, so that the growing path (run_linear) and the scratch
 // path (qi_hip_linear_device_noalloc) take the same kernels.
 struct LinearPlan {
-  enum Kind { kGemm, kRowMajor, kMfma, kPlanar, kF32Gemv, kF32Gemm, kExact } kind = kExact;
+  enum Kind { kGemm, kRowMajor, kMfma, kSplitGemm, kPlanar, kF32Gemv, kF32Gemm, kExact } kind = kExact;
   uint64_t m_pad = 0;
   uint32_t splits = 1;  // GEMM K splits, or row-major GEMV K splits for 4-row chunks
   uint64_t h_floats = 0, s_floats = 0, d_floats = 0;  // f16 activations, partials, records
@@ -183,6 +183,10 @@ struct LinearPlan {
 // M=16 29.5 / 23.8; Q4_0 12288x4096 M=4 16.6 / 18.0, M=16 28.1 / 22.9; Q4_K
 // 4096x24576 M=16 49.6 / 38.3.
 constexpr uint32_t kHalfMinRows = 9;
+
+// Rows from which Q4_K / Q5_K output rows take the split-half GEMM
+// (qi_gemm_split.hip) in F32 mode, and in AUTO mode below the f16 GEMM's 128.
+constexpr uint64_t kSplitMinRows = 17;
 
 qi_hip_status plan_linear(const Image& im, uint64_t m, int32_t mode, LinearPlan* p) {
   if (mode < QI_HIP_MODE_AUTO || mode > QI_HIP_MODE_MFMA)
@@ -223,6 +227,13 @@ qi_hip_status plan_linear(const Image& im, uint64_t m, int32_t mode, LinearPlan*
     const uint32_t chunk = m < 4 ? static_cast<uint32_t>(m) : 4u;
     p->splits = qi::gemv_rm_splits(im, chunk);
     if (p->splits > 1) p->s_floats = static_cast<uint64_t>(p->splits) * chunk * im.n;
+    return QI_HIP_OK;
+  }
+  if (mode != QI_HIP_MODE_EXACT && m >= kSplitMinRows && qi::gemm_split_supported(im)) {
+    p->kind = LinearPlan::kSplitGemm;
+    p->splits = qi::gemm_split_splits(im, m);
+    if (p->splits > 1) p->s_floats = static_cast<uint64_t>(p->splits) * m * im.n;
+    p->d_floats = (qi::gemm_split_records_bytes(m, im.k) + 3) / 4;
     return QI_HIP_OK;
   }
   if (mode != QI_HIP_MODE_EXACT && qi::gemv_mfma_supported(im.qtype, im.layout, im.k)) {
@@ -328,6 +339,10 @@ qi_hip_status enqueue_linear(const qi_hip_weights* w, const LinearPlan& p, const
           QI_HIP_TRY(qi::launch_gemv(im.qtype, im.wide != 0, mt, ga, st), "launch gemv");
         }
       }
+      return QI_HIP_OK;
+    case LinearPlan::kSplitGemm:
+      QI_HIP_TRY(qi::launch_gemm_split(im, v, x, m, y, sws, p.splits, reinterpret_cast<uint8_t*>(dws), st),
+                 "launch split-half gemm");
       return QI_HIP_OK;
     case LinearPlan::kF32Gemv:
       for (uint64_t m0 = 0; m0 < m; m0 += 8) {

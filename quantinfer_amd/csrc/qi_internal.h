@@ -79,6 +79,18 @@ hipError_t launch_gemv_half_records(const float* x, uint64_t k, int m, uint8_t* 
 hipError_t launch_gemv_half(int32_t qtype, bool wide, const View& w, const float* x, int m, float* y, float* part,
                             uint32_t ksplit, const uint8_t* records, hipStream_t st);
 
+// F32-mode GEMM of Q4_K / Q5_K output rows (qi_gemm_split.hip): split-half
+// activations against exact f16 codes with the sub-block scales folded in,
+// within the f32 GEMV's bars. launch_gemm_split converts the activations into
+// `records` (gemm_split_records_bytes) and runs the GEMM; with splits > 1
+// (gemm_split_splits) the partial sums [splits][m][n] go to `part` and are
+// added in order.
+bool gemm_split_supported(const Image& im);
+uint64_t gemm_split_records_bytes(uint64_t m, uint64_t k);
+uint32_t gemm_split_splits(const Image& im, uint64_t m);
+hipError_t launch_gemm_split(const Image& im, const View& v, const float* x, uint64_t m, float* y, float* part,
+                             uint32_t splits, uint8_t* records, hipStream_t st);
+
 // Row-major (blocks along N) GEMV of up to 4 activation rows, f32
 // accumulation, K split over the grid; `part` holds splits * m * n floats when
 // splits > 1.

@@ -174,9 +174,9 @@ struct UnitQ45K {
       r.s1 = reinterpret_cast<const uint16_t*>(rec + R.dmin)[col];
     }
   }
+  // the super-block's d and dmin
   template <bool W>
-  __device__ static void scales(uint32_t g, const Raw& r, float a[2], float b[2]) {
-    float d, dmin;
+  __device__ static void dmins(const Raw& r, float& d, float& dmin) {
     if constexpr (W) {
       d = __builtin_bit_cast(float, r.s0);
       dmin = __builtin_bit_cast(float, r.s1);
@@ -184,12 +184,21 @@ struct UnitQ45K {
       d = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(r.s0)));
       dmin = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(r.s1)));
     }
-    // lane group g's 24-bit field sits at bytes 3g..3g+2 of the 12 scale
-    // bytes: one byte permute from the word pair that holds it
+  }
+  // lane group g's 24-bit field sc[2g] | m[2g] << 6 | sc[2g+1] << 12 |
+  // m[2g+1] << 18, at bytes 3g..3g+2 of the 12 scale bytes: one byte permute
+  // from the word pair that holds it
+  __device__ static uint32_t field(uint32_t g, const Raw& r) {
     const uint32_t lo = g < 2 ? r.sc[0] : r.sc[1];
     const uint32_t hi = g < 2 ? r.sc[1] : r.sc[2];
     const uint32_t first = (0x5230u >> (4 * g)) & 15u;  // g = 0..3: bytes 0, 3, 2, 5 (no branch)
-    const uint32_t f = __builtin_amdgcn_perm(hi, lo, first * 0x00010101u + 0x0C020100u);
+    return __builtin_amdgcn_perm(hi, lo, first * 0x00010101u + 0x0C020100u);
+  }
+  template <bool W>
+  __device__ static void scales(uint32_t g, const Raw& r, float a[2], float b[2]) {
+    float d, dmin;
+    dmins<W>(r, d, dmin);
+    const uint32_t f = field(g, r);
     a[0] = d * static_cast<float>(f & 63u);
     b[0] = dmin * static_cast<float>((f >> 6) & 63u);
     a[1] = d * static_cast<float>((f >> 12) & 63u);

@@ -284,6 +284,54 @@ def test_f32_gemv_offset_cancellation(ctx, qtype):
         w.free()
 
 
+# F32 mode above 16 rows on Q4_K / Q5_K output rows: the split-half GEMM
+# (qi_gemm_split.hip). (K, N, rows): one unit per row (the offsets' largest
+# share, as in the cancellation case above), K parts over the grid with a
+# ragged last tile, a partial last 64-row tile, and a 512-row prompt.
+SPLIT_SHAPES = [(256, 8192, (17, 64, 200)), (12288, 1000, (40, 130)), (4096, 4096, (17, 100, 512)),
+                (1024, 24576, (65,))]
+
+
+@pytest.mark.parametrize("qtype", [qa.Q4_K, qa.Q5_K], ids=lambda q: NAMES[q])
+@pytest.mark.parametrize("shape", SPLIT_SHAPES, ids=lambda s: f"K{s[0]}-N{s[1]}")
+def test_f32_split_gemm_tolerance(ctx, qtype, shape):
+    k, n, ms = shape
+    blocks = po.make_weights(qtype, k, n, seed=4600 + qtype + k, outliers=True)
+    w = ctx.weights(qtype, qa.OUTPUT_ROWS, k, n, blocks)
+    for m in ms:
+        x = po.fill_normal(4700 + m + k, m * k).reshape(m, k)
+        y = w.linear(x, qa.MODE_F32)
+        _assert_f32(y, x, blocks, qtype, n, (k, n, m))
+        assert w.linear(x, qa.MODE_F32).tobytes() == y.tobytes()  # deterministic
+        if m >= 128:  # AUTO keeps the f16 GEMM from 128 rows; below, the same kernel
+            continue
+        assert w.linear(x, qa.MODE_AUTO).tobytes() == y.tobytes()
+    w.free()
+
+
+@pytest.mark.parametrize("qtype", [qa.Q4_K, qa.Q5_K], ids=lambda q: NAMES[q])
+def test_f32_split_gemm_wide_scales_and_scaled_rows(ctx, qtype):
+    """f32 d / dmin (not f16-exact), and activation rows of very different
+    magnitudes (1e-6 to 1e4) in one call: each (row, unit) takes its own
+    power-of-two scale. Bars (1) and (2) are relative and hold for every row;
+    the reference's absolute bound (3) is stated for N(0, 1) activations and
+    is checked on the rows of scale <= 1."""
+    k, n, m = 2048, 272, 48
+    blocks = po.make_weights(qtype, k, n, seed=4800 + qtype, outliers=True)
+    blocks["scale"] *= np.float32(1.0001)
+    blocks["min_scale"] *= np.float32(1.0001)
+    w = ctx.weights(qtype, qa.OUTPUT_ROWS, k, n, blocks)
+    assert w.info().f16_scales == 0
+    scales = 10.0 ** np.linspace(-6, 4, m)
+    x = po.fill_normal(4900, m * k).reshape(m, k) * scales.astype(np.float32)[:, None]
+    y = w.linear(x, qa.MODE_F32)
+    comp, norm, _ = _f32_checks(y, x, blocks, qtype, n)
+    assert comp <= F32_TOL and norm <= F32_TOL, (comp, norm)
+    low = scales <= 1.0
+    assert _f32_checks(y[low], x[low], blocks, qtype, n)[2]
+    w.free()
+
+
 def test_f32_gemv_unrounded_scales(ctx):
     # quantize_q8_0 output without storage rounding keeps f32 scales
     for qtype in (qa.Q8_0, qa.Q4_0):
