@@ -86,16 +86,18 @@ pub(crate) fn status(code: i32) -> Result<()> {
 }
 
 impl HipBackend {
-    /// Open HIP device `ordinal` (gfx950 only) with the AUTO arithmetic mode:
-    /// f32 GEMV below 128 activation rows, f16-operand matrix-core GEMM from
-    /// 128 rows on (within 2e-3 normwise of the CPU result).
+    /// Open HIP device `ordinal` (gfx950 only) with the F32 arithmetic mode:
+    /// every linear within 1e-5 of the CPU result at any row count (f32 GEMV
+    /// kernels; for Q4_K / Q5_K prompts of 48+ rows a matrix-core GEMM of
+    /// exact products), so greedy ids equal a CPU run's
+    /// (runtime/src/generation.rs:58-76).
     pub fn open(ordinal: usize) -> Result<Self> {
-        Self::open_with_mode(ordinal, ffi::QI_HIP_MODE_AUTO)
+        Self::open_with_mode(ordinal, ffi::QI_HIP_MODE_F32)
     }
 
-    /// `mode`: QI_HIP_MODE_EXACT reproduces CpuScalar bit for bit (for runs
-    /// whose greedy tokens must equal a CPU run); QI_HIP_MODE_F32 keeps the f32
-    /// kernels at every row count.
+    /// `mode`: QI_HIP_MODE_EXACT reproduces CpuScalar bit for bit;
+    /// QI_HIP_MODE_AUTO prefills 128+ rows on the f16-operand GEMM (faster
+    /// prompts, within 2e-3 normwise of the CPU result).
     pub fn open_with_mode(ordinal: usize, mode: i32) -> Result<Self> {
         if unsafe { ffi::qi_hip_abi_version() } != ffi::QI_HIP_ABI_VERSION {
             return Err(KernelError::Unsupported("HIP library ABI version mismatch".into()));

@@ -756,8 +756,9 @@ def e2e_step_bytes(cfg, position: int) -> int:
 def e2e_bench(repeats: int = 3, with_cpu: bool = True) -> dict:
     """Qwen3-8B-shape decode tokens/s: build the random-init model of
     quantinfer_amd.synth on the device, then `repeats` x (reset cache,
-    512-token prompt, 128 greedy decode steps) in F32 mode, whose ids equal
-    the CPU run's; the decode time is the HIP-event time of the decode steps.
+    512-token prompt, 128 greedy decode steps) in F32 mode (the decoder's
+    default), whose ids equal the CPU run's; the decode time is the HIP-event
+    time of the decode steps.
     One more run in AUTO mode (f16 GEMM prompt) is reported beside it. Both
     runs' ids are compared with the CPU run's."""
     import numpy as np
@@ -775,8 +776,9 @@ def e2e_bench(repeats: int = 3, with_cpu: bool = True) -> dict:
     build_s = time.perf_counter() - t0
     cache = model.kv_cache(E2E_PROMPT + E2E_NEW)
     prompt = synth.prompt(cfg, E2E_PROMPT)
-    # F32 mode: the configuration whose greedy ids equal the CPU run's
-    # (f32 prompt linears; the decode steps run the f32 GEMV in every mode)
+    # F32 mode: the configuration whose greedy ids equal the CPU run's (the
+    # split-half GEMM for the prompt's Q4_K linears; the decode steps run the
+    # f32 GEMV in every mode)
     model.set_mode(qa.MODE_F32)
     model.generate(cache, prompt, E2E_NEW)  # warm-up: workspaces and the decode graph
     runs, tokens = [], None
@@ -833,7 +835,7 @@ def e2e_bench(repeats: int = 3, with_cpu: bool = True) -> dict:
         "config": {"workload": "qwen3_8b_shape_decode_prompt512_new128", "layers": 36,
                    "hidden": 4096, "heads": 32, "kv_heads": 8, "head_dim": 128,
                    "intermediate": 12288, "vocab": 151936, "prompt_tokens": E2E_PROMPT,
-                   "decode_steps": steps, "mode": "f32 (f32 GEMV for the prompt and the decode steps)",
+                   "decode_steps": steps, "mode": "f32, the default (split-half matrix-core GEMM for the prompt, f32 GEMV for the decode steps)",
                    "repeats": repeats, "device": device},
         "prefill_tok_s": round(E2E_PROMPT / (prefill_ms * 1e-3), 1),
         "prefill_ms": round(prefill_ms, 3),

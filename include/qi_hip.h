@@ -58,8 +58,10 @@ typedef int32_t qi_hip_status;
 /* Arithmetic modes of a linear call.
  * AUTO  F32 below 128 activation rows, MFMA at 128 and above (the decode /
  *       prefill split of the kernels).
- * F32   f32 accumulation of f32 products for any M (GEMV kernels), judged by
- *       tolerance against the CPU reference.
+ * F32   f32-accurate for any M, judged by tolerance (1e-5) against the CPU
+ *       reference: f32 GEMV kernels, and for Q4_K / Q5_K output rows from 48
+ *       rows a matrix-core GEMM of exact products (activations split into two
+ *       f16 halves, weight codes exact in f16) accumulated in f32.
  * EXACT bit-identical to CpuScalar: per output, acc = acc + x[k]*w[k] in f32,
  *       k ascending, no FMA (backends/cpu/src/matmul.rs:146-157, 319-330).
  * MFMA  f16 operands into f32 matrix-core accumulation (prefill GEMM). */
@@ -297,8 +299,9 @@ qi_hip_status qi_hip_qwen3_set_layer(qi_hip_qwen3 *model, uint32_t index,
  * runtime/src/qwen3/loader.rs:47-61 does). */
 qi_hip_status qi_hip_qwen3_set_output(qi_hip_qwen3 *model, const float *final_norm,
                                       const qi_hip_linear_weight *lm_head);
-/* Arithmetic mode of every linear layer (QI_HIP_MODE_*; default AUTO: GEMV for
- * decode, MFMA GEMM for prompt chunks of 128+ tokens). */
+/* Arithmetic mode of every linear layer (QI_HIP_MODE_*). Default F32, whose
+ * greedy ids equal the CPU run's (runtime/src/generation.rs:58-76); AUTO
+ * prefills prompt chunks of 128+ tokens on the f16-operand GEMM instead. */
 qi_hip_status qi_hip_qwen3_set_mode(qi_hip_qwen3 *model, int32_t mode);
 void qi_hip_qwen3_free(qi_hip_qwen3 *model);
 

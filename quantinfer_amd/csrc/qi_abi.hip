@@ -186,7 +186,11 @@ constexpr uint32_t kHalfMinRows = 9;
 
 // Rows from which Q4_K / Q5_K output rows take the split-half GEMM
 // (qi_gemm_split.hip) in F32 mode, and in AUTO mode below the f16 GEMM's 128.
-constexpr uint64_t kSplitMinRows = 17;
+// Below it the 16-row GEMV chunks are faster. Measured on MI355X, us per
+// call, GEMV chunks / split GEMM: Q4_K 4096x6144 M=17 24.6 / 39.6, M=32
+// 33.7 / 41.5, M=48 47.9 / ~43, M=64 61.3 / 45.3; 4096x24576 M=32 71.9 /
+// 96.7, M=64 135.8 / 102.8; 12288x4096 M=32 45.3 / 44.9.
+constexpr uint64_t kSplitMinRows = 48;
 
 qi_hip_status plan_linear(const Image& im, uint64_t m, int32_t mode, LinearPlan* p) {
   if (mode < QI_HIP_MODE_AUTO || mode > QI_HIP_MODE_MFMA)

@@ -874,7 +874,7 @@ uint32_t elems_per_block(int32_t qtype) {
 struct qi_hip_qwen3 {
   qi_hip_ctx* ctx = nullptr;
   qi_hip_qwen3_config cfg{};
-  int32_t mode = QI_HIP_MODE_AUTO;
+  int32_t mode = QI_HIP_MODE_F32;  // token-identical to the CPU run; AUTO trades that for prompt speed
   uint64_t id = 0;
   std::vector<Layer> layers;
   float* embedding = nullptr;

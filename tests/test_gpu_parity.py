@@ -203,7 +203,7 @@ def test_reference_known_answers_on_gpu(ctx):
 # ---------------------------------------------------------- F32 GEMV path
 
 @pytest.mark.parametrize("qtype", ALL_Q, ids=lambda q: NAMES[q])
-@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 8, 11, 16, 17, 40])
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 8, 11, 16, 17, 40, 64])
 def test_f32_gemv_tolerance_small(ctx, qtype, m):
     k, n = 1024, 70  # n not a multiple of the row tile: exercises the ragged tile
     blocks = po.make_weights(qtype, k, n, seed=4000 + qtype, outliers=True)
@@ -284,11 +284,11 @@ def test_f32_gemv_offset_cancellation(ctx, qtype):
         w.free()
 
 
-# F32 mode above 16 rows on Q4_K / Q5_K output rows: the split-half GEMM
+# F32 mode from 48 rows on Q4_K / Q5_K output rows: the split-half GEMM
 # (qi_gemm_split.hip). (K, N, rows): one unit per row (the offsets' largest
 # share, as in the cancellation case above), K parts over the grid with a
 # ragged last tile, a partial last 64-row tile, and a 512-row prompt.
-SPLIT_SHAPES = [(256, 8192, (17, 64, 200)), (12288, 1000, (40, 130)), (4096, 4096, (17, 100, 512)),
+SPLIT_SHAPES = [(256, 8192, (48, 64, 200)), (12288, 1000, (48, 130)), (4096, 4096, (50, 100, 512)),
                 (1024, 24576, (65,))]
 
 

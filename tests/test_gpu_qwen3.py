@@ -63,7 +63,7 @@ def test_forward_logits_match_oracle(qa, small, mode):
         assert err <= TOL_F32, (mode, step, err)
         assert nxt == int(np.argmax(logits))
         assert cache.length == ref.length
-    dev.set_mode(qa.MODE_AUTO)
+    dev.set_mode(qa.MODE_F32)  # back to the default
 
 
 def test_generate_tokens_identical_to_cpu(qa, small):
@@ -80,7 +80,24 @@ def test_generate_tokens_identical_to_cpu(qa, small):
     t = dev.last_timing()
     assert t.prompt_tokens == 20 and t.decode_steps == 24
     assert t.prefill_ms > 0 and t.decode_ms > 0
-    dev.set_mode(qa.MODE_AUTO)
+    dev.set_mode(qa.MODE_F32)  # back to the default
+
+
+def test_default_mode_prompt_on_split_gemm_identical_to_cpu(qa, ctx):
+    """A freshly created decoder runs in its default mode, F32: a 100-token
+    prompt takes the split-half GEMM (48+ rows of Q4_K), and the greedy ids
+    equal the CPU run's."""
+    cfg = small_config(max_position_embeddings=256)
+    w = Qwen3Weights(cfg, seed=0x5EED0011)
+    dev = w.device_model(ctx)
+    toks = prompt(cfg, 100, seed=17)
+    print("qwen3 default mode prompt=100 new=16", flush=True)
+    cache = dev.kv_cache(128)
+    got = dev.generate(cache, toks, 16)
+    want = w.oracle_model(128).generate(toks, 16)
+    print(f"  gpu {got}\n  cpu {want}", flush=True)
+    assert got == want
+    dev.free()
 
 
 @pytest.mark.parametrize("env", ["QI_HIP_QWEN3_UNFUSED", "QI_HIP_QWEN3_EAGER"])
@@ -123,7 +140,7 @@ def test_generate_matches_forward_loop(qa, small):
     cache.reset()
     assert cache.length == 0
     assert dev.generate(cache, toks, 10) == gen
-    dev.set_mode(qa.MODE_AUTO)
+    dev.set_mode(qa.MODE_F32)  # back to the default
 
 
 def test_prefill_gemm_and_chunked_prompt(qa, small):
@@ -201,7 +218,7 @@ def test_eos_stops_generation(qa, small):
     assert dev.generate(cache, toks, 12, eos=eos) == gen[:first + 1]
     # the EOS itself is not forwarded (generation.rs:189-195)
     assert cache.length == 8 + first
-    dev.set_mode(qa.MODE_AUTO)
+    dev.set_mode(qa.MODE_F32)  # back to the default
 
 
 def test_head_dim_128_group_4(qa, ctx):

@@ -16,7 +16,8 @@ byte for byte (tests/test_abi_cpu.py); the test first checks the rebuilt
 weights' digest against the fixture's, so a mismatch in the inputs cannot
 pass for a mismatch in the decoder.
 
-F32 mode (f32 GEMV linears for the prompt and the steps) must give the CPU
+F32 mode, the decoder's default (the split-half matrix-core GEMM for the
+512-row prompt's Q4_K linears, f32 GEMV for the steps), must give the CPU
 run's ids exactly. AUTO mode (the f16-operand GEMM for the 512-row prompt)
 is run beside it: measured on MI355X it leaves the CPU run at step 1, whose
 CPU top-2 gap is 5e-4 of the logit scale, inside the f16 GEMM's error; the
