@@ -362,13 +362,17 @@ def library_f16_gemm(m: int, k: int, n: int, steps: int = 20) -> dict:
             "unit": "TFLOP/s", "frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4), "ms": round(ms, 5)}
 
 
-def gemm_bench(qtype: int, m: int, k: int, n: int, steps: int, warmup: int) -> dict:
-    """Prefill GEMM (MFMA mode, f16 operands, f32 accumulation): `steps`
-    back-to-back linear calls on resident inputs (two weight copies
-    alternating), event-timed on the launch stream; each call is the f16
-    activation conversion plus the GEMM."""
+def gemm_bench(qtype: int, m: int, k: int, n: int, steps: int, warmup: int, mode: str = "mfma") -> dict:
+    """Prefill GEMM: `steps` back-to-back linear calls on resident inputs (two
+    weight copies alternating), event-timed on the launch stream. mode "mfma":
+    the f16-operand GEMM (each call the f16 activation conversion plus the
+    GEMM); mode "f32": F32 mode, which for Q4_K / Q5_K from 48 rows is the
+    split-half GEMM (each call the activation halves plus the GEMM, and the
+    split-K sum where the shape takes one), within the f32 GEMV's bars."""
     import quantinfer_amd as qa
     from quantinfer_amd import hiprt
+
+    qmode = {"mfma": qa.MODE_MFMA, "f32": qa.MODE_F32}[mode]
 
     ctx = qa.Context(0)
     blocks = weight_blocks(qtype, k, n, seed=0x5EED0010 + qtype)
@@ -377,12 +381,12 @@ def gemm_bench(qtype: int, m: int, k: int, n: int, steps: int, warmup: int) -> d
     y = hiprt.DeviceBuffer(m * n * 4)
     stream = hiprt.Stream()
     for i in range(warmup):
-        weights[i % 2].linear_device(x.ptr, m, y.ptr, qa.MODE_MFMA, stream.handle)
+        weights[i % 2].linear_device(x.ptr, m, y.ptr, qmode, stream.handle)
     stream.synchronize()
     start, end = hiprt.Event(), hiprt.Event()
     start.record(stream)
     for i in range(steps):
-        weights[i % 2].linear_device(x.ptr, m, y.ptr, qa.MODE_MFMA, stream.handle)
+        weights[i % 2].linear_device(x.ptr, m, y.ptr, qmode, stream.handle)
     end.record(stream)
     stream.synchronize()
     ms = start.elapsed_ms(end) / steps
@@ -395,19 +399,25 @@ def gemm_bench(qtype: int, m: int, k: int, n: int, steps: int, warmup: int) -> d
     ctx.close()
     tflops = 2.0 * m * n * k / (ms * 1e-3) / 1e12
     qname = QNAME[qtype]
+    f32 = mode == "f32"
     return {
         "metric": "prefill GEMM TFLOP/s (% of dense f16 MFMA peak)",
         "value": round(tflops, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": steps,
         "warmup": warmup, "ms_per_step": round(ms, 5), "higher_is_better": True,
-        "scaling": "weak", "vs_baseline": None, "dtype": "f16 operands, f32 accumulation",
+        "scaling": "weak", "vs_baseline": None,
+        "dtype": ("f32 activations as two f16 halves x exact f16 codes, f32 accumulation" if f32
+                  else "f16 operands, f32 accumulation"),
         "data": f"synthetic: N(0,0.02^2) weights{' with 0.5% outliers' if qtype >= 3 else ''} quantized "
                 f"to {qname} (qi_hip_quantize); x ~ N(0,1)",
         "config": {"workload": f"{qname}_gemm_output_rows_m{m}_k{k}_n{n}", "qtype": qname,
-                   "m": m, "k": k, "n": n, "mode": "mfma",
-                   "step": "one linear call: f16 activation conversion + GEMM", "device": name},
+                   "m": m, "k": k, "n": n, "mode": mode,
+                   "step": ("one linear call: activation halves + split-half GEMM" if f32
+                            else "one linear call: f16 activation conversion + GEMM"), "device": name},
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": MFMA_F16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4),
                      "traffic": None},
+        **({"note": "two f16 matrix instructions per product (the activation halves): the useful "
+                    "rate is bounded by half the dense f16 peak"} if f32 else {}),
     }
 
 
@@ -919,6 +929,8 @@ def main():
     ap.add_argument("--cpu-simd", action="store_true",
                     help="only the CPU table: scalar and cpu-simd Q8_0/Q4_0 kernels, one core")
     ap.add_argument("--qtype", default="q4_k", help="gemv/gemm: q8_0, q4_0, q4_k, q5_k or q6_k")
+    ap.add_argument("--mode", choices=["mfma", "f32"], default="mfma",
+                    help="gemm: the f16-operand GEMM (mfma) or F32 mode's split-half GEMM (f32; Q4_K/Q5_K)")
     ap.add_argument("--mkn", default=None,
                     help="M,K,N (gemm default 2048,4096,12288; gemv default 1,4096,14336)")
     args = ap.parse_args()
@@ -936,7 +948,7 @@ def main():
     qt = {"q8_0": 1, "q4_0": 2, "q4_k": 3, "q5_k": 4, "q6_k": 5}[args.qtype]
     if args.workload == "gemm":
         m, k, n = (int(v) for v in (args.mkn or "2048,4096,12288").split(","))
-        print(json.dumps(gemm_bench(qt, m, k, n, max(args.steps, 20), args.warmup)))
+        print(json.dumps(gemm_bench(qt, m, k, n, max(args.steps, 20), args.warmup, args.mode)))
         return
     if args.workload == "e2e":
         print(json.dumps(e2e_bench(with_cpu=not args.no_cpu)))
@@ -987,6 +999,8 @@ def main():
             # the GEMM objects take their own counts: 20 warm-up calls (about
             # 6 ms, so that the clocks settle) and 50 timed ones
             line["gemm"] = {QNAME[q]: gemm_bench(q, 2048, 4096, 12288, 50, 20) for q in (3, 1)}
+            # F32 mode at the same shape: the split-half GEMM (token-identical prompts)
+            line["gemm_f32"] = {"q4_k": gemm_bench(3, 2048, 4096, 12288, 20, 5, "f32")}
         if not args.no_configs:
             line["configs"] = configs_table(min(args.steps, 10), min(args.warmup, 3), not args.no_cpu)
         if not args.no_e2e:

@@ -18,8 +18,10 @@
 // accumulator, 16 instructions per 16 x 16 block), and per unit
 //   sum_k x_k w_k = 2^-s * (d * C + sum_j S_j * (-b'_j)),
 // C the unit's matrix sum, S_j the sum of x' over sub-block j: the eight
-// offsets go through two v_mfma_f32_16x16x4_f32 (window sums x per-output
-// offsets), then two f32 fmas per output fold the unit into the running sum.
+// offsets go through one more f16 instruction (window sums and offsets each
+// as two f16 halves, scaled by powers of two into f16 range; the three
+// products that carry 22 bits), then three f32 operations per output fold
+// the unit into the running sum.
 // The rounding is that of f32 sums of exact products plus x to 22 bits, as in
 // the GEMV, so the same bars hold at every K.
 //
@@ -110,8 +112,19 @@ struct SplitArgs {
 struct SplitScales {
   float d;
   h2 sc[2], c[2];
-  float nb[2];
+  uint4 bo;  // the offsets' B operand: -b' of windows 2g, 2g+1 as f16 halves, scaled by 2^e
+  float fo;  // 2^(6 - e): the offsets' matrix sum back to the f32 scale
 };
+
+// x as hi (x truncated to 11 significant bits, exact in f16) + lo (the rest
+// rounded to f16)
+__device__ __forceinline__ void split_f16(float x, float& hi, float& lo) {
+  hi = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, x) & 0xFFFFE000u);
+  lo = x - hi;
+}
+__device__ __forceinline__ uint32_t pack_rtz(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(a, b));
+}
 
 template <int QT, bool WIDE>
 __device__ __forceinline__ void split_scales(const typename Unit<QT>::Raw& r, uint32_t g, SplitScales& o) {
@@ -121,6 +134,14 @@ __device__ __forceinline__ void split_scales(const typename Unit<QT>::Raw& r, ui
   U::template dmins<WIDE>(r, d, dmin);
   const uint32_t f = U::field(g, r);
   o.d = d;
+  // |b'| <= max(d sc / 2, dmin m) < max(32 d, 64 dmin) = B: scaled by 2^e
+  // with B 2^e < 2^15 the offsets fit f16 (the same e in every lane group of
+  // the output, as its four lane groups' offsets enter one sum)
+  const float bound = fmaxf(32.0f * d, 64.0f * dmin);
+  const int eb = bound > 0.0f ? __builtin_amdgcn_frexp_expf(bound) : 0;
+  const float up = __builtin_ldexpf(1.0f, 15 - eb);
+  o.fo = __builtin_ldexpf(1.0f, eb - 9);
+  float nh[2], nl[2];
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     const float sc = static_cast<float>((f >> (12 * h)) & 63u), mn = static_cast<float>((f >> (12 * h + 6)) & 63u);
@@ -128,10 +149,13 @@ __device__ __forceinline__ void split_scales(const typename Unit<QT>::Raw& r, ui
     // any integer z keeps the arithmetic exact; the nearest one keeps b'
     // small (a = 0 gives z = kQMax or 0 and b' = b, with codes times sc = 0)
     const float z = fminf(fmaxf(rintf(b * __builtin_amdgcn_rcpf(a)), 0.0f), kQMax);
-    o.nb[h] = fmaf(a, z, -b);
+    split_f16(fmaf(a, z, -b) * up, nh[h], nl[h]);
     o.sc[h] = splat(sc);
     o.c[h] = splat(h == 0 ? -(1024.0f + z) : -(64.0f + z));
   }
+  // slots 8g..8g+7: hi(2g), hi(2g+1), lo(2g), lo(2g+1), hi(2g), hi(2g+1), 0, 0
+  const uint32_t hh = pack_rtz(nh[0], nh[1]);
+  o.bo = make_uint4(hh, pack_rtz(nl[0], nl[1]), hh, 0u);
 }
 
 // The B operand of step t: the 8 codes of the lane's slice as sc (q - z), in
@@ -256,16 +280,23 @@ __global__ __launch_bounds__(kSThreads) void gemm_split_kernel(SplitArgs a) {
     const float* const unsc = reinterpret_cast<const float*>(st + kSUnsc);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      // offsets: A = S[row c][window 2g + h], B = -b'[window 2g + h][output c]
-      const float s0 = sums[(2 * g) * kSRows + 16 * i + c], s1 = sums[(2 * g + 1) * kSRows + 16 * i + c];
+      // offsets on one f16 instruction: lane (row c, lane group g) supplies
+      // S / 64 of windows 2g, 2g+1 (|S| < 2^20) as halves in the slots
+      // hi, hi, hi, hi, lo, lo, 0, 0 against the B slots of split_scales:
+      // S_hi b_hi + S_hi b_lo + S_lo b_hi of both windows (22 bits of each)
+      float sh[2], sl[2];
+      split_f16(sums[(2 * g) * kSRows + 16 * i + c] * 0x1p-6f, sh[0], sl[0]);
+      split_f16(sums[(2 * g + 1) * kSRows + 16 * i + c] * 0x1p-6f, sh[1], sl[1]);
+      const uint32_t ah = pack_rtz(sh[0], sh[1]);
+      const h8 ao = __builtin_bit_cast(h8, make_uint4(ah, ah, pack_rtz(sl[0], sl[1]), 0u));
       const float4 us = *reinterpret_cast<const float4*>(unsc + 16 * i + 4 * g);
       const float uu[4] = {us.x, us.y, us.z, us.w};
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        v4f off = __builtin_amdgcn_mfma_f32_16x16x4f32(s0, sc[j].nb[0], zero, 0, 0, 0);
-        off = __builtin_amdgcn_mfma_f32_16x16x4f32(s1, sc[j].nb[1], off, 0, 0, 0);
+        const v4f off = __builtin_amdgcn_mfma_f32_16x16x32_f16(ao, __builtin_bit_cast(h8, sc[j].bo), zero, 0, 0, 0);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) total[i][j][r] = fmaf(uu[r], fmaf(sc[j].d, tmp[i][j][r], off[r]), total[i][j][r]);
+        for (int r = 0; r < 4; ++r)
+          total[i][j][r] = fmaf(uu[r], fmaf(sc[j].fo, off[r], sc[j].d * tmp[i][j][r]), total[i][j][r]);
       }
     }
     if (u + 1 < ue) {
