@@ -88,8 +88,8 @@ pub(crate) fn status(code: i32) -> Result<()> {
 impl HipBackend {
     /// Open HIP device `ordinal` (gfx950 only) with the F32 arithmetic mode:
     /// every linear within 1e-5 of the CPU result at any row count (f32 GEMV
-    /// kernels; for Q4_K / Q5_K prompts of 48+ rows a matrix-core GEMM of
-    /// exact products), so greedy ids equal a CPU run's
+    /// kernels; for prompts of 48+ rows a matrix-core GEMM of exact
+    /// products), so greedy ids equal a CPU run's
     /// (runtime/src/generation.rs:58-76).
     pub fn open(ordinal: usize) -> Result<Self> {
         Self::open_with_mode(ordinal, ffi::QI_HIP_MODE_F32)

@@ -59,9 +59,10 @@ typedef int32_t qi_hip_status;
  * AUTO  F32 below 128 activation rows, MFMA at 128 and above (the decode /
  *       prefill split of the kernels).
  * F32   f32-accurate for any M, judged by tolerance (1e-5) against the CPU
- *       reference: f32 GEMV kernels, and for Q4_K / Q5_K output rows from 48
- *       rows a matrix-core GEMM of exact products (activations split into two
- *       f16 halves, weight codes exact in f16) accumulated in f32.
+ *       reference: f32 GEMV kernels, and for output rows (K a multiple of
+ *       256) from 48 rows a matrix-core GEMM of exact products (activations
+ *       split into two f16 halves, weights as exact f16 codes or two f16
+ *       halves) accumulated in f32.
  * EXACT bit-identical to CpuScalar: per output, acc = acc + x[k]*w[k] in f32,
  *       k ascending, no FMA (backends/cpu/src/matmul.rs:146-157, 319-330).
  * MFMA  f16 operands into f32 matrix-core accumulation (prefill GEMM). */

@@ -184,8 +184,8 @@ struct LinearPlan {
 // 4096x24576 M=16 49.6 / 38.3.
 constexpr uint32_t kHalfMinRows = 9;
 
-// Rows from which Q4_K / Q5_K output rows take the split-half GEMM
-// (qi_gemm_split.hip) in F32 mode, and in AUTO mode below the f16 GEMM's 128.
+// Rows from which output rows take the split-half GEMM (qi_gemm_split.hip)
+// in F32 mode, and in AUTO mode below the f16 GEMM's 128.
 // Below it the 16-row GEMV chunks are faster. Measured on MI355X, us per
 // call, GEMV chunks / split GEMM: Q4_K 4096x6144 M=17 24.6 / 39.6, M=32
 // 33.7 / 41.5, M=48 47.9 / ~43, M=64 61.3 / 45.3; 4096x24576 M=32 71.9 /

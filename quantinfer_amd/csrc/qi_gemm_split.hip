@@ -1,7 +1,9 @@
 // Prefill GEMM of F32 mode on the f16 matrix cores (v_mfma_f32_16x16x32_f16):
-// Q4_K and Q5_K output rows, K a multiple of 256, any M (planned for prompts,
-// above 16 rows). Its results meet the f32 GEMV's bars (1e-5 componentwise
-// and normwise), unlike the f16-operand GEMM of qi_gemm.hip.
+// output rows of every format (Q8_0 / Q4_0 with f16 block scales), K a
+// multiple of 256, any M (planned for prompts of 48 rows and more). Its
+// results meet the f32 GEMV's bars (1e-5 componentwise and normwise), unlike
+// the f16-operand GEMM of qi_gemm.hip. The arithmetic below is that of Q4_K /
+// Q5_K; the other formats' weights enter as two f16 planes (SplitFmt).
 //
 // Arithmetic (the split halves of the 9-16 row GEMV, qi_gemv_half.hip, with
 // the sub-block scales folded into the codes). Per (row, unit of 256
@@ -59,7 +61,6 @@ using namespace half;
 
 constexpr int kSThreads = 256;
 constexpr uint32_t kSRows = 64;   // activation rows of a workgroup (4 row tiles)
-constexpr uint32_t kSTiles = 16;  // 16-output tiles of a workgroup (4 per wavefront)
 constexpr uint32_t kSHalf = 8 * 4 * 64 * 16;            // one half plane: [step][row tile][lane] x 16 B
 constexpr uint32_t kSSums = kSHalf * 2;                  // offset of the window sums [window][row] (f32)
 constexpr uint32_t kSUnsc = kSSums + 8 * kSRows * 4;     // offset of the unscales [row] (f32)
@@ -69,7 +70,13 @@ constexpr uint32_t kSCUs = 256;                          // compute units of an 
 static_assert(kSStage % 16 == 0 && 2 * kSStage <= 160 * 1024, "two stages fit LDS");
 
 // One (64-row tile, unit) per workgroup; each half wavefront converts one row
-// per pass (item 4 w + s of its 32 lanes: window w, slice s) into the stage.
+// per pass (item 4 w + s of its 32 lanes: window w, slice s, elements
+// 32 w + 8 s + [0, 8)) into the stage, at the (step, lane group) whose
+// weights cover those elements: for Q8_0 / Q4_0 / Q4_K / Q5_K lane group g
+// holds windows 2g, 2g + 1 (step t: window 2g + t / 4, slice t % 4); Q6_K
+// (ORDER6) lane group g = 2 ip + c elements 128 ip + 32 c + 64 (t / 4) +
+// 8 (t % 4) + [0, 8) (Unit<kQ6_K>).
+template <bool ORDER6>
 __global__ __launch_bounds__(256) void split_prep_kernel(const float* __restrict__ x, uint32_t K, uint64_t M,
                                                          uint8_t* __restrict__ rec) {
   const uint32_t units = K / 256;
@@ -77,7 +84,9 @@ __global__ __launch_bounds__(256) void split_prep_kernel(const float* __restrict
   const uint32_t u = blockIdx.x % units;
   uint8_t* const st = rec + (mt * units + u) * kSStage;
   const uint32_t i32 = threadIdx.x & 31, w = i32 >> 2, s = i32 & 3, hw = threadIdx.x >> 5;
-  const uint32_t t = 4 * (w & 1) + s, g = w >> 1;  // the step and lane group that use this slice
+  // the step and lane group that use this slice
+  const uint32_t t = ORDER6 ? 4 * ((w >> 1) & 1) + s : 4 * (w & 1) + s;
+  const uint32_t g = ORDER6 ? 2 * (w >> 2) + (w & 1) : w >> 1;
   float* const sums = reinterpret_cast<float*>(st + kSSums);
   float* const unsc = reinterpret_cast<float*>(st + kSUnsc);
 #pragma unroll 1
@@ -106,14 +115,34 @@ struct SplitArgs {
   float* part;  // [splits][m][n] when splits > 1
 };
 
-// Per (output, sub-block) factors of one unit for lane group g: the scale
-// d, the sub-blocks' integer scales as f16 pairs, the centring constants and
-// the offsets -b'.
+// Per-format choices. Q4_K / Q5_K fold the 6-bit sub-block scale into an
+// exact f16 code (one weight plane, offsets through the window sums). The
+// other formats' per-block factors do not fold exactly into one f16 number
+// (Q8_0 d q: up to 19 bits; Q6_K sc (q - 32): up to 12), so the weight enters
+// as two f16 planes, hi = f16(w') and lo = w' - hi (exact, one fused
+// multiply-add), and every product takes three instructions: x_hi w_hi,
+// x_lo w_hi, x_hi w_lo (x_lo w_lo, below 2^-22 of the product, is left out).
+// Q8_0 / Q4_0: w' = 2^e d (q - bias), e per (output, unit) from the largest
+// of its eight block scales; Q6_K: w' = sc (q - 32), d applied in the
+// combine. Wavefronts hold 4 output tiles, 2 where the weight records are
+// large (Q8_0, Q6_K) so that two units of them fit in registers.
+template <int QT>
+struct SplitFmt {
+  static constexpr bool kK45 = QT == kQ4_K || QT == kQ5_K;
+  static constexpr int kPlanes = kK45 ? 1 : 2;
+  static constexpr int kTiles = (QT == kQ8_0 || QT == kQ6_K) ? 2 : 4;  // per wavefront
+  static constexpr bool kOrder6 = QT == kQ6_K;
+};
+
+// Per (output, unit) factors for lane group g. K45: the unit's d, the
+// windows' integer scales and centring constants, the offsets' operand.
+// Q8_0 / Q4_0: d = 2^-e, sc[h] = 2^e times block 2g + h's scale. Q6_K: d, and
+// sc[] the lane group's four sub-scales.
 struct SplitScales {
   float d;
-  h2 sc[2], c[2];
-  uint4 bo;  // the offsets' B operand: -b' of windows 2g, 2g+1 as f16 halves, scaled by 2^e
-  float fo;  // 2^(6 - e): the offsets' matrix sum back to the f32 scale
+  h2 sc[4], c[2];
+  uint4 bo;  // K45: the offsets' B operand: -b' of windows 2g, 2g+1 as f16 halves, scaled by 2^e
+  float fo;  // K45: 2^(6 - e), the offsets' matrix sum back to the f32 scale
 };
 
 // x as hi (x truncated to 11 significant bits, exact in f16) + lo (the rest
@@ -125,76 +154,123 @@ __device__ __forceinline__ void split_f16(float x, float& hi, float& lo) {
 __device__ __forceinline__ uint32_t pack_rtz(float a, float b) {
   return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(a, b));
 }
+__device__ __forceinline__ float f16_bits(uint32_t v) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(v & 0xFFFFu)));
+}
 
 template <int QT, bool WIDE>
 __device__ __forceinline__ void split_scales(const typename Unit<QT>::Raw& r, uint32_t g, SplitScales& o) {
   using U = Unit<QT>;
-  constexpr float kQMax = QT == kQ5_K ? 31.0f : 15.0f;
-  float d, dmin;
-  U::template dmins<WIDE>(r, d, dmin);
-  const uint32_t f = U::field(g, r);
-  o.d = d;
-  // |b'| <= max(d sc / 2, dmin m) < max(32 d, 64 dmin) = B: scaled by 2^e
-  // with B 2^e < 2^15 the offsets fit f16 (the same e in every lane group of
-  // the output, as its four lane groups' offsets enter one sum)
-  const float bound = fmaxf(32.0f * d, 64.0f * dmin);
-  const int eb = bound > 0.0f ? __builtin_amdgcn_frexp_expf(bound) : 0;
-  const float up = __builtin_ldexpf(1.0f, 15 - eb);
-  o.fo = __builtin_ldexpf(1.0f, eb - 9);
-  float nh[2], nl[2];
+  if constexpr (QT == kQ8_0 || QT == kQ4_0) {
+    static_assert(!WIDE, "f32 block scales are not exact in f16");
+    const float d0 = f16_bits(r.s0), d1 = f16_bits(r.s0 >> 16);
+    // the largest scale of the output's eight blocks (two per lane group)
+    uint32_t all[4];
+    gather4u(__builtin_bit_cast(uint32_t, fmaxf(fabsf(d0), fabsf(d1))), all);
+    const float dm = fmaxf(fmaxf(__builtin_bit_cast(float, all[0]), __builtin_bit_cast(float, all[1])),
+                           fmaxf(__builtin_bit_cast(float, all[2]), __builtin_bit_cast(float, all[3])));
+    // 2^e d_max in [2^7, 2^8): |w'| < 2^15 (Q8_0 codes up to 128 in magnitude)
+    const int e = dm > 0.0f ? 8 - __builtin_amdgcn_frexp_expf(dm) : 0;
+    o.d = __builtin_ldexpf(1.0f, -e);
+    o.sc[0] = splat(__builtin_ldexpf(d0, e));
+    o.sc[1] = splat(__builtin_ldexpf(d1, e));
+  } else if constexpr (QT == kQ6_K) {
+    o.d = WIDE ? __builtin_bit_cast(float, r.d) : f16_bits(r.d);
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const float sc = static_cast<float>((f >> (12 * h)) & 63u), mn = static_cast<float>((f >> (12 * h + 6)) & 63u);
-    const float a = d * sc, b = dmin * mn;  // both exact in f32
-    // any integer z keeps the arithmetic exact; the nearest one keeps b'
-    // small (a = 0 gives z = kQMax or 0 and b' = b, with codes times sc = 0)
-    const float z = fminf(fmaxf(rintf(b * __builtin_amdgcn_rcpf(a)), 0.0f), kQMax);
-    split_f16(fmaf(a, z, -b) * up, nh[h], nl[h]);
-    o.sc[h] = splat(sc);
-    o.c[h] = splat(h == 0 ? -(1024.0f + z) : -(64.0f + z));
+    for (int i = 0; i < 4; ++i) o.sc[i] = splat(static_cast<float>(static_cast<int32_t>(r.sc << (24 - 8 * i)) >> 24));
+  } else {
+    constexpr float kQMax = QT == kQ5_K ? 31.0f : 15.0f;
+    float d, dmin;
+    U::template dmins<WIDE>(r, d, dmin);
+    const uint32_t f = U::field(g, r);
+    o.d = d;
+    // |b'| <= max(d sc / 2, dmin m) < max(32 d, 64 dmin) = B: scaled by 2^e
+    // with B 2^e < 2^15 the offsets fit f16 (the same e in every lane group of
+    // the output, as its four lane groups' offsets enter one sum)
+    const float bound = fmaxf(32.0f * d, 64.0f * dmin);
+    const int eb = bound > 0.0f ? __builtin_amdgcn_frexp_expf(bound) : 0;
+    const float up = __builtin_ldexpf(1.0f, 15 - eb);
+    o.fo = __builtin_ldexpf(1.0f, eb - 9);
+    float nh[2], nl[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const float sc = static_cast<float>((f >> (12 * h)) & 63u), mn = static_cast<float>((f >> (12 * h + 6)) & 63u);
+      const float a = d * sc, b = dmin * mn;  // both exact in f32
+      // any integer z keeps the arithmetic exact; the nearest one keeps b'
+      // small (a = 0 gives z = kQMax or 0 and b' = b, with codes times sc = 0)
+      const float z = fminf(fmaxf(rintf(b * __builtin_amdgcn_rcpf(a)), 0.0f), kQMax);
+      split_f16(fmaf(a, z, -b) * up, nh[h], nl[h]);
+      o.sc[h] = splat(sc);
+      o.c[h] = splat(h == 0 ? -(1024.0f + z) : -(64.0f + z));
+    }
+    // slots 8g..8g+7: hi(2g), hi(2g+1), lo(2g), lo(2g+1), hi(2g), hi(2g+1), 0, 0
+    const uint32_t hh = pack_rtz(nh[0], nh[1]);
+    o.bo = make_uint4(hh, pack_rtz(nl[0], nl[1]), hh, 0u);
   }
-  // slots 8g..8g+7: hi(2g), hi(2g+1), lo(2g), lo(2g+1), hi(2g), hi(2g+1), 0, 0
-  const uint32_t hh = pack_rtz(nh[0], nh[1]);
-  o.bo = make_uint4(hh, pack_rtz(nl[0], nl[1]), hh, 0u);
 }
 
-// The B operand of step t: the 8 codes of the lane's slice as sc (q - z), in
-// the operand order (0, 2), (1, 3), (4, 6), (5, 7).
+// The B operand(s) of step t: the lane's 8 codes in the operand order (0, 2),
+// (1, 3), (4, 6), (5, 7). K45: sc (q - z), one plane. Other formats: the
+// centred code c times the factor f as hi = f16(c f) and lo = c f - hi.
 template <int QT>
 __device__ __forceinline__ void split_codes(const typename Unit<QT>::Raw& r, uint32_t g, int t, const SplitScales& s,
-                                            uint32_t out[4]) {
+                                            uint32_t out[SplitFmt<QT>::kPlanes][4]) {
   const int h = t >> 2, p = t & 3;
-  const uint4 q = r.q[p >> 1];
-  const uint32_t lo = (p & 1) ? q.z : q.x, hi = (p & 1) ? q.w : q.y;
-  if (h == 0) raw_pairs<kMaskLo>(lo, hi, lo >> 8, hi >> 8, out);
-  else raw_pairs<kMaskHi>(lo, hi, lo >> 8, hi >> 8, out);
-  if constexpr (QT == kQ5_K) {
-    // bit 2g + h of qh byte e is bit 4 of element e's code
-    const uint4 qh = r.h[p >> 1];
-    const uint32_t bit = 2 * g + static_cast<uint32_t>(h);
-    const uint32_t l = ((p & 1) ? qh.z : qh.x) >> bit, u = ((p & 1) ? qh.w : qh.y) >> bit;
-    if (h == 0) {
-      out[0] |= (l << 4) & 0x00100010u;
-      out[1] |= (l >> 4) & 0x00100010u;
-      out[2] |= (u << 4) & 0x00100010u;
-      out[3] |= (u >> 4) & 0x00100010u;
-    } else {
-      out[0] |= (l << 8) & 0x01000100u;
-      out[1] |= l & 0x01000100u;
-      out[2] |= (u << 8) & 0x01000100u;
-      out[3] |= u & 0x01000100u;
+  if constexpr (SplitFmt<QT>::kK45) {
+    const uint4 q = r.q[p >> 1];
+    const uint32_t lo = (p & 1) ? q.z : q.x, hi = (p & 1) ? q.w : q.y;
+    if (h == 0) raw_pairs<kMaskLo>(lo, hi, lo >> 8, hi >> 8, out[0]);
+    else raw_pairs<kMaskHi>(lo, hi, lo >> 8, hi >> 8, out[0]);
+    if constexpr (QT == kQ5_K) {
+      // bit 2g + h of qh byte e is bit 4 of element e's code
+      const uint4 qh = r.h[p >> 1];
+      const uint32_t bit = 2 * g + static_cast<uint32_t>(h);
+      const uint32_t l = ((p & 1) ? qh.z : qh.x) >> bit, u = ((p & 1) ? qh.w : qh.y) >> bit;
+      if (h == 0) {
+        out[0][0] |= (l << 4) & 0x00100010u;
+        out[0][1] |= (l >> 4) & 0x00100010u;
+        out[0][2] |= (u << 4) & 0x00100010u;
+        out[0][3] |= (u >> 4) & 0x00100010u;
+      } else {
+        out[0][0] |= (l << 8) & 0x01000100u;
+        out[0][1] |= l & 0x01000100u;
+        out[0][2] |= (u << 8) & 0x01000100u;
+        out[0][3] |= u & 0x01000100u;
+      }
     }
-  }
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const uint32_t centred = h == 0 ? pk_add(out[i], s.c[0]) : pk_fma(out[i], splat(0.0625f), s.c[1]);
-    out[i] = h2u(u2h(centred) * s.sc[h]);
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t centred = h == 0 ? pk_add(out[0][i], s.c[0]) : pk_fma(out[0][i], splat(0.0625f), s.c[1]);
+      out[0][i] = h2u(u2h(centred) * s.sc[h]);
+    }
+  } else {
+    // the step's 8 codes, one per byte (Q8_0 signed: + 128 by flipping bit 7)
+    const uint64_t w = static_cast<uint64_t>(Unit<QT>::codes(r, g, t));
+    uint32_t lo = static_cast<uint32_t>(w), hi = static_cast<uint32_t>(w >> 32);
+    if constexpr (QT == kQ8_0) {
+      lo ^= 0x80808080u;
+      hi ^= 0x80808080u;
+    }
+    uint32_t v[4];
+    raw_pairs<kMaskByte>(lo, hi, lo >> 8, hi >> 8, v);  // 1024 + byte
+    constexpr float kBias = QT == kQ8_0 ? 1152.0f : QT == kQ4_0 ? 1032.0f : 1056.0f;
+    // Q8_0 / Q4_0: block 2g + h's factor; Q6_K: sub-block 2 h + p / 2 of the lane group
+    const h2 f = QT == kQ6_K ? s.sc[2 * h + (p >> 1)] : s.sc[h];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const h2 cc = u2h(pk_add(v[i], splat(-kBias)));  // the centred code, exact
+      const h2 whi = cc * f;
+      out[0][i] = h2u(whi);
+      out[1][i] = h2u(__builtin_elementwise_fma(cc, f, -whi));  // exact: c f - f16(c f)
+    }
   }
 }
 
 template <int QT, bool WIDE>
 __global__ __launch_bounds__(kSThreads) void gemm_split_kernel(SplitArgs a) {
   using U = Unit<QT>;
+  using F = SplitFmt<QT>;
+  constexpr int TW = F::kTiles, NP = F::kPlanes;
   constexpr Record R = record_geometry(QT, WIDE);
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];  // two stages
 
@@ -209,10 +285,10 @@ __global__ __launch_bounds__(kSThreads) void gemm_split_kernel(SplitArgs a) {
   const uint32_t g = lane >> 4, c = lane & 15;
   const uint32_t units = a.w.units;
   const uint32_t ub = z * units / a.splits, ue = (z + 1) * units / a.splits;
-  const uint32_t tile0 = grp * kSTiles + wave * 4;
-  const uint8_t* trec[4];
+  const uint32_t tile0 = (grp * (kSThreads / 64) + wave) * TW;
+  const uint8_t* trec[TW];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
+  for (int j = 0; j < TW; ++j) {
     const uint32_t t = min(tile0 + j, a.w.tiles - 1);
     trec[j] = a.w.qs + static_cast<uint64_t>(t) * units * R.bytes;
   }
@@ -226,16 +302,16 @@ __global__ __launch_bounds__(kSThreads) void gemm_split_kernel(SplitArgs a) {
                                          (__attribute__((address_space(3))) void*)(dst + 1024 * j), 16, 0, 0);
   };
 
-  typename U::Raw cur[4], nxt[4];
+  typename U::Raw cur[TW], nxt[TW];
   copy_stage(ub, 0);
 #pragma unroll
-  for (int j = 0; j < 4; ++j) U::template load<WIDE>(trec[j] + static_cast<uint64_t>(ub) * R.bytes, lane, cur[j]);
+  for (int j = 0; j < TW; ++j) U::template load<WIDE>(trec[j] + static_cast<uint64_t>(ub) * R.bytes, lane, cur[j]);
 
-  v4f total[4][4];
+  v4f total[4][TW];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) total[i][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int j = 0; j < TW; ++j) total[i][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
   const v4f zero = {0.0f, 0.0f, 0.0f, 0.0f};
 
 #pragma unroll 1
@@ -248,60 +324,71 @@ __global__ __launch_bounds__(kSThreads) void gemm_split_kernel(SplitArgs a) {
     if (u + 1 < ue) {
       copy_stage(u + 1, slot ^ 1);
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
+      for (int j = 0; j < TW; ++j)
         U::template load<WIDE>(trec[j] + static_cast<uint64_t>(u + 1) * R.bytes, lane, nxt[j]);
     }
     const uint8_t* const st = lds + slot * kSStage;
-    SplitScales sc[4];
+    SplitScales sc[TW];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) split_scales<QT, WIDE>(cur[j], g, sc[j]);
+    for (int j = 0; j < TW; ++j) split_scales<QT, WIDE>(cur[j], g, sc[j]);
 
-    v4f tmp[4][4];
+    v4f tmp[4][TW];
 #pragma unroll
     for (int t = 0; t < 8; ++t) {
-      uint32_t b[4][4];
+      uint32_t b[TW][NP][4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) split_codes<QT>(cur[j], g, t, sc[j], b[j]);
+      for (int j = 0; j < TW; ++j) split_codes<QT>(cur[j], g, t, sc[j], b[j]);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const uint8_t* const ap = st + ((t * 4 + i) * 64 + lane) * 16;
         const h8 ahi = *reinterpret_cast<const h8*>(ap);
         const h8 alo = *reinterpret_cast<const h8*>(ap + kSHalf);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const h8 bj = __builtin_bit_cast(h8, make_uint4(b[j][0], b[j][1], b[j][2], b[j][3]));
-          tmp[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, bj, t == 0 ? zero : tmp[i][j], 0, 0, 0);
-          tmp[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, bj, tmp[i][j], 0, 0, 0);
+        for (int j = 0; j < TW; ++j) {
+          const h8 b0 = __builtin_bit_cast(h8, make_uint4(b[j][0][0], b[j][0][1], b[j][0][2], b[j][0][3]));
+          tmp[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, b0, t == 0 ? zero : tmp[i][j], 0, 0, 0);
+          tmp[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, b0, tmp[i][j], 0, 0, 0);
+          if constexpr (NP == 2) {
+            const h8 b1 = __builtin_bit_cast(h8, make_uint4(b[j][1][0], b[j][1][1], b[j][1][2], b[j][1][3]));
+            tmp[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, b1, tmp[i][j], 0, 0, 0);
+          }
         }
       }
     }
-    // fold the unit in: total += 2^-s (d C + window sums x offsets)
+    // fold the unit in: total += 2^-s (d C [+ window sums x offsets])
     const float* const sums = reinterpret_cast<const float*>(st + kSSums);
     const float* const unsc = reinterpret_cast<const float*>(st + kSUnsc);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      // offsets on one f16 instruction: lane (row c, lane group g) supplies
-      // S / 64 of windows 2g, 2g+1 (|S| < 2^20) as halves in the slots
-      // hi, hi, hi, hi, lo, lo, 0, 0 against the B slots of split_scales:
-      // S_hi b_hi + S_hi b_lo + S_lo b_hi of both windows (22 bits of each)
-      float sh[2], sl[2];
-      split_f16(sums[(2 * g) * kSRows + 16 * i + c] * 0x1p-6f, sh[0], sl[0]);
-      split_f16(sums[(2 * g + 1) * kSRows + 16 * i + c] * 0x1p-6f, sh[1], sl[1]);
-      const uint32_t ah = pack_rtz(sh[0], sh[1]);
-      const h8 ao = __builtin_bit_cast(h8, make_uint4(ah, ah, pack_rtz(sl[0], sl[1]), 0u));
       const float4 us = *reinterpret_cast<const float4*>(unsc + 16 * i + 4 * g);
       const float uu[4] = {us.x, us.y, us.z, us.w};
+      if constexpr (F::kK45) {
+        // offsets on one f16 instruction: lane (row c, lane group g)
+        // supplies S / 64 of windows 2g, 2g+1 (|S| < 2^20) as halves in the
+        // slots hi, hi, hi, hi, lo, lo, 0, 0 against the B slots of
+        // split_scales: S_hi b_hi + S_hi b_lo + S_lo b_hi of both windows
+        float sh[2], sl[2];
+        split_f16(sums[(2 * g) * kSRows + 16 * i + c] * 0x1p-6f, sh[0], sl[0]);
+        split_f16(sums[(2 * g + 1) * kSRows + 16 * i + c] * 0x1p-6f, sh[1], sl[1]);
+        const uint32_t ah = pack_rtz(sh[0], sh[1]);
+        const h8 ao = __builtin_bit_cast(h8, make_uint4(ah, ah, pack_rtz(sl[0], sl[1]), 0u));
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const v4f off = __builtin_amdgcn_mfma_f32_16x16x32_f16(ao, __builtin_bit_cast(h8, sc[j].bo), zero, 0, 0, 0);
+        for (int j = 0; j < TW; ++j) {
+          const v4f off = __builtin_amdgcn_mfma_f32_16x16x32_f16(ao, __builtin_bit_cast(h8, sc[j].bo), zero, 0, 0, 0);
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
-          total[i][j][r] = fmaf(uu[r], fmaf(sc[j].fo, off[r], sc[j].d * tmp[i][j][r]), total[i][j][r]);
+          for (int r = 0; r < 4; ++r)
+            total[i][j][r] = fmaf(uu[r], fmaf(sc[j].fo, off[r], sc[j].d * tmp[i][j][r]), total[i][j][r]);
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < TW; ++j)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) total[i][j][r] = fmaf(uu[r], sc[j].d * tmp[i][j][r], total[i][j][r]);
       }
     }
     if (u + 1 < ue) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) cur[j] = nxt[j];
+      for (int j = 0; j < TW; ++j) cur[j] = nxt[j];
     }
   }
 
@@ -315,7 +402,7 @@ __global__ __launch_bounds__(kSThreads) void gemm_split_kernel(SplitArgs a) {
     for (int r = 0; r < 4; ++r) {
       const uint64_t row = static_cast<uint64_t>(mt) * kSRows + 16 * i + 4 * g + r;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
+      for (int j = 0; j < TW; ++j) {
         const uint64_t col = static_cast<uint64_t>(tile0 + j) * 16 + c;
         if (row < a.m && col < n) {
           out[row * n + col] = total[i][j][r];
@@ -327,7 +414,7 @@ __global__ __launch_bounds__(kSThreads) void gemm_split_kernel(SplitArgs a) {
   if (a.splits == 1 && bad) {
     for (int i = 0; i < 16; ++i) {
       const uint64_t row = static_cast<uint64_t>(mt) * kSRows + 16 * (i >> 2) + 4 * g + (i & 3);
-      for (int j = 0; j < 4; ++j) {
+      for (int j = 0; j < TW; ++j) {
         const uint64_t col = static_cast<uint64_t>(tile0 + j) * 16 + c;
         if (row < a.m && col < n && !__builtin_isfinite(a.y[row * n + col]))
           a.y[row * n + col] = exact_output_row<QT, WIDE>(a.w, a.x + row * a.w.k, col);
@@ -352,11 +439,23 @@ hipError_t launch_split_t(const SplitArgs& a, hipStream_t st) {
   return hipGetLastError();
 }
 
+// 16-output tiles per workgroup
+uint32_t split_group_tiles(int32_t qtype) {
+  return (kSThreads / 64) * ((qtype == kQ8_0 || qtype == kQ6_K) ? 2u : 4u);
+}
+
 }  // namespace
 
 bool gemm_split_supported(const Image& im) {
-  return im.tiled != 0 && im.layout == kOutputRows && (im.qtype == kQ4_K || im.qtype == kQ5_K) && im.k % 256 == 0 &&
-         im.k / 256 <= 0xFFFFu;
+  if (im.tiled == 0 || im.layout != kOutputRows || im.k % 256 != 0 || im.k / 256 > 0xFFFFu) return false;
+  switch (im.qtype) {
+    case kQ4_K:
+    case kQ5_K:
+    case kQ6_K: return true;
+    case kQ8_0:
+    case kQ4_0: return im.wide == 0;  // f16 block scales: exact in the weight halves
+    default: return false;
+  }
 }
 
 uint64_t gemm_split_records_bytes(uint64_t m, uint64_t k) {
@@ -367,7 +466,8 @@ uint32_t gemm_split_splits(const Image& im, uint64_t m) {
   // fill the CUs once when the row and column blocks alone do not, keeping
   // at least 4 units per part; the count returned is the one the launch
   // runs (every part holds units)
-  const uint64_t blocks = (m + kSRows - 1) / kSRows * ((im.tiles + kSTiles - 1) / kSTiles);
+  const uint64_t gt = split_group_tiles(im.qtype);
+  const uint64_t blocks = (m + kSRows - 1) / kSRows * ((im.tiles + gt - 1) / gt);
   const uint64_t units = im.k / 256;
   if (blocks >= kSCUs || units < 8) return 1;
   uint64_t s = (kSCUs + blocks - 1) / blocks;
@@ -384,16 +484,24 @@ hipError_t launch_gemm_split(const Image& im, const View& v, const float* x, uin
       (splits > 1 && part == nullptr))
     return hipErrorInvalidValue;
   const uint64_t units = im.k / 256, mtiles = (m + kSRows - 1) / kSRows;
-  const uint64_t groups = (im.tiles + kSTiles - 1) / kSTiles;
+  const uint64_t gt = split_group_tiles(im.qtype);
+  const uint64_t groups = (im.tiles + gt - 1) / gt;
   if (mtiles * units > 0x7fffffffull || mtiles > 0xFFFFFFu || groups > 0xFFFFFFu) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(split_prep_kernel, dim3(static_cast<uint32_t>(mtiles * units)), dim3(256), 0, st, x,
-                     static_cast<uint32_t>(im.k), m, rec);
+  if (im.qtype == kQ6_K)
+    hipLaunchKernelGGL(split_prep_kernel<true>, dim3(static_cast<uint32_t>(mtiles * units)), dim3(256), 0, st, x,
+                       static_cast<uint32_t>(im.k), m, rec);
+  else
+    hipLaunchKernelGGL(split_prep_kernel<false>, dim3(static_cast<uint32_t>(mtiles * units)), dim3(256), 0, st, x,
+                       static_cast<uint32_t>(im.k), m, rec);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const SplitArgs a{v, x, y, m, rec, static_cast<uint32_t>(mtiles), static_cast<uint32_t>(groups), splits, part};
   switch (im.qtype) {
+    case kQ8_0: e = launch_split_t<kQ8_0, false>(a, st); break;
+    case kQ4_0: e = launch_split_t<kQ4_0, false>(a, st); break;
     case kQ4_K: e = im.wide ? launch_split_t<kQ4_K, true>(a, st) : launch_split_t<kQ4_K, false>(a, st); break;
     case kQ5_K: e = im.wide ? launch_split_t<kQ5_K, true>(a, st) : launch_split_t<kQ5_K, false>(a, st); break;
+    case kQ6_K: e = im.wide ? launch_split_t<kQ6_K, true>(a, st) : launch_split_t<kQ6_K, false>(a, st); break;
     default: return hipErrorInvalidValue;
   }
   if (e != hipSuccess || splits == 1) return e;

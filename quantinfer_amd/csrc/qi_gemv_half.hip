@@ -85,17 +85,6 @@ __device__ __forceinline__ void xpose4(uint32_t r[4]) {
   r[3] = d[1];
 }
 
-// All-gather across the lane groups: v is V[g] in lane group g; out[g'] = V[g'].
-__device__ __forceinline__ void gather4u(uint32_t u, uint32_t out[4]) {
-  const auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
-  const auto b = __builtin_amdgcn_permlane32_swap(a[0], a[0], false, false);
-  const auto c = __builtin_amdgcn_permlane32_swap(a[1], a[1], false, false);
-  out[0] = b[0];
-  out[1] = c[0];
-  out[2] = b[1];
-  out[3] = c[1];
-}
-
 
 // Per-format weight access of one unit: load() the record bytes (the
 // one-row kernel's loaders), prepare() the transposes, then for window w the

@@ -14,6 +14,17 @@ typedef float v4f __attribute__((ext_vector_type(4)));
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 
+// All-gather across the lane groups: v is V[g] in lane group g; out[g'] = V[g'].
+__device__ __forceinline__ void gather4u(uint32_t u, uint32_t out[4]) {
+  const auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  const auto b = __builtin_amdgcn_permlane32_swap(a[0], a[0], false, false);
+  const auto c = __builtin_amdgcn_permlane32_swap(a[1], a[1], false, false);
+  out[0] = b[0];
+  out[1] = c[0];
+  out[2] = b[1];
+  out[3] = c[1];
+}
+
 __device__ __forceinline__ uint32_t h2u(h2 v) { return __builtin_bit_cast(uint32_t, v); }
 __device__ __forceinline__ h2 u2h(uint32_t v) { return __builtin_bit_cast(h2, v); }
 // (a & m) | o in one v_and_or_b32: m from a scalar register, o from a vector

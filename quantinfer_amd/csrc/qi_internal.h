@@ -79,9 +79,10 @@ hipError_t launch_gemv_half_records(const float* x, uint64_t k, int m, uint8_t* 
 hipError_t launch_gemv_half(int32_t qtype, bool wide, const View& w, const float* x, int m, float* y, float* part,
                             uint32_t ksplit, const uint8_t* records, hipStream_t st);
 
-// F32-mode GEMM of Q4_K / Q5_K output rows (qi_gemm_split.hip): split-half
-// activations against exact f16 codes with the sub-block scales folded in,
-// within the f32 GEMV's bars. launch_gemm_split converts the activations into
+// F32-mode GEMM of output rows (qi_gemm_split.hip): split-half activations
+// against exact f16 weight codes (Q4_K / Q5_K, sub-block scales folded in) or
+// weights as two f16 halves (Q8_0 / Q4_0 with f16 scales, Q6_K), within the
+// f32 GEMV's bars. launch_gemm_split converts the activations into
 // `records` (gemm_split_records_bytes) and runs the GEMM; with splits > 1
 // (gemm_split_splits) the partial sums [splits][m][n] go to `part` and are
 // added in order.
