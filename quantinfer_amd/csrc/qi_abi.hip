@@ -191,6 +191,9 @@ constexpr uint32_t kHalfMinRows = 9;
 // 33.7 / 41.5, M=48 47.9 / ~43, M=64 61.3 / 45.3; 4096x24576 M=32 71.9 /
 // 96.7, M=64 135.8 / 102.8; 12288x4096 M=32 45.3 / 44.9.
 constexpr uint64_t kSplitMinRows = 48;
+// Rows per split-half GEMM launch: longer calls run in chunks, so that the
+// activation records (about 4.1 bytes per activation) stay bounded.
+constexpr uint64_t kSplitChunkRows = 4096;
 
 qi_hip_status plan_linear(const Image& im, uint64_t m, int32_t mode, LinearPlan* p) {
   if (mode < QI_HIP_MODE_AUTO || mode > QI_HIP_MODE_MFMA)
@@ -235,9 +238,18 @@ qi_hip_status plan_linear(const Image& im, uint64_t m, int32_t mode, LinearPlan*
   }
   if (mode != QI_HIP_MODE_EXACT && m >= kSplitMinRows && qi::gemm_split_supported(im)) {
     p->kind = LinearPlan::kSplitGemm;
-    p->splits = qi::gemm_split_splits(im, m);
-    if (p->splits > 1) p->s_floats = static_cast<uint64_t>(p->splits) * m * im.n;
-    p->d_floats = (qi::gemm_split_records_bytes(m, im.k) + 3) / 4;
+    // chunks of kSplitChunkRows rows; a shorter last chunk takes its own K
+    // split count (enqueue_linear asks again)
+    const uint64_t chunk = m < kSplitChunkRows ? m : kSplitChunkRows;
+    uint64_t floats = 0;
+    for (uint64_t r : {chunk, m > chunk ? m % chunk : 0}) {
+      if (r == 0) continue;
+      const uint32_t sp = qi::gemm_split_splits(im, r);
+      if (sp > 1) floats = std::max(floats, static_cast<uint64_t>(sp) * r * im.n);
+    }
+    p->splits = qi::gemm_split_splits(im, chunk);
+    p->s_floats = floats;
+    p->d_floats = (qi::gemm_split_records_bytes(chunk, im.k) + 3) / 4;
     return QI_HIP_OK;
   }
   if (mode != QI_HIP_MODE_EXACT && qi::gemv_mfma_supported(im.qtype, im.layout, im.k)) {
@@ -345,8 +357,12 @@ qi_hip_status enqueue_linear(const qi_hip_weights* w, const LinearPlan& p, const
       }
       return QI_HIP_OK;
     case LinearPlan::kSplitGemm:
-      QI_HIP_TRY(qi::launch_gemm_split(im, v, x, m, y, sws, p.splits, reinterpret_cast<uint8_t*>(dws), st),
-                 "launch split-half gemm");
+      for (uint64_t m0 = 0; m0 < m; m0 += kSplitChunkRows) {
+        const uint64_t rows = m - m0 < kSplitChunkRows ? m - m0 : kSplitChunkRows;
+        QI_HIP_TRY(qi::launch_gemm_split(im, v, x + m0 * im.k, rows, y + m0 * im.n, sws,
+                                         qi::gemm_split_splits(im, rows), reinterpret_cast<uint8_t*>(dws), st),
+                   "launch split-half gemm");
+      }
       return QI_HIP_OK;
     case LinearPlan::kF32Gemv:
       for (uint64_t m0 = 0; m0 < m; m0 += 8) {

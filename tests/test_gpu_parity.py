@@ -309,6 +309,21 @@ def test_f32_split_gemm_tolerance(ctx, qtype, shape):
     w.free()
 
 
+def test_f32_split_gemm_row_chunks(ctx):
+    """Calls above 4096 rows run in 4096-row launches (bounded activation
+    records): 4156 rows equal the 4096-row and 60-row calls of the same rows
+    bit for bit, within the F32 bars."""
+    qtype, k, n, m = qa.Q4_K, 512, 80, 4156
+    blocks = po.make_weights(qtype, k, n, seed=4950, outliers=True)
+    w = ctx.weights(qtype, qa.OUTPUT_ROWS, k, n, blocks)
+    x = po.fill_normal(4951, m * k).reshape(m, k)
+    y = w.linear(x, qa.MODE_F32)
+    _assert_f32(y, x, blocks, qtype, n, "chunks")
+    assert w.linear(np.ascontiguousarray(x[:4096]), qa.MODE_F32).tobytes() == y[:4096].tobytes()
+    assert w.linear(np.ascontiguousarray(x[4096:]), qa.MODE_F32).tobytes() == y[4096:].tobytes()
+    w.free()
+
+
 @pytest.mark.parametrize("qtype", ALL_Q, ids=lambda q: NAMES[q])
 def test_f32_split_gemm_wide_scales_and_scaled_rows(ctx, qtype):
     """f32 d / dmin (not f16-exact), and activation rows of very different
