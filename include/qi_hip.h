@@ -154,12 +154,14 @@ qi_hip_status qi_hip_linear_device(qi_hip_ctx *ctx, const qi_hip_weights *w, con
  * under HIP graph capture, tight serving loops, harnesses that forbid
  * hipMalloc). No counterpart in the reference. Same kernels and results as
  * qi_hip_linear_device, but every workspace (the GEMM's f16 activations and
- * split-K partials, the multi-row GEMV's activation records) is carved out of
- * a fixed 64 MiB scratch array the library holds on each GPU until the
- * process ends; no call allocates or frees. A call whose workspaces exceed
- * 64 MiB is refused with QI_HIP_INVALID_INPUT (the GEMM takes 2*M*K bytes of
- * f16 activations, M rounded up to 128, plus split-K partials when fewer than
- * 256 row x column blocks: every BASELINE GEMM shape fits). Every call on one GPU
+ * split-K partials, the activation records of the multi-row GEMV and of F32
+ * mode's split-half GEMM) is carved out of a fixed 64 MiB scratch array the
+ * library holds on each GPU until the process ends; no call allocates or
+ * frees. A call whose workspaces exceed 64 MiB is refused with
+ * QI_HIP_INVALID_INPUT (the f16 GEMM takes 2*M*K bytes of f16 activations, M
+ * rounded up to 128, plus split-K partials when fewer than 256 row x column
+ * blocks: every BASELINE GEMM shape fits; the split-half GEMM about 4.1*M*K
+ * bytes, M rounded up to 64 and at most 4096 per launch). Every call on one GPU
  * shares that GPU's array: calls that overlap on one GPU (other streams, other
  * threads, other contexts on the same device) race, and the caller must order
  * them. Nothing in the array needs clearing between calls. */
