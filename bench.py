@@ -682,7 +682,8 @@ def configs_table(steps: int, warmup: int, with_cpu: bool) -> dict:
     resident weight copy (copies >= 512 MB), GB/s of algorithmic bytes
     against 8 TB/s. GEMM points: MFMA mode (f16 operands, f32 accumulation),
     TFLOP/s against the attainable roofline min(2.5 PFLOP/s, intensity x
-    8 TB/s); weight copies rotated the same way."""
+    8 TB/s), and beside it F32 mode (the split-half GEMM); weight copies
+    rotated the same way."""
     import quantinfer_amd as qa
 
     ctx = qa.Context(0)
@@ -712,13 +713,17 @@ def configs_table(steps: int, warmup: int, with_cpu: bool) -> dict:
                     tflops = flops / (us * 1e-6) / 1e12
                     intensity = flops / abytes
                     attainable = min(MFMA_F16_PEAK_TFLOPS, intensity * HBM_PEAK_GBPS / 1e3)
+                    # the same point in F32 mode: the split-half GEMM, within the f32 bars
+                    us32 = _time_rotating(weights, m, k, n, qa.MODE_F32, reps, max(2, warmup))
                     entry = {"config": cfg_i, "qtype": QNAME[qtype], "m": m, "k": k, "n": n,
                              "us": round(us, 2), "tflops": round(tflops, 1),
                              "roofline": {"bound": "mfma" if intensity >= RIDGE_FLOP_PER_BYTE else "hbm",
                                           "achieved": round(tflops, 1), "peak": round(attainable, 1),
                                           "unit": "TFLOP/s", "frac": round(tflops / attainable, 4),
                                           "frac_of_f16_peak": round(tflops / MFMA_F16_PEAK_TFLOPS, 4),
-                                          "intensity_flop_per_byte": round(intensity, 1)}}
+                                          "intensity_flop_per_byte": round(intensity, 1)},
+                             "f32_mode": {"us": round(us32, 2), "tflops": round(flops / (us32 * 1e-6) / 1e12, 1),
+                                          "kernel": "split-half GEMM (token-identical prompts)"}}
                     if with_cpu:
                         entry["cpu_baseline"] = _cpu_point(qtype, k, n, m, blocks, "TFLOP/s", flops)
                 out[kind].append(entry)
@@ -729,7 +734,8 @@ def configs_table(steps: int, warmup: int, with_cpu: bool) -> dict:
     out["device"] = ctx.device_name()
     ctx.close()
     out["note"] = ("GEMV: F32 mode, us per call over resident weight copies (>= 512 MB); GEMM: MFMA mode, "
-                   "f16 activation conversion + GEMM per call; roofline.frac of the GEMM is against "
+                   "f16 activation conversion + GEMM per call (f32_mode: the same point in F32 mode, "
+                   "the split-half GEMM); roofline.frac of the GEMM is against "
                    "min(f16 peak, intensity x HBM peak); cpu_baseline: scalar CpuScalar port and, for "
                    "Q8_0/Q4_0, the cpu-simd block dot, one pinned core, in the unit of the point")
     return out
