@@ -6,7 +6,9 @@
 // synchronous host entry point. A mutex serializes calls on one context.
 // Calls may enqueue on different caller streams; the device work of calls
 // that use a workspace is ordered by an event (ws_before / ws_after), so two
-// such calls never use a workspace at the same time.
+// such calls never use a workspace at the same time. The event carries no
+// system-scope fence: it orders work on one device and tells the host when a
+// workspace is free, and a fence would write back the caches on every call.
 #include <hip/hip_runtime.h>
 #include <stdlib.h>
 #include <string.h>
@@ -324,7 +326,7 @@ qi_hip_status enqueue_linear(const qi_hip_weights* w, const LinearPlan& p, const
           const uint32_t rr = static_cast<uint32_t>(rows);
           if (rr >= kHalfMinRows) {
             const uint32_t parts = qi::gemv_half_splits(im.k, im.n, rr);
-            QI_HIP_TRY(qi::launch_gemv_half_records(xc, im.k, rows, reinterpret_cast<uint8_t*>(dws), st),
+            QI_HIP_TRY(qi::launch_gemv_half_records(im.qtype, xc, im.k, rows, reinterpret_cast<uint8_t*>(dws), st),
                        "launch gemv rows activation records");
             QI_HIP_TRY(qi::launch_gemv_half(im.qtype, im.wide != 0, v, xc, rows, yc, sws, parts,
                                             reinterpret_cast<const uint8_t*>(dws), st),
@@ -460,7 +462,7 @@ qi_hip_status qi_hip_open(int32_t device, qi_hip_ctx** out) {
   if (const char* env = getenv("QI_HIP_GEMV_SPLIT")) c->gemv_split = atoi(env);
   c->name = prop.name[0] ? std::string(prop.name) : std::string("AMD ") + prop.gcnArchName;
   e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
-  if (e == hipSuccess) e = hipEventCreateWithFlags(&c->ws_event, hipEventDisableTiming);
+  if (e == hipSuccess) e = hipEventCreateWithFlags(&c->ws_event, hipEventDisableTiming | hipEventDisableSystemFence);
   if (e == hipSuccess) {
     const qi_hip_status st = scratch_setup(device, &c->scratch);
     if (st != QI_HIP_OK) {

@@ -61,48 +61,22 @@ using namespace half;
 
 constexpr int kSThreads = 256;
 constexpr uint32_t kSRows = 64;   // activation rows of a workgroup (4 row tiles)
-constexpr uint32_t kSHalf = 8 * 4 * 64 * 16;            // one half plane: [step][row tile][lane] x 16 B
-constexpr uint32_t kSSums = kSHalf * 2;                  // offset of the window sums [window][row] (f32)
-constexpr uint32_t kSUnsc = kSSums + 8 * kSRows * 4;     // offset of the unscales [row] (f32)
-constexpr uint32_t kSStage = kSUnsc + kSRows * 4;        // bytes of one (row tile, unit) stage
+constexpr uint32_t kSHalf = SplitStage<kSRows>::kHalf;   // one half plane: [step][row tile][lane] x 16 B
+constexpr uint32_t kSSums = SplitStage<kSRows>::kSums;   // offset of the window sums [window][row] (f32)
+constexpr uint32_t kSUnsc = SplitStage<kSRows>::kUnsc;   // offset of the unscales [row] (f32)
+constexpr uint32_t kSStage = SplitStage<kSRows>::kBytes; // bytes of one (row tile, unit) stage
 constexpr uint32_t kSCopies = (kSStage + 1023) / 1024;   // 1 KB copies per stage
 constexpr uint32_t kSCUs = 256;                          // compute units of an MI355X (gfx950)
 static_assert(kSStage % 16 == 0 && 2 * kSStage <= 160 * 1024, "two stages fit LDS");
 
-// One (64-row tile, unit) per workgroup; each half wavefront converts one row
-// per pass (item 4 w + s of its 32 lanes: window w, slice s, elements
-// 32 w + 8 s + [0, 8)) into the stage, at the (step, lane group) whose
-// weights cover those elements: for Q8_0 / Q4_0 / Q4_K / Q5_K lane group g
-// holds windows 2g, 2g + 1 (step t: window 2g + t / 4, slice t % 4); Q6_K
-// (ORDER6) lane group g = 2 ip + c elements 128 ip + 32 c + 64 (t / 4) +
-// 8 (t % 4) + [0, 8) (Unit<kQ6_K>).
+// One (64-row tile, unit) stage per workgroup (split_stage).
 template <bool ORDER6>
 __global__ __launch_bounds__(256) void split_prep_kernel(const float* __restrict__ x, uint32_t K, uint64_t M,
                                                          uint8_t* __restrict__ rec) {
   const uint32_t units = K / 256;
   const uint64_t mt = blockIdx.x / units;
   const uint32_t u = blockIdx.x % units;
-  uint8_t* const st = rec + (mt * units + u) * kSStage;
-  const uint32_t i32 = threadIdx.x & 31, w = i32 >> 2, s = i32 & 3, hw = threadIdx.x >> 5;
-  // the step and lane group that use this slice
-  const uint32_t t = ORDER6 ? 4 * ((w >> 1) & 1) + s : 4 * (w & 1) + s;
-  const uint32_t g = ORDER6 ? 2 * (w >> 2) + (w & 1) : w >> 1;
-  float* const sums = reinterpret_cast<float*>(st + kSSums);
-  float* const unsc = reinterpret_cast<float*>(st + kSUnsc);
-#pragma unroll 1
-  for (uint32_t pass = 0; pass < kSRows / 8; ++pass) {
-    const uint32_t r = pass * 8 + hw;
-    const uint64_t row = mt * kSRows + r;
-    float4 v0 = make_float4(0.0f, 0.0f, 0.0f, 0.0f), v1 = v0;
-    if (row < M) {
-      const float4* p = reinterpret_cast<const float4*>(x + row * K + u * 256 + 32 * w + 8 * s);
-      v0 = p[0];
-      v1 = p[1];
-    }
-    const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
-    uint8_t* const hs = st + ((t * 4 + (r >> 4)) * 64 + 16 * g + (r & 15)) * 16;
-    half_convert(v, hs, hs + kSHalf, sums + w * kSRows + r, unsc + r, w, s);
-  }
+  split_stage<kSRows, ORDER6>(x, K, M, mt * kSRows, u, rec + (mt * units + u) * kSStage);
 }
 
 struct SplitArgs {
@@ -114,157 +88,6 @@ struct SplitArgs {
   uint32_t mtiles, groups, splits;
   float* part;  // [splits][m][n] when splits > 1
 };
-
-// Per-format choices. Q4_K / Q5_K fold the 6-bit sub-block scale into an
-// exact f16 code (one weight plane, offsets through the window sums). The
-// other formats' per-block factors do not fold exactly into one f16 number
-// (Q8_0 d q: up to 19 bits; Q6_K sc (q - 32): up to 12), so the weight enters
-// as two f16 planes, hi = f16(w') and lo = w' - hi (exact, one fused
-// multiply-add), and every product takes three instructions: x_hi w_hi,
-// x_lo w_hi, x_hi w_lo (x_lo w_lo, below 2^-22 of the product, is left out).
-// Q8_0 / Q4_0: w' = 2^e d (q - bias), e per (output, unit) from the largest
-// of its eight block scales; Q6_K: w' = sc (q - 32), d applied in the
-// combine. Wavefronts hold 4 output tiles, 2 where the weight records are
-// large (Q8_0, Q6_K) so that two units of them fit in registers.
-template <int QT>
-struct SplitFmt {
-  static constexpr bool kK45 = QT == kQ4_K || QT == kQ5_K;
-  static constexpr int kPlanes = kK45 ? 1 : 2;
-  static constexpr int kTiles = (QT == kQ8_0 || QT == kQ6_K) ? 2 : 4;  // per wavefront
-  static constexpr bool kOrder6 = QT == kQ6_K;
-};
-
-// Per (output, unit) factors for lane group g. K45: the unit's d, the
-// windows' integer scales and centring constants, the offsets' operand.
-// Q8_0 / Q4_0: d = 2^-e, sc[h] = 2^e times block 2g + h's scale. Q6_K: d, and
-// sc[] the lane group's four sub-scales.
-struct SplitScales {
-  float d;
-  h2 sc[4], c[2];
-  uint4 bo;  // K45: the offsets' B operand: -b' of windows 2g, 2g+1 as f16 halves, scaled by 2^e
-  float fo;  // K45: 2^(6 - e), the offsets' matrix sum back to the f32 scale
-};
-
-// x as hi (x truncated to 11 significant bits, exact in f16) + lo (the rest
-// rounded to f16)
-__device__ __forceinline__ void split_f16(float x, float& hi, float& lo) {
-  hi = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, x) & 0xFFFFE000u);
-  lo = x - hi;
-}
-__device__ __forceinline__ uint32_t pack_rtz(float a, float b) {
-  return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(a, b));
-}
-__device__ __forceinline__ float f16_bits(uint32_t v) {
-  return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(v & 0xFFFFu)));
-}
-
-template <int QT, bool WIDE>
-__device__ __forceinline__ void split_scales(const typename Unit<QT>::Raw& r, uint32_t g, SplitScales& o) {
-  using U = Unit<QT>;
-  if constexpr (QT == kQ8_0 || QT == kQ4_0) {
-    static_assert(!WIDE, "f32 block scales are not exact in f16");
-    const float d0 = f16_bits(r.s0), d1 = f16_bits(r.s0 >> 16);
-    // the largest scale of the output's eight blocks (two per lane group)
-    uint32_t all[4];
-    gather4u(__builtin_bit_cast(uint32_t, fmaxf(fabsf(d0), fabsf(d1))), all);
-    const float dm = fmaxf(fmaxf(__builtin_bit_cast(float, all[0]), __builtin_bit_cast(float, all[1])),
-                           fmaxf(__builtin_bit_cast(float, all[2]), __builtin_bit_cast(float, all[3])));
-    // 2^e d_max in [2^7, 2^8): |w'| < 2^15 (Q8_0 codes up to 128 in magnitude)
-    const int e = dm > 0.0f ? 8 - __builtin_amdgcn_frexp_expf(dm) : 0;
-    o.d = __builtin_ldexpf(1.0f, -e);
-    o.sc[0] = splat(__builtin_ldexpf(d0, e));
-    o.sc[1] = splat(__builtin_ldexpf(d1, e));
-  } else if constexpr (QT == kQ6_K) {
-    o.d = WIDE ? __builtin_bit_cast(float, r.d) : f16_bits(r.d);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) o.sc[i] = splat(static_cast<float>(static_cast<int32_t>(r.sc << (24 - 8 * i)) >> 24));
-  } else {
-    constexpr float kQMax = QT == kQ5_K ? 31.0f : 15.0f;
-    float d, dmin;
-    U::template dmins<WIDE>(r, d, dmin);
-    const uint32_t f = U::field(g, r);
-    o.d = d;
-    // |b'| <= max(d sc / 2, dmin m) < max(32 d, 64 dmin) = B: scaled by 2^e
-    // with B 2^e < 2^15 the offsets fit f16 (the same e in every lane group of
-    // the output, as its four lane groups' offsets enter one sum)
-    const float bound = fmaxf(32.0f * d, 64.0f * dmin);
-    const int eb = bound > 0.0f ? __builtin_amdgcn_frexp_expf(bound) : 0;
-    const float up = __builtin_ldexpf(1.0f, 15 - eb);
-    o.fo = __builtin_ldexpf(1.0f, eb - 9);
-    float nh[2], nl[2];
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const float sc = static_cast<float>((f >> (12 * h)) & 63u), mn = static_cast<float>((f >> (12 * h + 6)) & 63u);
-      const float a = d * sc, b = dmin * mn;  // both exact in f32
-      // any integer z keeps the arithmetic exact; the nearest one keeps b'
-      // small (a = 0 gives z = kQMax or 0 and b' = b, with codes times sc = 0)
-      const float z = fminf(fmaxf(rintf(b * __builtin_amdgcn_rcpf(a)), 0.0f), kQMax);
-      split_f16(fmaf(a, z, -b) * up, nh[h], nl[h]);
-      o.sc[h] = splat(sc);
-      o.c[h] = splat(h == 0 ? -(1024.0f + z) : -(64.0f + z));
-    }
-    // slots 8g..8g+7: hi(2g), hi(2g+1), lo(2g), lo(2g+1), hi(2g), hi(2g+1), 0, 0
-    const uint32_t hh = pack_rtz(nh[0], nh[1]);
-    o.bo = make_uint4(hh, pack_rtz(nl[0], nl[1]), hh, 0u);
-  }
-}
-
-// The B operand(s) of step t: the lane's 8 codes in the operand order (0, 2),
-// (1, 3), (4, 6), (5, 7). K45: sc (q - z), one plane. Other formats: the
-// centred code c times the factor f as hi = f16(c f) and lo = c f - hi.
-template <int QT>
-__device__ __forceinline__ void split_codes(const typename Unit<QT>::Raw& r, uint32_t g, int t, const SplitScales& s,
-                                            uint32_t out[SplitFmt<QT>::kPlanes][4]) {
-  const int h = t >> 2, p = t & 3;
-  if constexpr (SplitFmt<QT>::kK45) {
-    const uint4 q = r.q[p >> 1];
-    const uint32_t lo = (p & 1) ? q.z : q.x, hi = (p & 1) ? q.w : q.y;
-    if (h == 0) raw_pairs<kMaskLo>(lo, hi, lo >> 8, hi >> 8, out[0]);
-    else raw_pairs<kMaskHi>(lo, hi, lo >> 8, hi >> 8, out[0]);
-    if constexpr (QT == kQ5_K) {
-      // bit 2g + h of qh byte e is bit 4 of element e's code
-      const uint4 qh = r.h[p >> 1];
-      const uint32_t bit = 2 * g + static_cast<uint32_t>(h);
-      const uint32_t l = ((p & 1) ? qh.z : qh.x) >> bit, u = ((p & 1) ? qh.w : qh.y) >> bit;
-      if (h == 0) {
-        out[0][0] |= (l << 4) & 0x00100010u;
-        out[0][1] |= (l >> 4) & 0x00100010u;
-        out[0][2] |= (u << 4) & 0x00100010u;
-        out[0][3] |= (u >> 4) & 0x00100010u;
-      } else {
-        out[0][0] |= (l << 8) & 0x01000100u;
-        out[0][1] |= l & 0x01000100u;
-        out[0][2] |= (u << 8) & 0x01000100u;
-        out[0][3] |= u & 0x01000100u;
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint32_t centred = h == 0 ? pk_add(out[0][i], s.c[0]) : pk_fma(out[0][i], splat(0.0625f), s.c[1]);
-      out[0][i] = h2u(u2h(centred) * s.sc[h]);
-    }
-  } else {
-    // the step's 8 codes, one per byte (Q8_0 signed: + 128 by flipping bit 7)
-    const uint64_t w = static_cast<uint64_t>(Unit<QT>::codes(r, g, t));
-    uint32_t lo = static_cast<uint32_t>(w), hi = static_cast<uint32_t>(w >> 32);
-    if constexpr (QT == kQ8_0) {
-      lo ^= 0x80808080u;
-      hi ^= 0x80808080u;
-    }
-    uint32_t v[4];
-    raw_pairs<kMaskByte>(lo, hi, lo >> 8, hi >> 8, v);  // 1024 + byte
-    constexpr float kBias = QT == kQ8_0 ? 1152.0f : QT == kQ4_0 ? 1032.0f : 1056.0f;
-    // Q8_0 / Q4_0: block 2g + h's factor; Q6_K: sub-block 2 h + p / 2 of the lane group
-    const h2 f = QT == kQ6_K ? s.sc[2 * h + (p >> 1)] : s.sc[h];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const h2 cc = u2h(pk_add(v[i], splat(-kBias)));  // the centred code, exact
-      const h2 whi = cc * f;
-      out[0][i] = h2u(whi);
-      out[1][i] = h2u(__builtin_elementwise_fma(cc, f, -whi));  // exact: c f - f16(c f)
-    }
-  }
-}
 
 template <int QT, bool WIDE>
 __global__ __launch_bounds__(kSThreads) void gemm_split_kernel(SplitArgs a) {

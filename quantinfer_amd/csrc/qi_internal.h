@@ -68,14 +68,16 @@ hipError_t launch_gemv_rows(int32_t qtype, bool wide, const View& w, const float
 
 // Decode GEMV of 9-16 rows on the f16 matrix cores with split-half
 // activations (qi_gemv_half.hip): launch_gemv_half_records converts the
-// activations once per call into `records` (gemv_half_records_bytes bytes),
+// activations once per call into `records` (gemv_half_records_bytes bytes;
+// their layout depends on the format: pass the GEMV's qtype),
 // which the GEMV workgroups copy; one GEMV kernel, K parts over the grid
 // (gemv_half_splits) only for shapes with few tiles; with ksplit > 1 the
 // partial sums [ksplit][m][n] go to `part` and launch_splitk_sum adds them.
 // Shapes: those of gemv_mfma_supported.
 uint32_t gemv_half_splits(uint64_t k, uint64_t n, uint32_t m);
 uint64_t gemv_half_records_bytes(uint64_t k);
-hipError_t launch_gemv_half_records(const float* x, uint64_t k, int m, uint8_t* records, hipStream_t st);
+hipError_t launch_gemv_half_records(int32_t qtype, const float* x, uint64_t k, int m, uint8_t* records,
+                                    hipStream_t st);
 hipError_t launch_gemv_half(int32_t qtype, bool wide, const View& w, const float* x, int m, float* y, float* part,
                             uint32_t ksplit, const uint8_t* records, hipStream_t st);
 
