@@ -324,3 +324,30 @@ def test_errors(qa, ctx, small):
     with pytest.raises(qa.QiError) as e:
         qa.Qwen3(ctx, small_config(head_dim=32))
     assert e.value.status == qa.UNSUPPORTED
+
+
+def test_fused_groups_must_share_format(qa, ctx, small):
+    """q|k|v and gate|up are uploaded as fused projections: a layer that mixes
+    formats inside a group is refused with UNSUPPORTED (such models take the
+    per-linear path), while o, down and the head may differ."""
+    from oracle import pyoracle as po
+    cfg, w, _ = small
+    m = qa.Qwen3(ctx, cfg)
+    try:
+        base = dict(w.device_layers[0])
+        for group_member in ("v_proj", "up_proj"):
+            layer = dict(base)
+            qtype, layout, blocks = layer[group_member]
+            values = po.dequantize(qtype, blocks)
+            layer[group_member] = (qa.Q8_0, layout, qa.quantize(qa.Q8_0, values, storage_f16=True))
+            with pytest.raises(qa.QiError) as e:
+                m.set_layer(0, layer)
+            assert e.value.status == qa.UNSUPPORTED and "fused projections" in str(e.value)
+        # a different format outside the groups is accepted
+        layer = dict(base)
+        qtype, layout, blocks = layer["o_proj"]
+        values = po.dequantize(qtype, blocks)
+        layer["o_proj"] = (qa.Q8_0, layout, qa.quantize(qa.Q8_0, values, storage_f16=True))
+        m.set_layer(0, layer)
+    finally:
+        m.free()
