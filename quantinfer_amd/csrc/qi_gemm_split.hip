@@ -38,11 +38,14 @@
 // this operand order ([half][step][row tile][lane] x 16 B), the 8 window sums
 // per row and the unscales 2^-s: one contiguous 66.25 KB stage.
 //
-// Tiling. A workgroup of 4 wavefronts owns 64 rows x 256 outputs; wavefront
-// w holds 4 row tiles x 4 output tiles (tiles 4 w .. 4 w + 3). Per unit the
-// stage is copied global -> LDS (1 KB direct copies, double-buffered, one
-// unit ahead) while each wavefront loads its 4 tiles' weight records of the
-// next unit into registers. The grid's blocks are dealt XCD-aware (logical
+// Tiling. A workgroup of 8 wavefronts owns 64 rows x 256 outputs; wavefront
+// w holds 4 row tiles x 2 output tiles (tiles 2 w, 2 w + 1), about 200
+// registers, so two wavefronts share each SIMD (one workgroup per CU, its
+// double-buffered stage taking 133 KB of LDS) and one's matrix instructions
+// overlap the other's code construction. Per unit the stage is copied
+// global -> LDS (1 KB direct copies, double-buffered, one unit ahead) while
+// each wavefront loads its 2 tiles' weight records of the next unit into
+// registers. The grid's blocks are dealt XCD-aware (logical
 // block (b % 8) * ceil(B / 8) + b / 8, row tiles fastest), so the row tiles
 // that share a weight panel run on one XCD's L2. K parts over the grid (for
 // shapes with few blocks) write partial sums that launch_splitk_sum adds in
@@ -59,7 +62,7 @@ namespace {
 
 using namespace half;
 
-constexpr int kSThreads = 256;
+constexpr int kSThreads = 512;
 constexpr uint32_t kSRows = 64;   // activation rows of a workgroup (4 row tiles)
 constexpr uint32_t kSHalf = SplitStage<kSRows>::kHalf;   // one half plane: [step][row tile][lane] x 16 B
 constexpr uint32_t kSSums = SplitStage<kSRows>::kSums;   // offset of the window sums [window][row] (f32)
@@ -262,10 +265,8 @@ hipError_t launch_split_t(const SplitArgs& a, hipStream_t st) {
   return hipGetLastError();
 }
 
-// 16-output tiles per workgroup
-uint32_t split_group_tiles(int32_t qtype) {
-  return (kSThreads / 64) * ((qtype == kQ8_0 || qtype == kQ6_K) ? 2u : 4u);
-}
+// 16-output tiles per workgroup (every format: SplitFmt<QT>::kTiles = 2)
+uint32_t split_group_tiles() { return (kSThreads / 64) * 2u; }
 
 }  // namespace
 
@@ -289,7 +290,7 @@ uint32_t gemm_split_splits(const Image& im, uint64_t m) {
   // fill the CUs once when the row and column blocks alone do not, keeping
   // at least 4 units per part; the count returned is the one the launch
   // runs (every part holds units)
-  const uint64_t gt = split_group_tiles(im.qtype);
+  const uint64_t gt = split_group_tiles();
   const uint64_t blocks = (m + kSRows - 1) / kSRows * ((im.tiles + gt - 1) / gt);
   const uint64_t units = im.k / 256;
   if (blocks >= kSCUs || units < 8) return 1;
@@ -307,7 +308,7 @@ hipError_t launch_gemm_split(const Image& im, const View& v, const float* x, uin
       (splits > 1 && part == nullptr))
     return hipErrorInvalidValue;
   const uint64_t units = im.k / 256, mtiles = (m + kSRows - 1) / kSRows;
-  const uint64_t gt = split_group_tiles(im.qtype);
+  const uint64_t gt = split_group_tiles();
   const uint64_t groups = (im.tiles + gt - 1) / gt;
   if (mtiles * units > 0x7fffffffull || mtiles > 0xFFFFFFu || groups > 0xFFFFFFu) return hipErrorInvalidValue;
   if (im.qtype == kQ6_K)

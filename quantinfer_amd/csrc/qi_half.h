@@ -178,13 +178,13 @@ __device__ __forceinline__ void split_stage(const float* __restrict__ x, uint32_
 // x_lo w_hi, x_hi w_lo (x_lo w_lo, below 2^-22 of the product, is left out).
 // Q8_0 / Q4_0: w' = 2^e d (q - bias), e per (output, unit) from the largest
 // of its eight block scales; Q6_K: w' = sc (q - 32), d applied in the
-// combine. Wavefronts hold 4 output tiles, 2 where the weight records are
-// large (Q8_0, Q6_K) so that two units of them fit in registers.
+// combine. Wavefronts hold 2 output tiles (two units of records in registers
+// and two wavefronts per SIMD).
 template <int QT>
 struct SplitFmt {
   static constexpr bool kK45 = QT == kQ4_K || QT == kQ5_K;
   static constexpr int kPlanes = kK45 ? 1 : 2;
-  static constexpr int kTiles = (QT == kQ8_0 || QT == kQ6_K) ? 2 : 4;  // per wavefront
+  static constexpr int kTiles = 2;  // output tiles per wavefront
   static constexpr bool kOrder6 = QT == kQ6_K;
 };
 
