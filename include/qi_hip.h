@@ -60,7 +60,7 @@ typedef int32_t qi_hip_status;
  *       prefill split of the kernels).
  * F32   f32-accurate for any M, judged by tolerance (1e-5) against the CPU
  *       reference: f32 GEMV kernels, and for output rows (K a multiple of
- *       256) from 48 rows a matrix-core GEMM of exact products (activations
+ *       256) from 33 rows a matrix-core GEMM of exact products (activations
  *       split into two f16 halves, weights as exact f16 codes or two f16
  *       halves) accumulated in f32.
  * EXACT bit-identical to CpuScalar: per output, acc = acc + x[k]*w[k] in f32,

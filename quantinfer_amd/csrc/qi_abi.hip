@@ -189,10 +189,11 @@ constexpr uint32_t kHalfMinRows = 9;
 // Rows from which output rows take the split-half GEMM (qi_gemm_split.hip)
 // in F32 mode, and in AUTO mode below the f16 GEMM's 128.
 // Below it the 16-row GEMV chunks are faster. Measured on MI355X, us per
-// call, GEMV chunks / split GEMM: Q4_K 4096x6144 M=17 24.6 / 39.6, M=32
-// 33.7 / 41.5, M=48 47.9 / ~43, M=64 61.3 / 45.3; 4096x24576 M=32 71.9 /
-// 96.7, M=64 135.8 / 102.8; 12288x4096 M=32 45.3 / 44.9.
-constexpr uint64_t kSplitMinRows = 48;
+// call, GEMV chunks / split GEMM: Q4_K 4096x6144 M=17 22.9 / 31.9, M=24
+// 30.3 / 33.0, M=32 31.0 / 33.1, M=40 43.7 / 34.1, M=48 34.7 (GEMM);
+// at M=32 4096x24576 70.3 / 76.5, 12288x4096 43.2 / 36.9, Q8_0 4096x14336
+// 47.6 / 42.8, Q6_K 52.4 / 42.2. From 33 rows the GEMV needs a third chunk.
+constexpr uint64_t kSplitMinRows = 33;
 // Rows per split-half GEMM launch: longer calls run in chunks, so that the
 // activation records (about 4.1 bytes per activation) stay bounded.
 constexpr uint64_t kSplitChunkRows = 4096;

@@ -284,11 +284,11 @@ def test_f32_gemv_offset_cancellation(ctx, qtype):
         w.free()
 
 
-# F32 mode from 48 rows on output rows: the split-half GEMM
+# F32 mode from 33 rows on output rows: the split-half GEMM
 # (qi_gemm_split.hip). (K, N, rows): one unit per row (the offsets' largest
 # share, as in the cancellation case above), K parts over the grid with a
 # ragged last tile, a partial last 64-row tile, and a 512-row prompt.
-SPLIT_SHAPES = [(256, 8192, (48, 64, 200)), (12288, 1000, (48, 130)), (4096, 4096, (50, 100, 512)),
+SPLIT_SHAPES = [(256, 8192, (48, 64, 200)), (12288, 1000, (48, 130)), (4096, 4096, (33, 50, 100, 512)),
                 (1024, 24576, (65,))]
 
 
