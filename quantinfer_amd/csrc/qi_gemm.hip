@@ -116,11 +116,11 @@ __device__ __forceinline__ h8 weight_fragment(long codes, float a, float b) {
 // activation, |x| beyond f16's range) are recomputed in the reference's order
 // (exact_output_row), which decides which are NaN and which +-Inf. The lane
 // owns rows row0 + 16 rt + r (rt < rts, r < 4) of columns col0 + 16 ct
-// (ct < 4); its values are already stored in y.
-template <int QT, bool WIDE>
+// (ct < CT); its values are already stored in y.
+template <int QT, bool WIDE, int CT = 4>
 __device__ __forceinline__ void gemm_fix_nonfinite(const GemmArgs& a, uint64_t row0, int rts, uint64_t col0) {
 #pragma unroll 1
-  for (int i = 0; i < 16 * rts; ++i) {
+  for (int i = 0; i < 4 * CT * rts; ++i) {
     const uint64_t n = col0 + 16 * static_cast<uint64_t>(i / (4 * rts));
     const uint64_t m = row0 + 16 * static_cast<uint64_t>((i / 4) % rts) + (i % 4);
     if (n >= a.w.n || m >= a.m) continue;
@@ -135,13 +135,14 @@ __device__ __forceinline__ void gemm_fix_nonfinite(const GemmArgs& a, uint64_t r
 // a pair swap their four rows and each finishes two of them (the gate lane
 // rows 0-1, the up lane rows 2-3), writing gate / (1 + e^-gate) * up
 // (backends/cpu/src/backend.rs:224-237) to act[m][8 T + c16 % 8].
-__device__ __forceinline__ void gemm_store_silu(const GemmArgs& a, const f4 (&acc)[8][4], uint32_t tile0,
+template <int CT = 4>
+__device__ __forceinline__ void gemm_store_silu(const GemmArgs& a, const f4 (&acc)[8][CT], uint32_t tile0,
                                                 uint64_t m0, uint32_t g, uint32_t c16) {
   const uint64_t lda = a.w.n / 2;
   const bool up = c16 >= 8;
   const uint32_t c8 = c16 & 7;
 #pragma unroll
-  for (int ct = 0; ct < 4; ++ct) {
+  for (int ct = 0; ct < CT; ++ct) {
     const uint64_t T = tile0 + ct;
 #pragma unroll
     for (int rt = 0; rt < 8; ++rt) {
@@ -601,22 +602,27 @@ __device__ __forceinline__ void wait_vm_lgkm0() {
 // vector-memory instruction of the main loop is one of these copies, a known
 // number per stage, which lets a stage wait for exactly the copy it needs:
 //   activations: 2-step stages (16 KB, fragment order) in a ring of 4 LDS
-//     slots, stage s + 3 requested at the top of stage s (4 copies of 1 KB
-//     per wavefront);
-//   weights: each wavefront copies its 4 tiles' records of unit u + 1
-//     (LdsRec<QT>::kCopies instructions per record) into the other of its two
-//     LDS buffers at the top of unit u, and reads its code words and scales
-//     from there when the unit becomes current.
+//     slots, stage s + 3 requested at the top of stage s (P = 16 / W copies
+//     of 1 KB per wavefront, W wavefronts per workgroup);
+//   weights: each wavefront copies its CT = 16 / W tiles' records of unit
+//     u + 1 (LdsRec<QT>::kCopies instructions per record) into the other of
+//     its two LDS buffers at the top of unit u, and reads its code words and
+//     scales from there when the unit becomes current.
 // Waits at the top of stage s = 4u + q (copies issued after the one needed
-// stay in flight): q = 0: the stage's activations, 8 younger copies
-// (stages s + 1, s + 2); q = 1, 2: 8 + the unit's record copies; q = 3: the
-// next unit's records, 8 younger copies. The raw s_barrier (no fence) keeps
+// stay in flight): q = 0: the stage's activations, 2 P younger copies
+// (stages s + 1, s + 2); q = 1, 2: 2 P + the unit's record copies; q = 3: the
+// next unit's records, 2 P younger copies. The raw s_barrier (no fence) keeps
 // the other copies in flight; the wait before it also drains this
 // wavefront's LDS reads, so the slot the new copy overwrites is free.
-// Tiling, arithmetic and split-K as gemm_reg_kernel. Each step dequantizes
-// its fragments before its matrix instructions (dequantizing one step ahead
-// measured slower here: the second fragment set costs registers).
+// W = 8: a wavefront owns 128 rows x 2 output tiles (about 170 registers),
+// two wavefronts per SIMD; measured against W = 4 (4 tiles each, one per
+// SIMD): Q4_K 2048x4096x12288 245.5 -> 240.6 us, 512x4096x4096 50.1 -> 46.2,
+// Q5_K 2048x4096x12288 295.1 -> 272.7. Tiling, arithmetic and split-K as
+// gemm_reg_kernel. Each step dequantizes its fragments before its matrix
+// instructions (dequantizing one step ahead measured slower here: the second
+// fragment set costs registers).
 constexpr uint32_t kLdsSlots = 4, kLdsStage = 2 * 8 * 64 * 16;
+constexpr int kLdsWaves = 8;  // wavefronts per workgroup (16 output tiles over them)
 
 typedef __attribute__((address_space(3))) void* lds_ptr;
 
@@ -641,7 +647,8 @@ struct LdsRec<kQ4_K> {
                                      0);
     __builtin_amdgcn_global_load_lds(src + static_cast<uint32_t>(2048 + lane * 4), (lds_ptr)(dst + 2048), 4, 0, 0);
   }
-  __device__ static void read(uint32_t base, uint32_t lane, Unit<kQ4_K>::Raw cur[4]) {
+  template <int CT>
+  __device__ static void read(uint32_t base, uint32_t lane, Unit<kQ4_K>::Raw cur[CT]) {
     const uint32_t c16 = lane & 15;
     const uint32_t aq = base + lane * 16, asc = base + R.sc + c16 * 12, ad = base + R.d + c16 * 2;
     u32x4 q0[4], q1[4];
@@ -659,16 +666,23 @@ struct LdsRec<kQ4_K> {
                : "v"(aq), "v"(asc), "v"(ad))
     QI_Q4K_TILE_READ(0);
     QI_Q4K_TILE_READ(1);
-    QI_Q4K_TILE_READ(2);
-    QI_Q4K_TILE_READ(3);
+    if constexpr (CT == 4) {
+      QI_Q4K_TILE_READ(2);
+      QI_Q4K_TILE_READ(3);
+      asm volatile("s_waitcnt lgkmcnt(0)"
+                   : "+v"(q0[0]), "+v"(q1[0]), "+v"(sc0[0]), "+v"(sc1[0]), "+v"(sc2[0]), "+v"(d0[0]), "+v"(d1[0]),
+                     "+v"(q0[1]), "+v"(q1[1]), "+v"(sc0[1]), "+v"(sc1[1]), "+v"(sc2[1]), "+v"(d0[1]), "+v"(d1[1]),
+                     "+v"(q0[2]), "+v"(q1[2]), "+v"(sc0[2]), "+v"(sc1[2]), "+v"(sc2[2]), "+v"(d0[2]), "+v"(d1[2]),
+                     "+v"(q0[3]), "+v"(q1[3]), "+v"(sc0[3]), "+v"(sc1[3]), "+v"(sc2[3]), "+v"(d0[3]), "+v"(d1[3]));
+    } else {
+      static_assert(CT == 2, "2 or 4 tiles per wavefront");
+      asm volatile("s_waitcnt lgkmcnt(0)"
+                   : "+v"(q0[0]), "+v"(q1[0]), "+v"(sc0[0]), "+v"(sc1[0]), "+v"(sc2[0]), "+v"(d0[0]), "+v"(d1[0]),
+                     "+v"(q0[1]), "+v"(q1[1]), "+v"(sc0[1]), "+v"(sc1[1]), "+v"(sc2[1]), "+v"(d0[1]), "+v"(d1[1]));
+    }
 #undef QI_Q4K_TILE_READ
-    asm volatile("s_waitcnt lgkmcnt(0)"
-                 : "+v"(q0[0]), "+v"(q1[0]), "+v"(sc0[0]), "+v"(sc1[0]), "+v"(sc2[0]), "+v"(d0[0]), "+v"(d1[0]),
-                   "+v"(q0[1]), "+v"(q1[1]), "+v"(sc0[1]), "+v"(sc1[1]), "+v"(sc2[1]), "+v"(d0[1]), "+v"(d1[1]),
-                   "+v"(q0[2]), "+v"(q1[2]), "+v"(sc0[2]), "+v"(sc1[2]), "+v"(sc2[2]), "+v"(d0[2]), "+v"(d1[2]),
-                   "+v"(q0[3]), "+v"(q1[3]), "+v"(sc0[3]), "+v"(sc1[3]), "+v"(sc2[3]), "+v"(d0[3]), "+v"(d1[3]));
 #pragma unroll
-    for (int ct = 0; ct < 4; ++ct) {
+    for (int ct = 0; ct < CT; ++ct) {
       cur[ct].q[0] = __builtin_bit_cast(uint4, q0[ct]);
       cur[ct].q[1] = __builtin_bit_cast(uint4, q1[ct]);
       cur[ct].sc[0] = sc0[ct];
@@ -696,7 +710,8 @@ struct LdsRec<kQ5_K> {
       __builtin_amdgcn_global_load_lds(src + static_cast<uint32_t>(2048 + 256 * i + lane * 4),
                                        (lds_ptr)(dst + 2048 + 256 * i), 4, 0, 0);
   }
-  __device__ static void read(uint32_t base, uint32_t lane, Unit<kQ5_K>::Raw cur[4]) {
+  template <int CT>
+  __device__ static void read(uint32_t base, uint32_t lane, Unit<kQ5_K>::Raw cur[CT]) {
     const uint32_t c16 = lane & 15;
     const uint32_t aq = base + lane * 16, ah = base + R.qh + c16 * 16, asc = base + R.sc + c16 * 12,
                    ad = base + R.d + c16 * 2;
@@ -717,18 +732,26 @@ struct LdsRec<kQ5_K> {
                : "v"(aq), "v"(ah), "v"(asc), "v"(ad))
     QI_Q5K_TILE_READ(0);
     QI_Q5K_TILE_READ(1);
-    QI_Q5K_TILE_READ(2);
-    QI_Q5K_TILE_READ(3);
+    if constexpr (CT == 4) {
+      QI_Q5K_TILE_READ(2);
+      QI_Q5K_TILE_READ(3);
+      asm volatile("s_waitcnt lgkmcnt(0)"
+                   : "+v"(q0[0]), "+v"(q1[0]), "+v"(h0[0]), "+v"(h1[0]), "+v"(sc0[0]), "+v"(sc1[0]), "+v"(sc2[0]),
+                     "+v"(d0[0]), "+v"(d1[0]), "+v"(q0[1]), "+v"(q1[1]), "+v"(h0[1]), "+v"(h1[1]), "+v"(sc0[1]),
+                     "+v"(sc1[1]), "+v"(sc2[1]), "+v"(d0[1]), "+v"(d1[1]), "+v"(q0[2]), "+v"(q1[2]), "+v"(h0[2]),
+                     "+v"(h1[2]), "+v"(sc0[2]), "+v"(sc1[2]), "+v"(sc2[2]), "+v"(d0[2]), "+v"(d1[2]), "+v"(q0[3]),
+                     "+v"(q1[3]), "+v"(h0[3]), "+v"(h1[3]), "+v"(sc0[3]), "+v"(sc1[3]), "+v"(sc2[3]), "+v"(d0[3]),
+                     "+v"(d1[3]));
+    } else {
+      static_assert(CT == 2, "2 or 4 tiles per wavefront");
+      asm volatile("s_waitcnt lgkmcnt(0)"
+                   : "+v"(q0[0]), "+v"(q1[0]), "+v"(h0[0]), "+v"(h1[0]), "+v"(sc0[0]), "+v"(sc1[0]), "+v"(sc2[0]),
+                     "+v"(d0[0]), "+v"(d1[0]), "+v"(q0[1]), "+v"(q1[1]), "+v"(h0[1]), "+v"(h1[1]), "+v"(sc0[1]),
+                     "+v"(sc1[1]), "+v"(sc2[1]), "+v"(d0[1]), "+v"(d1[1]));
+    }
 #undef QI_Q5K_TILE_READ
-    asm volatile("s_waitcnt lgkmcnt(0)"
-                 : "+v"(q0[0]), "+v"(q1[0]), "+v"(h0[0]), "+v"(h1[0]), "+v"(sc0[0]), "+v"(sc1[0]), "+v"(sc2[0]),
-                   "+v"(d0[0]), "+v"(d1[0]), "+v"(q0[1]), "+v"(q1[1]), "+v"(h0[1]), "+v"(h1[1]), "+v"(sc0[1]),
-                   "+v"(sc1[1]), "+v"(sc2[1]), "+v"(d0[1]), "+v"(d1[1]), "+v"(q0[2]), "+v"(q1[2]), "+v"(h0[2]),
-                   "+v"(h1[2]), "+v"(sc0[2]), "+v"(sc1[2]), "+v"(sc2[2]), "+v"(d0[2]), "+v"(d1[2]), "+v"(q0[3]),
-                   "+v"(q1[3]), "+v"(h0[3]), "+v"(h1[3]), "+v"(sc0[3]), "+v"(sc1[3]), "+v"(sc2[3]), "+v"(d0[3]),
-                   "+v"(d1[3]));
 #pragma unroll
-    for (int ct = 0; ct < 4; ++ct) {
+    for (int ct = 0; ct < CT; ++ct) {
       cur[ct].q[0] = __builtin_bit_cast(uint4, q0[ct]);
       cur[ct].q[1] = __builtin_bit_cast(uint4, q1[ct]);
       cur[ct].h[0] = __builtin_bit_cast(uint4, h0[ct]);
@@ -747,13 +770,15 @@ constexpr uint32_t lds_gemm_bytes() {
   return kLdsSlots * kLdsStage + 4 * 2 * 4 * LdsRec<QT>::kBytes;
 }
 
-template <int QT>
-__global__ __launch_bounds__(256) void gemm_lds_kernel(GemmArgs a) {
+template <int QT, int W>
+__global__ __launch_bounds__(64 * W) void gemm_lds_kernel(GemmArgs a) {
   using U = Unit<QT>;
   using L = LdsRec<QT>;
   static_assert(lds_gemm_bytes<QT>() <= 160 * 1024, "LDS per workgroup");
   constexpr int RT = 8;
-  constexpr uint32_t kWBuf = 4 * L::kBytes;  // one wavefront's 4 records of a unit
+  constexpr int CT = 16 / W;                  // output tiles per wavefront
+  constexpr int P = 4 * 4 / W;                // activation copies per stage and wavefront
+  constexpr uint32_t kWBuf = CT * L::kBytes;  // one wavefront's CT records of a unit
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   uint8_t* const abuf = lds;
 
@@ -767,10 +792,11 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(GemmArgs a) {
   const uint32_t stages = 4 * ue;
   const u32x4* xa = reinterpret_cast<const u32x4*>(a.xh) + static_cast<uint64_t>(blockIdx.y) * units * 4096;
 
-  const uint8_t* trec[4];
+  const uint32_t tile0 = (blockIdx.x * W + wave) * CT;
+  const uint8_t* trec[CT];
 #pragma unroll
-  for (int ct = 0; ct < 4; ++ct) {
-    const uint32_t t = min((blockIdx.x * 4 + wave) * 4 + ct, a.w.tiles - 1);
+  for (int ct = 0; ct < CT; ++ct) {
+    const uint32_t t = min(tile0 + ct, a.w.tiles - 1);
     trec[ct] = a.w.qs + static_cast<uint64_t>(t) * units * L::kBytes;
   }
 
@@ -781,43 +807,44 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(GemmArgs a) {
     // uniform base plus a 32-bit lane offset: the scalar-base addressing form
     const uint8_t* src = reinterpret_cast<const uint8_t*>(xa + static_cast<uint64_t>(sl) * 1024);
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      __builtin_amdgcn_global_load_lds(src + static_cast<uint32_t>((tid + 256 * i) * 16),
-                                       (lds_ptr)(dst + (256 * i + 64 * wave) * 16), 16, 0, 0);
+    for (int i = 0; i < P; ++i)
+      __builtin_amdgcn_global_load_lds(src + static_cast<uint32_t>((tid + 64 * W * i) * 16),
+                                       (lds_ptr)(dst + (64 * W * i + 64 * wave) * 16), 16, 0, 0);
   };
   // this wavefront's records of unit u (clamped) into its buffer (u - ub) & 1
   auto copy_unit = [&](uint32_t u) {
     const uint32_t ul = u < ue ? u : ue - 1;
     uint8_t* dst = wbuf + ((u - ub) & 1) * kWBuf;
 #pragma unroll
-    for (int ct = 0; ct < 4; ++ct) L::copy(trec[ct] + static_cast<uint64_t>(ul) * L::kBytes, dst + ct * L::kBytes, lane);
+    for (int ct = 0; ct < CT; ++ct) L::copy(trec[ct] + static_cast<uint64_t>(ul) * L::kBytes, dst + ct * L::kBytes, lane);
   };
 
-  typename U::Raw cur[4];
-  float sa[4][U::kWindows], sb[4][U::kWindows];
+  typename U::Raw cur[CT];
+  float sa[CT][U::kWindows], sb[CT][U::kWindows];
   auto take_unit = [&](uint32_t u) {
     typedef __attribute__((address_space(3))) uint8_t* lds_u8;
-    L::read(static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_u8)wbuf)) + ((u - ub) & 1) * kWBuf, lane, cur);
+    L::template read<CT>(static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_u8)wbuf)) + ((u - ub) & 1) * kWBuf,
+                         lane, cur);
 #pragma unroll
-    for (int ct = 0; ct < 4; ++ct) {
+    for (int ct = 0; ct < CT; ++ct) {
       U::template scales<false>(g, cur[ct], sa[ct], sb[ct]);
       if constexpr (QT == kQ4_K) q4k_affine(sa[ct], sb[ct]);
     }
   };
-  auto frags = [&](auto tc, h8 out[4]) {
+  auto frags = [&](auto tc, h8 out[CT]) {
     constexpr int t = decltype(tc)::value, w = t / U::kSteps;
 #pragma unroll
-    for (int ct = 0; ct < 4; ++ct) {
+    for (int ct = 0; ct < CT; ++ct) {
       if constexpr (QT == kQ4_K) out[ct] = q4k_fragment(cur[ct], t, sa[ct][w], sb[ct][w]);
       else out[ct] = weight_fragment<QT>(U::codes(cur[ct], g, t), sa[ct][w], sb[ct][w]);
     }
   };
 
-  f4 acc[RT][4];
+  f4 acc[RT][CT];
 #pragma unroll
   for (int i = 0; i < RT; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = f4{0, 0, 0, 0};
+    for (int j = 0; j < CT; ++j) acc[i][j] = f4{0, 0, 0, 0};
 
   // prologue: stages 4 ub .. 4 ub + 2 and unit ub, all complete
   copy_stage(4 * ub);
@@ -828,26 +855,28 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(GemmArgs a) {
   __builtin_amdgcn_s_barrier();
   take_unit(ub);
 
-  constexpr int kMid = 8 + 4 * static_cast<int>(L::kCopies);  // copies younger than the stage's, q = 1, 2
+  // copies younger than the one a stage needs: the two next stages' (2 P),
+  // at q = 1, 2 also the next unit's records (CT per record copy count)
+  constexpr int kMid = 2 * P + CT * static_cast<int>(L::kCopies);
   for (uint32_t u = ub; u < ue; ++u) {
     auto step = [&](auto qc) {
       constexpr int q = decltype(qc)::value;
       const uint32_t s = 4 * u + q;
       if constexpr (q == 1 || q == 2) wait_vm_lgkm0<kMid>();
-      else wait_vm_lgkm0<8>();
+      else wait_vm_lgkm0<2 * P>();
       __builtin_amdgcn_s_barrier();
       copy_stage(s + 3);
       if constexpr (q == 0) copy_unit(u + 1);
       const uint8_t* A = abuf + (s % kLdsSlots) * kLdsStage;
       auto sub = [&](auto ttc) {
         constexpr int tt = decltype(ttc)::value, t = 2 * q + tt;
-        h8 af[RT], bf[4];
+        h8 af[RT], bf[CT];
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt)
           af[rt] = *reinterpret_cast<const h8*>(A + ((tt * 8 + rt) * 64 + lane) * 16);
         frags(std::integral_constant<int, t>{}, bf);
 #pragma unroll
-        for (int ct = 0; ct < 4; ++ct)
+        for (int ct = 0; ct < CT; ++ct)
 #pragma unroll
           for (int rt = 0; rt < RT; ++rt)
             acc[rt][ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[rt], bf[ct], acc[rt][ct], 0, 0, 0);
@@ -867,7 +896,7 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(GemmArgs a) {
   wait_vm_lgkm0<0>();
 
   if (a.act != nullptr) {
-    gemm_store_silu(a, acc, (blockIdx.x * 4 + wave) * 4, m0, g, c16);
+    gemm_store_silu<CT>(a, acc, tile0, m0, g, c16);
     return;
   }
   const uint64_t ld = a.w.n;
@@ -875,8 +904,8 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(GemmArgs a) {
   float* yrow = out + (m0 + 4 * g) * ld;
   bool bad = false;
 #pragma unroll
-  for (int ct = 0; ct < 4; ++ct) {
-    const uint64_t n = static_cast<uint64_t>((blockIdx.x * 4 + wave) * 4 + ct) * 16 + c16;
+  for (int ct = 0; ct < CT; ++ct) {
+    const uint64_t n = static_cast<uint64_t>(tile0 + ct) * 16 + c16;
     if (n >= a.w.n) continue;
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
@@ -892,7 +921,7 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(GemmArgs a) {
   }
   // with a K split the partial sums are checked by gemm_splitk_sum_kernel
   if (bad && a.splits == 1)
-    gemm_fix_nonfinite<QT, false>(a, m0 + 4 * g, RT, static_cast<uint64_t>((blockIdx.x * 4 + wave) * 4) * 16 + c16);
+    gemm_fix_nonfinite<QT, false, CT>(a, m0 + 4 * g, RT, static_cast<uint64_t>(tile0) * 16 + c16);
 }
 
 // y = sum of the split-K partial products, in split order (deterministic);
@@ -944,12 +973,12 @@ hipError_t launch_lds(const Image& im, const GemmArgs& a, hipStream_t st) {
   const uint32_t nblk = static_cast<uint32_t>((im.tiles + 15) / 16);
   const uint32_t mblk = static_cast<uint32_t>(a.m_pad / kTileM);
   if (a.splits < 1 || a.splits > im.k / 256 || (a.splits > 1 && a.part == nullptr)) return hipErrorInvalidValue;
-  auto kern = gemm_lds_kernel<QT>;
+  auto kern = gemm_lds_kernel<QT, kLdsWaves>;
   constexpr uint32_t bytes = lds_gemm_bytes<QT>();
   hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                      hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(bytes));
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(kern, dim3(nblk, mblk, a.splits), dim3(256), bytes, st, a);
+  hipLaunchKernelGGL(kern, dim3(nblk, mblk, a.splits), dim3(64 * kLdsWaves), bytes, st, a);
   e = hipGetLastError();
   if (e != hipSuccess || a.splits == 1) return e;
   const uint64_t count = a.m * im.n;
