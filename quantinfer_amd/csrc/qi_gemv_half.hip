@@ -72,9 +72,10 @@ constexpr int kHWaves = 16;
 constexpr uint32_t kHCUs = 256;  // compute units of an MI355X (gfx950)
 constexpr int kHRows = 16;      // rows of the A operand (9-16 activation rows)
 
-// LDS of a chunk of `cu` units for MR rows: the halves [unit][window][half]
-// [row][lane group] x 16 B, then the window sums [unit][row][window] and the
-// unscales 2^-s [unit][row] as f32.
+// LDS of a chunk of `cu` units for MR rows, the records' layout: Q8_0 /
+// Q4_0 / Q6_K the halves [unit][window][half][row][lane group] x 16 B, then
+// the window sums [unit][row][window] and the unscales 2^-s [unit][row] as
+// f32; Q4_K / Q5_K the units' stages (SplitStage<MR>), of the same size.
 constexpr uint32_t half_lds(int mr, uint32_t cu) { return cu * static_cast<uint32_t>(mr) * (1024 + 32 + 4); }
 constexpr uint32_t half_chunk_cap(int mr) { return 128 / static_cast<uint32_t>(mr); }
 static_assert(half_lds(16, 8) <= 160 * 1024 && half_lds(4, 32) <= 160 * 1024, "chunks fit LDS");
