@@ -234,7 +234,8 @@ qi_hip_status plan_linear(const Image& im, uint64_t m, int32_t mode, LinearPlan*
   }
   if (mode != QI_HIP_MODE_EXACT && qi::gemv_rm_supported(im)) {
     p->kind = LinearPlan::kRowMajor;
-    const uint32_t chunk = m < 4 ? static_cast<uint32_t>(m) : 4u;
+    const uint32_t rows = qi::gemv_rm_rows(im);
+    const uint32_t chunk = m < rows ? static_cast<uint32_t>(m) : rows;
     p->splits = qi::gemv_rm_splits(im, chunk);
     if (p->splits > 1) p->s_floats = static_cast<uint64_t>(p->splits) * chunk * im.n;
     return QI_HIP_OK;
@@ -305,11 +306,12 @@ qi_hip_status enqueue_linear(const qi_hip_weights* w, const LinearPlan& p, const
       return QI_HIP_OK;
     }
     case LinearPlan::kRowMajor: {
-      // the blocks-along-N GEMV, 4 rows per launch; a last chunk of fewer
-      // rows keeps at most the 4-row split count
-      for (uint64_t m0 = 0; m0 < m; m0 += 4) {
-        const uint32_t rows = static_cast<uint32_t>(m - m0 < 4 ? m - m0 : 4);
-        const uint32_t chunk = m < 4 ? static_cast<uint32_t>(m) : 4u;
+      // the blocks-along-N GEMV, gemv_rm_rows rows per launch; a last chunk
+      // of fewer rows keeps at most the full chunk's split count
+      const uint32_t per = qi::gemv_rm_rows(im);
+      for (uint64_t m0 = 0; m0 < m; m0 += per) {
+        const uint32_t rows = static_cast<uint32_t>(m - m0 < per ? m - m0 : per);
+        const uint32_t chunk = m < per ? static_cast<uint32_t>(m) : per;
         const uint32_t sp = rows == chunk ? p.splits : qi::gemv_rm_splits(im, rows);
         QI_HIP_TRY(qi::launch_gemv_rm(im, v, x + m0 * im.k, rows, y + m0 * im.n, sws,
                                       sp <= p.splits ? sp : p.splits, st),

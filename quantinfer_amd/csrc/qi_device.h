@@ -53,11 +53,16 @@ struct BlockLoc {
   uint32_t col, bi;    // tiled: row within the tile, block within the unit
 };
 
-// Block b of output row n (output-rows layout), or flat block b (n = 0).
+// Block b of output row n (output-rows layout), or flat block b (n = 0; row
+// major, where a tiled image's record row is one k of v.nb blocks).
 template <int QT>
 __device__ __forceinline__ BlockLoc locate(const View& v, uint64_t n, uint64_t b) {
   BlockLoc L;
   if (v.tiled) {
+    if (b >= v.nb) {
+      n += b / v.nb;
+      b %= v.nb;
+    }
     const uint64_t u = b / Geo<QT>::kBpu;
     L.rec = v.qs + ((n / 16) * v.units + u) * v.rec.bytes;
     L.col = static_cast<uint32_t>(n % 16);
@@ -228,8 +233,10 @@ __device__ __forceinline__ float exact_row_major_col(const View& w, const float*
   constexpr uint32_t bs = (QT == kQ8_0 || QT == kQ4_0) ? 32 : 256;
   float sum = 0.0f;
   for (uint64_t k = 0; k < w.k; ++k) {
-    const uint64_t f = k * w.n + n;  // flat index of element (k, n)
-    sum += x[k] * Exact<QT, WIDE>::value(w, locate<QT>(w, 0, f / bs), static_cast<uint32_t>(f % bs));
+    // element (k, n): in a tiled image (N a multiple of 256) element n % bs of
+    // block n / bs of record row k, else of flat block (k N + n) / bs
+    const uint64_t f = w.tiled ? n : k * w.n + n;
+    sum += x[k] * Exact<QT, WIDE>::value(w, locate<QT>(w, w.tiled ? k : 0, f / bs), static_cast<uint32_t>(f % bs));
   }
   return sum;
 }

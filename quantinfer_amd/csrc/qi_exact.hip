@@ -25,7 +25,8 @@ __global__ __launch_bounds__(256) void dequant_kernel(View w, uint64_t elements,
   constexpr uint32_t bs = (QT == kQ8_0 || QT == kQ4_0) ? 32 : 256;
   const uint64_t blk = e0 / bs;
   const uint32_t l0 = static_cast<uint32_t>(e0 % bs);  // 8 | bs, so all 8 share the block
-  // block order: output n owns blocks [n*nb, n*nb+nb) (row major: nb = all blocks)
+  // block order: output n owns blocks [n*nb, n*nb+nb) (row major: k owns them
+  // in a tiled image, nb = all blocks in a planar one)
   const BlockLoc L = locate<QT>(w, blk / nb, blk % nb);
   float v[8];
 #pragma unroll
@@ -120,7 +121,9 @@ hipError_t exact_wide(const Image& im, const View& w, const float* x, uint64_t m
 template <int QT>
 hipError_t dequant_wide(const Image& im, const View& w, float* out, hipStream_t st) {
   const uint64_t elements = im.k * im.n;
-  const uint64_t nb = im.layout == kOutputRows ? im.k / block_elems(im.qtype) : im.nblocks;
+  const uint64_t nb = im.layout == kOutputRows ? im.k / block_elems(im.qtype)
+                     : im.tiled                 ? im.n / block_elems(im.qtype)
+                                                : im.nblocks;
   return im.wide ? dequant_one<QT, true>(w, elements, nb, out, st)
                  : dequant_one<QT, false>(w, elements, nb, out, st);
 }

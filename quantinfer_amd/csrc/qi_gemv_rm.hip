@@ -1,10 +1,25 @@
 // Row-major (blocks along N) GEMV, F32 mode: y[m, n] = sum_k x[m, k] w(k, n)
 // for QuantInfer-layout weights (backends/cpu/src/backend.rs:62-140 ->
-// matmul.rs:14-90; element values matmul.rs:162-280). The weight image is
-// planar with flat block index k * (N / bs) + nb, so at one k the code bytes
-// of consecutive output blocks are contiguous.
+// matmul.rs:14-90; element values matmul.rs:162-280). Two kernels, by image:
 //
-// A lane owns one column unit: the outputs one 4-byte code word decodes to
+// Tiled image (N a multiple of 256; gemv_rmt_kernel): record (t, u) holds
+// rows k = 16t + c (c = 0..15) of outputs n = 256u + [0, 256), in the
+// arrangement of the output-rows records. Lane 16g + c of a wavefront loads row
+// c's lane group g with the GEMV's record loader (Unit<QT>, non-temporal): the
+// codes of 64 outputs at one k and the scales of their windows. The lane keeps
+// one f32 accumulator per output and activation row and adds x[k] w per code
+// (rmt_consume: the codes centred as the one-row output-rows GEMV takes them,
+// the weight formed in one multiply-add where an offset is left).
+// A workgroup of four wavefronts takes one unit and one K split, each
+// wavefront every fourth tile of the split: at most rmt_max_slots records,
+// all loaded before the first is consumed.
+// The 16 rows of a lane group are summed by two DPP steps (lanes c, c + 4,
+// c + 8, c + 12) and through LDS for the last four and the four wavefronts, in
+// a fixed order.
+//
+// Planar image (gemv_rm_kernel): flat block index k * (N / bs) + nb, so at
+// one k the code bytes of consecutive output blocks are contiguous. A lane
+// owns one column unit: the outputs one 4-byte code word decodes to
 // (Q8_0: 4 outputs; Q4_0 and Q4_K/Q5_K: 8, low and high nibbles; Q6_K: 16 from
 // two ql words and one qh word). 64 consecutive column units per workgroup
 // column, the four wavefronts split the workgroup's K range, and the grid's
@@ -17,6 +32,7 @@
 // judged by tolerance like the output-rows F32 GEMV.
 #include "qi_device.h"
 #include "qi_internal.h"
+#include "qi_unit.h"
 
 namespace qi {
 
@@ -182,6 +198,203 @@ __global__ __launch_bounds__(256) void rm_sum_kernel(const float* __restrict__ p
   y[i] = s;
 }
 
+// ------------------------------------------------------------ tiled image
+
+constexpr int kRmtRows = 2;     // activation rows per launch
+constexpr int kRmtStride = 17;  // float4s per summed lane in LDS: 64 outputs and one of padding
+
+// Records per wavefront, all loaded before the first is consumed: the most
+// that fit beside the accumulators at two wavefronts per SIMD (a record in
+// registers: Q4_0 11, Q4_K 14, Q8_0 and Q6_K 19, Q5_K 22 VGPRs, with its
+// activations).
+constexpr uint32_t rmt_max_slots(int32_t qtype, uint32_t rows) {
+  return rows > 1 ? 4u : (qtype == kQ4_0 || qtype == kQ4_K) ? 8u : 6u;
+}
+
+// Record of tile t into r, with the activations of its row k = 16t + c,
+// read at min(k, K - 1) (rows past K are zero in the record and their
+// activation is zeroed at use). No condition on loaded values here, so that
+// nothing waits for the loads before the record is consumed.
+template <int QT, bool WIDE, int MT>
+__device__ __forceinline__ void rmt_fetch(const uint8_t* rec, uint32_t lane, uint32_t k, uint32_t K,
+                                          const float* __restrict__ x, typename Unit<QT>::Raw& r,
+                                          float (&xs)[MT]) {
+  const uint32_t kk = k < K ? k : K - 1;
+#pragma unroll
+  for (int i = 0; i < MT; ++i) xs[i] = x[static_cast<uint64_t>(i) * K + kk];
+  Unit<QT>::template load<WIDE, true>(rec, lane, r);
+}
+
+// One record's products, acc[i][8 st + e] += x_i w for step st's code e. The
+// codes arrive centred, s (q - z) in a signed byte (one sign-extending
+// conversion); a / s is exact. Q8_0, Q4_0 and Q6_K have no offset left (w =
+// (a / s) s (q - z)): the lane forms x a / s once per window and multiplies.
+// Q4_K/Q5_K keep b - a z: the lane forms each weight with one fused
+// multiply-add, w = (a / s) s (q - z) - (b - a z), as a sum of x a q and of
+// x b over K would cancel in f32 at small K.
+template <int QT, bool WIDE, int MT>
+__device__ __forceinline__ void rmt_consume(const typename Unit<QT>::Raw& r, uint32_t g, bool live,
+                                            const float (&xr)[MT], float (&acc)[MT][64]) {
+  using U = Unit<QT>;
+  constexpr int kW = U::kWindows, kS = U::kSteps;
+  constexpr bool kOff = window_centered<QT>();
+  constexpr float kInv = 1.0f / static_cast<float>(code_scale<QT>());
+  constexpr float kCentre = static_cast<float>(code_centre<QT>());
+  float a[kW], b[kW], xa[MT][kW], xs[MT];
+#pragma unroll
+  for (int i = 0; i < MT; ++i) xs[i] = live ? xr[i] : 0.0f;
+  U::template scales<WIDE>(g, r, a, b);
+#pragma unroll
+  for (int w = 0; w < kW; ++w) {
+    if constexpr (kOff) {
+      b[w] = a[w] * kCentre - b[w];  // -(b - a z)
+      a[w] *= kInv;
+    } else {
+      const float as = a[w] * kInv;
+#pragma unroll
+      for (int i = 0; i < MT; ++i) xa[i][w] = xs[i] * as;
+    }
+  }
+#pragma unroll
+  for (int st = 0; st < 8; ++st) {
+    const uint64_t q = static_cast<uint64_t>(gemv_codes<QT>(r, g, st));
+    const uint32_t lo = static_cast<uint32_t>(q), hi = static_cast<uint32_t>(q >> 32);
+    const int w = st / kS;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const uint32_t word = e < 4 ? lo : hi;
+      const float qf = static_cast<float>(static_cast<int8_t>(word >> (8 * (e & 3))));
+      if constexpr (kOff) {
+        const float wt = fmaf(a[w], qf, b[w]);
+#pragma unroll
+        for (int i = 0; i < MT; ++i) acc[i][8 * st + e] = fmaf(xs[i], wt, acc[i][8 * st + e]);
+      } else {
+#pragma unroll
+        for (int i = 0; i < MT; ++i) acc[i][8 * st + e] = fmaf(xa[i][w], qf, acc[i][8 * st + e]);
+      }
+    }
+  }
+}
+
+template <int QT, bool WIDE, int MT, int R>
+__global__ __launch_bounds__(256) void gemv_rmt_kernel(View v, const float* __restrict__ x, uint32_t m,
+                                                       uint32_t ksplit, float* __restrict__ out) {
+  using U = Unit<QT>;
+  // [wavefront][row][lane group g * 4 + c, c < 4][64 outputs]
+  __shared__ float4 red[4][MT][16][kRmtStride];
+  const uint32_t lane = threadIdx.x & 63, g = lane >> 4, c = lane & 15;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: scalar branches
+  const uint32_t K = static_cast<uint32_t>(v.k), T = v.tiles;
+  const uint32_t tb = static_cast<uint32_t>((static_cast<uint64_t>(blockIdx.y) * T) / ksplit);
+  const uint32_t te = static_cast<uint32_t>((static_cast<uint64_t>(blockIdx.y + 1) * T) / ksplit);
+  const uint8_t* base = v.qs + static_cast<uint64_t>(blockIdx.x) * v.rec.bytes;
+  const uint64_t tile_bytes = static_cast<uint64_t>(v.units) * v.rec.bytes;
+
+  float acc[MT][64];
+#pragma unroll
+  for (int i = 0; i < MT; ++i)
+#pragma unroll
+    for (int j = 0; j < 64; ++j) acc[i][j] = 0.0f;
+  // this wavefront's records: tiles t0, t0 + 4, ... below te, n <= R of them
+  // (the host picks the split count so). All R loads are issued first, with
+  // no condition (slots past n load the last record again), so that each
+  // record waits only for its own loads.
+  const uint32_t t0 = tb + wave, n = t0 < te ? (te - t0 + 3) / 4 : 0;
+  if (n > 0) {
+    typename U::Raw r[R];
+    float xs[R][MT];
+#pragma unroll
+    for (int j = 0; j < R; ++j) {
+      const uint32_t t = t0 + 4 * (static_cast<uint32_t>(j) < n ? j : n - 1);
+      rmt_fetch<QT, WIDE, MT>(base + t * tile_bytes, lane, 16 * t + c, K, x, r[j], xs[j]);
+      // loads in record order, all before the first record's arithmetic
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // every slot is consumed (no branch, so no load sinks into one): a slot
+    // past n, or a row past K, adds zero
+#pragma unroll
+    for (int j = 0; j < R; ++j)
+      rmt_consume<QT, WIDE, MT>(r[j], g, static_cast<uint32_t>(j) < n && 16 * (t0 + 4 * j) + c < K, xs[j], acc);
+  }
+
+  // rows c, c + 4, c + 8, c + 12 of each lane group, then lanes c < 4 to LDS
+#pragma unroll
+  for (int i = 0; i < MT; ++i)
+#pragma unroll
+    for (int j = 0; j < 64; ++j) {
+      acc[i][j] += dpp_move<kDppRor8>(acc[i][j]);
+      acc[i][j] += dpp_move<kDppRor4>(acc[i][j]);
+    }
+  if (c < 4) {
+#pragma unroll
+    for (int i = 0; i < MT; ++i) {
+      float4* dst = red[wave][i][4 * g + c];
+#pragma unroll
+      for (int q = 0; q < 16; ++q)
+        dst[q] = make_float4(acc[i][4 * q], acc[i][4 * q + 1], acc[i][4 * q + 2], acc[i][4 * q + 3]);
+    }
+  }
+  __syncthreads();
+  // wavefront i sums activation row i: lane 16g + h takes outputs 4h .. 4h + 3
+  // of lane group g (step h / 2: elements window_first(g, h / 8) + 8 (h / 2 % 4)
+  // + 4 (h % 2) + [0, 4))
+  if (wave >= static_cast<uint32_t>(MT) || wave >= m) return;
+  const uint32_t h = c, step = h / 2;
+  float4 s = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+  for (int wv = 0; wv < 4; ++wv)
+#pragma unroll
+    for (int cc = 0; cc < 4; ++cc) {
+      const float4 p = red[wv][wave][4 * g + cc][h];
+      s.x += p.x; s.y += p.y; s.z += p.z; s.w += p.w;
+    }
+  const uint32_t e0 = window_first<QT>(g, step / 4) + 8 * (step % 4) + 4 * (h % 2);
+  const uint64_t n0 = static_cast<uint64_t>(blockIdx.x) * 256 + e0;
+  float* dst = out + (static_cast<uint64_t>(blockIdx.y) * m + wave) * v.n + n0;
+  const float val[4] = {s.x, s.y, s.z, s.w};
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    float y = val[e];
+    // a NaN or infinite activation: the reference's order decides NaN or
+    // +-Inf (with a K split, rm_sum_kernel checks the sum instead)
+    if (ksplit == 1 && !__builtin_isfinite(y))
+      y = exact_row_major_col<QT, WIDE>(v, x + static_cast<uint64_t>(wave) * K, n0 + e);
+    dst[e] = y;
+  }
+}
+
+template <int QT, bool WIDE, int MT>
+hipError_t launch_rmt_rows(const View& v, const float* x, uint32_t m, float* out, uint32_t splits, hipStream_t st) {
+  // records per wavefront: ceil(ceil(T / splits) / 4), served by the smallest slot count that holds them
+  const uint32_t per = static_cast<uint32_t>(((v.tiles + splits - 1) / splits + 3) / 4);
+  const dim3 grid(v.units, splits);
+  auto go = [&](auto kern) {
+    hipLaunchKernelGGL(kern, grid, dim3(256), 0, st, v, x, m, splits, out);
+    return hipGetLastError();
+  };
+  constexpr int kMax = static_cast<int>(rmt_max_slots(QT, MT));
+  if (per <= 2) return go(gemv_rmt_kernel<QT, WIDE, MT, 2>);
+  if (per <= 4) return go(gemv_rmt_kernel<QT, WIDE, MT, 4>);
+  if constexpr (kMax > 4) {
+    if (per <= kMax) return go(gemv_rmt_kernel<QT, WIDE, MT, kMax>);
+  }
+  return hipErrorInvalidValue;
+}
+
+template <int QT, bool WIDE>
+hipError_t launch_rmt_q(const View& v, const float* x, uint32_t m, float* y, float* part, uint32_t splits,
+                        hipStream_t st) {
+  float* out = splits > 1 ? part : y;
+  if (m != 1 && m != kRmtRows) return hipErrorInvalidValue;  // the kernel reads MT = m rows
+  hipError_t e = m == 1 ? launch_rmt_rows<QT, WIDE, 1>(v, x, m, out, splits, st)
+                        : launch_rmt_rows<QT, WIDE, kRmtRows>(v, x, m, out, splits, st);
+  if (e != hipSuccess || splits == 1) return e;
+  const uint64_t count = static_cast<uint64_t>(m) * v.n;
+  hipLaunchKernelGGL((rm_sum_kernel<QT, WIDE>), dim3(static_cast<uint32_t>((count + 255) / 256)), dim3(256), 0,
+                     st, part, splits, count, y, v, x);
+  return hipGetLastError();
+}
+
 template <int QT, bool WIDE>
 hipError_t launch_rm_q(const View& v, const float* x, uint32_t m, float* y, float* part, uint32_t splits,
                        hipStream_t st) {
@@ -203,15 +416,29 @@ hipError_t launch_rm_q(const View& v, const float* x, uint32_t m, float* y, floa
 }  // namespace
 
 bool gemv_rm_supported(const Image& im) {
-  return im.layout == kRowMajor && !im.tiled && im.qtype >= kQ8_0 && im.qtype <= kQ6_K &&
-         im.n % block_elems(im.qtype) == 0 && im.k > 0;
+  // tiled: grid x = units, grid y = splits of at most 4 * 4 records per workgroup
+  return im.layout == kRowMajor && im.qtype >= kQ8_0 && im.qtype <= kQ6_K && im.n % block_elems(im.qtype) == 0 &&
+         im.k > 0 && (!im.tiled || (im.units <= 0xFFFFu && im.tiles <= 16ull * 0xFFFFu));
 }
 
+uint32_t gemv_rm_rows(const Image& im) { return im.tiled ? kRmtRows : 4; }
+
 uint32_t gemv_rm_splits(const Image& im, uint32_t m) {
+  const uint32_t be = block_elems(im.qtype);
+  if (im.tiled) {
+    // About 512 workgroups (two wavefronts per SIMD on 256 CUs) give each
+    // wavefront ceil(T / (4 s)) records; that count is rounded up to a slot
+    // count of the kernel (2, 4 or the most), and s lowered to the fewest
+    // splits that keep it.
+    const uint64_t rmax = rmt_max_slots(im.qtype, m > 1 ? kRmtRows : 1);
+    const uint64_t s0 = (512 + im.units - 1) / im.units;
+    const uint64_t per = ((im.tiles + s0 - 1) / s0 + 3) / 4;
+    const uint64_t slots = per <= 2 ? 2 : per <= 4 ? 4 : rmax;
+    const uint64_t s = (im.tiles + 4 * slots - 1) / (4 * slots);
+    return static_cast<uint32_t>(s < 1 ? 1 : s);
+  }
   // enough K splits for about 1024 workgroups, keeping at least 16 k per
   // wavefront (4 wavefronts per workgroup) and at most 256 splits
-  const uint32_t be = block_elems(im.qtype);
-  (void)m;
   const uint64_t out = im.qtype == kQ8_0 ? 4 : im.qtype == kQ6_K ? 16 : 8;
   const uint64_t col_groups = ((im.n / be) * (be / out) + 63) / 64;
   uint64_t s = col_groups >= 1024 ? 1 : 1024 / col_groups;
@@ -222,8 +449,24 @@ uint32_t gemv_rm_splits(const Image& im, uint32_t m) {
 
 hipError_t launch_gemv_rm(const Image& im, const View& v, const float* x, uint32_t m, float* y, float* part,
                           uint32_t splits, hipStream_t st) {
-  if (m < 1 || m > 4 || splits < 1 || (splits > 1 && part == nullptr)) return hipErrorInvalidValue;
+  if (m < 1 || m > gemv_rm_rows(im) || splits < 1 || (splits > 1 && part == nullptr)) return hipErrorInvalidValue;
   const bool wide = im.wide != 0;
+  if (im.tiled) {
+    if (v.units != im.n / 256 || v.tiles != (im.k + 15) / 16 || !gemv_rm_supported(im)) return hipErrorInvalidValue;
+    switch (im.qtype) {
+      case kQ8_0: return wide ? launch_rmt_q<kQ8_0, true>(v, x, m, y, part, splits, st)
+                              : launch_rmt_q<kQ8_0, false>(v, x, m, y, part, splits, st);
+      case kQ4_0: return wide ? launch_rmt_q<kQ4_0, true>(v, x, m, y, part, splits, st)
+                              : launch_rmt_q<kQ4_0, false>(v, x, m, y, part, splits, st);
+      case kQ4_K: return wide ? launch_rmt_q<kQ4_K, true>(v, x, m, y, part, splits, st)
+                              : launch_rmt_q<kQ4_K, false>(v, x, m, y, part, splits, st);
+      case kQ5_K: return wide ? launch_rmt_q<kQ5_K, true>(v, x, m, y, part, splits, st)
+                              : launch_rmt_q<kQ5_K, false>(v, x, m, y, part, splits, st);
+      case kQ6_K: return wide ? launch_rmt_q<kQ6_K, true>(v, x, m, y, part, splits, st)
+                              : launch_rmt_q<kQ6_K, false>(v, x, m, y, part, splits, st);
+      default: return hipErrorInvalidValue;
+    }
+  }
   switch (im.qtype) {
     case kQ8_0: return wide ? launch_rm_q<kQ8_0, true>(v, x, m, y, part, splits, st)
                             : launch_rm_q<kQ8_0, false>(v, x, m, y, part, splits, st);

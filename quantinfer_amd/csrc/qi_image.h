@@ -6,7 +6,8 @@
 // blocks, unrounded Q8_0/Q4_0 quantizer output) switch the tensor to f32 scale
 // entries ("wide"). Two arrangements:
 //
-// planar (row-major weights, or K not a multiple of 256): one plane per field
+// planar (row major with N not a multiple of 256, output rows with K not a
+//   multiple of 256): one plane per field
 //   in the reference block order, each plane contiguous.
 //
 //   plane   Q8_0        Q4_0              Q4_K        Q5_K        Q6_K
@@ -16,10 +17,12 @@
 //   d       f16|f32     f16|f32           f16|f32     f16|f32     f16|f32
 //   dmin    -           -                 f16|f32     f16|f32     -
 //
-// tiled (output rows, K a multiple of 256; what the decode GEMV streams): the
-//   outputs are grouped in tiles of 16 (the last tile zero-padded) and K in
-//   units of 256 elements; one record per (tile, unit) holds the 16 rows'
-//   bytes of that unit, records ordered [tile][unit]. Inside a record:
+// tiled (output rows with K a multiple of 256, what the decode GEMV streams;
+//   row major with N a multiple of 256): the rows are grouped in tiles of 16
+//   (the last tile zero-padded) and each row in units of 256 elements; one
+//   record per (tile, unit) holds the 16 rows' bytes of that unit, records
+//   ordered [tile][unit]. A row is one output's K elements (output rows) or
+//   one k's N elements (row major, blocks along N). Inside a record:
 //     codes  the row slice of S code bytes (Q8_0 S=256, others 128) is split
 //            in four lane groups of S/4 bytes and 16-byte chunks; chunk q of
 //            lane group g of row c sits at q*1024 + (16g + c)*16, so a
@@ -123,7 +126,7 @@ struct View {
   const void* d;
   const void* dmin;
   uint64_t k, n;
-  uint32_t nb;     // blocks per output row (output-rows layout)
+  uint32_t nb;     // blocks per output row (output rows), per k (tiled row major)
   uint32_t tiled;  // 1: records
   uint32_t units;  // tiled: units per row
   uint32_t tiles;  // tiled: tiles
@@ -141,7 +144,8 @@ inline View make_view(const Image& im, const void* base) {
   v.k = im.k;
   v.n = im.n;
   const uint32_t be = block_elems(im.qtype);
-  v.nb = be ? static_cast<uint32_t>(im.k / be) : 0;
+  const uint64_t row = im.layout == kRowMajor && im.tiled ? im.n : im.k;
+  v.nb = be ? static_cast<uint32_t>(row / be) : 0;
   v.tiled = static_cast<uint32_t>(im.tiled);
   v.units = static_cast<uint32_t>(im.units);
   v.tiles = static_cast<uint32_t>(im.tiles);

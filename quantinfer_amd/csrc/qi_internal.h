@@ -94,10 +94,11 @@ uint32_t gemm_split_splits(const Image& im, uint64_t m);
 hipError_t launch_gemm_split(const Image& im, const View& v, const float* x, uint64_t m, float* y, float* part,
                              uint32_t splits, uint8_t* records, hipStream_t st);
 
-// Row-major (blocks along N) GEMV of up to 4 activation rows, f32
-// accumulation, K split over the grid; `part` holds splits * m * n floats when
-// splits > 1.
+// Row-major (blocks along N) GEMV of up to gemv_rm_rows activation rows (4
+// for planar images, 2 for tiled ones), f32 accumulation, K split over the
+// grid; `part` holds splits * m * n floats when splits > 1.
 bool gemv_rm_supported(const Image& im);
+uint32_t gemv_rm_rows(const Image& im);
 uint32_t gemv_rm_splits(const Image& im, uint32_t m);
 hipError_t launch_gemv_rm(const Image& im, const View& v, const float* x, uint32_t m, float* y, float* part,
                           uint32_t splits, hipStream_t st);

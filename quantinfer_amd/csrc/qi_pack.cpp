@@ -123,11 +123,13 @@ int32_t plan_image(int32_t qtype, int32_t layout, uint64_t k, uint64_t n, const 
   im.nblocks = count;
   im.wide = all_f16 ? 0 : 1;
   im.f16_gemm = f16_gemm ? 1 : 0;
-  if (layout == kOutputRows && k % 256 == 0) {
-    // tiled records: 16-output tiles x 256-element units
+  if ((layout == kOutputRows && k % 256 == 0) || (layout == kRowMajor && n % 256 == 0)) {
+    // tiled records: 16-row tiles x 256-element units, a row being one
+    // output's K elements (output rows) or one k's N elements (row major)
+    const uint64_t rows = layout == kOutputRows ? n : k, cols = layout == kOutputRows ? k : n;
     im.tiled = 1;
-    im.tiles = (n + 15) / 16;
-    im.units = k / 256;
+    im.tiles = (rows + 15) / 16;
+    im.units = cols / 256;
     im.rec = record_geometry(qtype, im.wide != 0);
     im.off_qs = im.off_qh = im.off_sc = im.off_d = im.off_dmin = 0;
     im.bytes = im.tiles * im.units * im.rec.bytes + 256;
@@ -250,8 +252,9 @@ void fill_image(const Image& im, const void* blocks, void* out) {
     return;
   }
   const uint64_t be = block_elems(im.qtype);
-  // block order of the reference: output rows (n, b) -> n*NB + b; row major is flat
-  const uint64_t nb = im.layout == kOutputRows ? im.k / be : im.nblocks;
+  // block order of the reference: output rows (n, b) -> n*NB + b; row major is
+  // flat, (k, b) -> k*(N/bs) + b, taken per k (a record row) when tiled
+  const uint64_t nb = im.layout == kOutputRows ? im.k / be : im.tiled ? im.n / be : im.nblocks;
   Dest dst{&im, base};
   for (uint64_t i = 0; i < im.nblocks; ++i) {
     dst.at(i / nb, i % nb);

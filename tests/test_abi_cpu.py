@@ -213,6 +213,21 @@ def test_tiled_image_holds_exactly_the_wire_bytes(qtype):
     assert pad and not any(p.any() for p in pad)
 
 
+@pytest.mark.parametrize("qtype", ALL_Q)
+def test_tiled_row_major_image_holds_exactly_the_wire_bytes(qtype):
+    # row major with N a multiple of 256: the records of the output-rows
+    # arrangement with a row per k (its N / bs blocks, flat block k * N/bs + b);
+    # K = 40 leaves 8 padding rows in the third tile
+    k, n = 40, 512
+    blocks = po.make_weights(qtype, n, k, seed=43 + qtype, outliers=True)  # [K][N/bs] blocks along N
+    image, f16 = qa.pack_weights(qtype, qa.ROW_MAJOR, k, n, blocks)
+    assert f16
+    fields, pad = _untile(qtype, image, n, k, True)
+    wire = po.wire_pack(qtype, blocks).reshape(blocks.size, po.WIRE_BYTES[qtype])
+    _check_wire_fields(qtype, fields, wire)
+    assert pad and not any(p.any() for p in pad)
+
+
 def test_tiled_image_with_unrounded_scales_keeps_f32_entries():
     blocks = po.quantize(po.Q8_0, po.fill_normal(5, 256 * 3, 0.02))
     image, f16 = qa.pack_weights(qa.Q8_0, qa.OUTPUT_ROWS, 256, 3, blocks)

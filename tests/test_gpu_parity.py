@@ -77,6 +77,18 @@ def test_dequant_bit_exact_f16_scales(ctx, qtype):
 
 
 @pytest.mark.parametrize("qtype", ALL_Q, ids=lambda q: NAMES[q])
+def test_dequant_bit_exact_row_major(ctx, qtype):
+    """Row-major images, tiled (N = 512, K = 40: a partial last tile) and, for
+    Q8_0/Q4_0, planar (N = 96): the flat block order of the reference."""
+    shapes = [(40, 512)] + ([(40, 96)] if po.BLOCK_ELEMS[qtype] == 32 else [])
+    for k, n in shapes:
+        blocks = po.make_weights(qtype, n, k, seed=1050 + qtype + n, outliers=True)  # [K][N/bs]
+        w = ctx.weights(qtype, qa.ROW_MAJOR, k, n, blocks)
+        assert w.dequantize().tobytes() == po.dequantize(qtype, blocks).tobytes(), (k, n)
+        w.free()
+
+
+@pytest.mark.parametrize("qtype", ALL_Q, ids=lambda q: NAMES[q])
 def test_dequant_bit_exact_f32_scales(ctx, qtype):
     bs = po.BLOCK_ELEMS[qtype]
     blocks = _wide_blocks(qtype, 64, 7 + qtype)
@@ -135,10 +147,12 @@ def _assert_f32_row_major(y, x, blocks, qtype, n, what=""):
 @pytest.mark.parametrize("qtype", ALL_Q, ids=lambda q: NAMES[q])
 def test_f32_row_major_gemv_tolerance(ctx, qtype):
     """Row-major (blocks along N) weights in F32/AUTO mode: the blocks-along-N
-    GEMV (K split over the grid, 4 rows per launch) within the F32 bars, and
-    deterministic."""
+    GEMV (K split over the grid) within the F32 bars, and deterministic. N a
+    multiple of 256 takes the tiled image (2 rows per launch; K = 200 leaves a
+    partial last tile of 8 rows), Q8_0/Q4_0 with N = 128 the planar one (4 rows
+    per launch)."""
     bs = po.BLOCK_ELEMS[qtype]
-    for k, n in ((96, 4 * bs), (1024, 8 * bs), (4096, 2048 if bs == 32 else 4096)):
+    for k, n in ((96, 4 * bs), (200, 512), (1024, 8 * bs), (4096, 2048 if bs == 32 else 4096)):
         blocks = po.make_weights(qtype, n, k, seed=2200 + qtype + k, outliers=qtype >= qa.Q4_K)
         w = ctx.weights(qtype, qa.ROW_MAJOR, k, n, blocks)
         for m in (1, 3, 6):

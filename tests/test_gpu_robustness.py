@@ -105,8 +105,12 @@ def test_nonfinite_activations_planar_gemv(ctx, qtype):
 
 
 @pytest.mark.parametrize("qtype", ALL_Q, ids=lambda q: NAMES[q])
-def test_nonfinite_activations_row_major(ctx, qtype):
-    k, n, m = 512, 256, 4
+@pytest.mark.parametrize("k", [512, 48], ids=["k-split", "one-split"])
+def test_nonfinite_activations_row_major(ctx, qtype, k):
+    """NaN/Inf activations on row-major weights: the K-split sum pass (K = 512)
+    and the GEMV itself (K = 48, three tiles: one split) recompute non-finite
+    outputs in the reference's order."""
+    n, m = 256, 4
     blocks = po.make_weights(qtype, n, k, seed=8600 + qtype)  # [K, N] blocks along N
     x = _poison(po.fill_normal(8601, m * k).reshape(m, k))
     w = ctx.weights(qtype, qa.ROW_MAJOR, k, n, blocks)
@@ -114,7 +118,7 @@ def test_nonfinite_activations_row_major(ctx, qtype):
     for mode in (qa.MODE_F32, qa.MODE_EXACT):
         y = w.linear(x, mode)
         _check_nonfinite_rows(y, ref, (0, 1, 2))
-    for m1 in (1, 9):  # one row (no K-split sum pass) and 4 + 4 + 1 rows
+    for m1 in (1, 9):  # one row, and 9 rows (a last launch of one row)
         x1 = po.fill_normal(8602, m1 * k).reshape(m1, k)
         x1[0, 5] = np.inf
         y1 = w.linear(x1, qa.MODE_F32)
