@@ -183,17 +183,19 @@ __global__ __launch_bounds__(256) void rm_sum_kernel(const float* __restrict__ p
                                                      const float* __restrict__ x) {
   const uint64_t i = static_cast<uint64_t>(blockIdx.x) * 256 + threadIdx.x;
   if (i >= count) return;
-  // loads batched 8 at a time ahead of the in-order adds
-  float s = part[i];
-  uint32_t p = 1;
-  for (; p + 8 <= splits; p += 8) {
+  // loads issued 8 at a time with no condition (past the last split the last
+  // one is read again and not added), ahead of the in-order adds
+  float s = 0.0f;
+  for (uint32_t p0 = 0; p0 < splits; p0 += 8) {
     float t[8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) t[j] = part[(p + j) * count + i];
+    for (int j = 0; j < 8; ++j) {
+      const uint32_t pj = p0 + j < splits ? p0 + j : splits - 1;
+      t[j] = part[static_cast<uint64_t>(pj) * count + i];
+    }
 #pragma unroll
-    for (int j = 0; j < 8; ++j) s += t[j];
+    for (int j = 0; j < 8; ++j) s = p0 + j == 0 ? t[j] : p0 + j < splits ? s + t[j] : s;
   }
-  for (; p < splits; ++p) s += part[p * count + i];
   if (!__builtin_isfinite(s)) s = exact_row_major_col<QT, WIDE>(v, x + (i / v.n) * v.k, i % v.n);
   y[i] = s;
 }
@@ -203,12 +205,13 @@ __global__ __launch_bounds__(256) void rm_sum_kernel(const float* __restrict__ p
 constexpr int kRmtRows = 2;     // activation rows per launch
 constexpr int kRmtStride = 17;  // float4s per summed lane in LDS: 64 outputs and one of padding
 
-// Records per wavefront, all loaded before the first is consumed: the most
-// that fit beside the accumulators at two wavefronts per SIMD (a record in
-// registers: Q4_0 11, Q4_K 14, Q8_0 and Q6_K 19, Q5_K 22 VGPRs, with its
-// activations).
+// Records per wavefront, all loaded before the first is consumed (a record
+// in registers with its activation: Q4_0 11, Q4_K 14, Q8_0 and Q6_K 19, Q5_K
+// 22 VGPRs). Q4_0/Q4_K take 8 at two wavefronts per SIMD; the others 4 at
+// three, as 6 leaves them at two: Q5_K 4096 x 14336 M=1 24.4 us with 6 slots,
+// 19.0 with 4; Q6_K 23.6 / 19.1; Q4_K with 4 slots 16.6 against 15.9 (MI355X).
 constexpr uint32_t rmt_max_slots(int32_t qtype, uint32_t rows) {
-  return rows > 1 ? 4u : (qtype == kQ4_0 || qtype == kQ4_K) ? 8u : 6u;
+  return rows > 1 ? 4u : (qtype == kQ4_0 || qtype == kQ4_K) ? 8u : 4u;
 }
 
 // Record of tile t into r, with the activations of its row k = 16t + c,
