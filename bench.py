@@ -582,6 +582,10 @@ def cpu_simd_table(repeats: int = 3) -> dict:
 GEMV_POINTS = ([(0, 1, 4096, 4096, (1,))] +
                [(1, 2, k, n, (1, 4, 16)) for k, n in ((4096, 4096), (4096, 1024), (4096, 12288), (12288, 4096))] +
                [(2, q, k, n, (1, 8)) for q in (3, 4, 5) for k, n in ((4096, 14336), (14336, 4096))])
+# The same decode GEMV on row-major weights (QuantInfer layout, blocks along
+# N: backends/cpu/src/matmul.rs:14-90), the tiled row-major image: Q4_K at the
+# FFN up shape, Q4_0 at 4096 x 12288, Q8_0 at 4096^2, one row.
+RM_POINTS = [(2, 3, 4096, 14336, (1,)), (1, 2, 4096, 12288, (1,)), (0, 1, 4096, 4096, (1,))]
 # the prefill GEMM, Q8_0 and Q4_K, M x (K, N)
 GEMM_POINTS = [(3, q, k, n, (128, 512, 2048)) for q in (1, 3)
                for k, n in ((4096, 4096), (4096, 12288), (12288, 4096))]
@@ -614,18 +618,23 @@ def _median_s(fn, repeats: int) -> float:
     return statistics.median(times)
 
 
-def _cpu_point(qtype: int, k: int, n: int, m: int, blocks, unit: str, work: float) -> dict:
-    """CpuScalar (and, for Q8_0/Q4_0, the cpu-simd per-block dot, cpu-simd
-    lib.rs:179-204) on one pinned core over `rows` <= m activation rows,
-    scaled linearly to m rows (rows are independent, matmul.rs:146-158).
-    `work` is the point's bytes (GB/s) or flops (TFLOP/s)."""
+def _cpu_point(qtype: int, k: int, n: int, m: int, blocks, unit: str, work: float,
+               row_major: bool = False) -> dict:
+    """CpuScalar (and, for Q8_0/Q4_0 output rows, the cpu-simd per-block
+    dot, cpu-simd lib.rs:179-204) on one pinned core over `rows` <= m
+    activation rows, scaled linearly to m rows (rows are independent,
+    matmul.rs:146-158). `work` is the point's bytes (GB/s) or flops
+    (TFLOP/s). row_major: CpuScalar's blocks-along-N matmul (matmul.rs:14-90)."""
     from oracle import pyoracle as po
 
     rows = m if m <= 4 else 2
     x = normal(0x5EED8100 + m, rows * k).reshape(rows, k)
     isa = 2 if po.simd_available(2) else (1 if po.simd_available(1) else 0)
-    legs = [("scalar", lambda: po.matmul_output_rows(qtype, x, blocks, n))]
-    if qtype in (1, 2) and isa:
+    if row_major:
+        legs = [("scalar", lambda: po.matmul_row_major(qtype, x, blocks, n))]
+    else:
+        legs = [("scalar", lambda: po.matmul_output_rows(qtype, x, blocks, n))]
+    if qtype in (1, 2) and isa and not row_major:
         legs.append(("simd", lambda: po.matmul_output_rows_simd(qtype, isa, x, blocks, n)))
     out = {"unit": unit, "cores": 1, "kind": "port"}
     with _OneCore():
@@ -637,7 +646,8 @@ def _cpu_point(qtype: int, k: int, n: int, m: int, blocks, unit: str, work: floa
         out["simd"] = None
     out["value"] = out["scalar"]
     out["sample"] = (f"{rows} of {m} rows, scaled x{m // rows}" if rows < m else f"all {m} rows") + \
-        f"; oracle C port of CpuScalar (matmul.rs:119-160, :282-332)" + \
+        (f"; oracle C port of CpuScalar's row-major matmul (matmul.rs:14-90)" if row_major else
+         f"; oracle C port of CpuScalar (matmul.rs:119-160, :282-332)") + \
         (f" and the cpu-simd {['', 'avx2', 'avx512f'][isa]} block dot" if len(legs) > 1 else
          ("; no cpu-simd path for K-quants in the reference" if qtype >= 3 else "")) + \
         f"; 1 pinned core of {host_cpu()}"
@@ -687,16 +697,20 @@ def configs_table(steps: int, warmup: int, with_cpu: bool) -> dict:
     import quantinfer_amd as qa
 
     ctx = qa.Context(0)
-    out = {"gemv": [], "gemm": []}
-    for kind, points in (("gemv", GEMV_POINTS), ("gemm", GEMM_POINTS)):
+    out = {"gemv": [], "gemv_row_major": [], "gemm": []}
+    for kind, points in (("gemv", GEMV_POINTS), ("gemv_row_major", RM_POINTS), ("gemm", GEMM_POINTS)):
         for cfg_i, qtype, k, n, ms in points:
-            blocks = weight_blocks(qtype, k, n, seed=0x5EED0000 + qtype)
+            row_major = kind == "gemv_row_major"
+            # row major: K rows of N / bs blocks along N
+            blocks = weight_blocks(qtype, n, k, seed=0x5EED0000 + qtype) if row_major else \
+                weight_blocks(qtype, k, n, seed=0x5EED0000 + qtype)
             wbytes = n * (k // BLOCK[qtype]) * WIRE[qtype]
             copies = max(2, int(-(-512e6 // wbytes)))
-            weights = [ctx.weights(qtype, qa.OUTPUT_ROWS, k, n, blocks) for _ in range(copies)]
+            layout = qa.ROW_MAJOR if row_major else qa.OUTPUT_ROWS
+            weights = [ctx.weights(qtype, layout, k, n, blocks) for _ in range(copies)]
             for m in ms:
                 abytes = algorithmic_bytes(qtype, k, n, m)
-                if kind == "gemv":
+                if kind != "gemm":
                     us = _time_rotating(weights, m, k, n, qa.MODE_F32, steps, warmup)
                     gbps = abytes / (us * 1e-6) / 1e9
                     entry = {"config": cfg_i, "qtype": QNAME[qtype], "m": m, "k": k, "n": n,
@@ -705,7 +719,7 @@ def configs_table(steps: int, warmup: int, with_cpu: bool) -> dict:
                                           "unit": "GB/s", "frac": round(gbps / HBM_PEAK_GBPS, 4),
                                           "algorithmic_bytes": abytes}}
                     if with_cpu:
-                        entry["cpu_baseline"] = _cpu_point(qtype, k, n, m, blocks, "GB/s", abytes)
+                        entry["cpu_baseline"] = _cpu_point(qtype, k, n, m, blocks, "GB/s", abytes, row_major)
                 else:
                     reps = max(3, steps // 2) if m >= 2048 else steps
                     us = _time_rotating(weights, m, k, n, qa.MODE_MFMA, reps, max(2, warmup))
@@ -733,7 +747,8 @@ def configs_table(steps: int, warmup: int, with_cpu: bool) -> dict:
                 w.free()
     out["device"] = ctx.device_name()
     ctx.close()
-    out["note"] = ("GEMV: F32 mode, us per call over resident weight copies (>= 512 MB); GEMM: MFMA mode, "
+    out["note"] = ("GEMV: F32 mode, us per call over resident weight copies (>= 512 MB); gemv_row_major: "
+                   "the same on row-major (blocks along N) weights, the tiled row-major image; GEMM: MFMA mode, "
                    "f16 activation conversion + GEMM per call (f32_mode: the same point in F32 mode, "
                    "the split-half GEMM); roofline.frac of the GEMM is against "
                    "min(f16 peak, intensity x HBM peak); cpu_baseline: scalar CpuScalar port and, for "
