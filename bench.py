@@ -80,17 +80,21 @@ def normal(seed: int, n: int, std: float = 1.0):
 
 
 def gemv_bench(qtype: int, k: int, n: int, m: int, steps: int, warmup: int, copies_mb: float = 512.0,
-               with_abi: bool = False) -> dict:
+               with_abi: bool = False, row_major: bool = False) -> dict:
     """`steps` passes over C resident weight copies, one launch per copy,
-    event-timed on the launch stream; plus the event region's own cost."""
+    event-timed on the launch stream; plus the event region's own cost.
+    row_major: the weight in the QuantInfer layout (K rows of N / bs blocks
+    along N, backends/cpu/src/matmul.rs:14-90)."""
     import quantinfer_amd as qa
     from quantinfer_amd import hiprt
 
     ctx = qa.Context(0)
-    blocks = weight_blocks(qtype, k, n, seed=0x5EED0000 + qtype)
+    blocks = weight_blocks(qtype, n, k, seed=0x5EED0000 + qtype) if row_major else \
+        weight_blocks(qtype, k, n, seed=0x5EED0000 + qtype)
     wbytes = n * (k // BLOCK[qtype]) * WIRE[qtype]
     copies = max(1, int(-(-copies_mb * 1e6 // wbytes)))
-    weights = [ctx.weights(qtype, qa.OUTPUT_ROWS, k, n, blocks) for _ in range(copies)]
+    layout = qa.ROW_MAJOR if row_major else qa.OUTPUT_ROWS
+    weights = [ctx.weights(qtype, layout, k, n, blocks) for _ in range(copies)]
     x = hiprt.DeviceBuffer.from_array(normal(0x5EED1000, m * k).reshape(m, k))
     y = hiprt.DeviceBuffer(m * n * 4)
     stream = hiprt.Stream()
@@ -144,12 +148,14 @@ def gemv_bench(qtype: int, k: int, n: int, m: int, steps: int, warmup: int, copi
     return out
 
 
-def gemv_line(qtype: int, k: int, n: int, m: int, g: dict, steps: int, warmup: int) -> dict:
+def gemv_line(qtype: int, k: int, n: int, m: int, g: dict, steps: int, warmup: int,
+              row_major: bool = False) -> dict:
     """The JSON object of one GEMV measurement."""
     abytes = algorithmic_bytes(qtype, k, n, m)
     us_launch = g["region_ms"] * 1e3 / g["launches"]
     gbps = abytes / (us_launch * 1e-6) / 1e9
     q = QNAME[qtype]
+    lay = "row_major" if row_major else "output_rows"
     return {
         "metric": f"quant GEMV GB/s (% of HBM peak) at {k}x{n}",
         "value": round(gbps, 2), "unit": "GB/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
@@ -157,14 +163,15 @@ def gemv_line(qtype: int, k: int, n: int, m: int, g: dict, steps: int, warmup: i
         "scaling": "weak", "vs_baseline": None, "dtype": "f32",
         "data": f"synthetic: N(0,0.02^2) weights{' with 0.5% N(0,0.2^2) outliers' if qtype >= 3 else ''}"
                 f" quantized to {q} (qi_hip_quantize, f16 storage); x ~ N(0,1)",
-        "config": {"workload": f"{q}_gemv_output_rows_m{m}_k{k}_n{n}", "qtype": q, "m": m, "k": k,
+        "config": {"workload": f"{q}_gemv_{lay}_m{m}_k{k}_n{n}", "qtype": q, "m": m, "k": k,
                    "n": n, "mode": "f32", "weight_copies": g["copies"],
                    "step": f"one GEMV launch over each of the {g['copies']} resident weight copies",
                    "launches": g["launches"], "us_per_launch": round(us_launch, 3),
                    "event_region_overhead_us": round(g["empty_region_us"], 2), "device": g["device"]},
         "roofline": {"bound": "hbm", "achieved": round(gbps, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(gbps / HBM_PEAK_GBPS, 4),
-                     "traffic": traffic_from_profile(f"{q}_gemv_{k}x{n}_traffic.md" if m == 1
+                     "traffic": traffic_from_profile(f"{q}_gemv_row_major_{k}x{n}_traffic.md" if row_major
+                                                     else f"{q}_gemv_{k}x{n}_traffic.md" if m == 1
                                                      else f"{q}_gemv_m{m}_{k}x{n}_counters.md")},
     }
 
@@ -950,6 +957,8 @@ def main():
     ap.add_argument("--cpu-simd", action="store_true",
                     help="only the CPU table: scalar and cpu-simd Q8_0/Q4_0 kernels, one core")
     ap.add_argument("--qtype", default="q4_k", help="gemv/gemm: q8_0, q4_0, q4_k, q5_k or q6_k")
+    ap.add_argument("--layout", choices=["output_rows", "row_major"], default="output_rows",
+                    help="gemv: the weight layout (row_major: QuantInfer blocks along N, the GEMV alone)")
     ap.add_argument("--mode", choices=["mfma", "f32"], default="mfma",
                     help="gemm: the f16-operand GEMM (mfma) or F32 mode's split-half GEMM (f32; Q4_K/Q5_K)")
     ap.add_argument("--mkn", default=None,
@@ -997,10 +1006,12 @@ def main():
         return
 
     m, k, n = (int(v) for v in (args.mkn or f"{M},{K},{N}").split(","))
-    g = gemv_bench(qt, k, n, m, args.steps, args.warmup, with_abi=not args.no_abi)
-    line = gemv_line(qt, k, n, m, g, args.steps, args.warmup)
-    line["metric"] = "quant GEMV GB/s (% of HBM peak) at 4096x14336; Qwen3-8B-shape decode tok/s"
-    line["cpu_baseline"] = None if args.no_cpu or (m, k, n) != (M, K, N) else cpu_baseline(qt)
+    rm = args.layout == "row_major"
+    g = gemv_bench(qt, k, n, m, args.steps, args.warmup, with_abi=not args.no_abi, row_major=rm)
+    line = gemv_line(qt, k, n, m, g, args.steps, args.warmup, row_major=rm)
+    if not rm:
+        line["metric"] = "quant GEMV GB/s (% of HBM peak) at 4096x14336; Qwen3-8B-shape decode tok/s"
+    line["cpu_baseline"] = None if args.no_cpu or (m, k, n) != (M, K, N) or rm else cpu_baseline(qt)
     abytes = algorithmic_bytes(qt, k, n, m)
     line["through_abi"] = None if args.no_abi else {
         "value": round(abytes / (g["abi_ms"] * 1e-3) / 1e9, 2), "unit": "GB/s",
@@ -1008,7 +1019,7 @@ def main():
         "note": "qi_hip_linear with host x and y (H2D, GEMV, D2H, synchronous): the "
                 "PCIe-inclusive KernelBackend call, median over calls; not `value`",
     }
-    if (qt, m, k, n) == (3, M, K, N):
+    if (qt, m, k, n) == (3, M, K, N) and not rm:
         g8 = gemv_bench(1, K, N, M, args.steps, args.warmup)
         line["gemv_q8_0"] = gemv_line(1, K, N, M, g8, args.steps, args.warmup)
         if not args.no_cpu:
