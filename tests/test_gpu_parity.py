@@ -163,6 +163,26 @@ def test_f32_row_major_gemv_tolerance(ctx, qtype):
         w.free()
 
 
+@pytest.mark.parametrize("qtype", ALL_Q, ids=lambda q: NAMES[q])
+def test_row_major_f32_block_scales(ctx, qtype):
+    """Row-major tiled images with f32 block scales (random codes, scales not
+    f16-exact): F32 mode within the bars with one split (K = 48) and with a
+    split sum (K = 1024), EXACT mode and dequantize bit-identical."""
+    n = 512
+    for k in (48, 1024):
+        count = k * n // po.BLOCK_ELEMS[qtype]
+        blocks = _wide_blocks(qtype, count, 2400 + qtype + k)
+        w = ctx.weights(qtype, qa.ROW_MAJOR, k, n, blocks)
+        assert w.info().f16_scales == 0
+        assert w.dequantize().tobytes() == po.dequantize(qtype, blocks).tobytes()
+        for m in (1, 2, 3):
+            x = po.fill_normal(3400 + m + k, m * k).reshape(m, k)
+            _assert_f32_row_major(w.linear(x, qa.MODE_F32), x, blocks, qtype, n, (k, m))
+        x = po.fill_normal(3410 + k, 2 * k).reshape(2, k)
+        assert w.linear(x, qa.MODE_EXACT).tobytes() == po.matmul_row_major(qtype, x, blocks, n).tobytes()
+        w.free()
+
+
 def test_exact_mode_f32_weights_bit_identical(ctx):
     """EXACT mode on F32 weights is CpuScalar's sequential-k matmul bit for
     bit (N = 1001 is not a multiple of 4, the width the streaming GEMV needs:
