@@ -118,7 +118,7 @@ def test_nonfinite_activations_row_major(ctx, qtype, k):
     for mode in (qa.MODE_F32, qa.MODE_EXACT):
         y = w.linear(x, mode)
         _check_nonfinite_rows(y, ref, (0, 1, 2))
-    for m1 in (1, 9):  # one row, and 9 rows (a last launch of one row)
+    for m1 in (1, 9, 20):  # one row, 9 rows (a last launch of one row), 20 rows
         x1 = po.fill_normal(8602, m1 * k).reshape(m1, k)
         x1[0, 5] = np.inf
         y1 = w.linear(x1, qa.MODE_F32)
