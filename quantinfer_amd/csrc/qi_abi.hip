@@ -170,11 +170,26 @@ qi_hip_status grow_ws(qi_hip_ctx* c, hipStream_t st, float** buf, uint64_t* cap,
 // function decides, so that the growing path (run_linear) and the scratch
 // path (qi_hip_linear_device_noalloc) take the same kernels.
 struct LinearPlan {
-  enum Kind { kGemm, kRowMajor, kMfma, kSplitGemm, kPlanar, kF32Gemv, kF32Gemm, kExact } kind = kExact;
+  enum Kind { kGemm, kRowMajor, kRowMajorGemm, kMfma, kSplitGemm, kPlanar, kF32Gemv, kF32Gemm, kExact } kind = kExact;
   uint64_t m_pad = 0;
-  uint32_t splits = 1;  // GEMM K splits, or row-major GEMV K splits for 4-row chunks
+  uint32_t splits = 1;  // GEMM K splits, or row-major GEMV K splits per row chunk
   uint64_t h_floats = 0, s_floats = 0, d_floats = 0;  // f16 activations, partials, records
+  uint64_t kslice = 0;  // kRowMajorGemm: weight rows per dequantized slice
 };
+
+// Rows from which row-major weights (tiled image, K a multiple of 4) take
+// the K-slice GEMM instead of the GEMV's 2-row launches, each of which reads
+// the whole weight: rows [k0, k0 + kc) of the weight are dequantized
+// (bit-exact f32) into a workspace of at most kRmSliceFloats and multiplied by
+// the f32 matrix-core GEMM (the F32 weights' kernel), each slice adding to y;
+// then non-finite outputs are recomputed in the reference's order. Measured
+// on MI355X, us per call, GEMV launches / K-slice GEMM: Q4_K 4096x14336 M=32
+// 422 / 402, M=64 839 / 580, M=128 1672 / 569, M=512 6672 / 1010; Q8_0
+// 4096x4096 M=32 214 / 265, M=64 424 / 403, M=512 3336 / 388; Q4_K
+// 14336x4096 M=32 445 / 938, M=64 889 / 1432 (few workgroups per slice at
+// N = 4096), M=512 7102 / 1367.
+constexpr uint64_t kRmGemmMinRows = 128;
+constexpr uint64_t kRmSliceFloats = 8ull << 20;
 
 // Rows of a chunk at which the 2-16 row GEMV switches from the int8-digit
 // kernel (qi_gemv_rows.hip) to the split-half kernel (qi_gemv_half.hip): the
@@ -230,6 +245,15 @@ qi_hip_status plan_linear(const Image& im, uint64_t m, int32_t mode, LinearPlan*
     p->kind = LinearPlan::kF32Gemv;
     p->splits = qi::f32w_splits(im);
     if (p->splits > 1) p->s_floats = static_cast<uint64_t>(p->splits) * (m < 8 ? m : 8) * im.n;
+    return QI_HIP_OK;
+  }
+  if (mode != QI_HIP_MODE_EXACT && qi::gemv_rm_supported(im) && im.tiled && m >= kRmGemmMinRows &&
+      im.k % 4 == 0) {
+    p->kind = LinearPlan::kRowMajorGemm;
+    uint64_t kc = kRmSliceFloats / im.n / 32 * 32;
+    if (kc < 32) kc = 32;
+    p->kslice = kc < im.k ? kc : im.k;
+    p->d_floats = p->kslice * im.n;
     return QI_HIP_OK;
   }
   if (mode != QI_HIP_MODE_EXACT && qi::gemv_rm_supported(im)) {
@@ -319,6 +343,17 @@ qi_hip_status enqueue_linear(const qi_hip_weights* w, const LinearPlan& p, const
       }
       return QI_HIP_OK;
     }
+    case LinearPlan::kRowMajorGemm:
+      // weight rows [k0, k0 + kc) as f32 [kc, N] in dws, then the f32 GEMM
+      // of x's columns [k0, k0 + kc), stored by the first slice and added by
+      // the others; then the non-finite outputs in the reference's order
+      for (uint64_t k0 = 0; k0 < im.k; k0 += p.kslice) {
+        const uint64_t kc = im.k - k0 < p.kslice ? im.k - k0 : p.kslice;
+        QI_HIP_TRY(qi::launch_dequant_rm_rows(im, v, k0, kc, dws, st), "dequantize row-major weight rows");
+        QI_HIP_TRY(qi::launch_f32_gemm_kslice(dws, kc, im.n, x + k0, im.k, m, y, k0 > 0, st), "row-major slice GEMM");
+      }
+      QI_HIP_TRY(qi::launch_rm_fix_nonfinite(im, v, x, m, y, st), "row-major non-finite outputs");
+      return QI_HIP_OK;
     case LinearPlan::kMfma:
     case LinearPlan::kPlanar:
       for (uint64_t m0 = 0; m0 < m; m0 += 16) {

@@ -198,11 +198,15 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr uint32_t kF32Kt = 32;
 
-template <int WM, int WN, int TM, int TN>
+// SLICE: W holds rows [k0, k0 + K) of a longer weight; x keeps its full row
+// stride ldx (x points at column k0); the products add to y after the first
+// slice (accum) and non-finite sums are left for the caller to recompute.
+template <int WM, int WN, int TM, int TN, bool SLICE>
 __global__ __launch_bounds__(WM * WN * 64) void f32w_gemm_kernel(const float* __restrict__ W, uint32_t K,
                                                                   uint32_t N, const float* __restrict__ x,
                                                                   uint32_t M, uint32_t mtiles,
-                                                                  uint32_t ntiles, float* __restrict__ y) {
+                                                                  uint32_t ntiles, float* __restrict__ y,
+                                                                  uint32_t ldx, uint32_t accum) {
   constexpr int MT = WM * TM * 16, NT = WN * TN * 16, KT = kF32Kt, THREADS = WM * WN * 64;
   constexpr int XS = KT + 4, WS = NT + 4;
   constexpr int XL = MT * KT / 4 / THREADS, WL = KT * NT / 4 / THREADS;  // 16-byte loads per thread
@@ -224,7 +228,7 @@ __global__ __launch_bounds__(WM * WN * 64) void f32w_gemm_kernel(const float* __
     for (int i = 0; i < XL; ++i) {
       const uint32_t e = t + i * THREADS, row = e / (KT / 4), k = k0 + (e % (KT / 4)) * 4;
       xr[i] = (m0 + row < M && k < K)
-                  ? *reinterpret_cast<const f32x4*>(x + static_cast<uint64_t>(m0 + row) * K + k)
+                  ? *reinterpret_cast<const f32x4*>(x + static_cast<uint64_t>(m0 + row) * (SLICE ? ldx : K) + k)
                   : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     }
 #pragma unroll
@@ -264,6 +268,12 @@ __global__ __launch_bounds__(WM * WN * 64) void f32w_gemm_kernel(const float* __
     if (s + 1 < stages) load((s + 1) * KT);
     const float* xb = &xs[b][(wm * TM * 16 + r16) * XS + 4 * g];
     const float* wb = &ws[b][(4 * g) * WS + wn * TN * 16 + r16];
+    // SLICE: the stage's KT products in sums of their own, added to the
+    // running ones once per stage, so that each output's chain of dependent
+    // f32 additions is KT / 4 long and then K / KT (dequantized Q8_0 weights
+    // at K = 4096 missed the F32 bars over 130 x 4096 outputs, 1.09e-5, with
+    // one chain over each 2048-row slice)
+    [[maybe_unused]] f32x4 part[TM][TN];
 #pragma unroll
     for (int kk = 0; kk < KT / 16; ++kk) {
       f32x4 a[TM];
@@ -277,8 +287,20 @@ __global__ __launch_bounds__(WM * WN * 64) void f32w_gemm_kernel(const float* __
 #pragma unroll
         for (int i = 0; i < TM; ++i)
 #pragma unroll
-          for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i][st], bv[j], acc[i][j], 0, 0, 0);
+          for (int j = 0; j < TN; ++j) {
+            if constexpr (SLICE)
+              part[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(
+                  a[i][st], bv[j], kk == 0 && st == 0 ? f32x4{0.0f, 0.0f, 0.0f, 0.0f} : part[i][j], 0, 0, 0);
+            else
+              acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i][st], bv[j], acc[i][j], 0, 0, 0);
+          }
       }
+    }
+    if constexpr (SLICE) {
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] += part[i][j];
     }
     if (s + 1 < stages) store(b ^ 1);
     __syncthreads();
@@ -296,23 +318,36 @@ __global__ __launch_bounds__(WM * WN * 64) void f32w_gemm_kernel(const float* __
         const uint32_t m = m0 + wm * TM * 16 + i * 16 + 4 * g + q;
         if (m >= M) continue;
         float v = acc[i][j][q];
-        if (!__builtin_isfinite(v)) v = f32w_exact(W, K, N, x + static_cast<uint64_t>(m) * K, n);
-        y[static_cast<uint64_t>(m) * N + n] = v;
+        float* dst = y + static_cast<uint64_t>(m) * N + n;
+        if constexpr (SLICE) {
+          if (accum) v = *dst + v;
+        } else if (!__builtin_isfinite(v)) {
+          v = f32w_exact(W, K, N, x + static_cast<uint64_t>(m) * K, n);
+        }
+        *dst = v;
       }
     }
 }
 
-template <int WM, int WN, int TM, int TN>
+template <int WM, int WN, int TM, int TN, bool SLICE>
 hipError_t launch_f32w_gemm_t(const float* W, uint32_t K, uint32_t N, const float* x, uint32_t M, float* y,
-                              hipStream_t st) {
+                              uint32_t ldx, uint32_t accum, hipStream_t st) {
   constexpr uint32_t MT = WM * TM * 16, NT = WN * TN * 16;
   const uint32_t mtiles = (M + MT - 1) / MT, ntiles = (N + NT - 1) / NT;
   const uint64_t tiles = static_cast<uint64_t>(mtiles) * ntiles;
   if (tiles > 0x7fffffffull) return hipErrorInvalidValue;
   const uint32_t grid = static_cast<uint32_t>((tiles + 7) / 8 * 8);
-  hipLaunchKernelGGL((f32w_gemm_kernel<WM, WN, TM, TN>), dim3(grid), dim3(WM * WN * 64), 0, st, W, K, N, x, M,
-                     mtiles, ntiles, y);
+  hipLaunchKernelGGL((f32w_gemm_kernel<WM, WN, TM, TN, SLICE>), dim3(grid), dim3(WM * WN * 64), 0, st, W, K, N, x,
+                     M, mtiles, ntiles, y, ldx, accum);
   return hipGetLastError();
+}
+
+template <bool SLICE>
+hipError_t launch_f32w_gemm_any(const float* W, uint32_t K, uint32_t N, const float* x, uint32_t M, float* y,
+                                uint32_t ldx, uint32_t accum, hipStream_t st) {
+  if (M <= 32) return launch_f32w_gemm_t<1, 4, 2, 4, SLICE>(W, K, N, x, M, y, ldx, accum, st);
+  if (M <= 64) return launch_f32w_gemm_t<1, 4, 4, 4, SLICE>(W, K, N, x, M, y, ldx, accum, st);
+  return launch_f32w_gemm_t<2, 2, 4, 4, SLICE>(W, K, N, x, M, y, ldx, accum, st);
 }
 
 }  // namespace
@@ -324,9 +359,16 @@ hipError_t launch_f32w_gemm(const Image& im, const View& v, const float* x, uint
     return hipErrorInvalidValue;
   const float* W = reinterpret_cast<const float*>(v.qs);
   const uint32_t K = static_cast<uint32_t>(im.k), N = static_cast<uint32_t>(im.n), M = static_cast<uint32_t>(m);
-  if (M <= 32) return launch_f32w_gemm_t<1, 4, 2, 4>(W, K, N, x, M, y, st);
-  if (M <= 64) return launch_f32w_gemm_t<1, 4, 4, 4>(W, K, N, x, M, y, st);
-  return launch_f32w_gemm_t<2, 2, 4, 4>(W, K, N, x, M, y, st);
+  return launch_f32w_gemm_any<false>(W, K, N, x, M, y, K, 0, st);
+}
+
+hipError_t launch_f32_gemm_kslice(const float* w, uint64_t kc, uint64_t n, const float* x, uint64_t ldx, uint64_t m,
+                                  float* y, bool accum, hipStream_t st) {
+  if (w == nullptr || kc < 1 || kc % 4 != 0 || n < 1 || n % 4 != 0 || ldx < kc || ldx % 4 != 0 || m < 1 ||
+      m > 0x7fffffffull || ldx > 0x7fffffffull || n > 0x7fffffffull)
+    return hipErrorInvalidValue;
+  return launch_f32w_gemm_any<true>(w, static_cast<uint32_t>(kc), static_cast<uint32_t>(n), x,
+                                    static_cast<uint32_t>(m), y, static_cast<uint32_t>(ldx), accum ? 1u : 0u, st);
 }
 
 }  // namespace qi

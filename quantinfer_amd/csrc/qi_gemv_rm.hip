@@ -418,6 +418,112 @@ hipError_t launch_rm_q(const View& v, const float* x, uint32_t m, float* y, floa
 
 }  // namespace
 
+namespace {
+
+// Weight rows [k0, k0 + kc) of a tiled row-major image as an f32 [kc, N]
+// matrix: wavefront w of workgroup (x, y) takes the record of unit 4x + w in
+// tile k0 / 16 + y, lane 16g + c its row c, lane group g (Unit<QT>), and
+// stores that row's 64 weights of the lane group, 8 consecutive per step.
+// Each weight by the reference's operation sequence, so bit-identical to
+// dequantize (matmul.rs:162-280): Q8_0 d q; Q4_0 d (q - 8); Q4_K/Q5_K
+// (d sc) q - dmin m, no fused multiply-add (the file is compiled with
+// -ffp-contract=off); Q6_K (d sc) (q - 32).
+template <int QT, bool WIDE>
+__global__ __launch_bounds__(256) void dequant_rm_rows_kernel(View v, uint32_t k0, uint32_t kc,
+                                                              float* __restrict__ out) {
+  using U = Unit<QT>;
+  constexpr int kW = U::kWindows, kS = U::kSteps;
+  const uint32_t lane = threadIdx.x & 63, g = lane >> 4, c = lane & 15;
+  const uint32_t u = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (u >= v.units) return;
+  const uint32_t t = k0 / 16 + blockIdx.y, k = 16 * t + c;
+  typename U::Raw r;
+  U::template load<WIDE, true>(v.qs + (static_cast<uint64_t>(t) * v.units + u) * v.rec.bytes, lane, r);
+  if (k < k0 || k >= k0 + kc) return;
+  float a[kW], b[kW];
+  U::template scales<WIDE>(g, r, a, b);
+  float* row = out + static_cast<uint64_t>(k - k0) * v.n + static_cast<uint64_t>(u) * 256;
+#pragma unroll
+  for (int st = 0; st < 8; ++st) {
+    const uint64_t q = static_cast<uint64_t>(U::codes(r, g, st));
+    const int w = st / kS;
+    float o[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const uint32_t byte = static_cast<uint32_t>(q >> (8 * e)) & 0xFFu;
+      if constexpr (QT == kQ8_0) {
+        o[e] = a[w] * static_cast<float>(static_cast<int8_t>(byte));
+      } else if constexpr (QT == kQ4_0) {
+        o[e] = a[w] * (static_cast<float>(byte) - 8.0f);
+      } else if constexpr (QT == kQ6_K) {
+        o[e] = a[w] * static_cast<float>(static_cast<int32_t>(byte) - 32);
+      } else {
+        o[e] = a[w] * static_cast<float>(byte) - b[w];
+      }
+    }
+    float4* dst = reinterpret_cast<float4*>(row + window_first<QT>(g, st / 4) + 8 * (st % 4));
+    dst[0] = make_float4(o[0], o[1], o[2], o[3]);
+    dst[1] = make_float4(o[4], o[5], o[6], o[7]);
+  }
+}
+
+template <int QT, bool WIDE>
+hipError_t launch_rows_q(const View& v, uint32_t k0, uint32_t kc, float* out, hipStream_t st) {
+  const dim3 grid((v.units + 3) / 4, (k0 + kc + 15) / 16 - k0 / 16);
+  hipLaunchKernelGGL((dequant_rm_rows_kernel<QT, WIDE>), grid, dim3(256), 0, st, v, k0, kc, out);
+  return hipGetLastError();
+}
+
+template <int QT, bool WIDE>
+__global__ __launch_bounds__(256) void rm_fix_kernel(View v, const float* __restrict__ x, uint64_t count,
+                                                     float* __restrict__ y) {
+  const uint64_t i = static_cast<uint64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= count || __builtin_isfinite(y[i])) return;
+  y[i] = exact_row_major_col<QT, WIDE>(v, x + (i / v.n) * v.k, i % v.n);
+}
+
+template <int QT, bool WIDE>
+hipError_t launch_fix_q(const View& v, const float* x, uint64_t count, float* y, hipStream_t st) {
+  hipLaunchKernelGGL((rm_fix_kernel<QT, WIDE>), dim3(static_cast<uint32_t>((count + 255) / 256)), dim3(256), 0, st, v,
+                     x, count, y);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_dequant_rm_rows(const Image& im, const View& v, uint64_t k0, uint64_t kc, float* out,
+                                  hipStream_t st) {
+  // k0 on a tile boundary; grid y = the tiles rows [k0, k0 + kc) touch
+  if (im.layout != kRowMajor || !im.tiled || kc == 0 || k0 % 16 != 0 || k0 + kc > im.k || im.k > 0xFFFFFFF0ull ||
+      v.units != im.n / 256 || (kc + 15) / 16 > 0xFFFFu)
+    return hipErrorInvalidValue;
+  const uint32_t a = static_cast<uint32_t>(k0), c = static_cast<uint32_t>(kc);
+  const bool w = im.wide != 0;
+  switch (im.qtype) {
+    case kQ8_0: return w ? launch_rows_q<kQ8_0, true>(v, a, c, out, st) : launch_rows_q<kQ8_0, false>(v, a, c, out, st);
+    case kQ4_0: return w ? launch_rows_q<kQ4_0, true>(v, a, c, out, st) : launch_rows_q<kQ4_0, false>(v, a, c, out, st);
+    case kQ4_K: return w ? launch_rows_q<kQ4_K, true>(v, a, c, out, st) : launch_rows_q<kQ4_K, false>(v, a, c, out, st);
+    case kQ5_K: return w ? launch_rows_q<kQ5_K, true>(v, a, c, out, st) : launch_rows_q<kQ5_K, false>(v, a, c, out, st);
+    case kQ6_K: return w ? launch_rows_q<kQ6_K, true>(v, a, c, out, st) : launch_rows_q<kQ6_K, false>(v, a, c, out, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_rm_fix_nonfinite(const Image& im, const View& v, const float* x, uint64_t m, float* y,
+                                   hipStream_t st) {
+  const uint64_t count = m * im.n;
+  if (im.layout != kRowMajor || count == 0 || (count + 255) / 256 > 0x7fffffffull) return hipErrorInvalidValue;
+  const bool w = im.wide != 0;
+  switch (im.qtype) {
+    case kQ8_0: return w ? launch_fix_q<kQ8_0, true>(v, x, count, y, st) : launch_fix_q<kQ8_0, false>(v, x, count, y, st);
+    case kQ4_0: return w ? launch_fix_q<kQ4_0, true>(v, x, count, y, st) : launch_fix_q<kQ4_0, false>(v, x, count, y, st);
+    case kQ4_K: return w ? launch_fix_q<kQ4_K, true>(v, x, count, y, st) : launch_fix_q<kQ4_K, false>(v, x, count, y, st);
+    case kQ5_K: return w ? launch_fix_q<kQ5_K, true>(v, x, count, y, st) : launch_fix_q<kQ5_K, false>(v, x, count, y, st);
+    case kQ6_K: return w ? launch_fix_q<kQ6_K, true>(v, x, count, y, st) : launch_fix_q<kQ6_K, false>(v, x, count, y, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
 bool gemv_rm_supported(const Image& im) {
   // tiled: grid x = units, grid y = splits of at most 4 * 4 records per workgroup
   return im.layout == kRowMajor && im.qtype >= kQ8_0 && im.qtype <= kQ6_K && im.n % block_elems(im.qtype) == 0 &&
