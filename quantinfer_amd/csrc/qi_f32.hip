@@ -201,7 +201,8 @@ constexpr uint32_t kF32Kt = 32;
 // SLICE: W holds rows [k0, k0 + K) of a longer weight; x keeps its full row
 // stride ldx (x points at column k0); the products add to y after the first
 // slice (accum) and non-finite sums are left for the caller to recompute.
-template <int WM, int WN, int TM, int TN, bool SLICE>
+// STAGED (slices only): per-stage sums, below.
+template <int WM, int WN, int TM, int TN, bool SLICE, bool STAGED = false>
 __global__ __launch_bounds__(WM * WN * 64) void f32w_gemm_kernel(const float* __restrict__ W, uint32_t K,
                                                                   uint32_t N, const float* __restrict__ x,
                                                                   uint32_t M, uint32_t mtiles,
@@ -268,11 +269,12 @@ __global__ __launch_bounds__(WM * WN * 64) void f32w_gemm_kernel(const float* __
     if (s + 1 < stages) load((s + 1) * KT);
     const float* xb = &xs[b][(wm * TM * 16 + r16) * XS + 4 * g];
     const float* wb = &ws[b][(4 * g) * WS + wn * TN * 16 + r16];
-    // SLICE: the stage's KT products in sums of their own, added to the
+    // STAGED: the stage's KT products in sums of their own, added to the
     // running ones once per stage, so that each output's chain of dependent
     // f32 additions is KT / 4 long and then K / KT (dequantized Q8_0 weights
     // at K = 4096 missed the F32 bars over 130 x 4096 outputs, 1.09e-5, with
-    // one chain over each 2048-row slice)
+    // one chain over each 2048-row slice). It doubles the accumulator
+    // registers (one wavefront per SIMD for the 128 x 128 tile).
     [[maybe_unused]] f32x4 part[TM][TN];
 #pragma unroll
     for (int kk = 0; kk < KT / 16; ++kk) {
@@ -288,7 +290,7 @@ __global__ __launch_bounds__(WM * WN * 64) void f32w_gemm_kernel(const float* __
         for (int i = 0; i < TM; ++i)
 #pragma unroll
           for (int j = 0; j < TN; ++j) {
-            if constexpr (SLICE)
+            if constexpr (STAGED)
               part[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(
                   a[i][st], bv[j], kk == 0 && st == 0 ? f32x4{0.0f, 0.0f, 0.0f, 0.0f} : part[i][j], 0, 0, 0);
             else
@@ -296,7 +298,7 @@ __global__ __launch_bounds__(WM * WN * 64) void f32w_gemm_kernel(const float* __
           }
       }
     }
-    if constexpr (SLICE) {
+    if constexpr (STAGED) {
 #pragma unroll
       for (int i = 0; i < TM; ++i)
 #pragma unroll
@@ -329,7 +331,7 @@ __global__ __launch_bounds__(WM * WN * 64) void f32w_gemm_kernel(const float* __
     }
 }
 
-template <int WM, int WN, int TM, int TN, bool SLICE>
+template <int WM, int WN, int TM, int TN, bool SLICE, bool STAGED>
 hipError_t launch_f32w_gemm_t(const float* W, uint32_t K, uint32_t N, const float* x, uint32_t M, float* y,
                               uint32_t ldx, uint32_t accum, hipStream_t st) {
   constexpr uint32_t MT = WM * TM * 16, NT = WN * TN * 16;
@@ -337,17 +339,17 @@ hipError_t launch_f32w_gemm_t(const float* W, uint32_t K, uint32_t N, const floa
   const uint64_t tiles = static_cast<uint64_t>(mtiles) * ntiles;
   if (tiles > 0x7fffffffull) return hipErrorInvalidValue;
   const uint32_t grid = static_cast<uint32_t>((tiles + 7) / 8 * 8);
-  hipLaunchKernelGGL((f32w_gemm_kernel<WM, WN, TM, TN, SLICE>), dim3(grid), dim3(WM * WN * 64), 0, st, W, K, N, x,
+  hipLaunchKernelGGL((f32w_gemm_kernel<WM, WN, TM, TN, SLICE, STAGED>), dim3(grid), dim3(WM * WN * 64), 0, st, W, K, N, x,
                      M, mtiles, ntiles, y, ldx, accum);
   return hipGetLastError();
 }
 
-template <bool SLICE>
+template <bool SLICE, bool STAGED = false>
 hipError_t launch_f32w_gemm_any(const float* W, uint32_t K, uint32_t N, const float* x, uint32_t M, float* y,
                                 uint32_t ldx, uint32_t accum, hipStream_t st) {
-  if (M <= 32) return launch_f32w_gemm_t<1, 4, 2, 4, SLICE>(W, K, N, x, M, y, ldx, accum, st);
-  if (M <= 64) return launch_f32w_gemm_t<1, 4, 4, 4, SLICE>(W, K, N, x, M, y, ldx, accum, st);
-  return launch_f32w_gemm_t<2, 2, 4, 4, SLICE>(W, K, N, x, M, y, ldx, accum, st);
+  if (M <= 32) return launch_f32w_gemm_t<1, 4, 2, 4, SLICE, STAGED>(W, K, N, x, M, y, ldx, accum, st);
+  if (M <= 64) return launch_f32w_gemm_t<1, 4, 4, 4, SLICE, STAGED>(W, K, N, x, M, y, ldx, accum, st);
+  return launch_f32w_gemm_t<2, 2, 4, 4, SLICE, STAGED>(W, K, N, x, M, y, ldx, accum, st);
 }
 
 }  // namespace
@@ -367,8 +369,13 @@ hipError_t launch_f32_gemm_kslice(const float* w, uint64_t kc, uint64_t n, const
   if (w == nullptr || kc < 1 || kc % 4 != 0 || n < 1 || n % 4 != 0 || ldx < kc || ldx % 4 != 0 || m < 1 ||
       m > 0x7fffffffull || ldx > 0x7fffffffull || n > 0x7fffffffull)
     return hipErrorInvalidValue;
-  return launch_f32w_gemm_any<true>(w, static_cast<uint32_t>(kc), static_cast<uint32_t>(n), x,
-                                    static_cast<uint32_t>(m), y, static_cast<uint32_t>(ldx), accum ? 1u : 0u, st);
+  // Always the staged sums: the plain chain missed the F32 bars on 2048-row
+  // slices and on 672-row ones too (Q4_0 1024 x 12288, 128 rows: 1.10e-5),
+  // though it ran faster at two wavefronts per SIMD (Q4_K 4096 x 14336
+  // M=512: 818 against 1010 us)
+  return launch_f32w_gemm_any<true, true>(w, static_cast<uint32_t>(kc), static_cast<uint32_t>(n), x,
+                                          static_cast<uint32_t>(m), y, static_cast<uint32_t>(ldx), accum ? 1u : 0u,
+                                          st);
 }
 
 }  // namespace qi

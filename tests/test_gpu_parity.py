@@ -170,8 +170,10 @@ def test_f32_row_major_many_rows_tolerance(ctx, qtype):
     with a 1-row launch; K with a partial last tile: 200, 42), from 128 rows
     (K a multiple of 4) the K-slice GEMM: one slice at K = 200, two at
     K = 4096 (2048 weight rows each) and 14336 (8192), a partial last slice at
-    K = 14336. K = 42 keeps the GEMV at 130 rows."""
-    for k, n, ms in ((200, 512, (16, 128)), (4096, 4096, (16, 130)), (14336, 1024, (17, 300)), (42, 256, (20, 130))):
+    K = 14336, 672 and 352 at N = 12288. K = 42 keeps the GEMV at 130
+    rows."""
+    for k, n, ms in ((200, 512, (16, 128)), (4096, 4096, (16, 130)), (14336, 1024, (17, 300)), (42, 256, (20, 130)),
+                     (1024, 12288, (128,))):
         blocks = po.make_weights(qtype, n, k, seed=2300 + qtype + k, outliers=qtype >= qa.Q4_K)
         w = ctx.weights(qtype, qa.ROW_MAJOR, k, n, blocks)
         for m in ms:
