@@ -201,7 +201,7 @@ constexpr uint32_t kF32Kt = 32;
 // SLICE: W holds rows [k0, k0 + K) of a longer weight; x keeps its full row
 // stride ldx (x points at column k0); the products add to y after the first
 // slice (accum) and non-finite sums are left for the caller to recompute.
-// STAGED (slices only): per-stage sums, below.
+// STAGED: per-stage sums, below (every launch takes them).
 template <int WM, int WN, int TM, int TN, bool SLICE, bool STAGED = false>
 __global__ __launch_bounds__(WM * WN * 64) void f32w_gemm_kernel(const float* __restrict__ W, uint32_t K,
                                                                   uint32_t N, const float* __restrict__ x,
@@ -271,10 +271,13 @@ __global__ __launch_bounds__(WM * WN * 64) void f32w_gemm_kernel(const float* __
     const float* wb = &ws[b][(4 * g) * WS + wn * TN * 16 + r16];
     // STAGED: the stage's KT products in sums of their own, added to the
     // running ones once per stage, so that each output's chain of dependent
-    // f32 additions is KT / 4 long and then K / KT (dequantized Q8_0 weights
-    // at K = 4096 missed the F32 bars over 130 x 4096 outputs, 1.09e-5, with
-    // one chain over each 2048-row slice). It doubles the accumulator
-    // registers (one wavefront per SIMD for the 128 x 128 tile).
+    // matrix-instruction accumulations is KT / 4 long and then K / KT f32
+    // additions. One chain over K missed the F32 bars wherever many outputs
+    // were checked: F32 weights N(0, 0.02^2) at K = 4096, N = 4096, 130 and
+    // 512 rows 1.06e-5 and 1.45e-5 componentwise, 2048 x 8192 x 300 rows
+    // 1.15e-5; dequantized Q8_0 at 4096 x 4096 x 130 rows 1.09e-5. It
+    // doubles the accumulator registers (one wavefront per SIMD for the
+    // 128 x 128 tile).
     [[maybe_unused]] f32x4 part[TM][TN];
 #pragma unroll
     for (int kk = 0; kk < KT / 16; ++kk) {
@@ -347,9 +350,12 @@ hipError_t launch_f32w_gemm_t(const float* W, uint32_t K, uint32_t N, const floa
 template <bool SLICE, bool STAGED = false>
 hipError_t launch_f32w_gemm_any(const float* W, uint32_t K, uint32_t N, const float* x, uint32_t M, float* y,
                                 uint32_t ldx, uint32_t accum, hipStream_t st) {
+  // 32 x 256 tiles up to 32 rows, 64 x 128 above: with the staged sums the
+  // 64 x 256 and 128 x 128 tiles ran at one wavefront per SIMD (LM head
+  // 4096 x 151936, us per call: M=64 1122 against 933, M=512 6368 against
+  // 5657 for 64 x 128)
   if (M <= 32) return launch_f32w_gemm_t<1, 4, 2, 4, SLICE, STAGED>(W, K, N, x, M, y, ldx, accum, st);
-  if (M <= 64) return launch_f32w_gemm_t<1, 4, 4, 4, SLICE, STAGED>(W, K, N, x, M, y, ldx, accum, st);
-  return launch_f32w_gemm_t<2, 2, 4, 4, SLICE, STAGED>(W, K, N, x, M, y, ldx, accum, st);
+  return launch_f32w_gemm_t<2, 2, 2, 4, SLICE, STAGED>(W, K, N, x, M, y, ldx, accum, st);
 }
 
 }  // namespace
@@ -361,7 +367,7 @@ hipError_t launch_f32w_gemm(const Image& im, const View& v, const float* x, uint
     return hipErrorInvalidValue;
   const float* W = reinterpret_cast<const float*>(v.qs);
   const uint32_t K = static_cast<uint32_t>(im.k), N = static_cast<uint32_t>(im.n), M = static_cast<uint32_t>(m);
-  return launch_f32w_gemm_any<false>(W, K, N, x, M, y, K, 0, st);
+  return launch_f32w_gemm_any<false, true>(W, K, N, x, M, y, K, 0, st);
 }
 
 hipError_t launch_f32_gemm_kslice(const float* w, uint64_t kc, uint64_t n, const float* x, uint64_t ldx, uint64_t m,

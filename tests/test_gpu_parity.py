@@ -750,6 +750,20 @@ def test_f32_weights_tolerance(ctx, m):
     assert wt.linear(x, qa.MODE_F32).tobytes() == y.tobytes()  # deterministic
 
 
+@pytest.mark.parametrize("k,n,m", [(4096, 4096, 130), (2048, 8192, 300)])
+def test_f32_weights_gemm_every_output(ctx, k, n, m):
+    """The F32 bars over every output of larger products (532 K and 2.5 M
+    outputs), where a single accumulation chain over K exceeded 1e-5
+    componentwise."""
+    w = po.fill_normal(9900 + m, k * n, 0.02).reshape(k, n)
+    wt = ctx.weights(qa.F32, qa.ROW_MAJOR, k, n, w)
+    x = po.fill_normal(9950 + m, m * k).reshape(m, k)
+    y = wt.linear(x, qa.MODE_F32)
+    comp, norm = _f32w_checks(y, x, w)
+    assert comp <= F32_TOL and norm <= F32_TOL, (k, n, m, comp, norm)
+    wt.free()
+
+
 @pytest.mark.parametrize("k,n", [(1022, 1000), (4096, 260), (256, 4100)])
 def test_f32_weights_gemm_edges(ctx, k, n):
     """K not a multiple of 4 (the GEMM's 16-byte x loads): 8-row GEMV chunks
