@@ -174,22 +174,20 @@ struct LinearPlan {
   uint64_t m_pad = 0;
   uint32_t splits = 1;  // GEMM K splits, or row-major GEMV K splits per row chunk
   uint64_t h_floats = 0, s_floats = 0, d_floats = 0;  // f16 activations, partials, records
-  uint64_t kslice = 0;  // kRowMajorGemm: weight rows per dequantized slice
 };
 
 // Rows from which row-major weights (tiled image, K a multiple of 4) take
-// the K-slice GEMM instead of the GEMV's 2-row launches, each of which reads
-// the whole weight: rows [k0, k0 + kc) of the weight are dequantized
-// (bit-exact f32) into a workspace of at most kRmSliceFloats and multiplied by
-// the f32 matrix-core GEMM (the F32 weights' kernel), each slice adding to y;
-// then non-finite outputs are recomputed in the reference's order. Measured
-// on MI355X, us per call, GEMV launches / K-slice GEMM: Q4_K 4096x14336 M=32
-// 422 / 402, M=64 839 / 580, M=128 1672 / 569, M=512 6672 / 1010; Q8_0
-// 4096x4096 M=32 214 / 265, M=64 424 / 403, M=512 3336 / 388; Q4_K
-// 14336x4096 M=32 445 / 938, M=64 889 / 1432 (few workgroups per slice at
-// N = 4096), M=512 7102 / 1367.
-constexpr uint64_t kRmGemmMinRows = 128;
-constexpr uint64_t kRmSliceFloats = 8ull << 20;
+// the row-major GEMM (weights dequantized into LDS for the f32 matrix cores,
+// K split into parts whose partial sums take at most kRmPartFloats) instead
+// of the GEMV's 2-row launches, each of which reads and converts the whole
+// weight. Calls run in chunks of kRmGemmChunkRows rows. Measured on MI355X,
+// us per call, Q4_K 4096x14336, GEMV launches / GEMM: M=2 28.0 / 36.4,
+// M=4 54.7 / 37.7, M=16 211.6 / 39.6, M=64 838 / 105 (the K-slice GEMM it
+// replaced, f32 weight slices dequantized to HBM: 580), M=512 843 (K slices)
+// / 660, M=2048 2446 (K slices) / 2272.
+constexpr uint64_t kRmGemmMinRows = 3;
+constexpr uint64_t kRmGemmChunkRows = 4096;
+constexpr uint64_t kRmPartFloats = 8ull << 20;
 
 // Rows of a chunk at which the 2-16 row GEMV switches from the int8-digit
 // kernel (qi_gemv_rows.hip) to the split-half kernel (qi_gemv_half.hip): the
@@ -247,13 +245,17 @@ qi_hip_status plan_linear(const Image& im, uint64_t m, int32_t mode, LinearPlan*
     if (p->splits > 1) p->s_floats = static_cast<uint64_t>(p->splits) * (m < 8 ? m : 8) * im.n;
     return QI_HIP_OK;
   }
-  if (mode != QI_HIP_MODE_EXACT && qi::gemv_rm_supported(im) && im.tiled && m >= kRmGemmMinRows &&
-      im.k % 4 == 0) {
+  if (mode != QI_HIP_MODE_EXACT && qi::rm_gemm_supported(im) && m >= kRmGemmMinRows) {
     p->kind = LinearPlan::kRowMajorGemm;
-    uint64_t kc = kRmSliceFloats / im.n / 32 * 32;
-    if (kc < 32) kc = 32;
-    p->kslice = kc < im.k ? kc : im.k;
-    p->d_floats = p->kslice * im.n;
+    // chunks of kRmGemmChunkRows rows; a shorter last chunk takes its own
+    // part count (enqueue_linear asks again)
+    const uint64_t chunk = m < kRmGemmChunkRows ? m : kRmGemmChunkRows;
+    for (uint64_t r : {chunk, m > chunk ? m % chunk : 0}) {
+      if (r == 0) continue;
+      const uint32_t parts = qi::rm_gemm_parts(im, r, kRmPartFloats);
+      if (parts > 1) p->s_floats = std::max(p->s_floats, static_cast<uint64_t>(parts) * r * im.n);
+    }
+    p->splits = qi::rm_gemm_parts(im, chunk, kRmPartFloats);
     return QI_HIP_OK;
   }
   if (mode != QI_HIP_MODE_EXACT && qi::gemv_rm_supported(im)) {
@@ -344,15 +346,12 @@ qi_hip_status enqueue_linear(const qi_hip_weights* w, const LinearPlan& p, const
       return QI_HIP_OK;
     }
     case LinearPlan::kRowMajorGemm:
-      // weight rows [k0, k0 + kc) as f32 [kc, N] in dws, then the f32 GEMM
-      // of x's columns [k0, k0 + kc), stored by the first slice and added by
-      // the others; then the non-finite outputs in the reference's order
-      for (uint64_t k0 = 0; k0 < im.k; k0 += p.kslice) {
-        const uint64_t kc = im.k - k0 < p.kslice ? im.k - k0 : p.kslice;
-        QI_HIP_TRY(qi::launch_dequant_rm_rows(im, v, k0, kc, dws, st), "dequantize row-major weight rows");
-        QI_HIP_TRY(qi::launch_f32_gemm_kslice(dws, kc, im.n, x + k0, im.k, m, y, k0 > 0, st), "row-major slice GEMM");
+      for (uint64_t m0 = 0; m0 < m; m0 += kRmGemmChunkRows) {
+        const uint64_t rows = m - m0 < kRmGemmChunkRows ? m - m0 : kRmGemmChunkRows;
+        const uint32_t parts = qi::rm_gemm_parts(im, rows, kRmPartFloats);
+        QI_HIP_TRY(qi::launch_rm_gemm(im, v, x + m0 * im.k, rows, y + m0 * im.n, sws, parts, st),
+                   "launch row-major GEMM");
       }
-      QI_HIP_TRY(qi::launch_rm_fix_nonfinite(im, v, x, m, y, st), "row-major non-finite outputs");
       return QI_HIP_OK;
     case LinearPlan::kMfma:
     case LinearPlan::kPlanar:

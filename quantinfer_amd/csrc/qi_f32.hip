@@ -198,16 +198,12 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr uint32_t kF32Kt = 32;
 
-// SLICE: W holds rows [k0, k0 + K) of a longer weight; x keeps its full row
-// stride ldx (x points at column k0); the products add to y after the first
-// slice (accum) and non-finite sums are left for the caller to recompute.
 // STAGED: per-stage sums, below (every launch takes them).
-template <int WM, int WN, int TM, int TN, bool SLICE, bool STAGED = false>
+template <int WM, int WN, int TM, int TN, bool STAGED = false>
 __global__ __launch_bounds__(WM * WN * 64) void f32w_gemm_kernel(const float* __restrict__ W, uint32_t K,
                                                                   uint32_t N, const float* __restrict__ x,
                                                                   uint32_t M, uint32_t mtiles,
-                                                                  uint32_t ntiles, float* __restrict__ y,
-                                                                  uint32_t ldx, uint32_t accum) {
+                                                                  uint32_t ntiles, float* __restrict__ y) {
   constexpr int MT = WM * TM * 16, NT = WN * TN * 16, KT = kF32Kt, THREADS = WM * WN * 64;
   constexpr int XS = KT + 4, WS = NT + 4;
   constexpr int XL = MT * KT / 4 / THREADS, WL = KT * NT / 4 / THREADS;  // 16-byte loads per thread
@@ -229,7 +225,7 @@ __global__ __launch_bounds__(WM * WN * 64) void f32w_gemm_kernel(const float* __
     for (int i = 0; i < XL; ++i) {
       const uint32_t e = t + i * THREADS, row = e / (KT / 4), k = k0 + (e % (KT / 4)) * 4;
       xr[i] = (m0 + row < M && k < K)
-                  ? *reinterpret_cast<const f32x4*>(x + static_cast<uint64_t>(m0 + row) * (SLICE ? ldx : K) + k)
+                  ? *reinterpret_cast<const f32x4*>(x + static_cast<uint64_t>(m0 + row) * K + k)
                   : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     }
 #pragma unroll
@@ -323,39 +319,34 @@ __global__ __launch_bounds__(WM * WN * 64) void f32w_gemm_kernel(const float* __
         const uint32_t m = m0 + wm * TM * 16 + i * 16 + 4 * g + q;
         if (m >= M) continue;
         float v = acc[i][j][q];
-        float* dst = y + static_cast<uint64_t>(m) * N + n;
-        if constexpr (SLICE) {
-          if (accum) v = *dst + v;
-        } else if (!__builtin_isfinite(v)) {
-          v = f32w_exact(W, K, N, x + static_cast<uint64_t>(m) * K, n);
-        }
-        *dst = v;
+        if (!__builtin_isfinite(v)) v = f32w_exact(W, K, N, x + static_cast<uint64_t>(m) * K, n);
+        y[static_cast<uint64_t>(m) * N + n] = v;
       }
     }
 }
 
-template <int WM, int WN, int TM, int TN, bool SLICE, bool STAGED>
+template <int WM, int WN, int TM, int TN, bool STAGED>
 hipError_t launch_f32w_gemm_t(const float* W, uint32_t K, uint32_t N, const float* x, uint32_t M, float* y,
-                              uint32_t ldx, uint32_t accum, hipStream_t st) {
+                              hipStream_t st) {
   constexpr uint32_t MT = WM * TM * 16, NT = WN * TN * 16;
   const uint32_t mtiles = (M + MT - 1) / MT, ntiles = (N + NT - 1) / NT;
   const uint64_t tiles = static_cast<uint64_t>(mtiles) * ntiles;
   if (tiles > 0x7fffffffull) return hipErrorInvalidValue;
   const uint32_t grid = static_cast<uint32_t>((tiles + 7) / 8 * 8);
-  hipLaunchKernelGGL((f32w_gemm_kernel<WM, WN, TM, TN, SLICE, STAGED>), dim3(grid), dim3(WM * WN * 64), 0, st, W, K, N, x,
-                     M, mtiles, ntiles, y, ldx, accum);
+  hipLaunchKernelGGL((f32w_gemm_kernel<WM, WN, TM, TN, STAGED>), dim3(grid), dim3(WM * WN * 64), 0, st, W, K, N, x,
+                     M, mtiles, ntiles, y);
   return hipGetLastError();
 }
 
-template <bool SLICE, bool STAGED = false>
+template <bool STAGED = false>
 hipError_t launch_f32w_gemm_any(const float* W, uint32_t K, uint32_t N, const float* x, uint32_t M, float* y,
-                                uint32_t ldx, uint32_t accum, hipStream_t st) {
+                                hipStream_t st) {
   // 32 x 256 tiles up to 32 rows, 64 x 128 above: with the staged sums the
   // 64 x 256 and 128 x 128 tiles ran at one wavefront per SIMD (LM head
   // 4096 x 151936, us per call: M=64 1122 against 933, M=512 6368 against
   // 5657 for 64 x 128)
-  if (M <= 32) return launch_f32w_gemm_t<1, 4, 2, 4, SLICE, STAGED>(W, K, N, x, M, y, ldx, accum, st);
-  return launch_f32w_gemm_t<2, 2, 2, 4, SLICE, STAGED>(W, K, N, x, M, y, ldx, accum, st);
+  if (M <= 32) return launch_f32w_gemm_t<1, 4, 2, 4, STAGED>(W, K, N, x, M, y, st);
+  return launch_f32w_gemm_t<2, 2, 2, 4, STAGED>(W, K, N, x, M, y, st);
 }
 
 }  // namespace
@@ -367,21 +358,7 @@ hipError_t launch_f32w_gemm(const Image& im, const View& v, const float* x, uint
     return hipErrorInvalidValue;
   const float* W = reinterpret_cast<const float*>(v.qs);
   const uint32_t K = static_cast<uint32_t>(im.k), N = static_cast<uint32_t>(im.n), M = static_cast<uint32_t>(m);
-  return launch_f32w_gemm_any<false, true>(W, K, N, x, M, y, K, 0, st);
-}
-
-hipError_t launch_f32_gemm_kslice(const float* w, uint64_t kc, uint64_t n, const float* x, uint64_t ldx, uint64_t m,
-                                  float* y, bool accum, hipStream_t st) {
-  if (w == nullptr || kc < 1 || kc % 4 != 0 || n < 1 || n % 4 != 0 || ldx < kc || ldx % 4 != 0 || m < 1 ||
-      m > 0x7fffffffull || ldx > 0x7fffffffull || n > 0x7fffffffull)
-    return hipErrorInvalidValue;
-  // Always the staged sums: the plain chain missed the F32 bars on 2048-row
-  // slices and on 672-row ones too (Q4_0 1024 x 12288, 128 rows: 1.10e-5),
-  // though it ran faster at two wavefronts per SIMD (Q4_K 4096 x 14336
-  // M=512: 818 against 1010 us)
-  return launch_f32w_gemm_any<true, true>(w, static_cast<uint32_t>(kc), static_cast<uint32_t>(n), x,
-                                          static_cast<uint32_t>(m), y, static_cast<uint32_t>(ldx), accum ? 1u : 0u,
-                                          st);
+  return launch_f32w_gemm_any<true>(W, K, N, x, M, y, st);
 }
 
 }  // namespace qi

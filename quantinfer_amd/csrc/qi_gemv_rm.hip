@@ -420,106 +420,263 @@ hipError_t launch_rm_q(const View& v, const float* x, uint32_t m, float* y, floa
 
 namespace {
 
-// Weight rows [k0, k0 + kc) of a tiled row-major image as an f32 [kc, N]
-// matrix: wavefront w of workgroup (x, y) takes the record of unit 4x + w in
-// tile k0 / 16 + y, lane 16g + c its row c, lane group g (Unit<QT>), and
-// stores that row's 64 weights of the lane group, 8 consecutive per step.
-// Each weight by the reference's operation sequence, so bit-identical to
-// dequantize (matmul.rs:162-280): Q8_0 d q; Q4_0 d (q - 8); Q4_K/Q5_K
-// (d sc) q - dmin m, no fused multiply-add (the file is compiled with
-// -ffp-contract=off); Q6_K (d sc) (q - 32).
-template <int QT, bool WIDE>
-__global__ __launch_bounds__(256) void dequant_rm_rows_kernel(View v, uint32_t k0, uint32_t kc,
-                                                              float* __restrict__ out) {
+// Row-major GEMM, 2 rows and more: y[m, n] = sum_k x[m, k] w(k, n) with the
+// weights dequantized in LDS, never stored to HBM. Workgroup (u, mb, z) takes
+// unit u (outputs 256u .. 256u + 255), rows 16 TM mb .. of x and K part z
+// (tiles [z T / P, (z + 1) T / P)). A stage is 64 weight rows: wavefront w
+// loads the record of the stage's tile w (Unit<QT>, lane 16g + c row c's lane
+// group g) and writes its 64 weights per lane to LDS as f32, each by the
+// reference's operation sequence, so bit-identical to dequantize
+// (matmul.rs:162-280): Q8_0 d q; Q4_0 d (q - 8); Q4_K/Q5_K (d sc) q - dmin m,
+// no fused multiply-add (the file is compiled with -ffp-contract=off); Q6_K
+// (d sc) (q - 32). The stage's activations go to LDS beside it. The
+// next stage's record and activations are loaded into registers while the
+// matrix cores (v_mfma_f32_16x16x4f32, f32 products) take the current one:
+// wavefront w owns outputs 64w .. 64w + 63 for all 16 TM rows. Each 32-row
+// half of a stage is summed apart and then added to the running sums (the
+// f32 matrix-core GEMM's staged order). One part stores y, recomputing a
+// non-finite sum in the reference's order; more store partial sums, which
+// rm_sum_kernel adds in part order.
+constexpr uint32_t kRmgStageK = 64;       // weight rows per stage: one record per wavefront
+constexpr uint32_t kRmgWs = 256 + 4;      // LDS row stride of the stage's weights (floats)
+constexpr uint32_t kRmgXs = kRmgStageK + 4;  // LDS row stride of the stage's activations
+
+typedef float rmg_f32x4 __attribute__((ext_vector_type(4)));
+
+template <int QT, bool WIDE, int TM>
+__global__ __launch_bounds__(256) void rm_gemm_kernel(View v, const float* __restrict__ x, uint32_t M,
+                                                      uint32_t parts, float* __restrict__ out) {
   using U = Unit<QT>;
   constexpr int kW = U::kWindows, kS = U::kSteps;
+  __shared__ __align__(16) float ws[kRmgStageK * kRmgWs];
+  __shared__ __align__(16) float xs[TM * 16 * kRmgXs];
   const uint32_t lane = threadIdx.x & 63, g = lane >> 4, c = lane & 15;
-  const uint32_t u = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (u >= v.units) return;
-  const uint32_t t = k0 / 16 + blockIdx.y, k = 16 * t + c;
-  typename U::Raw r;
-  U::template load<WIDE, true>(v.qs + (static_cast<uint64_t>(t) * v.units + u) * v.rec.bytes, lane, r);
-  if (k < k0 || k >= k0 + kc) return;
-  float a[kW], b[kW];
-  U::template scales<WIDE>(g, r, a, b);
-  float* row = out + static_cast<uint64_t>(k - k0) * v.n + static_cast<uint64_t>(u) * 256;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint32_t u = blockIdx.x, m0 = blockIdx.y * TM * 16, z = blockIdx.z;
+  const uint32_t K = static_cast<uint32_t>(v.k), T = v.tiles;
+  const uint32_t tb = static_cast<uint32_t>((static_cast<uint64_t>(z) * T) / parts);
+  const uint32_t te = static_cast<uint32_t>((static_cast<uint64_t>(z + 1) * T) / parts);
+  const uint32_t kend = 16 * te < K ? 16 * te : K;  // activations past it are zero
+  const uint32_t stages = (te - tb + 3) / 4;
+  const uint8_t* base = v.qs + static_cast<uint64_t>(u) * v.rec.bytes;
+  const uint64_t tile_bytes = static_cast<uint64_t>(v.units) * v.rec.bytes;
+
+  // two stages in flight: stage s's record and activations in registers
+  // r[s % 2], xr[s % 2] (s + 1 loads while s is multiplied)
+  typename U::Raw r[2];
+  rmg_f32x4 xr[2][TM];
+  // stage s: tile tb + 4s + wave (if below te) and activation columns
+  // 16 tb + 64 s .. + 63 of rows m0 .. m0 + 16 TM - 1
+  auto fetch = [&](uint32_t s, typename U::Raw& rr, rmg_f32x4 (&xx)[TM]) {
+    const uint32_t t = tb + 4 * s + wave;
+    if (t < te) U::template load<WIDE>(base + t * tile_bytes, lane, rr);
 #pragma unroll
-  for (int st = 0; st < 8; ++st) {
-    const uint64_t q = static_cast<uint64_t>(U::codes(r, g, st));
-    const int w = st / kS;
-    float o[8];
+    for (int i = 0; i < TM; ++i) {
+      const uint32_t e = threadIdx.x + 256 * i, row = e / 16, k = 16 * tb + kRmgStageK * s + (e % 16) * 4;
+      xx[i] = (m0 + row < M && k < kend)
+                  ? *reinterpret_cast<const rmg_f32x4*>(x + static_cast<uint64_t>(m0 + row) * K + k)
+                  : rmg_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+  };
+  auto put = [&](uint32_t s, const typename U::Raw& rr, const rmg_f32x4 (&xx)[TM]) {
+    const uint32_t t = tb + 4 * s + wave;
+    float* wrow = ws + (16 * wave + c) * kRmgWs;
+    if (t < te) {
+      float a[kW], b[kW];
+      U::template scales<WIDE>(g, rr, a, b);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const uint32_t byte = static_cast<uint32_t>(q >> (8 * e)) & 0xFFu;
-      if constexpr (QT == kQ8_0) {
-        o[e] = a[w] * static_cast<float>(static_cast<int8_t>(byte));
-      } else if constexpr (QT == kQ4_0) {
-        o[e] = a[w] * (static_cast<float>(byte) - 8.0f);
-      } else if constexpr (QT == kQ6_K) {
-        o[e] = a[w] * static_cast<float>(static_cast<int32_t>(byte) - 32);
-      } else {
-        o[e] = a[w] * static_cast<float>(byte) - b[w];
+      for (int st = 0; st < 8; ++st) {
+        const uint64_t q = static_cast<uint64_t>(U::codes(rr, g, st));
+        const int w = st / kS;
+        float o[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const uint32_t byte = static_cast<uint32_t>(q >> (8 * e)) & 0xFFu;
+          if constexpr (QT == kQ8_0) {
+            o[e] = a[w] * static_cast<float>(static_cast<int8_t>(byte));
+          } else if constexpr (QT == kQ4_0) {
+            o[e] = a[w] * (static_cast<float>(byte) - 8.0f);
+          } else if constexpr (QT == kQ6_K) {
+            o[e] = a[w] * static_cast<float>(static_cast<int32_t>(byte) - 32);
+          } else {
+            o[e] = a[w] * static_cast<float>(byte) - b[w];
+          }
+        }
+        float4* dst = reinterpret_cast<float4*>(wrow + window_first<QT>(g, st / 4) + 8 * (st % 4));
+        dst[0] = make_float4(o[0], o[1], o[2], o[3]);
+        dst[1] = make_float4(o[4], o[5], o[6], o[7]);
+      }
+    } else {
+#pragma unroll
+      for (int st = 0; st < 8; ++st) {
+        float4* dst = reinterpret_cast<float4*>(wrow + window_first<QT>(g, st / 4) + 8 * (st % 4));
+        dst[0] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        dst[1] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
       }
     }
-    float4* dst = reinterpret_cast<float4*>(row + window_first<QT>(g, st / 4) + 8 * (st % 4));
-    dst[0] = make_float4(o[0], o[1], o[2], o[3]);
-    dst[1] = make_float4(o[4], o[5], o[6], o[7]);
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const uint32_t e = threadIdx.x + 256 * i;
+      *reinterpret_cast<rmg_f32x4*>(xs + (e / 16) * kRmgXs + (e % 16) * 4) = xx[i];
+    }
+  };
+
+  rmg_f32x4 acc[TM][4];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = rmg_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  // lane (c, g) supplies A[c][g] = x[row c][k] and B[g][c] = w(k, column c)
+  // of each 16 x 16 x 4 product, k = 16 kk + 4 g + step
+  const float* xb = xs + c * kRmgXs + 4 * g;
+  const float* wb = ws + (4 * g) * kRmgWs + wave * 64 + c;
+  auto multiply = [&]() {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      rmg_f32x4 part[TM][4];
+#pragma unroll
+      for (int k2 = 0; k2 < 2; ++k2) {
+        const int kk = 2 * h + k2;
+        rmg_f32x4 a[TM];
+#pragma unroll
+        for (int i = 0; i < TM; ++i) a[i] = *reinterpret_cast<const rmg_f32x4*>(xb + i * 16 * kRmgXs + kk * 16);
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+          float bv[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) bv[j] = wb[(kk * 16 + st) * kRmgWs + j * 16];
+#pragma unroll
+          for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+              part[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(
+                  a[i][st], bv[j], k2 == 0 && st == 0 ? rmg_f32x4{0.0f, 0.0f, 0.0f, 0.0f} : part[i][j], 0, 0, 0);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] += part[i][j];
+    }
+  };
+  if (stages > 0) fetch(0, r[0], xr[0]);
+  if (stages > 1) fetch(1, r[1], xr[1]);
+  for (uint32_t s = 0; s < stages; s += 2) {
+    put(s, r[0], xr[0]);
+    __syncthreads();
+    if (s + 2 < stages) fetch(s + 2, r[0], xr[0]);
+    multiply();
+    __syncthreads();
+    if (s + 1 < stages) {
+      put(s + 1, r[1], xr[1]);
+      __syncthreads();
+      if (s + 3 < stages) fetch(s + 3, r[1], xr[1]);
+      multiply();
+      __syncthreads();
+    }
+  }
+
+  // lane (c, g) holds rows 4g .. 4g + 3 of each 16 x 16 block, column c
+  float* const dst = out + (parts == 1 ? 0 : static_cast<uint64_t>(z) * M * v.n);
+  bool bad = false;
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint64_t n = static_cast<uint64_t>(u) * 256 + wave * 64 + j * 16 + c;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const uint32_t m = m0 + i * 16 + 4 * g + q;
+        if (m >= M) continue;
+        bad |= !__builtin_isfinite(acc[i][j][q]);
+        dst[static_cast<uint64_t>(m) * v.n + n] = acc[i][j][q];
+      }
+    }
+  // with one part, a non-finite sum (NaN or infinite activations) is
+  // recomputed in the reference's order, which decides NaN or +-Inf; this
+  // lane's own stores are read back (a loop of its own, so that the
+  // accumulator tile above stays in registers)
+  if (parts == 1 && bad) {
+#pragma unroll 1
+    for (int e = 0; e < TM * 16; ++e) {
+      const uint32_t i = e / 16, j = (e / 4) % 4, q = e % 4, m = m0 + i * 16 + 4 * g + q;
+      const uint64_t n = static_cast<uint64_t>(u) * 256 + wave * 64 + j * 16 + c;
+      float* p = dst + static_cast<uint64_t>(m) * v.n + n;
+      if (m < M && !__builtin_isfinite(*p)) *p = exact_row_major_col<QT, WIDE>(v, x + static_cast<uint64_t>(m) * K, n);
+    }
   }
 }
 
 template <int QT, bool WIDE>
-hipError_t launch_rows_q(const View& v, uint32_t k0, uint32_t kc, float* out, hipStream_t st) {
-  const dim3 grid((v.units + 3) / 4, (k0 + kc + 15) / 16 - k0 / 16);
-  hipLaunchKernelGGL((dequant_rm_rows_kernel<QT, WIDE>), grid, dim3(256), 0, st, v, k0, kc, out);
-  return hipGetLastError();
-}
-
-template <int QT, bool WIDE>
-__global__ __launch_bounds__(256) void rm_fix_kernel(View v, const float* __restrict__ x, uint64_t count,
-                                                     float* __restrict__ y) {
-  const uint64_t i = static_cast<uint64_t>(blockIdx.x) * 256 + threadIdx.x;
-  if (i >= count || __builtin_isfinite(y[i])) return;
-  y[i] = exact_row_major_col<QT, WIDE>(v, x + (i / v.n) * v.k, i % v.n);
-}
-
-template <int QT, bool WIDE>
-hipError_t launch_fix_q(const View& v, const float* x, uint64_t count, float* y, hipStream_t st) {
-  hipLaunchKernelGGL((rm_fix_kernel<QT, WIDE>), dim3(static_cast<uint32_t>((count + 255) / 256)), dim3(256), 0, st, v,
-                     x, count, y);
+hipError_t launch_rm_gemm_q(const View& v, const float* x, uint32_t m, float* y, float* part, uint32_t parts,
+                            hipStream_t st) {
+  const uint32_t tm = rm_gemm_tile_rows(m) / 16;
+  const dim3 grid(v.units, (m + 16 * tm - 1) / (16 * tm), parts);
+  float* out = parts > 1 ? part : y;
+  if (tm == 1)
+    hipLaunchKernelGGL((rm_gemm_kernel<QT, WIDE, 1>), grid, dim3(256), 0, st, v, x, m, parts, out);
+  else
+    hipLaunchKernelGGL((rm_gemm_kernel<QT, WIDE, 2>), grid, dim3(256), 0, st, v, x, m, parts, out);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || parts == 1) return e;
+  const uint64_t count = static_cast<uint64_t>(m) * v.n;
+  hipLaunchKernelGGL((rm_sum_kernel<QT, WIDE>), dim3(static_cast<uint32_t>((count + 255) / 256)), dim3(256), 0,
+                     st, part, parts, count, y, v, x);
   return hipGetLastError();
 }
 
 }  // namespace
 
-hipError_t launch_dequant_rm_rows(const Image& im, const View& v, uint64_t k0, uint64_t kc, float* out,
-                                  hipStream_t st) {
-  // k0 on a tile boundary; grid y = the tiles rows [k0, k0 + kc) touch
-  if (im.layout != kRowMajor || !im.tiled || kc == 0 || k0 % 16 != 0 || k0 + kc > im.k || im.k > 0xFFFFFFF0ull ||
-      v.units != im.n / 256 || (kc + 15) / 16 > 0xFFFFu)
-    return hipErrorInvalidValue;
-  const uint32_t a = static_cast<uint32_t>(k0), c = static_cast<uint32_t>(kc);
-  const bool w = im.wide != 0;
-  switch (im.qtype) {
-    case kQ8_0: return w ? launch_rows_q<kQ8_0, true>(v, a, c, out, st) : launch_rows_q<kQ8_0, false>(v, a, c, out, st);
-    case kQ4_0: return w ? launch_rows_q<kQ4_0, true>(v, a, c, out, st) : launch_rows_q<kQ4_0, false>(v, a, c, out, st);
-    case kQ4_K: return w ? launch_rows_q<kQ4_K, true>(v, a, c, out, st) : launch_rows_q<kQ4_K, false>(v, a, c, out, st);
-    case kQ5_K: return w ? launch_rows_q<kQ5_K, true>(v, a, c, out, st) : launch_rows_q<kQ5_K, false>(v, a, c, out, st);
-    case kQ6_K: return w ? launch_rows_q<kQ6_K, true>(v, a, c, out, st) : launch_rows_q<kQ6_K, false>(v, a, c, out, st);
-    default: return hipErrorInvalidValue;
+// 16-row tiles up to 16 rows, 32 above: 64-row tiles (one wavefront per
+// SIMD) ran 2-5% slower from 64 rows on (MI355X, Q4_K 4096 x 14336 M=512
+// 684 against 660 us, M=2048 2388 against 2272; Q8_0 4096 x 4096 M=2048 682
+// against 642)
+uint32_t rm_gemm_tile_rows(uint64_t m) { return m <= 16 ? 16 : 32; }
+
+uint32_t rm_gemm_parts(const Image& im, uint64_t m, uint64_t max_part_floats) {
+  // The part count with the fewest rounds of resident workgroups per part
+  // (two per CU, 256 CUs), the smaller count on a tie; each part at least two
+  // stages (8 tiles), the partial sums within max_part_floats.
+  const uint64_t rows = rm_gemm_tile_rows(m), slots = 512;
+  const uint64_t groups = static_cast<uint64_t>(im.units) * ((m + rows - 1) / rows);
+  uint64_t pmax = im.tiles / 8;
+  const uint64_t by_space = max_part_floats / (m * im.n);
+  if (pmax > by_space) pmax = by_space;
+  if (pmax > 64) pmax = 64;
+  uint64_t best = 1;
+  for (uint64_t p = 2; p <= pmax; ++p) {
+    // rounds(p) / p < rounds(best) / best
+    const uint64_t rp = (groups * p + slots - 1) / slots, rb = (groups * best + slots - 1) / slots;
+    if (rp * best < rb * p) best = p;
   }
+  return static_cast<uint32_t>(best);
 }
 
-hipError_t launch_rm_fix_nonfinite(const Image& im, const View& v, const float* x, uint64_t m, float* y,
-                                   hipStream_t st) {
-  const uint64_t count = m * im.n;
-  if (im.layout != kRowMajor || count == 0 || (count + 255) / 256 > 0x7fffffffull) return hipErrorInvalidValue;
+bool rm_gemm_supported(const Image& im) {
+  return gemv_rm_supported(im) && im.tiled && im.k % 4 == 0 && im.k <= 0xFFFFFFF0ull;
+}
+
+hipError_t launch_rm_gemm(const Image& im, const View& v, const float* x, uint64_t m, float* y, float* part,
+                          uint32_t parts, hipStream_t st) {
+  // grid: units x row blocks (at most 0xFFFF) x parts; each part at least one tile
+  if (!rm_gemm_supported(im) || m < 1 || (m + 31) / 32 > 0xFFFFu || parts < 1 || parts > 0xFFFFu ||
+      parts > im.tiles || (parts > 1 && part == nullptr) || v.units != im.n / 256 || v.tiles != (im.k + 15) / 16 ||
+      (m * im.n + 255) / 256 > 0x7fffffffull)
+    return hipErrorInvalidValue;
+  const uint32_t mm = static_cast<uint32_t>(m);
   const bool w = im.wide != 0;
   switch (im.qtype) {
-    case kQ8_0: return w ? launch_fix_q<kQ8_0, true>(v, x, count, y, st) : launch_fix_q<kQ8_0, false>(v, x, count, y, st);
-    case kQ4_0: return w ? launch_fix_q<kQ4_0, true>(v, x, count, y, st) : launch_fix_q<kQ4_0, false>(v, x, count, y, st);
-    case kQ4_K: return w ? launch_fix_q<kQ4_K, true>(v, x, count, y, st) : launch_fix_q<kQ4_K, false>(v, x, count, y, st);
-    case kQ5_K: return w ? launch_fix_q<kQ5_K, true>(v, x, count, y, st) : launch_fix_q<kQ5_K, false>(v, x, count, y, st);
-    case kQ6_K: return w ? launch_fix_q<kQ6_K, true>(v, x, count, y, st) : launch_fix_q<kQ6_K, false>(v, x, count, y, st);
+    case kQ8_0: return w ? launch_rm_gemm_q<kQ8_0, true>(v, x, mm, y, part, parts, st)
+                         : launch_rm_gemm_q<kQ8_0, false>(v, x, mm, y, part, parts, st);
+    case kQ4_0: return w ? launch_rm_gemm_q<kQ4_0, true>(v, x, mm, y, part, parts, st)
+                         : launch_rm_gemm_q<kQ4_0, false>(v, x, mm, y, part, parts, st);
+    case kQ4_K: return w ? launch_rm_gemm_q<kQ4_K, true>(v, x, mm, y, part, parts, st)
+                         : launch_rm_gemm_q<kQ4_K, false>(v, x, mm, y, part, parts, st);
+    case kQ5_K: return w ? launch_rm_gemm_q<kQ5_K, true>(v, x, mm, y, part, parts, st)
+                         : launch_rm_gemm_q<kQ5_K, false>(v, x, mm, y, part, parts, st);
+    case kQ6_K: return w ? launch_rm_gemm_q<kQ6_K, true>(v, x, mm, y, part, parts, st)
+                         : launch_rm_gemm_q<kQ6_K, false>(v, x, mm, y, part, parts, st);
     default: return hipErrorInvalidValue;
   }
 }

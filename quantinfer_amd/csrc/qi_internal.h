@@ -102,10 +102,15 @@ uint32_t gemv_rm_rows(const Image& im);
 uint32_t gemv_rm_splits(const Image& im, uint32_t m);
 hipError_t launch_gemv_rm(const Image& im, const View& v, const float* x, uint32_t m, float* y, float* part,
                           uint32_t splits, hipStream_t st);
-// y[r][n] that is not finite recomputed in the reference's order from the
-// row-major image (after the K-slice GEMM).
-hipError_t launch_rm_fix_nonfinite(const Image& im, const View& v, const float* x, uint64_t m, float* y,
-                                   hipStream_t st);
+// Row-major GEMM on a tiled image (K a multiple of 4), any row count: the
+// weights dequantized into LDS for f32 matrix-core products, K split into
+// `parts` (partial sums in `part`, parts * m * n floats, when parts > 1),
+// non-finite outputs recomputed in the reference's order.
+bool rm_gemm_supported(const Image& im);
+uint32_t rm_gemm_tile_rows(uint64_t m);
+uint32_t rm_gemm_parts(const Image& im, uint64_t m, uint64_t max_part_floats);
+hipError_t launch_rm_gemm(const Image& im, const View& v, const float* x, uint64_t m, float* y, float* part,
+                          uint32_t parts, hipStream_t st);
 
 // F32 weights (row-major [K, N] f32, N a multiple of 4): the streaming GEMV
 // for up to 8 rows per launch (K split over the grid; `part` holds splits * m * n floats
@@ -121,22 +126,12 @@ hipError_t launch_f32w_gemv(const Image& im, const View& v, const float* x, uint
                             uint32_t splits, hipStream_t st);
 bool f32w_gemm_supported(const Image& im);
 hipError_t launch_f32w_gemm(const Image& im, const View& v, const float* x, uint64_t m, float* y, hipStream_t st);
-// The same GEMM on rows [k0, k0 + kc) of a longer f32 weight held contiguous
-// as [kc, n] in `w` (kc, n and ldx multiples of 4): x points at column k0 of
-// rows of stride ldx; the products are stored (accum false) or added to y;
-// non-finite sums are not recomputed here.
-hipError_t launch_f32_gemm_kslice(const float* w, uint64_t kc, uint64_t n, const float* x, uint64_t ldx, uint64_t m,
-                                  float* y, bool accum, hipStream_t st);
 
 // Exact-order matmul: bit-identical to CpuScalar (any M, either layout).
 hipError_t launch_exact(const Image& im, const View& w, const float* x, uint64_t m, float* y,
                         hipStream_t st);
 // Bit-exact dequantization in block order.
 hipError_t launch_dequant(const Image& im, const View& w, float* out, hipStream_t st);
-// Rows [k0, k0 + kc) of a tiled row-major image as a contiguous f32 [kc, N]
-// matrix, bit-exact.
-hipError_t launch_dequant_rm_rows(const Image& im, const View& w, uint64_t k0, uint64_t kc, float* out,
-                                  hipStream_t st);
 
 struct GemmArgs {
   View w;

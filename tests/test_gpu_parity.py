@@ -165,15 +165,13 @@ def test_f32_row_major_gemv_tolerance(ctx, qtype):
 
 @pytest.mark.parametrize("qtype", ALL_Q, ids=lambda q: NAMES[q])
 def test_f32_row_major_many_rows_tolerance(ctx, qtype):
-    """16 to 300 rows on tiled row-major images, within the F32 bars and
-    deterministic: the GEMV's 2-row launches below 128 rows (an odd count ends
-    with a 1-row launch; K with a partial last tile: 200, 42), from 128 rows
-    (K a multiple of 4) the K-slice GEMM: one slice at K = 200, two at
-    K = 4096 (2048 weight rows each) and 14336 (8192), a partial last slice at
-    K = 14336, 672 and 352 at N = 12288. K = 42 keeps the GEMV at 130
-    rows."""
-    for k, n, ms in ((200, 512, (16, 128)), (4096, 4096, (16, 130)), (14336, 1024, (17, 300)), (42, 256, (20, 130)),
-                     (1024, 12288, (128,))):
+    """16 to 4100 rows on tiled row-major images, within the F32 bars and
+    deterministic. K a multiple of 4 takes the row-major GEMM (16- and 32-row
+    tiles, K parts summed in order or one part; K = 200 with a partial last
+    tile, 4100 rows in a 4096-row chunk and a 4-row one); K = 42 keeps the
+    GEMV's 2-row launches (an odd count ends with a 1-row launch)."""
+    for k, n, ms in ((200, 512, (16, 128, 4100)), (4096, 4096, (16, 130)), (14336, 1024, (17, 300)),
+                     (42, 256, (20, 130)), (1024, 12288, (128,))):
         blocks = po.make_weights(qtype, n, k, seed=2300 + qtype + k, outliers=qtype >= qa.Q4_K)
         w = ctx.weights(qtype, qa.ROW_MAJOR, k, n, blocks)
         for m in ms:
@@ -186,11 +184,11 @@ def test_f32_row_major_many_rows_tolerance(ctx, qtype):
 
 @pytest.mark.parametrize("qtype", ALL_Q, ids=lambda q: NAMES[q])
 def test_row_major_slice_weights_are_the_dequantized_ones(ctx, qtype):
-    """The K-slice GEMM's f32 weights equal the reference's dequantized values:
-    with one-hot activation rows (row i picks weight row k_i) the outputs are
-    those weight rows (every other product is zero, added exactly), here across
-    the three slices of K = 4100 at N = 4096 (2048, 2048 and a 4-row partial
-    tile)."""
+    """The row-major GEMM's f32 weights (dequantized in LDS) equal the
+    reference's dequantized values: with one-hot activation rows (row i picks
+    weight row k_i) the outputs are those weight rows (every other product is
+    zero, added exactly), here at K = 4100 and N = 4096 (K parts whose partial
+    sums are added in order, a 4-row partial last tile)."""
     k, n = 4100, 4096
     blocks = po.make_weights(qtype, n, k, seed=2350 + qtype, outliers=qtype >= qa.Q4_K)
     w = ctx.weights(qtype, qa.ROW_MAJOR, k, n, blocks)

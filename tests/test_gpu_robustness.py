@@ -107,10 +107,11 @@ def test_nonfinite_activations_planar_gemv(ctx, qtype):
 @pytest.mark.parametrize("qtype", ALL_Q, ids=lambda q: NAMES[q])
 @pytest.mark.parametrize("k", [512, 48], ids=["k-split", "one-split"])
 def test_nonfinite_activations_row_major(ctx, qtype, k):
-    """NaN/Inf activations on row-major weights: the K-split sum pass (K = 512),
-    the GEMV itself (K = 48, three tiles: one split) and the K-slice GEMM's
-    last pass (130 rows) recompute non-finite outputs in the reference's
-    order."""
+    """NaN/Inf activations on row-major weights: non-finite outputs are
+    recomputed in the reference's order by the GEMV at 1 and 2 rows (K = 512
+    in its split sum, K = 48 in the GEMV itself) and by the row-major GEMM
+    from 3 rows (K = 512 in the sum of its 4 parts, K = 48 in the GEMM itself:
+    three tiles, one part; 9, 20 and 130 rows on its 16- and 32-row tiles)."""
     n, m = 256, 4
     blocks = po.make_weights(qtype, n, k, seed=8600 + qtype)  # [K, N] blocks along N
     x = _poison(po.fill_normal(8601, m * k).reshape(m, k))
@@ -119,7 +120,7 @@ def test_nonfinite_activations_row_major(ctx, qtype, k):
     for mode in (qa.MODE_F32, qa.MODE_EXACT):
         y = w.linear(x, mode)
         _check_nonfinite_rows(y, ref, (0, 1, 2))
-    for m1 in (1, 9, 20, 130):  # one row, 9 rows (a last launch of one row), 20 rows, the K-slice GEMM
+    for m1 in (1, 2, 9, 20, 130):  # the GEMV at 1 and 2 rows, the GEMM's 16- and 32-row tiles
         x1 = po.fill_normal(8602, m1 * k).reshape(m1, k)
         x1[0, 5] = np.inf
         y1 = w.linear(x1, qa.MODE_F32)

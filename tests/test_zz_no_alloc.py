@@ -38,8 +38,8 @@ CASES = [
     (qa.Q4_0, qa.OUTPUT_ROWS, 4096, 12288, 16, 9, qa.MODE_F32),      # 2-16 row GEMV, activation records
     (qa.Q6_K, qa.OUTPUT_ROWS, 14336, 4096, 16, 9, qa.MODE_F32),      # Q6_K 2-16 rows: records and K parts
     (qa.Q4_K, qa.OUTPUT_ROWS, 4096, 1024, 100, 50, qa.MODE_F32),     # split-half GEMM: records and K parts
-    (qa.Q4_0, qa.ROW_MAJOR, 4096, 4096, 9, 1, qa.MODE_F32),          # row-major GEMV with K-split partials
-    (qa.Q4_K, qa.ROW_MAJOR, 4096, 4096, 130, 64, qa.MODE_F32),       # row-major K-slice GEMM (two slices), then the GEMV
+    (qa.Q4_0, qa.ROW_MAJOR, 4096, 4096, 9, 1, qa.MODE_F32),          # row-major GEMM K parts, then the GEMV's
+    (qa.Q4_K, qa.ROW_MAJOR, 4096, 4096, 130, 2, qa.MODE_F32),        # row-major GEMM, 32-row tiles, then 2-row GEMV
     (qa.Q4_K, qa.OUTPUT_ROWS, 512, 64, 5, 2, qa.MODE_EXACT),         # no workspace
     (qa.F32, qa.ROW_MAJOR, 1024, 2000, 40, 12, qa.MODE_F32),          # F32 weights: GEMM, then GEMV K parts
 ]
