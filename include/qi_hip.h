@@ -155,8 +155,8 @@ qi_hip_status qi_hip_linear_device(qi_hip_ctx *ctx, const qi_hip_weights *w, con
  * hipMalloc). No counterpart in the reference. Same kernels and results as
  * qi_hip_linear_device, but every workspace (the GEMM's f16 activations and
  * split-K partials, the activation records of the multi-row GEMV and of F32
- * mode's split-half GEMM, the f32 weight slices of row-major calls of 128
- * rows or more, at most 32 MB) is carved out of a fixed 64 MiB scratch array the
+ * mode's split-half GEMM, the K-part sums of row-major calls of 3 rows or
+ * more, at most 32 MB) is carved out of a fixed 64 MiB scratch array the
  * library holds on each GPU until the process ends; no call allocates or
  * frees. A call whose workspaces exceed 64 MiB is refused with
  * QI_HIP_INVALID_INPUT (the f16 GEMM takes 2*M*K bytes of f16 activations, M
