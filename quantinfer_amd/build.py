@@ -53,7 +53,8 @@ FLAGS = [
 # sum read in its combine; its accumulators are small). The GEMMs keep the
 # default: their 128-register accumulator tiles need the accumulator file.
 FILE_FLAGS = {"qi_gemv_mfma.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
-              "qi_gemv_rows.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+              "qi_gemv_rows.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+              "qi_gemv_rm.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 
 
 def hipcc() -> str:
