@@ -26,6 +26,7 @@ const FLAGS: &[&str] = &[
 const FILE_FLAGS: &[(&str, &[&str])] = &[
     ("qi_gemv_mfma.hip", &["-mllvm", "-amdgpu-mfma-vgpr-form"]),
     ("qi_gemv_rows.hip", &["-mllvm", "-amdgpu-mfma-vgpr-form"]),
+    ("qi_gemv_rm.hip", &["-mllvm", "-amdgpu-mfma-vgpr-form"]),
 ];
 
 fn main() {

@@ -589,10 +589,11 @@ def cpu_simd_table(repeats: int = 3) -> dict:
 GEMV_POINTS = ([(0, 1, 4096, 4096, (1,))] +
                [(1, 2, k, n, (1, 4, 16)) for k, n in ((4096, 4096), (4096, 1024), (4096, 12288), (12288, 4096))] +
                [(2, q, k, n, (1, 8)) for q in (3, 4, 5) for k, n in ((4096, 14336), (14336, 4096))])
-# The same decode GEMV on row-major weights (QuantInfer layout, blocks along
-# N: backends/cpu/src/matmul.rs:14-90), the tiled row-major image: Q4_K at the
-# FFN up shape, Q4_0 at 4096 x 12288, Q8_0 at 4096^2, one row.
-RM_POINTS = [(2, 3, 4096, 14336, (1,)), (1, 2, 4096, 12288, (1,)), (0, 1, 4096, 4096, (1,))]
+# The same points on row-major weights (QuantInfer layout, blocks along N:
+# backends/cpu/src/matmul.rs:14-90), the tiled row-major image: Q4_K at the
+# FFN up shape, Q4_0 at 4096 x 12288, Q8_0 at 4096^2, at their configs' row
+# counts (one row on the row-major GEMV, from 3 rows the row-major GEMM).
+RM_POINTS = [(2, 3, 4096, 14336, (1, 8)), (1, 2, 4096, 12288, (1, 4, 16)), (0, 1, 4096, 4096, (1,))]
 # the prefill GEMM, Q8_0 and Q4_K, M x (K, N)
 GEMM_POINTS = [(3, q, k, n, (128, 512, 2048)) for q in (1, 3)
                for k, n in ((4096, 4096), (4096, 12288), (12288, 4096))]
