@@ -1,6 +1,9 @@
-// Row-major (blocks along N) GEMV, F32 mode: y[m, n] = sum_k x[m, k] w(k, n)
-// for QuantInfer-layout weights (backends/cpu/src/backend.rs:62-140 ->
-// matmul.rs:14-90; element values matmul.rs:162-280). Two kernels, by image:
+// Row-major (blocks along N) GEMV and GEMM, F32 mode: y[m, n] = sum_k x[m, k]
+// w(k, n) for QuantInfer-layout weights (backends/cpu/src/backend.rs:62-140 ->
+// matmul.rs:14-90; element values matmul.rs:162-280). From 3 rows on a tiled
+// image with K a multiple of 4 the call is rm_gemm_kernel (its comment below):
+// the records dequantized into LDS for the f32 matrix cores. The GEMV takes 1
+// and 2 rows, two kernels by image:
 //
 // Tiled image (N a multiple of 256; gemv_rmt_kernel): record (t, u) holds
 // rows k = 16t + c (c = 0..15) of outputs n = 256u + [0, 256), in the
